@@ -1,0 +1,567 @@
+/*
+ * CPU ORACLE — TEST INFRASTRUCTURE ONLY (see oracle.h).
+ *
+ * Scalar translation unit: seeded generators, bf16 narrowing, the polynomial
+ * exp, the scalar attention primitives, the two-pass cpu::attention oracle,
+ * KV scatter/gather, the deterministic thread pool and the public entries.
+ * Built with -ffp-contract=off and no -mfma so that, like the reference's
+ * scalar TU on the x86-64 baseline, no multiply-add is ever contracted.
+ */
+#define _GNU_SOURCE
+#include <math.h>
+#include <pthread.h>
+#include <stdatomic.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "oracle.h"
+#include "oracle_internal.h"
+
+/* ------------------------------------------------------------------------ */
+/* mt19937_64 (the C++ standard's parameters, [rand.predef]) and the fills  */
+/* of src/tensor/ops.cpp:205-224 (Rng) and :451-477 (fill_normal).          */
+/* ------------------------------------------------------------------------ */
+#define MT_N 312
+#define MT_M 156
+#define MT_UPPER 0xFFFFFFFF80000000ULL
+#define MT_LOWER 0x000000007FFFFFFFULL
+
+void orc_mt64_seed(orc_mt64* g, uint64_t seed) {
+  g->mt[0] = seed;
+  for (int i = 1; i < MT_N; ++i)
+    g->mt[i] = 6364136223846793005ULL * (g->mt[i - 1] ^ (g->mt[i - 1] >> 62)) +
+               (uint64_t)i;
+  g->idx = MT_N;
+}
+
+uint64_t orc_mt64_next(orc_mt64* g) {
+  if (g->idx >= MT_N) {
+    for (int i = 0; i < MT_N; ++i) {
+      const uint64_t x = (g->mt[i] & MT_UPPER) | (g->mt[(i + 1) % MT_N] & MT_LOWER);
+      uint64_t xa = x >> 1;
+      if (x & 1ULL) xa ^= 0xB5026F5AA96619E9ULL;
+      g->mt[i] = g->mt[(i + MT_M) % MT_N] ^ xa;
+    }
+    g->idx = 0;
+  }
+  uint64_t y = g->mt[g->idx++];
+  y ^= (y >> 29) & 0x5555555555555555ULL;
+  y ^= (y << 17) & 0x71D67FFFEDA60000ULL;
+  y ^= (y << 37) & 0xFFF7EEE000000000ULL;
+  y ^= y >> 43;
+  return y;
+}
+
+double orc_mt64_unit(orc_mt64* g) {
+  return (double)(orc_mt64_next(g) >> 11) * 0x1.0p-53;
+}
+
+double orc_mt64_unit_nonzero(orc_mt64* g) {
+  return (double)((orc_mt64_next(g) >> 11) + 1) * 0x1.0p-53;
+}
+
+void orc_fill_normal(float* out, int64_t n, double mean, double stddev,
+                     uint64_t seed) {
+  orc_mt64 g;
+  orc_mt64_seed(&g, seed);
+  const double two_pi = 6.283185307179586476925286766559;
+  for (int64_t i = 0; i < n; i += 2) {
+    const double u1 = orc_mt64_unit_nonzero(&g);
+    const double u2 = orc_mt64_unit(&g);
+    const double radius = sqrt(-2.0 * log(u1));
+    const double angle = two_pi * u2;
+    out[i] = (float)(mean + stddev * (radius * cos(angle)));
+    if (i + 1 < n) out[i + 1] = (float)(mean + stddev * (radius * sin(angle)));
+  }
+}
+
+void orc_fill_uniform(float* out, int64_t n, double low, double high,
+                      uint64_t seed) {
+  orc_mt64 g;
+  orc_mt64_seed(&g, seed);
+  const double extent = high - low;
+  for (int64_t i = 0; i < n; ++i) out[i] = (float)(low + orc_mt64_unit(&g) * extent);
+}
+
+/* ------------------------------------------------------------------------ */
+/* bf16 narrowing / widening (src/tensor/half.h:111-129).                   */
+/* ------------------------------------------------------------------------ */
+uint16_t orc_fp32_to_bf16_bits(float v) {
+  uint32_t bits;
+  memcpy(&bits, &v, sizeof bits);
+  if ((bits & 0x7FFFFFFFu) > 0x7F800000u) {
+    uint16_t r = (uint16_t)(bits >> 16);
+    if ((r & 0x007Fu) == 0u) r |= 0x0040u;
+    return r;
+  }
+  const uint32_t rounded = bits + 0x7FFFu + ((bits >> 16) & 1u);
+  return (uint16_t)(rounded >> 16);
+}
+
+float orc_bf16_bits_to_fp32(uint16_t b) {
+  const uint32_t bits = (uint32_t)b << 16;
+  float f;
+  memcpy(&f, &bits, sizeof f);
+  return f;
+}
+
+void orc_fp32_to_bf16_array(const float* in, uint16_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = orc_fp32_to_bf16_bits(in[i]);
+}
+
+void orc_bf16_to_fp32_array(const uint16_t* in, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = orc_bf16_bits_to_fp32(in[i]);
+}
+
+#include "oracle_exp.h"
+
+float orc_exp_scalar(float x) { return orc_exp_inline(x); }
+
+/* ------------------------------------------------------------------------ */
+/* Scalar primitives (src/kernels/scalar/attention.cpp:20-58).              */
+/* ------------------------------------------------------------------------ */
+static float ops_dot_score_row(const float* q, const float* k_block, int64_t n,
+                               int64_t d, float scale, float* scores) {
+  float row_max = -INFINITY;
+  for (int64_t j = 0; j < n; ++j) {
+    const float* k = k_block + j * d;
+    float dot = 0.0f;
+    for (int64_t e = 0; e < d; ++e) dot += q[e] * k[e];
+    const float s = dot * scale;
+    scores[j] = s;
+    row_max = s > row_max ? s : row_max;
+  }
+  return row_max;
+}
+
+static float ops_exp_row_sum(float* scores, int64_t n, float m_new) {
+  float sum = 0.0f;
+  for (int64_t j = 0; j < n; ++j) {
+    const float e = orc_exp_scalar(scores[j] - m_new);
+    scores[j] = e;
+    sum += e;
+  }
+  return sum;
+}
+
+static void ops_scale_row(float* out, float s, int64_t d) {
+  for (int64_t e = 0; e < d; ++e) out[e] *= s;
+}
+
+static void ops_axpy_row(float* out, float s, const float* x, int64_t d) {
+  for (int64_t e = 0; e < d; ++e) out[e] += s * x[e];
+}
+
+#define ORC_UNITS(name) orc_scalar_##name
+#include "oracle_units.h"
+
+/* ------------------------------------------------------------------------ */
+/* Deterministic thread pool. Persistent workers; one region at a time.     */
+/* ------------------------------------------------------------------------ */
+#define ORC_MAX_THREADS 256
+static struct {
+  pthread_mutex_t mu;
+  pthread_cond_t work_cv;
+  pthread_cond_t done_cv;
+  int nthreads; /* including the caller */
+  int started;  /* workers created */
+  uint64_t generation;
+  orc_body_fn body;
+  void* ctx;
+  int64_t n, grain, num_chunks;
+  atomic_llong next_chunk;
+  int active;
+  pthread_t workers[ORC_MAX_THREADS];
+} g_pool = {PTHREAD_MUTEX_INITIALIZER, PTHREAD_COND_INITIALIZER,
+            PTHREAD_COND_INITIALIZER, 1, 0, 0, 0, 0, 0, 0, 0, 0, 0, {0}};
+
+static void run_chunks(void) {
+  for (;;) {
+    const long long c = atomic_fetch_add(&g_pool.next_chunk, 1);
+    if (c >= g_pool.num_chunks) break;
+    const int64_t begin = (int64_t)c * g_pool.grain;
+    const int64_t end = ORC_MIN(begin + g_pool.grain, g_pool.n);
+    g_pool.body(g_pool.ctx, begin, end);
+  }
+}
+
+static void* worker_main(void* arg) {
+  (void)arg;
+  uint64_t seen = 0;
+  for (;;) {
+    pthread_mutex_lock(&g_pool.mu);
+    while (g_pool.generation == seen) pthread_cond_wait(&g_pool.work_cv, &g_pool.mu);
+    seen = g_pool.generation;
+    pthread_mutex_unlock(&g_pool.mu);
+    run_chunks();
+    pthread_mutex_lock(&g_pool.mu);
+    if (--g_pool.active == 0) pthread_cond_signal(&g_pool.done_cv);
+    pthread_mutex_unlock(&g_pool.mu);
+  }
+  return NULL;
+}
+
+void orc_set_threads(int n) {
+  if (n < 1) n = 1;
+  if (n > ORC_MAX_THREADS) n = ORC_MAX_THREADS;
+  pthread_mutex_lock(&g_pool.mu);
+  while (g_pool.started < n - 1) {
+    pthread_create(&g_pool.workers[g_pool.started], NULL, worker_main, NULL);
+    pthread_detach(g_pool.workers[g_pool.started]);
+    ++g_pool.started;
+  }
+  g_pool.nthreads = n;
+  pthread_mutex_unlock(&g_pool.mu);
+}
+
+int orc_get_threads(void) { return g_pool.nthreads; }
+
+void orc_parallel_for(int64_t n, int64_t grain, orc_body_fn body, void* ctx) {
+  if (n <= 0) return;
+  const int64_t num_chunks = (n + grain - 1) / grain;
+  if (num_chunks <= 1 || g_pool.nthreads <= 1 || g_pool.started == 0) {
+    body(ctx, 0, n);
+    return;
+  }
+  pthread_mutex_lock(&g_pool.mu);
+  g_pool.body = body;
+  g_pool.ctx = ctx;
+  g_pool.n = n;
+  g_pool.grain = grain;
+  g_pool.num_chunks = num_chunks;
+  atomic_store(&g_pool.next_chunk, 0);
+  /* Workers beyond nthreads-1 stay asleep only if never started; started
+   * workers all join every region (they find no chunks when n is small). */
+  g_pool.active = g_pool.started;
+  ++g_pool.generation;
+  pthread_cond_broadcast(&g_pool.work_cv);
+  pthread_mutex_unlock(&g_pool.mu);
+  run_chunks();
+  pthread_mutex_lock(&g_pool.mu);
+  while (g_pool.active > 0) pthread_cond_wait(&g_pool.done_cv, &g_pool.mu);
+  pthread_mutex_unlock(&g_pool.mu);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Public attention entries (src/kernels/paged_attention.cpp:76-147,        */
+/* src/kernels/attention.cpp:76-187).                                       */
+/* ------------------------------------------------------------------------ */
+typedef void (*paged_units_fn)(const orc_paged_args*, int64_t, int64_t);
+typedef void (*prefill_units_fn)(const orc_prefill_args*, int64_t, int64_t);
+typedef void (*decode_units_fn)(const orc_decode_args*, int64_t, int64_t);
+
+static paged_units_fn paged_fn(int isa) {
+  return isa == ORC_ISA_AVX2 ? orc_avx2_paged_decode_units
+                             : orc_scalar_paged_decode_units;
+}
+static prefill_units_fn prefill_fn(int isa) {
+  return isa == ORC_ISA_AVX2 ? orc_avx2_prefill_units : orc_scalar_prefill_units;
+}
+static decode_units_fn decode_fn(int isa) {
+  return isa == ORC_ISA_AVX2 ? orc_avx2_decode_units : orc_scalar_decode_units;
+}
+
+static int bs_ok(int64_t bs) { return bs > 0 && ORC_KB % bs == 0; }
+
+typedef struct {
+  const orc_paged_args* a;
+  paged_units_fn fn;
+} paged_single_ctx;
+
+static void paged_single_body(void* c, int64_t b, int64_t e) {
+  const paged_single_ctx* p = (const paged_single_ctx*)c;
+  p->fn(p->a, b, e);
+}
+
+int orc_paged_decode_f32(int isa, const float* q, const float* k_slab,
+                         const float* v_slab, const int32_t* block_table,
+                         int64_t num_blocks, int64_t length, int64_t heads,
+                         int64_t kv_heads, int64_t d, int64_t block_size,
+                         int64_t block_stride, float scale, float* out) {
+  (void)num_blocks;
+  if (!bs_ok(block_size)) return 2;
+  const orc_paged_args a = {q, k_slab, v_slab, block_table, out, d, length,
+                            heads / kv_heads, block_size, block_stride, scale};
+  paged_single_ctx c = {&a, paged_fn(isa)};
+  orc_parallel_for(kv_heads, 1, paged_single_body, &c);
+  return 0;
+}
+
+typedef struct {
+  const float* q;
+  const float* k_slab;
+  const float* v_slab;
+  const int32_t* const* block_tables;
+  const int64_t* lengths;
+  float* out;
+  int64_t heads, kv_heads, d, group, block_size, block_stride;
+  float scale;
+  paged_units_fn fn;
+} paged_batched_ctx;
+
+/* Unit u -> (sequence u / Hkv, kv head u % Hkv), each unit running the
+ * single-sequence recurrence (src/kernels/paged_attention.cpp:51-72). */
+static void paged_batched_body(void* c, int64_t begin, int64_t end) {
+  const paged_batched_ctx* p = (const paged_batched_ctx*)c;
+  const int64_t row = p->heads * p->d;
+  for (int64_t u = begin; u < end; ++u) {
+    const int64_t b = u / p->kv_heads;
+    const int64_t hk = u % p->kv_heads;
+    const orc_paged_args a = {p->q + b * row,       p->k_slab,
+                              p->v_slab,            p->block_tables[b],
+                              p->out + b * row,     p->d,
+                              p->lengths[b],        p->group,
+                              p->block_size,        p->block_stride,
+                              p->scale};
+    p->fn(&a, hk, hk + 1);
+  }
+}
+
+int orc_paged_decode_batched_f32(int isa, const float* q, const float* k_slab,
+                                 const float* v_slab,
+                                 const int32_t* const* block_tables,
+                                 const int64_t* lengths, int64_t num_seqs,
+                                 int64_t heads, int64_t kv_heads, int64_t d,
+                                 int64_t block_size, int64_t block_stride,
+                                 float scale, float* out) {
+  if (num_seqs == 0) return 0;
+  if (!bs_ok(block_size)) return 2;
+  paged_batched_ctx c = {q,       k_slab,   v_slab,           block_tables,
+                         lengths, out,      heads,            kv_heads,
+                         d,       heads / kv_heads, block_size, block_stride,
+                         scale,   paged_fn(isa)};
+  orc_parallel_for(num_seqs * kv_heads, 1, paged_batched_body, &c);
+  return 0;
+}
+
+typedef struct {
+  const orc_decode_args* a;
+  decode_units_fn fn;
+} decode_ctx;
+
+static void decode_body(void* c, int64_t b, int64_t e) {
+  const decode_ctx* p = (const decode_ctx*)c;
+  p->fn(p->a, b, e);
+}
+
+void orc_decode_f32(int isa, const float* q, const float* k, const float* v,
+                    float* out, int64_t heads, int64_t kv_heads, int64_t d,
+                    int64_t l_dim, float scale) {
+  const orc_decode_args a = {q, k, v, out, d, l_dim, heads / kv_heads, scale};
+  decode_ctx c = {&a, decode_fn(isa)};
+  orc_parallel_for(kv_heads, 1, decode_body, &c);
+}
+
+typedef struct {
+  const orc_prefill_args* a;
+  prefill_units_fn fn;
+} prefill_ctx;
+
+static void prefill_body(void* c, int64_t b, int64_t e) {
+  const prefill_ctx* p = (const prefill_ctx*)c;
+  p->fn(p->a, b, e);
+}
+
+void orc_prefill_f32(int isa, const float* q, const float* k, const float* v,
+                     float* out, int64_t t_dim, int64_t heads, int64_t kv_heads,
+                     int64_t d, int64_t l_dim, float scale) {
+  const int64_t nqb = (t_dim + ORC_QB - 1) / ORC_QB;
+  const orc_prefill_args a = {q,     k,     v,          out,
+                              t_dim, heads, d,          l_dim,
+                              heads / kv_heads, l_dim - t_dim, nqb, scale};
+  prefill_ctx c = {&a, prefill_fn(isa)};
+  orc_parallel_for(heads * nqb, 1, prefill_body, &c);
+}
+
+typedef struct {
+  const float* q;
+  const int32_t* cu;
+  int64_t num_seqs;
+  const float* const* k_seqs;
+  const float* const* v_seqs;
+  const int64_t* l_dims;
+  float* out;
+  int64_t heads, d, group;
+  float scale;
+  prefill_units_fn fn;
+} varlen_ctx;
+
+/* Sequence-major unit walk: sequence b owns H * ceil(T_b/32) units
+ * (src/kernels/attention.cpp:76-108). */
+static void varlen_body(void* c, int64_t unit_begin, int64_t unit_end) {
+  const varlen_ctx* p = (const varlen_ctx*)c;
+  int64_t base = 0;
+  for (int64_t b = 0; b < p->num_seqs; ++b) {
+    const int64_t t0 = p->cu[b];
+    const int64_t t_dim = p->cu[b + 1] - t0;
+    const int64_t nqb = (t_dim + ORC_QB - 1) / ORC_QB;
+    const int64_t seq_end = base + p->heads * nqb;
+    const int64_t lo = unit_begin > base ? unit_begin : base;
+    const int64_t hi = unit_end < seq_end ? unit_end : seq_end;
+    if (lo < hi) {
+      const int64_t l_dim = p->l_dims[b];
+      const orc_prefill_args a = {p->q + t0 * p->heads * p->d,
+                                  p->k_seqs[b],
+                                  p->v_seqs[b],
+                                  p->out + t0 * p->heads * p->d,
+                                  t_dim,
+                                  p->heads,
+                                  p->d,
+                                  l_dim,
+                                  p->group,
+                                  l_dim - t_dim,
+                                  nqb,
+                                  p->scale};
+      p->fn(&a, lo - base, hi - base);
+    }
+    base = seq_end;
+  }
+}
+
+void orc_prefill_varlen_f32(int isa, const float* q, const int32_t* cu_seqlens,
+                            int64_t num_seqs, const float* const* k_seqs,
+                            const float* const* v_seqs, const int64_t* l_dims,
+                            float* out, int64_t heads, int64_t kv_heads,
+                            int64_t d, float scale) {
+  int64_t total = 0;
+  for (int64_t b = 0; b < num_seqs; ++b) {
+    const int64_t t_dim = cu_seqlens[b + 1] - cu_seqlens[b];
+    total += heads * ((t_dim + ORC_QB - 1) / ORC_QB);
+  }
+  varlen_ctx c = {q,   cu_seqlens, num_seqs, k_seqs,           v_seqs,
+                  l_dims, out,     heads,    d,                heads / kv_heads,
+                  scale, prefill_fn(isa)};
+  orc_parallel_for(total, 1, varlen_body, &c);
+}
+
+/* ------------------------------------------------------------------------ */
+/* KV scatter / gather (src/kernels/kv_scatter.cpp:27-61,                   */
+/* src/kernels/kv_gather.cpp:42-89).                                        */
+/* ------------------------------------------------------------------------ */
+void orc_kv_scatter_f32(const float* src_k, const float* src_v,
+                        const int64_t* slot_mapping, int64_t t_dim,
+                        int64_t kv_heads, int64_t d, int64_t block_size,
+                        float* k_slab, float* v_slab) {
+  const int64_t head_stride = block_size * d;
+  for (int64_t t = 0; t < t_dim; ++t) {
+    const int64_t slot = slot_mapping[t];
+    const int64_t block = slot / block_size;
+    const int64_t p = slot % block_size;
+    const int64_t dst_base = block * kv_heads * head_stride + p * d;
+    const int64_t src_base = t * kv_heads * d;
+    for (int64_t h = 0; h < kv_heads; ++h) {
+      memcpy(k_slab + dst_base + h * head_stride, src_k + src_base + h * d,
+             (size_t)d * sizeof(float));
+      memcpy(v_slab + dst_base + h * head_stride, src_v + src_base + h * d,
+             (size_t)d * sizeof(float));
+    }
+  }
+}
+
+void orc_kv_scatter_bf16(const float* src_k, const float* src_v,
+                         const int64_t* slot_mapping, int64_t t_dim,
+                         int64_t kv_heads, int64_t d, int64_t block_size,
+                         uint16_t* k_slab, uint16_t* v_slab) {
+  const int64_t head_stride = block_size * d;
+  for (int64_t t = 0; t < t_dim; ++t) {
+    const int64_t slot = slot_mapping[t];
+    const int64_t block = slot / block_size;
+    const int64_t p = slot % block_size;
+    const int64_t dst_base = block * kv_heads * head_stride + p * d;
+    const int64_t src_base = t * kv_heads * d;
+    for (int64_t h = 0; h < kv_heads; ++h)
+      for (int64_t e = 0; e < d; ++e) {
+        k_slab[dst_base + h * head_stride + e] =
+            orc_fp32_to_bf16_bits(src_k[src_base + h * d + e]);
+        v_slab[dst_base + h * head_stride + e] =
+            orc_fp32_to_bf16_bits(src_v[src_base + h * d + e]);
+      }
+  }
+}
+
+void orc_kv_gather_f32(const float* k_slab, const float* v_slab,
+                       const int32_t* block_table, int64_t block_size,
+                       int64_t length, int64_t kv_heads, int64_t d,
+                       float* out_k, float* out_v) {
+  if (length == 0) return;
+  const int64_t nb = (length + block_size - 1) / block_size;
+  const int64_t block_stride = kv_heads * block_size * d;
+  const int64_t head_stride = block_size * d;
+  for (int64_t u = 0; u < kv_heads * nb; ++u) {
+    const int64_t h = u / nb;
+    const int64_t b = u % nb;
+    const int64_t base = b * block_size;
+    const int64_t rows = ORC_MIN(block_size, length - base);
+    const int64_t src = (int64_t)block_table[b] * block_stride + h * head_stride;
+    const int64_t dst = h * length * d + base * d;
+    memcpy(out_k + dst, k_slab + src, (size_t)(rows * d) * sizeof(float));
+    memcpy(out_v + dst, v_slab + src, (size_t)(rows * d) * sizeof(float));
+  }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Two-pass oracle (src/cpu/attention.cpp:40-177, src/cpu/softmax.cpp).     */
+/* Rows are processed one at a time ([L] scores per row instead of the      */
+/* reference's materialized [H*T, L] matrix); each row's arithmetic is the  */
+/* same: ascending single-accumulator dots, -inf mask, max, expf(x - max),  */
+/* ascending sum, multiply by 1/sum, ascending context sum over all L keys. */
+/* ------------------------------------------------------------------------ */
+typedef struct {
+  const float* q;
+  const float* k;
+  const float* v;
+  float* out;
+  int64_t t_dim, heads, d, l_dim, group, past;
+  float scale;
+} attn_ctx;
+
+static void attention_rows(void* c, int64_t begin, int64_t end) {
+  const attn_ctx* a = (const attn_ctx*)c;
+  float* row = (float*)malloc((size_t)a->l_dim * sizeof(float));
+  for (int64_t r = begin; r < end; ++r) {
+    const int64_t h = r / a->t_dim;
+    const int64_t t = r % a->t_dim;
+    const int64_t hk = h / a->group;
+    const int64_t limit = a->past + t;
+    const float* qv = a->q + (t * a->heads + h) * a->d;
+    for (int64_t s = 0; s < a->l_dim; ++s) {
+      if (s > limit) {
+        row[s] = -INFINITY;
+        continue;
+      }
+      const float* kv = a->k + (hk * a->l_dim + s) * a->d;
+      float dot = 0.0f;
+      for (int64_t e = 0; e < a->d; ++e) dot += qv[e] * kv[e];
+      row[s] = dot * a->scale;
+    }
+    float row_max = row[0];
+    for (int64_t j = 1; j < a->l_dim; ++j) row_max = row_max < row[j] ? row[j] : row_max;
+    float sum = 0.0f;
+    for (int64_t j = 0; j < a->l_dim; ++j) {
+      const float e = expf(row[j] - row_max);
+      row[j] = e;
+      sum += e;
+    }
+    const float inv = 1.0f / sum;
+    for (int64_t j = 0; j < a->l_dim; ++j) row[j] *= inv;
+    float* ov = a->out + (t * a->heads + h) * a->d;
+    for (int64_t e = 0; e < a->d; ++e) {
+      float acc = 0.0f;
+      for (int64_t s = 0; s < a->l_dim; ++s)
+        acc += row[s] * a->v[(hk * a->l_dim + s) * a->d + e];
+      ov[e] = acc;
+    }
+  }
+  free(row);
+}
+
+int orc_cpu_attention(const float* q, const float* k, const float* v,
+                      int64_t t_dim, int64_t heads, int64_t kv_heads, int64_t d,
+                      int64_t l_dim, float scale, float* out) {
+  if (t_dim < 1 || heads < 1 || d < 1 || kv_heads < 1 || l_dim < 1) return 2;
+  if (heads % kv_heads != 0 || l_dim < t_dim) return 2;
+  attn_ctx c = {q, k, v, out, t_dim, heads, d, l_dim, heads / kv_heads,
+                l_dim - t_dim, scale};
+  orc_parallel_for(heads * t_dim, 1, attention_rows, &c);
+  return 0;
+}

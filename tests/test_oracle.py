@@ -1,0 +1,319 @@
+"""Pins the CPU oracle (oracle/) before anything is checked against it.
+
+Each check is chosen so that a plausible restatement mistake (a dropped term,
+a swapped index, a wrong rounding rule) fails: known-answer vectors, the
+reference's own kernels compiled from its sources (oracle/_ref, bit-exact),
+the HF goldens the reference's tests replay, closed forms and fp64 brute force.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from paged_util import (allclose_ref, brute_force_f64, normal, paged_layout, scale_for,
+                        shared_pool_layout)
+
+needs_ref = pytest.mark.skipif(
+    not __import__("oracle.oracle", fromlist=["x"]).ref_available(),
+    reason="oracle/_ref not built (needs /root/reference)")
+
+
+# ------------------------------------------------------------------ generators
+def test_mt19937_64_known_answer(orc):
+    # The C++ standard fixes the 10000th output of a default-seeded (5489)
+    # std::mt19937_64 ([rand.predef]).
+    g = orc.Mt64(5489)
+    for _ in range(9999):
+        g.next()
+    assert g.next() == 9981545732273789042
+
+
+def test_fill_normal_moments_and_pairing(orc):
+    x = orc.fill_normal(200001, 0.0, 0.5, 42).astype(np.float64)
+    assert abs(x.mean()) < 5e-3 and abs(x.std() - 0.5) < 5e-3
+    # Box-Muller pairs: (z0, z1) share a radius, so z0^2 + z1^2 = -2 ln u1 >= 0
+    # and the odd tail element is the cosine branch of its pair only.
+    y = orc.fill_normal(200000, 0.0, 1.0, 42)
+    assert np.array_equal(y, orc.fill_normal(200001, 0.0, 1.0, 42)[:200000])
+    g = orc.Mt64(42)
+    u1 = ((g.next() >> 11) + 1) * 2.0 ** -53
+    u2 = (g.next() >> 11) * 2.0 ** -53
+    r = math.sqrt(-2.0 * math.log(u1))
+    assert y[0] == np.float32(r * math.cos(2 * math.pi * u2))
+    assert y[1] == np.float32(r * math.sin(2 * math.pi * u2))
+
+
+# ------------------------------------------------------------------ bf16
+def test_bf16_rne_matches_torch_on_finite_values(orc):
+    import torch
+    rng = np.random.default_rng(1)
+    bits = rng.integers(0, 2 ** 32, 1 << 18, dtype=np.uint64).astype(np.uint32)
+    x = bits.view(np.float32)
+    x = x[np.isfinite(x)]
+    ours = orc.to_bf16_bits(x)
+    theirs = torch.from_numpy(x.copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(ours, theirs)
+
+
+def test_bf16_special_cases(orc):
+    def nb(bits):  # narrow raw fp32 bit patterns (arrays keep signaling NaNs intact)
+        return orc.to_bf16_bits(np.array([bits], np.uint32).view(np.float32))[0]
+    # exact ties round to even: 1 + 2^-8 (0x3F808000) -> 0x3F80; 0x3F818000 -> 0x3F82
+    assert nb(0x3F808000) == 0x3F80
+    assert nb(0x3F818000) == 0x3F82
+    # overflow to inf through the carry
+    assert nb(0x7F7FFFFF) == 0x7F80
+    # NaN keeps NaN-ness; a payload living only in the dropped bits is quieted
+    assert nb(0x7F800001) == 0x7FC0
+    assert nb(0xFFC00000) == 0xFFC0
+    assert nb(0x7F810000) == 0x7F81
+    # widening is exact
+    b = np.arange(0, 1 << 16, dtype=np.uint16)
+    assert np.array_equal(orc.bf16_bits_to_f32(b).view(np.uint32), b.astype(np.uint32) << 16)
+
+
+# ------------------------------------------------------------------ exp
+def test_exp_scalar_ulp_bound_and_domain(orc):
+    xs = np.linspace(-87.33, 88.37, 200001, dtype=np.float32)
+    ours = np.array([orc.exp_scalar(float(x)) for x in xs[::20]], np.float32)
+    truth = np.exp(xs[::20].astype(np.float64)).astype(np.float32)
+    ulp = np.abs(ours.view(np.int32).astype(np.int64) - truth.view(np.int32).astype(np.int64))
+    assert ulp.max() <= 2
+    assert orc.exp_scalar(-87.34) == 0.0 and orc.exp_scalar(float("-inf")) == 0.0
+    assert orc.exp_scalar(0.0) == 1.0
+    assert orc.exp_scalar(1000.0) == orc.exp_scalar(88.3762626647949)
+    assert math.isnan(orc.exp_scalar(float("nan")))
+
+
+def test_exp_avx2_ulp_bound(orc):
+    xs = np.linspace(-87.33, 88.37, 80000, dtype=np.float32)
+    ours = orc.exp_avx2(xs)
+    truth = np.exp(xs.astype(np.float64)).astype(np.float32)
+    ulp = np.abs(ours.view(np.int32).astype(np.int64) - truth.view(np.int32).astype(np.int64))
+    assert ulp.max() <= 2
+    assert orc.exp_avx2(np.full(8, -100.0, np.float32)).max() == 0.0
+
+
+@needs_ref
+def test_exp_scalar_bit_exact_vs_reference(orc):
+    R = orc.ref()
+    xs = np.linspace(-90.0, 90.0, 30001, dtype=np.float32)
+    for x in xs:
+        assert orc.exp_scalar(float(x)) == R.ref_exp_scalar(float(x)) or (
+            math.isnan(orc.exp_scalar(float(x))))
+
+
+# ------------------------------------------------------------------ attention vs HF goldens
+CASES = ["l0_prefill_empty", "l1_prefill_empty", "l0_prefill_continue", "l1_prefill_continue",
+         "l0_decode"]
+
+
+@pytest.mark.parametrize("name", CASES)
+def test_cpu_attention_matches_hf_goldens(orc, golden, name):
+    # rtol/atol 1e-4 as tests/unit/attention_test.cpp:153-176 uses.
+    q, k, v, ctx = (golden[f"{name}.{s}"] for s in ("q_rot", "k_all", "v_all", "ctx"))
+    out = orc.cpu_attention(q, k, v, 4, 2, 16, 0.25)
+    assert allclose_ref(out, ctx, 1e-4, 1e-4)
+
+
+@pytest.mark.parametrize("name", CASES)
+@pytest.mark.parametrize("isa", [0, 1])
+def test_prefill_units_match_hf_goldens(orc, golden, name, isa):
+    q, k, v, ctx = (golden[f"{name}.{s}"] for s in ("q_rot", "k_all", "v_all", "ctx"))
+    out = orc.prefill(q, k, v, 4, 2, 16, 0.25, isa=isa)
+    assert allclose_ref(out, ctx, 1e-4, 1e-5)
+
+
+@pytest.mark.parametrize("name", CASES)
+@pytest.mark.parametrize("isa", [0, 1])
+def test_paged_decode_matches_hf_goldens(orc, golden, name, isa):
+    # The last query row of each case is the decode of its final token
+    # (tests/unit/paged_decode_attention_kernel_test.cpp:388-444, bs = 8).
+    q, k, v, ctx = (golden[f"{name}.{s}"] for s in ("q_rot", "k_all", "v_all", "ctx"))
+    ks, vs, table = paged_layout(k, v, 8, extra_blocks=1)
+    out = orc.paged_decode(q[-1], ks, vs, table, k.shape[1], 4, 2, 16, 8, 0.25, isa=isa)
+    assert allclose_ref(out, ctx[-1], 1e-4, 1e-4)
+
+
+# ------------------------------------------------------------------ closed forms / brute force
+def test_single_key_returns_v_row_of_group_head(orc):
+    # L = 1: softmax over one key is 1, so out[h] = v[h // g, 0] exactly; a
+    # head-to-kv-head mapping of h % Hkv instead of h // g fails this.
+    rng = np.random.default_rng(3)
+    H, Hkv, d = 8, 2, 16
+    q = normal(rng, (1, H, d))
+    k = normal(rng, (Hkv, 1, d))
+    v = normal(rng, (Hkv, 1, d))
+    out = orc.cpu_attention(q, k, v, H, Hkv, d, 0.25)
+    for h in range(H):
+        assert np.array_equal(out[0, h], v[h // 4, 0])
+    ks, vs, table = paged_layout(k, v, 16)
+    out2 = orc.paged_decode(q[0], ks, vs, table, 1, H, Hkv, d, 16, 0.25)
+    for h in range(H):
+        assert np.array_equal(out2[h], v[h // 4, 0])
+
+
+def test_equal_keys_average_values(orc):
+    rng = np.random.default_rng(4)
+    H, Hkv, d, L = 4, 1, 32, 100
+    q = normal(rng, (1, H, d))
+    k = np.repeat(normal(rng, (Hkv, 1, d)), L, axis=1)
+    v = normal(rng, (Hkv, L, d))
+    ks, vs, table = paged_layout(k, v, 16, rng=rng)
+    out = orc.paged_decode(q[0], ks, vs, table, L, H, Hkv, d, 16, scale_for(d))
+    np.testing.assert_allclose(out, np.broadcast_to(v[0].mean(0), (H, d)), rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("H,Hkv,d,L", [(4, 4, 18, 70), (8, 1, 24, 129), (24, 2, 64, 300),
+                                       (14, 2, 64, 513)])
+def test_paged_decode_vs_fp64_brute_force(orc, H, Hkv, d, L):
+    rng = np.random.default_rng(L)
+    q = normal(rng, (1, H, d))
+    k = normal(rng, (Hkv, L, d))
+    v = normal(rng, (Hkv, L, d))
+    truth = brute_force_f64(q, k, v, H, Hkv, scale_for(d))[0]
+    for isa in (0, 1):
+        ks, vs, table = paged_layout(k, v, 16, extra_blocks=3, rng=rng)
+        out = orc.paged_decode(q[0], ks, vs, table, L, H, Hkv, d, 16, scale_for(d), isa=isa)
+        assert allclose_ref(out, truth, 1e-4, 1e-5)
+    assert allclose_ref(orc.cpu_attention(q, k, v, H, Hkv, d, scale_for(d))[0], truth,
+                        1e-4, 1e-5)
+
+
+def test_causal_mask_prefill_continue_vs_brute_force(orc):
+    rng = np.random.default_rng(5)
+    H, Hkv, d, P, T = 8, 2, 32, 37, 45
+    q = normal(rng, (T, H, d))
+    k = normal(rng, (Hkv, P + T, d))
+    v = normal(rng, (Hkv, P + T, d))
+    truth = brute_force_f64(q, k, v, H, Hkv, scale_for(d))
+    assert allclose_ref(orc.cpu_attention(q, k, v, H, Hkv, d, scale_for(d)), truth, 1e-4, 1e-5)
+    assert allclose_ref(orc.prefill(q, k, v, H, Hkv, d, scale_for(d)), truth, 1e-4, 1e-5)
+
+
+def test_paged_rejects_block_size_not_dividing_64(orc):
+    k = np.zeros((2, 40, 64), np.float32)
+    ks, vs, table = paged_layout(k, k, 24)
+    with pytest.raises(ValueError):
+        orc.paged_decode(np.zeros((4, 64), np.float32), ks, vs, table, 40, 4, 2, 64, 24, 0.125)
+
+
+# ------------------------------------------------------------------ bitwise invariants
+@pytest.mark.parametrize("bs", [8, 16, 32, 64])
+@pytest.mark.parametrize("L", [1, 7, 63, 64, 65, 129, 511])
+def test_paged_equals_contiguous_bitwise(orc, bs, L):
+    rng = np.random.default_rng(bs * 1000 + L)
+    H, Hkv, d = 4, 2, 64
+    q = normal(rng, (H, d))
+    k = normal(rng, (Hkv, L, d))
+    v = normal(rng, (Hkv, L, d))
+    ks, vs, table = paged_layout(k, v, bs)
+    for isa in (0, 1):
+        assert np.array_equal(orc.paged_decode(q, ks, vs, table, L, H, Hkv, d, bs, 0.125, isa=isa),
+                              orc.decode_contig(q, k, v, H, Hkv, d, 0.125, isa=isa))
+
+
+def test_batched_equals_per_member_and_threads_invariant(orc):
+    rng = np.random.default_rng(9)
+    H, Hkv, d, bs = 14, 2, 64, 16
+    lens = [1, 16, 33, 63, 128, 300]
+    ks = [normal(rng, (Hkv, L, d)) for L in lens]
+    vs = [normal(rng, (Hkv, L, d)) for L in lens]
+    kslab, vslab, tables = shared_pool_layout(ks, vs, bs, rng)
+    q = normal(rng, (len(lens), H, d))
+    for isa in (0, 1):
+        orc.set_threads(1)
+        a = orc.paged_decode_batched(q, kslab, vslab, tables, lens, H, Hkv, d, bs, 0.125, isa=isa)
+        orc.set_threads(6)
+        b = orc.paged_decode_batched(q, kslab, vslab, tables, lens, H, Hkv, d, bs, 0.125, isa=isa)
+        assert np.array_equal(a, b)
+        for i, L in enumerate(lens):
+            assert np.array_equal(a[i], orc.paged_decode(q[i], kslab, vslab, tables[i], L, H, Hkv,
+                                                         d, bs, 0.125, isa=isa))
+    orc.set_threads(1)
+    assert orc.paged_decode_batched(q[:0], kslab, vslab, [], [], H, Hkv, d, bs, 0.125).shape[0] == 0
+
+
+# ------------------------------------------------------------------ vs the reference's own code
+@needs_ref
+@pytest.mark.parametrize("isa", [0, 1])
+@pytest.mark.parametrize("H,Hkv,d,bs", [(14, 2, 64, 16), (32, 8, 128, 16), (4, 2, 16, 8),
+                                        (24, 2, 24, 32), (8, 1, 18, 64)])
+def test_paged_batched_bit_exact_vs_reference_build(orc, isa, H, Hkv, d, bs):
+    rng = np.random.default_rng(H * d + bs)
+    lens = [int(x) for x in rng.integers(1, 700, 7)]
+    ks = [normal(rng, (Hkv, L, d)) for L in lens]
+    vs = [normal(rng, (Hkv, L, d)) for L in lens]
+    kslab, vslab, tables = shared_pool_layout(ks, vs, bs, rng)
+    q = normal(rng, (len(lens), H, d))
+    sc = scale_for(d)
+    ours = orc.paged_decode_batched(q, kslab, vslab, tables, lens, H, Hkv, d, bs, sc, isa=isa)
+    theirs = orc.paged_decode_batched(q, kslab, vslab, tables, lens, H, Hkv, d, bs, sc, isa=isa,
+                                      use_ref=True)
+    assert np.array_equal(ours.view(np.uint32), theirs.view(np.uint32))
+
+
+@needs_ref
+@pytest.mark.parametrize("isa", [0, 1])
+def test_prefill_varlen_bit_exact_vs_reference_build(orc, isa):
+    rng = np.random.default_rng(77)
+    H, Hkv, d = 8, 2, 64
+    Ts = [1, 33, 70, 5]
+    Ps = [0, 17, 64, 200]
+    qs = normal(rng, (sum(Ts), H, d))
+    cu = np.concatenate([[0], np.cumsum(Ts)]).astype(np.int32)
+    ks = [normal(rng, (Hkv, P + T, d)) for P, T in zip(Ps, Ts)]
+    vs = [normal(rng, (Hkv, P + T, d)) for P, T in zip(Ps, Ts)]
+    a = orc.prefill_varlen(qs, cu, ks, vs, H, Hkv, d, 0.125, isa=isa)
+    b = orc.prefill_varlen(qs, cu, ks, vs, H, Hkv, d, 0.125, isa=isa, use_ref=True)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@needs_ref
+def test_scatter_gather_bit_exact_vs_reference_build(orc):
+    rng = np.random.default_rng(11)
+    Hkv, d, bs, nb = 3, 40, 16, 23
+    T = 150
+    slots = rng.permutation(nb * bs)[:T].astype(np.int64)
+    sk = normal(rng, (T, Hkv, d))
+    sv = normal(rng, (T, Hkv, d))
+    a_k = np.full((nb, Hkv, bs, d), 7.0, np.float32)
+    a_v = a_k.copy()
+    b_k, b_v = a_k.copy(), a_k.copy()
+    orc.kv_scatter(sk, sv, slots, Hkv, d, bs, a_k, a_v)
+    orc.kv_scatter(sk, sv, slots, Hkv, d, bs, b_k, b_v, use_ref=True)
+    assert np.array_equal(a_k, b_k) and np.array_equal(a_v, b_v)
+    table = rng.permutation(nb).astype(np.int32)
+    for L in (0, 1, 15, 16, 17, 200):
+        g1 = orc.kv_gather(a_k, a_v, table, bs, L, Hkv, d)
+        g2 = orc.kv_gather(a_k, a_v, table, bs, L, Hkv, d, use_ref=True)
+        assert np.array_equal(g1[0], g2[0]) and np.array_equal(g1[1], g2[1])
+
+
+# ------------------------------------------------------------------ scatter closed form
+def test_scatter_closed_form_and_round_trip(orc):
+    # dst = ((block * Hkv + h) * bs + p) * d with block = slot / bs, p = slot % bs
+    # (src/kernels/kv_scatter.cpp:33-40); gather inverts it for a table walk.
+    rng = np.random.default_rng(12)
+    Hkv, d, bs, nb = 2, 8, 8, 9
+    table = rng.permutation(nb)[:5].astype(np.int32)
+    L = 37
+    slots = np.array([table[p // bs] * bs + p % bs for p in range(L)], np.int64)
+    sk = normal(rng, (L, Hkv, d))
+    sv = normal(rng, (L, Hkv, d))
+    ksl = np.zeros((nb, Hkv, bs, d), np.float32)
+    vsl = np.zeros_like(ksl)
+    orc.kv_scatter(sk, sv, slots, Hkv, d, bs, ksl, vsl)
+    flat = ksl.reshape(-1)
+    for t in range(L):
+        for h in range(Hkv):
+            blk, p = divmod(int(slots[t]), bs)
+            off = ((blk * Hkv + h) * bs + p) * d
+            assert np.array_equal(flat[off:off + d], sk[t, h])
+    gk, gv = orc.kv_gather(ksl, vsl, table, bs, L, Hkv, d)
+    assert np.array_equal(gk, sk.transpose(1, 0, 2)) and np.array_equal(gv, sv.transpose(1, 0, 2))
+    # bf16 storage: same addressing, element-wise RNE narrowing
+    kb = np.zeros((nb, Hkv, bs, d), np.uint16)
+    vb = np.zeros_like(kb)
+    orc.kv_scatter(sk, sv, slots, Hkv, d, bs, kb, vb)
+    assert np.array_equal(kb, orc.to_bf16_bits(ksl) * (ksl != 0) + 0 * kb)
