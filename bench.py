@@ -1,0 +1,233 @@
+#!/usr/bin/env python3
+"""Benchmark of the ragged paged-attention decode step on one MI355X.
+
+One step = one scheduler step of the configured workload (default C4: the
+Llama-3-8B-shape 256-sequence ragged bf16-KV decode, 32 layers): one step
+descriptor upload (host packing + one async copy), then per layer the
+KV-append of the step's new token rows and one attention launch over every
+sequence. All K/V pools, queries and new rows are resident in HBM before the
+timed region (synthetic N(0, 0.5) data from a device-side generator).
+
+Prints ONE JSON line (metric/value/unit as BASELINE.json names them):
+  value      = algorithmic HBM bytes of the step (unique K/V + Q + O + tables
+               + append) / step time, in GB/s;
+  roofline   = the attention kernel alone: its algorithmic bytes per launch /
+               its average launch duration (HIP events on the launch stream);
+  cpu_baseline = the oracle's AVX2 restatement of the reference's batched
+               paged decode, timed on this host on a bounded fp32 sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "llm-inference-engine_amd" / "python"))
+sys.path.insert(0, str(ROOT))
+
+import numpy as np  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="C4", choices=["C2", "C3", "C4", "C5"])
+    ap.add_argument("--layers", type=int, default=0, help="override the config's layer count")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+def traffic_from_profiles(config: str):
+    """HBM bytes per attention launch from the committed rocprofv3 PMC summary
+    (FETCH_SIZE / WRITE_SIZE per dispatch, each scaled by the same counter's
+    reading on a copy kernel of known size), or None."""
+    p = ROOT / "profiles" / f"decode_{config.lower()}_traffic.json"
+    if not p.exists():
+        return None
+    t = json.loads(p.read_text())
+    return (t["fetch_kib_per_dispatch"] * t["fetch_scale"]
+            + t["write_kib_per_dispatch"] * t["write_scale"]) * 1024.0
+
+
+def cpu_baseline(w, seconds: float):
+    """Oracle AVX2 batched paged decode (bit-identical restatement of the
+    reference's PagedDecodeAttentionBatchedF32) on a bounded fp32 sample of
+    the workload: its first 32 sequences, one layer."""
+    from oracle import oracle as orc
+    threads = max(1, min(16, os.cpu_count() or 1))
+    orc.set_threads(threads)
+    B = min(32, w.num_seqs)
+    lens = [int(x) for x in w.context_lens[:B]]
+    H, Hkv, d, bs = w.heads, w.kv_heads, w.head_dim, w.block_size
+    need = [(L + bs - 1) // bs for L in lens]
+    nb = sum(need)
+    rng = np.random.default_rng(0)
+    k = (rng.standard_normal((nb, Hkv, bs, d), dtype=np.float32) * 0.5)
+    v = (rng.standard_normal((nb, Hkv, bs, d), dtype=np.float32) * 0.5)
+    perm = rng.permutation(nb).astype(np.int32)
+    tables, off = [], 0
+    for n in need:
+        tables.append(perm[off:off + n].copy())
+        off += n
+    q = (rng.standard_normal((B, H, d), dtype=np.float32) * 0.5)
+    times = []
+    t_end = time.perf_counter() + seconds
+    while len(times) < 3 or time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        orc.paged_decode_batched(q, k, v, tables, lens, H, Hkv, d, bs, w.scale, isa=orc.ISA_AVX2)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 200:
+            break
+    t = float(np.median(times))
+    kv_bytes = Hkv * d * 4 * 2 * sum(lens)
+    bytes_ = kv_bytes + 4 * B * H * d * 2 + 4 * nb + 8 * B
+    return {"value": round(bytes_ / t / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": (f"oracle AVX2 PagedDecodeAttentionBatchedF32 restatement, fp32 K/V, "
+                       f"first {B} sequences of {w.name} (sum L={sum(lens)}), 1 layer, median of "
+                       f"{len(times)} calls"),
+            "attended_kv_tok_per_s": round(sum(lens) / t, 1),
+            "ms_per_call": round(t * 1e3, 3)}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
+              "the per-GPU throughput at N=1 is the figure it reports", file=sys.stderr)
+        sys.exit(2)
+    import ehip
+    from ehip import workloads
+
+    w = workloads.CONFIGS[args.config]()
+    layers = args.layers or w.layers
+    H, Hkv, d, bs = w.heads, w.kv_heads, w.head_dim, w.block_size
+    R = w.rows
+    kvb = w.kv_bytes
+    slab_bytes = w.pool_blocks * Hkv * bs * d * kvb
+    log(f"[bench] {w.name}: B={w.num_seqs} rows={R} sumL={int(w.context_lens.sum())} "
+        f"pool={w.pool_blocks} blocks, {layers} layers, slabs {2 * layers * slab_bytes / 2**30:.1f} GiB")
+
+    ctx = ehip.Context(0)
+    slabs, qs, kns, vns, outs = [], [], [], [], []
+    for layer in range(layers):
+        ks, vs = ctx.alloc(slab_bytes), ctx.alloc(slab_bytes)
+        ctx.fill_normal(ks, w.pool_blocks * Hkv * bs * d, w.kv_dtype, 0.0, w.qkv_std, 10 + layer)
+        ctx.fill_normal(vs, w.pool_blocks * Hkv * bs * d, w.kv_dtype, 0.0, w.qkv_std, 1000 + layer)
+        slabs.append((ks, vs))
+        q, kn, vn = ctx.alloc(R * H * d * 4), ctx.alloc(R * Hkv * d * 4), ctx.alloc(R * Hkv * d * 4)
+        ctx.fill_normal(q, R * H * d, ehip.KV_F32, 0.0, w.qkv_std, 2000 + layer)
+        ctx.fill_normal(kn, R * Hkv * d, ehip.KV_F32, 0.0, w.qkv_std, 3000 + layer)
+        ctx.fill_normal(vn, R * Hkv * d, ehip.KV_F32, 0.0, w.qkv_std, 4000 + layer)
+        qs.append(q)
+        kns.append(kn)
+        vns.append(vn)
+        outs.append(ctx.alloc(R * H * d * 4))
+    ctx.sync()
+    log("[bench] pools resident")
+
+    g = ehip.geometry(H, Hkv, d, bs, w.kv_dtype, w.pool_blocks, w.scale)
+    st = ehip.StepArrays(w.query_lens, w.context_lens, w.tables, w.slot_mapping)
+
+    def step(evs=None):
+        ctx._check(ctx.step_upload(g, st))
+        for layer in range(layers):
+            ks, vs = slabs[layer]
+            ctx._check(ctx.step_kv_append(kns[layer], vns[layer], ks, vs))
+            if evs is not None:
+                ctx.record(evs[layer][0])
+            ctx._check(ctx.step_attention(qs[layer], ks, vs, outs[layer]))
+            if evs is not None:
+                ctx.record(evs[layer][1])
+
+    for _ in range(args.warmup):
+        step()
+    ctx.sync()
+    log("[bench] warmup done")
+    rows, items, partials = ctx.step_info()
+
+    K = args.steps
+    evs = [[(ctx.event(), ctx.event()) for _ in range(layers)] for _ in range(K)]
+    e_start, e_end = ctx.event(), ctx.event()
+    ctx.sync()
+    t0 = time.perf_counter()
+    ctx.record(e_start)
+    for s in range(K):
+        step(evs[s])
+    ctx.record(e_end)
+    ctx.sync()
+    wall = time.perf_counter() - t0
+    gpu_ms = ctx.elapsed_ms(e_start, e_end)
+    attn_ms = [ctx.elapsed_ms(a, b) for per in evs for (a, b) in per]
+    log(f"[bench] timed {K} steps: wall {wall * 1e3:.2f} ms, events {gpu_ms:.2f} ms")
+
+    t_step = max(wall, gpu_ms / 1e3) / K
+    per_layer = w.bytes_per_layer(with_append=True)
+    step_bytes = per_layer["total"] * layers
+    value = step_bytes / t_step / 1e9
+    attn_bytes = per_layer["unique_kv"] + per_layer["q_o"] + per_layer["tables"]
+    attn_avg = float(np.mean(attn_ms)) / 1e3
+    achieved = attn_bytes / attn_avg / 1e9
+    tok = int(w.context_lens.sum())
+    traffic = traffic_from_profiles(w.name)
+
+    result = {
+        "metric": "ragged paged-attn decode: HBM GB/s (% of 8 TB/s) + attended KV tok/s per step",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(t_step * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": (f"{w.name}: {w.num_seqs} sequences, {layers} layers, H={H} Hkv={Hkv} "
+                         f"d={d} bs={bs}, kv {'bf16' if w.kv_dtype else 'fp32'}, "
+                         f"sum L={tok}, rows={R}"),
+            "kv_dtype": "bf16" if w.kv_dtype else "f32",
+            "num_seqs": w.num_seqs, "layers": layers, "sum_context": tok,
+            "work_items": items, "split_partials": partials,
+            "parallelism": "single GPU",
+        },
+        "hbm_frac": round(value / HBM_PEAK_GBS, 4),
+        "attended_kv_tok_per_s": round(tok * layers / t_step, 1),
+        "bytes_per_step": step_bytes,
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "kernel": "paged decode attention (one launch per layer)",
+            "algorithmic_bytes_per_launch": attn_bytes,
+            "avg_launch_us": round(attn_avg * 1e6, 3),
+        },
+    }
+    if not args.no_cpu_baseline:
+        log("[bench] cpu baseline ...")
+        result["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
+    ctx.close()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,209 @@
+/*
+ * ehip.h — C ABI of the MI355X (gfx950) paged-attention path.
+ *
+ * This is the single device boundary of the engine's attention hot path: the
+ * host C++ (kvcache bookkeeping, step packing) and any foreign caller (ctypes,
+ * cgo, JNI) call HIP only through these functions. Plain pointers and sizes;
+ * no C++ or framework types cross it.
+ *
+ * Conventions
+ *   - Every function returns an int status with the values of the reference's
+ *     core::StatusCode (src/core/status.h:52-64): 0 OK, 2 InvalidArgument,
+ *     5 FailedPrecondition, 7 ResourceExhausted, 8 OutOfMemory,
+ *     9 Unimplemented, 11 Internal. On failure ehip_last_error() holds a
+ *     message. Where the reference CHECK-aborts on a programmer error
+ *     (block_size not dividing 64, src/kernels/paged_attention.cpp:88-91) this
+ *     ABI returns InvalidArgument instead, so a foreign caller can recover.
+ *   - Pointers named d_* are device (HBM) pointers, normally from
+ *     ehip_malloc. Pointers named h_* are host memory; they are read before
+ *     the call returns and may be reused immediately.
+ *   - Compute calls are asynchronous on the context's stream (all-or-nothing:
+ *     argument validation happens before anything is enqueued). ehip_sync()
+ *     waits, and reports device-side range errors (a slot or block id outside
+ *     the slab, which the kernels skip instead of touching memory out of
+ *     bounds).
+ *   - Slabs use the reference layout [slab_blocks, Hkv, bs, d]
+ *     (docs/design/paged-kv-cache.md:146-160): block id `blk` at
+ *     blk*block_stride elements, kv head `hk` at +hk*bs*d, slot p at +p*d.
+ *     KV element type is fp32 or bf16 (bf16 = the reference's
+ *     Fp32ToBf16Bits round-to-nearest-even, src/tensor/half.h:112-124).
+ *   - Queries and outputs are fp32, [rows, H, d] contiguous; arithmetic is
+ *     fp32 throughout (bf16 K/V are widened exactly).
+ *   - A context is used from one host thread at a time (the reference's
+ *     single engine thread, src/runtime/engine.h:27-33).
+ */
+#ifndef EHIP_H_
+#define EHIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  EHIP_OK = 0,
+  EHIP_INVALID_ARGUMENT = 2,
+  EHIP_FAILED_PRECONDITION = 5,
+  EHIP_RESOURCE_EXHAUSTED = 7,
+  EHIP_OUT_OF_MEMORY = 8,
+  EHIP_UNIMPLEMENTED = 9,
+  EHIP_INTERNAL = 11
+};
+
+enum { EHIP_KV_F32 = 0, EHIP_KV_BF16 = 1 };
+
+typedef struct ehip_ctx ehip_ctx;
+
+/* Attention geometry of one model (constant across layers and steps).
+ * Mirrors kvcache::CacheGeometry (src/kvcache/kv_cache.h:45-50) plus the
+ * per-call scalars the reference kernels take (paged_attention.h:50-57). */
+typedef struct {
+  int32_t heads;        /* H (query heads)                                   */
+  int32_t kv_heads;     /* Hkv; H % Hkv == 0, group g = H / Hkv              */
+  int32_t head_dim;     /* d                                                 */
+  int32_t block_size;   /* bs in {8,16,32,64} (src/kvcache/block_pool.cpp:28-31) */
+  int32_t kv_dtype;     /* EHIP_KV_F32 or EHIP_KV_BF16                       */
+  int32_t reserved;     /* must be 0                                         */
+  int64_t slab_blocks;  /* blocks in each slab (bounds every block id)       */
+  int64_t block_stride; /* elements per block id; 0 = Hkv*bs*d               */
+  float scale;          /* multiplies the finished q.k dot (HF order)        */
+} ehip_geometry;
+
+/* One scheduler step (ragged): B sequences, sequence b contributes T_b query
+ * rows (1 for decode, a causal chunk for prefill) at the END of its context
+ * of L_b tokens (post-append), i.e. at positions L_b-T_b .. L_b-1, and
+ * attends keys [0, position] (src/kernels/attention.h:221-227 for chunks,
+ * src/kernels/paged_attention.h:105-110 for T_b == 1). Rows are packed
+ * sequence-major like engine::BatchInputs::cu_seqlens
+ * (src/engine/batch.h:81-103). */
+typedef struct {
+  int32_t num_seqs;              /* B >= 0                                   */
+  int32_t reserved;              /* must be 0                                */
+  const int32_t* h_query_lens;   /* [B]   T_b >= 1                           */
+  const int64_t* h_context_lens; /* [B]   L_b >= T_b (post-append)           */
+  const int32_t* h_table_offsets;/* [B+1] CSR offsets into h_table_ids       */
+  const int32_t* h_table_ids;    /* [offsets[B]] physical block ids, >= ceil(L_b/bs) per seq */
+  const int64_t* h_slot_mapping; /* [sum T_b] slots of the appended tokens, or NULL */
+} ehip_step_desc;
+
+/* ------------------------------------------------------------ context ---- */
+int ehip_init(int device, ehip_ctx** out);
+int ehip_destroy(ehip_ctx* ctx);
+/* Copies the last failure message (NUL-terminated, truncated to n). */
+int ehip_last_error(const ehip_ctx* ctx, char* buf, size_t n);
+/* Device count, without creating a context (0 when no GPU is visible). */
+int ehip_device_count(int* out);
+/* Waits for all enqueued work; returns InvalidArgument if a kernel skipped an
+ * out-of-range slot or block id since the previous ehip_sync. */
+int ehip_sync(ehip_ctx* ctx);
+
+/* ------------------------------------------------------------ memory ----- */
+/* HBM allocation, 256-byte aligned, zero-filled (the reference BlockPool
+ * zero-fills its slabs, src/kvcache/block_pool.cpp:195-220). */
+int ehip_malloc(ehip_ctx* ctx, int64_t bytes, void** d_out);
+int ehip_free(ehip_ctx* ctx, void* d_ptr);
+/* Blocking copies (stream-ordered behind all enqueued work). */
+int ehip_copy_to_device(ehip_ctx* ctx, void* d_dst, const void* h_src, int64_t bytes);
+int ehip_copy_to_host(ehip_ctx* ctx, void* h_dst, const void* d_src, int64_t bytes);
+int ehip_copy_device(ehip_ctx* ctx, void* d_dst, const void* d_src, int64_t bytes);
+/* Synthetic N(mean, std) fill on the device (counter-based hash + Box-Muller;
+ * for benchmarks whose pools are too large to generate on the host).
+ * dtype: EHIP_KV_F32 writes float, EHIP_KV_BF16 writes RNE bf16 bits. */
+int ehip_fill_normal(ehip_ctx* ctx, void* d_dst, int64_t n, int32_t dtype, float mean,
+                     float stddev, uint64_t seed);
+
+/* ------------------------------------------------------------ timing ----- */
+/* HIP events on the context's stream (the stream every kernel runs on). */
+int ehip_event_create(ehip_ctx* ctx, void** ev_out);
+int ehip_event_destroy(ehip_ctx* ctx, void* ev);
+int ehip_event_record(ehip_ctx* ctx, void* ev);
+int ehip_event_elapsed_ms(ehip_ctx* ctx, void* ev_start, void* ev_end, float* ms_out);
+
+/* ----------------------------------------- reference kernel entry points --
+ * Device-pointer versions of the reference kernels-module API, same argument
+ * meaning and order, plus the slab capacity (`slab_blocks`) that lets the
+ * kernels bound every block id they dereference. */
+
+/* kernels::KvScatterF32 (src/kernels/kv_scatter.h:47-50,
+ * src/kernels/kv_scatter.cpp:27-61): token t's K/V rows (src [T, Hkv, d],
+ * token-major) go to slot slot_mapping[t] = block*bs + p, head h at
+ * ((block*Hkv + h)*bs + p)*d. Bit-exact copy. */
+int ehip_kv_scatter_f32(ehip_ctx* ctx, const float* d_src_k, const float* d_src_v,
+                        const int64_t* d_slot_mapping, int64_t t_dim, int64_t kv_heads,
+                        int64_t d, int64_t block_size, int64_t slab_blocks, float* d_k_slab,
+                        float* d_v_slab);
+/* The same scatter into bf16 slabs; every element narrowed with the
+ * reference's Fp32ToBf16Bits (src/tensor/half.h:112-124), bit-exact. */
+int ehip_kv_scatter_bf16(ehip_ctx* ctx, const float* d_src_k, const float* d_src_v,
+                         const int64_t* d_slot_mapping, int64_t t_dim, int64_t kv_heads,
+                         int64_t d, int64_t block_size, int64_t slab_blocks,
+                         uint16_t* d_k_slab, uint16_t* d_v_slab);
+
+/* kernels::KvGatherF32 (src/kernels/kv_gather.h:55-58,
+ * src/kernels/kv_gather.cpp:63-89): paged -> contiguous [Hkv, L, d]. */
+int ehip_kv_gather_f32(ehip_ctx* ctx, const float* d_k_slab, const float* d_v_slab,
+                       const int32_t* d_block_table, int64_t block_size, int64_t length,
+                       int64_t kv_heads, int64_t d, int64_t slab_blocks, float* d_out_k,
+                       float* d_out_v);
+
+/* kernels::PagedDecodeAttentionF32 (src/kernels/paged_attention.h:50-57):
+ * out[H,d] = softmax(scale * q.K^T) V over keys [0, length-1] read through
+ * d_block_table. block_size must divide 64 (else InvalidArgument). */
+int ehip_paged_decode_attention_f32(ehip_ctx* ctx, const float* d_q, const float* d_k_slab,
+                                    const float* d_v_slab, const int32_t* d_block_table,
+                                    int64_t num_blocks, int64_t length, int64_t heads,
+                                    int64_t kv_heads, int64_t d, int64_t block_size,
+                                    int64_t block_stride, int64_t slab_blocks, float scale,
+                                    float* d_out);
+
+/* kernels::PagedDecodeAttentionBatchedF32 (src/kernels/paged_attention.h:105-110):
+ * B sequences over one shared slab pair. Like the reference, the tables are
+ * host arrays of per-sequence pointers (h_block_tables[b] has
+ * >= ceil(h_lengths[b]/bs) entries); they are packed into one CSR descriptor
+ * and uploaded with a single copy. q/out [B, H, d]. B == 0 is a no-op. */
+int ehip_paged_decode_attention_batched_f32(
+    ehip_ctx* ctx, const float* d_q, const float* d_k_slab, const float* d_v_slab,
+    const int32_t* const* h_block_tables, const int64_t* h_lengths, int64_t num_seqs,
+    int64_t heads, int64_t kv_heads, int64_t d, int64_t block_size, int64_t block_stride,
+    int64_t slab_blocks, float scale, float* d_out);
+/* The bf16-KV variant of the batched decode (slabs hold bf16 bits). */
+int ehip_paged_decode_attention_batched_bf16(
+    ehip_ctx* ctx, const float* d_q, const uint16_t* d_k_slab, const uint16_t* d_v_slab,
+    const int32_t* const* h_block_tables, const int64_t* h_lengths, int64_t num_seqs,
+    int64_t heads, int64_t kv_heads, int64_t d, int64_t block_size, int64_t block_stride,
+    int64_t slab_blocks, float scale, float* d_out);
+
+/* ------------------------------------------------ step path (hot path) ----
+ * One descriptor upload per scheduler step, then per layer one append and one
+ * attention launch covering every sequence (decode rows and prefill chunks
+ * alike). Replaces the per-sequence loops of OptimizedModel::BatchedAttention
+ * (src/model/optimized_model.cpp:370-467) and PagedKvCache::append
+ * (src/kvcache/paged_cache.cpp:62-123). Block tables are layer-independent
+ * (src/kvcache/block_pool.h:22-24), so one upload serves every layer. */
+
+/* Validates the step against the geometry, builds the work list (split-KV
+ * partition, load-balanced order) and uploads it with one async copy. */
+int ehip_step_upload(ehip_ctx* ctx, const ehip_geometry* geom, const ehip_step_desc* step);
+/* Append the step's new K/V rows (src [sum T_b, Hkv, d] fp32) at the uploaded
+ * slot mapping; slabs are fp32 or bf16 per geom.kv_dtype. */
+int ehip_step_kv_append(ehip_ctx* ctx, const float* d_src_k, const float* d_src_v,
+                        void* d_k_slab, void* d_v_slab);
+/* Attention for every row of the step: q/out [sum T_b, H, d] fp32. */
+int ehip_step_attention(ehip_ctx* ctx, const float* d_q, const void* d_k_slab,
+                        const void* d_v_slab, float* d_out);
+/* Counts of the uploaded plan (rows, work items, split partials). */
+int ehip_step_info(const ehip_ctx* ctx, int64_t* rows, int64_t* items, int64_t* partials);
+
+/* ------------------------------------------------ host-only planning ------
+ * The work-list builder behind ehip_step_upload, callable without a GPU (for
+ * tests of the host logic). Fills the counts the plan would have. */
+int ehip_plan_counts(const ehip_geometry* geom, const ehip_step_desc* step, int64_t* rows,
+                     int64_t* items, int64_t* partials, int32_t* split_tokens);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EHIP_H_ */

@@ -1,0 +1,587 @@
+// C-ABI implementation: context, HBM memory, events, the per-step descriptor
+// upload and the launch entry points (declared in include/ehip.h).
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "ehip.h"
+#include "kernels.h"
+#include "plan.h"
+
+struct ehip_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::string last_error;
+
+  // Step descriptor: host staging (pinned, double-buffered so building step
+  // n+1 never overwrites a buffer whose copy is still queued) and its device
+  // image.
+  void* h_stage[2] = {nullptr, nullptr};
+  hipEvent_t stage_done[2] = {nullptr, nullptr};
+  size_t h_stage_bytes[2] = {0, 0};
+  int stage_cur = 0;
+  void* d_desc = nullptr;
+  size_t d_desc_bytes = 0;
+
+  // Split-KV workspace and merge counters (counters stay zero between
+  // launches: the merging wavefront resets its own).
+  float* d_part = nullptr;
+  size_t d_part_bytes = 0;
+  int32_t* d_counters = nullptr;
+  size_t counters_len = 0;
+  int32_t* d_err = nullptr;
+
+  // The uploaded step.
+  bool have_step = false;
+  ehip_geometry geom{};
+  ehip::Plan plan;
+  const ehip::RowDesc* d_rows = nullptr;
+  const ehip::WorkItem* d_items = nullptr;
+  const int32_t* d_table = nullptr;
+  const int64_t* d_slots = nullptr;
+};
+
+namespace {
+
+using ehip::Plan;
+
+int SetError(ehip_ctx* ctx, int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  if (ctx) ctx->last_error = buf;
+  return code;
+}
+
+int HipFail(ehip_ctx* ctx, hipError_t e, const char* what) {
+  const int code = (e == hipErrorOutOfMemory) ? EHIP_OUT_OF_MEMORY : EHIP_INTERNAL;
+  return SetError(ctx, code, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define EHIP_HIP(ctx, expr)                                  \
+  do {                                                       \
+    hipError_t e_ = (expr);                                  \
+    if (e_ != hipSuccess) return HipFail((ctx), e_, #expr); \
+  } while (0)
+
+int CheckCtx(ehip_ctx* ctx) {
+  if (!ctx) return EHIP_INVALID_ARGUMENT;
+  hipError_t e = hipSetDevice(ctx->device);
+  if (e != hipSuccess) return HipFail(ctx, e, "hipSetDevice");
+  return EHIP_OK;
+}
+
+size_t Align256(size_t x) { return (x + 255) & ~size_t{255}; }
+
+// Grows the split workspace / counters to what `plan` needs.
+int EnsureWorkspace(ehip_ctx* ctx, const ehip_geometry& g, const Plan& plan) {
+  const int64_t grp = g.heads / g.kv_heads;
+  const size_t part_o = static_cast<size_t>(plan.partials) * grp * g.head_dim;
+  const size_t part_ml = static_cast<size_t>(plan.partials) * grp * 2;
+  const size_t need = Align256((part_o + part_ml) * sizeof(float));
+  if (need > ctx->d_part_bytes) {
+    const size_t bytes = std::max(need, ctx->d_part_bytes * 3 / 2);
+    EHIP_HIP(ctx, hipStreamSynchronize(ctx->stream));  // queued kernels may use it
+    if (ctx->d_part) EHIP_HIP(ctx, hipFree(ctx->d_part));
+    ctx->d_part = nullptr;
+    ctx->d_part_bytes = 0;
+    EHIP_HIP(ctx, hipMalloc(&ctx->d_part, bytes));
+    ctx->d_part_bytes = bytes;
+  }
+  const size_t ctrs = std::max<size_t>(1, plan.rows.size() * g.kv_heads);
+  if (ctrs > ctx->counters_len) {
+    const size_t len = std::max(ctrs, ctx->counters_len * 3 / 2);
+    EHIP_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (ctx->d_counters) EHIP_HIP(ctx, hipFree(ctx->d_counters));
+    ctx->d_counters = nullptr;
+    ctx->counters_len = 0;
+    EHIP_HIP(ctx, hipMalloc(&ctx->d_counters, len * sizeof(int32_t)));
+    EHIP_HIP(ctx, hipMemsetAsync(ctx->d_counters, 0, len * sizeof(int32_t), ctx->stream));
+    ctx->counters_len = len;
+  }
+  return EHIP_OK;
+}
+
+// Packs rows | items | table ids | slots into one pinned staging buffer and
+// uploads it with one async copy; records the device pointers of each part.
+int UploadPlan(ehip_ctx* ctx, const ehip_geometry& g, Plan&& plan, const int32_t* d_user_table) {
+  const size_t rows_b = Align256(plan.rows.size() * sizeof(ehip::RowDesc));
+  const size_t items_b = Align256(plan.items.size() * sizeof(ehip::WorkItem));
+  const size_t table_b = Align256(plan.table_ids.size() * sizeof(int32_t));
+  const size_t slots_b = Align256(plan.slots.size() * sizeof(int64_t));
+  const size_t total = std::max<size_t>(256, rows_b + items_b + table_b + slots_b);
+
+  const int cur = ctx->stage_cur;
+  ctx->stage_cur ^= 1;
+  if (ctx->stage_done[cur]) EHIP_HIP(ctx, hipEventSynchronize(ctx->stage_done[cur]));
+  if (total > ctx->h_stage_bytes[cur]) {
+    const size_t bytes = std::max(total, ctx->h_stage_bytes[cur] * 3 / 2);
+    if (ctx->h_stage[cur]) EHIP_HIP(ctx, hipHostFree(ctx->h_stage[cur]));
+    ctx->h_stage[cur] = nullptr;
+    ctx->h_stage_bytes[cur] = 0;
+    EHIP_HIP(ctx, hipHostMalloc(&ctx->h_stage[cur], bytes, hipHostMallocDefault));
+    ctx->h_stage_bytes[cur] = bytes;
+  }
+  if (total > ctx->d_desc_bytes) {
+    // The old descriptor may still be read by queued kernels: wait first.
+    const size_t bytes = std::max(total, ctx->d_desc_bytes * 3 / 2);
+    EHIP_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (ctx->d_desc) EHIP_HIP(ctx, hipFree(ctx->d_desc));
+    ctx->d_desc = nullptr;
+    ctx->d_desc_bytes = 0;
+    EHIP_HIP(ctx, hipMalloc(&ctx->d_desc, bytes));
+    ctx->d_desc_bytes = bytes;
+  }
+  char* h = static_cast<char*>(ctx->h_stage[cur]);
+  std::memcpy(h, plan.rows.data(), plan.rows.size() * sizeof(ehip::RowDesc));
+  std::memcpy(h + rows_b, plan.items.data(), plan.items.size() * sizeof(ehip::WorkItem));
+  std::memcpy(h + rows_b + items_b, plan.table_ids.data(), plan.table_ids.size() * sizeof(int32_t));
+  std::memcpy(h + rows_b + items_b + table_b, plan.slots.data(),
+              plan.slots.size() * sizeof(int64_t));
+  EHIP_HIP(ctx, hipMemcpyAsync(ctx->d_desc, h, total, hipMemcpyHostToDevice, ctx->stream));
+  if (!ctx->stage_done[cur]) EHIP_HIP(ctx, hipEventCreateWithFlags(&ctx->stage_done[cur],
+                                                                   hipEventDisableTiming));
+  EHIP_HIP(ctx, hipEventRecord(ctx->stage_done[cur], ctx->stream));
+
+  char* d = static_cast<char*>(ctx->d_desc);
+  ctx->d_rows = reinterpret_cast<const ehip::RowDesc*>(d);
+  ctx->d_items = reinterpret_cast<const ehip::WorkItem*>(d + rows_b);
+  ctx->d_table = d_user_table ? d_user_table
+                              : reinterpret_cast<const int32_t*>(d + rows_b + items_b);
+  ctx->d_slots = reinterpret_cast<const int64_t*>(d + rows_b + items_b + table_b);
+  if (int rc = EnsureWorkspace(ctx, g, plan)) return rc;
+  ctx->geom = g;
+  ctx->plan = std::move(plan);
+  ctx->have_step = true;
+  return EHIP_OK;
+}
+
+int LaunchAttention(ehip_ctx* ctx, const float* q, const void* k_slab, const void* v_slab,
+                    float* out) {
+  const ehip_geometry& g = ctx->geom;
+  const Plan& plan = ctx->plan;
+  if (plan.items.empty()) return EHIP_OK;
+  if (plan.items.size() > static_cast<size_t>(INT32_MAX))
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "too many work items");
+  ehip::DecodeParams p{};
+  p.q = q;
+  p.k_slab = k_slab;
+  p.v_slab = v_slab;
+  p.out = out;
+  p.rows = ctx->d_rows;
+  p.items = ctx->d_items;
+  p.table = ctx->d_table;
+  const int64_t grp = g.heads / g.kv_heads;
+  p.part_o = ctx->d_part;
+  p.part_ml = ctx->d_part + static_cast<size_t>(plan.partials) * grp * g.head_dim;
+  p.counters = ctx->d_counters;
+  p.err = ctx->d_err;
+  p.block_stride = ehip::BlockStride(g);
+  p.slab_blocks = g.slab_blocks;
+  p.n_items = static_cast<int32_t>(plan.items.size());
+  p.heads = g.heads;
+  p.kv_heads = g.kv_heads;
+  p.group = static_cast<int32_t>(grp);
+  p.d = g.head_dim;
+  p.bs = g.block_size;
+  p.scale_log2 = g.scale * 1.4426950408889634f;
+  EHIP_HIP(ctx, ehip::LaunchDecode(p, g.kv_dtype, ctx->stream));
+  return EHIP_OK;
+}
+
+bool NonNull(const void* a) { return a != nullptr; }
+
+}  // namespace
+
+extern "C" {
+
+int ehip_device_count(int* out) {
+  if (!out) return EHIP_INVALID_ARGUMENT;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
+  *out = n;
+  return EHIP_OK;
+}
+
+int ehip_init(int device, ehip_ctx** out) {
+  if (!out) return EHIP_INVALID_ARGUMENT;
+  *out = nullptr;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return EHIP_FAILED_PRECONDITION;
+  if (device < 0 || device >= n) return EHIP_INVALID_ARGUMENT;
+  ehip_ctx* ctx = new (std::nothrow) ehip_ctx;
+  if (!ctx) return EHIP_OUT_OF_MEMORY;
+  ctx->device = device;
+  int rc = EHIP_OK;
+  do {
+    hipError_t e = hipSetDevice(device);
+    if (e != hipSuccess) { rc = HipFail(ctx, e, "hipSetDevice"); break; }
+    // Default priority (a non-default priority stream has hung on this pool).
+    e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) { rc = HipFail(ctx, e, "hipStreamCreate"); break; }
+    e = hipMalloc(&ctx->d_err, 256);
+    if (e != hipSuccess) { rc = HipFail(ctx, e, "hipMalloc(err)"); break; }
+    e = hipMemset(ctx->d_err, 0, 256);
+    if (e != hipSuccess) { rc = HipFail(ctx, e, "hipMemset(err)"); break; }
+  } while (false);
+  if (rc != EHIP_OK) {
+    ehip_destroy(ctx);
+    return rc;
+  }
+  *out = ctx;
+  return EHIP_OK;
+}
+
+int ehip_destroy(ehip_ctx* ctx) {
+  if (!ctx) return EHIP_OK;
+  (void)hipSetDevice(ctx->device);
+  if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+  for (int i = 0; i < 2; ++i) {
+    if (ctx->stage_done[i]) (void)hipEventDestroy(ctx->stage_done[i]);
+    if (ctx->h_stage[i]) (void)hipHostFree(ctx->h_stage[i]);
+  }
+  if (ctx->d_desc) (void)hipFree(ctx->d_desc);
+  if (ctx->d_part) (void)hipFree(ctx->d_part);
+  if (ctx->d_counters) (void)hipFree(ctx->d_counters);
+  if (ctx->d_err) (void)hipFree(ctx->d_err);
+  if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+  delete ctx;
+  return EHIP_OK;
+}
+
+int ehip_last_error(const ehip_ctx* ctx, char* buf, size_t n) {
+  if (!ctx || !buf || n == 0) return EHIP_INVALID_ARGUMENT;
+  std::snprintf(buf, n, "%s", ctx->last_error.c_str());
+  return EHIP_OK;
+}
+
+int ehip_sync(ehip_ctx* ctx) {
+  if (int rc = CheckCtx(ctx)) return rc;
+  EHIP_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  int32_t flags = 0;
+  EHIP_HIP(ctx, hipMemcpy(&flags, ctx->d_err, sizeof(flags), hipMemcpyDeviceToHost));
+  if (flags != 0) {
+    EHIP_HIP(ctx, hipMemset(ctx->d_err, 0, sizeof(flags)));
+    return SetError(ctx, EHIP_INVALID_ARGUMENT,
+                    "device range check failed (flags=%d: %s%s); the offending rows were skipped",
+                    flags, (flags & ehip::kErrSlotRange) ? "slot outside slab " : "",
+                    (flags & ehip::kErrBlockRange) ? "block id outside slab" : "");
+  }
+  return EHIP_OK;
+}
+
+int ehip_malloc(ehip_ctx* ctx, int64_t bytes, void** d_out) {
+  if (int rc = CheckCtx(ctx)) return rc;
+  if (!d_out || bytes < 0) return SetError(ctx, EHIP_INVALID_ARGUMENT, "bad malloc arguments");
+  *d_out = nullptr;
+  void* p = nullptr;
+  const size_t n = std::max<size_t>(256, Align256(static_cast<size_t>(bytes)));
+  EHIP_HIP(ctx, hipMalloc(&p, n));  // hipMalloc returns >= 256-byte aligned memory
+  hipError_t e = hipMemsetAsync(p, 0, n, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
+    (void)hipFree(p);
+    return HipFail(ctx, e, "zero-fill");
+  }
+  *d_out = p;
+  return EHIP_OK;
+}
+
+int ehip_free(ehip_ctx* ctx, void* d_ptr) {
+  if (int rc = CheckCtx(ctx)) return rc;
+  if (!d_ptr) return EHIP_OK;
+  EHIP_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  EHIP_HIP(ctx, hipFree(d_ptr));
+  return EHIP_OK;
+}
+
+int ehip_copy_to_device(ehip_ctx* ctx, void* d_dst, const void* h_src, int64_t bytes) {
+  if (int rc = CheckCtx(ctx)) return rc;
+  if (bytes < 0 || (bytes > 0 && (!d_dst || !h_src)))
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "bad copy arguments");
+  if (bytes == 0) return EHIP_OK;
+  EHIP_HIP(ctx, hipMemcpyAsync(d_dst, h_src, bytes, hipMemcpyHostToDevice, ctx->stream));
+  EHIP_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return EHIP_OK;
+}
+
+int ehip_copy_to_host(ehip_ctx* ctx, void* h_dst, const void* d_src, int64_t bytes) {
+  if (int rc = CheckCtx(ctx)) return rc;
+  if (bytes < 0 || (bytes > 0 && (!h_dst || !d_src)))
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "bad copy arguments");
+  if (bytes == 0) return EHIP_OK;
+  EHIP_HIP(ctx, hipMemcpyAsync(h_dst, d_src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+  EHIP_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return EHIP_OK;
+}
+
+int ehip_copy_device(ehip_ctx* ctx, void* d_dst, const void* d_src, int64_t bytes) {
+  if (int rc = CheckCtx(ctx)) return rc;
+  if (bytes < 0 || (bytes > 0 && (!d_dst || !d_src)))
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "bad copy arguments");
+  if (bytes == 0) return EHIP_OK;
+  EHIP_HIP(ctx, hipMemcpyAsync(d_dst, d_src, bytes, hipMemcpyDeviceToDevice, ctx->stream));
+  return EHIP_OK;
+}
+
+int ehip_fill_normal(ehip_ctx* ctx, void* d_dst, int64_t n, int32_t dtype, float mean,
+                     float stddev, uint64_t seed) {
+  if (int rc = CheckCtx(ctx)) return rc;
+  if (n < 0 || (n > 0 && !d_dst) || (dtype != EHIP_KV_F32 && dtype != EHIP_KV_BF16))
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "bad fill arguments");
+  EHIP_HIP(ctx, ehip::LaunchFillNormal(d_dst, n, dtype, mean, stddev, seed, ctx->stream));
+  return EHIP_OK;
+}
+
+int ehip_event_create(ehip_ctx* ctx, void** ev_out) {
+  if (int rc = CheckCtx(ctx)) return rc;
+  if (!ev_out) return SetError(ctx, EHIP_INVALID_ARGUMENT, "null event out");
+  hipEvent_t ev = nullptr;
+  EHIP_HIP(ctx, hipEventCreate(&ev));
+  *ev_out = ev;
+  return EHIP_OK;
+}
+
+int ehip_event_destroy(ehip_ctx* ctx, void* ev) {
+  if (int rc = CheckCtx(ctx)) return rc;
+  if (ev) EHIP_HIP(ctx, hipEventDestroy(static_cast<hipEvent_t>(ev)));
+  return EHIP_OK;
+}
+
+int ehip_event_record(ehip_ctx* ctx, void* ev) {
+  if (int rc = CheckCtx(ctx)) return rc;
+  if (!ev) return SetError(ctx, EHIP_INVALID_ARGUMENT, "null event");
+  EHIP_HIP(ctx, hipEventRecord(static_cast<hipEvent_t>(ev), ctx->stream));
+  return EHIP_OK;
+}
+
+int ehip_event_elapsed_ms(ehip_ctx* ctx, void* ev_start, void* ev_end, float* ms_out) {
+  if (int rc = CheckCtx(ctx)) return rc;
+  if (!ev_start || !ev_end || !ms_out) return SetError(ctx, EHIP_INVALID_ARGUMENT, "null event");
+  EHIP_HIP(ctx, hipEventSynchronize(static_cast<hipEvent_t>(ev_end)));
+  EHIP_HIP(ctx, hipEventElapsedTime(ms_out, static_cast<hipEvent_t>(ev_start),
+                                    static_cast<hipEvent_t>(ev_end)));
+  return EHIP_OK;
+}
+
+// ----------------------------------------------------- reference kernels --
+
+int ehip_kv_scatter_f32(ehip_ctx* ctx, const float* d_src_k, const float* d_src_v,
+                        const int64_t* d_slot_mapping, int64_t t_dim, int64_t kv_heads,
+                        int64_t d, int64_t block_size, int64_t slab_blocks, float* d_k_slab,
+                        float* d_v_slab) {
+  if (int rc = CheckCtx(ctx)) return rc;
+  if (t_dim < 0 || kv_heads < 1 || d < 1 || block_size < 1 || slab_blocks < 1 ||
+      kv_heads > INT32_MAX || d > INT32_MAX || block_size > INT32_MAX)
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "bad scatter geometry");
+  if (t_dim == 0) return EHIP_OK;
+  if (!d_src_k || !d_src_v || !d_slot_mapping || !d_k_slab || !d_v_slab)
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "null scatter operand");
+  EHIP_HIP(ctx, ehip::LaunchKvScatter(d_src_k, d_src_v, d_slot_mapping, t_dim,
+                                      static_cast<int32_t>(kv_heads), static_cast<int32_t>(d),
+                                      static_cast<int32_t>(block_size), slab_blocks, d_k_slab,
+                                      d_v_slab, EHIP_KV_F32, ctx->d_err, ctx->stream));
+  return EHIP_OK;
+}
+
+int ehip_kv_scatter_bf16(ehip_ctx* ctx, const float* d_src_k, const float* d_src_v,
+                         const int64_t* d_slot_mapping, int64_t t_dim, int64_t kv_heads,
+                         int64_t d, int64_t block_size, int64_t slab_blocks,
+                         uint16_t* d_k_slab, uint16_t* d_v_slab) {
+  if (int rc = CheckCtx(ctx)) return rc;
+  if (t_dim < 0 || kv_heads < 1 || d < 1 || block_size < 1 || slab_blocks < 1 ||
+      kv_heads > INT32_MAX || d > INT32_MAX || block_size > INT32_MAX)
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "bad scatter geometry");
+  if (t_dim == 0) return EHIP_OK;
+  if (!d_src_k || !d_src_v || !d_slot_mapping || !d_k_slab || !d_v_slab)
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "null scatter operand");
+  EHIP_HIP(ctx, ehip::LaunchKvScatter(d_src_k, d_src_v, d_slot_mapping, t_dim,
+                                      static_cast<int32_t>(kv_heads), static_cast<int32_t>(d),
+                                      static_cast<int32_t>(block_size), slab_blocks, d_k_slab,
+                                      d_v_slab, EHIP_KV_BF16, ctx->d_err, ctx->stream));
+  return EHIP_OK;
+}
+
+int ehip_kv_gather_f32(ehip_ctx* ctx, const float* d_k_slab, const float* d_v_slab,
+                       const int32_t* d_block_table, int64_t block_size, int64_t length,
+                       int64_t kv_heads, int64_t d, int64_t slab_blocks, float* d_out_k,
+                       float* d_out_v) {
+  if (int rc = CheckCtx(ctx)) return rc;
+  if (length < 0 || kv_heads < 1 || d < 1 || block_size < 1 || slab_blocks < 1 ||
+      kv_heads > INT32_MAX || d > INT32_MAX || block_size > INT32_MAX)
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "bad gather geometry");
+  if (length == 0) return EHIP_OK;  // the reference returns early (kv_gather.cpp:66-68)
+  if (!d_k_slab || !d_v_slab || !d_block_table || !d_out_k || !d_out_v)
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "null gather operand");
+  EHIP_HIP(ctx, ehip::LaunchKvGather(d_k_slab, d_v_slab, d_block_table,
+                                     static_cast<int32_t>(block_size), length,
+                                     static_cast<int32_t>(kv_heads), static_cast<int32_t>(d),
+                                     slab_blocks, d_out_k, d_out_v, ctx->d_err, ctx->stream));
+  return EHIP_OK;
+}
+
+int ehip_paged_decode_attention_f32(ehip_ctx* ctx, const float* d_q, const float* d_k_slab,
+                                    const float* d_v_slab, const int32_t* d_block_table,
+                                    int64_t num_blocks, int64_t length, int64_t heads,
+                                    int64_t kv_heads, int64_t d, int64_t block_size,
+                                    int64_t block_stride, int64_t slab_blocks, float scale,
+                                    float* d_out) {
+  if (int rc = CheckCtx(ctx)) return rc;
+  if (heads > INT32_MAX || kv_heads > INT32_MAX || d > INT32_MAX || block_size > INT32_MAX)
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "geometry out of range");
+  ehip_geometry g{static_cast<int32_t>(heads), static_cast<int32_t>(kv_heads),
+                  static_cast<int32_t>(d),     static_cast<int32_t>(block_size),
+                  EHIP_KV_F32,                 0,
+                  slab_blocks,                 block_stride,
+                  scale};
+  if (!NonNull(d_q) || !NonNull(d_k_slab) || !NonNull(d_v_slab) || !NonNull(d_block_table) ||
+      !NonNull(d_out))
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "null decode operand");
+  Plan plan;
+  std::string err;
+  if (int rc = ehip::BuildSingleRowPlan(g, length, num_blocks, &plan, &err))
+    return SetError(ctx, rc, "%s", err.c_str());
+  if (int rc = UploadPlan(ctx, g, std::move(plan), d_block_table)) return rc;
+  return LaunchAttention(ctx, d_q, d_k_slab, d_v_slab, d_out);
+}
+
+namespace {
+int BatchedDecode(ehip_ctx* ctx, int kv_dtype, const float* d_q, const void* d_k_slab,
+                  const void* d_v_slab, const int32_t* const* h_block_tables,
+                  const int64_t* h_lengths, int64_t num_seqs, int64_t heads, int64_t kv_heads,
+                  int64_t d, int64_t block_size, int64_t block_stride, int64_t slab_blocks,
+                  float scale, float* d_out) {
+  if (int rc = CheckCtx(ctx)) return rc;
+  if (num_seqs < 0 || num_seqs > INT32_MAX || heads > INT32_MAX || kv_heads > INT32_MAX ||
+      d > INT32_MAX || block_size > INT32_MAX)
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "geometry out of range");
+  ehip_geometry g{static_cast<int32_t>(heads), static_cast<int32_t>(kv_heads),
+                  static_cast<int32_t>(d),     static_cast<int32_t>(block_size),
+                  kv_dtype,                    0,
+                  slab_blocks,                 block_stride,
+                  scale};
+  std::string err;
+  if (int rc = ehip::ValidateGeometry(g, &err)) return SetError(ctx, rc, "%s", err.c_str());
+  if (num_seqs == 0) return EHIP_OK;  // the reference's B == 0 no-op
+  if (!h_block_tables || !h_lengths || !d_q || !d_k_slab || !d_v_slab || !d_out)
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "null batched-decode operand");
+  // Pack the per-sequence tables into CSR (the reference passes pointer
+  // arrays, which cannot cross the device boundary).
+  std::vector<int32_t> qlens(num_seqs, 1), offsets(num_seqs + 1, 0), ids;
+  for (int64_t b = 0; b < num_seqs; ++b) {
+    const int64_t L = h_lengths[b];
+    if (L < 1 || L > (int64_t{1} << 30))
+      return SetError(ctx, EHIP_INVALID_ARGUMENT, "lengths[%lld]=%lld out of range",
+                      static_cast<long long>(b), static_cast<long long>(L));
+    if (!h_block_tables[b])
+      return SetError(ctx, EHIP_INVALID_ARGUMENT, "block_tables[%lld] is null",
+                      static_cast<long long>(b));
+    const int64_t need = (L + block_size - 1) / block_size;
+    ids.insert(ids.end(), h_block_tables[b], h_block_tables[b] + need);
+    if (ids.size() > static_cast<size_t>(INT32_MAX))
+      return SetError(ctx, EHIP_INVALID_ARGUMENT, "too many table entries");
+    offsets[b + 1] = static_cast<int32_t>(ids.size());
+  }
+  ehip_step_desc s{static_cast<int32_t>(num_seqs), 0, qlens.data(), h_lengths, offsets.data(),
+                   ids.data(), nullptr};
+  Plan plan;
+  if (int rc = ehip::BuildPlan(g, s, &plan, &err)) return SetError(ctx, rc, "%s", err.c_str());
+  if (int rc = UploadPlan(ctx, g, std::move(plan), nullptr)) return rc;
+  return LaunchAttention(ctx, d_q, d_k_slab, d_v_slab, d_out);
+}
+}  // namespace
+
+int ehip_paged_decode_attention_batched_f32(
+    ehip_ctx* ctx, const float* d_q, const float* d_k_slab, const float* d_v_slab,
+    const int32_t* const* h_block_tables, const int64_t* h_lengths, int64_t num_seqs,
+    int64_t heads, int64_t kv_heads, int64_t d, int64_t block_size, int64_t block_stride,
+    int64_t slab_blocks, float scale, float* d_out) {
+  return BatchedDecode(ctx, EHIP_KV_F32, d_q, d_k_slab, d_v_slab, h_block_tables, h_lengths,
+                       num_seqs, heads, kv_heads, d, block_size, block_stride, slab_blocks,
+                       scale, d_out);
+}
+
+int ehip_paged_decode_attention_batched_bf16(
+    ehip_ctx* ctx, const float* d_q, const uint16_t* d_k_slab, const uint16_t* d_v_slab,
+    const int32_t* const* h_block_tables, const int64_t* h_lengths, int64_t num_seqs,
+    int64_t heads, int64_t kv_heads, int64_t d, int64_t block_size, int64_t block_stride,
+    int64_t slab_blocks, float scale, float* d_out) {
+  return BatchedDecode(ctx, EHIP_KV_BF16, d_q, d_k_slab, d_v_slab, h_block_tables, h_lengths,
+                       num_seqs, heads, kv_heads, d, block_size, block_stride, slab_blocks,
+                       scale, d_out);
+}
+
+// ------------------------------------------------------------ step path --
+
+int ehip_step_upload(ehip_ctx* ctx, const ehip_geometry* geom, const ehip_step_desc* step) {
+  if (int rc = CheckCtx(ctx)) return rc;
+  if (!geom || !step) return SetError(ctx, EHIP_INVALID_ARGUMENT, "null geometry or step");
+  Plan plan;
+  std::string err;
+  if (int rc = ehip::BuildPlan(*geom, *step, &plan, &err))
+    return SetError(ctx, rc, "%s", err.c_str());
+  return UploadPlan(ctx, *geom, std::move(plan), nullptr);
+}
+
+int ehip_step_kv_append(ehip_ctx* ctx, const float* d_src_k, const float* d_src_v,
+                        void* d_k_slab, void* d_v_slab) {
+  if (int rc = CheckCtx(ctx)) return rc;
+  if (!ctx->have_step) return SetError(ctx, EHIP_FAILED_PRECONDITION, "no step uploaded");
+  const Plan& plan = ctx->plan;
+  if (plan.slots.empty()) {
+    if (plan.rows.empty()) return EHIP_OK;
+    return SetError(ctx, EHIP_FAILED_PRECONDITION, "the uploaded step has no slot mapping");
+  }
+  if (!d_src_k || !d_src_v || !d_k_slab || !d_v_slab)
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "null append operand");
+  const ehip_geometry& g = ctx->geom;
+  if (ehip::BlockStride(g) != int64_t{g.kv_heads} * g.block_size * g.head_dim)
+    return SetError(ctx, EHIP_UNIMPLEMENTED, "append needs the dense Hkv*bs*d block stride");
+  EHIP_HIP(ctx, ehip::LaunchKvScatter(d_src_k, d_src_v, ctx->d_slots,
+                                      static_cast<int64_t>(plan.slots.size()), g.kv_heads,
+                                      g.head_dim, g.block_size, g.slab_blocks, d_k_slab,
+                                      d_v_slab, g.kv_dtype, ctx->d_err, ctx->stream));
+  return EHIP_OK;
+}
+
+int ehip_step_attention(ehip_ctx* ctx, const float* d_q, const void* d_k_slab,
+                        const void* d_v_slab, float* d_out) {
+  if (int rc = CheckCtx(ctx)) return rc;
+  if (!ctx->have_step) return SetError(ctx, EHIP_FAILED_PRECONDITION, "no step uploaded");
+  if (ctx->plan.rows.empty()) return EHIP_OK;
+  if (!d_q || !d_k_slab || !d_v_slab || !d_out)
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "null attention operand");
+  return LaunchAttention(ctx, d_q, d_k_slab, d_v_slab, d_out);
+}
+
+int ehip_step_info(const ehip_ctx* ctx, int64_t* rows, int64_t* items, int64_t* partials) {
+  if (!ctx || !ctx->have_step) return EHIP_FAILED_PRECONDITION;
+  if (rows) *rows = static_cast<int64_t>(ctx->plan.rows.size());
+  if (items) *items = static_cast<int64_t>(ctx->plan.items.size());
+  if (partials) *partials = ctx->plan.partials;
+  return EHIP_OK;
+}
+
+int ehip_plan_counts(const ehip_geometry* geom, const ehip_step_desc* step, int64_t* rows,
+                     int64_t* items, int64_t* partials, int32_t* split_tokens) {
+  if (!geom || !step) return EHIP_INVALID_ARGUMENT;
+  Plan plan;
+  std::string err;
+  if (int rc = ehip::BuildPlan(*geom, *step, &plan, &err)) return rc;
+  if (rows) *rows = static_cast<int64_t>(plan.rows.size());
+  if (items) *items = static_cast<int64_t>(plan.items.size());
+  if (partials) *partials = plan.partials;
+  if (split_tokens) *split_tokens = plan.split_tokens;
+  return EHIP_OK;
+}
+
+}  // extern "C"

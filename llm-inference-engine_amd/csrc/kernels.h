@@ -1,0 +1,60 @@
+// Kernel launch interfaces (host side), shared by the runtime and the kernel
+// translation units.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+
+#include "plan.h"
+
+namespace ehip {
+
+// Device-side error bits (OR-ed into the context's error word).
+enum : int32_t {
+  kErrSlotRange = 1,   // an append slot outside the slab
+  kErrBlockRange = 2,  // a block-table id outside the slab
+};
+
+struct DecodeParams {
+  const float* q;           // [rows, H, d]
+  const void* k_slab;       // [slab_blocks, Hkv, bs, d] f32 or bf16
+  const void* v_slab;
+  float* out;               // [rows, H, d]
+  const RowDesc* rows;
+  const WorkItem* items;
+  const int32_t* table;     // CSR ids (or a single sequence's table)
+  float* part_o;            // [partials, g, d]
+  float* part_ml;           // [partials, g, 2]
+  int32_t* counters;        // [rows * Hkv], zero between launches
+  int32_t* err;
+  int64_t block_stride;     // elements
+  int64_t slab_blocks;
+  int32_t n_items;
+  int32_t heads;
+  int32_t kv_heads;
+  int32_t group;            // g = H / Hkv
+  int32_t d;
+  int32_t bs;
+  float scale_log2;         // scale * log2(e)
+};
+
+// Launch the decode kernel family for the given plan (one wavefront per work
+// item). Picks the specialised (dtype, d, g) kernel or the generic one.
+hipError_t LaunchDecode(const DecodeParams& p, int kv_dtype, hipStream_t stream);
+
+// KvScatter: rows [T, Hkv, d] fp32 into slabs (fp32 copy or bf16 RNE).
+hipError_t LaunchKvScatter(const float* src_k, const float* src_v, const int64_t* slots,
+                           int64_t t_dim, int32_t kv_heads, int32_t d, int32_t bs,
+                           int64_t slab_blocks, void* k_slab, void* v_slab, int kv_dtype,
+                           int32_t* err, hipStream_t stream);
+
+hipError_t LaunchKvGather(const float* k_slab, const float* v_slab, const int32_t* table,
+                          int32_t bs, int64_t length, int32_t kv_heads, int32_t d,
+                          int64_t slab_blocks, float* out_k, float* out_v, int32_t* err,
+                          hipStream_t stream);
+
+hipError_t LaunchFillNormal(void* dst, int64_t n, int dtype, float mean, float stddev,
+                            uint64_t seed, hipStream_t stream);
+
+}  // namespace ehip

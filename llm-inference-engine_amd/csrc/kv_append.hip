@@ -1,0 +1,205 @@
+// KV append (scatter), gather and synthetic fills for gfx950.
+//
+// Scatter semantics: kernels::KvScatterF32 (src/kernels/kv_scatter.cpp:27-61):
+// token t's row for kv head h (src + (t*Hkv + h)*d) lands at slot
+// s = slot_mapping[t], block s / bs, row s % bs, i.e. slab element
+// ((block*Hkv + h)*bs + s % bs)*d. A pure copy (fp32) or the reference's
+// round-to-nearest-even narrowing (bf16), so the result is bit-exact.
+//
+// One thread moves one 16-byte source vector (4 floats) of one (token, head)
+// row; consecutive threads cover consecutive source bytes, so reads are fully
+// coalesced and each row's destination is a contiguous 4*d (or 2*d) bytes.
+#include "device_util.h"
+#include "kernels.h"
+
+namespace ehip {
+namespace {
+
+template <class KV>
+__device__ __forceinline__ void Store4(KV* dst, float4 x);
+template <>
+__device__ __forceinline__ void Store4<float>(float* dst, float4 x) {
+  *reinterpret_cast<float4*>(dst) = x;
+}
+template <>
+__device__ __forceinline__ void Store4<uint16_t>(uint16_t* dst, float4 x) {
+  uint2 w;
+  w.x = Fp32ToBf16Bits(x.x) | (Fp32ToBf16Bits(x.y) << 16);
+  w.y = Fp32ToBf16Bits(x.z) | (Fp32ToBf16Bits(x.w) << 16);
+  *reinterpret_cast<uint2*>(dst) = w;
+}
+
+__device__ __forceinline__ void Store1(float* dst, float x) { *dst = x; }
+__device__ __forceinline__ void Store1(uint16_t* dst, float x) {
+  *dst = static_cast<uint16_t>(Fp32ToBf16Bits(x));
+}
+
+// d % 4 == 0 path.
+template <class KV>
+__global__ __launch_bounds__(256) void KvScatterVec(const float* __restrict__ src_k,
+                                                    const float* __restrict__ src_v,
+                                                    const int64_t* __restrict__ slots,
+                                                    int64_t n_vec, int kv_heads, int d, int bs,
+                                                    int64_t slab_blocks, KV* k_slab, KV* v_slab,
+                                                    int32_t* err) {
+  const int vpr = d >> 2;  // vectors per (token, head) row
+  for (int64_t i = blockIdx.x * int64_t{blockDim.x} + threadIdx.x; i < n_vec;
+       i += int64_t{gridDim.x} * blockDim.x) {
+    const int64_t row = i / vpr;  // token * Hkv + head
+    const int e = static_cast<int>(i - row * vpr) << 2;
+    const int64_t t = row / kv_heads;
+    const int h = static_cast<int>(row - t * kv_heads);
+    const int64_t slot = slots[t];
+    if (slot < 0 || slot >= slab_blocks * bs) {
+      atomicOr(err, kErrSlotRange);
+      continue;
+    }
+    const int64_t block = slot / bs;
+    const int64_t pos = slot - block * bs;
+    const int64_t dst = ((block * kv_heads + h) * bs + pos) * d + e;
+    const float4 kx = *reinterpret_cast<const float4*>(src_k + row * d + e);
+    const float4 vx = *reinterpret_cast<const float4*>(src_v + row * d + e);
+    Store4<KV>(k_slab + dst, kx);
+    Store4<KV>(v_slab + dst, vx);
+  }
+}
+
+template <class KV>
+__global__ __launch_bounds__(256) void KvScatterScalar(const float* __restrict__ src_k,
+                                                       const float* __restrict__ src_v,
+                                                       const int64_t* __restrict__ slots,
+                                                       int64_t n, int kv_heads, int d, int bs,
+                                                       int64_t slab_blocks, KV* k_slab,
+                                                       KV* v_slab, int32_t* err) {
+  for (int64_t i = blockIdx.x * int64_t{blockDim.x} + threadIdx.x; i < n;
+       i += int64_t{gridDim.x} * blockDim.x) {
+    const int64_t row = i / d;
+    const int e = static_cast<int>(i - row * d);
+    const int64_t t = row / kv_heads;
+    const int h = static_cast<int>(row - t * kv_heads);
+    const int64_t slot = slots[t];
+    if (slot < 0 || slot >= slab_blocks * bs) {
+      atomicOr(err, kErrSlotRange);
+      continue;
+    }
+    const int64_t block = slot / bs;
+    const int64_t pos = slot - block * bs;
+    const int64_t dst = ((block * kv_heads + h) * bs + pos) * d + e;
+    Store1(k_slab + dst, src_k[i]);
+    Store1(v_slab + dst, src_v[i]);
+  }
+}
+
+// kernels::KvGatherF32 (src/kernels/kv_gather.cpp:42-89): out[h, j, :] is
+// token j of kv head h, read through the table.
+__global__ __launch_bounds__(256) void KvGather(const float* __restrict__ k_slab,
+                                                const float* __restrict__ v_slab,
+                                                const int32_t* __restrict__ table, int bs,
+                                                int64_t length, int kv_heads, int d,
+                                                int64_t slab_blocks, float* out_k, float* out_v,
+                                                int32_t* err) {
+  const int64_t n = int64_t{kv_heads} * length * d;
+  for (int64_t i = blockIdx.x * int64_t{blockDim.x} + threadIdx.x; i < n;
+       i += int64_t{gridDim.x} * blockDim.x) {
+    const int64_t hj = i / d;
+    const int e = static_cast<int>(i - hj * d);
+    const int h = static_cast<int>(hj / length);
+    const int64_t j = hj - int64_t{h} * length;
+    const int64_t phys = table[j / bs];
+    if (phys < 0 || phys >= slab_blocks) {
+      atomicOr(err, kErrBlockRange);
+      continue;
+    }
+    const int64_t src = ((phys * kv_heads + h) * bs + j % bs) * d + e;
+    out_k[i] = k_slab[src];
+    out_v[i] = v_slab[src];
+  }
+}
+
+// Counter-based N(mean, std) fill: element pair i/2 hashes (seed, i/2) with
+// splitmix64 into two uniforms and takes the Box-Muller cosine/sine branch.
+__device__ __forceinline__ uint64_t SplitMix64(uint64_t x) {
+  x += 0x9E3779B97F4A7C15ull;
+  x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+  x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+  return x ^ (x >> 31);
+}
+
+template <class KV>
+__global__ __launch_bounds__(256) void FillNormal(KV* dst, int64_t n, float mean, float stddev,
+                                                  uint64_t seed) {
+  for (int64_t i = blockIdx.x * int64_t{blockDim.x} + threadIdx.x; i < n;
+       i += int64_t{gridDim.x} * blockDim.x) {
+    const uint64_t h = SplitMix64(seed * 0x2545F4914F6CDD1Dull + static_cast<uint64_t>(i >> 1));
+    const float u1 = (static_cast<float>(h >> 40) + 1.0f) * (1.0f / 16777216.0f);  // (0, 1]
+    const float u2 = static_cast<float>((h >> 16) & 0xFFFFFFu) * (1.0f / 16777216.0f);
+    const float r = sqrtf(-2.0f * __logf(u1));
+    const float z = (i & 1) ? r * __sinf(6.283185307f * u2) : r * __cosf(6.283185307f * u2);
+    Store1(dst + i, mean + stddev * z);
+  }
+}
+
+int GridFor(int64_t work, int block) {
+  const int64_t g = (work + block - 1) / block;
+  return static_cast<int>(g < 65536 ? (g < 1 ? 1 : g) : 65536);
+}
+
+}  // namespace
+
+hipError_t LaunchKvScatter(const float* src_k, const float* src_v, const int64_t* slots,
+                           int64_t t_dim, int32_t kv_heads, int32_t d, int32_t bs,
+                           int64_t slab_blocks, void* k_slab, void* v_slab, int kv_dtype,
+                           int32_t* err, hipStream_t stream) {
+  if (t_dim == 0) return hipSuccess;
+  const bool vec = (d % 4 == 0) && (reinterpret_cast<uintptr_t>(src_k) % 16 == 0) &&
+                   (reinterpret_cast<uintptr_t>(src_v) % 16 == 0) &&
+                   (reinterpret_cast<uintptr_t>(k_slab) % 16 == 0) &&
+                   (reinterpret_cast<uintptr_t>(v_slab) % 16 == 0);
+  const int64_t n = t_dim * kv_heads * d;
+  if (vec) {
+    const int64_t nv = n / 4;
+    if (kv_dtype == EHIP_KV_BF16)
+      hipLaunchKernelGGL(KvScatterVec<uint16_t>, dim3(GridFor(nv, 256)), dim3(256), 0, stream,
+                         src_k, src_v, slots, nv, kv_heads, d, bs, slab_blocks,
+                         static_cast<uint16_t*>(k_slab), static_cast<uint16_t*>(v_slab), err);
+    else
+      hipLaunchKernelGGL(KvScatterVec<float>, dim3(GridFor(nv, 256)), dim3(256), 0, stream,
+                         src_k, src_v, slots, nv, kv_heads, d, bs, slab_blocks,
+                         static_cast<float*>(k_slab), static_cast<float*>(v_slab), err);
+  } else {
+    if (kv_dtype == EHIP_KV_BF16)
+      hipLaunchKernelGGL(KvScatterScalar<uint16_t>, dim3(GridFor(n, 256)), dim3(256), 0, stream,
+                         src_k, src_v, slots, n, kv_heads, d, bs, slab_blocks,
+                         static_cast<uint16_t*>(k_slab), static_cast<uint16_t*>(v_slab), err);
+    else
+      hipLaunchKernelGGL(KvScatterScalar<float>, dim3(GridFor(n, 256)), dim3(256), 0, stream,
+                         src_k, src_v, slots, n, kv_heads, d, bs, slab_blocks,
+                         static_cast<float*>(k_slab), static_cast<float*>(v_slab), err);
+  }
+  return hipGetLastError();
+}
+
+hipError_t LaunchKvGather(const float* k_slab, const float* v_slab, const int32_t* table,
+                          int32_t bs, int64_t length, int32_t kv_heads, int32_t d,
+                          int64_t slab_blocks, float* out_k, float* out_v, int32_t* err,
+                          hipStream_t stream) {
+  const int64_t n = int64_t{kv_heads} * length * d;
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(KvGather, dim3(GridFor(n, 256)), dim3(256), 0, stream, k_slab, v_slab,
+                     table, bs, length, kv_heads, d, slab_blocks, out_k, out_v, err);
+  return hipGetLastError();
+}
+
+hipError_t LaunchFillNormal(void* dst, int64_t n, int dtype, float mean, float stddev,
+                            uint64_t seed, hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  if (dtype == EHIP_KV_BF16)
+    hipLaunchKernelGGL(FillNormal<uint16_t>, dim3(GridFor(n, 256)), dim3(256), 0, stream,
+                       static_cast<uint16_t*>(dst), n, mean, stddev, seed);
+  else
+    hipLaunchKernelGGL(FillNormal<float>, dim3(GridFor(n, 256)), dim3(256), 0, stream,
+                       static_cast<float*>(dst), n, mean, stddev, seed);
+  return hipGetLastError();
+}
+
+}  // namespace ehip

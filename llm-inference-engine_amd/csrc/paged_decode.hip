@@ -1,0 +1,438 @@
+// Ragged paged decode attention for gfx950 (VALU path).
+//
+// Semantics: kernels::PagedDecodeAttention{,Batched}F32
+// (src/kernels/paged_attention.h:50-57, :105-110): for a query row attending
+// keys [0, L-1], out[h] = softmax(scale * q_h . K^T) V with K/V read through
+// the block table, query head h reading kv head h / g. The reference runs the
+// online recurrence of src/kernels/internal/paged_attention_common.h:69-136
+// per (sequence, kv head); here one wavefront handles one (row, kv head, key
+// split) work item and the splits are merged by log-sum-exp rescaling.
+//
+// Wavefront layout (specialised kernel): LPT lanes hold one token's head_dim
+// row, each lane E contiguous-by-16-bytes elements, so one 16-byte load per
+// lane per vector and each load instruction reads whole 128/256-byte row
+// segments. TPR = 64/LPT tokens are processed per "row" of the wavefront and
+// 32 tokens per tile. The g query heads of the kv head live in registers
+// (fp32), so every K/V byte is read from HBM once for all g heads.
+//
+// Softmax: scores are formed as dot * scale * log2(e) and exponentiated with
+// the hardware exp2; the running max/sum are per tile (32 keys), the tile's
+// max is a wavefront reduction, so alpha rescaling happens once per tile.
+#include "device_util.h"
+#include "kernels.h"
+
+namespace ehip {
+namespace {
+
+constexpr int kWavesPerBlock = 4;
+
+template <class KV>
+struct KvT;
+template <>
+struct KvT<float> {
+  static constexpr int EPV = 4;  // elements per 16-byte vector
+};
+template <>
+struct KvT<uint16_t> {
+  static constexpr int EPV = 8;
+};
+
+template <class KV>
+__device__ __forceinline__ void Widen(const uint4 r, float* o);
+template <>
+__device__ __forceinline__ void Widen<float>(const uint4 r, float* o) {
+  o[0] = __uint_as_float(r.x);
+  o[1] = __uint_as_float(r.y);
+  o[2] = __uint_as_float(r.z);
+  o[3] = __uint_as_float(r.w);
+}
+template <>
+__device__ __forceinline__ void Widen<uint16_t>(const uint4 r, float* o) {
+  o[0] = Bf16Lo(r.x);
+  o[1] = Bf16Hi(r.x);
+  o[2] = Bf16Lo(r.y);
+  o[3] = Bf16Hi(r.y);
+  o[4] = Bf16Lo(r.z);
+  o[5] = Bf16Hi(r.z);
+  o[6] = Bf16Lo(r.w);
+  o[7] = Bf16Hi(r.w);
+}
+
+__device__ __forceinline__ float KvAt(const float* p, int64_t i) { return p[i]; }
+__device__ __forceinline__ float KvAt(const uint16_t* p, int64_t i) {
+  return __uint_as_float(uint32_t{p[i]} << 16);
+}
+
+__device__ __forceinline__ int64_t PartialIndex(const RowDesc& rd, int kv_heads, int hk,
+                                                int nsplit, int split) {
+  return int64_t{rd.split_base} * kv_heads + int64_t{hk} * nsplit + split;
+}
+
+// Log-sum-exp merge of one (row, kv head) group's split partials, done by the
+// wavefront that finished last. Splits are combined in split order, so the
+// result does not depend on which wavefront arrived last.
+__device__ void MergeSplits(const DecodeParams& p, int row, int hk, int64_t pbase, int nsplit) {
+  const int lane = threadIdx.x & 63;
+  const int g = p.group, d = p.d;
+  float* out = p.out + (int64_t{row} * p.heads + int64_t{hk} * g) * d;
+  for (int h = 0; h < g; ++h) {
+    float M = -INFINITY;
+    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, p.part_ml[((pbase + s) * g + h) * 2]);
+    float L = 0.f;
+    for (int s = 0; s < nsplit; ++s) {
+      const float* ml = p.part_ml + ((pbase + s) * g + h) * 2;
+      L += ml[1] * Exp2(ml[0] - M);
+    }
+    const float inv = 1.0f / L;
+    for (int e = lane; e < d; e += 64) {
+      float acc = 0.f;
+      for (int s = 0; s < nsplit; ++s) {
+        const float w = Exp2(p.part_ml[((pbase + s) * g + h) * 2] - M);
+        acc += w * p.part_o[((pbase + s) * g + h) * d + e];
+      }
+      out[int64_t{h} * d + e] = acc * inv;
+    }
+  }
+}
+
+// Publish this wavefront's partial and, if it is the last split of its group
+// to finish, merge the group. Release/acquire at agent scope makes the
+// partials of every XCD visible to the merging wavefront.
+__device__ __forceinline__ void ArriveAndMaybeMerge(const DecodeParams& p, const WorkItem& it,
+                                                    const RowDesc& rd) {
+  __threadfence();
+  const int lane = threadIdx.x & 63;
+  int prev = 0;
+  int32_t* ctr = p.counters + int64_t{it.row} * p.kv_heads + it.kv_head;
+  if (lane == 0) prev = atomicAdd(ctr, 1);
+  prev = __shfl(prev, 0);
+  if (prev == it.nsplit - 1) {
+    __threadfence();
+    MergeSplits(p, it.row, it.kv_head, PartialIndex(rd, p.kv_heads, it.kv_head, it.nsplit, 0),
+                it.nsplit);
+    if (lane == 0) *ctr = 0;  // ready for the next launch
+  }
+}
+
+// ----------------------------------------------------------------------------
+// Specialised kernel: KV in {f32, bf16}, D in {64, 128}, G = g exactly.
+template <class KV, int D, int G>
+__global__ __launch_bounds__(kWavesPerBlock * 64) void DecodeValu(DecodeParams p) {
+  constexpr int EPV = KvT<KV>::EPV;
+  constexpr int LPT = (G * D / 8 > 64) ? 16 : 8;  // lanes per token row
+  constexpr int E = D / LPT;                      // elements per lane
+  constexpr int NV = E / EPV;                     // 16-byte vectors per lane
+  constexpr int TPR = 64 / LPT;                   // tokens per wavefront row
+  constexpr int ROWS = 32 / TPR;                  // rows per 32-token tile
+  constexpr int VSPAN = D / NV;                   // elements spanned by one vector index
+  static_assert(NV >= 1 && NV * EPV == E && E * LPT == D, "layout");
+
+  const int lane = threadIdx.x & 63;
+  const int item_idx = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  if (item_idx >= p.n_items) return;
+  const WorkItem it = p.items[item_idx];
+  const RowDesc rd = p.rows[it.row];
+  const int tl = lane / LPT;
+  const int sub = lane % LPT;
+  const int hk = it.kv_head;
+  const int bs = p.bs;
+
+  float q[G][E];
+  {
+    const float* qp = p.q + (int64_t{it.row} * p.heads + int64_t{hk} * G) * D + sub * EPV;
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+      for (int v = 0; v < NV; ++v)
+#pragma unroll
+        for (int c = 0; c < EPV; c += 4) {
+          const float4 x = *reinterpret_cast<const float4*>(qp + h * D + v * VSPAN + c);
+          q[h][v * EPV + c + 0] = x.x;
+          q[h][v * EPV + c + 1] = x.y;
+          q[h][v * EPV + c + 2] = x.z;
+          q[h][v * EPV + c + 3] = x.w;
+        }
+  }
+
+  const int tb = it.split * rd.split_len;
+  const int te = min(rd.length, tb + rd.split_len);
+  const int lb0 = tb / bs;
+  const int nblk = (te - 1) / bs - lb0 + 1;  // <= 64 (split_len <= 64 * bs)
+  int tab = -1;
+  if (lane < nblk) {
+    tab = p.table[rd.table_off + lb0 + lane];
+    if (tab < 0 || tab >= p.slab_blocks) {
+      atomicOr(p.err, kErrBlockRange);
+      tab = -1;
+    }
+  }
+
+  const KV* kbase = static_cast<const KV*>(p.k_slab) + int64_t{hk} * bs * D + sub * EPV;
+  const KV* vbase = static_cast<const KV*>(p.v_slab) + int64_t{hk} * bs * D + sub * EPV;
+
+  float m[G], l[G], o[G][E];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    m[h] = -INFINITY;
+    l[h] = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) o[h][e] = 0.f;
+  }
+
+  for (int t0 = tb; t0 < te; t0 += 32) {
+    uint4 kr[ROWS][NV], vr[ROWS][NV];
+    int phys[ROWS];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+      const int j0 = t0 + r * TPR;  // wavefront-uniform; the row lies in one block
+      phys[r] = j0 < te ? __builtin_amdgcn_readlane(tab, j0 / bs - lb0) : -1;
+      if (phys[r] >= 0) {
+        const int64_t off = int64_t{phys[r]} * p.block_stride + int64_t{(j0 + tl) % bs} * D;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+          kr[r][v] = *reinterpret_cast<const uint4*>(kbase + off + v * VSPAN);
+          vr[r][v] = *reinterpret_cast<const uint4*>(vbase + off + v * VSPAN);
+        }
+      } else {
+#pragma unroll
+        for (int v = 0; v < NV; ++v) kr[r][v] = vr[r][v] = make_uint4(0, 0, 0, 0);
+      }
+    }
+    const bool partial = t0 + 32 > te;
+
+    float s[ROWS][G];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+      float kf[E];
+#pragma unroll
+      for (int v = 0; v < NV; ++v) Widen<KV>(kr[r][v], kf + v * EPV);
+      const bool valid = phys[r] >= 0 && (!partial || t0 + r * TPR + tl < te);
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        float acc = 0.f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) acc = fmaf(q[h][e], kf[e], acc);
+        acc = SumGroup<LPT>(acc);
+        s[r][h] = valid ? acc * p.scale_log2 : -INFINITY;
+      }
+    }
+
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      float mx = s[0][h];
+#pragma unroll
+      for (int r = 1; r < ROWS; ++r) mx = fmaxf(mx, s[r][h]);
+      mx = MaxAcross<LPT>(mx);
+      const float mn = fmaxf(m[h], mx);
+      // A tile whose every key sits in an out-of-range block leaves mn at
+      // -inf; keep alpha finite (and the state untouched) in that case.
+      const float alpha = mn == -INFINITY ? 1.f : Exp2(m[h] - mn);
+      m[h] = mn;
+      float psum = 0.f;
+#pragma unroll
+      for (int r = 0; r < ROWS; ++r) {
+        s[r][h] = mn == -INFINITY ? 0.f : Exp2(s[r][h] - mn);
+        psum += s[r][h];
+      }
+      l[h] = l[h] * alpha + psum;
+#pragma unroll
+      for (int e = 0; e < E; ++e) o[h][e] *= alpha;
+    }
+
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+      float vf[E];
+#pragma unroll
+      for (int v = 0; v < NV; ++v) Widen<KV>(vr[r][v], vf + v * EPV);
+      if (partial && t0 + r * TPR + tl >= te) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) vf[e] = 0.f;  // never let a stale row reach the sum
+      }
+#pragma unroll
+      for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int e = 0; e < E; ++e) o[h][e] = fmaf(s[r][h], vf[e], o[h][e]);
+    }
+  }
+
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    l[h] = SumAcross<LPT>(l[h]);
+#pragma unroll
+    for (int e = 0; e < E; ++e) o[h][e] = SumAcross<LPT>(o[h][e]);
+  }
+
+  if (it.nsplit == 1) {
+    if (tl == 0) {
+      float* op = p.out + (int64_t{it.row} * p.heads + int64_t{hk} * G) * D + sub * EPV;
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        const float inv = 1.0f / l[h];
+#pragma unroll
+        for (int v = 0; v < NV; ++v)
+#pragma unroll
+          for (int c = 0; c < EPV; c += 4) {
+            float4 x;
+            x.x = o[h][v * EPV + c + 0] * inv;
+            x.y = o[h][v * EPV + c + 1] * inv;
+            x.z = o[h][v * EPV + c + 2] * inv;
+            x.w = o[h][v * EPV + c + 3] * inv;
+            *reinterpret_cast<float4*>(op + h * D + v * VSPAN + c) = x;
+          }
+      }
+    }
+    return;
+  }
+
+  const int64_t pidx = PartialIndex(rd, p.kv_heads, hk, it.nsplit, it.split);
+  if (tl == 0) {
+    float* po = p.part_o + pidx * G * D + sub * EPV;
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+      for (int v = 0; v < NV; ++v)
+#pragma unroll
+        for (int c = 0; c < EPV; c += 4) {
+          float4 x;
+          x.x = o[h][v * EPV + c + 0];
+          x.y = o[h][v * EPV + c + 1];
+          x.z = o[h][v * EPV + c + 2];
+          x.w = o[h][v * EPV + c + 3];
+          *reinterpret_cast<float4*>(po + h * D + v * VSPAN + c) = x;
+        }
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      p.part_ml[(pidx * G + h) * 2 + 0] = m[h];
+      p.part_ml[(pidx * G + h) * 2 + 1] = l[h];
+    }
+  }
+  ArriveAndMaybeMerge(p, it, rd);
+}
+
+// ----------------------------------------------------------------------------
+// Generic kernel: any d <= 256, any g (heads processed in chunks of 8, one
+// pass over the split's keys per chunk). Lanes own head_dim elements
+// e = lane + 64k; every key is one wavefront-wide dot product. Used for the
+// shapes the specialised kernels do not cover.
+template <class KV>
+__global__ __launch_bounds__(kWavesPerBlock * 64) void DecodeGeneric(DecodeParams p) {
+  constexpr int HC = 8;
+  const int lane = threadIdx.x & 63;
+  const int item_idx = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  if (item_idx >= p.n_items) return;
+  const WorkItem it = p.items[item_idx];
+  const RowDesc rd = p.rows[it.row];
+  const int hk = it.kv_head;
+  const int g = p.group, d = p.d, bs = p.bs;
+  const int tb = it.split * rd.split_len;
+  const int te = min(rd.length, tb + rd.split_len);
+  const KV* kslab = static_cast<const KV*>(p.k_slab) + int64_t{hk} * bs * d;
+  const KV* vslab = static_cast<const KV*>(p.v_slab) + int64_t{hk} * bs * d;
+  const int64_t pidx = PartialIndex(rd, p.kv_heads, hk, it.nsplit, it.split);
+
+  for (int h0 = 0; h0 < g; h0 += HC) {
+    const int hc = min(HC, g - h0);
+    float q[HC][4], o[HC][4], m[HC], l[HC];
+    for (int h = 0; h < HC; ++h) {
+      m[h] = -INFINITY;
+      l[h] = 0.f;
+      for (int k = 0; k < 4; ++k) {
+        const int e = lane + 64 * k;
+        q[h][k] = (h < hc && e < d)
+                      ? p.q[(int64_t{it.row} * p.heads + int64_t{hk} * g + h0 + h) * d + e]
+                      : 0.f;
+        o[h][k] = 0.f;
+      }
+    }
+    for (int j = tb; j < te; ++j) {
+      const int phys = p.table[rd.table_off + j / bs];
+      if (phys < 0 || phys >= p.slab_blocks) {
+        if (lane == 0) atomicOr(p.err, kErrBlockRange);
+        continue;
+      }
+      const int64_t off = int64_t{phys} * p.block_stride + int64_t{j % bs} * d;
+      float kv[4], vv[4];
+      for (int k = 0; k < 4; ++k) {
+        const int e = lane + 64 * k;
+        kv[k] = e < d ? KvAt(kslab, off + e) : 0.f;
+        vv[k] = e < d ? KvAt(vslab, off + e) : 0.f;
+      }
+      for (int h = 0; h < HC; ++h) {
+        if (h >= hc) break;
+        float acc = 0.f;
+        for (int k = 0; k < 4; ++k) acc = fmaf(q[h][k], kv[k], acc);
+        const float s = WaveSum(acc) * p.scale_log2;
+        const float mn = fmaxf(m[h], s);
+        const float alpha = Exp2(m[h] - mn);
+        const float pr = Exp2(s - mn);
+        m[h] = mn;
+        l[h] = l[h] * alpha + pr;
+        for (int k = 0; k < 4; ++k) o[h][k] = fmaf(pr, vv[k], o[h][k] * alpha);
+      }
+    }
+    for (int h = 0; h < hc; ++h) {
+      if (it.nsplit == 1) {
+        const float inv = 1.0f / l[h];
+        for (int k = 0; k < 4; ++k) {
+          const int e = lane + 64 * k;
+          if (e < d)
+            p.out[(int64_t{it.row} * p.heads + int64_t{hk} * g + h0 + h) * d + e] = o[h][k] * inv;
+        }
+      } else {
+        for (int k = 0; k < 4; ++k) {
+          const int e = lane + 64 * k;
+          if (e < d) p.part_o[(pidx * g + h0 + h) * d + e] = o[h][k];
+        }
+        if (lane == 0) {
+          p.part_ml[(pidx * g + h0 + h) * 2 + 0] = m[h];
+          p.part_ml[(pidx * g + h0 + h) * 2 + 1] = l[h];
+        }
+      }
+    }
+  }
+  if (it.nsplit > 1) ArriveAndMaybeMerge(p, it, rd);
+}
+
+template <class KV>
+hipError_t LaunchTyped(const DecodeParams& p, hipStream_t stream) {
+  const dim3 grid((p.n_items + kWavesPerBlock - 1) / kWavesPerBlock);
+  const dim3 block(kWavesPerBlock * 64);
+  constexpr int EPV = KvT<KV>::EPV;
+  const bool aligned = (reinterpret_cast<uintptr_t>(p.k_slab) % 16 == 0) &&
+                       (reinterpret_cast<uintptr_t>(p.v_slab) % 16 == 0) &&
+                       (reinterpret_cast<uintptr_t>(p.q) % 16 == 0) &&
+                       (reinterpret_cast<uintptr_t>(p.out) % 16 == 0) &&
+                       (p.block_stride % EPV == 0);
+#define EHIP_DECODE_CASE(DD, GG)                                              \
+  if (p.d == DD && p.group == GG) {                                           \
+    hipLaunchKernelGGL((DecodeValu<KV, DD, GG>), grid, block, 0, stream, p); \
+    return hipGetLastError();                                                 \
+  }
+  if (aligned) {
+    EHIP_DECODE_CASE(64, 1)
+    EHIP_DECODE_CASE(64, 2)
+    EHIP_DECODE_CASE(64, 4)
+    EHIP_DECODE_CASE(64, 7)
+    EHIP_DECODE_CASE(64, 8)
+    EHIP_DECODE_CASE(128, 1)
+    EHIP_DECODE_CASE(128, 2)
+    EHIP_DECODE_CASE(128, 4)
+    EHIP_DECODE_CASE(128, 7)
+    EHIP_DECODE_CASE(128, 8)
+  }
+#undef EHIP_DECODE_CASE
+  hipLaunchKernelGGL((DecodeGeneric<KV>), grid, block, 0, stream, p);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t LaunchDecode(const DecodeParams& p, int kv_dtype, hipStream_t stream) {
+  if (p.n_items == 0) return hipSuccess;
+  return kv_dtype == EHIP_KV_BF16 ? LaunchTyped<uint16_t>(p, stream)
+                                  : LaunchTyped<float>(p, stream);
+}
+
+}  // namespace ehip

@@ -1,0 +1,207 @@
+#include "plan.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+
+namespace ehip {
+namespace {
+
+constexpr int32_t kTile = 64;             // split lengths are whole 64-key units
+constexpr int64_t kTargetItems = 6144;    // ~6 wavefront work items per SIMD (1024 SIMDs)
+constexpr int32_t kMinSplit = 128;
+constexpr int32_t kMaxSplitsPerRow = 64;  // bounds the merge a single wave performs
+
+int Fail(std::string* err, int code, const char* fmt, long long a = 0, long long b = 0,
+         long long c = 0) {
+  char buf[256];
+  std::snprintf(buf, sizeof(buf), fmt, a, b, c);
+  if (err) *err = buf;
+  return code;
+}
+
+int64_t RoundUp(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+
+}  // namespace
+
+int64_t BlockStride(const ehip_geometry& g) {
+  return g.block_stride != 0 ? g.block_stride
+                             : int64_t{g.kv_heads} * g.block_size * g.head_dim;
+}
+
+int ValidateGeometry(const ehip_geometry& g, std::string* err) {
+  if (g.heads < 1 || g.kv_heads < 1 || g.head_dim < 1)
+    return Fail(err, EHIP_INVALID_ARGUMENT, "heads=%lld kv_heads=%lld d=%lld must be >= 1",
+                g.heads, g.kv_heads, g.head_dim);
+  if (g.heads % g.kv_heads != 0)
+    return Fail(err, EHIP_INVALID_ARGUMENT, "heads=%lld is not a multiple of kv_heads=%lld",
+                g.heads, g.kv_heads);
+  if (g.head_dim > 256)
+    return Fail(err, EHIP_UNIMPLEMENTED, "head_dim=%lld > 256 is not supported", g.head_dim);
+  if (g.heads / g.kv_heads > 64)
+    return Fail(err, EHIP_UNIMPLEMENTED, "GQA group %lld > 64 is not supported",
+                g.heads / g.kv_heads);
+  // The reference CHECKs bs | 64 (src/kernels/paged_attention.cpp:88-91) and the
+  // pool admits {8,16,32,64} (src/kvcache/block_pool.cpp:28-31).
+  if (g.block_size != 8 && g.block_size != 16 && g.block_size != 32 && g.block_size != 64)
+    return Fail(err, EHIP_INVALID_ARGUMENT,
+                "block_size=%lld must be one of 8, 16, 32, 64 (a power of two dividing 64)",
+                g.block_size);
+  if (g.kv_dtype != EHIP_KV_F32 && g.kv_dtype != EHIP_KV_BF16)
+    return Fail(err, EHIP_INVALID_ARGUMENT, "kv_dtype=%lld is not F32 (0) or BF16 (1)",
+                g.kv_dtype);
+  if (g.reserved != 0) return Fail(err, EHIP_INVALID_ARGUMENT, "reserved field must be 0");
+  if (g.slab_blocks < 1)
+    return Fail(err, EHIP_INVALID_ARGUMENT, "slab_blocks=%lld must be >= 1", g.slab_blocks);
+  const int64_t tile = int64_t{g.kv_heads} * g.block_size * g.head_dim;
+  if (g.block_stride != 0 && g.block_stride < tile)
+    return Fail(err, EHIP_INVALID_ARGUMENT, "block_stride=%lld < Hkv*bs*d=%lld",
+                g.block_stride, tile);
+  if (!std::isfinite(g.scale))
+    return Fail(err, EHIP_INVALID_ARGUMENT, "scale must be finite");
+  return EHIP_OK;
+}
+
+int32_t ChooseSplitTokens(const ehip_geometry& g, int64_t unit_tokens) {
+  const int32_t max_split = 64 * g.block_size;
+  if (const char* env = std::getenv("EHIP_SPLIT_TOKENS")) {
+    const long v = std::strtol(env, nullptr, 10);
+    if (v > 0) return static_cast<int32_t>(std::min<int64_t>(RoundUp(v, kTile), max_split));
+  }
+  int64_t s = (unit_tokens + kTargetItems - 1) / kTargetItems;
+  s = RoundUp(std::max<int64_t>(s, kMinSplit), kTile);
+  return static_cast<int32_t>(std::min<int64_t>(s, max_split));
+}
+
+namespace {
+
+// Row splitting + load-balanced item order, shared by both plan builders.
+void FinishPlan(const ehip_geometry& g, Plan* plan) {
+  int64_t units = 0;
+  for (const RowDesc& r : plan->rows) units += int64_t{r.length} * g.kv_heads;
+  const int32_t base = ChooseSplitTokens(g, units);
+  const int32_t max_split = 64 * g.block_size;
+  plan->split_tokens = base;
+  int64_t split_base = 0;
+  std::vector<WorkItem> full, partial;
+  for (size_t ri = 0; ri < plan->rows.size(); ++ri) {
+    RowDesc& r = plan->rows[ri];
+    int32_t sl = base;
+    if ((r.length + sl - 1) / sl > kMaxSplitsPerRow) {
+      const int64_t want = RoundUp((r.length + kMaxSplitsPerRow - 1) / kMaxSplitsPerRow, kTile);
+      sl = static_cast<int32_t>(std::min<int64_t>(want, max_split));
+    }
+    r.split_len = sl;
+    r.split_base = static_cast<int32_t>(split_base);
+    const int32_t nsplit = (r.length + sl - 1) / sl;
+    split_base += nsplit;
+    for (int32_t hk = 0; hk < g.kv_heads; ++hk) {
+      for (int32_t s = 0; s < nsplit; ++s) {
+        const WorkItem it{static_cast<int32_t>(ri), hk, s, nsplit};
+        const int32_t count = std::min(r.length, (s + 1) * sl) - s * sl;
+        (count == base ? full : partial).push_back(it);
+      }
+    }
+  }
+  // Longest work first so the tail of the dispatch is made of short items.
+  std::stable_sort(partial.begin(), partial.end(), [&](const WorkItem& a, const WorkItem& b) {
+    const RowDesc& ra = plan->rows[a.row];
+    const RowDesc& rb = plan->rows[b.row];
+    const int32_t ca = std::min(ra.length, (a.split + 1) * ra.split_len) - a.split * ra.split_len;
+    const int32_t cb = std::min(rb.length, (b.split + 1) * rb.split_len) - b.split * rb.split_len;
+    return ca > cb;
+  });
+  plan->items.clear();
+  plan->items.reserve(full.size() + partial.size());
+  plan->items.insert(plan->items.end(), full.begin(), full.end());
+  plan->items.insert(plan->items.end(), partial.begin(), partial.end());
+  plan->partials = split_base * g.kv_heads;
+}
+
+}  // namespace
+
+int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::string* err) {
+  if (int rc = ValidateGeometry(g, err)) return rc;
+  if (s.num_seqs < 0) return Fail(err, EHIP_INVALID_ARGUMENT, "num_seqs=%lld < 0", s.num_seqs);
+  if (s.reserved != 0) return Fail(err, EHIP_INVALID_ARGUMENT, "reserved field must be 0");
+  plan->rows.clear();
+  plan->items.clear();
+  plan->table_ids.clear();
+  plan->slots.clear();
+  plan->partials = 0;
+  const int32_t B = s.num_seqs;
+  if (B == 0) {
+    FinishPlan(g, plan);
+    return EHIP_OK;
+  }
+  if (!s.h_query_lens || !s.h_context_lens || !s.h_table_offsets || !s.h_table_ids)
+    return Fail(err, EHIP_INVALID_ARGUMENT, "step arrays must be non-null");
+  if (s.h_table_offsets[0] != 0)
+    return Fail(err, EHIP_INVALID_ARGUMENT, "table_offsets[0]=%lld must be 0",
+                s.h_table_offsets[0]);
+  int64_t total_rows = 0;
+  for (int32_t b = 0; b < B; ++b) {
+    const int64_t T = s.h_query_lens[b];
+    const int64_t L = s.h_context_lens[b];
+    if (T < 1) return Fail(err, EHIP_INVALID_ARGUMENT, "query_lens[%lld]=%lld < 1", b, T);
+    if (L < T || L > (int64_t{1} << 30))
+      return Fail(err, EHIP_INVALID_ARGUMENT, "context_lens[%lld]=%lld out of range (T=%lld)",
+                  b, L, T);
+    const int64_t lo = s.h_table_offsets[b], hi = s.h_table_offsets[b + 1];
+    const int64_t need = (L + g.block_size - 1) / g.block_size;
+    if (hi < lo || hi - lo < need)
+      return Fail(err, EHIP_INVALID_ARGUMENT,
+                  "sequence %lld: table has %lld entries, needs ceil(L/bs)=%lld", b, hi - lo,
+                  need);
+    for (int64_t i = lo; i < lo + need; ++i) {
+      const int32_t id = s.h_table_ids[i];
+      if (id < 0 || id >= g.slab_blocks)
+        return Fail(err, EHIP_INVALID_ARGUMENT, "sequence %lld: block id %lld outside [0, %lld)",
+                    b, id, g.slab_blocks);
+    }
+    total_rows += T;
+  }
+  const int64_t n_ids = s.h_table_offsets[B];
+  if (n_ids > (int64_t{1} << 31) - 1 || total_rows > (int64_t{1} << 24))
+    return Fail(err, EHIP_INVALID_ARGUMENT, "step too large (%lld ids, %lld rows)", n_ids,
+                total_rows);
+  plan->table_ids.assign(s.h_table_ids, s.h_table_ids + n_ids);
+  plan->rows.reserve(total_rows);
+  for (int32_t b = 0; b < B; ++b) {
+    const int32_t T = s.h_query_lens[b];
+    const int64_t L = s.h_context_lens[b];
+    const int64_t P = L - T;
+    for (int32_t t = 0; t < T; ++t)
+      plan->rows.push_back(RowDesc{s.h_table_offsets[b], static_cast<int32_t>(P + t + 1), 0, 0});
+  }
+  if (s.h_slot_mapping) {
+    const int64_t cap = g.slab_blocks * g.block_size;
+    for (int64_t i = 0; i < total_rows; ++i) {
+      const int64_t slot = s.h_slot_mapping[i];
+      if (slot < 0 || slot >= cap)
+        return Fail(err, EHIP_INVALID_ARGUMENT, "slot_mapping[%lld]=%lld outside [0, %lld)", i,
+                    slot, cap);
+    }
+    plan->slots.assign(s.h_slot_mapping, s.h_slot_mapping + total_rows);
+  }
+  FinishPlan(g, plan);
+  return EHIP_OK;
+}
+
+int BuildSingleRowPlan(const ehip_geometry& g, int64_t length, int64_t num_blocks, Plan* plan,
+                       std::string* err) {
+  if (int rc = ValidateGeometry(g, err)) return rc;
+  if (length < 1 || length > (int64_t{1} << 30))
+    return Fail(err, EHIP_INVALID_ARGUMENT, "length=%lld out of range", length);
+  if ((length + g.block_size - 1) / g.block_size > num_blocks)
+    return Fail(err, EHIP_INVALID_ARGUMENT, "ceil(length/bs) exceeds num_blocks=%lld",
+                num_blocks);
+  plan->rows.assign(1, RowDesc{0, static_cast<int32_t>(length), 0, 0});
+  plan->table_ids.clear();
+  plan->slots.clear();
+  FinishPlan(g, plan);
+  return EHIP_OK;
+}
+
+}  // namespace ehip

@@ -26,3 +26,19 @@ def orc():
 def golden():
     from safetensors.numpy import load_file
     return load_file(str(ROOT / "tests" / "golden" / "hf_attention.safetensors"))
+
+
+@pytest.fixture(scope="session")
+def ehip_mod():
+    import ehip
+    ehip.lib()
+    return ehip
+
+
+@pytest.fixture(scope="session")
+def gctx(ehip_mod):
+    """One HIP context for the whole GPU session (fails loudly without a GPU:
+    there is no CPU fallback behind the GPU tests)."""
+    ctx = ehip_mod.Context(0)
+    yield ctx
+    ctx.close()

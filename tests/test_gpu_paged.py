@@ -1,0 +1,416 @@
+"""GPU parity: the HIP path (through the C ABI) against the CPU oracle.
+
+Bars (from the path's contract): indexing and append bit-exact; fp32 outputs
+within 1e-4 relative error of the scalar reference attention (per output
+vector, max|a-b| / max|b|) and inside the reference's own allclose
+(rtol 1e-4, atol 1e-5, src/tensor/ops.h:207); bf16-KV outputs within 2e-2
+absolute of the fp32 reference, and within 1e-4 relative of the reference run
+on the same bf16-rounded K/V.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from gpu_util import max_abs, new_rows, rel_norm, seeded_pool
+from paged_util import POISON, allclose_ref, brute_force_f64, normal, paged_layout, scale_for
+
+pytestmark = pytest.mark.gpu
+
+FP32_REL = 1e-4
+BF16_ABS = 2e-2
+
+
+def check_fp32(out, ref):
+    assert rel_norm(out, ref) <= FP32_REL, rel_norm(out, ref)
+    assert allclose_ref(out, ref, 1e-4, 1e-5)
+
+
+# ------------------------------------------------------------------ append
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("d,hkv,bs", [(64, 2, 16), (128, 8, 16), (16, 2, 8), (18, 3, 32),
+                                      (24, 1, 64)])
+def test_kv_scatter_bit_exact(gctx, orc, bf16, d, hkv, bs):
+    rng = np.random.default_rng(d * 7 + hkv + bs)
+    nb, T = 40, 97
+    slots = rng.permutation(nb * bs)[:T].astype(np.int64)  # boundary-straddling, non-monotone
+    src_k = normal(rng, (T, hkv, d), 3.0)
+    src_v = normal(rng, (T, hkv, d), 3.0)
+    dt = np.uint16 if bf16 else np.float32
+    k_ref = np.zeros((nb, hkv, bs, d), dt)
+    v_ref = np.zeros((nb, hkv, bs, d), dt)
+    orc.kv_scatter(src_k, src_v, slots, hkv, d, bs, k_ref, v_ref)
+    dk, dv = gctx.alloc(k_ref.nbytes), gctx.alloc(v_ref.nbytes)
+    rc = gctx.kv_scatter(gctx.to_device(src_k), gctx.to_device(src_v), gctx.to_device(slots),
+                         T, hkv, d, bs, nb, dk, dv, bf16)
+    assert rc == 0, gctx.last_error()
+    gctx.sync()
+    assert np.array_equal(dk.download(dt, k_ref.shape).view(np.uint8), k_ref.view(np.uint8))
+    assert np.array_equal(dv.download(dt, v_ref.shape).view(np.uint8), v_ref.view(np.uint8))
+
+
+def test_kv_scatter_bf16_special_values(gctx, orc):
+    # RNE ties, carry into inf, NaN payload quieting, denormals, signed zero.
+    bits = np.array([0x3F808000, 0x3F818000, 0x7F7FFFFF, 0x7F800001, 0xFFC00000, 0x7F810000,
+                     0x00000001, 0x80000000, 0x7F800000, 0xFF800000, 0x007FFFFF, 0x3F7FFFFF,
+                     0x40490FDB, 0xC0490FDB, 0x00008000, 0x00018000], np.uint32)
+    src = bits.view(np.float32).reshape(1, 1, 16)
+    slots = np.array([5], np.int64)
+    ref_k = np.zeros((2, 1, 8, 16), np.uint16)
+    ref_v = np.zeros((2, 1, 8, 16), np.uint16)
+    orc.kv_scatter(src, src, slots, 1, 16, 8, ref_k, ref_v)
+    dk, dv = gctx.alloc(ref_k.nbytes), gctx.alloc(ref_v.nbytes)
+    s = gctx.to_device(src)
+    assert gctx.kv_scatter(s, s, gctx.to_device(slots), 1, 1, 16, 8, 2, dk, dv, True) == 0
+    gctx.sync()
+    assert np.array_equal(dk.download(np.uint16, ref_k.shape), ref_k)
+
+
+def test_kv_scatter_rejects_out_of_range_slot(gctx, ehip_mod):
+    # The kernel bounds every slot before writing; the range error surfaces at sync.
+    src = np.ones((2, 1, 16), np.float32)
+    slots = np.array([3, 2 * 8], np.int64)  # the second slot is one past a 2-block slab
+    dk, dv = gctx.alloc(2 * 8 * 16 * 4), gctx.alloc(2 * 8 * 16 * 4)
+    s = gctx.to_device(src)
+    assert gctx.kv_scatter(s, s, gctx.to_device(slots), 2, 1, 16, 8, 2, dk, dv, False) == 0
+    with pytest.raises(ehip_mod.EhipError) as e:
+        gctx.sync()
+    assert e.value.code == ehip_mod.INVALID_ARGUMENT
+    gctx.sync()  # the flag was cleared
+    got = dk.download(np.float32, (2, 1, 8, 16))
+    assert np.all(got[0, 0, 3] == 1) and np.count_nonzero(got) == 16
+
+
+def test_kv_gather_round_trip(gctx, orc):
+    rng = np.random.default_rng(11)
+    hkv, d, bs, L = 2, 24, 8, 61
+    k = normal(rng, (hkv, L, d))
+    v = normal(rng, (hkv, L, d))
+    ks, vs, table = paged_layout(k, v, bs, extra_blocks=3, rng=rng)
+    ok, ov = gctx.alloc(k.nbytes), gctx.alloc(v.nbytes)
+    rc = gctx.kv_gather(gctx.to_device(ks), gctx.to_device(vs), gctx.to_device(table), bs, L,
+                        hkv, d, ks.shape[0], ok, ov)
+    assert rc == 0
+    gctx.sync()
+    assert np.array_equal(ok.download(np.float32, k.shape), k)
+    assert np.array_equal(ov.download(np.float32, v.shape), v)
+    rk, rv = orc.kv_gather(ks, vs, table, bs, L, hkv, d)
+    assert np.array_equal(rk, k) and np.array_equal(rv, v)
+
+
+# ------------------------------------------------------------------ decode
+def run_single(gctx, q, ks, vs, table, L, H, Hkv, d, bs, scale):
+    out = gctx.alloc(q.nbytes)
+    rc = gctx.paged_decode(gctx.to_device(q), gctx.to_device(ks), gctx.to_device(vs),
+                           gctx.to_device(table), len(table), L, H, Hkv, d, bs, Hkv * bs * d,
+                           ks.shape[0], scale, out)
+    assert rc == 0, gctx.last_error()
+    gctx.sync()
+    return out.download(np.float32, q.shape)
+
+
+def test_c1_single_sequence_decode(gctx, orc, ehip_mod):
+    """C1: Qwen2-0.5B shape, 512 cached + 1 appended token in a permuted
+    33-of-64 block table; append on the GPU, then attend."""
+    from ehip import workloads
+    w = workloads.c1()
+    kpool, vpool = seeded_pool(orc, w, 101)
+    kn, vn, q = new_rows(orc, w, 201)
+    d, H, Hkv, bs = w.head_dim, w.heads, w.kv_heads, w.block_size
+    dk, dv = gctx.to_device(kpool), gctx.to_device(vpool)
+    rc = gctx.kv_scatter(gctx.to_device(kn), gctx.to_device(vn), gctx.to_device(w.slot_mapping),
+                         1, Hkv, d, bs, w.pool_blocks, dk, dv, False)
+    assert rc == 0
+    orc.kv_scatter(kn, vn, w.slot_mapping, Hkv, d, bs, kpool, vpool)
+    gctx.sync()
+    assert np.array_equal(dk.download(np.float32, kpool.shape).view(np.uint32),
+                          kpool.view(np.uint32))
+    out = gctx.alloc(q.nbytes)
+    rc = gctx.paged_decode(gctx.to_device(q), dk, dv, gctx.to_device(w.tables[0]), 33, 513, H,
+                           Hkv, d, bs, Hkv * bs * d, w.pool_blocks, w.scale, out)
+    assert rc == 0, gctx.last_error()
+    gctx.sync()
+    got = out.download(np.float32, (H, d))
+    ref = orc.paged_decode(q[0], kpool, vpool, w.tables[0], 513, H, Hkv, d, bs, w.scale)
+    check_fp32(got, ref)
+    kc = orc.paged_to_contig(kpool, w.tables[0], 513, Hkv, d, bs)
+    vc = orc.paged_to_contig(vpool, w.tables[0], 513, Hkv, d, bs)
+    bf = brute_force_f64(q, kc, vc, H, Hkv, w.scale)[0]
+    assert rel_norm(got, bf) <= FP32_REL
+
+
+@pytest.mark.parametrize("H,Hkv", [(4, 4), (4, 2), (8, 1), (24, 2), (14, 2), (32, 8), (64, 8)])
+@pytest.mark.parametrize("d", [18, 24, 64, 128])
+def test_decode_gqa_and_head_dim_sweep(gctx, orc, H, Hkv, d):
+    rng = np.random.default_rng(H * 1000 + Hkv * 10 + d)
+    L, bs = 300, 16
+    q = normal(rng, (H, d), 2.0)
+    k = normal(rng, (Hkv, L, d), 2.0)
+    v = normal(rng, (Hkv, L, d), 2.0)
+    ks, vs, table = paged_layout(k, v, bs, extra_blocks=2)
+    scale = scale_for(d)
+    got = run_single(gctx, q, ks, vs, table, L, H, Hkv, d, bs, scale)
+    ref = orc.paged_decode(q, ks, vs, table, L, H, Hkv, d, bs, scale)
+    check_fp32(got, ref)
+
+
+@pytest.mark.parametrize("bs", [8, 16, 32, 64])
+@pytest.mark.parametrize("L", [1, 7, 8, 9, 15, 16, 17, 63, 64, 65, 127, 128, 129, 511, 2048, 4096])
+def test_decode_length_and_block_size_sweep(gctx, orc, bs, L):
+    rng = np.random.default_rng(L * 131 + bs)
+    H, Hkv, d = 8, 2, 64
+    q = normal(rng, (H, d))
+    k = normal(rng, (Hkv, L, d))
+    v = normal(rng, (Hkv, L, d))
+    ks, vs, table = paged_layout(k, v, bs, extra_blocks=1)  # reverse-permuted, poisoned
+    got = run_single(gctx, q, ks, vs, table, L, H, Hkv, d, bs, scale_for(d))
+    ref = orc.paged_decode(q, ks, vs, table, L, H, Hkv, d, bs, scale_for(d))
+    check_fp32(got, ref)
+
+
+def test_decode_single_key_and_equal_keys_closed_forms(gctx):
+    # L = 1: out[h] = v[h // g, 0] exactly; equal keys: out = mean of V rows.
+    rng = np.random.default_rng(5)
+    H, Hkv, d, bs = 8, 2, 64, 16
+    q = normal(rng, (H, d))
+    k = normal(rng, (Hkv, 1, d))
+    v = normal(rng, (Hkv, 1, d))
+    ks, vs, table = paged_layout(k, v, bs)
+    got = run_single(gctx, q, ks, vs, table, 1, H, Hkv, d, bs, 0.125)
+    assert np.array_equal(got, v[np.arange(H) // 4, 0])
+    L = 100
+    k = np.repeat(normal(rng, (Hkv, 1, d)), L, axis=1)
+    v = normal(rng, (Hkv, L, d))
+    ks, vs, table = paged_layout(k, v, bs)
+    got = run_single(gctx, q, ks, vs, table, L, H, Hkv, d, bs, 0.125)
+    mean = v.astype(np.float64).mean(axis=1)[np.arange(H) // 4]
+    assert rel_norm(got, mean) <= 1e-5
+
+
+def test_decode_large_magnitude_inputs(gctx, orc):
+    rng = np.random.default_rng(9)
+    H, Hkv, d, bs, L = 32, 8, 128, 16, 1500
+    q = normal(rng, (H, d), 6.0)
+    k = normal(rng, (Hkv, L, d), 6.0)
+    v = normal(rng, (Hkv, L, d), 2.0)
+    ks, vs, table = paged_layout(k, v, bs, rng=rng, extra_blocks=7)
+    got = run_single(gctx, q, ks, vs, table, L, H, Hkv, d, bs, scale_for(d))
+    ref = orc.paged_decode(q, ks, vs, table, L, H, Hkv, d, bs, scale_for(d))
+    check_fp32(got, ref)
+
+
+@pytest.mark.parametrize("name", ["l0_prefill_empty", "l1_prefill_empty", "l0_prefill_continue",
+                                  "l1_prefill_continue", "l0_decode"])
+def test_decode_matches_hf_goldens(gctx, golden, name):
+    # Last query row of each HF case is the decode of its final token
+    # (tests/unit/paged_decode_attention_kernel_test.cpp:388-444, bs = 8).
+    q, k, v, ctx = (golden[f"{name}.{s}"] for s in ("q_rot", "k_all", "v_all", "ctx"))
+    ks, vs, table = paged_layout(k, v, 8, extra_blocks=1)
+    got = run_single(gctx, q[-1], ks, vs, table, k.shape[1], 4, 2, 16, 8, 0.25)
+    assert allclose_ref(got, ctx[-1], 1e-4, 1e-4)
+
+
+def test_decode_rejects_bad_block_size_and_zero_batch(gctx, ehip_mod):
+    q = np.zeros((4, 16), np.float32)
+    dq = gctx.to_device(q)
+    slab = gctx.alloc(4 * 2 * 12 * 16 * 4)
+    tab = gctx.to_device(np.arange(4, dtype=np.int32))
+    out = gctx.alloc(q.nbytes)
+    rc = gctx.paged_decode(dq, slab, slab, tab, 4, 20, 4, 2, 16, 12, 2 * 12 * 16, 4, 0.25, out)
+    assert rc == ehip_mod.INVALID_ARGUMENT
+    assert "block_size" in gctx.last_error()
+    # B == 0 is a no-op (paged_attention.h: "B == 0 is a no-op").
+    rc = gctx.paged_decode_batched(None, None, None, [], [], 4, 2, 16, 16, 0, 4, 0.25, None)
+    assert rc == 0
+
+
+def test_decode_table_id_out_of_range_is_reported(gctx, ehip_mod):
+    # Device-resident table: the kernel bounds every id it dereferences and
+    # the host learns of the bad id at sync.
+    H, Hkv, d, bs, L = 4, 2, 64, 16, 40
+    q = np.ones((H, d), np.float32)
+    slab = gctx.alloc(4 * Hkv * bs * d * 4)
+    tab = gctx.to_device(np.array([0, 1, 99], np.int32))
+    out = gctx.alloc(q.nbytes)
+    assert gctx.paged_decode(gctx.to_device(q), slab, slab, tab, 3, L, H, Hkv, d, bs,
+                             Hkv * bs * d, 4, 0.125, out) == 0
+    with pytest.raises(ehip_mod.EhipError) as e:
+        gctx.sync()
+    assert e.value.code == ehip_mod.INVALID_ARGUMENT
+    # Host tables are validated before anything is enqueued.
+    rc = gctx.paged_decode_batched(gctx.to_device(q), slab, slab, [np.array([0, 1, 99], np.int32)],
+                                   [L], H, Hkv, d, bs, 0, 4, 0.125, out)
+    assert rc == ehip_mod.INVALID_ARGUMENT
+
+
+# ------------------------------------------------------------------ batched
+def batched_case(orc, rng, lengths, H, Hkv, d, bs):
+    ks_l = [normal(rng, (Hkv, L, d)) for L in lengths]
+    vs_l = [normal(rng, (Hkv, L, d)) for L in lengths]
+    from paged_util import shared_pool_layout
+    k_slab, v_slab, tables = shared_pool_layout(ks_l, vs_l, bs, rng)
+    q = normal(rng, (len(lengths), H, d))
+    return q, k_slab, v_slab, tables
+
+
+@pytest.mark.parametrize("bs", [8, 16, 32, 64])
+def test_batched_decode_heterogeneous_lengths(gctx, orc, bs):
+    rng = np.random.default_rng(bs)
+    lengths = [1, bs, 2 * bs + 1, 63, 128, 300, 1000]
+    H, Hkv, d = 14, 2, 64
+    q, ks, vs, tables = batched_case(orc, rng, lengths, H, Hkv, d, bs)
+    out = gctx.alloc(q.nbytes)
+    rc = gctx.paged_decode_batched(gctx.to_device(q), gctx.to_device(ks), gctx.to_device(vs),
+                                   tables, lengths, H, Hkv, d, bs, 0, ks.shape[0],
+                                   scale_for(d), out)
+    assert rc == 0, gctx.last_error()
+    gctx.sync()
+    got = out.download(np.float32, q.shape)
+    ref = orc.paged_decode_batched(q, ks, vs, tables, lengths, H, Hkv, d, bs, scale_for(d))
+    check_fp32(got, ref)
+    # Each member equals a standalone single-sequence run (within tolerance:
+    # the split partition may differ with the batch's total work).
+    for b in (0, 3, 6):
+        single = run_single(gctx, q[b], ks, vs, tables[b], lengths[b], H, Hkv, d, bs,
+                            scale_for(d))
+        assert rel_norm(got[b], single) <= FP32_REL
+
+
+def test_batched_decode_bf16_kv(gctx, orc):
+    rng = np.random.default_rng(77)
+    lengths = list(rng.integers(1, 3000, 24))
+    H, Hkv, d, bs = 32, 8, 128, 16
+    q, ks, vs, tables = batched_case(orc, rng, lengths, H, Hkv, d, bs)
+    ks_b, vs_b = orc.to_bf16_bits(ks), orc.to_bf16_bits(vs)
+    out = gctx.alloc(q.nbytes)
+    rc = gctx.paged_decode_batched(gctx.to_device(q), gctx.to_device(ks_b), gctx.to_device(vs_b),
+                                   tables, lengths, H, Hkv, d, bs, 0, ks.shape[0],
+                                   scale_for(d), out, bf16=True)
+    assert rc == 0, gctx.last_error()
+    gctx.sync()
+    got = out.download(np.float32, q.shape)
+    ref32 = orc.paged_decode_batched(q, ks, vs, tables, lengths, H, Hkv, d, bs, scale_for(d))
+    assert max_abs(got, ref32) <= BF16_ABS
+    ref_r = orc.paged_decode_batched(q, orc.bf16_bits_to_f32(ks_b), orc.bf16_bits_to_f32(vs_b),
+                                     tables, lengths, H, Hkv, d, bs, scale_for(d))
+    check_fp32(got, ref_r)
+
+
+@pytest.mark.parametrize("split", ["64", "128", "512", "1024"])
+def test_split_count_independence(gctx, orc, split, monkeypatch):
+    # The merged result must not depend on how the keys were split.
+    monkeypatch.setenv("EHIP_SPLIT_TOKENS", split)
+    rng = np.random.default_rng(3)
+    lengths = [4000, 17, 1025, 2048, 64]
+    H, Hkv, d, bs = 32, 8, 128, 16
+    q, ks, vs, tables = batched_case(orc, rng, lengths, H, Hkv, d, bs)
+    out = gctx.alloc(q.nbytes)
+    assert gctx.paged_decode_batched(gctx.to_device(q), gctx.to_device(ks), gctx.to_device(vs),
+                                     tables, lengths, H, Hkv, d, bs, 0, ks.shape[0],
+                                     scale_for(d), out) == 0
+    gctx.sync()
+    got = out.download(np.float32, q.shape)
+    ref = orc.paged_decode_batched(q, ks, vs, tables, lengths, H, Hkv, d, bs, scale_for(d))
+    check_fp32(got, ref)
+
+
+# ------------------------------------------------------------------ step path
+def run_step(gctx, ehip_mod, orc, w, seed, layers=1):
+    """Upload one step, then per layer append + attend on the GPU; the oracle
+    does the same with its scatter and varlen reference."""
+    H, Hkv, d, bs = w.heads, w.kv_heads, w.head_dim, w.block_size
+    bf16 = w.kv_dtype == ehip_mod.KV_BF16
+    g = ehip_mod.geometry(H, Hkv, d, bs, w.kv_dtype, w.pool_blocks, w.scale)
+    st = ehip_mod.StepArrays(w.query_lens, w.context_lens, w.tables, w.slot_mapping)
+    assert gctx.step_upload(g, st) == 0, gctx.last_error()
+    results = []
+    for layer in range(layers):
+        kpool, vpool = seeded_pool(orc, w, seed + 1000 * layer)
+        kn, vn, q = new_rows(orc, w, seed + 1000 * layer + 500)
+        if bf16:
+            dk = gctx.to_device(orc.to_bf16_bits(kpool))
+            dv = gctx.to_device(orc.to_bf16_bits(vpool))
+        else:
+            dk, dv = gctx.to_device(kpool), gctx.to_device(vpool)
+        dq = gctx.to_device(q)
+        out = gctx.alloc(q.nbytes)
+        assert gctx.step_kv_append(gctx.to_device(kn), gctx.to_device(vn), dk, dv) == 0
+        assert gctx.step_attention(dq, dk, dv, out) == 0, gctx.last_error()
+        gctx.sync()
+        got = out.download(np.float32, q.shape)
+        # Oracle: the same append (bit-exact check of the whole slab), then
+        # the reference attention over the post-append cache.
+        if bf16:
+            kb, vb = orc.to_bf16_bits(kpool), orc.to_bf16_bits(vpool)
+            orc.kv_scatter(kn, vn, w.slot_mapping, Hkv, d, bs, kb, vb)
+            assert np.array_equal(dk.download(np.uint16, kb.shape), kb)
+            assert np.array_equal(dv.download(np.uint16, vb.shape), vb)
+            kref, vref = orc.bf16_bits_to_f32(kb), orc.bf16_bits_to_f32(vb)
+            orc.kv_scatter(kn, vn, w.slot_mapping, Hkv, d, bs, kpool, vpool)
+        else:
+            orc.kv_scatter(kn, vn, w.slot_mapping, Hkv, d, bs, kpool, vpool)
+            assert np.array_equal(dk.download(np.float32, kpool.shape).view(np.uint32),
+                                  kpool.view(np.uint32))
+            kref, vref = kpool, vpool
+        cu = np.concatenate([[0], np.cumsum(w.query_lens)]).astype(np.int32)
+        kseq = [orc.paged_to_contig(kref, t, int(L), Hkv, d, bs) for t, L in
+                zip(w.tables, w.context_lens)]
+        vseq = [orc.paged_to_contig(vref, t, int(L), Hkv, d, bs) for t, L in
+                zip(w.tables, w.context_lens)]
+        ref = orc.prefill_varlen(q, cu, kseq, vseq, H, Hkv, d, w.scale, isa=1)
+        results.append((got, ref, kpool, vpool, q, cu))
+        for b in (dk, dv, dq, out):
+            b.free()
+    return results
+
+
+def test_step_c2_ragged_decode(gctx, ehip_mod, orc):
+    """C2 shape (B=32, L~U[64,2048]+1, fp32 pool 1.25x need): two layers of
+    append + attention through the per-step descriptor."""
+    from ehip import workloads
+    w = workloads.c2()
+    for got, ref, *_ in run_step(gctx, ehip_mod, orc, w, 7, layers=2):
+        check_fp32(got, ref)
+
+
+def test_step_c3_mixed_prefill_and_decode(gctx, ehip_mod, orc):
+    """C3 composition scaled down (2 causal chunks + 12 decodes, bf16 KV): one
+    launch covers chunk rows and decode rows."""
+    from ehip import workloads
+    w = workloads.c3()
+    keep = [0, 1] + list(range(4, 16))
+    w.query_lens = w.query_lens[keep].copy()
+    w.context_lens = w.context_lens[keep].copy()
+    w.tables = [w.tables[i] for i in keep]
+    w.slot_mapping = workloads._append_slots(w.tables, w.query_lens, w.context_lens,
+                                             w.block_size)
+    (got, ref, kpool, vpool, q, cu), = run_step(gctx, ehip_mod, orc, w, 9)
+    check_fp32(got, ref)   # vs the reference on the same bf16-rounded K/V
+    # and vs fp32 K/V
+    H, Hkv, d, bs = w.heads, w.kv_heads, w.head_dim, w.block_size
+    kseq = [orc.paged_to_contig(kpool, t, int(L), Hkv, d, bs) for t, L in
+            zip(w.tables, w.context_lens)]
+    vseq = [orc.paged_to_contig(vpool, t, int(L), Hkv, d, bs) for t, L in
+            zip(w.tables, w.context_lens)]
+    ref32 = orc.prefill_varlen(q, cu, kseq, vseq, H, Hkv, d, w.scale, isa=1)
+    assert max_abs(got, ref32) <= BF16_ABS
+
+
+def test_step_c4_shape_with_shared_prefix_blocks(gctx, ehip_mod, orc):
+    """C4 construction (log-uniform lengths, pair-shared prefix blocks, bf16)
+    at 24 sequences."""
+    from ehip import workloads
+    w = workloads.c4(num_seqs=24, share_frac=0.3)
+    assert (w.refcount == 2).any()
+    (got, ref, *_), = run_step(gctx, ehip_mod, orc, w, 13)
+    check_fp32(got, ref)
+
+
+def test_step_requires_upload_and_validates(gctx, ehip_mod):
+    g = ehip_mod.geometry(4, 2, 64, 16, 0, 8, 0.125)
+    bad = ehip_mod.StepArrays([1], [40], [np.array([0, 1], np.int32)])  # needs 3 blocks
+    assert gctx.step_upload(g, bad) == ehip_mod.INVALID_ARGUMENT
+    bad = ehip_mod.StepArrays([1], [20], [np.array([0, 8], np.int32)])  # id 8 of 8 blocks
+    assert gctx.step_upload(g, bad) == ehip_mod.INVALID_ARGUMENT
+    bad = ehip_mod.StepArrays([1], [20], [np.array([0, 1], np.int32)], [8 * 16])
+    assert gctx.step_upload(g, bad) == ehip_mod.INVALID_ARGUMENT

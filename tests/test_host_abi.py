@@ -1,0 +1,150 @@
+"""Host-side checks of the C ABI (no GPU needed): the library loads, exports
+every function include/ehip.h declares, and the step planner validates and
+partitions ragged steps as specified."""
+import ctypes as C
+import math
+
+import numpy as np
+import pytest
+
+
+def test_library_exports_every_declared_symbol(ehip_mod):
+    L = ehip_mod.lib()
+    names = ehip_mod.header_symbols()
+    assert len(names) >= 20
+    for n in names:
+        assert hasattr(L, n), n
+
+
+def test_device_count_without_context(ehip_mod):
+    assert ehip_mod.device_count() >= 0
+
+
+def geom(ehip_mod, **kw):
+    base = dict(heads=32, kv_heads=8, head_dim=128, block_size=16, kv_dtype=1, slab_blocks=1000,
+                scale=0.088)
+    base.update(kw)
+    return ehip_mod.geometry(**base)
+
+
+def simple_step(ehip_mod, lens, qlens=None, bs=16, slots=None, start=0):
+    tabs, off = [], start
+    for L in lens:
+        n = (L + bs - 1) // bs
+        tabs.append(np.arange(off, off + n, dtype=np.int32))
+        off += n
+    q = np.ones(len(lens), np.int32) if qlens is None else qlens
+    return ehip_mod.StepArrays(q, lens, tabs, slots)
+
+
+def expected_items(lens, hkv, split, bs=16):
+    items = 0
+    for L in lens:
+        s = split
+        if math.ceil(L / s) > 64:
+            s = min(64 * bs, math.ceil(math.ceil(L / 64) / 64) * 64)
+        items += math.ceil(L / s) * hkv
+    return items
+
+
+def test_plan_partitions_c4_shape(ehip_mod):
+    from ehip import workloads
+    w = workloads.c4()
+    g = ehip_mod.geometry(w.heads, w.kv_heads, w.head_dim, w.block_size, w.kv_dtype,
+                          w.pool_blocks, w.scale)
+    st = ehip_mod.StepArrays(w.query_lens, w.context_lens, w.tables, w.slot_mapping)
+    rc, rows, items, partials, split = ehip_mod.plan_counts(g, st)
+    assert rc == 0
+    assert rows == 256
+    assert split % 64 == 0 and 128 <= split <= 64 * w.block_size
+    assert items == expected_items(w.context_lens, w.kv_heads, split)
+    assert partials == items  # one partial slot per (row, kv head, split)
+
+
+def test_plan_split_override_and_long_rows(ehip_mod, monkeypatch):
+    monkeypatch.setenv("EHIP_SPLIT_TOKENS", "100")  # rounds up to 128
+    lens = [32768, 5, 128, 129]
+    rc, rows, items, partials, split = ehip_mod.plan_counts(
+        geom(ehip_mod, slab_blocks=4000), simple_step(ehip_mod, lens))
+    assert rc == 0 and split == 128
+    # 32768 keys would need 256 splits of 128: the row's split grows to keep
+    # at most 64 splits (512 keys each).
+    assert items == 8 * (64 + 1 + 1 + 2)
+
+
+def test_plan_prefill_rows_are_causal(ehip_mod, monkeypatch):
+    monkeypatch.setenv("EHIP_SPLIT_TOKENS", "128")
+    # One chunk of T=300 on top of P=100 cached tokens: rows attend 101..400 keys.
+    st = simple_step(ehip_mod, [400], qlens=np.array([300], np.int32))
+    rc, rows, items, partials, split = ehip_mod.plan_counts(geom(ehip_mod), st)
+    assert rc == 0 and rows == 300
+    assert items == 8 * sum(math.ceil(n / 128) for n in range(101, 401))
+
+
+def test_plan_empty_step(ehip_mod):
+    st = ehip_mod.StepArrays([], [], [])
+    assert ehip_mod.plan_counts(geom(ehip_mod), st)[:4] == (0, 0, 0, 0)
+
+
+@pytest.mark.parametrize("kw", [dict(block_size=12), dict(block_size=128), dict(heads=30),
+                                dict(kv_dtype=3), dict(head_dim=0), dict(slab_blocks=0),
+                                dict(head_dim=512)])
+def test_plan_rejects_bad_geometry(ehip_mod, kw):
+    rc = ehip_mod.plan_counts(geom(ehip_mod, **kw), simple_step(ehip_mod, [40]))[0]
+    assert rc in (ehip_mod.INVALID_ARGUMENT, ehip_mod.UNIMPLEMENTED)
+
+
+def test_plan_rejects_bad_steps(ehip_mod):
+    g = geom(ehip_mod, slab_blocks=10)
+    # table shorter than ceil(L/bs)
+    st = ehip_mod.StepArrays([1], [40], [np.array([0, 1], np.int32)])
+    assert ehip_mod.plan_counts(g, st)[0] == ehip_mod.INVALID_ARGUMENT
+    # id outside the slab
+    st = ehip_mod.StepArrays([1], [20], [np.array([0, 10], np.int32)])
+    assert ehip_mod.plan_counts(g, st)[0] == ehip_mod.INVALID_ARGUMENT
+    st = ehip_mod.StepArrays([1], [20], [np.array([-1, 3], np.int32)])
+    assert ehip_mod.plan_counts(g, st)[0] == ehip_mod.INVALID_ARGUMENT
+    # slot outside the slab, and a negative slot
+    for bad in (10 * 16, -1):
+        st = ehip_mod.StepArrays([1], [20], [np.array([0, 1], np.int32)], [bad])
+        assert ehip_mod.plan_counts(g, st)[0] == ehip_mod.INVALID_ARGUMENT
+    # T > L, T < 1
+    st = ehip_mod.StepArrays([5], [3], [np.array([0], np.int32)])
+    assert ehip_mod.plan_counts(g, st)[0] == ehip_mod.INVALID_ARGUMENT
+    st = ehip_mod.StepArrays([0], [3], [np.array([0], np.int32)])
+    assert ehip_mod.plan_counts(g, st)[0] == ehip_mod.INVALID_ARGUMENT
+    # a table longer than needed is fine (tables are a bound, like num_blocks)
+    st = ehip_mod.StepArrays([1], [20], [np.array([0, 1, 9, 9], np.int32)])
+    assert ehip_mod.plan_counts(g, st)[0] == 0
+
+
+def test_workload_slots_follow_block_table_closed_form(ehip_mod):
+    from ehip import workloads
+    for w in (workloads.c1(), workloads.c2(), workloads.c3()):
+        r = 0
+        for t, T, L in zip(w.tables, w.query_lens, w.context_lens):
+            for pos in range(int(L) - int(T), int(L)):
+                # slot(pos) = blocks[pos / bs] * bs + pos % bs (block_table.cpp:97-103)
+                assert w.slot_mapping[r] == t[pos // w.block_size] * w.block_size + pos % w.block_size
+                r += 1
+        assert r == len(w.slot_mapping)
+        used = np.concatenate(w.tables)
+        assert len(np.unique(used)) == len(used)  # C1-C3 tables never share
+        assert used.max() < w.pool_blocks
+
+
+def test_c4_sharing_and_byte_accounting():
+    from ehip import workloads
+    w = workloads.c4()
+    rc = w.refcount
+    in_use = int((rc > 0).sum())
+    frac = int((rc == 2).sum()) / in_use
+    assert 0.09 <= frac <= 0.11, frac
+    b = w.bytes_per_layer(with_append=False)
+    row = 8 * 128 * 2 * 2
+    assert b["logical_kv"] == row * int(w.context_lens.sum())
+    assert b["logical_kv"] - b["unique_kv"] == row * 16 * int((rc == 2).sum())
+    # Shared blocks are full prefix blocks of both sharers: the appended token
+    # never lands in one.
+    blocks = w.slot_mapping // w.block_size
+    assert (rc[blocks] == 1).all()
