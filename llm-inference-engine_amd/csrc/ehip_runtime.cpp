@@ -30,12 +30,9 @@ struct ehip_ctx {
   void* d_desc = nullptr;
   size_t d_desc_bytes = 0;
 
-  // Split-KV workspace and merge counters (counters stay zero between
-  // launches: the merging wavefront resets its own).
+  // Split-KV partials (max, sum, unnormalised output per split).
   float* d_part = nullptr;
   size_t d_part_bytes = 0;
-  int32_t* d_counters = nullptr;
-  size_t counters_len = 0;
   int32_t* d_err = nullptr;
 
   // The uploaded step.
@@ -82,7 +79,7 @@ int CheckCtx(ehip_ctx* ctx) {
 
 size_t Align256(size_t x) { return (x + 255) & ~size_t{255}; }
 
-// Grows the split workspace / counters to what `plan` needs.
+// Grows the split-partial workspace to what `plan` needs.
 int EnsureWorkspace(ehip_ctx* ctx, const ehip_geometry& g, const Plan& plan) {
   const int64_t grp = g.heads / g.kv_heads;
   const size_t part_o = static_cast<size_t>(plan.partials) * grp * g.head_dim;
@@ -96,17 +93,6 @@ int EnsureWorkspace(ehip_ctx* ctx, const ehip_geometry& g, const Plan& plan) {
     ctx->d_part_bytes = 0;
     EHIP_HIP(ctx, hipMalloc(&ctx->d_part, bytes));
     ctx->d_part_bytes = bytes;
-  }
-  const size_t ctrs = std::max<size_t>(1, plan.rows.size() * g.kv_heads);
-  if (ctrs > ctx->counters_len) {
-    const size_t len = std::max(ctrs, ctx->counters_len * 3 / 2);
-    EHIP_HIP(ctx, hipStreamSynchronize(ctx->stream));
-    if (ctx->d_counters) EHIP_HIP(ctx, hipFree(ctx->d_counters));
-    ctx->d_counters = nullptr;
-    ctx->counters_len = 0;
-    EHIP_HIP(ctx, hipMalloc(&ctx->d_counters, len * sizeof(int32_t)));
-    EHIP_HIP(ctx, hipMemsetAsync(ctx->d_counters, 0, len * sizeof(int32_t), ctx->stream));
-    ctx->counters_len = len;
   }
   return EHIP_OK;
 }
@@ -183,11 +169,12 @@ int LaunchAttention(ehip_ctx* ctx, const float* q, const void* k_slab, const voi
   const int64_t grp = g.heads / g.kv_heads;
   p.part_o = ctx->d_part;
   p.part_ml = ctx->d_part + static_cast<size_t>(plan.partials) * grp * g.head_dim;
-  p.counters = ctx->d_counters;
   p.err = ctx->d_err;
   p.block_stride = ehip::BlockStride(g);
   p.slab_blocks = g.slab_blocks;
   p.n_items = static_cast<int32_t>(plan.items.size());
+  p.n_rows = static_cast<int32_t>(plan.rows.size());
+  p.need_merge = plan.partials != static_cast<int64_t>(plan.rows.size()) * g.kv_heads;
   p.heads = g.heads;
   p.kv_heads = g.kv_heads;
   p.group = static_cast<int32_t>(grp);
@@ -251,7 +238,6 @@ int ehip_destroy(ehip_ctx* ctx) {
   }
   if (ctx->d_desc) (void)hipFree(ctx->d_desc);
   if (ctx->d_part) (void)hipFree(ctx->d_part);
-  if (ctx->d_counters) (void)hipFree(ctx->d_counters);
   if (ctx->d_err) (void)hipFree(ctx->d_err);
   if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
   delete ctx;

@@ -26,11 +26,12 @@ struct DecodeParams {
   const int32_t* table;     // CSR ids (or a single sequence's table)
   float* part_o;            // [partials, g, d]
   float* part_ml;           // [partials, g, 2]
-  int32_t* counters;        // [rows * Hkv], zero between launches
   int32_t* err;
   int64_t block_stride;     // elements
   int64_t slab_blocks;
   int32_t n_items;
+  int32_t n_rows;
+  int32_t need_merge;       // some row has more than one split
   int32_t heads;
   int32_t kv_heads;
   int32_t group;            // g = H / Hkv
@@ -40,8 +41,14 @@ struct DecodeParams {
 };
 
 // Launch the decode kernel family for the given plan (one wavefront per work
-// item). Picks the specialised (dtype, d, g) kernel or the generic one.
+// item; picks the specialised (dtype, d, g) kernel or the generic one), then,
+// if any row was split, the merge of the split partials. The kernel boundary
+// between the two publishes the partials: no device-wide fences or counters.
 hipError_t LaunchDecode(const DecodeParams& p, int kv_dtype, hipStream_t stream);
+
+// bf16-KV decode with QK^T on MFMA; returns false (nothing launched) when the
+// shape is not covered (d not 64/128, g not 1/2/4/8, bs < 16, misaligned).
+bool LaunchDecodeMfma(const DecodeParams& p, hipStream_t stream, hipError_t* err);
 
 // KvScatter: rows [T, Hkv, d] fp32 into slabs (fp32 copy or bf16 RNE).
 hipError_t LaunchKvScatter(const float* src_k, const float* src_v, const int64_t* slots,

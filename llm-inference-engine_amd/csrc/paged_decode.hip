@@ -18,6 +18,10 @@
 // Softmax: scores are formed as dot * scale * log2(e) and exponentiated with
 // the hardware exp2; the running max/sum are per tile (32 keys), the tile's
 // max is a wavefront reduction, so alpha rescaling happens once per tile.
+#include <cstdlib>
+#include <cstring>
+
+#include "decode_common.h"
 #include "device_util.h"
 #include "kernels.h"
 
@@ -61,57 +65,6 @@ __device__ __forceinline__ void Widen<uint16_t>(const uint4 r, float* o) {
 __device__ __forceinline__ float KvAt(const float* p, int64_t i) { return p[i]; }
 __device__ __forceinline__ float KvAt(const uint16_t* p, int64_t i) {
   return __uint_as_float(uint32_t{p[i]} << 16);
-}
-
-__device__ __forceinline__ int64_t PartialIndex(const RowDesc& rd, int kv_heads, int hk,
-                                                int nsplit, int split) {
-  return int64_t{rd.split_base} * kv_heads + int64_t{hk} * nsplit + split;
-}
-
-// Log-sum-exp merge of one (row, kv head) group's split partials, done by the
-// wavefront that finished last. Splits are combined in split order, so the
-// result does not depend on which wavefront arrived last.
-__device__ void MergeSplits(const DecodeParams& p, int row, int hk, int64_t pbase, int nsplit) {
-  const int lane = threadIdx.x & 63;
-  const int g = p.group, d = p.d;
-  float* out = p.out + (int64_t{row} * p.heads + int64_t{hk} * g) * d;
-  for (int h = 0; h < g; ++h) {
-    float M = -INFINITY;
-    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, p.part_ml[((pbase + s) * g + h) * 2]);
-    float L = 0.f;
-    for (int s = 0; s < nsplit; ++s) {
-      const float* ml = p.part_ml + ((pbase + s) * g + h) * 2;
-      L += ml[1] * Exp2(ml[0] - M);
-    }
-    const float inv = 1.0f / L;
-    for (int e = lane; e < d; e += 64) {
-      float acc = 0.f;
-      for (int s = 0; s < nsplit; ++s) {
-        const float w = Exp2(p.part_ml[((pbase + s) * g + h) * 2] - M);
-        acc += w * p.part_o[((pbase + s) * g + h) * d + e];
-      }
-      out[int64_t{h} * d + e] = acc * inv;
-    }
-  }
-}
-
-// Publish this wavefront's partial and, if it is the last split of its group
-// to finish, merge the group. Release/acquire at agent scope makes the
-// partials of every XCD visible to the merging wavefront.
-__device__ __forceinline__ void ArriveAndMaybeMerge(const DecodeParams& p, const WorkItem& it,
-                                                    const RowDesc& rd) {
-  __threadfence();
-  const int lane = threadIdx.x & 63;
-  int prev = 0;
-  int32_t* ctr = p.counters + int64_t{it.row} * p.kv_heads + it.kv_head;
-  if (lane == 0) prev = atomicAdd(ctr, 1);
-  prev = __shfl(prev, 0);
-  if (prev == it.nsplit - 1) {
-    __threadfence();
-    MergeSplits(p, it.row, it.kv_head, PartialIndex(rd, p.kv_heads, it.kv_head, it.nsplit, 0),
-                it.nsplit);
-    if (lane == 0) *ctr = 0;  // ready for the next launch
-  }
 }
 
 // ----------------------------------------------------------------------------
@@ -308,7 +261,6 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void DecodeValu(DecodeParams p
       p.part_ml[(pidx * G + h) * 2 + 1] = l[h];
     }
   }
-  ArriveAndMaybeMerge(p, it, rd);
 }
 
 // ----------------------------------------------------------------------------
@@ -392,7 +344,18 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void DecodeGeneric(DecodeParam
       }
     }
   }
-  if (it.nsplit > 1) ArriveAndMaybeMerge(p, it, rd);
+}
+
+// One wavefront per (row, kv head) group with more than one split.
+__global__ __launch_bounds__(kWavesPerBlock * 64) void MergeSplitsKernel(DecodeParams p) {
+  const int64_t grp = int64_t{blockIdx.x} * kWavesPerBlock + (threadIdx.x >> 6);
+  if (grp >= int64_t{p.n_rows} * p.kv_heads) return;
+  const int row = static_cast<int>(grp / p.kv_heads);
+  const int hk = static_cast<int>(grp - int64_t{row} * p.kv_heads);
+  const RowDesc rd = p.rows[row];
+  const int nsplit = (rd.length + rd.split_len - 1) / rd.split_len;
+  if (nsplit == 1) return;
+  MergeSplits(p, row, hk, PartialIndex(rd, p.kv_heads, hk, nsplit, 0), nsplit);
 }
 
 template <class KV>
@@ -429,10 +392,27 @@ hipError_t LaunchTyped(const DecodeParams& p, hipStream_t stream) {
 
 }  // namespace
 
+namespace {
+hipError_t LaunchSplits(const DecodeParams& p, int kv_dtype, hipStream_t stream) {
+  if (kv_dtype != EHIP_KV_BF16) return LaunchTyped<float>(p, stream);
+  // EHIP_DECODE_KERNEL=valu selects the all-VALU kernel for bf16 as well.
+  const char* pick = std::getenv("EHIP_DECODE_KERNEL");
+  if (!(pick && std::strcmp(pick, "valu") == 0)) {
+    hipError_t err = hipSuccess;
+    if (LaunchDecodeMfma(p, stream, &err)) return err;
+  }
+  return LaunchTyped<uint16_t>(p, stream);
+}
+}  // namespace
+
 hipError_t LaunchDecode(const DecodeParams& p, int kv_dtype, hipStream_t stream) {
   if (p.n_items == 0) return hipSuccess;
-  return kv_dtype == EHIP_KV_BF16 ? LaunchTyped<uint16_t>(p, stream)
-                                  : LaunchTyped<float>(p, stream);
+  hipError_t e = LaunchSplits(p, kv_dtype, stream);
+  if (e != hipSuccess || !p.need_merge) return e;
+  const int64_t groups = int64_t{p.n_rows} * p.kv_heads;
+  hipLaunchKernelGGL(MergeSplitsKernel, dim3((groups + kWavesPerBlock - 1) / kWavesPerBlock),
+                     dim3(kWavesPerBlock * 64), 0, stream, p);
+  return hipGetLastError();
 }
 
 }  // namespace ehip

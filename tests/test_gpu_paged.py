@@ -295,10 +295,15 @@ def test_batched_decode_heterogeneous_lengths(gctx, orc, bs):
         assert rel_norm(got[b], single) <= FP32_REL
 
 
-def test_batched_decode_bf16_kv(gctx, orc):
-    rng = np.random.default_rng(77)
+@pytest.mark.parametrize("kernel", ["mfma", "valu"])
+@pytest.mark.parametrize("bs", [16, 64, 8])
+def test_batched_decode_bf16_kv(gctx, orc, kernel, bs, monkeypatch):
+    # Both bf16 kernels (QK^T on MFMA, or all-VALU); bs = 8 always takes the
+    # VALU kernel.
+    monkeypatch.setenv("EHIP_DECODE_KERNEL", kernel)
+    rng = np.random.default_rng(77 + bs)
     lengths = list(rng.integers(1, 3000, 24))
-    H, Hkv, d, bs = 32, 8, 128, 16
+    H, Hkv, d = 32, 8, 128
     q, ks, vs, tables = batched_case(orc, rng, lengths, H, Hkv, d, bs)
     ks_b, vs_b = orc.to_bf16_bits(ks), orc.to_bf16_bits(vs)
     out = gctx.alloc(q.nbytes)
@@ -313,6 +318,24 @@ def test_batched_decode_bf16_kv(gctx, orc):
     ref_r = orc.paged_decode_batched(q, orc.bf16_bits_to_f32(ks_b), orc.bf16_bits_to_f32(vs_b),
                                      tables, lengths, H, Hkv, d, bs, scale_for(d))
     check_fp32(got, ref_r)
+
+
+@pytest.mark.parametrize("H,Hkv", [(8, 8), (8, 4), (32, 8), (64, 8), (14, 2)])
+@pytest.mark.parametrize("d", [64, 128])
+def test_bf16_decode_gqa_sweep(gctx, orc, H, Hkv, d):
+    rng = np.random.default_rng(H * 100 + Hkv + d)
+    lengths = [1, 15, 16, 17, 33, 700, 2049]
+    q, ks, vs, tables = batched_case(orc, rng, lengths, H, Hkv, d, 16)
+    ks_b, vs_b = orc.to_bf16_bits(ks), orc.to_bf16_bits(vs)
+    out = gctx.alloc(q.nbytes)
+    assert gctx.paged_decode_batched(gctx.to_device(q), gctx.to_device(ks_b),
+                                     gctx.to_device(vs_b), tables, lengths, H, Hkv, d, 16, 0,
+                                     ks.shape[0], scale_for(d), out, bf16=True) == 0
+    gctx.sync()
+    got = out.download(np.float32, q.shape)
+    ref = orc.paged_decode_batched(q, orc.bf16_bits_to_f32(ks_b), orc.bf16_bits_to_f32(vs_b),
+                                   tables, lengths, H, Hkv, d, 16, scale_for(d))
+    check_fp32(got, ref)
 
 
 @pytest.mark.parametrize("split", ["64", "128", "512", "1024"])
@@ -415,9 +438,11 @@ def test_step_c3_mixed_prefill_and_decode(gctx, ehip_mod, orc):
     assert max_abs(got, ref32) <= BF16_ABS
 
 
-def test_step_c4_shape_with_shared_prefix_blocks(gctx, ehip_mod, orc):
+@pytest.mark.parametrize("kernel", ["mfma", "valu"])
+def test_step_c4_shape_with_shared_prefix_blocks(gctx, ehip_mod, orc, kernel, monkeypatch):
     """C4 construction (log-uniform lengths, pair-shared prefix blocks, bf16)
     at 24 sequences."""
+    monkeypatch.setenv("EHIP_DECODE_KERNEL", kernel)
     from ehip import workloads
     w = workloads.c4(num_seqs=24, share_frac=0.3)
     assert (w.refcount == 2).any()
