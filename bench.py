@@ -48,6 +48,9 @@ def parse():
     ap.add_argument("--layers", type=int, default=0, help="override the config's layer count")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="run one device-to-device copy of this size first (a known-size "
+                         "dispatch that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     return ap.parse_args()
 
 
@@ -123,6 +126,14 @@ def main():
         f"pool={w.pool_blocks} blocks, {layers} layers, slabs {2 * layers * slab_bytes / 2**30:.1f} GiB")
 
     ctx = ehip.Context(0)
+    if args.copy_probe_mib:
+        nbytes = args.copy_probe_mib << 20
+        a, b = ctx.alloc(nbytes), ctx.alloc(nbytes)
+        ctx._check(ehip.lib().ehip_copy_device(ctx.h, b.ptr, a.ptr, nbytes))
+        ctx.sync()
+        a.free()
+        b.free()
+        log(f"[bench] copy probe: {nbytes} bytes device-to-device")
     slabs, qs, kns, vns, outs = [], [], [], [], []
     for layer in range(layers):
         ks, vs = ctx.alloc(slab_bytes), ctx.alloc(slab_bytes)

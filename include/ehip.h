@@ -198,9 +198,13 @@ int ehip_step_info(const ehip_ctx* ctx, int64_t* rows, int64_t* items, int64_t* 
 
 /* ------------------------------------------------ host-only planning ------
  * The work-list builder behind ehip_step_upload, callable without a GPU (for
- * tests of the host logic). Fills the counts the plan would have. */
+ * tests of the host logic). Fills the counts the plan would have: query rows,
+ * work items (of which joint_items serve two rows sharing leading blocks),
+ * split partial slots, the base split length and the keys read jointly
+ * (summed over row pairs). Any out pointer may be NULL. */
 int ehip_plan_counts(const ehip_geometry* geom, const ehip_step_desc* step, int64_t* rows,
-                     int64_t* items, int64_t* partials, int32_t* split_tokens);
+                     int64_t* items, int64_t* partials, int32_t* split_tokens,
+                     int64_t* joint_items, int64_t* shared_tokens);
 
 #ifdef __cplusplus
 }

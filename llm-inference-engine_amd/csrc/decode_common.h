@@ -1,5 +1,5 @@
-// Split-KV bookkeeping shared by the decode kernels: partial-slot indexing and
-// the log-sum-exp merge of a (row, kv head) group's split partials.
+// Shared by the decode kernels: work-item decoding, the range's table slice,
+// partial-slot indexing and the sequential split merge.
 #pragma once
 
 #include "device_util.h"
@@ -8,15 +8,59 @@
 namespace ehip {
 
 __device__ __forceinline__ int64_t PartialIndex(const RowDesc& rd, int kv_heads, int hk,
-                                                int nsplit, int split) {
-  return int64_t{rd.split_base} * kv_heads + int64_t{hk} * nsplit + split;
+                                                int split) {
+  return int64_t{rd.split_base} * kv_heads + int64_t{hk} * rd.nsplit + split;
 }
 
-// Log-sum-exp merge of one (row, kv head) group's split partials by one
-// wavefront: M = max_s m_s, L = sum_s l_s 2^(m_s - M),
-// out = (sum_s o_s 2^(m_s - M)) / L. Splits are combined in split order, so
-// the result is deterministic.
-__device__ inline void MergeSplits(const DecodeParams& p, int row, int hk, int64_t pbase, int nsplit) {
+// Table entries of logical blocks lb0 .. lb0+63 of a key range (lb0 =
+// tb / bs), one per lane: -1 past the range, -2 for an id outside the slab
+// (ReportRejectedBlocks flags those at the end of the item). The load is
+// unconditional and branch-free (lanes past the range re-read its last
+// entry) so it issues together with the item's other loads.
+__device__ __forceinline__ int LoadRangeTable(const DecodeParams& p, int table_off, int tb,
+                                              int te, int lane) {
+  const int lb0 = tb / p.bs;
+  const int nblk = (te - 1) / p.bs - lb0 + 1;  // <= 64: ranges are <= 64 * bs keys
+  const int raw = p.table[table_off + lb0 + min(lane, nblk - 1)];
+  const bool bad = raw < 0 || raw >= p.slab_blocks;
+  return lane < nblk ? (bad ? -2 : raw) : -1;
+}
+
+__device__ __forceinline__ void ReportRejectedBlocks(const DecodeParams& p, int tab) {
+  if (__any(tab == -2) && (threadIdx.x & 63) == 0) atomicOr(p.err, kErrBlockRange);
+}
+
+// A work item decoded: its rows (one, or both of a joint pair), kv head, key
+// range and split slot.
+struct ItemRef {
+  int rows[kMaxJointRows];
+  int nrows;
+  int hk;
+  int split;
+  int tb;
+  int te;
+  int table_off;
+};
+
+__device__ __forceinline__ ItemRef DecodeItem(const WorkItem& it) {
+  ItemRef r;
+  r.rows[0] = it.row0;
+  r.rows[1] = it.row1 >= 0 ? it.row1 : it.row0;
+  r.nrows = it.row1 >= 0 ? 2 : 1;
+  r.hk = it.hk_split & ((1 << kHkBits) - 1);
+  r.split = it.hk_split >> kHkBits;
+  r.tb = it.tok_begin;
+  r.te = it.tok_end;
+  r.table_off = it.table_off;
+  return r;
+}
+
+// Sequential log-sum-exp merge of one (row, kv head) group's split partials
+// by one wavefront (the fallback for groups too long for the parallel merge):
+// M = max_s m_s, L = sum_s l_s 2^(m_s - M), out = (sum_s o_s 2^(m_s - M)) / L.
+// Splits are combined in split order, so the result is deterministic.
+__device__ inline void MergeSplits(const DecodeParams& p, int row, int hk, int64_t pbase,
+                                   int nsplit) {
   const int lane = threadIdx.x & 63;
   const int g = p.group, d = p.d;
   float* out = p.out + (int64_t{row} * p.heads + int64_t{hk} * g) * d;

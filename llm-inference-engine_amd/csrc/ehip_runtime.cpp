@@ -104,7 +104,8 @@ int UploadPlan(ehip_ctx* ctx, const ehip_geometry& g, Plan&& plan, const int32_t
   const size_t items_b = Align256(plan.items.size() * sizeof(ehip::WorkItem));
   const size_t table_b = Align256(plan.table_ids.size() * sizeof(int32_t));
   const size_t slots_b = Align256(plan.slots.size() * sizeof(int64_t));
-  const size_t total = std::max<size_t>(256, rows_b + items_b + table_b + slots_b);
+  const size_t total =
+      std::max<size_t>(256, rows_b + items_b + table_b + slots_b);
 
   const int cur = ctx->stage_cur;
   ctx->stage_cur ^= 1;
@@ -130,7 +131,8 @@ int UploadPlan(ehip_ctx* ctx, const ehip_geometry& g, Plan&& plan, const int32_t
   char* h = static_cast<char*>(ctx->h_stage[cur]);
   std::memcpy(h, plan.rows.data(), plan.rows.size() * sizeof(ehip::RowDesc));
   std::memcpy(h + rows_b, plan.items.data(), plan.items.size() * sizeof(ehip::WorkItem));
-  std::memcpy(h + rows_b + items_b, plan.table_ids.data(), plan.table_ids.size() * sizeof(int32_t));
+  std::memcpy(h + rows_b + items_b, plan.table_ids.data(),
+              plan.table_ids.size() * sizeof(int32_t));
   std::memcpy(h + rows_b + items_b + table_b, plan.slots.data(),
               plan.slots.size() * sizeof(int64_t));
   EHIP_HIP(ctx, hipMemcpyAsync(ctx->d_desc, h, total, hipMemcpyHostToDevice, ctx->stream));
@@ -141,8 +143,9 @@ int UploadPlan(ehip_ctx* ctx, const ehip_geometry& g, Plan&& plan, const int32_t
   char* d = static_cast<char*>(ctx->d_desc);
   ctx->d_rows = reinterpret_cast<const ehip::RowDesc*>(d);
   ctx->d_items = reinterpret_cast<const ehip::WorkItem*>(d + rows_b);
-  ctx->d_table = d_user_table ? d_user_table
-                              : reinterpret_cast<const int32_t*>(d + rows_b + items_b);
+  ctx->d_table = d_user_table
+                     ? d_user_table
+                     : reinterpret_cast<const int32_t*>(d + rows_b + items_b);
   ctx->d_slots = reinterpret_cast<const int64_t*>(d + rows_b + items_b + table_b);
   if (int rc = EnsureWorkspace(ctx, g, plan)) return rc;
   ctx->geom = g;
@@ -175,6 +178,7 @@ int LaunchAttention(ehip_ctx* ctx, const float* q, const void* k_slab, const voi
   p.n_items = static_cast<int32_t>(plan.items.size());
   p.n_rows = static_cast<int32_t>(plan.rows.size());
   p.need_merge = plan.partials != static_cast<int64_t>(plan.rows.size()) * g.kv_heads;
+  p.n_joint = static_cast<int32_t>(plan.joint_items);
   p.heads = g.heads;
   p.kv_heads = g.kv_heads;
   p.group = static_cast<int32_t>(grp);
@@ -558,7 +562,8 @@ int ehip_step_info(const ehip_ctx* ctx, int64_t* rows, int64_t* items, int64_t* 
 }
 
 int ehip_plan_counts(const ehip_geometry* geom, const ehip_step_desc* step, int64_t* rows,
-                     int64_t* items, int64_t* partials, int32_t* split_tokens) {
+                     int64_t* items, int64_t* partials, int32_t* split_tokens,
+                     int64_t* joint_items, int64_t* shared_tokens) {
   if (!geom || !step) return EHIP_INVALID_ARGUMENT;
   Plan plan;
   std::string err;
@@ -567,6 +572,8 @@ int ehip_plan_counts(const ehip_geometry* geom, const ehip_step_desc* step, int6
   if (items) *items = static_cast<int64_t>(plan.items.size());
   if (partials) *partials = plan.partials;
   if (split_tokens) *split_tokens = plan.split_tokens;
+  if (joint_items) *joint_items = plan.joint_items;
+  if (shared_tokens) *shared_tokens = plan.shared_tokens;
   return EHIP_OK;
 }
 

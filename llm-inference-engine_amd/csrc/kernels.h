@@ -32,6 +32,7 @@ struct DecodeParams {
   int32_t n_items;
   int32_t n_rows;
   int32_t need_merge;       // some row has more than one split
+  int32_t n_joint;          // joint work items in the plan
   int32_t heads;
   int32_t kv_heads;
   int32_t group;            // g = H / Hkv

@@ -1,4 +1,4 @@
-// Ragged paged decode attention for gfx950 (VALU path).
+// Ragged paged decode attention for gfx950 (VALU path), and the split merge.
 //
 // Semantics: kernels::PagedDecodeAttention{,Batched}F32
 // (src/kernels/paged_attention.h:50-57, :105-110): for a query row attending
@@ -6,18 +6,20 @@
 // the block table, query head h reading kv head h / g. The reference runs the
 // online recurrence of src/kernels/internal/paged_attention_common.h:69-136
 // per (sequence, kv head); here one wavefront handles one (row, kv head, key
-// split) work item and the splits are merged by log-sum-exp rescaling.
+// range) work item and the ranges are merged by log-sum-exp rescaling.
 //
 // Wavefront layout (specialised kernel): LPT lanes hold one token's head_dim
-// row, each lane E contiguous-by-16-bytes elements, so one 16-byte load per
-// lane per vector and each load instruction reads whole 128/256-byte row
-// segments. TPR = 64/LPT tokens are processed per "row" of the wavefront and
-// 32 tokens per tile. The g query heads of the kv head live in registers
-// (fp32), so every K/V byte is read from HBM once for all g heads.
+// row, each lane E elements in 16-byte vectors, so each load instruction reads
+// whole 128/256-byte row segments. TPR = 64/LPT tokens are processed per
+// "row" of the wavefront and 32 tokens per tile. The g query heads of the kv
+// head live in registers (fp32), so every K/V byte is read from HBM once for
+// all g heads. A joint work item (two rows sharing the range's blocks) is
+// processed one row after the other here; the MFMA kernel serves both rows
+// from one pass.
 //
 // Softmax: scores are formed as dot * scale * log2(e) and exponentiated with
-// the hardware exp2; the running max/sum are per tile (32 keys), the tile's
-// max is a wavefront reduction, so alpha rescaling happens once per tile.
+// the hardware exp2; the running max/sum are per 32-key tile, so alpha
+// rescaling happens once per tile.
 #include <cstdlib>
 #include <cstring>
 
@@ -68,9 +70,10 @@ __device__ __forceinline__ float KvAt(const uint16_t* p, int64_t i) {
 }
 
 // ----------------------------------------------------------------------------
-// Specialised kernel: KV in {f32, bf16}, D in {64, 128}, G = g exactly.
+// Specialised kernel body: KV in {f32, bf16}, D in {64, 128}, G = g exactly.
 template <class KV, int D, int G>
-__global__ __launch_bounds__(kWavesPerBlock * 64) void DecodeValu(DecodeParams p) {
+__device__ __forceinline__ void DecodeValuRow(const DecodeParams& p, int row, int hk, int tb,
+                                              int te, int split, int table_off) {
   constexpr int EPV = KvT<KV>::EPV;
   constexpr int LPT = (G * D / 8 > 64) ? 16 : 8;  // lanes per token row
   constexpr int E = D / LPT;                      // elements per lane
@@ -81,18 +84,14 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void DecodeValu(DecodeParams p
   static_assert(NV >= 1 && NV * EPV == E && E * LPT == D, "layout");
 
   const int lane = threadIdx.x & 63;
-  const int item_idx = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
-  if (item_idx >= p.n_items) return;
-  const WorkItem it = p.items[item_idx];
-  const RowDesc rd = p.rows[it.row];
+  const RowDesc rd = p.rows[row];
   const int tl = lane / LPT;
   const int sub = lane % LPT;
-  const int hk = it.kv_head;
   const int bs = p.bs;
 
   float q[G][E];
   {
-    const float* qp = p.q + (int64_t{it.row} * p.heads + int64_t{hk} * G) * D + sub * EPV;
+    const float* qp = p.q + (int64_t{row} * p.heads + int64_t{hk} * G) * D + sub * EPV;
 #pragma unroll
     for (int h = 0; h < G; ++h)
 #pragma unroll
@@ -107,19 +106,8 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void DecodeValu(DecodeParams p
         }
   }
 
-  const int tb = it.split * rd.split_len;
-  const int te = min(rd.length, tb + rd.split_len);
   const int lb0 = tb / bs;
-  const int nblk = (te - 1) / bs - lb0 + 1;  // <= 64 (split_len <= 64 * bs)
-  int tab = -1;
-  if (lane < nblk) {
-    tab = p.table[rd.table_off + lb0 + lane];
-    if (tab < 0 || tab >= p.slab_blocks) {
-      atomicOr(p.err, kErrBlockRange);
-      tab = -1;
-    }
-  }
-
+  const int tab = LoadRangeTable(p, table_off, tb, te, lane);
   const KV* kbase = static_cast<const KV*>(p.k_slab) + int64_t{hk} * bs * D + sub * EPV;
   const KV* vbase = static_cast<const KV*>(p.v_slab) + int64_t{hk} * bs * D + sub * EPV;
 
@@ -177,8 +165,8 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void DecodeValu(DecodeParams p
       for (int r = 1; r < ROWS; ++r) mx = fmaxf(mx, s[r][h]);
       mx = MaxAcross<LPT>(mx);
       const float mn = fmaxf(m[h], mx);
-      // A tile whose every key sits in an out-of-range block leaves mn at
-      // -inf; keep alpha finite (and the state untouched) in that case.
+      // A tile whose every key sits in a rejected block leaves mn at -inf;
+      // keep alpha finite (and the state untouched) in that case.
       const float alpha = mn == -INFINITY ? 1.f : Exp2(m[h] - mn);
       m[h] = mn;
       float psum = 0.f;
@@ -208,6 +196,7 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void DecodeValu(DecodeParams p
     }
   }
 
+  ReportRejectedBlocks(p, tab);
 #pragma unroll
   for (int h = 0; h < G; ++h) {
     l[h] = SumAcross<LPT>(l[h]);
@@ -215,9 +204,9 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void DecodeValu(DecodeParams p
     for (int e = 0; e < E; ++e) o[h][e] = SumAcross<LPT>(o[h][e]);
   }
 
-  if (it.nsplit == 1) {
+  if (rd.nsplit == 1) {
     if (tl == 0) {
-      float* op = p.out + (int64_t{it.row} * p.heads + int64_t{hk} * G) * D + sub * EPV;
+      float* op = p.out + (int64_t{row} * p.heads + int64_t{hk} * G) * D + sub * EPV;
 #pragma unroll
       for (int h = 0; h < G; ++h) {
         const float inv = 1.0f / l[h];
@@ -237,7 +226,7 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void DecodeValu(DecodeParams p
     return;
   }
 
-  const int64_t pidx = PartialIndex(rd, p.kv_heads, hk, it.nsplit, it.split);
+  const int64_t pidx = PartialIndex(rd, p.kv_heads, hk, split);
   if (tl == 0) {
     float* po = p.part_o + pidx * G * D + sub * EPV;
 #pragma unroll
@@ -263,26 +252,30 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void DecodeValu(DecodeParams p
   }
 }
 
+template <class KV, int D, int G>
+__global__ __launch_bounds__(kWavesPerBlock * 64) void DecodeValu(DecodeParams p) {
+  const int item_idx = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  if (item_idx >= p.n_items) return;
+  const ItemRef it = DecodeItem(p.items[item_idx]);
+  for (int r = 0; r < it.nrows; ++r)
+    DecodeValuRow<KV, D, G>(p, it.rows[r], it.hk, it.tb, it.te, it.split, it.table_off);
+}
+
 // ----------------------------------------------------------------------------
 // Generic kernel: any d <= 256, any g (heads processed in chunks of 8, one
-// pass over the split's keys per chunk). Lanes own head_dim elements
+// pass over the range's keys per chunk). Lanes own head_dim elements
 // e = lane + 64k; every key is one wavefront-wide dot product. Used for the
 // shapes the specialised kernels do not cover.
 template <class KV>
-__global__ __launch_bounds__(kWavesPerBlock * 64) void DecodeGeneric(DecodeParams p) {
+__device__ void DecodeGenericRow(const DecodeParams& p, int row, int hk, int tb, int te,
+                                 int split) {
   constexpr int HC = 8;
   const int lane = threadIdx.x & 63;
-  const int item_idx = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
-  if (item_idx >= p.n_items) return;
-  const WorkItem it = p.items[item_idx];
-  const RowDesc rd = p.rows[it.row];
-  const int hk = it.kv_head;
+  const RowDesc rd = p.rows[row];
   const int g = p.group, d = p.d, bs = p.bs;
-  const int tb = it.split * rd.split_len;
-  const int te = min(rd.length, tb + rd.split_len);
   const KV* kslab = static_cast<const KV*>(p.k_slab) + int64_t{hk} * bs * d;
   const KV* vslab = static_cast<const KV*>(p.v_slab) + int64_t{hk} * bs * d;
-  const int64_t pidx = PartialIndex(rd, p.kv_heads, hk, it.nsplit, it.split);
+  const int64_t pidx = PartialIndex(rd, p.kv_heads, hk, split);
 
   for (int h0 = 0; h0 < g; h0 += HC) {
     const int hc = min(HC, g - h0);
@@ -293,7 +286,7 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void DecodeGeneric(DecodeParam
       for (int k = 0; k < 4; ++k) {
         const int e = lane + 64 * k;
         q[h][k] = (h < hc && e < d)
-                      ? p.q[(int64_t{it.row} * p.heads + int64_t{hk} * g + h0 + h) * d + e]
+                      ? p.q[(int64_t{row} * p.heads + int64_t{hk} * g + h0 + h) * d + e]
                       : 0.f;
         o[h][k] = 0.f;
       }
@@ -325,12 +318,12 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void DecodeGeneric(DecodeParam
       }
     }
     for (int h = 0; h < hc; ++h) {
-      if (it.nsplit == 1) {
+      if (rd.nsplit == 1) {
         const float inv = 1.0f / l[h];
         for (int k = 0; k < 4; ++k) {
           const int e = lane + 64 * k;
           if (e < d)
-            p.out[(int64_t{it.row} * p.heads + int64_t{hk} * g + h0 + h) * d + e] = o[h][k] * inv;
+            p.out[(int64_t{row} * p.heads + int64_t{hk} * g + h0 + h) * d + e] = o[h][k] * inv;
         }
       } else {
         for (int k = 0; k < 4; ++k) {
@@ -346,16 +339,74 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void DecodeGeneric(DecodeParam
   }
 }
 
-// One wavefront per (row, kv head) group with more than one split.
-__global__ __launch_bounds__(kWavesPerBlock * 64) void MergeSplitsKernel(DecodeParams p) {
-  const int64_t grp = int64_t{blockIdx.x} * kWavesPerBlock + (threadIdx.x >> 6);
-  if (grp >= int64_t{p.n_rows} * p.kv_heads) return;
+template <class KV>
+__global__ __launch_bounds__(kWavesPerBlock * 64) void DecodeGeneric(DecodeParams p) {
+  const int item_idx = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  if (item_idx >= p.n_items) return;
+  const ItemRef it = DecodeItem(p.items[item_idx]);
+  for (int r = 0; r < it.nrows; ++r)
+    DecodeGenericRow<KV>(p, it.rows[r], it.hk, it.tb, it.te, it.split);
+}
+
+// ----------------------------------------------------------------------------
+// Split merge. A (row, kv head) group with more than one split is merged by
+// ceil(g*d / 256) workgroups of 256 threads, one output element per thread:
+// the group's (max, sum) pairs are read into LDS in one parallel sweep, the g
+// per-head weights 2^(m_s - M) / L are formed there, and each thread then sums
+// its element's split partials with independent loads, so a group costs a few
+// memory round trips whatever its split count.
+constexpr int kMergeThreads = 256;
+constexpr int kMergeMaxPairs = 2048;  // nsplit * g held in LDS (16 KiB)
+
+__global__ __launch_bounds__(kMergeThreads) void MergeSplitsKernel(DecodeParams p, int chunks) {
+  __shared__ float2 ml[kMergeMaxPairs];
+  const int64_t grp = blockIdx.x / chunks;
+  const int chunk = static_cast<int>(blockIdx.x - grp * chunks);
   const int row = static_cast<int>(grp / p.kv_heads);
   const int hk = static_cast<int>(grp - int64_t{row} * p.kv_heads);
   const RowDesc rd = p.rows[row];
-  const int nsplit = (rd.length + rd.split_len - 1) / rd.split_len;
+  const int nsplit = rd.nsplit;
   if (nsplit == 1) return;
-  MergeSplits(p, row, hk, PartialIndex(rd, p.kv_heads, hk, nsplit, 0), nsplit);
+  const int64_t pbase = PartialIndex(rd, p.kv_heads, hk, 0);
+  const int g = p.group, d = p.d;
+  const int npairs = nsplit * g;
+  const int tid = threadIdx.x;
+  if (npairs > kMergeMaxPairs) {  // very long rows: one wavefront, sequential merge
+    if (chunk == 0 && tid < 64) MergeSplits(p, row, hk, pbase, nsplit);
+    return;
+  }
+  const int gd = g * d;
+  const int j = chunk * kMergeThreads + tid;
+  const bool has = j < gd;
+  const int h = has ? j / d : 0;
+  const float* po = p.part_o + pbase * gd + (has ? j : 0);
+  // The partial outputs do not depend on the weights: the first kMergeBatch
+  // of them are loaded together with the (max, sum) pairs.
+  constexpr int kMergeBatch = 16;
+  float ov[kMergeBatch];
+#pragma unroll
+  for (int s = 0; s < kMergeBatch; ++s) ov[s] = s < nsplit ? po[int64_t{s} * gd] : 0.f;
+  const float2* src = reinterpret_cast<const float2*>(p.part_ml) + pbase * g;
+  for (int i = tid; i < npairs; i += kMergeThreads) ml[i] = src[i];
+  __syncthreads();
+  if (tid < g) {
+    float M = -INFINITY;
+    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, ml[s * g + tid].x);
+    float L = 0.f;
+    for (int s = 0; s < nsplit; ++s) L += ml[s * g + tid].y * Exp2(ml[s * g + tid].x - M);
+    const float inv = 1.0f / L;
+    for (int s = 0; s < nsplit; ++s) ml[s * g + tid].x = Exp2(ml[s * g + tid].x - M) * inv;
+  }
+  __syncthreads();
+  if (!has) return;
+  float acc = 0.f;
+#pragma unroll
+  for (int s = 0; s < kMergeBatch; ++s)
+    if (s < nsplit) acc = fmaf(ml[s * g + h].x, ov[s], acc);
+#pragma unroll 8
+  for (int s = kMergeBatch; s < nsplit; ++s)
+    acc = fmaf(ml[s * g + h].x, po[int64_t{s} * gd], acc);
+  p.out[(int64_t{row} * p.heads + int64_t{hk} * g) * d + j] = acc;
 }
 
 template <class KV>
@@ -390,9 +441,6 @@ hipError_t LaunchTyped(const DecodeParams& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-}  // namespace
-
-namespace {
 hipError_t LaunchSplits(const DecodeParams& p, int kv_dtype, hipStream_t stream) {
   if (kv_dtype != EHIP_KV_BF16) return LaunchTyped<float>(p, stream);
   // EHIP_DECODE_KERNEL=valu selects the all-VALU kernel for bf16 as well.
@@ -403,6 +451,7 @@ hipError_t LaunchSplits(const DecodeParams& p, int kv_dtype, hipStream_t stream)
   }
   return LaunchTyped<uint16_t>(p, stream);
 }
+
 }  // namespace
 
 hipError_t LaunchDecode(const DecodeParams& p, int kv_dtype, hipStream_t stream) {
@@ -410,8 +459,9 @@ hipError_t LaunchDecode(const DecodeParams& p, int kv_dtype, hipStream_t stream)
   hipError_t e = LaunchSplits(p, kv_dtype, stream);
   if (e != hipSuccess || !p.need_merge) return e;
   const int64_t groups = int64_t{p.n_rows} * p.kv_heads;
-  hipLaunchKernelGGL(MergeSplitsKernel, dim3((groups + kWavesPerBlock - 1) / kWavesPerBlock),
-                     dim3(kWavesPerBlock * 64), 0, stream, p);
+  const int chunks = (p.group * p.d + kMergeThreads - 1) / kMergeThreads;
+  hipLaunchKernelGGL(MergeSplitsKernel, dim3(groups * chunks), dim3(kMergeThreads), 0, stream, p,
+                     chunks);
   return hipGetLastError();
 }
 

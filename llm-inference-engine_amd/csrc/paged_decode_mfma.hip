@@ -2,28 +2,31 @@
 // cores, softmax and PV on the vector ALUs in fp32.
 //
 // Same semantics and work partition as the VALU kernel (paged_decode.hip):
-// one wavefront per (row, kv head, key split) work item, splits merged by
+// one wavefront per (row(s), kv head, key range) work item, ranges merged by
 // log-sum-exp. What changes is where the arithmetic runs.
 //
-// QK^T: S[h][t] = sum_e Q[h][e] K[t][e] for the g query heads of the kv head
-// and a 16-token block half, as v_mfma_f32_16x16x32_bf16 with A = Q (M = head,
-// padded to 16) and B = K^T (N = token). The B operand of lane l is K row
-// (l % 16), elements c*32 + (l/16)*8 .. +8 of chunk c: one 16-byte load per
-// lane straight from the slab, no widening. Q is split into bf16 hi + lo
+// QK^T: S[m][t] = sum_e Q[m][e] K[t][e] for the "virtual heads" m of the item
+// (the g query heads of the kv head, for each row of the item: a joint item
+// serves two rows sharing the range's blocks from one pass over K/V) and a
+// 16-token block half, as v_mfma_f32_16x16x32_bf16 with A = Q (M = virtual
+// head, padded to 16) and B = K^T (N = token). The B operand of lane l is K
+// row (l % 16), elements c*32 + (l/16)*8 .. +8 of chunk c: one 16-byte load
+// per lane straight from the slab, no widening. Q is split into bf16 hi + lo
 // parts (q = hi + lo to ~2^-17 relative) and both are multiplied, so the
 // scores carry fp32-class accuracy while K stays in its stored bf16.
 // Accumulator layout: lane l holds S[4*(l/16) + i][l % 16], i = 0..3.
 //
-// Softmax: online per 32-token tile (two MFMA halves): each 16-lane row
-// reduces its heads' tile max with DPP; probabilities go through a small LDS
-// buffer [token][head] to the PV layout.
+// Softmax: online per tile (one or two MFMA halves): each 16-lane row reduces
+// its virtual heads' tile max with DPP; probabilities go through a small LDS
+// buffer [token][virtual head] to the PV layout.
 //
-// PV: lane l owns head_dim elements 8*(l % (d/8)) .. +8 of every other token
-// row (d/8 lanes per row), accumulating o[h][e] in fp32 for all g heads; the
-// token-parallel partial sums are reduced once at the end.
+// PV: lane l owns head_dim elements 8*(l % (d/8)) .. +8 of every (64/(d/8))-th
+// token row, accumulating o[m][e] in fp32; the token-parallel partial sums are
+// reduced once at the end.
 //
-// K/V tiles are double-buffered in registers: the loads of tile k+1 are in
-// flight while tile k is computed.
+// K/V arrive through buffer loads whose descriptor is the (block, head) tile
+// base, double-buffered in registers: the next tile's loads are in flight
+// while the current one is computed.
 #include <cstdlib>
 #include <cstring>
 
@@ -63,70 +66,54 @@ struct Tile {
   int phys[TH];
 };
 
-template <int D, int G, int TH>
+template <int D, int G, int RMAX, int TH>
 __global__ __launch_bounds__(64) void DecodeMfmaBf16(DecodeParams p) {
   using T = Tile<D, TH>;
   constexpr int TT = 16 * TH;        // tokens per tile
+  constexpr int GV = G * RMAX;       // virtual heads (row-major over the item's rows)
   constexpr int NC = T::NC;          // MFMA k-chunks over head_dim
-  constexpr int HR = (G + 3) / 4;    // 16-lane accumulator rows holding real heads
-  constexpr int HP = HR * 4;         // heads padded to whole rows
+  constexpr int HR = (GV + 3) / 4;   // 16-lane accumulator rows holding virtual heads
+  constexpr int HP = HR * 4;         // virtual heads padded to whole rows
   constexpr int PV_LPT = T::PV_LPT;  // PV lanes per token row
   constexpr int PV_TPI = 64 / PV_LPT;
   constexpr int PV_J = T::PV_J;
-  static_assert(G >= 1 && G <= 16 && (D == 64 || D == 128), "shape");
+  static_assert(GV >= 1 && GV <= 16 && (D == 64 || D == 128), "shape");
 
   __shared__ float p_lds[TT * HP];
 
   const int lane = threadIdx.x;
   const int item_idx = blockIdx.x;
   if (item_idx >= p.n_items) return;
-  const WorkItem it = p.items[item_idx];
-  const RowDesc rd = p.rows[it.row];
-  const int hk = it.kv_head;
+  const ItemRef it = DecodeItem(p.items[item_idx]);
+  const int nrows = it.nrows;  // <= RMAX (the host launches RMAX = 2 only for joint plans)
+  const int hk = it.hk;
+  const int tb = it.tb, te = it.te;
   const int bs = p.bs;
-  const int n = lane & 15;   // MFMA column (token of a half) / A row (head)
+  const int n = lane & 15;   // MFMA column (token of a half) / A row (virtual head)
   const int kq = lane >> 4;  // MFMA k-group and accumulator row
   const int pv_e = (lane % PV_LPT) * 8;
   const int pv_t = lane / PV_LPT;
 
-  // Q as MFMA A operands (hi and lo bf16 parts), zero for padding heads.
-  bf16x8_t qa_hi[NC], qa_lo[NC];
+  // Everything the item needs is fetched at once: the range's table slice
+  // (every row of the item reads the same blocks over [tb, te)) and the
+  // queries; the first tile's K/V follow as soon as the table lands.
+  const int vrow = n / G;  // item row of this lane's virtual head
+  const bool live = n < GV && vrow < nrows;
+  float4 qraw[NC][2];
   {
-    const float* qp = p.q + (int64_t{it.row} * p.heads + int64_t{hk} * G) * D;
+    // Every lane loads (padding lanes read a live head) and padding is
+    // zeroed afterwards, so no branch sits around the loads.
+    const int qrow = (live && vrow == 1) ? it.rows[1] : it.rows[0];  // no dynamic indexing
+    const int qh = live ? n % G : 0;
+    const float* qp = p.q + (int64_t{qrow} * p.heads + int64_t{hk} * G + qh) * D + kq * 8;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      uint32_t hi[4], lo[4];
-      // Every lane loads (padding heads read head 0) and padding is zeroed
-      // after, so no branch sits around the loads.
-      const int hq = n < G ? n : 0;
-      const float4 a = *reinterpret_cast<const float4*>(qp + hq * D + c * 32 + kq * 8);
-      const float4 b = *reinterpret_cast<const float4*>(qp + hq * D + c * 32 + kq * 8 + 4);
-      const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-      for (int i = 0; i < 8; i += 2) {
-        const uint32_t h0 = Fp32ToBf16Bits(x[i]), h1 = Fp32ToBf16Bits(x[i + 1]);
-        const uint32_t l0 = Fp32ToBf16Bits(x[i] - __uint_as_float(h0 << 16));
-        const uint32_t l1 = Fp32ToBf16Bits(x[i + 1] - __uint_as_float(h1 << 16));
-        hi[i / 2] = n < G ? (h0 | (h1 << 16)) : 0u;
-        lo[i / 2] = n < G ? (l0 | (l1 << 16)) : 0u;
-      }
-      qa_hi[c] = AsBf16x8(make_uint4(hi[0], hi[1], hi[2], hi[3]));
-      qa_lo[c] = AsBf16x8(make_uint4(lo[0], lo[1], lo[2], lo[3]));
+      qraw[c][0] = *reinterpret_cast<const float4*>(qp + c * 32);
+      qraw[c][1] = *reinterpret_cast<const float4*>(qp + c * 32 + 4);
     }
   }
-
-  const int tb = it.split * rd.split_len;
-  const int te = min(rd.length, tb + rd.split_len);
   const int lb0 = tb / bs;
-  const int nblk = (te - 1) / bs - lb0 + 1;  // <= 64
-  int tab = -1;
-  if (lane < nblk) {
-    tab = p.table[rd.table_off + lb0 + lane];
-    if (tab < 0 || tab >= p.slab_blocks) {
-      atomicOr(p.err, kErrBlockRange);
-      tab = -1;
-    }
-  }
+  const int tab = LoadRangeTable(p, it.table_off, tb, te, lane);
   const uint16_t* kbase = static_cast<const uint16_t*>(p.k_slab) + int64_t{hk} * bs * D;
   const uint16_t* vbase = static_cast<const uint16_t*>(p.v_slab) + int64_t{hk} * bs * D;
   const int bmask = bs - 1;
@@ -135,12 +122,9 @@ __global__ __launch_bounds__(64) void DecodeMfmaBf16(DecodeParams p) {
   const int koff = (n * D + kq * 8) * 2;
   const int voff = (pv_t * D + pv_e) * 2;
 
-  // K/V come in through buffer loads: the (block, head) tile base is a
-  // scalar descriptor and each lane adds its fixed offset, so no 64-bit
-  // address arithmetic sits between the loads and the compiler keeps the
-  // next tile's loads in flight while the current one is computed. A half
-  // beyond the split, or on a rejected block id, gets an empty descriptor:
-  // its loads return zeros without touching memory, and it is masked.
+  // A half beyond the range, or on a rejected block id, gets an empty
+  // descriptor: its loads return zeros without touching memory, and it is
+  // masked in the arithmetic.
   auto load = [&](T& t, int t0) {
 #pragma unroll
     for (int h2 = 0; h2 < TH; ++h2) {
@@ -150,10 +134,10 @@ __global__ __launch_bounds__(64) void DecodeMfmaBf16(DecodeParams p) {
       t.phys[h2] = ok ? phys : -1;
       const int64_t boff = int64_t{ok ? phys : 0} * p.block_stride;
       const uint32_t range = ok ? tile_bytes : 0u;
-      const __amdgpu_buffer_rsrc_t rk =
-          __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kbase + boff), 0, range, 0x00020000);
-      const __amdgpu_buffer_rsrc_t rv =
-          __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vbase + boff), 0, range, 0x00020000);
+      const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint16_t*>(kbase + boff), 0, range, 0x00020000);
+      const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint16_t*>(vbase + boff), 0, range, 0x00020000);
       const int sbase = (th & bmask) * D * 2;
 #pragma unroll
       for (int c = 0; c < NC; ++c)
@@ -166,14 +150,33 @@ __global__ __launch_bounds__(64) void DecodeMfmaBf16(DecodeParams p) {
     }
   };
 
-  float m[4], lsum[4], o[G][8];
+  T bufA, bufB;
+  load(bufA, tb);  // first tile in flight while Q is split
+
+  // Q as MFMA A operands: q = hi + lo, both bf16 (round-to-nearest-even
+  // narrowing, branch-free); padding virtual heads are zero.
+  bf16x8_t qa_hi[NC], qa_lo[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const float x[8] = {qraw[c][0].x, qraw[c][0].y, qraw[c][0].z, qraw[c][0].w,
+                        qraw[c][1].x, qraw[c][1].y, qraw[c][1].z, qraw[c][1].w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float xv = live ? x[i] : 0.f;
+      const __bf16 hb = static_cast<__bf16>(xv);
+      qa_hi[c][i] = hb;
+      qa_lo[c][i] = static_cast<__bf16>(xv - static_cast<float>(hb));
+    }
+  }
+
+  float m[4], lsum[4], o[GV][8];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     m[i] = -INFINITY;
     lsum[i] = 0.f;
   }
 #pragma unroll
-  for (int h = 0; h < G; ++h)
+  for (int h = 0; h < GV; ++h)
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[h][e] = 0.f;
 
@@ -223,7 +226,8 @@ __global__ __launch_bounds__(64) void DecodeMfmaBf16(DecodeParams p) {
     }
     __syncthreads();
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
+    for (int h = 0; h < GV; ++h) {
+      if (h / G >= nrows) break;
       const float a = ReadLane(alpha[h & 3], 16 * (h >> 2));
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[h][e] *= a;
@@ -252,66 +256,90 @@ __global__ __launch_bounds__(64) void DecodeMfmaBf16(DecodeParams p) {
           pv[4 * r4 + 3] = x.w;
         }
 #pragma unroll
-        for (int h = 0; h < G; ++h)
+        for (int rr = 0; rr < RMAX; ++rr) {
+          if (rr >= nrows) break;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) o[h][e] = fmaf(pv[h], vf[e], o[h][e]);
+          for (int h = rr * G; h < (rr + 1) * G; ++h)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[h][e] = fmaf(pv[h], vf[e], o[h][e]);
+        }
       }
     }
     __syncthreads();  // p_lds is rewritten by the next tile
   };
 
-  T bufA, bufB;
-  load(bufA, tb);
-  for (int t0 = tb; t0 < te; t0 += 2 * TT) {
+  // A work item's range is never empty (tb < te), so the loop has no entry
+  // test for the compiler to sink the Q loads behind.
+  for (int t0 = tb;; t0 += 2 * TT) {
     load(bufB, t0 + TT);
     process(bufA, t0);
     if (t0 + TT >= te) break;
     load(bufA, t0 + 2 * TT);
     process(bufB, t0 + TT);
+    if (t0 + 2 * TT >= te) break;
   }
 
-  // Token-parallel partial sums -> per (head, element) totals.
+  ReportRejectedBlocks(p, tab);
+  // Token-parallel partial sums -> per (virtual head, element) totals.
 #pragma unroll
-  for (int h = 0; h < G; ++h)
+  for (int h = 0; h < GV; ++h)
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[h][e] = SumAcross<PV_LPT>(o[h][e]);
   float lrow[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) lrow[i] = SumGroup16(lsum[i]);
 
-  if (it.nsplit == 1) {
+#pragma unroll
+  for (int rr = 0; rr < RMAX; ++rr) {
+    if (rr >= nrows) break;
+    const int row = it.rows[rr];
+    const RowDesc rd = p.rows[row];
+    if (rd.nsplit == 1) {
+      if (lane < PV_LPT) {
+        float* op = p.out + (int64_t{row} * p.heads + int64_t{hk} * G) * D + pv_e;
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+          const int v = rr * G + h;
+          const float inv = 1.0f / ReadLane(lrow[v & 3], 16 * (v >> 2));
+          *reinterpret_cast<float4*>(op + h * D) =
+              make_float4(o[v][0] * inv, o[v][1] * inv, o[v][2] * inv, o[v][3] * inv);
+          *reinterpret_cast<float4*>(op + h * D + 4) =
+              make_float4(o[v][4] * inv, o[v][5] * inv, o[v][6] * inv, o[v][7] * inv);
+        }
+      }
+      continue;
+    }
+    const int64_t pidx = PartialIndex(rd, p.kv_heads, hk, it.split);
     if (lane < PV_LPT) {
-      float* op = p.out + (int64_t{it.row} * p.heads + int64_t{hk} * G) * D + pv_e;
+      float* po = p.part_o + pidx * G * D + pv_e;
 #pragma unroll
       for (int h = 0; h < G; ++h) {
-        const float inv = 1.0f / ReadLane(lrow[h & 3], 16 * (h >> 2));
-        *reinterpret_cast<float4*>(op + h * D) =
-            make_float4(o[h][0] * inv, o[h][1] * inv, o[h][2] * inv, o[h][3] * inv);
-        *reinterpret_cast<float4*>(op + h * D + 4) =
-            make_float4(o[h][4] * inv, o[h][5] * inv, o[h][6] * inv, o[h][7] * inv);
+        const int v = rr * G + h;
+        *reinterpret_cast<float4*>(po + h * D) = make_float4(o[v][0], o[v][1], o[v][2], o[v][3]);
+        *reinterpret_cast<float4*>(po + h * D + 4) =
+            make_float4(o[v][4], o[v][5], o[v][6], o[v][7]);
       }
     }
-    return;
-  }
-  const int64_t pidx = PartialIndex(rd, p.kv_heads, hk, it.nsplit, it.split);
-  if (lane < PV_LPT) {
-    float* po = p.part_o + pidx * G * D + pv_e;
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-      *reinterpret_cast<float4*>(po + h * D) = make_float4(o[h][0], o[h][1], o[h][2], o[h][3]);
-      *reinterpret_cast<float4*>(po + h * D + 4) =
-          make_float4(o[h][4], o[h][5], o[h][6], o[h][7]);
+      const int v = rr * G + h;
+      const float mh = ReadLane(m[v & 3], 16 * (v >> 2));
+      const float lh = ReadLane(lrow[v & 3], 16 * (v >> 2));
+      if (lane == 0) {
+        p.part_ml[(pidx * G + h) * 2 + 0] = mh;
+        p.part_ml[(pidx * G + h) * 2 + 1] = lh;
+      }
     }
   }
-#pragma unroll
-  for (int h = 0; h < G; ++h) {
-    const float mh = ReadLane(m[h & 3], 16 * (h >> 2));
-    const float lh = ReadLane(lrow[h & 3], 16 * (h >> 2));
-    if (lane == 0) {
-      p.part_ml[(pidx * G + h) * 2 + 0] = mh;
-      p.part_ml[(pidx * G + h) * 2 + 1] = lh;
-    }
-  }
+}
+
+template <int D, int G, int RMAX>
+void LaunchShape(const DecodeParams& p, hipStream_t stream, bool wide) {
+  const dim3 grid(p.n_items), block(64);
+  if (wide)
+    hipLaunchKernelGGL((DecodeMfmaBf16<D, G, RMAX, 2>), grid, block, 0, stream, p);
+  else
+    hipLaunchKernelGGL((DecodeMfmaBf16<D, G, RMAX, 1>), grid, block, 0, stream, p);
 }
 
 }  // namespace
@@ -323,18 +351,19 @@ bool LaunchDecodeMfma(const DecodeParams& p, hipStream_t stream, hipError_t* err
                        (reinterpret_cast<uintptr_t>(p.out) % 16 == 0) &&
                        (p.block_stride % 8 == 0);
   if (!aligned || p.bs < 16) return false;
-  const dim3 grid(p.n_items), block(64);
-  // EHIP_DECODE_TILE=32 selects 32-token tiles (two MFMA halves per tile).
+  // 16-token tiles (one MFMA half per tile, double-buffered) by default;
+  // EHIP_DECODE_TILE=32 selects 32-token tiles.
   const char* tile = std::getenv("EHIP_DECODE_TILE");
   const bool wide = tile && std::strcmp(tile, "32") == 0;
-#define EHIP_MFMA_CASE(DD, GG)                                                     \
-  if (p.d == DD && p.group == GG) {                                                \
-    if (wide)                                                                      \
-      hipLaunchKernelGGL((DecodeMfmaBf16<DD, GG, 2>), grid, block, 0, stream, p); \
-    else                                                                           \
-      hipLaunchKernelGGL((DecodeMfmaBf16<DD, GG, 1>), grid, block, 0, stream, p); \
-    *err = hipGetLastError();                                                      \
-    return true;                                                                   \
+  const bool joint = p.n_joint > 0;
+#define EHIP_MFMA_CASE(DD, GG)                          \
+  if (p.d == DD && p.group == GG) {                     \
+    if (joint)                                          \
+      LaunchShape<DD, GG, 2>(p, stream, wide);          \
+    else                                                \
+      LaunchShape<DD, GG, 1>(p, stream, wide);          \
+    *err = hipGetLastError();                           \
+    return true;                                        \
   }
   EHIP_MFMA_CASE(128, 1)
   EHIP_MFMA_CASE(128, 2)

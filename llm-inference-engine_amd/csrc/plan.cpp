@@ -9,7 +9,7 @@ namespace ehip {
 namespace {
 
 constexpr int32_t kTile = 64;             // split lengths are whole 64-key units
-constexpr int64_t kTargetItems = 6144;    // ~6 wavefront work items per SIMD (1024 SIMDs)
+constexpr int64_t kTargetItems = 10240;   // ~10 wavefront work items per SIMD (1024 SIMDs)
 constexpr int32_t kMinSplit = 128;
 constexpr int32_t kMaxSplitsPerRow = 64;  // bounds the merge a single wave performs
 
@@ -76,47 +76,110 @@ int32_t ChooseSplitTokens(const ehip_geometry& g, int64_t unit_tokens) {
 
 namespace {
 
-// Row splitting + load-balanced item order, shared by both plan builders.
-void FinishPlan(const ehip_geometry& g, Plan* plan) {
+constexpr int32_t kMinJointTokens = 128;  // shorter shared runs are not worth a joint pass
+
+// Full leading blocks two rows read from the same physical block ids.
+int32_t SharedFullBlocks(const Plan& plan, const RowDesc& a, const RowDesc& b, int32_t bs) {
+  const int32_t limit = std::min(a.length, b.length) / bs;
+  if (a.table_off == b.table_off) return limit;  // rows of one sequence
+  const int32_t* ta = plan.table_ids.data() + a.table_off;
+  const int32_t* tb = plan.table_ids.data() + b.table_off;
+  int32_t c = 0;
+  while (c < limit && ta[c] == tb[c]) ++c;
+  return c;
+}
+
+// Pairs rows that share leading blocks (greedy over rows ordered by their
+// first block id and table), splits every row into whole-tile key ranges
+// (joint ranges first), assigns partial slots and orders the work longest
+// first.
+void FinishPlan(const ehip_geometry& g, Plan* plan, bool allow_joint) {
+  const int32_t bs = g.block_size;
+  const int32_t max_split = 64 * bs;
+  const size_t n = plan->rows.size();
   int64_t units = 0;
   for (const RowDesc& r : plan->rows) units += int64_t{r.length} * g.kv_heads;
   const int32_t base = ChooseSplitTokens(g, units);
-  const int32_t max_split = 64 * g.block_size;
   plan->split_tokens = base;
-  int64_t split_base = 0;
-  std::vector<WorkItem> full, partial;
-  for (size_t ri = 0; ri < plan->rows.size(); ++ri) {
-    RowDesc& r = plan->rows[ri];
-    int32_t sl = base;
-    if ((r.length + sl - 1) / sl > kMaxSplitsPerRow) {
-      const int64_t want = RoundUp((r.length + kMaxSplitsPerRow - 1) / kMaxSplitsPerRow, kTile);
-      sl = static_cast<int32_t>(std::min<int64_t>(want, max_split));
-    }
-    r.split_len = sl;
-    r.split_base = static_cast<int32_t>(split_base);
-    const int32_t nsplit = (r.length + sl - 1) / sl;
-    split_base += nsplit;
-    for (int32_t hk = 0; hk < g.kv_heads; ++hk) {
-      for (int32_t s = 0; s < nsplit; ++s) {
-        const WorkItem it{static_cast<int32_t>(ri), hk, s, nsplit};
-        const int32_t count = std::min(r.length, (s + 1) * sl) - s * sl;
-        (count == base ? full : partial).push_back(it);
-      }
+  plan->groups.clear();
+  plan->joint_items = 0;
+  plan->shared_tokens = 0;
+
+  std::vector<int32_t> joint_len(n, 0);
+  const char* no_joint = std::getenv("EHIP_NO_JOINT");
+  if (allow_joint && n >= 2 && !(no_joint && no_joint[0] == '1')) {
+    std::vector<int32_t> order(n);
+    for (size_t i = 0; i < n; ++i) order[i] = static_cast<int32_t>(i);
+    auto first_block = [&](int32_t r) { return plan->table_ids[plan->rows[r].table_off]; };
+    std::sort(order.begin(), order.end(), [&](int32_t a, int32_t b) {
+      const int32_t fa = first_block(a), fb = first_block(b);
+      if (fa != fb) return fa < fb;
+      if (plan->rows[a].table_off != plan->rows[b].table_off)
+        return plan->rows[a].table_off < plan->rows[b].table_off;
+      return a < b;
+    });
+    for (size_t i = 0; i + 1 < n; ++i) {
+      const int32_t a = order[i], b = order[i + 1];
+      const int32_t c = SharedFullBlocks(*plan, plan->rows[a], plan->rows[b], bs);
+      if (c * bs < kMinJointTokens) continue;
+      plan->groups.push_back(a);
+      plan->groups.push_back(b);
+      joint_len[a] = joint_len[b] = c * bs;
+      plan->shared_tokens += int64_t{c} * bs;
+      ++i;  // b is taken
     }
   }
-  // Longest work first so the tail of the dispatch is made of short items.
-  std::stable_sort(partial.begin(), partial.end(), [&](const WorkItem& a, const WorkItem& b) {
-    const RowDesc& ra = plan->rows[a.row];
-    const RowDesc& rb = plan->rows[b.row];
-    const int32_t ca = std::min(ra.length, (a.split + 1) * ra.split_len) - a.split * ra.split_len;
-    const int32_t cb = std::min(rb.length, (b.split + 1) * rb.split_len) - b.split * rb.split_len;
-    return ca > cb;
-  });
-  plan->items.clear();
-  plan->items.reserve(full.size() + partial.size());
-  plan->items.insert(plan->items.end(), full.begin(), full.end());
-  plan->items.insert(plan->items.end(), partial.begin(), partial.end());
+
+  // Split length per row (a group's members use the larger of the two).
+  auto row_split = [&](int32_t len) {
+    int32_t sl = base;
+    if ((len + sl - 1) / sl > kMaxSplitsPerRow) {
+      const int64_t want = RoundUp((len + kMaxSplitsPerRow - 1) / kMaxSplitsPerRow, kTile);
+      sl = static_cast<int32_t>(std::min<int64_t>(want, max_split));
+    }
+    return sl;
+  };
+  std::vector<int32_t> split_len(n);
+  for (size_t r = 0; r < n; ++r) split_len[r] = row_split(plan->rows[r].length);
+  for (size_t k = 0; k < plan->groups.size(); k += kMaxJointRows) {
+    const int32_t a = plan->groups[k], b = plan->groups[k + 1];
+    split_len[a] = split_len[b] = std::max(split_len[a], split_len[b]);
+  }
+
+  int64_t split_base = 0;
+  for (size_t r = 0; r < n; ++r) {
+    RowDesc& rd = plan->rows[r];
+    const int32_t sl = split_len[r], P = joint_len[r];
+    rd.nsplit = (P + sl - 1) / sl + (rd.length - P + sl - 1) / sl;
+    rd.split_base = static_cast<int32_t>(split_base);
+    split_base += rd.nsplit;
+  }
   plan->partials = split_base * g.kv_heads;
+
+  plan->items.clear();
+  for (size_t k = 0; k < plan->groups.size(); k += kMaxJointRows) {
+    const int32_t a = plan->groups[k];
+    const int32_t sl = split_len[a], P = joint_len[a];
+    for (int32_t hk = 0; hk < g.kv_heads; ++hk)
+      for (int32_t s = 0, t = 0; t < P; ++s, t += sl)
+        plan->items.push_back(WorkItem{a, plan->groups[k + 1], t, std::min(P, t + sl),
+                                       PackHkSplit(hk, s), plan->rows[a].table_off, 0, 0});
+  }
+  plan->joint_items = static_cast<int64_t>(plan->items.size());
+  for (size_t r = 0; r < n; ++r) {
+    const RowDesc& rd = plan->rows[r];
+    const int32_t sl = split_len[r], P = joint_len[r];
+    const int32_t s0 = (P + sl - 1) / sl;
+    for (int32_t hk = 0; hk < g.kv_heads; ++hk)
+      for (int32_t s = s0, t = P; t < rd.length; ++s, t += sl)
+        plan->items.push_back(WorkItem{static_cast<int32_t>(r), -1, t, std::min(rd.length, t + sl),
+                                       PackHkSplit(hk, s), rd.table_off, 0, 0});
+  }
+  // Longest key range first, so the tail of the dispatch is short items.
+  std::stable_sort(plan->items.begin(), plan->items.end(),
+                   [](const WorkItem& x, const WorkItem& y) {
+                     return x.tok_end - x.tok_begin > y.tok_end - y.tok_begin;
+                   });
 }
 
 }  // namespace
@@ -132,7 +195,7 @@ int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::
   plan->partials = 0;
   const int32_t B = s.num_seqs;
   if (B == 0) {
-    FinishPlan(g, plan);
+    FinishPlan(g, plan, false);
     return EHIP_OK;
   }
   if (!s.h_query_lens || !s.h_context_lens || !s.h_table_offsets || !s.h_table_ids)
@@ -185,7 +248,9 @@ int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::
     }
     plan->slots.assign(s.h_slot_mapping, s.h_slot_mapping + total_rows);
   }
-  FinishPlan(g, plan);
+  if (g.kv_heads >= (1 << kHkBits))
+    return Fail(err, EHIP_UNIMPLEMENTED, "kv_heads=%lld >= 4096", g.kv_heads);
+  FinishPlan(g, plan, true);
   return EHIP_OK;
 }
 
@@ -200,7 +265,7 @@ int BuildSingleRowPlan(const ehip_geometry& g, int64_t length, int64_t num_block
   plan->rows.assign(1, RowDesc{0, static_cast<int32_t>(length), 0, 0});
   plan->table_ids.clear();
   plan->slots.clear();
-  FinishPlan(g, plan);
+  FinishPlan(g, plan, false);
   return EHIP_OK;
 }
 

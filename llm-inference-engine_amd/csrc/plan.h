@@ -10,6 +10,14 @@
 // rule, src/kernels/internal/attention_common.h:229-235), and a long context
 // is cut into splits of whole 64-token tiles whose (max, sum, output)
 // partials are merged with a log-sum-exp rescale.
+//
+// Shared prefixes: blocks are shared only as whole leading blocks of forked
+// sequences (BlockPool::Share, src/kvcache/block_pool.cpp:256-266; shared
+// blocks are immutable, docs/design/paged-kv-cache.md:487-507), and every row
+// of a prefill chunk reads its sequence's table. The planner pairs rows whose
+// tables agree on a run of leading full blocks and emits "joint" work items
+// for that run: one pass over the shared K/V serves both rows, each of which
+// still gets its own split partial.
 #pragma once
 
 #include <cstdint>
@@ -20,33 +28,49 @@
 
 namespace ehip {
 
-// One query row: its sequence's table slice and the number of keys it
-// attends (a decode row attends the whole post-append context; row t of a
-// prefill chunk attends P + t + 1 keys).
+// One query row: its sequence's table slice and the keys it attends (a decode
+// row attends the whole post-append context; row t of a prefill chunk
+// attends P + t + 1 keys). Its splits own partial slots
+// [split_base*Hkv + hk*nsplit, +nsplit) for kv head hk.
 struct RowDesc {
   int32_t table_off;   // first entry of this row's sequence in the CSR ids
   int32_t length;      // keys attended, >= 1
   int32_t split_base;  // prefix sum of nsplit over earlier rows
-  int32_t split_len;   // tokens per split (multiple of 64, <= 64 * bs)
+  int32_t nsplit;      // splits of this row (joint ones first)
 };
 
-// One work item = one wavefront: keys [split*split_len, min(length,
-// (split+1)*split_len)) of row `row`, for all g query heads of kv head
-// `kv_head`.
+// One work item = one wavefront: keys [tok_begin, tok_end) of row0 (and of
+// row1 too for a joint item, row1 = -1 otherwise), for the g query heads of
+// one kv head. `split` is the partial slot index inside each row's range.
+// The range's table slice starts at table_off (both rows read the same
+// blocks), so a kernel can fetch the table, the queries and the row
+// descriptors in parallel as soon as it has the item.
 struct WorkItem {
-  int32_t row;
-  int32_t kv_head;
-  int32_t split;
-  int32_t nsplit;
+  int32_t row0;
+  int32_t row1;
+  int32_t tok_begin;
+  int32_t tok_end;
+  int32_t hk_split;  // kv_head | split << 12
+  int32_t table_off;
+  int32_t reserved0;
+  int32_t reserved1;
 };
+
+constexpr int kMaxJointRows = 2;
+constexpr int kHkBits = 12;
+
+inline int32_t PackHkSplit(int32_t hk, int32_t split) { return hk | (split << kHkBits); }
 
 struct Plan {
   std::vector<RowDesc> rows;
   std::vector<WorkItem> items;
+  std::vector<int32_t> groups;      // [n_groups * kMaxJointRows] member rows (host side)
   std::vector<int32_t> table_ids;   // CSR ids, copied
   std::vector<int64_t> slots;       // slot mapping of appended tokens (may be empty)
   int64_t partials = 0;             // sum over rows of nsplit * Hkv
   int32_t split_tokens = 0;         // base split length chosen for this step
+  int64_t joint_items = 0;
+  int64_t shared_tokens = 0;        // sum over groups of the jointly read prefix
 };
 
 // Geometry validation shared by every entry point. Returns a StatusCode and
@@ -62,12 +86,11 @@ int64_t BlockStride(const ehip_geometry& g);
 int32_t ChooseSplitTokens(const ehip_geometry& g, int64_t unit_tokens);
 
 // Validates the step (lengths, CSR offsets, every table id and slot in range)
-// and builds the plan. `with_tables` copies the CSR ids; `table_ids_valid`
-// false skips the id range check (ids live on the device).
+// and builds the plan.
 int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::string* err);
 
-// Plan for rows that all read one device-resident table (single-sequence
-// paged decode): one row of `length` keys, table offset 0.
+// Plan for one row reading a device-resident table (single-sequence paged
+// decode): one row of `length` keys, table offset 0.
 int BuildSingleRowPlan(const ehip_geometry& g, int64_t length, int64_t num_blocks, Plan* plan,
                        std::string* err);
 

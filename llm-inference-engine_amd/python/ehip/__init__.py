@@ -96,7 +96,7 @@ def lib():
             "ehip_step_attention": [_vp, _vp, _vp, _vp, _vp],
             "ehip_step_info": [_vp, _I64P, _I64P, _I64P],
             "ehip_plan_counts": [C.POINTER(Geometry), C.POINTER(StepDesc), _I64P, _I64P, _I64P,
-                                 C.POINTER(C.c_int32)],
+                                 C.POINTER(C.c_int32), _I64P, _I64P],
         }
         for name, args in sig.items():
             f = getattr(L, name)
@@ -147,13 +147,15 @@ def geometry(heads, kv_heads, head_dim, block_size, kv_dtype, slab_blocks, scale
                     block_stride, scale)
 
 
-def plan_counts(geom: Geometry, step: StepArrays):
-    """Host-only planning (no GPU): (status, rows, items, partials, split_tokens)."""
-    r, i, p = C.c_int64(), C.c_int64(), C.c_int64()
+def plan_counts(geom: Geometry, step: StepArrays, joint: bool = False):
+    """Host-only planning (no GPU): (status, rows, items, partials, split_tokens)
+    and, with joint=True, also (joint_items, shared_tokens)."""
+    r, i, p, j, sh = C.c_int64(), C.c_int64(), C.c_int64(), C.c_int64(), C.c_int64()
     s = C.c_int32()
     rc = lib().ehip_plan_counts(C.byref(geom), C.byref(step.desc), C.byref(r), C.byref(i),
-                                C.byref(p), C.byref(s))
-    return rc, r.value, i.value, p.value, s.value
+                                C.byref(p), C.byref(s), C.byref(j), C.byref(sh))
+    out = (rc, r.value, i.value, p.value, s.value)
+    return out + (j.value, sh.value) if joint else out
 
 
 class DeviceBuffer:

@@ -450,6 +450,32 @@ def test_step_c4_shape_with_shared_prefix_blocks(gctx, ehip_mod, orc, kernel, mo
     check_fp32(got, ref)
 
 
+@pytest.mark.parametrize("joint", ["1", "0"])
+def test_step_shared_prefix_fp32_valu(gctx, ehip_mod, orc, joint, monkeypatch):
+    """Pair-shared prefix blocks through the fp32 VALU kernel, with and without
+    joint work items (joint items are processed row by row there)."""
+    monkeypatch.setenv("EHIP_NO_JOINT", "0" if joint == "1" else "1")
+    from ehip import workloads
+    w = workloads.c4(num_seqs=12, share_frac=0.4)
+    w.kv_dtype = ehip_mod.KV_F32
+    (got, ref, *_), = run_step(gctx, ehip_mod, orc, w, 17)
+    check_fp32(got, ref)
+
+
+def test_step_joint_items_match_plain_partition(gctx, ehip_mod, orc, monkeypatch):
+    """Joint items (one pass over shared blocks for two rows) against the plain
+    per-row partition on the same bf16 step."""
+    from ehip import workloads
+    w = workloads.c4(num_seqs=16, share_frac=0.4)
+    outs = []
+    for flag in ("0", "1"):
+        monkeypatch.setenv("EHIP_NO_JOINT", flag)
+        (got, ref, *_), = run_step(gctx, ehip_mod, orc, w, 21)
+        check_fp32(got, ref)
+        outs.append(got)
+    assert rel_norm(outs[0], outs[1]) <= 1e-5
+
+
 def test_step_requires_upload_and_validates(gctx, ehip_mod):
     g = ehip_mod.geometry(4, 2, 64, 16, 0, 8, 0.125)
     bad = ehip_mod.StepArrays([1], [40], [np.array([0, 1], np.int32)])  # needs 3 blocks

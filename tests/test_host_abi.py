@@ -47,7 +47,8 @@ def expected_items(lens, hkv, split, bs=16):
     return items
 
 
-def test_plan_partitions_c4_shape(ehip_mod):
+def test_plan_partitions_c4_shape(ehip_mod, monkeypatch):
+    monkeypatch.setenv("EHIP_NO_JOINT", "1")  # plain per-row partition
     from ehip import workloads
     w = workloads.c4()
     g = ehip_mod.geometry(w.heads, w.kv_heads, w.head_dim, w.block_size, w.kv_dtype,
@@ -67,13 +68,14 @@ def test_plan_split_override_and_long_rows(ehip_mod, monkeypatch):
     rc, rows, items, partials, split = ehip_mod.plan_counts(
         geom(ehip_mod, slab_blocks=4000), simple_step(ehip_mod, lens))
     assert rc == 0 and split == 128
-    # 32768 keys would need 256 splits of 128: the row's split grows to keep
+    # (distinct tables: no joint items) 32768 keys would need 256 splits of 128: the row's split grows to keep
     # at most 64 splits (512 keys each).
     assert items == 8 * (64 + 1 + 1 + 2)
 
 
 def test_plan_prefill_rows_are_causal(ehip_mod, monkeypatch):
     monkeypatch.setenv("EHIP_SPLIT_TOKENS", "128")
+    monkeypatch.setenv("EHIP_NO_JOINT", "1")
     # One chunk of T=300 on top of P=100 cached tokens: rows attend 101..400 keys.
     st = simple_step(ehip_mod, [400], qlens=np.array([300], np.int32))
     rc, rows, items, partials, split = ehip_mod.plan_counts(geom(ehip_mod), st)
@@ -148,3 +150,77 @@ def test_c4_sharing_and_byte_accounting():
     # never lands in one.
     blocks = w.slot_mapping // w.block_size
     assert (rc[blocks] == 1).all()
+
+
+def joint_expectation(w, split, bs=16, min_joint=128):
+    """Mirror of the planner's pairing for tables that share only as forked
+    prefixes: rows ordered by (first block id, table, index), adjacent rows
+    sharing >= min_joint keys of full leading blocks are paired."""
+    n = len(w.context_lens)
+    first = [int(t[0]) for t in w.tables]
+    order = sorted(range(n), key=lambda r: (first[r], r))
+    joint_len = [0] * n
+    pairs = []
+    i = 0
+    while i + 1 < n:
+        a, b = order[i], order[i + 1]
+        L = min(int(w.context_lens[a]), int(w.context_lens[b])) // bs
+        c = 0
+        while c < L and w.tables[a][c] == w.tables[b][c]:
+            c += 1
+        if c * bs >= min_joint:
+            joint_len[a] = joint_len[b] = c * bs
+            pairs.append((a, b))
+            i += 2
+        else:
+            i += 1
+    return joint_len, pairs
+
+
+def test_plan_joint_items_for_shared_prefixes(ehip_mod):
+    from ehip import workloads
+    w = workloads.c4()
+    g = ehip_mod.geometry(w.heads, w.kv_heads, w.head_dim, w.block_size, w.kv_dtype,
+                          w.pool_blocks, w.scale)
+    st = ehip_mod.StepArrays(w.query_lens, w.context_lens, w.tables, w.slot_mapping)
+    rc, rows, items, partials, split, joint, shared = ehip_mod.plan_counts(g, st, joint=True)
+    assert rc == 0
+    joint_len, pairs = joint_expectation(w, split)
+    assert len(pairs) > 0
+    assert shared == sum(joint_len[a] for a, _ in pairs)
+    # every pair shares exactly the blocks the workload forked (>= 8 blocks)
+    assert shared <= 16 * w.notes["shared_blocks"]
+    exp_joint = sum(math.ceil(joint_len[a] / split) for a, _ in pairs) * w.kv_heads
+    exp_private = sum(math.ceil((int(L) - P) / split) for L, P in zip(w.context_lens, joint_len))
+    assert joint == exp_joint
+    assert items == exp_joint + exp_private * w.kv_heads
+    nsplit = [math.ceil(P / split) + math.ceil((int(L) - P) / split)
+              for L, P in zip(w.context_lens, joint_len)]
+    assert partials == sum(nsplit) * w.kv_heads
+
+
+def test_plan_chunk_rows_pair_up(ehip_mod, monkeypatch):
+    monkeypatch.setenv("EHIP_SPLIT_TOKENS", "128")
+    # A chunk of 300 rows over 100 cached keys: row t attends 101 + t keys;
+    # consecutive rows of one sequence read the same table.
+    st = simple_step(ehip_mod, [400], qlens=np.array([300], np.int32))
+    rc, rows, items, partials, split, joint, shared = ehip_mod.plan_counts(geom(ehip_mod), st,
+                                                                           joint=True)
+    assert rc == 0 and rows == 300
+    lens = [101 + t for t in range(300)]
+    joint_len = [0] * 300
+    exp_joint = exp_shared = 0
+    i = 0
+    while i + 1 < 300:  # the planner's greedy pairing over one table
+        P = (min(lens[i], lens[i + 1]) // 16) * 16
+        if P >= 128:
+            joint_len[i] = joint_len[i + 1] = P
+            exp_shared += P
+            exp_joint += math.ceil(P / 128)
+            i += 2
+        else:
+            i += 1
+    exp_private = sum(math.ceil((L - P) / 128) for L, P in zip(lens, joint_len))
+    assert shared == exp_shared
+    assert joint == 8 * exp_joint
+    assert items == 8 * (exp_joint + exp_private)
