@@ -351,10 +351,10 @@ bool LaunchDecodeMfma(const DecodeParams& p, hipStream_t stream, hipError_t* err
                        (reinterpret_cast<uintptr_t>(p.out) % 16 == 0) &&
                        (p.block_stride % 8 == 0);
   if (!aligned || p.bs < 16) return false;
-  // 16-token tiles (one MFMA half per tile, double-buffered) by default;
-  // EHIP_DECODE_TILE=32 selects 32-token tiles.
+  // 32-token tiles (two MFMA halves per tile, double-buffered) measured best
+  // on C4; EHIP_DECODE_TILE=16 selects one half per tile (fewer registers).
   const char* tile = std::getenv("EHIP_DECODE_TILE");
-  const bool wide = tile && std::strcmp(tile, "32") == 0;
+  const bool wide = !(tile && std::strcmp(tile, "16") == 0);
   const bool joint = p.n_joint > 0;
 #define EHIP_MFMA_CASE(DD, GG)                          \
   if (p.d == DD && p.group == GG) {                     \

@@ -9,7 +9,7 @@ namespace ehip {
 namespace {
 
 constexpr int32_t kTile = 64;             // split lengths are whole 64-key units
-constexpr int64_t kTargetItems = 10240;   // ~10 wavefront work items per SIMD (1024 SIMDs)
+constexpr int64_t kTargetItems = 7680;    // ~7.5 wavefront work items per SIMD (1024 SIMDs)
 constexpr int32_t kMinSplit = 128;
 constexpr int32_t kMaxSplitsPerRow = 64;  // bounds the merge a single wave performs
 
