@@ -41,6 +41,7 @@ struct ehip_ctx {
   ehip::Plan plan;
   const ehip::RowDesc* d_rows = nullptr;
   const ehip::WorkItem* d_items = nullptr;
+  const ehip::PrefillItem* d_prefill = nullptr;
   const int32_t* d_table = nullptr;
   const int64_t* d_slots = nullptr;
 };
@@ -102,10 +103,11 @@ int EnsureWorkspace(ehip_ctx* ctx, const ehip_geometry& g, const Plan& plan) {
 int UploadPlan(ehip_ctx* ctx, const ehip_geometry& g, Plan&& plan, const int32_t* d_user_table) {
   const size_t rows_b = Align256(plan.rows.size() * sizeof(ehip::RowDesc));
   const size_t items_b = Align256(plan.items.size() * sizeof(ehip::WorkItem));
+  const size_t prefill_b = Align256(plan.prefill.size() * sizeof(ehip::PrefillItem));
   const size_t table_b = Align256(plan.table_ids.size() * sizeof(int32_t));
   const size_t slots_b = Align256(plan.slots.size() * sizeof(int64_t));
   const size_t total =
-      std::max<size_t>(256, rows_b + items_b + table_b + slots_b);
+      std::max<size_t>(256, rows_b + items_b + prefill_b + table_b + slots_b);
 
   const int cur = ctx->stage_cur;
   ctx->stage_cur ^= 1;
@@ -131,9 +133,11 @@ int UploadPlan(ehip_ctx* ctx, const ehip_geometry& g, Plan&& plan, const int32_t
   char* h = static_cast<char*>(ctx->h_stage[cur]);
   std::memcpy(h, plan.rows.data(), plan.rows.size() * sizeof(ehip::RowDesc));
   std::memcpy(h + rows_b, plan.items.data(), plan.items.size() * sizeof(ehip::WorkItem));
-  std::memcpy(h + rows_b + items_b, plan.table_ids.data(),
+  std::memcpy(h + rows_b + items_b, plan.prefill.data(),
+              plan.prefill.size() * sizeof(ehip::PrefillItem));
+  std::memcpy(h + rows_b + items_b + prefill_b, plan.table_ids.data(),
               plan.table_ids.size() * sizeof(int32_t));
-  std::memcpy(h + rows_b + items_b + table_b, plan.slots.data(),
+  std::memcpy(h + rows_b + items_b + prefill_b + table_b, plan.slots.data(),
               plan.slots.size() * sizeof(int64_t));
   EHIP_HIP(ctx, hipMemcpyAsync(ctx->d_desc, h, total, hipMemcpyHostToDevice, ctx->stream));
   if (!ctx->stage_done[cur]) EHIP_HIP(ctx, hipEventCreateWithFlags(&ctx->stage_done[cur],
@@ -143,10 +147,11 @@ int UploadPlan(ehip_ctx* ctx, const ehip_geometry& g, Plan&& plan, const int32_t
   char* d = static_cast<char*>(ctx->d_desc);
   ctx->d_rows = reinterpret_cast<const ehip::RowDesc*>(d);
   ctx->d_items = reinterpret_cast<const ehip::WorkItem*>(d + rows_b);
+  ctx->d_prefill = reinterpret_cast<const ehip::PrefillItem*>(d + rows_b + items_b);
   ctx->d_table = d_user_table
                      ? d_user_table
-                     : reinterpret_cast<const int32_t*>(d + rows_b + items_b);
-  ctx->d_slots = reinterpret_cast<const int64_t*>(d + rows_b + items_b + table_b);
+                     : reinterpret_cast<const int32_t*>(d + rows_b + items_b + prefill_b);
+  ctx->d_slots = reinterpret_cast<const int64_t*>(d + rows_b + items_b + prefill_b + table_b);
   if (int rc = EnsureWorkspace(ctx, g, plan)) return rc;
   ctx->geom = g;
   ctx->plan = std::move(plan);
@@ -158,9 +163,39 @@ int LaunchAttention(ehip_ctx* ctx, const float* q, const void* k_slab, const voi
                     float* out) {
   const ehip_geometry& g = ctx->geom;
   const Plan& plan = ctx->plan;
-  if (plan.items.empty()) return EHIP_OK;
-  if (plan.items.size() > static_cast<size_t>(INT32_MAX))
+  if (plan.items.size() > static_cast<size_t>(INT32_MAX) ||
+      plan.prefill.size() > static_cast<size_t>(INT32_MAX))
     return SetError(ctx, EHIP_INVALID_ARGUMENT, "too many work items");
+  if (!plan.prefill.empty()) {
+    const bool aligned = reinterpret_cast<uintptr_t>(q) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(k_slab) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(v_slab) % 16 == 0 &&
+                         ehip::BlockStride(g) % 8 == 0;
+    if (!aligned)
+      return SetError(ctx, EHIP_INVALID_ARGUMENT,
+                      "prefill chunks need 16-byte aligned q and slabs (ehip_malloc gives 256)");
+    ehip::PrefillParams pp{};
+    pp.q = q;
+    pp.k_slab = k_slab;
+    pp.v_slab = v_slab;
+    pp.out = out;
+    pp.items = ctx->d_prefill;
+    pp.table = ctx->d_table;
+    pp.err = ctx->d_err;
+    pp.block_stride = ehip::BlockStride(g);
+    pp.slab_blocks = g.slab_blocks;
+    pp.n_items = static_cast<int32_t>(plan.prefill.size());
+    pp.heads = g.heads;
+    pp.group = g.heads / g.kv_heads;
+    pp.d = g.head_dim;
+    pp.bs = g.block_size;
+    pp.scale_log2 = g.scale * 1.4426950408889634f;
+    hipError_t e = hipSuccess;
+    if (!ehip::LaunchPrefillMfma(pp, ctx->stream, &e))
+      return SetError(ctx, EHIP_INTERNAL, "prefill plan for a shape the kernel does not cover");
+    EHIP_HIP(ctx, e);
+  }
+  if (plan.items.empty()) return EHIP_OK;
   ehip::DecodeParams p{};
   p.q = q;
   p.k_slab = k_slab;
@@ -177,7 +212,7 @@ int LaunchAttention(ehip_ctx* ctx, const float* q, const void* k_slab, const voi
   p.slab_blocks = g.slab_blocks;
   p.n_items = static_cast<int32_t>(plan.items.size());
   p.n_rows = static_cast<int32_t>(plan.rows.size());
-  p.need_merge = plan.partials != static_cast<int64_t>(plan.rows.size()) * g.kv_heads;
+  p.need_merge = plan.any_split;
   p.n_joint = static_cast<int32_t>(plan.joint_items);
   p.heads = g.heads;
   p.kv_heads = g.kv_heads;
@@ -517,7 +552,10 @@ int ehip_step_upload(ehip_ctx* ctx, const ehip_geometry* geom, const ehip_step_d
   if (!geom || !step) return SetError(ctx, EHIP_INVALID_ARGUMENT, "null geometry or step");
   Plan plan;
   std::string err;
-  if (int rc = ehip::BuildPlan(*geom, *step, &plan, &err))
+  const bool prefill_ok = ehip::PrefillSupported(geom->kv_dtype, geom->head_dim,
+                                                 geom->kv_heads > 0 ? geom->heads / geom->kv_heads : 0,
+                                                 geom->block_size);
+  if (int rc = ehip::BuildPlan(*geom, *step, &plan, &err, prefill_ok))
     return SetError(ctx, rc, "%s", err.c_str());
   return UploadPlan(ctx, *geom, std::move(plan), nullptr);
 }
@@ -556,7 +594,7 @@ int ehip_step_attention(ehip_ctx* ctx, const float* d_q, const void* d_k_slab,
 int ehip_step_info(const ehip_ctx* ctx, int64_t* rows, int64_t* items, int64_t* partials) {
   if (!ctx || !ctx->have_step) return EHIP_FAILED_PRECONDITION;
   if (rows) *rows = static_cast<int64_t>(ctx->plan.rows.size());
-  if (items) *items = static_cast<int64_t>(ctx->plan.items.size());
+  if (items) *items = static_cast<int64_t>(ctx->plan.items.size() + ctx->plan.prefill.size());
   if (partials) *partials = ctx->plan.partials;
   return EHIP_OK;
 }

@@ -41,6 +41,30 @@ struct DecodeParams {
   float scale_log2;         // scale * log2(e)
 };
 
+struct PrefillParams {
+  const float* q;           // [rows, H, d]
+  const void* k_slab;       // bf16 slabs
+  const void* v_slab;
+  float* out;               // [rows, H, d]
+  const PrefillItem* items;
+  const int32_t* table;
+  int32_t* err;
+  int64_t block_stride;
+  int64_t slab_blocks;
+  int32_t n_items;
+  int32_t heads;
+  int32_t group;
+  int32_t d;
+  int32_t bs;
+  float scale_log2;
+};
+
+// Causal prefill chunks on MFMA (bf16 K/V, d = 128, g in {4, 8}, bs >= 16):
+// one 4-wavefront workgroup per (chunk, kv head, 16 query rows). Returns
+// false (nothing launched) for shapes it does not cover.
+bool LaunchPrefillMfma(const PrefillParams& p, hipStream_t stream, hipError_t* err);
+bool PrefillSupported(int kv_dtype, int d, int group, int bs);
+
 // Launch the decode kernel family for the given plan (one wavefront per work
 // item; picks the specialised (dtype, d, g) kernel or the generic one), then,
 // if any row was split, the merge of the split partials. The kernel boundary

@@ -366,7 +366,7 @@ __global__ __launch_bounds__(kMergeThreads) void MergeSplitsKernel(DecodeParams 
   const int hk = static_cast<int>(grp - int64_t{row} * p.kv_heads);
   const RowDesc rd = p.rows[row];
   const int nsplit = rd.nsplit;
-  if (nsplit == 1) return;
+  if (nsplit <= 1) return;  // written directly (1) or a prefill-kernel row (0)
   const int64_t pbase = PartialIndex(rd, p.kv_heads, hk, 0);
   const int g = p.group, d = p.d;
   const int npairs = nsplit * g;

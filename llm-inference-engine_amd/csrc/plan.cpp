@@ -93,12 +93,15 @@ int32_t SharedFullBlocks(const Plan& plan, const RowDesc& a, const RowDesc& b, i
 // first block id and table), splits every row into whole-tile key ranges
 // (joint ranges first), assigns partial slots and orders the work longest
 // first.
-void FinishPlan(const ehip_geometry& g, Plan* plan, bool allow_joint) {
+void FinishPlan(const ehip_geometry& g, Plan* plan, bool allow_joint,
+                const std::vector<uint8_t>* skip = nullptr) {
   const int32_t bs = g.block_size;
   const int32_t max_split = 64 * bs;
   const size_t n = plan->rows.size();
+  auto skipped = [&](size_t r) { return skip && (*skip)[r]; };
   int64_t units = 0;
-  for (const RowDesc& r : plan->rows) units += int64_t{r.length} * g.kv_heads;
+  for (size_t r = 0; r < n; ++r)
+    if (!skipped(r)) units += int64_t{plan->rows[r].length} * g.kv_heads;
   const int32_t base = ChooseSplitTokens(g, units);
   plan->split_tokens = base;
   plan->groups.clear();
@@ -108,8 +111,10 @@ void FinishPlan(const ehip_geometry& g, Plan* plan, bool allow_joint) {
   std::vector<int32_t> joint_len(n, 0);
   const char* no_joint = std::getenv("EHIP_NO_JOINT");
   if (allow_joint && n >= 2 && !(no_joint && no_joint[0] == '1')) {
-    std::vector<int32_t> order(n);
-    for (size_t i = 0; i < n; ++i) order[i] = static_cast<int32_t>(i);
+    std::vector<int32_t> order;
+    order.reserve(n);
+    for (size_t i = 0; i < n; ++i)
+      if (!skipped(i)) order.push_back(static_cast<int32_t>(i));
     auto first_block = [&](int32_t r) { return plan->table_ids[plan->rows[r].table_off]; };
     std::sort(order.begin(), order.end(), [&](int32_t a, int32_t b) {
       const int32_t fa = first_block(a), fb = first_block(b);
@@ -118,7 +123,7 @@ void FinishPlan(const ehip_geometry& g, Plan* plan, bool allow_joint) {
         return plan->rows[a].table_off < plan->rows[b].table_off;
       return a < b;
     });
-    for (size_t i = 0; i + 1 < n; ++i) {
+    for (size_t i = 0; i + 1 < order.size(); ++i) {
       const int32_t a = order[i], b = order[i + 1];
       const int32_t c = SharedFullBlocks(*plan, plan->rows[a], plan->rows[b], bs);
       if (c * bs < kMinJointTokens) continue;
@@ -147,12 +152,14 @@ void FinishPlan(const ehip_geometry& g, Plan* plan, bool allow_joint) {
   }
 
   int64_t split_base = 0;
+  plan->any_split = false;
   for (size_t r = 0; r < n; ++r) {
     RowDesc& rd = plan->rows[r];
     const int32_t sl = split_len[r], P = joint_len[r];
-    rd.nsplit = (P + sl - 1) / sl + (rd.length - P + sl - 1) / sl;
+    rd.nsplit = skipped(r) ? 0 : (P + sl - 1) / sl + (rd.length - P + sl - 1) / sl;
     rd.split_base = static_cast<int32_t>(split_base);
     split_base += rd.nsplit;
+    plan->any_split = plan->any_split || rd.nsplit > 1;
   }
   plan->partials = split_base * g.kv_heads;
 
@@ -167,6 +174,7 @@ void FinishPlan(const ehip_geometry& g, Plan* plan, bool allow_joint) {
   }
   plan->joint_items = static_cast<int64_t>(plan->items.size());
   for (size_t r = 0; r < n; ++r) {
+    if (skipped(r)) continue;
     const RowDesc& rd = plan->rows[r];
     const int32_t sl = split_len[r], P = joint_len[r];
     const int32_t s0 = (P + sl - 1) / sl;
@@ -184,12 +192,14 @@ void FinishPlan(const ehip_geometry& g, Plan* plan, bool allow_joint) {
 
 }  // namespace
 
-int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::string* err) {
+int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::string* err,
+              bool prefill_ok) {
   if (int rc = ValidateGeometry(g, err)) return rc;
   if (s.num_seqs < 0) return Fail(err, EHIP_INVALID_ARGUMENT, "num_seqs=%lld < 0", s.num_seqs);
   if (s.reserved != 0) return Fail(err, EHIP_INVALID_ARGUMENT, "reserved field must be 0");
   plan->rows.clear();
   plan->items.clear();
+  plan->prefill.clear();
   plan->table_ids.clear();
   plan->slots.clear();
   plan->partials = 0;
@@ -250,7 +260,35 @@ int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::
   }
   if (g.kv_heads >= (1 << kHkBits))
     return Fail(err, EHIP_UNIMPLEMENTED, "kv_heads=%lld >= 4096", g.kv_heads);
-  FinishPlan(g, plan, true);
+
+  // Chunks big enough for the MFMA prefill kernel leave the decode partition.
+  std::vector<uint8_t> skip(plan->rows.size(), 0);
+  const char* pf = std::getenv("EHIP_PREFILL");
+  if (prefill_ok && !(pf && pf[0] == '0')) {
+    struct Block { int32_t b, q0, keys; };
+    std::vector<Block> blocks;
+    std::vector<int32_t> row_base(B + 1, 0);
+    for (int32_t b = 0; b < B; ++b) row_base[b + 1] = row_base[b] + s.h_query_lens[b];
+    for (int32_t b = 0; b < B; ++b) {
+      const int32_t T = s.h_query_lens[b];
+      if (T < kMinPrefillRows) continue;
+      const int32_t P = static_cast<int32_t>(s.h_context_lens[b] - T);
+      for (int32_t q0 = 0; q0 < T; q0 += 16) blocks.push_back({b, q0, P + std::min(T, q0 + 16)});
+      std::fill(skip.begin() + row_base[b], skip.begin() + row_base[b + 1], 1);
+    }
+    // Most keys first; kv head fastest, so the blocks of one kv head are
+    // dispatched 8 workgroups apart and land on one XCD's L2 together.
+    std::stable_sort(blocks.begin(), blocks.end(),
+                     [](const Block& x, const Block& y) { return x.keys > y.keys; });
+    for (const Block& bl : blocks) {
+      const int32_t T = s.h_query_lens[bl.b];
+      const int32_t P = static_cast<int32_t>(s.h_context_lens[bl.b] - T);
+      for (int32_t hk = 0; hk < g.kv_heads; ++hk)
+        plan->prefill.push_back(PrefillItem{row_base[bl.b], T, P, bl.q0, hk,
+                                            s.h_table_offsets[bl.b], 0, 0});
+    }
+  }
+  FinishPlan(g, plan, true, &skip);
   return EHIP_OK;
 }
 

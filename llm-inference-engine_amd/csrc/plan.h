@@ -56,6 +56,20 @@ struct WorkItem {
   int32_t reserved1;
 };
 
+// One causal prefill block: 16 query rows q0 .. q0+15 of a chunk of `chunk`
+// rows (starting at packed row row_base) over `past` cached keys, for the g
+// query heads of one kv head.
+struct PrefillItem {
+  int32_t row_base;
+  int32_t chunk;
+  int32_t past;
+  int32_t q0;
+  int32_t kv_head;
+  int32_t table_off;
+  int32_t reserved0;
+  int32_t reserved1;
+};
+
 constexpr int kMaxJointRows = 2;
 constexpr int kHkBits = 12;
 
@@ -64,6 +78,7 @@ inline int32_t PackHkSplit(int32_t hk, int32_t split) { return hk | (split << kH
 struct Plan {
   std::vector<RowDesc> rows;
   std::vector<WorkItem> items;
+  std::vector<PrefillItem> prefill;  // chunk rows served by the MFMA prefill kernel
   std::vector<int32_t> groups;      // [n_groups * kMaxJointRows] member rows (host side)
   std::vector<int32_t> table_ids;   // CSR ids, copied
   std::vector<int64_t> slots;       // slot mapping of appended tokens (may be empty)
@@ -71,6 +86,7 @@ struct Plan {
   int32_t split_tokens = 0;         // base split length chosen for this step
   int64_t joint_items = 0;
   int64_t shared_tokens = 0;        // sum over groups of the jointly read prefix
+  bool any_split = false;           // some decode row has more than one split (merge needed)
 };
 
 // Geometry validation shared by every entry point. Returns a StatusCode and
@@ -86,8 +102,12 @@ int64_t BlockStride(const ehip_geometry& g);
 int32_t ChooseSplitTokens(const ehip_geometry& g, int64_t unit_tokens);
 
 // Validates the step (lengths, CSR offsets, every table id and slot in range)
-// and builds the plan.
-int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::string* err);
+// and builds the plan. Chunks of at least kMinPrefillRows rows go to the MFMA
+// prefill kernel when it covers the geometry (prefill_ok; EHIP_PREFILL=0
+// keeps every row on the decode kernels); their rows get nsplit = 0.
+constexpr int32_t kMinPrefillRows = 16;
+int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::string* err,
+              bool prefill_ok = false);
 
 // Plan for one row reading a device-resident table (single-sequence paged
 // decode): one row of `length` keys, table offset 0.

@@ -415,9 +415,38 @@ def test_step_c2_ragged_decode(gctx, ehip_mod, orc):
         check_fp32(got, ref)
 
 
-def test_step_c3_mixed_prefill_and_decode(gctx, ehip_mod, orc):
-    """C3 composition scaled down (2 causal chunks + 12 decodes, bf16 KV): one
-    launch covers chunk rows and decode rows."""
+PREFILL_REL = 1e-2  # MFMA prefill multiplies bf16 Q and bf16 P (fp32 accumulate)
+
+
+def check_step_rows(w, got, ref, ref32):
+    """Decode rows (T == 1) to the fp32 bar against the reference on the same
+    bf16-rounded K/V; prefill-chunk rows (bf16 Q/P on MFMA) to the bf16-KV bar
+    against the fp32 reference (2e-2 absolute) and to 1e-2 relative against
+    the rounded one."""
+    rows = np.repeat(w.query_lens, w.query_lens)
+    dec = rows == 1
+    if dec.any():
+        check_fp32(got[dec], ref[dec])
+    if (~dec).any():
+        assert rel_norm(got[~dec], ref[~dec]) <= PREFILL_REL, rel_norm(got[~dec], ref[~dec])
+    assert max_abs(got, ref32) <= BF16_ABS
+
+
+def fp32_reference(orc, w, kpool, vpool, q, cu):
+    H, Hkv, d, bs = w.heads, w.kv_heads, w.head_dim, w.block_size
+    kseq = [orc.paged_to_contig(kpool, t, int(L), Hkv, d, bs) for t, L in
+            zip(w.tables, w.context_lens)]
+    vseq = [orc.paged_to_contig(vpool, t, int(L), Hkv, d, bs) for t, L in
+            zip(w.tables, w.context_lens)]
+    return orc.prefill_varlen(q, cu, kseq, vseq, H, Hkv, d, w.scale, isa=1)
+
+
+@pytest.mark.parametrize("prefill", ["1", "0"])
+def test_step_c3_mixed_prefill_and_decode(gctx, ehip_mod, orc, prefill, monkeypatch):
+    """C3 composition scaled down (2 causal chunks + 12 decodes, bf16 KV): the
+    chunks run on the MFMA prefill kernel (or, with EHIP_PREFILL=0, on the
+    decode kernels), the decodes on the decode kernel."""
+    monkeypatch.setenv("EHIP_PREFILL", prefill)
     from ehip import workloads
     w = workloads.c3()
     keep = [0, 1] + list(range(4, 16))
@@ -427,15 +456,42 @@ def test_step_c3_mixed_prefill_and_decode(gctx, ehip_mod, orc):
     w.slot_mapping = workloads._append_slots(w.tables, w.query_lens, w.context_lens,
                                              w.block_size)
     (got, ref, kpool, vpool, q, cu), = run_step(gctx, ehip_mod, orc, w, 9)
-    check_fp32(got, ref)   # vs the reference on the same bf16-rounded K/V
-    # and vs fp32 K/V
-    H, Hkv, d, bs = w.heads, w.kv_heads, w.head_dim, w.block_size
-    kseq = [orc.paged_to_contig(kpool, t, int(L), Hkv, d, bs) for t, L in
-            zip(w.tables, w.context_lens)]
-    vseq = [orc.paged_to_contig(vpool, t, int(L), Hkv, d, bs) for t, L in
-            zip(w.tables, w.context_lens)]
-    ref32 = orc.prefill_varlen(q, cu, kseq, vseq, H, Hkv, d, w.scale, isa=1)
-    assert max_abs(got, ref32) <= BF16_ABS
+    ref32 = fp32_reference(orc, w, kpool, vpool, q, cu)
+    if prefill == "0":
+        check_fp32(got, ref)
+        assert max_abs(got, ref32) <= BF16_ABS
+    else:
+        check_step_rows(w, got, ref, ref32)
+
+
+def chunk_workload(H, Hkv, T, P, extra_decodes=1, seed=0, std=0.5):
+    """One causal chunk of T rows over P cached keys plus a few decode rows of
+    other sequences, bf16 KV, d = 128, bs = 16, shuffled pool."""
+    from ehip import workloads
+    rng = np.random.default_rng(seed)
+    qlens = [T] + [1] * extra_decodes
+    L = [P + T] + list(rng.integers(20, 400, extra_decodes) + 1)
+    need = [(x + 15) // 16 for x in L]
+    pool = int(sum(need) * 1.3) + 2
+    tables, _ = workloads._tables_from_pool(np.array(need), pool, rng)
+    return workloads._finish("chunk", H, Hkv, 128, 16, ehip_mod_kv_bf16(), 1, qlens, L, tables,
+                             pool, std)
+
+
+def ehip_mod_kv_bf16():
+    import ehip
+    return ehip.KV_BF16
+
+
+@pytest.mark.parametrize("H,Hkv", [(32, 8), (64, 8)])
+@pytest.mark.parametrize("T,P", [(16, 0), (37, 0), (300, 0), (45, 100), (130, 515)])
+def test_prefill_chunk_shapes(gctx, ehip_mod, orc, H, Hkv, T, P):
+    """Causal chunks on the MFMA prefill kernel: ragged last query block,
+    continuation chunks (P > 0), g = 4 and 8."""
+    w = chunk_workload(H, Hkv, T, P, extra_decodes=2, seed=T + P + H)
+    (got, ref, kpool, vpool, q, cu), = run_step(gctx, ehip_mod, orc, w, 31)
+    ref32 = fp32_reference(orc, w, kpool, vpool, q, cu)
+    check_step_rows(w, got, ref, ref32)
 
 
 @pytest.mark.parametrize("kernel", ["mfma", "valu"])
