@@ -44,7 +44,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="C4", choices=["C2", "C3", "C4", "C5"])
+    ap.add_argument("--config", default="C4", choices=["C1", "C2", "C3", "C4", "C5"])
     ap.add_argument("--layers", type=int, default=0, help="override the config's layer count")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -105,6 +105,78 @@ def cpu_baseline(w, seconds: float):
                        f"{len(times)} calls"),
             "attended_kv_tok_per_s": round(sum(lens) / t, 1),
             "ms_per_call": round(t * 1e3, 3)}
+
+
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def time_chunks(ctx, ehip, w, slabs, qs, outs, layers, reps=5):
+    """Attention time per layer of the workload's prefill chunks alone (a
+    step holding only the chunk sequences; their K/V are already in the
+    pools), so the MFMA prefill kernel can be priced against its roofline."""
+    idx = [i for i, T in enumerate(w.query_lens) if T > 1]
+    if not idx:
+        return None
+    qlens = w.query_lens[idx]
+    st = ehip.StepArrays(qlens, w.context_lens[idx], [w.tables[i] for i in idx])
+    g = ehip.geometry(w.heads, w.kv_heads, w.head_dim, w.block_size, w.kv_dtype,
+                      w.pool_blocks, w.scale)
+    ctx._check(ctx.step_upload(g, st))
+    ev = [(ctx.event(), ctx.event()) for _ in range(reps * layers)]
+    for r in range(reps + 1):
+        for layer in range(layers):
+            ks, vs = slabs[layer]
+            if r:
+                ctx.record(ev[(r - 1) * layers + layer][0])
+            ctx._check(ctx.step_attention(qs[layer], ks, vs, outs[layer]))
+            if r:
+                ctx.record(ev[(r - 1) * layers + layer][1])
+    ctx.sync()
+    t = float(np.mean([ctx.elapsed_ms(a, b) for a, b in ev])) / 1e3
+    flops = 0
+    for T, L in zip(qlens, w.context_lens[idx]):
+        P = int(L) - int(T)
+        flops += 4 * w.heads * w.head_dim * (int(T) * P + int(T) * (int(T) + 1) // 2)
+    return {"chunks": len(idx), "rows": int(qlens.sum()), "flops_per_layer": flops,
+            "us_per_layer": round(t * 1e6, 2), "tflops": round(flops / t / 1e12, 2),
+            "roofline": {"bound": "mfma", "achieved": round(flops / t / 1e12, 2),
+                         "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(flops / t / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+                         "kernel": "causal prefill chunks (bf16 MFMA)"}}
+
+
+def c5_reprefill(ctx, ehip, w, slabs, layers, reps=3):
+    """C5's preempt-and-recompute event: one evicted sequence re-prefilled as
+    a 4096-token causal chunk (P = 0), per layer, on the C5 pools."""
+    T = 4096
+    table = np.asarray(w.tables[0][:T // w.block_size], np.int32)  # 256 blocks of the pool
+    st = ehip.StepArrays([T], [T], [table])
+    g = ehip.geometry(w.heads, w.kv_heads, w.head_dim, w.block_size, w.kv_dtype,
+                      w.pool_blocks, w.scale)
+    q = ctx.alloc(T * w.heads * w.head_dim * 4)
+    out = ctx.alloc(T * w.heads * w.head_dim * 4)
+    ctx.fill_normal(q, T * w.heads * w.head_dim, ehip.KV_F32, 0.0, w.qkv_std, 77)
+    ctx._check(ctx.step_upload(g, st))
+    ev = [(ctx.event(), ctx.event()) for _ in range(reps * layers)]
+    for r in range(reps + 1):
+        for layer in range(layers):
+            ks, vs = slabs[layer]
+            if r:
+                ctx.record(ev[(r - 1) * layers + layer][0])
+            ctx._check(ctx.step_attention(q, ks, vs, out))
+            if r:
+                ctx.record(ev[(r - 1) * layers + layer][1])
+    ctx.sync()
+    t = float(np.mean([ctx.elapsed_ms(a, b) for a, b in ev])) / 1e3
+    flops = 4 * w.heads * w.head_dim * (T * (T + 1) // 2)
+    q.free()
+    out.free()
+    return {"tokens": T, "flops_per_layer": flops, "us_per_layer": round(t * 1e6, 2),
+            "tflops": round(flops / t / 1e12, 2), "event_ms": round(t * layers * 1e3, 3),
+            "roofline": {"bound": "mfma", "achieved": round(flops / t / 1e12, 2),
+                         "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(flops / t / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+                         "kernel": "causal prefill chunk (bf16 MFMA)"}}
 
 
 def main():
@@ -233,6 +305,16 @@ def main():
             "avg_launch_us": round(attn_avg * 1e6, 3),
         },
     }
+    pre = time_chunks(ctx, ehip, w, slabs, qs, outs, layers)
+    if pre is not None:
+        result["prefill"] = pre
+        log(f"[bench] prefill chunks: {pre['us_per_layer']} us/layer, {pre['tflops']} TFLOP/s")
+    if w.name == "C5":
+        ev = c5_reprefill(ctx, ehip, w, slabs, layers)
+        result["reprefill_event"] = ev
+        # One 4096-token re-prefill every 50 decode steps, amortised per step.
+        result["ms_per_step_with_reprefill"] = round(t_step * 1e3 + ev["event_ms"] / 50, 4)
+        log(f"[bench] C5 re-prefill: {ev['us_per_layer']} us/layer, {ev['tflops']} TFLOP/s")
     if not args.no_cpu_baseline:
         log("[bench] cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
