@@ -1,0 +1,832 @@
+// Tests of the host layer (llm-inference-engine_amd/host): block pool, block
+// tables, paged caches, scheduler and step assembly, modelled on the
+// reference's own unit tests (tests/kvcache/block_pool_test.cpp,
+// block_table_test.cpp, paged_cache_test.cpp, tests/scheduler/
+// scheduler_test.cpp, tests/engine/batch_test.cpp).
+//
+//   host_tests --cpu   bookkeeping on host-memory slabs (no GPU needed)
+//   host_tests --gpu   the same layer over HBM slabs through the C ABI,
+//                      checked against the CPU oracle (oracle/liboracle.so)
+//
+// Death tests fork; the child's abort is the expected outcome.
+#include <sys/wait.h>
+#include <unistd.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <functional>
+#include <string>
+#include <vector>
+
+#include "batch.h"
+#include "block_pool.h"
+#include "block_table.h"
+#include "ehip.h"
+#include "kernels.h"
+#include "oracle.h"
+#include "paged_kv_cache.h"
+#include "scheduler.h"
+
+using namespace ehip::host;
+
+namespace {
+
+struct TestCase {
+  const char* name;
+  bool gpu;
+  std::function<void()> fn;
+};
+std::vector<TestCase>& Registry() {
+  static std::vector<TestCase> r;
+  return r;
+}
+int g_failures = 0;
+
+struct Register {
+  Register(const char* n, bool gpu, std::function<void()> f) {
+    Registry().push_back({n, gpu, std::move(f)});
+  }
+};
+
+#define CAT2(a, b) a##b
+#define CAT(a, b) CAT2(a, b)
+#define TEST_CPU(name)                                                  \
+  static void name();                                                   \
+  static Register CAT(reg_, name)(#name, false, name);                  \
+  static void name()
+#define TEST_GPU(name)                                                  \
+  static void name();                                                   \
+  static Register CAT(reg_, name)(#name, true, name);                   \
+  static void name()
+
+#define EXPECT(cond)                                                          \
+  do {                                                                        \
+    if (!(cond)) {                                                            \
+      std::fprintf(stderr, "  %s:%d: EXPECT(%s) failed\n", __FILE__, __LINE__, #cond); \
+      ++g_failures;                                                           \
+    }                                                                         \
+  } while (0)
+#define EXPECT_EQ(a, b)                                                              \
+  do {                                                                               \
+    const auto va_ = (a);                                                            \
+    const auto vb_ = (b);                                                            \
+    if (!(va_ == vb_)) {                                                             \
+      std::fprintf(stderr, "  %s:%d: EXPECT_EQ(%s, %s) failed: %lld vs %lld\n", __FILE__, \
+                   __LINE__, #a, #b, static_cast<long long>(va_),                    \
+                   static_cast<long long>(vb_));                                     \
+      ++g_failures;                                                                  \
+    }                                                                                \
+  } while (0)
+#define ASSERT_OK(expr)                                                                   \
+  do {                                                                                    \
+    const Status st_ = (expr);                                                            \
+    if (!st_.ok()) {                                                                      \
+      std::fprintf(stderr, "  %s:%d: %s -> code %d: %s\n", __FILE__, __LINE__, #expr,      \
+                   static_cast<int>(st_.code()), st_.message().c_str());                  \
+      ++g_failures;                                                                       \
+      return;                                                                             \
+    }                                                                                     \
+  } while (0)
+#define EXPECT_CODE(expr, c) EXPECT_EQ(static_cast<int>((expr).code()), static_cast<int>(c))
+
+// Runs `body` in a child process; passes when the child dies by SIGABRT.
+bool DiesWithAbort(const std::function<void()>& body) {
+  std::fflush(stdout);
+  std::fflush(stderr);
+  const pid_t pid = fork();
+  if (pid == 0) {
+    if (std::freopen("/dev/null", "w", stderr) == nullptr) std::_Exit(3);
+    body();
+    std::_Exit(0);
+  }
+  int status = 0;
+  waitpid(pid, &status, 0);
+  return WIFSIGNALED(status) && WTERMSIG(status) == SIGABRT;
+}
+#define EXPECT_DEATH(stmt) EXPECT(DiesWithAbort([&] { stmt; }))
+
+CacheGeometry Geom(int layers, int hkv, int d, KvDtype dt = KvDtype::kFloat32) {
+  CacheGeometry g;
+  g.num_layers = layers;
+  g.num_kv_heads = hkv;
+  g.head_dim = d;
+  g.dtype = dt;
+  return g;
+}
+
+HostSlabAllocator g_host_alloc;
+
+std::unique_ptr<BlockPool> HostPool(int64_t blocks, int bs = 16, int layers = 2, int hkv = 2,
+                                    int d = 8) {
+  StatusOr<std::unique_ptr<BlockPool>> p =
+      BlockPool::Create(Geom(layers, hkv, d), bs, blocks, &g_host_alloc);
+  if (!p.ok()) {
+    std::fprintf(stderr, "pool create failed: %s\n", p.status().message().c_str());
+    std::abort();
+  }
+  return std::move(*p);
+}
+
+// ---------------------------------------------------------------- BlockPool
+
+TEST_CPU(BytesPerBlockMatchesConfigs) {
+  // 2 · L · Hkv · bs · d · itemsize: Llama-3-8B bf16 bs16 = 2 MiB, 70B = 5 MiB.
+  EXPECT_EQ(*BlockPool::BytesPerBlock(Geom(32, 8, 128, KvDtype::kBFloat16), 16), 2LL << 20);
+  EXPECT_EQ(*BlockPool::BytesPerBlock(Geom(80, 8, 128, KvDtype::kBFloat16), 16), 5LL << 20);
+  // Qwen2-0.5B fp32: 2·24·2·16·64·4.
+  EXPECT_EQ(*BlockPool::BytesPerBlock(Geom(24, 2, 64), 16), 2LL * 24 * 2 * 16 * 64 * 4);
+  for (int bad : {0, 4, 12, 128})
+    EXPECT_CODE(BlockPool::BytesPerBlock(Geom(2, 2, 8), bad).status(),
+                StatusCode::kInvalidArgument);
+  EXPECT_CODE(BlockPool::BytesPerBlock(Geom(0, 2, 8), 16).status(), StatusCode::kInvalidArgument);
+  EXPECT_CODE(BlockPool::BytesPerBlock(Geom(1 << 30, 1 << 30, 1 << 30), 64).status(),
+              StatusCode::kInvalidArgument);
+}
+
+TEST_CPU(NumBlocksForBudget) {
+  const CacheGeometry g = Geom(32, 8, 128, KvDtype::kBFloat16);
+  EXPECT_EQ(*BlockPool::NumBlocksForBudget(g, 16, (2LL << 20) * 10 + 5), 10);
+  EXPECT_CODE(BlockPool::NumBlocksForBudget(g, 16, (2LL << 20) - 1).status(),
+              StatusCode::kResourceExhausted);
+  EXPECT_CODE(BlockPool::NumBlocksForBudget(g, 16, 0).status(), StatusCode::kInvalidArgument);
+}
+
+TEST_CPU(CreateValidatesAndZeroFills) {
+  EXPECT_CODE(BlockPool::Create(Geom(2, 2, 8), 16, 0, &g_host_alloc).status(),
+              StatusCode::kInvalidArgument);
+  EXPECT_CODE(BlockPool::Create(Geom(2, 2, 8), 24, 4, &g_host_alloc).status(),
+              StatusCode::kInvalidArgument);
+  EXPECT_CODE(BlockPool::Create(Geom(2, 2, 8), 16, 4, nullptr).status(),
+              StatusCode::kInvalidArgument);
+  auto pool = HostPool(5, 16, 3, 2, 8);
+  EXPECT_EQ(pool->slab_bytes(), 5 * 2 * 16 * 8 * 4);
+  EXPECT_EQ(pool->total_bytes(), pool->slab_bytes() * 6);
+  EXPECT_EQ(pool->block_stride(), 2 * 16 * 8);
+  EXPECT_EQ(pool->head_stride(), 16 * 8);
+  EXPECT_EQ(pool->row_stride(), 8);
+  for (int l = 0; l < 3; ++l) {
+    for (void* s : {pool->k_slab(l), pool->v_slab(l)}) {
+      EXPECT_EQ(reinterpret_cast<uintptr_t>(s) % BlockPool::kSlabAlignment, 0u);
+      const auto* f = static_cast<const float*>(s);
+      bool zero = true;
+      for (int64_t i = 0; i < pool->slab_bytes() / 4; ++i) zero = zero && f[i] == 0.0f;
+      EXPECT(zero);
+    }
+  }
+}
+
+TEST_CPU(AllocateIsLifoFromBlockZero) {
+  auto pool = HostPool(4);
+  EXPECT_EQ(*pool->Allocate(), 0);
+  EXPECT_EQ(*pool->Allocate(), 1);
+  EXPECT_EQ(*pool->Allocate(), 2);
+  pool->Release(1);
+  EXPECT_EQ(*pool->Allocate(), 1);  // most recently freed first
+  EXPECT_EQ(*pool->Allocate(), 3);
+  StatusOr<int32_t> none = pool->Allocate();
+  EXPECT_CODE(none.status(), StatusCode::kResourceExhausted);
+  const BlockPoolStats s = pool->stats();
+  EXPECT_EQ(s.total, 4);
+  EXPECT_EQ(s.used, 4);
+  EXPECT_EQ(s.free, 0);
+  EXPECT_EQ(s.peak_used, 4);
+  EXPECT_EQ(s.exhaustions, 1);
+  EXPECT_EQ(s.block_size, 16);
+  EXPECT(s.utilization == 1.0);
+  for (int32_t b = 0; b < 4; ++b) pool->Release(b);
+  const BlockPoolStats t = pool->stats();
+  EXPECT_EQ(t.used, 0);
+  EXPECT_EQ(t.free, 4);
+  EXPECT_EQ(t.peak_used, 4);  // monotone
+}
+
+TEST_CPU(ShareReleaseRefcounts) {
+  auto pool = HostPool(3);
+  const int32_t b = *pool->Allocate();
+  pool->Share(b);
+  pool->Share(b);
+  EXPECT_EQ(pool->refcount(b), 3);
+  pool->Release(b);
+  pool->Release(b);
+  EXPECT_EQ(pool->refcount(b), 1);
+  EXPECT_EQ(pool->free_blocks(), 2);
+  pool->Release(b);
+  EXPECT_EQ(pool->free_blocks(), 3);
+  EXPECT_EQ(pool->stats().used, 0);
+}
+
+TEST_CPU(ProgrammerErrorsAbort) {
+  auto pool = HostPool(3);
+  EXPECT_DEATH(pool->Release(0));          // never allocated: double free
+  EXPECT_DEATH(pool->Share(1));            // sharing a free block
+  EXPECT_DEATH(pool->Release(3));          // out of range
+  EXPECT_DEATH(pool->Share(-1));
+  EXPECT_DEATH((void)pool->blocks_needed(-1, 1));
+  const int32_t b = *pool->Allocate();
+  pool->Release(b);
+  EXPECT_DEATH(pool->Release(b));  // released twice
+}
+
+TEST_CPU(BlocksNeededIsBoundaryCrossingCount) {
+  auto pool = HostPool(2, 16);
+  // Brute force: count positions p in [cur, cur+add) with p % bs == 0.
+  for (int64_t cur = 0; cur < 70; ++cur)
+    for (int64_t add = 0; add < 70; ++add) {
+      int64_t n = 0;
+      for (int64_t p = cur; p < cur + add; ++p) n += p % 16 == 0;
+      EXPECT_EQ(pool->blocks_needed(cur, add), n);
+      EXPECT_EQ(scheduler::BlocksNeeded(cur, add, 16), n);
+    }
+}
+
+// --------------------------------------------------------------- BlockTable
+
+TEST_CPU(AppendTokensSlotMapping) {
+  auto pool = HostPool(8, 8);
+  // Take blocks 0..2 out first so the table's blocks are not 0, 1, 2 ...
+  const int32_t a = *pool->Allocate(), b = *pool->Allocate(), c = *pool->Allocate();
+  pool->Release(b);  // free stack top: b(1), then 3, 4, ...
+  BlockTable t(pool.get());
+  StatusOr<std::vector<int64_t>> s1 = t.AppendTokens(5);
+  ASSERT_OK(s1.status());
+  EXPECT_EQ(t.num_blocks(), 1);
+  EXPECT_EQ(t.blocks()[0], 1);
+  for (int i = 0; i < 5; ++i) EXPECT_EQ((*s1)[static_cast<size_t>(i)], 1 * 8 + i);
+  StatusOr<std::vector<int64_t>> s2 = t.AppendTokens(12);  // positions 5..16
+  ASSERT_OK(s2.status());
+  EXPECT_EQ(t.num_blocks(), 3);
+  EXPECT_EQ(t.blocks()[1], 3);
+  EXPECT_EQ(t.blocks()[2], 4);
+  for (int64_t p = 5; p < 17; ++p) {
+    const int64_t want = int64_t{t.blocks()[static_cast<size_t>(p / 8)]} * 8 + p % 8;
+    EXPECT_EQ((*s2)[static_cast<size_t>(p - 5)], want);
+    EXPECT_EQ(t.slot(p), want);
+  }
+  EXPECT_EQ(t.num_tokens(), 17);
+  EXPECT_CODE(t.AppendTokens(0).status(), StatusCode::kInvalidArgument);
+  EXPECT_DEATH((void)t.slot(17));
+  EXPECT_DEATH((void)t.slot(-1));
+  pool->Release(a);
+  pool->Release(c);
+}
+
+TEST_CPU(AppendTokensAllOrNothing) {
+  auto pool = HostPool(4, 16);
+  BlockTable t(pool.get());
+  ASSERT_OK(t.AppendTokens(20).status());  // 2 blocks
+  const BlockPoolStats before = pool->stats();
+  const std::vector<int32_t> blocks = t.blocks();
+  // 20 + 60 = 80 tokens needs 5 blocks: 3 more, only 2 free.
+  EXPECT_CODE(t.AppendTokens(60).status(), StatusCode::kResourceExhausted);
+  const BlockPoolStats after = pool->stats();
+  EXPECT_EQ(after.used, before.used);
+  EXPECT_EQ(after.free, before.free);
+  EXPECT_EQ(after.exhaustions, before.exhaustions + 1);
+  EXPECT_EQ(t.num_tokens(), 20);
+  EXPECT(t.blocks() == blocks);
+  // The blocks taken (2, then 3) were released in that order, so the stack
+  // now yields 3 first.
+  ASSERT_OK(t.AppendTokens(44).status());  // exactly 4 blocks
+  EXPECT_EQ(t.blocks()[2], 3);
+  EXPECT_EQ(t.blocks()[3], 2);
+}
+
+TEST_CPU(TruncateKeepsPartialTailReleasesTailFirst) {
+  auto pool = HostPool(8, 8);
+  BlockTable t(pool.get());
+  ASSERT_OK(t.AppendTokens(40).status());  // blocks 0..4
+  EXPECT_CODE(t.Truncate(41), StatusCode::kInvalidArgument);
+  EXPECT_CODE(t.Truncate(-1), StatusCode::kInvalidArgument);
+  ASSERT_OK(t.Truncate(13));  // keeps ceil(13/8) = 2 blocks
+  EXPECT_EQ(t.num_blocks(), 2);
+  EXPECT_EQ(t.num_tokens(), 13);
+  EXPECT_EQ(pool->free_blocks(), 6);
+  // Released 4, 3, 2 in that order: the next allocations return 2, 3, 4.
+  ASSERT_OK(t.AppendTokens(11).status());  // 24 tokens = 3 blocks
+  EXPECT_EQ(t.blocks()[2], 2);
+  EXPECT_EQ(t.slot(13), 1 * 8 + 5);  // the partial tail block is reused in place
+  ASSERT_OK(t.Truncate(0));
+  EXPECT_EQ(t.num_blocks(), 0);
+  EXPECT_EQ(pool->free_blocks(), 8);
+}
+
+TEST_CPU(FreeAllAndMove) {
+  auto pool = HostPool(6, 16);
+  {
+    BlockTable t(pool.get());
+    ASSERT_OK(t.AppendTokens(33).status());
+    EXPECT_EQ(pool->stats().used, 3);
+    BlockTable moved(std::move(t));
+    EXPECT_EQ(t.num_tokens(), 0);
+    EXPECT_EQ(t.num_blocks(), 0);
+    EXPECT_EQ(moved.num_tokens(), 33);
+    EXPECT_EQ(pool->stats().used, 3);
+  }  // both destroyed: moved releases, the moved-from one releases nothing
+  EXPECT_EQ(pool->stats().used, 0);
+  EXPECT_DEATH(BlockTable bad(nullptr));
+}
+
+TEST_CPU(ForkSharesLeadingBlocks) {
+  auto pool = HostPool(8, 8);
+  BlockTable parent(pool.get());
+  ASSERT_OK(parent.AppendTokens(20).status());  // blocks 0, 1, 2 (2 partial)
+  BlockTable child(pool.get());
+  EXPECT_CODE(child.ForkFrom(parent, 12), StatusCode::kInvalidArgument);  // not whole blocks
+  EXPECT_CODE(child.ForkFrom(parent, 24), StatusCode::kInvalidArgument);  // beyond the parent
+  ASSERT_OK(child.ForkFrom(parent, 16));
+  EXPECT_EQ(pool->refcount(0), 2);
+  EXPECT_EQ(pool->refcount(1), 2);
+  EXPECT_EQ(pool->refcount(2), 1);
+  EXPECT_EQ(pool->stats().used, 3);
+  EXPECT_CODE(child.ForkFrom(parent, 8), StatusCode::kFailedPrecondition);  // not empty
+  // The child's appends go to fresh blocks: shared blocks are never written.
+  StatusOr<std::vector<int64_t>> s = child.AppendTokens(3);
+  ASSERT_OK(s.status());
+  EXPECT_EQ((*s)[0], 3 * 8 + 0);
+  // Truncating into a shared block would leave it as a writable tail.
+  EXPECT_CODE(child.Truncate(10), StatusCode::kFailedPrecondition);
+  EXPECT_EQ(child.num_tokens(), 19);
+  ASSERT_OK(child.Truncate(16));  // whole shared blocks stay, nothing written
+  parent.FreeAll();
+  EXPECT_EQ(pool->refcount(0), 1);
+  EXPECT_EQ(pool->stats().used, 2);
+}
+
+// ------------------------------------------------------------- PagedKvCache
+
+TEST_CPU(PagedCacheBookkeepingOnHostPool) {
+  auto pool = HostPool(8, 16);
+  PagedKvCache cache(pool.get(), nullptr);
+  EXPECT_EQ(cache.length(), 0);
+  EXPECT_EQ(cache.capacity(), 8 * 16);
+  float dummy[4] = {0};
+  // The device scatter needs HBM slabs.
+  EXPECT_CODE(cache.append(0, dummy, dummy, 1), StatusCode::kFailedPrecondition);
+  EXPECT_CODE(cache.append(2, dummy, dummy, 1), StatusCode::kInvalidArgument);
+  StatusOr<const std::vector<int64_t>*> g = cache.Grow(17);
+  ASSERT_OK(g.status());
+  EXPECT_EQ((*g)->size(), 17u);
+  EXPECT_EQ(cache.length(), 17);
+  EXPECT_EQ(cache.capacity(), 8 * 16);  // 2 owned blocks + 6 free
+  StatusOr<PagedKvView> v = cache.paged_view(1);
+  ASSERT_OK(v.status());
+  EXPECT(v->k_slab == pool->k_slab(1));
+  EXPECT(v->v_slab == pool->v_slab(1));
+  EXPECT(v->d_block_table == nullptr);
+  EXPECT_EQ(v->num_blocks, 2);
+  EXPECT_EQ(v->length, 17);
+  EXPECT_EQ(v->block_stride, pool->block_stride());
+  EXPECT_EQ(v->block_table[1], cache.block_table().blocks()[1]);
+  EXPECT_CODE(cache.paged_view(2).status(), StatusCode::kInvalidArgument);
+  ASSERT_OK(cache.truncate(3));
+  EXPECT_EQ(cache.length(), 3);
+  cache.reset();
+  EXPECT_EQ(cache.length(), 0);
+  EXPECT_EQ(pool->stats().used, 0);
+}
+
+// ---------------------------------------------------------------- Scheduler
+
+scheduler::SeqDesc Seq(uint64_t id, uint64_t arrival, int64_t computed, int64_t prompt,
+                       int64_t held) {
+  scheduler::SeqDesc s;
+  s.id = id;
+  s.arrival_index = arrival;
+  s.num_computed_tokens = computed;
+  s.num_prompt_tokens = prompt;
+  s.blocks_held = held;
+  return s;
+}
+
+TEST_CPU(SchedulerDecodeFirstThenFcfsAdmission) {
+  // Running: lengths 16 (needs a block) and 20 (fits its tail). Waiting:
+  // prompts of 30, 40, 10 tokens.
+  std::vector<scheduler::SeqDesc> running = {Seq(1, 0, 16, 0, 1), Seq(2, 1, 20, 0, 2)};
+  std::vector<scheduler::SeqDesc> waiting = {Seq(3, 2, 0, 30, 0), Seq(4, 3, 0, 40, 0),
+                                             Seq(5, 4, 0, 10, 0)};
+  scheduler::ScheduleInputs in;
+  in.running = running;
+  in.waiting = waiting;
+  in.pool = {6, 10, 16};
+  in.config.max_num_seqs = 8;
+  in.config.max_num_batched_tokens = 100;
+  scheduler::Scheduler sched;
+  scheduler::SchedulerOutput out = sched.Schedule(in);
+  EXPECT(out.preempt.empty());
+  EXPECT_EQ(out.decode.size(), 2u);
+  EXPECT_EQ(out.decode[0], 1u);
+  EXPECT_EQ(out.decode[1], 2u);
+  // Budget 6 - 1 = 5: 30 tokens (2 blocks) fits, 40 (3 blocks) fits, 10
+  // (1 block) does not (0 left).
+  EXPECT_EQ(out.prefill.size(), 2u);
+  EXPECT_EQ(out.prefill[0].id, 3u);
+  EXPECT_EQ(out.prefill[0].num_tokens, 30);
+  EXPECT_EQ(out.prefill[1].id, 4u);
+
+  // Token budget stops admission at the first prompt that does not fit,
+  // even when a later, smaller one would (no skipping: FCFS).
+  in.config.max_num_batched_tokens = 60;
+  out = sched.Schedule(in);
+  EXPECT_EQ(out.prefill.size(), 1u);
+  // Width cap.
+  in.config.max_num_batched_tokens = 100;
+  in.config.max_num_seqs = 3;
+  out = sched.Schedule(in);
+  EXPECT_EQ(out.prefill.size(), 1u);
+}
+
+TEST_CPU(SchedulerPreemptsLatestArrival) {
+  // Four running sequences each at a block boundary (each needs one block),
+  // one free block: preempt latest arrivals until demand fits.
+  std::vector<scheduler::SeqDesc> running = {Seq(10, 5, 32, 0, 2), Seq(11, 9, 16, 0, 1),
+                                             Seq(12, 2, 48, 0, 3), Seq(13, 9, 64, 0, 4)};
+  scheduler::ScheduleInputs in;
+  in.running = running;
+  in.pool = {1, 16, 16};
+  scheduler::SchedulerOutput out = scheduler::Scheduler().Schedule(in);
+  // Tie on arrival 9: the later entry (13) goes first; freeing its 4 blocks
+  // gives 5 >= demand 3, so only one preemption.
+  EXPECT_EQ(out.preempt.size(), 1u);
+  EXPECT_EQ(out.preempt[0], 13u);
+  EXPECT_EQ(out.decode.size(), 3u);
+  EXPECT_EQ(out.decode[0], 10u);
+  EXPECT_EQ(out.decode[1], 11u);
+  EXPECT_EQ(out.decode[2], 12u);
+
+  // No free blocks and nobody holds any: everyone is preempted.
+  std::vector<scheduler::SeqDesc> bare = {Seq(1, 0, 0, 0, 0), Seq(2, 1, 0, 0, 0)};
+  in.running = bare;
+  in.pool = {0, 16, 16};
+  out = scheduler::Scheduler().Schedule(in);
+  EXPECT_EQ(out.preempt.size(), 2u);
+  EXPECT_EQ(out.preempt[0], 2u);
+  EXPECT_EQ(out.preempt[1], 1u);
+  EXPECT(out.decode.empty());
+}
+
+TEST_CPU(SchedulerLongContextReprefill) {
+  // The long-context workload's preemption event: 32 running sequences, the
+  // pool one block short; the victim (latest arrival, 4096 tokens held in 256
+  // blocks) is re-admitted as a 4096-token prefill in a later step.
+  std::vector<scheduler::SeqDesc> running;
+  for (uint64_t i = 0; i < 32; ++i)
+    running.push_back(Seq(i, i, i == 31 ? 4096 : 1024 + 16 * i, 0, i == 31 ? 256 : 64 + i));
+  scheduler::ScheduleInputs in;
+  in.running = running;
+  in.pool = {31, 20000, 16};
+  in.config.max_num_batched_tokens = 8192;
+  scheduler::SchedulerOutput out = scheduler::Scheduler().Schedule(in);
+  EXPECT_EQ(out.preempt.size(), 1u);
+  EXPECT_EQ(out.preempt[0], 31u);
+  EXPECT_EQ(out.decode.size(), 31u);
+  // Next step: it waits with its 4096-token context as the prompt.
+  running.pop_back();
+  std::vector<scheduler::SeqDesc> waiting = {Seq(31, 31, 0, 4096, 0)};
+  in.running = running;
+  in.waiting = waiting;
+  // 31 decodes at block boundaries take 31 blocks; 256 remain for the prompt.
+  in.pool = {31 + 256, 20000, 16};
+  out = scheduler::Scheduler().Schedule(in);
+  EXPECT(out.preempt.empty());
+  EXPECT_EQ(out.prefill.size(), 1u);
+  EXPECT_EQ(out.prefill[0].num_tokens, 4096);
+}
+
+TEST_CPU(SchedulerBadConfigAborts) {
+  scheduler::ScheduleInputs in;
+  in.pool = {4, 4, 0};
+  EXPECT_DEATH((void)scheduler::Scheduler().Schedule(in));
+  in.pool = {4, 4, 16};
+  in.config.max_num_seqs = 0;
+  EXPECT_DEATH((void)scheduler::Scheduler().Schedule(in));
+  in.config.max_num_seqs = 4;
+  in.pool.free_blocks = -1;
+  EXPECT_DEATH((void)scheduler::Scheduler().Schedule(in));
+}
+
+// ------------------------------------------------------------ BatchAssembler
+
+TEST_CPU(AssembleMixedStep) {
+  auto pool = HostPool(32, 16, 2, 2, 8);
+  PagedKvCache a(pool.get(), nullptr), b(pool.get(), nullptr), c(pool.get(), nullptr);
+  ASSERT_OK(a.Grow(40).status());
+  ASSERT_OK(c.Grow(16).status());
+  std::vector<int32_t> ta = {7}, tb(21, 3), tc = {9};
+  std::vector<BatchSeqInput> seqs = {{ta, &a}, {tb, &b}, {tc, &c}};
+  BatchAssembler asmb;
+  EXPECT_CODE(asmb.AssembleDecode(seqs), StatusCode::kInvalidArgument);
+  EXPECT_EQ(a.length(), 40);  // validation failed before any growth
+  ASSERT_OK(asmb.AssembleMixed(seqs));
+  const BatchInputs& in = asmb.inputs();
+  EXPECT_EQ(in.num_seqs(), 3);
+  EXPECT_EQ(in.num_tokens(), 23);
+  EXPECT(in.cu_seqlens == (std::vector<int32_t>{0, 1, 22, 23}));
+  EXPECT_EQ(in.positions[0], 40);
+  EXPECT_EQ(in.positions[1], 0);
+  EXPECT_EQ(in.positions[21], 20);
+  EXPECT_EQ(in.positions[22], 16);
+  EXPECT(in.query_lens == (std::vector<int32_t>{1, 21, 1}));
+  EXPECT(in.context_lens == (std::vector<int64_t>{41, 21, 17}));
+  EXPECT(in.table_offsets == (std::vector<int32_t>{0, 3, 5, 7}));
+  for (int s = 0; s < 3; ++s) {
+    const std::vector<int32_t>& ids = in.caches[static_cast<size_t>(s)]->block_table().blocks();
+    for (size_t i = 0; i < ids.size(); ++i)
+      EXPECT_EQ(in.table_ids[static_cast<size_t>(in.table_offsets[static_cast<size_t>(s)]) + i],
+                ids[i]);
+  }
+  EXPECT_EQ(in.slot_mapping[0], a.block_table().slot(40));
+  for (int t = 0; t < 21; ++t)
+    EXPECT_EQ(in.slot_mapping[static_cast<size_t>(1 + t)], b.block_table().slot(t));
+  EXPECT_EQ(in.slot_mapping[22], c.block_table().slot(16));
+
+  // The packed descriptor is a valid step for the planner.
+  ehip_geometry geo{};
+  geo.heads = 4;
+  geo.kv_heads = 2;
+  geo.head_dim = 8;
+  geo.block_size = 16;
+  geo.kv_dtype = EHIP_KV_F32;
+  geo.slab_blocks = pool->num_blocks();
+  geo.scale = kernels::AttentionScale(8);
+  const ehip_step_desc d = in.desc();
+  int64_t rows = 0;
+  EXPECT_EQ(ehip_plan_counts(&geo, &d, &rows, nullptr, nullptr, nullptr, nullptr, nullptr), 0);
+  EXPECT_EQ(rows, 23);
+}
+
+TEST_CPU(AssembleRollsBackOnExhaustion) {
+  auto pool = HostPool(4, 16);
+  PagedKvCache a(pool.get(), nullptr), b(pool.get(), nullptr);
+  ASSERT_OK(a.Grow(16).status());
+  std::vector<int32_t> one = {1}, many(60, 2);
+  std::vector<BatchSeqInput> seqs = {{one, &a}, {many, &b}};
+  BatchAssembler asmb;
+  // a needs 1 block (16 -> 17), b needs 4: 5 > 3 free.
+  EXPECT_CODE(asmb.AssembleMixed(seqs), StatusCode::kResourceExhausted);
+  EXPECT_EQ(a.length(), 16);
+  EXPECT_EQ(b.length(), 0);
+  EXPECT_EQ(pool->stats().used, 1);
+  EXPECT_EQ(asmb.inputs().num_seqs(), 0);
+  // Duplicate caches and null caches are rejected before growth.
+  std::vector<BatchSeqInput> dup = {{one, &a}, {one, &a}};
+  EXPECT_CODE(asmb.AssembleDecode(dup), StatusCode::kInvalidArgument);
+  std::vector<BatchSeqInput> null_cache = {{one, nullptr}};
+  EXPECT_CODE(asmb.AssembleDecode(null_cache), StatusCode::kInvalidArgument);
+  std::vector<int32_t> none;
+  std::vector<BatchSeqInput> empty_tokens = {{none, &a}};
+  EXPECT_CODE(asmb.AssemblePrefill(empty_tokens), StatusCode::kInvalidArgument);
+  EXPECT_EQ(a.length(), 16);
+}
+
+TEST_CPU(AssembleStagingIsStableAfterWarmup) {
+  auto pool = HostPool(4096, 16);
+  std::vector<PagedKvCache> caches;
+  caches.reserve(64);
+  for (int i = 0; i < 64; ++i) caches.emplace_back(pool.get(), nullptr);
+  std::vector<int32_t> tok = {1};
+  std::vector<BatchSeqInput> seqs;
+  for (auto& c : caches) seqs.push_back({tok, &c});
+  BatchAssembler asmb;
+  ASSERT_OK(asmb.AssembleDecode(seqs));
+  ASSERT_OK(asmb.AssembleDecode(seqs));
+  // Tables grow by at most one block per 16 steps; give the table vector its
+  // high-water mark first, then steps allocate nothing.
+  for (int i = 0; i < 32; ++i) ASSERT_OK(asmb.AssembleDecode(seqs));
+  const size_t warm = asmb.staging_bytes();
+  for (int i = 0; i < 8; ++i) ASSERT_OK(asmb.AssembleDecode(seqs));
+  EXPECT_EQ(asmb.staging_bytes(), warm);
+  EXPECT_EQ(asmb.inputs().context_lens[0], 42);
+}
+
+// --------------------------------------------------------------------- GPU
+
+struct Gpu {
+  ehip_ctx* ctx = nullptr;
+  Gpu() {
+    if (ehip_init(0, &ctx) != EHIP_OK) {
+      std::fprintf(stderr, "ehip_init failed\n");
+      std::abort();
+    }
+  }
+  ~Gpu() { ehip_destroy(ctx); }
+};
+
+std::vector<float> Normal(int64_t n, uint64_t seed) {
+  std::vector<float> v(static_cast<size_t>(n));
+  orc_fill_normal(v.data(), n, 0.0, 1.0, seed);
+  return v;
+}
+
+template <class T>
+std::vector<T> ToHost(ehip_ctx* ctx, const void* d, int64_t n) {
+  std::vector<T> h(static_cast<size_t>(n));
+  if (ehip_copy_to_host(ctx, h.data(), d, n * static_cast<int64_t>(sizeof(T))) != EHIP_OK)
+    std::abort();
+  return h;
+}
+
+DeviceBuffer ToDevice(ehip_ctx* ctx, const std::vector<float>& h) {
+  DeviceBuffer b;
+  if (!b.Upload(ctx, h.data(), static_cast<int64_t>(h.size() * sizeof(float))).ok()) std::abort();
+  return b;
+}
+
+TEST_GPU(GpuPagedCacheAppendViewDecode) {
+  Gpu gpu;
+  HbmSlabAllocator hbm(gpu.ctx);
+  const int L = 2, Hkv = 2, d = 64, bs = 16, H = 14;
+  StatusOr<std::unique_ptr<BlockPool>> pr = BlockPool::Create(Geom(L, Hkv, d), bs, 64, &hbm);
+  ASSERT_OK(pr.status());
+  BlockPool& pool = **pr;
+  // Scramble the free list so the table is not the identity.
+  std::vector<int32_t> taken;
+  for (int i = 0; i < 9; ++i) taken.push_back(*pool.Allocate());
+  for (int i : {3, 7, 1, 5}) pool.Release(taken[static_cast<size_t>(i)]);
+  PagedKvCache cache(&pool, gpu.ctx);
+
+  // Forward 1: a 37-token prompt; forward 2: one decode token.
+  std::vector<float> slab_k(static_cast<size_t>(pool.slab_bytes() / 4) * L, 0.0f);
+  std::vector<float> slab_v(slab_k.size(), 0.0f);
+  uint64_t seed = 11;
+  for (int64_t t : {37, 1}) {
+    const std::vector<int64_t> slots_before;
+    for (int layer = 0; layer < L; ++layer) {
+      std::vector<float> k = Normal(t * Hkv * d, seed++), v = Normal(t * Hkv * d, seed++);
+      DeviceBuffer dk = ToDevice(gpu.ctx, k), dv = ToDevice(gpu.ctx, v);
+      if (layer == 1) {  // out of order / wrong T are rejected without effect
+        EXPECT_CODE(cache.append(0, static_cast<float*>(dk.get()), static_cast<float*>(dv.get()), t),
+                    StatusCode::kInvalidArgument);
+        EXPECT_CODE(cache.append(1, static_cast<float*>(dk.get()), static_cast<float*>(dv.get()),
+                                 t + 1),
+                    StatusCode::kInvalidArgument);
+      }
+      ASSERT_OK(cache.append(layer, static_cast<float*>(dk.get()), static_cast<float*>(dv.get()), t));
+      // The oracle scatter on the host mirror.
+      std::vector<int64_t> slots;
+      for (int64_t p = cache.length() - t; p < cache.length(); ++p)
+        slots.push_back(cache.block_table().slot(p));
+      const size_t off = static_cast<size_t>(layer) * static_cast<size_t>(pool.slab_bytes() / 4);
+      orc_kv_scatter_f32(k.data(), v.data(), slots.data(), t, Hkv, d, bs, slab_k.data() + off,
+                         slab_v.data() + off);
+      if (layer == 0) {  // layer 1 has not seen this forward's tokens yet
+        EXPECT_EQ(cache.visible_length(1), cache.length() - t);
+        EXPECT_EQ(cache.visible_length(0), cache.length());
+      }
+    }
+  }
+  EXPECT_EQ(cache.length(), 38);
+  ASSERT_OK(FromRc(gpu.ctx, ehip_sync(gpu.ctx)));
+  for (int layer = 0; layer < L; ++layer) {
+    const size_t n = static_cast<size_t>(pool.slab_bytes() / 4);
+    const size_t off = static_cast<size_t>(layer) * n;
+    std::vector<float> gk = ToHost<float>(gpu.ctx, pool.k_slab(layer), static_cast<int64_t>(n));
+    std::vector<float> gv = ToHost<float>(gpu.ctx, pool.v_slab(layer), static_cast<int64_t>(n));
+    EXPECT(std::memcmp(gk.data(), slab_k.data() + off, n * 4) == 0);  // bit-exact
+    EXPECT(std::memcmp(gv.data(), slab_v.data() + off, n * 4) == 0);
+
+    // view(): the contiguous gather, bit-exact against the oracle's.
+    const int64_t len = cache.length();
+    DeviceBuffer ok_, ov_;
+    ASSERT_OK(ok_.Reserve(gpu.ctx, Hkv * len * d * 4));
+    ASSERT_OK(ov_.Reserve(gpu.ctx, Hkv * len * d * 4));
+    ASSERT_OK(cache.view(layer, static_cast<float*>(ok_.get()), static_cast<float*>(ov_.get())));
+    std::vector<float> want_k(static_cast<size_t>(Hkv * len * d)), want_v(want_k.size());
+    orc_kv_gather_f32(slab_k.data() + off, slab_v.data() + off, cache.block_table().blocks().data(),
+                      bs, len, Hkv, d, want_k.data(), want_v.data());
+    std::vector<float> got_k = ToHost<float>(gpu.ctx, ok_.get(), Hkv * len * d);
+    EXPECT(std::memcmp(got_k.data(), want_k.data(), want_k.size() * 4) == 0);
+
+    // Single-sequence decode over paged_view (the ForwardLayer call).
+    StatusOr<PagedKvView> pv = cache.paged_view(layer);
+    ASSERT_OK(pv.status());
+    std::vector<float> q = Normal(H * d, 100 + static_cast<uint64_t>(layer));
+    DeviceBuffer dq = ToDevice(gpu.ctx, q), dout;
+    ASSERT_OK(dout.Reserve(gpu.ctx, H * d * 4));
+    const float scale = kernels::AttentionScale(d);
+    ASSERT_OK(kernels::PagedDecodeAttentionF32(
+        gpu.ctx, static_cast<float*>(dq.get()), static_cast<const float*>(pv->k_slab),
+        static_cast<const float*>(pv->v_slab), pv->d_block_table, pv->num_blocks, pv->length, H,
+        Hkv, d, bs, pv->block_stride, pv->slab_blocks, scale, static_cast<float*>(dout.get())));
+    std::vector<float> want(static_cast<size_t>(H * d));
+    orc_paged_decode_f32(ORC_ISA_SCALAR, q.data(), slab_k.data() + off, slab_v.data() + off,
+                         pv->block_table, pv->num_blocks, pv->length, H, Hkv, d, bs,
+                         pv->block_stride, scale, want.data());
+    std::vector<float> got = ToHost<float>(gpu.ctx, dout.get(), H * d);
+    double num = 0, den = 0;
+    for (size_t i = 0; i < want.size(); ++i) {
+      num += (got[i] - want[i]) * double(got[i] - want[i]);
+      den += want[i] * double(want[i]);
+    }
+    EXPECT(std::sqrt(num / den) <= 1e-4);
+  }
+  ASSERT_OK(FromRc(gpu.ctx, ehip_sync(gpu.ctx)));
+}
+
+TEST_GPU(GpuBatchedStepMixedBf16) {
+  // A mixed step over a bf16 pool: 5 decodes (one a fork sharing 2 blocks of
+  // another sequence) and one 40-token prefill chunk, three layers, through
+  // BatchAssembler + BatchedAttention; each layer's output against the fp32
+  // oracle on the widened bf16 slab (bf16 storage tolerance 2e-2 abs).
+  Gpu gpu;
+  HbmSlabAllocator hbm(gpu.ctx);
+  const int L = 3, Hkv = 2, d = 128, bs = 16, H = 8;
+  StatusOr<std::unique_ptr<BlockPool>> pr =
+      BlockPool::Create(Geom(L, Hkv, d, KvDtype::kBFloat16), bs, 96, &hbm);
+  ASSERT_OK(pr.status());
+  BlockPool& pool = **pr;
+  BatchedAttention attn(gpu.ctx, &pool, H);
+  BatchAssembler asmb;
+  std::vector<PagedKvCache> caches;
+  caches.reserve(6);
+  for (int i = 0; i < 6; ++i) caches.emplace_back(&pool, gpu.ctx);
+
+  const size_t slab_n = static_cast<size_t>(pool.slab_bytes() / 2);
+  std::vector<uint16_t> mk(slab_n * L, 0), mv(slab_n * L, 0);  // host mirror of the slabs
+  uint64_t seed = 500;
+  // Step 1: prompts for sequences 0..4 (the fifth forks sequence 0's first
+  // 32 tokens afterwards). Step 2: decodes + a 40-token chunk for seq 5.
+  const std::vector<std::vector<int>> steps = {{50, 17, 33, 90, 0, 0}, {1, 1, 1, 1, 1, 40}};
+  for (size_t step = 0; step < steps.size(); ++step) {
+    if (step == 1) ASSERT_OK(caches[4].ForkFrom(caches[0], 32));
+    std::vector<std::vector<int32_t>> toks;
+    std::vector<BatchSeqInput> seqs;
+    for (int s = 0; s < 6; ++s) toks.emplace_back(static_cast<size_t>(steps[step][static_cast<size_t>(s)]), 1);
+    for (int s = 0; s < 6; ++s)
+      if (!toks[static_cast<size_t>(s)].empty()) seqs.push_back({toks[static_cast<size_t>(s)], &caches[static_cast<size_t>(s)]});
+    ASSERT_OK(asmb.AssembleMixed(seqs));
+    const BatchInputs& in = asmb.inputs();
+    ASSERT_OK(attn.Upload(in));
+    const int64_t T = in.num_tokens();
+    for (int layer = 0; layer < L; ++layer) {
+      std::vector<float> q = Normal(T * H * d, seed++), k = Normal(T * Hkv * d, seed++),
+                         v = Normal(T * Hkv * d, seed++);
+      DeviceBuffer dq = ToDevice(gpu.ctx, q), dk = ToDevice(gpu.ctx, k), dv = ToDevice(gpu.ctx, v),
+                   dout;
+      ASSERT_OK(dout.Reserve(gpu.ctx, T * H * d * 4));
+      if (layer == 1)
+        EXPECT_CODE(attn.ForwardLayer(2, static_cast<float*>(dq.get()), static_cast<float*>(dk.get()),
+                                      static_cast<float*>(dv.get()), static_cast<float*>(dout.get())),
+                    StatusCode::kInvalidArgument);
+      ASSERT_OK(attn.ForwardLayer(layer, static_cast<float*>(dq.get()), static_cast<float*>(dk.get()),
+                                  static_cast<float*>(dv.get()), static_cast<float*>(dout.get())));
+      const size_t off = static_cast<size_t>(layer) * slab_n;
+      orc_kv_scatter_bf16(k.data(), v.data(), in.slot_mapping.data(), T, Hkv, d, bs,
+                          mk.data() + off, mv.data() + off);
+      std::vector<float> got = ToHost<float>(gpu.ctx, dout.get(), T * H * d);
+      ASSERT_OK(FromRc(gpu.ctx, ehip_sync(gpu.ctx)));
+      // Reference: widen the mirror, gather each sequence, causal attention
+      // for its rows at the end of its context.
+      std::vector<float> wk(slab_n), wv(slab_n);
+      orc_bf16_to_fp32_array(mk.data() + off, wk.data(), static_cast<int64_t>(slab_n));
+      orc_bf16_to_fp32_array(mv.data() + off, wv.data(), static_cast<int64_t>(slab_n));
+      double worst = 0;
+      for (int64_t s = 0; s < in.num_seqs(); ++s) {
+        const int64_t len = in.context_lens[static_cast<size_t>(s)];
+        const int64_t tq = in.query_lens[static_cast<size_t>(s)];
+        std::vector<float> ck(static_cast<size_t>(Hkv * len * d)), cv(ck.size());
+        orc_kv_gather_f32(wk.data(), wv.data(), in.caches[static_cast<size_t>(s)]->block_table().blocks().data(),
+                          bs, len, Hkv, d, ck.data(), cv.data());
+        std::vector<float> want(static_cast<size_t>(tq * H * d));
+        const int64_t r0 = in.cu_seqlens[static_cast<size_t>(s)];
+        orc_prefill_f32(ORC_ISA_SCALAR, q.data() + r0 * H * d, ck.data(), cv.data(), want.data(), tq,
+                        H, Hkv, d, len, attn.scale());
+        for (size_t i = 0; i < want.size(); ++i)
+          worst = std::max(worst, std::fabs(double(got[static_cast<size_t>(r0 * H * d) + i]) - want[i]));
+      }
+      if (worst > 2e-2) std::fprintf(stderr, "  step %zu layer %d: max abs err %.3g\n", step, layer, worst);
+      EXPECT(worst <= 2e-2);
+    }
+  }
+  // Shared blocks were read by both sequences and never rewritten.
+  EXPECT_EQ(pool.refcount(caches[0].block_table().blocks()[0]), 2);
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  bool gpu = false;
+  const char* only = nullptr;
+  for (int i = 1; i < argc; ++i) {
+    if (std::strcmp(argv[i], "--gpu") == 0) gpu = true;
+    else if (std::strcmp(argv[i], "--cpu") == 0) gpu = false;
+    else only = argv[i];
+  }
+  int ran = 0, failed_tests = 0;
+  for (const TestCase& t : Registry()) {
+    if (t.gpu != gpu || (only != nullptr && std::strcmp(only, t.name) != 0)) continue;
+    const int before = g_failures;
+    std::printf("[ RUN  ] %s\n", t.name);
+    std::fflush(stdout);
+    t.fn();
+    const bool ok = g_failures == before;
+    failed_tests += ok ? 0 : 1;
+    std::printf("[ %s ] %s\n", ok ? " OK " : "FAIL", t.name);
+    std::fflush(stdout);
+    ++ran;
+  }
+  std::printf("%d tests, %d failed\n", ran, failed_tests);
+  return failed_tests == 0 && ran > 0 ? 0 : 1;
+}
