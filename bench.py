@@ -12,7 +12,10 @@ Prints ONE JSON line (metric/value/unit as BASELINE.json names them):
   value      = algorithmic HBM bytes of the step (unique K/V + Q + O + tables
                + append) / step time, in GB/s;
   roofline   = the attention kernel alone: its algorithmic bytes per launch /
-               its average launch duration (HIP events on the launch stream);
+               its average launch duration (HIP events on the launch stream,
+               bracketing every layer's attention call of every SAMPLE-th
+               timed step: an event pair per launch on every step perturbs
+               the stream enough to cost ~2% of the step time);
   cpu_baseline = the oracle's AVX2 restatement of the reference's batched
                paged decode, timed on this host on a bounded fp32 sample.
 """
@@ -27,6 +30,7 @@ import time
 from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
+EVENT_SAMPLE = 4  # per-launch events on one timed step in four
 sys.path.insert(0, str(ROOT / "llm-inference-engine_amd" / "python"))
 sys.path.insert(0, str(ROOT))
 
@@ -244,19 +248,25 @@ def main():
     rows, items, partials = ctx.step_info()
 
     K = args.steps
-    evs = [[(ctx.event(), ctx.event()) for _ in range(layers)] for _ in range(K)]
+    sampled = [s for s in range(K) if s % EVENT_SAMPLE == EVENT_SAMPLE // 2] or [0]
+    evs = {s: [(ctx.event(), ctx.event()) for _ in range(layers)] for s in sampled}
     e_start, e_end = ctx.event(), ctx.event()
     ctx.sync()
     t0 = time.perf_counter()
     ctx.record(e_start)
     for s in range(K):
-        step(evs[s])
+        step(evs.get(s))
     ctx.record(e_end)
     ctx.sync()
     wall = time.perf_counter() - t0
     gpu_ms = ctx.elapsed_ms(e_start, e_end)
-    attn_ms = [ctx.elapsed_ms(a, b) for per in evs for (a, b) in per]
+    attn_ms = [ctx.elapsed_ms(a, b) for s in sampled for (a, b) in evs[s]]
     log(f"[bench] timed {K} steps: wall {wall * 1e3:.2f} ms, events {gpu_ms:.2f} ms")
+    a = np.array(attn_ms).reshape(len(sampled), layers) * 1e3
+    q = np.percentile(a, [0, 10, 50, 90, 100])
+    log("[bench] attention us per launch: min %.1f p10 %.1f p50 %.1f p90 %.1f max %.1f" % tuple(q))
+    log("[bench] per-layer mean us: " + " ".join(f"{x:.0f}" for x in a.mean(axis=0)))
+    log("[bench] sampled-step mean us: " + " ".join(f"{x:.0f}" for x in a.mean(axis=1)))
 
     t_step = max(wall, gpu_ms / 1e3) / K
     per_layer = w.bytes_per_layer(with_append=True)
@@ -303,6 +313,8 @@ def main():
             "kernel": "paged decode attention (one launch per layer)",
             "algorithmic_bytes_per_launch": attn_bytes,
             "avg_launch_us": round(attn_avg * 1e6, 3),
+            "launches_timed": len(attn_ms),
+            "timed_steps_sampled": len(sampled),
         },
     }
     pre = time_chunks(ctx, ehip, w, slabs, qs, outs, layers)

@@ -20,9 +20,12 @@
 // its virtual heads' tile max with DPP; probabilities go through a small LDS
 // buffer [token][virtual head] to the PV layout.
 //
-// PV: lane l owns head_dim elements 8*(l % (d/8)) .. +8 of every (64/(d/8))-th
-// token row, accumulating o[m][e] in fp32; the token-parallel partial sums are
-// reduced once at the end.
+// PV: lane l owns head_dim elements 2*(l % (d/2)) and +1 of every
+// (128/d)-th token row (all rows for d = 128), accumulating o[m][e] in fp32
+// for every virtual head; V arrives as one 4-byte load per lane per row group,
+// so each load instruction reads whole 256-byte rows, and the accumulators
+// take 2·GV registers (the token-parallel sums of d = 64 are reduced once at
+// the end).
 //
 // K/V arrive through buffer loads whose descriptor is the (block, head) tile
 // base, double-buffered in registers: the next tile's loads are in flight
@@ -42,6 +45,11 @@ typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 
 __device__ __forceinline__ bf16x8_t AsBf16x8(uint4 u) { return __builtin_bit_cast(bf16x8_t, u); }
 
+// Cache policy of the K/V tile loads: non-temporal (nt) at system coherence
+// scope (sc1). Every tile is streamed once per launch; the streaming policy
+// raised a measured gather of this pattern from 5.98 to 6.52 TB/s on MI355X.
+constexpr int kKvLoadAux = 2 | 16;
+
 __device__ __forceinline__ float ReadLane(float x, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
 }
@@ -59,27 +67,33 @@ __device__ __forceinline__ float Max16(float x) {
 template <int D, int TH>
 struct Tile {
   static constexpr int NC = D / 32;
-  static constexpr int PV_LPT = D / 8;
-  static constexpr int PV_J = 16 * PV_LPT / 64;
+  static constexpr int VLPT = D / 2;    // PV lanes per token row (2 elements each)
+  static constexpr int VT = 64 / VLPT;  // token rows per V load instruction
+  static constexpr int VJ = 16 / VT;    // V loads per 16-token half
   uint4 k[TH][NC];
-  uint4 v[TH][PV_J];
+  uint32_t v[TH][VJ];
   int phys[TH];
 };
 
-template <int D, int G, int RMAX, int TH>
-__global__ __launch_bounds__(64) void DecodeMfmaBf16(DecodeParams p) {
+// QL: keep the Q operands in LDS (read per MFMA) instead of 8·NC registers,
+// so the wide shapes fit two wavefronts per SIMD.
+// OCC: wavefronts per SIMD the register allocation must allow.
+template <int D, int G, int RMAX, int TH, int NBUF, bool QL, int OCC>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(OCC)))
+void DecodeMfmaBf16(DecodeParams p) {
   using T = Tile<D, TH>;
   constexpr int TT = 16 * TH;        // tokens per tile
   constexpr int GV = G * RMAX;       // virtual heads (row-major over the item's rows)
   constexpr int NC = T::NC;          // MFMA k-chunks over head_dim
   constexpr int HR = (GV + 3) / 4;   // 16-lane accumulator rows holding virtual heads
   constexpr int HP = HR * 4;         // virtual heads padded to whole rows
-  constexpr int PV_LPT = T::PV_LPT;  // PV lanes per token row
-  constexpr int PV_TPI = 64 / PV_LPT;
-  constexpr int PV_J = T::PV_J;
+  constexpr int VLPT = T::VLPT;
+  constexpr int VT = T::VT;
+  constexpr int VJ = T::VJ;
   static_assert(GV >= 1 && GV <= 16 && (D == 64 || D == 128), "shape");
 
   __shared__ float p_lds[TT * HP];
+  __shared__ uint4 q_lds[QL ? 2 * NC * 64 : 1];
 
   const int lane = threadIdx.x;
   const int item_idx = blockIdx.x;
@@ -91,8 +105,8 @@ __global__ __launch_bounds__(64) void DecodeMfmaBf16(DecodeParams p) {
   const int bs = p.bs;
   const int n = lane & 15;   // MFMA column (token of a half) / A row (virtual head)
   const int kq = lane >> 4;  // MFMA k-group and accumulator row
-  const int pv_e = (lane % PV_LPT) * 8;
-  const int pv_t = lane / PV_LPT;
+  const int ev = (lane % VLPT) * 2;  // PV head_dim elements ev, ev + 1
+  const int tv = lane / VLPT;        // PV token row within a load's row group
 
   // Everything the item needs is fetched at once: the range's table slice
   // (every row of the item reads the same blocks over [tb, te)) and the
@@ -117,14 +131,15 @@ __global__ __launch_bounds__(64) void DecodeMfmaBf16(DecodeParams p) {
   const uint16_t* kbase = static_cast<const uint16_t*>(p.k_slab) + int64_t{hk} * bs * D;
   const uint16_t* vbase = static_cast<const uint16_t*>(p.v_slab) + int64_t{hk} * bs * D;
   const int bmask = bs - 1;
-  const uint32_t tile_bytes = static_cast<uint32_t>(bs) * D * 2;  // one (block, head) tile
   // Per-lane byte offsets inside a (block, head) tile: loop-invariant.
   const int koff = (n * D + kq * 8) * 2;
-  const int voff = (pv_t * D + pv_e) * 2;
+  const int voff = (tv * D + ev) * 2;
 
-  // A half beyond the range, or on a rejected block id, gets an empty
-  // descriptor: its loads return zeros without touching memory, and it is
-  // masked in the arithmetic.
+  // Each half's descriptor starts at its first token row and covers only the
+  // rows inside the range: rows past the range end read as zeros (so stale
+  // slab rows never reach the PV sums, whatever they hold), and a half beyond
+  // the range, or on a rejected block id, gets an empty descriptor whose loads
+  // return zeros without touching memory. Scores of such rows are masked.
   auto load = [&](T& t, int t0) {
 #pragma unroll
     for (int h2 = 0; h2 < TH; ++h2) {
@@ -132,26 +147,25 @@ __global__ __launch_bounds__(64) void DecodeMfmaBf16(DecodeParams p) {
       const int phys = __builtin_amdgcn_readlane(tab, min(th, te - 1) / bs - lb0);
       const bool ok = th < te && phys >= 0;
       t.phys[h2] = ok ? phys : -1;
-      const int64_t boff = int64_t{ok ? phys : 0} * p.block_stride;
-      const uint32_t range = ok ? tile_bytes : 0u;
+      const int64_t boff = int64_t{ok ? phys : 0} * p.block_stride + (th & bmask) * D;
+      const uint32_t range = ok ? static_cast<uint32_t>(min(16, te - th) * D * 2) : 0u;
       const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
           const_cast<uint16_t*>(kbase + boff), 0, range, 0x00020000);
       const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
           const_cast<uint16_t*>(vbase + boff), 0, range, 0x00020000);
-      const int sbase = (th & bmask) * D * 2;
 #pragma unroll
       for (int c = 0; c < NC; ++c)
         t.k[h2][c] = __builtin_bit_cast(
-            uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, koff + c * 64, sbase, 0));
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, koff + c * 64, 0, kKvLoadAux));
 #pragma unroll
-      for (int j = 0; j < PV_J; ++j)
-        t.v[h2][j] = __builtin_bit_cast(
-            uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, voff + j * PV_TPI * D * 2, sbase, 0));
+      for (int j = 0; j < VJ; ++j)
+        t.v[h2][j] = __builtin_amdgcn_raw_buffer_load_b32(rv, voff + j * VT * D * 2, 0, kKvLoadAux);
     }
   };
 
-  T bufA, bufB;
-  load(bufA, tb);  // first tile in flight while Q is split
+  T bufA, bufB, bufC;
+  load(bufA, tb);  // first tiles in flight while Q is split
+  if constexpr (NBUF == 3) load(bufB, tb + TT);
 
   // Q as MFMA A operands: q = hi + lo, both bf16 (round-to-nearest-even
   // narrowing, branch-free); padding virtual heads are zero.
@@ -167,18 +181,20 @@ __global__ __launch_bounds__(64) void DecodeMfmaBf16(DecodeParams p) {
       qa_hi[c][i] = hb;
       qa_lo[c][i] = static_cast<__bf16>(xv - static_cast<float>(hb));
     }
+    if constexpr (QL) {
+      q_lds[(2 * c) * 64 + lane] = __builtin_bit_cast(uint4, qa_hi[c]);
+      q_lds[(2 * c + 1) * 64 + lane] = __builtin_bit_cast(uint4, qa_lo[c]);
+    }
   }
 
-  float m[4], lsum[4], o[GV][8];
+  float m[4], lsum[4], o[GV][2];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     m[i] = -INFINITY;
     lsum[i] = 0.f;
   }
 #pragma unroll
-  for (int h = 0; h < GV; ++h)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[h][e] = 0.f;
+  for (int h = 0; h < GV; ++h) o[h][0] = o[h][1] = 0.f;
 
   auto process = [&](const T& t, int t0) {
     f32x4_t acc[TH];
@@ -188,8 +204,10 @@ __global__ __launch_bounds__(64) void DecodeMfmaBf16(DecodeParams p) {
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         const bf16x8_t kb = AsBf16x8(t.k[h2][c]);
-        acc[h2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa_hi[c], kb, acc[h2], 0, 0, 0);
-        acc[h2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa_lo[c], kb, acc[h2], 0, 0, 0);
+        const bf16x8_t qh = QL ? AsBf16x8(q_lds[(2 * c) * 64 + lane]) : qa_hi[c];
+        const bf16x8_t ql = QL ? AsBf16x8(q_lds[(2 * c + 1) * 64 + lane]) : qa_lo[c];
+        acc[h2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qh, kb, acc[h2], 0, 0, 0);
+        acc[h2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ql, kb, acc[h2], 0, 0, 0);
       }
     }
     float s[TH][4];
@@ -229,23 +247,17 @@ __global__ __launch_bounds__(64) void DecodeMfmaBf16(DecodeParams p) {
     for (int h = 0; h < GV; ++h) {
       if (h / G >= nrows) break;
       const float a = ReadLane(alpha[h & 3], 16 * (h >> 2));
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[h][e] *= a;
+      o[h][0] *= a;
+      o[h][1] *= a;
     }
-    const bool partial = t0 + TT > te;
 #pragma unroll
     for (int h2 = 0; h2 < TH; ++h2) {
       if (t.phys[h2] < 0) continue;
 #pragma unroll
-      for (int j = 0; j < PV_J; ++j) {
-        const int tt = 16 * h2 + j * PV_TPI + pv_t;
-        const uint4 r = t.v[h2][j];
-        float vf[8] = {Bf16Lo(r.x), Bf16Hi(r.x), Bf16Lo(r.y), Bf16Hi(r.y),
-                       Bf16Lo(r.z), Bf16Hi(r.z), Bf16Lo(r.w), Bf16Hi(r.w)};
-        if (partial && t0 + tt >= te) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) vf[e] = 0.f;  // stale rows never reach the sum
-        }
+      for (int j = 0; j < VJ; ++j) {
+        const int tt = 16 * h2 + j * VT + tv;
+        const uint32_t r = t.v[h2][j];
+        const float v0 = Bf16Lo(r), v1 = Bf16Hi(r);
         float pv[HP];
 #pragma unroll
         for (int r4 = 0; r4 < HR; ++r4) {
@@ -259,32 +271,54 @@ __global__ __launch_bounds__(64) void DecodeMfmaBf16(DecodeParams p) {
         for (int rr = 0; rr < RMAX; ++rr) {
           if (rr >= nrows) break;
 #pragma unroll
-          for (int h = rr * G; h < (rr + 1) * G; ++h)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) o[h][e] = fmaf(pv[h], vf[e], o[h][e]);
+          for (int h = rr * G; h < (rr + 1) * G; ++h) {
+            o[h][0] = fmaf(pv[h], v0, o[h][0]);
+            o[h][1] = fmaf(pv[h], v1, o[h][1]);
+          }
         }
+        // Keep the broadcast probability reads next to their use: hoisting
+        // a whole tile's worth would cost 8·GV registers per token.
+        if ((j & 3) == 3) __builtin_amdgcn_sched_barrier(0);
       }
     }
     __syncthreads();  // p_lds is rewritten by the next tile
   };
 
   // A work item's range is never empty (tb < te), so the loop has no entry
-  // test for the compiler to sink the Q loads behind.
-  for (int t0 = tb;; t0 += 2 * TT) {
-    load(bufB, t0 + TT);
-    process(bufA, t0);
-    if (t0 + TT >= te) break;
-    load(bufA, t0 + 2 * TT);
-    process(bufB, t0 + TT);
-    if (t0 + 2 * TT >= te) break;
+  // test for the compiler to sink the Q loads behind. NBUF - 1 tiles are in
+  // flight while one is computed; loads past the range are empty.
+  if constexpr (NBUF == 2) {
+    for (int t0 = tb;; t0 += 2 * TT) {
+      load(bufB, t0 + TT);
+      process(bufA, t0);
+      if (t0 + TT >= te) break;
+      load(bufA, t0 + 2 * TT);
+      process(bufB, t0 + TT);
+      if (t0 + 2 * TT >= te) break;
+    }
+  } else {
+    for (int t0 = tb;; t0 += 3 * TT) {
+      load(bufC, t0 + 2 * TT);
+      process(bufA, t0);
+      if (t0 + TT >= te) break;
+      load(bufA, t0 + 3 * TT);
+      process(bufB, t0 + TT);
+      if (t0 + 2 * TT >= te) break;
+      load(bufB, t0 + 4 * TT);
+      process(bufC, t0 + 2 * TT);
+      if (t0 + 3 * TT >= te) break;
+    }
   }
 
   ReportRejectedBlocks(p, tab);
-  // Token-parallel partial sums -> per (virtual head, element) totals.
+  // Token-parallel partial sums (d = 64) -> per (virtual head, element) totals.
+  if constexpr (VT > 1) {
 #pragma unroll
-  for (int h = 0; h < GV; ++h)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[h][e] = SumAcross<PV_LPT>(o[h][e]);
+    for (int h = 0; h < GV; ++h) {
+      o[h][0] = SumAcross<VLPT>(o[h][0]);
+      o[h][1] = SumAcross<VLPT>(o[h][1]);
+    }
+  }
   float lrow[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) lrow[i] = SumGroup16(lsum[i]);
@@ -295,29 +329,24 @@ __global__ __launch_bounds__(64) void DecodeMfmaBf16(DecodeParams p) {
     const int row = it.rows[rr];
     const RowDesc rd = p.rows[row];
     if (rd.nsplit == 1) {
-      if (lane < PV_LPT) {
-        float* op = p.out + (int64_t{row} * p.heads + int64_t{hk} * G) * D + pv_e;
+      if (lane < VLPT) {
+        float* op = p.out + (int64_t{row} * p.heads + int64_t{hk} * G) * D + ev;
 #pragma unroll
         for (int h = 0; h < G; ++h) {
           const int v = rr * G + h;
           const float inv = 1.0f / ReadLane(lrow[v & 3], 16 * (v >> 2));
-          *reinterpret_cast<float4*>(op + h * D) =
-              make_float4(o[v][0] * inv, o[v][1] * inv, o[v][2] * inv, o[v][3] * inv);
-          *reinterpret_cast<float4*>(op + h * D + 4) =
-              make_float4(o[v][4] * inv, o[v][5] * inv, o[v][6] * inv, o[v][7] * inv);
+          *reinterpret_cast<float2*>(op + h * D) = make_float2(o[v][0] * inv, o[v][1] * inv);
         }
       }
       continue;
     }
     const int64_t pidx = PartialIndex(rd, p.kv_heads, hk, it.split);
-    if (lane < PV_LPT) {
-      float* po = p.part_o + pidx * G * D + pv_e;
+    if (lane < VLPT) {
+      float* po = p.part_o + pidx * G * D + ev;
 #pragma unroll
       for (int h = 0; h < G; ++h) {
         const int v = rr * G + h;
-        *reinterpret_cast<float4*>(po + h * D) = make_float4(o[v][0], o[v][1], o[v][2], o[v][3]);
-        *reinterpret_cast<float4*>(po + h * D + 4) =
-            make_float4(o[v][4], o[v][5], o[v][6], o[v][7]);
+        *reinterpret_cast<float2*>(po + h * D) = make_float2(o[v][0], o[v][1]);
       }
     }
 #pragma unroll
@@ -334,12 +363,21 @@ __global__ __launch_bounds__(64) void DecodeMfmaBf16(DecodeParams p) {
 }
 
 template <int D, int G, int RMAX>
-void LaunchShape(const DecodeParams& p, hipStream_t stream, bool wide) {
+void LaunchShape(const DecodeParams& p, hipStream_t stream, bool wide, bool deep) {
+  // Two wavefronts per SIMD wherever the shape fits 256 registers without
+  // spilling (the 16-virtual-head and triple-buffered 128-wide shapes do not).
+  constexpr bool QL = D * G * RMAX >= 1024;
+  constexpr int OCC = (D == 128 && G * RMAX >= 16) ? 1 : 2;
+  constexpr int OCC3 = D == 128 ? 1 : 2;
   const dim3 grid(p.n_items), block(64);
-  if (wide)
-    hipLaunchKernelGGL((DecodeMfmaBf16<D, G, RMAX, 2>), grid, block, 0, stream, p);
+  if (wide && deep)
+    hipLaunchKernelGGL((DecodeMfmaBf16<D, G, RMAX, 2, 3, QL, OCC3>), grid, block, 0, stream, p);
+  else if (wide)
+    hipLaunchKernelGGL((DecodeMfmaBf16<D, G, RMAX, 2, 2, QL, OCC>), grid, block, 0, stream, p);
+  else if (deep)
+    hipLaunchKernelGGL((DecodeMfmaBf16<D, G, RMAX, 1, 3, QL, OCC3>), grid, block, 0, stream, p);
   else
-    hipLaunchKernelGGL((DecodeMfmaBf16<D, G, RMAX, 1>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((DecodeMfmaBf16<D, G, RMAX, 1, 2, QL, OCC>), grid, block, 0, stream, p);
 }
 
 }  // namespace
@@ -355,13 +393,16 @@ bool LaunchDecodeMfma(const DecodeParams& p, hipStream_t stream, hipError_t* err
   // on C4; EHIP_DECODE_TILE=16 selects one half per tile (fewer registers).
   const char* tile = std::getenv("EHIP_DECODE_TILE");
   const bool wide = !(tile && std::strcmp(tile, "16") == 0);
+  // EHIP_DECODE_BUFS=3: three tiles in registers (two in flight).
+  const char* bufs = std::getenv("EHIP_DECODE_BUFS");
+  const bool deep = bufs && std::strcmp(bufs, "3") == 0;
   const bool joint = p.n_joint > 0;
 #define EHIP_MFMA_CASE(DD, GG)                          \
   if (p.d == DD && p.group == GG) {                     \
     if (joint)                                          \
-      LaunchShape<DD, GG, 2>(p, stream, wide);          \
+      LaunchShape<DD, GG, 2>(p, stream, wide, deep);    \
     else                                                \
-      LaunchShape<DD, GG, 1>(p, stream, wide);          \
+      LaunchShape<DD, GG, 1>(p, stream, wide, deep);    \
     *err = hipGetLastError();                           \
     return true;                                        \
   }
