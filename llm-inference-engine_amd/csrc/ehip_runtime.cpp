@@ -44,6 +44,7 @@ struct ehip_ctx {
   const ehip::PrefillItem* d_prefill = nullptr;
   const int32_t* d_table = nullptr;
   const int64_t* d_slots = nullptr;
+  const int32_t* d_merge_rows = nullptr;
 };
 
 namespace {
@@ -106,8 +107,9 @@ int UploadPlan(ehip_ctx* ctx, const ehip_geometry& g, Plan&& plan, const int32_t
   const size_t prefill_b = Align256(plan.prefill.size() * sizeof(ehip::PrefillItem));
   const size_t table_b = Align256(plan.table_ids.size() * sizeof(int32_t));
   const size_t slots_b = Align256(plan.slots.size() * sizeof(int64_t));
+  const size_t merge_b = Align256(plan.merge_rows.size() * sizeof(int32_t));
   const size_t total =
-      std::max<size_t>(256, rows_b + items_b + prefill_b + table_b + slots_b);
+      std::max<size_t>(256, rows_b + items_b + prefill_b + table_b + slots_b + merge_b);
 
   const int cur = ctx->stage_cur;
   ctx->stage_cur ^= 1;
@@ -139,6 +141,8 @@ int UploadPlan(ehip_ctx* ctx, const ehip_geometry& g, Plan&& plan, const int32_t
               plan.table_ids.size() * sizeof(int32_t));
   std::memcpy(h + rows_b + items_b + prefill_b + table_b, plan.slots.data(),
               plan.slots.size() * sizeof(int64_t));
+  std::memcpy(h + rows_b + items_b + prefill_b + table_b + slots_b, plan.merge_rows.data(),
+              plan.merge_rows.size() * sizeof(int32_t));
   EHIP_HIP(ctx, hipMemcpyAsync(ctx->d_desc, h, total, hipMemcpyHostToDevice, ctx->stream));
   if (!ctx->stage_done[cur]) EHIP_HIP(ctx, hipEventCreateWithFlags(&ctx->stage_done[cur],
                                                                    hipEventDisableTiming));
@@ -152,6 +156,8 @@ int UploadPlan(ehip_ctx* ctx, const ehip_geometry& g, Plan&& plan, const int32_t
                      ? d_user_table
                      : reinterpret_cast<const int32_t*>(d + rows_b + items_b + prefill_b);
   ctx->d_slots = reinterpret_cast<const int64_t*>(d + rows_b + items_b + prefill_b + table_b);
+  ctx->d_merge_rows =
+      reinterpret_cast<const int32_t*>(d + rows_b + items_b + prefill_b + table_b + slots_b);
   if (int rc = EnsureWorkspace(ctx, g, plan)) return rc;
   ctx->geom = g;
   ctx->plan = std::move(plan);
@@ -212,7 +218,8 @@ int LaunchAttention(ehip_ctx* ctx, const float* q, const void* k_slab, const voi
   p.slab_blocks = g.slab_blocks;
   p.n_items = static_cast<int32_t>(plan.items.size());
   p.n_rows = static_cast<int32_t>(plan.rows.size());
-  p.need_merge = plan.any_split;
+  p.merge_rows = ctx->d_merge_rows;
+  p.n_merge = static_cast<int32_t>(plan.merge_rows.size());
   p.n_joint = static_cast<int32_t>(plan.joint_items);
   p.heads = g.heads;
   p.kv_heads = g.kv_heads;

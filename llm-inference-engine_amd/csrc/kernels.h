@@ -31,7 +31,8 @@ struct DecodeParams {
   int64_t slab_blocks;
   int32_t n_items;
   int32_t n_rows;
-  int32_t need_merge;       // some row has more than one split
+  const int32_t* merge_rows;  // [n_merge] rows with more than one split
+  int32_t n_merge;
   int32_t n_joint;          // joint work items in the plan
   int32_t heads;
   int32_t kv_heads;

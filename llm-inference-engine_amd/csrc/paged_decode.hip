@@ -108,8 +108,9 @@ __device__ __forceinline__ void DecodeValuRow(const DecodeParams& p, int row, in
 
   const int lb0 = tb / bs;
   const int tab = LoadRangeTable(p, table_off, tb, te, lane);
-  const KV* kbase = static_cast<const KV*>(p.k_slab) + int64_t{hk} * bs * D + sub * EPV;
-  const KV* vbase = static_cast<const KV*>(p.v_slab) + int64_t{hk} * bs * D + sub * EPV;
+  const KV* kbase = static_cast<const KV*>(p.k_slab) + int64_t{hk} * bs * D;
+  const KV* vbase = static_cast<const KV*>(p.v_slab) + int64_t{hk} * bs * D;
+  const int lane_off = (tl * D + sub * EPV) * static_cast<int>(sizeof(KV));
 
   float m[G], l[G], o[G][E];
 #pragma unroll
@@ -125,18 +126,27 @@ __device__ __forceinline__ void DecodeValuRow(const DecodeParams& p, int row, in
     int phys[ROWS];
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
-      const int j0 = t0 + r * TPR;  // wavefront-uniform; the row lies in one block
-      phys[r] = j0 < te ? __builtin_amdgcn_readlane(tab, j0 / bs - lb0) : -1;
-      if (phys[r] >= 0) {
-        const int64_t off = int64_t{phys[r]} * p.block_stride + int64_t{(j0 + tl) % bs} * D;
+      // One buffer descriptor per wavefront row of TPR tokens (they lie in
+      // one block): it starts at the row group's first token and covers
+      // only tokens inside the range, so tokens past the range end read as
+      // zeros and a row group past the end (or on a rejected block id) reads
+      // nothing at all. Loads are non-temporal: every tile streams once.
+      const int j0 = t0 + r * TPR;  // wavefront-uniform
+      const int ph = __builtin_amdgcn_readlane(tab, min(j0, te - 1) / bs - lb0);
+      const bool ok = j0 < te && ph >= 0;
+      phys[r] = ok ? ph : -1;
+      const int64_t off = int64_t{ok ? ph : 0} * p.block_stride + int64_t{j0 & (bs - 1)} * D;
+      const uint32_t range =
+          ok ? static_cast<uint32_t>(min(TPR, te - j0) * D * static_cast<int>(sizeof(KV))) : 0u;
+      const __amdgpu_buffer_rsrc_t rk =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<KV*>(kbase + off), 0, range, 0x00020000);
+      const __amdgpu_buffer_rsrc_t rv =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<KV*>(vbase + off), 0, range, 0x00020000);
 #pragma unroll
-        for (int v = 0; v < NV; ++v) {
-          kr[r][v] = *reinterpret_cast<const uint4*>(kbase + off + v * VSPAN);
-          vr[r][v] = *reinterpret_cast<const uint4*>(vbase + off + v * VSPAN);
-        }
-      } else {
-#pragma unroll
-        for (int v = 0; v < NV; ++v) kr[r][v] = vr[r][v] = make_uint4(0, 0, 0, 0);
+      for (int v = 0; v < NV; ++v) {
+        const int vo = lane_off + v * VSPAN * static_cast<int>(sizeof(KV));
+        kr[r][v] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, vo, 0, kKvLoadAux));
+        vr[r][v] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, vo, 0, kKvLoadAux));
       }
     }
     const bool partial = t0 + 32 > te;
@@ -182,13 +192,9 @@ __device__ __forceinline__ void DecodeValuRow(const DecodeParams& p, int row, in
 
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
-      float vf[E];
+      float vf[E];  // rows past the range end were read as zeros
 #pragma unroll
       for (int v = 0; v < NV; ++v) Widen<KV>(vr[r][v], vf + v * EPV);
-      if (partial && t0 + r * TPR + tl >= te) {
-#pragma unroll
-        for (int e = 0; e < E; ++e) vf[e] = 0.f;  // never let a stale row reach the sum
-      }
 #pragma unroll
       for (int h = 0; h < G; ++h)
 #pragma unroll
@@ -362,11 +368,12 @@ __global__ __launch_bounds__(kMergeThreads) void MergeSplitsKernel(DecodeParams 
   __shared__ float2 ml[kMergeMaxPairs];
   const int64_t grp = blockIdx.x / chunks;
   const int chunk = static_cast<int>(blockIdx.x - grp * chunks);
-  const int row = static_cast<int>(grp / p.kv_heads);
-  const int hk = static_cast<int>(grp - int64_t{row} * p.kv_heads);
+  const int mi = static_cast<int>(grp / p.kv_heads);
+  const int hk = static_cast<int>(grp - int64_t{mi} * p.kv_heads);
+  const int row = p.merge_rows[mi];
   const RowDesc rd = p.rows[row];
   const int nsplit = rd.nsplit;
-  if (nsplit <= 1) return;  // written directly (1) or a prefill-kernel row (0)
+  if (nsplit <= 1) return;  // merge_rows holds split rows only
   const int64_t pbase = PartialIndex(rd, p.kv_heads, hk, 0);
   const int g = p.group, d = p.d;
   const int npairs = nsplit * g;
@@ -457,8 +464,10 @@ hipError_t LaunchSplits(const DecodeParams& p, int kv_dtype, hipStream_t stream)
 hipError_t LaunchDecode(const DecodeParams& p, int kv_dtype, hipStream_t stream) {
   if (p.n_items == 0) return hipSuccess;
   hipError_t e = LaunchSplits(p, kv_dtype, stream);
-  if (e != hipSuccess || !p.need_merge) return e;
-  const int64_t groups = int64_t{p.n_rows} * p.kv_heads;
+  if (e != hipSuccess || p.n_merge == 0) return e;
+  // Only the rows that were split: a step dominated by prefill-chunk rows
+  // (which need no merge) launches no idle merge blocks.
+  const int64_t groups = int64_t{p.n_merge} * p.kv_heads;
   const int chunks = (p.group * p.d + kMergeThreads - 1) / kMergeThreads;
   hipLaunchKernelGGL(MergeSplitsKernel, dim3(groups * chunks), dim3(kMergeThreads), 0, stream, p,
                      chunks);

@@ -45,10 +45,6 @@ typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 
 __device__ __forceinline__ bf16x8_t AsBf16x8(uint4 u) { return __builtin_bit_cast(bf16x8_t, u); }
 
-// Cache policy of the K/V tile loads: non-temporal (nt) at system coherence
-// scope (sc1). Every tile is streamed once per launch; the streaming policy
-// raised a measured gather of this pattern from 5.98 to 6.52 TB/s on MI355X.
-constexpr int kKvLoadAux = 2 | 16;
 
 __device__ __forceinline__ float ReadLane(float x, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));

@@ -153,6 +153,7 @@ void FinishPlan(const ehip_geometry& g, Plan* plan, bool allow_joint,
 
   int64_t split_base = 0;
   plan->any_split = false;
+  plan->merge_rows.clear();
   for (size_t r = 0; r < n; ++r) {
     RowDesc& rd = plan->rows[r];
     const int32_t sl = split_len[r], P = joint_len[r];
@@ -160,6 +161,7 @@ void FinishPlan(const ehip_geometry& g, Plan* plan, bool allow_joint,
     rd.split_base = static_cast<int32_t>(split_base);
     split_base += rd.nsplit;
     plan->any_split = plan->any_split || rd.nsplit > 1;
+    if (rd.nsplit > 1) plan->merge_rows.push_back(static_cast<int32_t>(r));
   }
   plan->partials = split_base * g.kv_heads;
 

@@ -82,6 +82,7 @@ struct Plan {
   std::vector<int32_t> groups;      // [n_groups * kMaxJointRows] member rows (host side)
   std::vector<int32_t> table_ids;   // CSR ids, copied
   std::vector<int64_t> slots;       // slot mapping of appended tokens (may be empty)
+  std::vector<int32_t> merge_rows;  // rows with more than one split, ascending
   int64_t partials = 0;             // sum over rows of nsplit * Hkv
   int32_t split_tokens = 0;         // base split length chosen for this step
   int64_t joint_items = 0;
