@@ -559,10 +559,10 @@ int ehip_step_upload(ehip_ctx* ctx, const ehip_geometry* geom, const ehip_step_d
   if (!geom || !step) return SetError(ctx, EHIP_INVALID_ARGUMENT, "null geometry or step");
   Plan plan;
   std::string err;
-  const bool prefill_ok = ehip::PrefillSupported(geom->kv_dtype, geom->head_dim,
-                                                 geom->kv_heads > 0 ? geom->heads / geom->kv_heads : 0,
-                                                 geom->block_size);
-  if (int rc = ehip::BuildPlan(*geom, *step, &plan, &err, prefill_ok))
+  const int prefill_rows = ehip::PrefillRowsPerItem(
+      geom->kv_dtype, geom->head_dim, geom->kv_heads > 0 ? geom->heads / geom->kv_heads : 0,
+      geom->block_size);
+  if (int rc = ehip::BuildPlan(*geom, *step, &plan, &err, prefill_rows))
     return SetError(ctx, rc, "%s", err.c_str());
   return UploadPlan(ctx, *geom, std::move(plan), nullptr);
 }

@@ -61,10 +61,12 @@ struct PrefillParams {
 };
 
 // Causal prefill chunks on MFMA (bf16 K/V, d = 128, g in {4, 8}, bs >= 16):
-// one 4-wavefront workgroup per (chunk, kv head, 16 query rows). Returns
+// one 4-wavefront workgroup per (chunk, kv head, M query rows). Returns
 // false (nothing launched) for shapes it does not cover.
 bool LaunchPrefillMfma(const PrefillParams& p, hipStream_t stream, hipError_t* err);
-bool PrefillSupported(int kv_dtype, int d, int group, int bs);
+// Query rows per prefill work item for this geometry, or 0 when the MFMA
+// prefill kernel does not cover it (bf16 K/V, d = 128, g in {4, 8}, bs >= 16).
+int PrefillRowsPerItem(int kv_dtype, int d, int group, int bs);
 
 // Launch the decode kernel family for the given plan (one wavefront per work
 // item; picks the specialised (dtype, d, g) kernel or the generic one), then,

@@ -9,10 +9,14 @@
 // sequence's K/V into a contiguous copy first (src/kvcache/paged_gather.cpp:16-49);
 // here K/V are read through the block table directly.
 //
-// Work: one workgroup of 4 wavefronts per (sequence, kv head, 16 query rows);
-// wavefront w owns query heads hk*g + w*HPW .. +HPW (HPW = g / 4) of those
-// rows. Keys stream in 32-token tiles staged in LDS (double-buffered, loaded
-// one tile ahead into registers):
+// Work: one workgroup of 4 wavefronts per (sequence, kv head, M query rows);
+// wavefront w owns 16 of those rows for 4 of the kv head's g query heads
+// (g = 4: M = 64, the wavefronts take rows 16w..; g = 8: M = 32, two row
+// groups x two head groups). Each wavefront keeps 4 (row block, head)
+// accumulator blocks, so every K and V operand read from LDS feeds four
+// MFMAs and every 16 KiB K/V tile staged in LDS serves 4M (row, head) pairs.
+// Keys stream in 32-token tiles staged in LDS (double-buffered, loaded one
+// tile ahead into registers):
 //   - K row-major [token][d], rows padded by 16 bytes, so the MFMA A operand
 //     (16 tokens x 8 elements per lane) is one conflict-free 16-byte read;
 //   - V transposed [d][token'], token' a permutation that puts the 8 tokens a
@@ -22,7 +26,9 @@
 // scores of tokens 4*(l/16) + i of each 16-token half for query row l % 16,
 // which is exactly the A-operand layout P needs for O = P V once the two
 // halves' token order is folded into the V permutation. The online softmax
-// (max/sum per row) runs in fp32 across the 4 lanes that share a row.
+// (max/sum per row) runs in fp32 across the 4 lanes that share a row; the
+// output rescale is skipped for a tile in which no row's running max moved.
+#include <climits>
 #include <cstdlib>
 
 #include "device_util.h"
@@ -34,9 +40,22 @@ namespace {
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 
-constexpr int kQRows = 16;   // query rows per workgroup
 constexpr int kTile = 32;    // keys per tile
+constexpr float kRefSlack = 8.f;
 constexpr int kWaves = 4;
+
+// Query rows per workgroup for group size g when each wavefront keeps hb
+// (head) accumulator blocks of 16 rows: 4 wavefronts over g / hb head groups.
+constexpr int PrefillRows(int g, int hb) { return 16 * (kWaves / (g / hb)); }
+
+// Accumulator blocks per wavefront (EHIP_PREFILL_HB=2|4 selects; 2 default).
+int PrefillHeadsPerWave() {
+  static const int hb = [] {
+    const char* e = std::getenv("EHIP_PREFILL_HB");
+    return e && e[0] == '4' ? 4 : 2;
+  }();
+  return hb;
+}
 
 __device__ __forceinline__ float ShflF(float x, int src_lane) {
   return __int_as_float(__builtin_amdgcn_ds_bpermute(src_lane << 2, __float_as_int(x)));
@@ -56,15 +75,25 @@ struct PrefillSmem {
   static constexpr int KBYTES = kTile * KROW;
   static constexpr int VBYTES = D * VROW;
   static constexpr int BYTES = 2 * (KBYTES + VBYTES);  // double-buffered
+  // Q^T operands of every wavefront (when kept in LDS):
+  // [wave][head][chunk][lane] x 16 bytes.
+  static constexpr int QBYTES = kWaves * 4 * (D / 32) * 64 * 16;
+  static constexpr int TOTAL = BYTES + QBYTES;
 };
 
-template <int D, int G>
+template <int D, int G, int HB>
 __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) {
-  constexpr int HPW = G / kWaves;     // query heads per wavefront
+  // HB: heads (accumulator blocks) per wavefront. Q operands stay in
+  // registers for HB = 2 and move to LDS for HB = 4 (register pressure).
+  constexpr bool QL = HB > 2;
+  constexpr int NHG = G / HB;         // head groups
+  constexpr int RG = kWaves / NHG;    // 16-row groups per workgroup
+  constexpr int M = 16 * RG;          // query rows per workgroup
   constexpr int NC = D / 32;          // MFMA k-chunks over head_dim (QK^T)
   constexpr int NB = D / 16;          // 16-wide output column blocks (PV)
   using SM = PrefillSmem<D>;
-  static_assert(G % kWaves == 0 && HPW >= 1, "g must be a multiple of 4");
+  static_assert(G % HB == 0 && NHG >= 1 && kWaves % NHG == 0, "g must be 4 or 8");
+  static_assert(M == PrefillRows(G, HB), "rows per workgroup");
   // Per thread per tile: 2 x 16-byte K loads and 2 x 16-byte V loads.
   constexpr int KV_VECS = kTile * D / 8;  // 16-byte vectors per tile (K or V)
   static_assert(KV_VECS == 2 * kWaves * 64, "tile / block shape");
@@ -75,33 +104,44 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
   const int wave = tid >> 6;
   const int n = lane & 15;
   const int kq = lane >> 4;
+  const int rg = wave % RG;   // this wavefront's 16-row group
+  const int hgi = wave / RG;  // and head group
 
   const PrefillItem it = p.items[blockIdx.x];
   const int hk = it.kv_head;
   const int P = it.past;       // cached keys before the chunk
   const int T = it.chunk;      // chunk rows
-  const int q0 = it.q0;        // first chunk row of this block
+  const int q0 = it.q0;        // first chunk row of this workgroup
   const int bs = p.bs;
-  const int qn = min(kQRows, T - q0);        // live query rows of this block
+  const int qn = min(M, T - q0);             // live query rows of the workgroup
   const int kend = P + q0 + qn;              // keys [0, kend) are attended by some row
-  const int kdiag = P + q0;                  // keys < kdiag are seen by every row
+  const int r0 = q0 + 16 * rg;               // this wavefront's first row
+  const int qnw = min(16, max(0, T - r0));   // its live rows (0: nothing to compute)
+  const int wend = P + r0 + qnw;             // keys this wavefront's rows attend
 
   // Q^T as MFMA B operands (bf16, round-to-nearest-even): lane l holds
-  // Q[row q0 + l%16][c*32 + 8*kq .. +8] for each of its heads.
-  bf16x8_t qb[HPW][NC];
+  // Q[row r0 + l%16][c*32 + 8*kq .. +8] for each of its heads. They are kept
+  // in LDS (each is read once per tile) rather than in 64 registers.
+  uint4* qlds = reinterpret_cast<uint4*>(smem + SM::BYTES) + wave * HB * NC * 64;
+  bf16x8_t qreg[QL ? 1 : HB][NC];
   {
-    const int qr = q0 + min(n, qn - 1);
+    const int qr = r0 + min(n, max(qnw, 1) - 1);
 #pragma unroll
-    for (int hh = 0; hh < HPW; ++hh) {
-      const int head = hk * G + wave * HPW + hh;
-      const float* qp = p.q + (int64_t{it.row_base + qr} * p.heads + head) * D + kq * 8;
+    for (int hh = 0; hh < HB; ++hh) {
+      const int head = hk * G + hgi * HB + hh;
+      const float* qp = p.q + (int64_t{it.row_base + min(qr, T - 1)} * p.heads + head) * D + kq * 8;
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         const float4 a = *reinterpret_cast<const float4*>(qp + c * 32);
         const float4 b = *reinterpret_cast<const float4*>(qp + c * 32 + 4);
         const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        bf16x8_t qv;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) qb[hh][c][i] = static_cast<__bf16>(x[i]);
+        for (int i = 0; i < 8; ++i) qv[i] = static_cast<__bf16>(x[i]);
+        if constexpr (QL)
+          qlds[(hh * NC + c) * 64 + lane] = __builtin_bit_cast(uint4, qv);
+        else
+          qreg[QL ? 0 : hh][c] = qv;
       }
     }
   }
@@ -117,38 +157,45 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
   // V token pair vp = tid % 16 (tokens 2vp, 2vp + 1), group tid / 16.
   const int tk0 = tid / EG, tk1 = (tid + kWaves * 64) / EG, ek = tid % EG;
   const int vp = tid % 16, ev = tid / 16;
+  // bs is a power of two: block index and slot by shift and mask.
+  const int bsh = __builtin_ctz(bs), bmask = bs - 1;
+  const int32_t* tab = p.table + it.table_off;
+  const uint32_t nblk = static_cast<uint32_t>(p.slab_blocks);
 #define EHIP_PF_GLOAD(K0)                                                                    \
   do {                                                                                      \
     const int pk0 = min((K0) + tk0, kend - 1), pk1 = min((K0) + tk1, kend - 1);             \
     const int pv0 = min((K0) + 2 * vp, kend - 1), pv1 = min((K0) + 2 * vp + 1, kend - 1);    \
-    int b0 = p.table[it.table_off + pk0 / bs], b1 = p.table[it.table_off + pk1 / bs];         \
-    int b2 = p.table[it.table_off + pv0 / bs], b3 = p.table[it.table_off + pv1 / bs];         \
-    if (b0 < 0 || b0 >= p.slab_blocks) { bad = true; b0 = 0; }                               \
-    if (b1 < 0 || b1 >= p.slab_blocks) { bad = true; b1 = 0; }                               \
-    if (b2 < 0 || b2 >= p.slab_blocks) { bad = true; b2 = 0; }                               \
-    if (b3 < 0 || b3 >= p.slab_blocks) { bad = true; b3 = 0; }                               \
+    int b0 = tab[pk0 >> bsh], b1 = tab[pk1 >> bsh];                                          \
+    int b2 = tab[pv0 >> bsh], b3 = tab[pv1 >> bsh];                                          \
+    const bool ok0 = static_cast<uint32_t>(b0) < nblk, ok1 = static_cast<uint32_t>(b1) < nblk; \
+    const bool ok2 = static_cast<uint32_t>(b2) < nblk, ok3 = static_cast<uint32_t>(b3) < nblk; \
+    bad = bad | !(ok0 & ok1 & ok2 & ok3);                                                    \
+    b0 = ok0 ? b0 : 0;                                                                       \
+    b1 = ok1 ? b1 : 0;                                                                       \
+    b2 = ok2 ? b2 : 0;                                                                       \
+    b3 = ok3 ? b3 : 0;                                                                       \
     kr0 = *reinterpret_cast<const uint4*>(kslab + int64_t{b0} * p.block_stride +             \
-                                          (pk0 % bs) * D + ek * 8);                          \
+                                          (pk0 & bmask) * D + ek * 8);                       \
     kr1 = *reinterpret_cast<const uint4*>(kslab + int64_t{b1} * p.block_stride +             \
-                                          (pk1 % bs) * D + ek * 8);                          \
+                                          (pk1 & bmask) * D + ek * 8);                       \
     vr0 = *reinterpret_cast<const uint4*>(vslab + int64_t{b2} * p.block_stride +             \
-                                          (pv0 % bs) * D + ev * 8);                          \
+                                          (pv0 & bmask) * D + ev * 8);                       \
     vr1 = *reinterpret_cast<const uint4*>(vslab + int64_t{b3} * p.block_stride +             \
-                                          (pv1 % bs) * D + ev * 8);                          \
+                                          (pv1 & bmask) * D + ev * 8);                       \
   } while (0)
 
   // Per head state. Scores/probabilities live in the S^T layout (row n =
   // l % 16); the output accumulators in the MFMA D layout (rows 4kq+i).
-  f32x4_t o[HPW][NB];
-  float m[HPW], l[HPW];
+  f32x4_t o[HB][NB];
+  float m[HB], l[HB];
 #pragma unroll
-  for (int hh = 0; hh < HPW; ++hh) {
+  for (int hh = 0; hh < HB; ++hh) {
     m[hh] = -INFINITY;
     l[hh] = 0.f;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) o[hh][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
-  const int qpos = P + q0 + n;  // this lane's query position (S^T layout)
+  const int qpos = P + r0 + n;  // this lane's query position (S^T layout)
 
   const int ntiles = (kend + kTile - 1) / kTile;
   const int vtp = VPerm(2 * vp);
@@ -176,64 +223,93 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
     }
     __syncthreads();
     if (tile + 1 < ntiles) EHIP_PF_GLOAD(k0 + kTile);  // next tile in flight during compute
-    const unsigned char* kb = smem + buf * (SM::KBYTES + SM::VBYTES);
-    const unsigned char* vb = kb + SM::KBYTES;
-    const bool diag = k0 + kTile > kdiag;  // some key of the tile is masked for some row
+    // Wavefront-uniform: a tile wholly past this wavefront's last row (the
+    // other row groups' diagonal) is skipped.
+    if (k0 < wend) {
+      const unsigned char* kb = smem + buf * (SM::KBYTES + SM::VBYTES);
+      const unsigned char* vb = kb + SM::KBYTES;
+      // Keys past this lane's query position (or past the workgroup's last
+      // key) are masked; only tiles reaching the diagonal mask anything.
+      const int lim = k0 + kTile > P + r0 ? min(qpos, kend - 1) : INT_MAX;
 
+      // S^T for all heads: each K operand feeds HB MFMAs, each Q operand two
+      // (the tile's halves).
+      f32x4_t s[HB][2];
 #pragma unroll
-    for (int hh = 0; hh < HPW; ++hh) {
-      f32x4_t s[2];
+      for (int hh = 0; hh < HB; ++hh) s[hh][0] = s[hh][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) {
-        s[h2] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      for (int c = 0; c < NC; ++c) {
+        bf16x8_t ka[2];
 #pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          const bf16x8_t ka = __builtin_bit_cast(
+        for (int h2 = 0; h2 < 2; ++h2)
+          ka[h2] = __builtin_bit_cast(
               bf16x8_t, *reinterpret_cast<const uint4*>(kb + (16 * h2 + n) * SM::KROW +
                                                         (c * 32 + kq * 8) * 2));
-          s[h2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[hh][c], s[h2], 0, 0, 0);
+#pragma unroll
+        for (int hh = 0; hh < HB; ++hh) {
+          const bf16x8_t qv = QL ? __builtin_bit_cast(bf16x8_t, qlds[(hh * NC + c) * 64 + lane])
+                                 : qreg[QL ? 0 : hh][c];
+#pragma unroll
+          for (int h2 = 0; h2 < 2; ++h2)
+            s[hh][h2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[h2], qv, s[hh][h2], 0, 0, 0);
         }
       }
-      // s[h2][i] = score(token k0 + 16*h2 + 4*kq + i, query row n)
-      float sv[8];
+      // s[hh][h2][i] = score(token k0 + 16*h2 + 4*kq + i, query row n)
+      bf16x8_t pa[HB];
+      float alpha[HB];
+      bool moved = false;
 #pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2)
+      for (int hh = 0; hh < HB; ++hh) {
+        float sv[8];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int kpos = k0 + 16 * h2 + 4 * kq + i;
-          const bool ok = !diag || (kpos <= qpos && kpos < kend);
-          sv[4 * h2 + i] = ok ? s[h2][i] * p.scale_log2 : -INFINITY;
+        for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int kpos = k0 + 16 * h2 + 4 * kq + i;
+            sv[4 * h2 + i] = kpos <= lim ? s[hh][h2][i] * p.scale_log2 : -INFINITY;
+          }
+        float mx = sv[0];
+#pragma unroll
+        for (int i = 1; i < 8; ++i) mx = fmaxf(mx, sv[i]);
+        mx = fmaxf(mx, ShflF(mx, lane ^ 16));
+        mx = fmaxf(mx, ShflF(mx, lane ^ 32));
+        // Lazy rescaling (FlashAttention-3, Shah et al. 2024): the running
+        // reference moves only when the tile's max exceeds it by more than
+        // kRefSlack (log2 units), so probabilities stay below 2^kRefSlack and
+        // the output rescale is skipped for most tiles; O / l is unchanged.
+        const float mn = mx > m[hh] + kRefSlack ? mx : m[hh];
+        alpha[hh] = mn == -INFINITY ? 1.f : Exp2(m[hh] - mn);
+        moved = moved || mn != m[hh];
+        m[hh] = mn;
+        float ps = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float pv = mn == -INFINITY ? 0.f : Exp2(sv[i] - mn);
+          ps += pv;
+          pa[hh][i] = static_cast<__bf16>(pv);
         }
-      float mx = sv[0];
-#pragma unroll
-      for (int i = 1; i < 8; ++i) mx = fmaxf(mx, sv[i]);
-      mx = fmaxf(mx, ShflF(mx, lane ^ 16));
-      mx = fmaxf(mx, ShflF(mx, lane ^ 32));
-      const float mn = fmaxf(m[hh], mx);
-      const float alpha = mn == -INFINITY ? 1.f : Exp2(m[hh] - mn);
-      m[hh] = mn;
-      bf16x8_t pa;
-      float ps = 0.f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float pv = mn == -INFINITY ? 0.f : Exp2(sv[i] - mn);
-        ps += pv;
-        pa[i] = static_cast<__bf16>(pv);
+        l[hh] = l[hh] * alpha[hh] + ps;  // lane-partial over this lane's tokens
       }
-      l[hh] = l[hh] * alpha + ps;  // lane-partial over this lane's tokens
       // Rescale the output rows (D layout: row 4kq+i) by their row's alpha,
-      // which lives in lanes l % 16 == row.
+      // which lives in lanes l % 16 == row; skipped when no max moved.
+      if (__any(moved)) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float ar = ShflF(alpha, 4 * kq + i);
+        for (int hh = 0; hh < HB; ++hh)
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) o[hh][nb][i] *= ar;
+          for (int i = 0; i < 4; ++i) {
+            const float ar = ShflF(alpha[hh], 4 * kq + i);
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) o[hh][nb][i] *= ar;
+          }
       }
+      // O += P V: each V operand read once, HB MFMAs.
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
         const bf16x8_t vbv = __builtin_bit_cast(
             bf16x8_t, *reinterpret_cast<const uint4*>(vb + (16 * nb + n) * SM::VROW + kq * 16));
-        o[hh][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vbv, o[hh][nb], 0, 0, 0);
+#pragma unroll
+        for (int hh = 0; hh < HB; ++hh)
+          o[hh][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[hh], vbv, o[hh][nb], 0, 0, 0);
       }
     }
   }
@@ -241,17 +317,17 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
   // Row sums: each lane holds a partial over its tokens; the 4 lanes of a
   // row (l % 16 equal) together hold the row total.
 #pragma unroll
-  for (int hh = 0; hh < HPW; ++hh) {
+  for (int hh = 0; hh < HB; ++hh) {
     float lt = l[hh];
     lt += ShflF(lt, lane ^ 16);
     lt += ShflF(lt, lane ^ 32);
-    const int head = hk * G + wave * HPW + hh;
+    const int head = hk * G + hgi * HB + hh;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 4 * kq + i;  // D-layout row of register i
       const float inv = 1.0f / ShflF(lt, r);
-      if (r < qn) {
-        float* op = p.out + (int64_t{it.row_base + q0 + r} * p.heads + head) * D + n;
+      if (r < qnw) {
+        float* op = p.out + (int64_t{it.row_base + r0 + r} * p.heads + head) * D + n;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) op[16 * nb] = o[hh][nb][i] * inv;
       }
@@ -269,12 +345,17 @@ bool LaunchPrefillMfma(const PrefillParams& p, hipStream_t stream, hipError_t* e
     return true;
   }
   const dim3 grid(p.n_items), block(kWaves * 64);
-#define EHIP_PREFILL_CASE(DD, GG)                                                        \
-  if (p.d == DD && p.group == GG) {                                                      \
-    hipLaunchKernelGGL((PrefillMfmaBf16<DD, GG>), grid, block, PrefillSmem<DD>::BYTES, \
-                       stream, p);                                                       \
-    *err = hipGetLastError();                                                            \
-    return true;                                                                         \
+  const int hb = PrefillHeadsPerWave();
+#define EHIP_PREFILL_CASE(DD, GG)                                                         \
+  if (p.d == DD && p.group == GG) {                                                       \
+    if (hb == 4)                                                                          \
+      hipLaunchKernelGGL((PrefillMfmaBf16<DD, GG, 4>), grid, block,                       \
+                         PrefillSmem<DD>::TOTAL, stream, p);                              \
+    else                                                                                  \
+      hipLaunchKernelGGL((PrefillMfmaBf16<DD, GG, 2>), grid, block, PrefillSmem<DD>::BYTES, \
+                         stream, p);                                                      \
+    *err = hipGetLastError();                                                             \
+    return true;                                                                          \
   }
   EHIP_PREFILL_CASE(128, 4)
   EHIP_PREFILL_CASE(128, 8)
@@ -282,8 +363,9 @@ bool LaunchPrefillMfma(const PrefillParams& p, hipStream_t stream, hipError_t* e
   return false;
 }
 
-bool PrefillSupported(int kv_dtype, int d, int group, int bs) {
-  return kv_dtype == EHIP_KV_BF16 && d == 128 && (group == 4 || group == 8) && bs >= 16;
+int PrefillRowsPerItem(int kv_dtype, int d, int group, int bs) {
+  if (kv_dtype != EHIP_KV_BF16 || d != 128 || (group != 4 && group != 8) || bs < 16) return 0;
+  return PrefillRows(group, PrefillHeadsPerWave());
 }
 
 }  // namespace ehip

@@ -195,7 +195,7 @@ void FinishPlan(const ehip_geometry& g, Plan* plan, bool allow_joint,
 }  // namespace
 
 int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::string* err,
-              bool prefill_ok) {
+              int prefill_rows) {
   if (int rc = ValidateGeometry(g, err)) return rc;
   if (s.num_seqs < 0) return Fail(err, EHIP_INVALID_ARGUMENT, "num_seqs=%lld < 0", s.num_seqs);
   if (s.reserved != 0) return Fail(err, EHIP_INVALID_ARGUMENT, "reserved field must be 0");
@@ -266,7 +266,7 @@ int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::
   // Chunks big enough for the MFMA prefill kernel leave the decode partition.
   std::vector<uint8_t> skip(plan->rows.size(), 0);
   const char* pf = std::getenv("EHIP_PREFILL");
-  if (prefill_ok && !(pf && pf[0] == '0')) {
+  if (prefill_rows > 0 && !(pf && pf[0] == '0')) {
     struct Block { int32_t b, q0, keys; };
     std::vector<Block> blocks;
     std::vector<int32_t> row_base(B + 1, 0);
@@ -275,7 +275,8 @@ int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::
       const int32_t T = s.h_query_lens[b];
       if (T < kMinPrefillRows) continue;
       const int32_t P = static_cast<int32_t>(s.h_context_lens[b] - T);
-      for (int32_t q0 = 0; q0 < T; q0 += 16) blocks.push_back({b, q0, P + std::min(T, q0 + 16)});
+      for (int32_t q0 = 0; q0 < T; q0 += prefill_rows)
+        blocks.push_back({b, q0, P + std::min(T, q0 + prefill_rows)});
       std::fill(skip.begin() + row_base[b], skip.begin() + row_base[b + 1], 1);
     }
     // Most keys first; kv head fastest, so the blocks of one kv head are

@@ -56,9 +56,9 @@ struct WorkItem {
   int32_t reserved1;
 };
 
-// One causal prefill block: 16 query rows q0 .. q0+15 of a chunk of `chunk`
+// One causal prefill block: query rows q0 .. q0+M-1 of a chunk of `chunk`
 // rows (starting at packed row row_base) over `past` cached keys, for the g
-// query heads of one kv head.
+// query heads of one kv head (M = PrefillRowsPerItem for the geometry).
 struct PrefillItem {
   int32_t row_base;
   int32_t chunk;
@@ -104,11 +104,12 @@ int32_t ChooseSplitTokens(const ehip_geometry& g, int64_t unit_tokens);
 
 // Validates the step (lengths, CSR offsets, every table id and slot in range)
 // and builds the plan. Chunks of at least kMinPrefillRows rows go to the MFMA
-// prefill kernel when it covers the geometry (prefill_ok; EHIP_PREFILL=0
+// prefill kernel when it covers the geometry (prefill_rows > 0: query rows
+// per prefill work item; EHIP_PREFILL=0
 // keeps every row on the decode kernels); their rows get nsplit = 0.
 constexpr int32_t kMinPrefillRows = 16;
 int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::string* err,
-              bool prefill_ok = false);
+              int prefill_rows = 0);
 
 // Plan for one row reading a device-resident table (single-sequence paged
 // decode): one row of `length` keys, table offset 0.
