@@ -151,7 +151,9 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
   const uint16_t* kslab = static_cast<const uint16_t*>(p.k_slab) + int64_t{hk} * bs * D;
   const uint16_t* vslab = static_cast<const uint16_t*>(p.v_slab) + int64_t{hk} * bs * D;
   constexpr int EG = D / 8;  // 8-element groups per row
-  uint4 kr0, kr1, vr0, vr1;  // the next tile, two 16-byte vectors of K and of V
+  // Two staging slots: each holds a later tile's two 16-byte vectors of K and
+  // of V (K0, K1, V0, V1), so global loads run two tiles ahead of compute.
+  uint4 stA0, stA1, stA2, stA3, stB0, stB1, stB2, stB3;
   bool bad = false;
   // Thread -> K vectors u = tid and tid + 256 (token u / EG, group u % EG);
   // V token pair vp = tid % 16 (tokens 2vp, 2vp + 1), group tid / 16.
@@ -161,7 +163,7 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
   const int bsh = __builtin_ctz(bs), bmask = bs - 1;
   const int32_t* tab = p.table + it.table_off;
   const uint32_t nblk = static_cast<uint32_t>(p.slab_blocks);
-#define EHIP_PF_GLOAD(K0)                                                                    \
+#define EHIP_PF_GLOAD(ST, K0)                                                                  \
   do {                                                                                      \
     const int pk0 = min((K0) + tk0, kend - 1), pk1 = min((K0) + tk1, kend - 1);             \
     const int pv0 = min((K0) + 2 * vp, kend - 1), pv1 = min((K0) + 2 * vp + 1, kend - 1);    \
@@ -174,13 +176,13 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
     b1 = ok1 ? b1 : 0;                                                                       \
     b2 = ok2 ? b2 : 0;                                                                       \
     b3 = ok3 ? b3 : 0;                                                                       \
-    kr0 = *reinterpret_cast<const uint4*>(kslab + int64_t{b0} * p.block_stride +             \
+    ST##0 = *reinterpret_cast<const uint4*>(kslab + int64_t{b0} * p.block_stride +             \
                                           (pk0 & bmask) * D + ek * 8);                       \
-    kr1 = *reinterpret_cast<const uint4*>(kslab + int64_t{b1} * p.block_stride +             \
+    ST##1 = *reinterpret_cast<const uint4*>(kslab + int64_t{b1} * p.block_stride +             \
                                           (pk1 & bmask) * D + ek * 8);                       \
-    vr0 = *reinterpret_cast<const uint4*>(vslab + int64_t{b2} * p.block_stride +             \
+    ST##2 = *reinterpret_cast<const uint4*>(vslab + int64_t{b2} * p.block_stride +             \
                                           (pv0 & bmask) * D + ev * 8);                       \
-    vr1 = *reinterpret_cast<const uint4*>(vslab + int64_t{b3} * p.block_stride +             \
+    ST##3 = *reinterpret_cast<const uint4*>(vslab + int64_t{b3} * p.block_stride +             \
                                           (pv1 & bmask) * D + ev * 8);                       \
   } while (0)
 
@@ -196,41 +198,42 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
     for (int nb = 0; nb < NB; ++nb) o[hh][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
   const int qpos = P + r0 + n;  // this lane's query position (S^T layout)
+  const float sl2 = p.scale_log2;          // scores -> log2 domain
+  const float slack = kRefSlack / sl2;     // the rescale slack in raw score units
 
   const int ntiles = (kend + kTile - 1) / kTile;
   const int vtp = VPerm(2 * vp);
-  EHIP_PF_GLOAD(0);
-  for (int tile = 0; tile < ntiles; ++tile) {
-    const int buf = tile & 1;
+  // Writes a staged tile into LDS buffer BUF: K row-major; V packed into
+  // (t, t+1) dwords (lo: element 2w, hi: element 2w + 1 of the pair) and
+  // written transposed, V^T[e][perm(t)], with perm(2vp + 1) = perm(2vp) + 1.
+#define EHIP_PF_STORE(ST, BUF)                                                     \
+  do {                                                                           \
+    unsigned char* kw = smem + (BUF) * (SM::KBYTES + SM::VBYTES);                 \
+    unsigned char* vw = kw + SM::KBYTES;                                          \
+    *reinterpret_cast<uint4*>(kw + tk0 * SM::KROW + ek * 16) = ST##0;             \
+    *reinterpret_cast<uint4*>(kw + tk1 * SM::KROW + ek * 16) = ST##1;             \
+    const uint4 va = ST##2, vb2 = ST##3;                                          \
+    const uint32_t a[4] = {va.x, va.y, va.z, va.w};                               \
+    const uint32_t b[4] = {vb2.x, vb2.y, vb2.z, vb2.w};                           \
+    _Pragma("unroll") for (int w = 0; w < 4; ++w) {                               \
+      const uint32_t lo = (a[w] & 0xFFFFu) | (b[w] << 16);                        \
+      const uint32_t hi = (a[w] >> 16) | (b[w] & 0xFFFF0000u);                    \
+      const int e = ev * 8 + 2 * w;                                               \
+      *reinterpret_cast<uint32_t*>(vw + e * SM::VROW + vtp * 2) = lo;             \
+      *reinterpret_cast<uint32_t*>(vw + (e + 1) * SM::VROW + vtp * 2) = hi;       \
+    }                                                                             \
+  } while (0)
+  auto compute_tile = [&](int tile, int buf) __attribute__((always_inline)) {
     const int k0 = tile * kTile;
-    {
-      unsigned char* kw = smem + buf * (SM::KBYTES + SM::VBYTES);
-      unsigned char* vw = kw + SM::KBYTES;
-      *reinterpret_cast<uint4*>(kw + tk0 * SM::KROW + ek * 16) = kr0;
-      *reinterpret_cast<uint4*>(kw + tk1 * SM::KROW + ek * 16) = kr1;
-      // V: pack the token pair's elements into (t, t+1) dwords and write
-      // them transposed, V^T[e][perm(t)], with perm(2vp + 1) = perm(2vp) + 1.
-      const uint32_t a[4] = {vr0.x, vr0.y, vr0.z, vr0.w};
-      const uint32_t b[4] = {vr1.x, vr1.y, vr1.z, vr1.w};
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const uint32_t lo = (a[w] & 0xFFFFu) | (b[w] << 16);       // element 2w
-        const uint32_t hi = (a[w] >> 16) | (b[w] & 0xFFFF0000u);   // element 2w + 1
-        const int e = ev * 8 + 2 * w;
-        *reinterpret_cast<uint32_t*>(vw + e * SM::VROW + vtp * 2) = lo;
-        *reinterpret_cast<uint32_t*>(vw + (e + 1) * SM::VROW + vtp * 2) = hi;
-      }
-    }
-    __syncthreads();
-    if (tile + 1 < ntiles) EHIP_PF_GLOAD(k0 + kTile);  // next tile in flight during compute
     // Wavefront-uniform: a tile wholly past this wavefront's last row (the
     // other row groups' diagonal) is skipped.
     if (k0 < wend) {
       const unsigned char* kb = smem + buf * (SM::KBYTES + SM::VBYTES);
       const unsigned char* vb = kb + SM::KBYTES;
       // Keys past this lane's query position (or past the workgroup's last
-      // key) are masked; only tiles reaching the diagonal mask anything.
-      const int lim = k0 + kTile > P + r0 ? min(qpos, kend - 1) : INT_MAX;
+      // key) are masked.
+      const bool diag = k0 + kTile > P + r0;
+      const int lim = min(qpos, kend - 1);
 
       // S^T for all heads: each K operand feeds HB MFMAs, each Q operand two
       // (the tile's halves).
@@ -254,40 +257,46 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
             s[hh][h2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[h2], qv, s[hh][h2], 0, 0, 0);
         }
       }
-      // s[hh][h2][i] = score(token k0 + 16*h2 + 4*kq + i, query row n)
+      // s[hh][h2][i] = score(token k0 + 16*h2 + 4*kq + i, query row n), raw
+      // q.k. Only tiles reaching the diagonal mask anything.
+      if (diag) {
+#pragma unroll
+        for (int hh = 0; hh < HB; ++hh)
+#pragma unroll
+          for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (k0 + 16 * h2 + 4 * kq + i > lim) s[hh][h2][i] = -INFINITY;
+      }
       bf16x8_t pa[HB];
       float alpha[HB];
       bool moved = false;
 #pragma unroll
       for (int hh = 0; hh < HB; ++hh) {
-        float sv[8];
+        float mx = fmaxf(s[hh][0][0], s[hh][1][0]);
+#pragma unroll
+        for (int i = 1; i < 4; ++i) mx = fmaxf(mx, fmaxf(s[hh][0][i], s[hh][1][i]));
+        mx = fmaxf(mx, ShflF(mx, lane ^ 16));
+        mx = fmaxf(mx, ShflF(mx, lane ^ 32));
+        // Lazy rescaling (FlashAttention-3, Shah et al. 2024): the running
+        // reference (raw score units) moves only when the tile's max exceeds
+        // it by more than kRefSlack in log2 units, so probabilities stay below
+        // 2^kRefSlack and the output rescale is skipped for most tiles;
+        // O / l is unchanged.
+        const float mn = mx > m[hh] + slack ? mx : m[hh];
+        alpha[hh] = mn == -INFINITY ? 1.f : Exp2((m[hh] - mn) * sl2);
+        moved = moved || mn != m[hh];
+        m[hh] = mn;
+        const float mc = mn == -INFINITY ? 0.f : mn * sl2;  // masked scores give exp2(-inf) = 0
+        float ps = 0.f;
 #pragma unroll
         for (int h2 = 0; h2 < 2; ++h2)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const int kpos = k0 + 16 * h2 + 4 * kq + i;
-            sv[4 * h2 + i] = kpos <= lim ? s[hh][h2][i] * p.scale_log2 : -INFINITY;
+            const float pv = Exp2(fmaf(s[hh][h2][i], sl2, -mc));
+            ps += pv;
+            pa[hh][4 * h2 + i] = static_cast<__bf16>(pv);
           }
-        float mx = sv[0];
-#pragma unroll
-        for (int i = 1; i < 8; ++i) mx = fmaxf(mx, sv[i]);
-        mx = fmaxf(mx, ShflF(mx, lane ^ 16));
-        mx = fmaxf(mx, ShflF(mx, lane ^ 32));
-        // Lazy rescaling (FlashAttention-3, Shah et al. 2024): the running
-        // reference moves only when the tile's max exceeds it by more than
-        // kRefSlack (log2 units), so probabilities stay below 2^kRefSlack and
-        // the output rescale is skipped for most tiles; O / l is unchanged.
-        const float mn = mx > m[hh] + kRefSlack ? mx : m[hh];
-        alpha[hh] = mn == -INFINITY ? 1.f : Exp2(m[hh] - mn);
-        moved = moved || mn != m[hh];
-        m[hh] = mn;
-        float ps = 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float pv = mn == -INFINITY ? 0.f : Exp2(sv[i] - mn);
-          ps += pv;
-          pa[hh][i] = static_cast<__bf16>(pv);
-        }
         l[hh] = l[hh] * alpha[hh] + ps;  // lane-partial over this lane's tokens
       }
       // Rescale the output rows (D layout: row 4kq+i) by their row's alpha,
@@ -312,6 +321,21 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
           o[hh][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[hh], vbv, o[hh][nb], 0, 0, 0);
       }
     }
+  };
+  // Tile t is staged in slot t % 2 and LDS buffer t % 2; its slot is
+  // refilled with tile t + 2 right after it is written to LDS.
+  EHIP_PF_GLOAD(stA, 0);
+  if (ntiles > 1) EHIP_PF_GLOAD(stB, kTile);
+  for (int tile = 0; tile < ntiles; tile += 2) {
+    EHIP_PF_STORE(stA, 0);
+    __syncthreads();
+    if (tile + 2 < ntiles) EHIP_PF_GLOAD(stA, (tile + 2) * kTile);
+    compute_tile(tile, 0);
+    if (tile + 1 >= ntiles) break;
+    EHIP_PF_STORE(stB, 1);
+    __syncthreads();
+    if (tile + 3 < ntiles) EHIP_PF_GLOAD(stB, (tile + 3) * kTile);
+    compute_tile(tile + 1, 1);
   }
 
   // Row sums: each lane holds a partial over its tokens; the 4 lanes of a
@@ -335,6 +359,7 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
   }
   if (__any(bad) && lane == 0) atomicOr(p.err, kErrBlockRange);
 #undef EHIP_PF_GLOAD
+#undef EHIP_PF_STORE
 }
 
 }  // namespace
