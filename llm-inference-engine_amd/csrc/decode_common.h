@@ -46,6 +46,7 @@ struct ItemRef {
   int tb;
   int te;
   int table_off;
+  int first[2];  // block ids of the first two 16-token halves, or -1
 };
 
 __device__ __forceinline__ ItemRef DecodeItem(const WorkItem& it) {
@@ -58,6 +59,8 @@ __device__ __forceinline__ ItemRef DecodeItem(const WorkItem& it) {
   r.tb = it.tok_begin;
   r.te = it.tok_end;
   r.table_off = it.table_off;
+  r.first[0] = it.first_block0;
+  r.first[1] = it.first_block1;
   return r;
 }
 

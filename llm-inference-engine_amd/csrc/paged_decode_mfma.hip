@@ -136,11 +136,13 @@ void DecodeMfmaBf16(DecodeParams p) {
   // slab rows never reach the PV sums, whatever they hold), and a half beyond
   // the range, or on a rejected block id, gets an empty descriptor whose loads
   // return zeros without touching memory. Scores of such rows are masked.
-  auto load = [&](T& t, int t0) {
+  // given: the halves' block ids come from the work item (first tile only).
+  auto load = [&](T& t, int t0, bool given) {
 #pragma unroll
     for (int h2 = 0; h2 < TH; ++h2) {
       const int th = t0 + 16 * h2;  // wavefront-uniform; a half lies in one block (bs >= 16)
-      const int phys = __builtin_amdgcn_readlane(tab, min(th, te - 1) / bs - lb0);
+      const int phys = given ? it.first[h2 > 0 ? 1 : 0]
+                             : __builtin_amdgcn_readlane(tab, min(th, te - 1) / bs - lb0);
       const bool ok = th < te && phys >= 0;
       t.phys[h2] = ok ? phys : -1;
       const int64_t boff = int64_t{ok ? phys : 0} * p.block_stride + (th & bmask) * D;
@@ -160,8 +162,13 @@ void DecodeMfmaBf16(DecodeParams p) {
   };
 
   T bufA, bufB, bufC;
-  load(bufA, tb);  // first tiles in flight while Q is split
-  if constexpr (NBUF == 3) load(bufB, tb + TT);
+  // First tiles in flight while Q is split; the first one does not wait for
+  // the table when the item carries its block ids.
+  if (it.first[0] >= 0)
+    load(bufA, tb, true);
+  else
+    load(bufA, tb, false);
+  if constexpr (NBUF == 3) load(bufB, tb + TT, false);
 
   // Q as MFMA A operands: q = hi + lo, both bf16 (round-to-nearest-even
   // narrowing, branch-free); padding virtual heads are zero.
@@ -285,22 +292,22 @@ void DecodeMfmaBf16(DecodeParams p) {
   // flight while one is computed; loads past the range are empty.
   if constexpr (NBUF == 2) {
     for (int t0 = tb;; t0 += 2 * TT) {
-      load(bufB, t0 + TT);
+      load(bufB, t0 + TT, false);
       process(bufA, t0);
       if (t0 + TT >= te) break;
-      load(bufA, t0 + 2 * TT);
+      load(bufA, t0 + 2 * TT, false);
       process(bufB, t0 + TT);
       if (t0 + 2 * TT >= te) break;
     }
   } else {
     for (int t0 = tb;; t0 += 3 * TT) {
-      load(bufC, t0 + 2 * TT);
+      load(bufC, t0 + 2 * TT, false);
       process(bufA, t0);
       if (t0 + TT >= te) break;
-      load(bufA, t0 + 3 * TT);
+      load(bufA, t0 + 3 * TT, false);
       process(bufB, t0 + TT);
       if (t0 + 2 * TT >= te) break;
-      load(bufB, t0 + 4 * TT);
+      load(bufB, t0 + 4 * TT, false);
       process(bufC, t0 + 2 * TT);
       if (t0 + 3 * TT >= te) break;
     }

@@ -190,6 +190,18 @@ void FinishPlan(const ehip_geometry& g, Plan* plan, bool allow_joint,
                    [](const WorkItem& x, const WorkItem& y) {
                      return x.tok_end - x.tok_begin > y.tok_end - y.tok_begin;
                    });
+  // The block ids of each item's first two 16-token halves ride in the item,
+  // so a wavefront can issue its first K/V loads without waiting for its
+  // table slice (-1 when the table is device-resident and unknown here).
+  for (WorkItem& w : plan->items) {
+    if (plan->table_ids.empty()) {
+      w.first_block0 = w.first_block1 = -1;
+      continue;
+    }
+    const int32_t* t = plan->table_ids.data() + w.table_off;
+    w.first_block0 = t[w.tok_begin / g.block_size];
+    w.first_block1 = t[std::min(w.tok_begin + 16, w.tok_end - 1) / g.block_size];
+  }
 }
 
 }  // namespace

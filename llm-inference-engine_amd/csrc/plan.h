@@ -52,8 +52,8 @@ struct WorkItem {
   int32_t tok_end;
   int32_t hk_split;  // kv_head | split << 12
   int32_t table_off;
-  int32_t reserved0;
-  int32_t reserved1;
+  int32_t first_block0;  // block id of token tok_begin (-1: read the table)
+  int32_t first_block1;  // block id of token min(tok_begin + 16, tok_end - 1)
 };
 
 // One causal prefill block: query rows q0 .. q0+M-1 of a chunk of `chunk`
