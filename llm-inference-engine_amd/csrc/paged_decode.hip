@@ -121,9 +121,13 @@ __device__ __forceinline__ void DecodeValuRow(const DecodeParams& p, int row, in
     for (int e = 0; e < E; ++e) o[h][e] = 0.f;
   }
 
-  for (int t0 = tb; t0 < te; t0 += 32) {
-    uint4 kr[ROWS][NV], vr[ROWS][NV];
+  // K/V of one 32-token tile; two of them ping-pong so the next tile's loads
+  // are in flight while the current one is computed.
+  struct VTile {
+    uint4 k[ROWS][NV], v[ROWS][NV];
     int phys[ROWS];
+  };
+  auto load = [&](VTile& t, int t0) {
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
       // One buffer descriptor per wavefront row of TPR tokens (they lie in
@@ -134,7 +138,7 @@ __device__ __forceinline__ void DecodeValuRow(const DecodeParams& p, int row, in
       const int j0 = t0 + r * TPR;  // wavefront-uniform
       const int ph = __builtin_amdgcn_readlane(tab, min(j0, te - 1) / bs - lb0);
       const bool ok = j0 < te && ph >= 0;
-      phys[r] = ok ? ph : -1;
+      t.phys[r] = ok ? ph : -1;
       const int64_t off = int64_t{ok ? ph : 0} * p.block_stride + int64_t{j0 & (bs - 1)} * D;
       const uint32_t range =
           ok ? static_cast<uint32_t>(min(TPR, te - j0) * D * static_cast<int>(sizeof(KV))) : 0u;
@@ -145,10 +149,12 @@ __device__ __forceinline__ void DecodeValuRow(const DecodeParams& p, int row, in
 #pragma unroll
       for (int v = 0; v < NV; ++v) {
         const int vo = lane_off + v * VSPAN * static_cast<int>(sizeof(KV));
-        kr[r][v] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, vo, 0, kKvLoadAux));
-        vr[r][v] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, vo, 0, kKvLoadAux));
+        t.k[r][v] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, vo, 0, kKvLoadAux));
+        t.v[r][v] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, vo, 0, kKvLoadAux));
       }
     }
+  };
+  auto compute = [&](const VTile& t, int t0) {
     const bool partial = t0 + 32 > te;
 
     float s[ROWS][G];
@@ -156,8 +162,8 @@ __device__ __forceinline__ void DecodeValuRow(const DecodeParams& p, int row, in
     for (int r = 0; r < ROWS; ++r) {
       float kf[E];
 #pragma unroll
-      for (int v = 0; v < NV; ++v) Widen<KV>(kr[r][v], kf + v * EPV);
-      const bool valid = phys[r] >= 0 && (!partial || t0 + r * TPR + tl < te);
+      for (int v = 0; v < NV; ++v) Widen<KV>(t.k[r][v], kf + v * EPV);
+      const bool valid = t.phys[r] >= 0 && (!partial || t0 + r * TPR + tl < te);
 #pragma unroll
       for (int h = 0; h < G; ++h) {
         float acc = 0.f;
@@ -194,11 +200,33 @@ __device__ __forceinline__ void DecodeValuRow(const DecodeParams& p, int row, in
     for (int r = 0; r < ROWS; ++r) {
       float vf[E];  // rows past the range end were read as zeros
 #pragma unroll
-      for (int v = 0; v < NV; ++v) Widen<KV>(vr[r][v], vf + v * EPV);
+      for (int v = 0; v < NV; ++v) Widen<KV>(t.v[r][v], vf + v * EPV);
 #pragma unroll
       for (int h = 0; h < G; ++h)
 #pragma unroll
         for (int e = 0; e < E; ++e) o[h][e] = fmaf(s[r][h], vf[e], o[h][e]);
+    }
+  };
+  // Double-buffered unless the shape's registers would spill (fp32, d = 128,
+  // g >= 7 keeps one tile in flight at a time).
+  constexpr bool kDouble = !(sizeof(KV) == 4 && D == 128 && G >= 7);
+  VTile bufA;
+  if constexpr (kDouble) {
+    VTile bufB;
+    load(bufA, tb);
+    // A work item's range is never empty; loads past its end are empty.
+    for (int t0 = tb;; t0 += 64) {
+      load(bufB, t0 + 32);
+      compute(bufA, t0);
+      if (t0 + 32 >= te) break;
+      load(bufA, t0 + 64);
+      compute(bufB, t0 + 32);
+      if (t0 + 64 >= te) break;
+    }
+  } else {
+    for (int t0 = tb; t0 < te; t0 += 32) {
+      load(bufA, t0);
+      compute(bufA, t0);
     }
   }
 
@@ -260,7 +288,10 @@ __device__ __forceinline__ void DecodeValuRow(const DecodeParams& p, int row, in
 
 template <class KV, int D, int G>
 __global__ __launch_bounds__(kWavesPerBlock * 64) void DecodeValu(DecodeParams p) {
-  const int item_idx = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  // Wavefront-uniform (readfirstlane): the item and everything derived from
+  // it live in scalar registers, so the K/V buffer descriptors are uniform.
+  const int item_idx =
+      blockIdx.x * kWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (item_idx >= p.n_items) return;
   const ItemRef it = DecodeItem(p.items[item_idx]);
   for (int r = 0; r < it.nrows; ++r)
@@ -347,7 +378,10 @@ __device__ void DecodeGenericRow(const DecodeParams& p, int row, int hk, int tb,
 
 template <class KV>
 __global__ __launch_bounds__(kWavesPerBlock * 64) void DecodeGeneric(DecodeParams p) {
-  const int item_idx = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  // Wavefront-uniform (readfirstlane): the item and everything derived from
+  // it live in scalar registers, so the K/V buffer descriptors are uniform.
+  const int item_idx =
+      blockIdx.x * kWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (item_idx >= p.n_items) return;
   const ItemRef it = DecodeItem(p.items[item_idx]);
   for (int r = 0; r < it.nrows; ++r)
