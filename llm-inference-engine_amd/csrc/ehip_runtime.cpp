@@ -187,11 +187,16 @@ int LaunchAttention(ehip_ctx* ctx, const float* q, const void* k_slab, const voi
     pp.out = out;
     pp.items = ctx->d_prefill;
     pp.table = ctx->d_table;
+    pp.rows = ctx->d_rows;
+    pp.part_o = ctx->d_part;
+    pp.part_ml = ctx->d_part + static_cast<size_t>(plan.partials) * (g.heads / g.kv_heads) *
+                                   g.head_dim;
     pp.err = ctx->d_err;
     pp.block_stride = ehip::BlockStride(g);
     pp.slab_blocks = g.slab_blocks;
     pp.n_items = static_cast<int32_t>(plan.prefill.size());
     pp.heads = g.heads;
+    pp.kv_heads = g.kv_heads;
     pp.group = g.heads / g.kv_heads;
     pp.d = g.head_dim;
     pp.bs = g.block_size;
@@ -201,7 +206,7 @@ int LaunchAttention(ehip_ctx* ctx, const float* q, const void* k_slab, const voi
       return SetError(ctx, EHIP_INTERNAL, "prefill plan for a shape the kernel does not cover");
     EHIP_HIP(ctx, e);
   }
-  if (plan.items.empty()) return EHIP_OK;
+  if (plan.items.empty() && plan.merge_rows.empty()) return EHIP_OK;
   ehip::DecodeParams p{};
   p.q = q;
   p.k_slab = k_slab;
@@ -559,9 +564,14 @@ int ehip_step_upload(ehip_ctx* ctx, const ehip_geometry* geom, const ehip_step_d
   if (!geom || !step) return SetError(ctx, EHIP_INVALID_ARGUMENT, "null geometry or step");
   Plan plan;
   std::string err;
+  const int64_t stride = ehip::BlockStride(*geom);
+  const int64_t slab_bytes =
+      geom->slab_blocks > 0 && stride > 0 && geom->slab_blocks <= INT64_MAX / stride / 2
+          ? geom->slab_blocks * stride * 2
+          : INT64_MAX;
   const int prefill_rows = ehip::PrefillRowsPerItem(
       geom->kv_dtype, geom->head_dim, geom->kv_heads > 0 ? geom->heads / geom->kv_heads : 0,
-      geom->block_size);
+      geom->block_size, slab_bytes);
   if (int rc = ehip::BuildPlan(*geom, *step, &plan, &err, prefill_rows))
     return SetError(ctx, rc, "%s", err.c_str());
   return UploadPlan(ctx, *geom, std::move(plan), nullptr);

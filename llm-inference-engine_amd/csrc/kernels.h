@@ -49,11 +49,15 @@ struct PrefillParams {
   float* out;               // [rows, H, d]
   const PrefillItem* items;
   const int32_t* table;
+  const RowDesc* rows;      // split slots of the rows of key-split items
+  float* part_o;            // [partials, g, d]
+  float* part_ml;           // [partials, g, 2]
   int32_t* err;
   int64_t block_stride;
   int64_t slab_blocks;
   int32_t n_items;
   int32_t heads;
+  int32_t kv_heads;
   int32_t group;
   int32_t d;
   int32_t bs;
@@ -65,8 +69,9 @@ struct PrefillParams {
 // false (nothing launched) for shapes it does not cover.
 bool LaunchPrefillMfma(const PrefillParams& p, hipStream_t stream, hipError_t* err);
 // Query rows per prefill work item for this geometry, or 0 when the MFMA
-// prefill kernel does not cover it (bf16 K/V, d = 128, g in {4, 8}, bs >= 16).
-int PrefillRowsPerItem(int kv_dtype, int d, int group, int bs);
+// prefill kernel does not cover it (bf16 K/V, d = 128, g in {4, 8}, bs >= 16,
+// slabs below 4 GiB).
+int PrefillRowsPerItem(int kv_dtype, int d, int group, int bs, int64_t slab_bytes);
 
 // Launch the decode kernel family for the given plan (one wavefront per work
 // item; picks the specialised (dtype, d, g) kernel or the generic one), then,

@@ -496,8 +496,8 @@ hipError_t LaunchSplits(const DecodeParams& p, int kv_dtype, hipStream_t stream)
 }  // namespace
 
 hipError_t LaunchDecode(const DecodeParams& p, int kv_dtype, hipStream_t stream) {
-  if (p.n_items == 0) return hipSuccess;
-  hipError_t e = LaunchSplits(p, kv_dtype, stream);
+  // Split rows may come from prefill key splits alone (no decode items).
+  hipError_t e = p.n_items > 0 ? LaunchSplits(p, kv_dtype, stream) : hipSuccess;
   if (e != hipSuccess || p.n_merge == 0) return e;
   // Only the rows that were split: a step dominated by prefill-chunk rows
   // (which need no merge) launches no idle merge blocks.

@@ -31,6 +31,7 @@
 #include <climits>
 #include <cstdlib>
 
+#include "decode_common.h"
 #include "device_util.h"
 #include "kernels.h"
 
@@ -108,16 +109,20 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
   const int hgi = wave / RG;  // and head group
 
   const PrefillItem it = p.items[blockIdx.x];
-  const int hk = it.kv_head;
+  const int hk = it.hk_split & ((1 << kHkBits) - 1);
+  const int split = it.hk_split >> kHkBits;
   const int P = it.past;       // cached keys before the chunk
   const int T = it.chunk;      // chunk rows
   const int q0 = it.q0;        // first chunk row of this workgroup
   const int bs = p.bs;
   const int qn = min(M, T - q0);             // live query rows of the workgroup
   const int kend = P + q0 + qn;              // keys [0, kend) are attended by some row
+  const int key0 = it.key_begin;             // this item's key range [key0, key1)
+  const int key1 = it.key_end;
+  const bool whole = key0 == 0 && key1 >= kend;  // else: partials for the split merge
   const int r0 = q0 + 16 * rg;               // this wavefront's first row
   const int qnw = min(16, max(0, T - r0));   // its live rows (0: nothing to compute)
-  const int wend = P + r0 + qnw;             // keys this wavefront's rows attend
+  const int wend = min(P + r0 + qnw, key1);  // keys this wavefront's rows attend here
 
   // Q^T as MFMA B operands (bf16, round-to-nearest-even): lane l holds
   // Q[row r0 + l%16][c*32 + 8*kq .. +8] for each of its heads. They are kept
@@ -159,31 +164,44 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
   // V token pair vp = tid % 16 (tokens 2vp, 2vp + 1), group tid / 16.
   const int tk0 = tid / EG, tk1 = (tid + kWaves * 64) / EG, ek = tid % EG;
   const int vp = tid % 16, ev = tid / 16;
-  // bs is a power of two: block index and slot by shift and mask.
+  // bs is a power of two: block index and slot by shift and mask. A 32-key
+  // tile spans at most two blocks (bs >= 16, tiles start at multiples of
+  // 32): their two ids are read once per wavefront and selected per thread,
+  // and K/V are read through buffer descriptors with 32-bit byte offsets
+  // (the host routes slabs of 4 GiB or more away from this kernel).
   const int bsh = __builtin_ctz(bs), bmask = bs - 1;
   const int32_t* tab = p.table + it.table_off;
   const uint32_t nblk = static_cast<uint32_t>(p.slab_blocks);
+  const int last_blk = (key1 - 1) >> bsh;
+  const uint32_t stride_b = static_cast<uint32_t>(p.block_stride) * 2u;
+  const __amdgpu_buffer_rsrc_t rk =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kslab), 0, 0xFFFFFFFFu, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vslab), 0, 0xFFFFFFFFu, 0x00020000);
+  const uint32_t ko = static_cast<uint32_t>(ek * 16), vo = static_cast<uint32_t>(ev * 16);
 #define EHIP_PF_GLOAD(ST, K0)                                                                  \
   do {                                                                                      \
-    const int pk0 = min((K0) + tk0, kend - 1), pk1 = min((K0) + tk1, kend - 1);             \
-    const int pv0 = min((K0) + 2 * vp, kend - 1), pv1 = min((K0) + 2 * vp + 1, kend - 1);    \
-    int b0 = tab[pk0 >> bsh], b1 = tab[pk1 >> bsh];                                          \
-    int b2 = tab[pv0 >> bsh], b3 = tab[pv1 >> bsh];                                          \
-    const bool ok0 = static_cast<uint32_t>(b0) < nblk, ok1 = static_cast<uint32_t>(b1) < nblk; \
-    const bool ok2 = static_cast<uint32_t>(b2) < nblk, ok3 = static_cast<uint32_t>(b3) < nblk; \
-    bad = bad | !(ok0 & ok1 & ok2 & ok3);                                                    \
-    b0 = ok0 ? b0 : 0;                                                                       \
-    b1 = ok1 ? b1 : 0;                                                                       \
-    b2 = ok2 ? b2 : 0;                                                                       \
-    b3 = ok3 ? b3 : 0;                                                                       \
-    ST##0 = *reinterpret_cast<const uint4*>(kslab + int64_t{b0} * p.block_stride +             \
-                                          (pk0 & bmask) * D + ek * 8);                       \
-    ST##1 = *reinterpret_cast<const uint4*>(kslab + int64_t{b1} * p.block_stride +             \
-                                          (pk1 & bmask) * D + ek * 8);                       \
-    ST##2 = *reinterpret_cast<const uint4*>(vslab + int64_t{b2} * p.block_stride +             \
-                                          (pv0 & bmask) * D + ev * 8);                       \
-    ST##3 = *reinterpret_cast<const uint4*>(vslab + int64_t{b3} * p.block_stride +             \
-                                          (pv1 & bmask) * D + ev * 8);                       \
+    const int kb0 = (K0) >> bsh;                                                            \
+    int id0 = __builtin_amdgcn_readfirstlane(tab[kb0]);                                     \
+    int id1 = __builtin_amdgcn_readfirstlane(tab[min(kb0 + 1, last_blk)]);                   \
+    const bool okb = static_cast<uint32_t>(id0) < nblk && static_cast<uint32_t>(id1) < nblk; \
+    bad = bad | !okb;                                                                        \
+    id0 = okb ? id0 : 0;                                                                     \
+    id1 = okb ? id1 : 0;                                                                     \
+    const int pk0 = min((K0) + tk0, key1 - 1), pk1 = min((K0) + tk1, key1 - 1);             \
+    const int pv0 = min((K0) + 2 * vp, key1 - 1), pv1 = min((K0) + 2 * vp + 1, key1 - 1);    \
+    const uint32_t a0 = static_cast<uint32_t>((pk0 >> bsh) != kb0 ? id1 : id0) * stride_b +  \
+                        static_cast<uint32_t>((pk0 & bmask) * D * 2) + ko;                   \
+    const uint32_t a1 = static_cast<uint32_t>((pk1 >> bsh) != kb0 ? id1 : id0) * stride_b +  \
+                        static_cast<uint32_t>((pk1 & bmask) * D * 2) + ko;                   \
+    const uint32_t a2 = static_cast<uint32_t>((pv0 >> bsh) != kb0 ? id1 : id0) * stride_b +  \
+                        static_cast<uint32_t>((pv0 & bmask) * D * 2) + vo;                   \
+    const uint32_t a3 = static_cast<uint32_t>((pv1 >> bsh) != kb0 ? id1 : id0) * stride_b +  \
+                        static_cast<uint32_t>((pv1 & bmask) * D * 2) + vo;                   \
+    ST##0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, a0, 0, 0)); \
+    ST##1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, a1, 0, 0)); \
+    ST##2 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, a2, 0, 0)); \
+    ST##3 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, a3, 0, 0)); \
   } while (0)
 
   // Per head state. Scores/probabilities live in the S^T layout (row n =
@@ -201,7 +219,7 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
   const float sl2 = p.scale_log2;          // scores -> log2 domain
   const float slack = kRefSlack / sl2;     // the rescale slack in raw score units
 
-  const int ntiles = (kend + kTile - 1) / kTile;
+  const int ntiles = (key1 - key0 + kTile - 1) / kTile;
   const int vtp = VPerm(2 * vp);
   // Writes a staged tile into LDS buffer BUF: K row-major; V packed into
   // (t, t+1) dwords (lo: element 2w, hi: element 2w + 1 of the pair) and
@@ -224,7 +242,7 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
     }                                                                             \
   } while (0)
   auto compute_tile = [&](int tile, int buf) __attribute__((always_inline)) {
-    const int k0 = tile * kTile;
+    const int k0 = key0 + tile * kTile;
     // Wavefront-uniform: a tile wholly past this wavefront's last row (the
     // other row groups' diagonal) is skipped.
     if (k0 < wend) {
@@ -232,8 +250,8 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
       const unsigned char* vb = kb + SM::KBYTES;
       // Keys past this lane's query position (or past the workgroup's last
       // key) are masked.
-      const bool diag = k0 + kTile > P + r0;
-      const int lim = min(qpos, kend - 1);
+      const bool diag = k0 + kTile > P + r0 || k0 + kTile > key1;
+      const int lim = min(qpos, key1 - 1);
 
       // S^T for all heads: each K operand feeds HB MFMAs, each Q operand two
       // (the tile's halves).
@@ -324,17 +342,17 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
   };
   // Tile t is staged in slot t % 2 and LDS buffer t % 2; its slot is
   // refilled with tile t + 2 right after it is written to LDS.
-  EHIP_PF_GLOAD(stA, 0);
-  if (ntiles > 1) EHIP_PF_GLOAD(stB, kTile);
+  EHIP_PF_GLOAD(stA, key0);
+  if (ntiles > 1) EHIP_PF_GLOAD(stB, key0 + kTile);
   for (int tile = 0; tile < ntiles; tile += 2) {
     EHIP_PF_STORE(stA, 0);
     __syncthreads();
-    if (tile + 2 < ntiles) EHIP_PF_GLOAD(stA, (tile + 2) * kTile);
+    if (tile + 2 < ntiles) EHIP_PF_GLOAD(stA, key0 + (tile + 2) * kTile);
     compute_tile(tile, 0);
     if (tile + 1 >= ntiles) break;
     EHIP_PF_STORE(stB, 1);
     __syncthreads();
-    if (tile + 3 < ntiles) EHIP_PF_GLOAD(stB, (tile + 3) * kTile);
+    if (tile + 3 < ntiles) EHIP_PF_GLOAD(stB, key0 + (tile + 3) * kTile);
     compute_tile(tile + 1, 1);
   }
 
@@ -345,15 +363,38 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
     float lt = l[hh];
     lt += ShflF(lt, lane ^ 16);
     lt += ShflF(lt, lane ^ 32);
-    const int head = hk * G + hgi * HB + hh;
+    const int hg = hgi * HB + hh;  // head within the kv head's group
+    const int head = hk * G + hg;
+    if (whole) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = 4 * kq + i;  // D-layout row of register i
-      const float inv = 1.0f / ShflF(lt, r);
-      if (r < qnw) {
-        float* op = p.out + (int64_t{it.row_base + r0 + r} * p.heads + head) * D + n;
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * kq + i;  // D-layout row of register i
+        const float inv = 1.0f / ShflF(lt, r);
+        if (r < qnw) {
+          float* op = p.out + (int64_t{it.row_base + r0 + r} * p.heads + head) * D + n;
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) op[16 * nb] = o[hh][nb][i] * inv;
+          for (int nb = 0; nb < NB; ++nb) op[16 * nb] = o[hh][nb][i] * inv;
+        }
+      }
+    } else {
+      // Split partials: unnormalised output, the reference in log2 units and
+      // the row sum, at the rows' split slots.
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * kq + i;
+        if (r < qnw) {
+          const RowDesc rd = p.rows[it.row_base + r0 + r];
+          const int64_t pidx = PartialIndex(rd, p.kv_heads, hk, split);
+          float* po = p.part_o + (pidx * G + hg) * D + n;
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) po[16 * nb] = o[hh][nb][i];
+        }
+      }
+      if (kq == 0 && n < qnw) {
+        const RowDesc rd = p.rows[it.row_base + r0 + n];
+        const int64_t pidx = PartialIndex(rd, p.kv_heads, hk, split);
+        const float ms = m[hh] == -INFINITY ? -INFINITY : m[hh] * sl2;
+        *reinterpret_cast<float2*>(p.part_ml + (pidx * G + hg) * 2) = make_float2(ms, lt);
       }
     }
   }
@@ -388,8 +429,9 @@ bool LaunchPrefillMfma(const PrefillParams& p, hipStream_t stream, hipError_t* e
   return false;
 }
 
-int PrefillRowsPerItem(int kv_dtype, int d, int group, int bs) {
+int PrefillRowsPerItem(int kv_dtype, int d, int group, int bs, int64_t slab_bytes) {
   if (kv_dtype != EHIP_KV_BF16 || d != 128 || (group != 4 && group != 8) || bs < 16) return 0;
+  if (slab_bytes > int64_t{0xFFFFFFFF}) return 0;  // 32-bit K/V byte offsets
   return PrefillRows(group, PrefillHeadsPerWave());
 }
 

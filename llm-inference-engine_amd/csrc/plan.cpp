@@ -93,12 +93,13 @@ int32_t SharedFullBlocks(const Plan& plan, const RowDesc& a, const RowDesc& b, i
 // first block id and table), splits every row into whole-tile key ranges
 // (joint ranges first), assigns partial slots and orders the work longest
 // first.
+// skip[r] > 0: row r is served by the prefill kernel in skip[r] key splits.
 void FinishPlan(const ehip_geometry& g, Plan* plan, bool allow_joint,
-                const std::vector<uint8_t>* skip = nullptr) {
+                const std::vector<int32_t>* skip = nullptr) {
   const int32_t bs = g.block_size;
   const int32_t max_split = 64 * bs;
   const size_t n = plan->rows.size();
-  auto skipped = [&](size_t r) { return skip && (*skip)[r]; };
+  auto skipped = [&](size_t r) { return skip && (*skip)[r] > 0; };
   int64_t units = 0;
   for (size_t r = 0; r < n; ++r)
     if (!skipped(r)) units += int64_t{plan->rows[r].length} * g.kv_heads;
@@ -157,7 +158,8 @@ void FinishPlan(const ehip_geometry& g, Plan* plan, bool allow_joint,
   for (size_t r = 0; r < n; ++r) {
     RowDesc& rd = plan->rows[r];
     const int32_t sl = split_len[r], P = joint_len[r];
-    rd.nsplit = skipped(r) ? 0 : (P + sl - 1) / sl + (rd.length - P + sl - 1) / sl;
+    rd.nsplit = skipped(r) ? ((*skip)[r] > 1 ? (*skip)[r] : 0)
+                           : (P + sl - 1) / sl + (rd.length - P + sl - 1) / sl;
     rd.split_base = static_cast<int32_t>(split_base);
     split_base += rd.nsplit;
     plan->any_split = plan->any_split || rd.nsplit > 1;
@@ -276,31 +278,68 @@ int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::
     return Fail(err, EHIP_UNIMPLEMENTED, "kv_heads=%lld >= 4096", g.kv_heads);
 
   // Chunks big enough for the MFMA prefill kernel leave the decode partition.
-  std::vector<uint8_t> skip(plan->rows.size(), 0);
+  std::vector<int32_t> skip(plan->rows.size(), 0);
   const char* pf = std::getenv("EHIP_PREFILL");
   if (prefill_rows > 0 && !(pf && pf[0] == '0')) {
     struct Block { int32_t b, q0, keys; };
     std::vector<Block> blocks;
     std::vector<int32_t> row_base(B + 1, 0);
     for (int32_t b = 0; b < B; ++b) row_base[b + 1] = row_base[b] + s.h_query_lens[b];
+    int64_t total_tiles = 0;
     for (int32_t b = 0; b < B; ++b) {
       const int32_t T = s.h_query_lens[b];
       if (T < kMinPrefillRows) continue;
       const int32_t P = static_cast<int32_t>(s.h_context_lens[b] - T);
-      for (int32_t q0 = 0; q0 < T; q0 += prefill_rows)
+      for (int32_t q0 = 0; q0 < T; q0 += prefill_rows) {
         blocks.push_back({b, q0, P + std::min(T, q0 + prefill_rows)});
+        total_tiles += (blocks.back().keys + kPrefillTile - 1) / kPrefillTile;
+      }
       std::fill(skip.begin() + row_base[b], skip.begin() + row_base[b + 1], 1);
     }
+    // Key splits: a block with more than twice the per-workgroup share of
+    // the step's tiles is cut into splits of about that share, so the last
+    // query blocks of a long chunk do not walk all their keys alone
+    // (EHIP_PREFILL_SPLIT=0 keeps every block whole).
+    const char* ps = std::getenv("EHIP_PREFILL_SPLIT");
+    const bool split_ok = !(ps && ps[0] == '0');
+    const int64_t share = std::max<int64_t>(
+        kMinPrefillSplitTiles,
+        (total_tiles * g.kv_heads + kPrefillSlots - 1) / kPrefillSlots);
+    auto block_splits = [&](const Block& bl) {
+      const int64_t tiles = (bl.keys + kPrefillTile - 1) / kPrefillTile;
+      if (!split_ok || tiles <= 2 * share) return int64_t{1};
+      return std::min<int64_t>((tiles + share - 1) / share, kMaxSplitsPerRow);
+    };
     // Most keys first; kv head fastest, so the blocks of one kv head are
     // dispatched 8 workgroups apart and land on one XCD's L2 together.
     std::stable_sort(blocks.begin(), blocks.end(),
                      [](const Block& x, const Block& y) { return x.keys > y.keys; });
-    for (const Block& bl : blocks) {
+    struct Piece { int32_t bi, split, kb, ke; };
+    std::vector<Piece> pieces;
+    for (size_t i = 0; i < blocks.size(); ++i) {
+      const Block& bl = blocks[i];
+      const int32_t T = s.h_query_lens[bl.b];
+      const int32_t ns = static_cast<int32_t>(block_splits(bl));
+      const int32_t r0 = row_base[bl.b] + bl.q0;
+      const int32_t r1 = row_base[bl.b] + std::min(T, bl.q0 + prefill_rows);
+      std::fill(skip.begin() + r0, skip.begin() + r1, ns);
+      const int32_t tiles = (bl.keys + kPrefillTile - 1) / kPrefillTile;
+      const int32_t per = (tiles + ns - 1) / ns;
+      for (int32_t sp = 0, kb = 0; kb < bl.keys; ++sp, kb += per * kPrefillTile)
+        pieces.push_back({static_cast<int32_t>(i), sp, kb,
+                          std::min(bl.keys, kb + per * kPrefillTile)});
+    }
+    // Longest piece first (the sort above keeps blocks in key order).
+    std::stable_sort(pieces.begin(), pieces.end(), [](const Piece& x, const Piece& y) {
+      return x.ke - x.kb > y.ke - y.kb;
+    });
+    for (const Piece& pc : pieces) {
+      const Block& bl = blocks[pc.bi];
       const int32_t T = s.h_query_lens[bl.b];
       const int32_t P = static_cast<int32_t>(s.h_context_lens[bl.b] - T);
       for (int32_t hk = 0; hk < g.kv_heads; ++hk)
-        plan->prefill.push_back(PrefillItem{row_base[bl.b], T, P, bl.q0, hk,
-                                            s.h_table_offsets[bl.b], 0, 0});
+        plan->prefill.push_back(PrefillItem{row_base[bl.b], T, P, bl.q0, PackHkSplit(hk, pc.split),
+                                            s.h_table_offsets[bl.b], pc.kb, pc.ke});
     }
   }
   FinishPlan(g, plan, true, &skip);

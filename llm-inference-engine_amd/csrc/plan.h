@@ -59,15 +59,20 @@ struct WorkItem {
 // One causal prefill block: query rows q0 .. q0+M-1 of a chunk of `chunk`
 // rows (starting at packed row row_base) over `past` cached keys, for the g
 // query heads of one kv head (M = PrefillRowsPerItem for the geometry).
+// A block whose key range is long relative to the step's prefill work is
+// cut into key splits [key_begin, key_end) of whole 32-key tiles; each split
+// writes (max, sum, output) partials for its rows that the split merge
+// combines (the rows' RowDesc.nsplit counts the splits). An unsplit item
+// covers [0, P + q0 + rows) and writes the output directly.
 struct PrefillItem {
   int32_t row_base;
   int32_t chunk;
   int32_t past;
   int32_t q0;
-  int32_t kv_head;
+  int32_t hk_split;   // kv_head | split << 12
   int32_t table_off;
-  int32_t reserved0;
-  int32_t reserved1;
+  int32_t key_begin;
+  int32_t key_end;
 };
 
 constexpr int kMaxJointRows = 2;
@@ -108,6 +113,9 @@ int32_t ChooseSplitTokens(const ehip_geometry& g, int64_t unit_tokens);
 // per prefill work item; EHIP_PREFILL=0
 // keeps every row on the decode kernels); their rows get nsplit = 0.
 constexpr int32_t kMinPrefillRows = 16;
+constexpr int32_t kPrefillTile = 32;       // keys per prefill tile
+constexpr int32_t kPrefillSlots = 512;     // workgroups resident at once (2 per CU)
+constexpr int32_t kMinPrefillSplitTiles = 8;
 int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::string* err,
               int prefill_rows = 0);
 

@@ -494,6 +494,29 @@ def test_prefill_chunk_shapes(gctx, ehip_mod, orc, H, Hkv, T, P):
     check_step_rows(w, got, ref, ref32)
 
 
+@pytest.mark.parametrize("H,Hkv", [(32, 8), (64, 8)])
+@pytest.mark.parametrize("T,P", [(512, 1024), (700, 0), (96, 4000)])
+def test_prefill_key_splits(gctx, ehip_mod, orc, H, Hkv, T, P, monkeypatch):
+    """Prefill blocks cut into key splits (the long ones relative to the
+    step's prefill work) and merged by the split merge: against the
+    references, and against the same step with every block whole."""
+    w = chunk_workload(H, Hkv, T, P, extra_decodes=3, seed=T + P + H + 7)
+    outs, partials = [], []
+    for flag in ("1", "0"):
+        monkeypatch.setenv("EHIP_PREFILL_SPLIT", flag)
+        (got, ref, kpool, vpool, q, cu), = run_step(gctx, ehip_mod, orc, w, 41)
+        partials.append(gctx.step_info()[2])
+        if flag == "1":
+            ref32 = fp32_reference(orc, w, kpool, vpool, q, cu)
+            check_step_rows(w, got, ref, ref32)
+        outs.append(got)
+    assert partials[0] > partials[1], f"expected key splits in the plan: {partials}"
+    # Same bf16 products up to where P is rounded (each split keeps its own
+    # softmax reference): within the prefill bar of each other.
+    rows = np.repeat(w.query_lens, w.query_lens) > 1
+    assert rel_norm(outs[0][rows], outs[1][rows]) <= PREFILL_REL
+
+
 @pytest.mark.parametrize("kernel", ["mfma", "valu"])
 def test_step_c4_shape_with_shared_prefix_blocks(gctx, ehip_mod, orc, kernel, monkeypatch):
     """C4 construction (log-uniform lengths, pair-shared prefix blocks, bf16)
