@@ -300,14 +300,18 @@ int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::
     // the step's tiles is cut into splits of about that share, so the last
     // query blocks of a long chunk do not walk all their keys alone
     // (EHIP_PREFILL_SPLIT=0 keeps every block whole).
+    // EHIP_PREFILL_SPLIT: 0 keeps every block whole; a number x > 0 splits
+    // blocks longer than x shares (default 1).
     const char* ps = std::getenv("EHIP_PREFILL_SPLIT");
-    const bool split_ok = !(ps && ps[0] == '0');
+    const double split_mult = ps ? std::strtod(ps, nullptr) : 1.0;
+    const bool split_ok = split_mult > 0.0;
     const int64_t share = std::max<int64_t>(
         kMinPrefillSplitTiles,
         (total_tiles * g.kv_heads + kPrefillSlots - 1) / kPrefillSlots);
     auto block_splits = [&](const Block& bl) {
       const int64_t tiles = (bl.keys + kPrefillTile - 1) / kPrefillTile;
-      if (!split_ok || tiles <= 2 * share) return int64_t{1};
+      if (!split_ok || static_cast<double>(tiles) <= split_mult * static_cast<double>(share))
+        return int64_t{1};
       return std::min<int64_t>((tiles + share - 1) / share, kMaxSplitsPerRow);
     };
     // Most keys first; kv head fastest, so the blocks of one kv head are
