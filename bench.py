@@ -52,6 +52,8 @@ def parse():
     ap.add_argument("--layers", type=int, default=0, help="override the config's layer count")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-ceiling-probe", action="store_true",
+                    help="skip the read-bandwidth probes that price the practical ceiling")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="run one device-to-device copy of this size first (a known-size "
                          "dispatch that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -112,6 +114,28 @@ def cpu_baseline(w, seconds: float):
 
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def ceiling_probe(ctx, w, slab_pair, slab_bytes):
+    """Practical read ceilings on this device (libehip's probes, no
+    arithmetic): a streaming read of one K slab, and the decode access pattern
+    (random (block, kv head) tiles of K and V, 36 per wavefront) with the
+    default and the non-temporal load policy."""
+    ks, vs = slab_pair
+    tile = w.block_size * w.head_dim * w.kv_bytes
+    rng = np.random.default_rng(5)
+    blocks = rng.permutation(w.pool_blocks).astype(np.int32)
+    tiles = 36
+    blocks = blocks[: blocks.size // tiles * tiles]
+    out = {"stream_read_gbps": round(ctx.probe_stream_read(ks, min(slab_bytes, (1 << 32) - 16),
+                                                           nt=False), 1)}
+    for nt in (False, True):
+        g = ctx.probe_tile_gather(ks, vs, w.pool_blocks, blocks, tiles, w.kv_heads,
+                                  w.kv_heads * tile, tile, nt=nt)
+        out["tile_gather_nt_gbps" if nt else "tile_gather_gbps"] = round(g, 1)
+    out["note"] = ("best of 3; tile gather = the decode kernels' access pattern alone, "
+                   f"{tile}-byte (block, head) tiles of both slabs")
+    return out
 
 
 def time_chunks(ctx, ehip, w, slabs, qs, outs, layers, reps=5):
@@ -317,6 +341,9 @@ def main():
             "timed_steps_sampled": len(sampled),
         },
     }
+    if not args.no_ceiling_probe:
+        result["ceiling"] = ceiling_probe(ctx, w, slabs[0], slab_bytes)
+        log(f"[bench] read ceiling: {result['ceiling']}")
     pre = time_chunks(ctx, ehip, w, slabs, qs, outs, layers)
     if pre is not None:
         result["prefill"] = pre

@@ -175,6 +175,22 @@ int ehip_paged_decode_attention_batched_bf16(
     int64_t heads, int64_t kv_heads, int64_t d, int64_t block_size, int64_t block_stride,
     int64_t slab_blocks, float scale, float* d_out);
 
+/* ------------------------------------------- measurement probes -------
+ * Read-bandwidth probes that price the attention kernels' roofline on the
+ * running device (not part of the attention path): a streaming pass over
+ * d_buf (16 <= bytes < 4 GiB), and the decode access pattern alone, in which
+ * each of (n_blocks / tiles_per_item) * kv_heads wavefronts reads
+ * tiles_per_item (block, head) tiles of tile_bytes from both slabs, at the
+ * block ids h_blocks (each < slab_blocks; a block is block_bytes long).
+ * nt selects the non-temporal load policy the decode kernels use. Each runs
+ * reps times; *gbps gets the best rate in GB/s (bytes read / time). */
+int ehip_probe_stream_read(ehip_ctx* ctx, const void* d_buf, int64_t bytes, int32_t nt,
+                           int32_t reps, float* gbps);
+int ehip_probe_tile_gather(ehip_ctx* ctx, const void* d_k_slab, const void* d_v_slab,
+                           int64_t slab_blocks, const int32_t* h_blocks, int64_t n_blocks,
+                           int32_t tiles_per_item, int32_t kv_heads, int64_t block_bytes,
+                           int32_t tile_bytes, int32_t nt, int32_t reps, float* gbps);
+
 /* ------------------------------------------------ step path (hot path) ----
  * One descriptor upload per scheduler step, then per layer one append and one
  * attention launch covering every sequence (decode rows and prefill chunks

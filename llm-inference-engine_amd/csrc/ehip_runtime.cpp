@@ -66,6 +66,30 @@ int HipFail(ehip_ctx* ctx, hipError_t e, const char* what) {
   return SetError(ctx, code, "%s: %s", what, hipGetErrorString(e));
 }
 
+// Best-of-reps rate of `launch` over `bytes` bytes, timed with events on the
+// context stream.
+template <class F>
+int TimeProbe(ehip_ctx* ctx, double bytes, int32_t reps, F launch, float* gbps) {
+  hipEvent_t a = nullptr, b = nullptr;
+  hipError_t e = hipEventCreate(&a);
+  if (e == hipSuccess) e = hipEventCreate(&b);
+  float best = 0.f;
+  for (int r = 0; e == hipSuccess && r < reps; ++r) {
+    e = hipEventRecord(a, ctx->stream);
+    if (e == hipSuccess) e = launch();
+    if (e == hipSuccess) e = hipEventRecord(b, ctx->stream);
+    if (e == hipSuccess) e = hipEventSynchronize(b);
+    float ms = 0.f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, a, b);
+    if (e == hipSuccess && ms > 0.f) best = std::max(best, static_cast<float>(bytes / ms / 1e6));
+  }
+  if (a) (void)hipEventDestroy(a);
+  if (b) (void)hipEventDestroy(b);
+  if (e != hipSuccess) return HipFail(ctx, e, "probe");
+  *gbps = best;
+  return EHIP_OK;
+}
+
 #define EHIP_HIP(ctx, expr)                                  \
   do {                                                       \
     hipError_t e_ = (expr);                                  \
@@ -377,6 +401,55 @@ int ehip_fill_normal(ehip_ctx* ctx, void* d_dst, int64_t n, int32_t dtype, float
     return SetError(ctx, EHIP_INVALID_ARGUMENT, "bad fill arguments");
   EHIP_HIP(ctx, ehip::LaunchFillNormal(d_dst, n, dtype, mean, stddev, seed, ctx->stream));
   return EHIP_OK;
+}
+
+
+int ehip_probe_stream_read(ehip_ctx* ctx, const void* d_buf, int64_t bytes, int32_t nt,
+                           int32_t reps, float* gbps) {
+  if (int rc = CheckCtx(ctx)) return rc;
+  if (!d_buf || !gbps || reps < 1 || bytes < 16 || bytes >= (int64_t{1} << 32))
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "probe needs 16 <= bytes < 4 GiB and reps >= 1");
+  uint32_t* sink = reinterpret_cast<uint32_t*>(ctx->d_err) + 32;  // a spare word of the err page
+  const int64_t used = bytes / 16 * 16;
+  return TimeProbe(ctx, static_cast<double>(used), reps, [&] {
+    return ehip::LaunchStreamRead(d_buf, used, nt != 0, sink, ctx->stream);
+  }, gbps);
+}
+
+int ehip_probe_tile_gather(ehip_ctx* ctx, const void* d_k_slab, const void* d_v_slab,
+                           int64_t slab_blocks, const int32_t* h_blocks, int64_t n_blocks,
+                           int32_t tiles_per_item, int32_t kv_heads, int64_t block_bytes,
+                           int32_t tile_bytes, int32_t nt, int32_t reps, float* gbps) {
+  if (int rc = CheckCtx(ctx)) return rc;
+  if (!d_k_slab || !d_v_slab || !h_blocks || !gbps || reps < 1 || tiles_per_item < 1 ||
+      kv_heads < 1 || tile_bytes < 16 || tile_bytes % 16 != 0 ||
+      int64_t{tile_bytes} * kv_heads > block_bytes || n_blocks < tiles_per_item ||
+      n_blocks / tiles_per_item * kv_heads > INT32_MAX)
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "bad tile-gather probe arguments");
+  for (int64_t i = 0; i < n_blocks; ++i)
+    if (h_blocks[i] < 0 || h_blocks[i] >= slab_blocks)
+      return SetError(ctx, EHIP_INVALID_ARGUMENT, "probe block id %d out of range",
+                      static_cast<int>(h_blocks[i]));
+  const int32_t items = static_cast<int32_t>(n_blocks / tiles_per_item * kv_heads);
+  void* d_blocks = nullptr;
+  EHIP_HIP(ctx, hipMalloc(&d_blocks, static_cast<size_t>(n_blocks) * 4));
+  hipError_t e = hipMemcpyAsync(d_blocks, h_blocks, static_cast<size_t>(n_blocks) * 4,
+                                hipMemcpyHostToDevice, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
+    (void)hipFree(d_blocks);
+    return HipFail(ctx, e, "probe upload");
+  }
+  uint32_t* sink = reinterpret_cast<uint32_t*>(ctx->d_err) + 32;
+  const double bytes = 2.0 * items * tiles_per_item * tile_bytes;
+  const int rc = TimeProbe(ctx, bytes, reps, [&] {
+    return ehip::LaunchTileGather(d_k_slab, d_v_slab, static_cast<const int32_t*>(d_blocks), items,
+                                  tiles_per_item, kv_heads, block_bytes, tile_bytes, nt != 0, sink,
+                                  ctx->stream);
+  }, gbps);
+  (void)hipStreamSynchronize(ctx->stream);
+  (void)hipFree(d_blocks);
+  return rc;
 }
 
 int ehip_event_create(ehip_ctx* ctx, void** ev_out) {

@@ -94,6 +94,14 @@ hipError_t LaunchKvGather(const float* k_slab, const float* v_slab, const int32_
                           int64_t slab_blocks, float* out_k, float* out_v, int32_t* err,
                           hipStream_t stream);
 
+// Measurement probes (probe.hip): a streaming read of a buffer below 4 GiB,
+// and the decode access pattern without arithmetic.
+hipError_t LaunchStreamRead(const void* p, int64_t bytes, bool nt, uint32_t* sink,
+                            hipStream_t stream);
+hipError_t LaunchTileGather(const void* k, const void* v, const int32_t* blocks, int32_t n_items,
+                            int32_t tiles, int32_t kv_heads, int64_t block_bytes,
+                            int32_t tile_bytes, bool nt, uint32_t* sink, hipStream_t stream);
+
 hipError_t LaunchFillNormal(void* dst, int64_t n, int dtype, float mean, float stddev,
                             uint64_t seed, hipStream_t stream);
 
