@@ -206,6 +206,22 @@ int ehip_step_upload(ehip_ctx* ctx, const ehip_geometry* geom, const ehip_step_d
  * slot mapping; slabs are fp32 or bf16 per geom.kv_dtype. */
 int ehip_step_kv_append(ehip_ctx* ctx, const float* d_src_k, const float* d_src_v,
                         void* d_k_slab, void* d_v_slab);
+/* RoPE fused into the append: rotates q [sum T_b, H, d] in place and each new
+ * K row (src [sum T_b, Hkv, d] fp32) on its way into the slab, and appends V
+ * unrotated. Row t of sequence b sits at position context_lens[b] -
+ * query_lens[b] + t (the positions BatchAssembler hands the model,
+ * src/engine/batch.cpp:70-76). d_cos/d_sin are [table_positions, d/2] fp32
+ * (Rope::cos()/sin(), src/model/modules.h:185-207). Replaces the two
+ * kernels::RopeApplyF32 calls before the append in OptimizedModel's layer
+ * forward (src/model/optimized_model.cpp:284-291, kernels in
+ * src/kernels/rope.h:34) plus ehip_step_kv_append; q and the slab rows equal
+ * the reference AVX2 kernel's results bit for bit (bf16 slabs after
+ * round-to-nearest-even). d_src_k is left unrotated. EHIP_INVALID_ARGUMENT
+ * when a position is >= table_positions, as OptimizedModel::forward rejects
+ * positions past max_position_embeddings (src/model/optimized_model.cpp:529-535). */
+int ehip_step_rope_kv_append(ehip_ctx* ctx, float* d_q, const float* d_src_k,
+                             const float* d_src_v, const float* d_cos, const float* d_sin,
+                             int64_t table_positions, void* d_k_slab, void* d_v_slab);
 /* Attention for every row of the step: q/out [sum T_b, H, d] fp32. */
 int ehip_step_attention(ehip_ctx* ctx, const float* d_q, const void* d_k_slab,
                         const void* d_v_slab, float* d_out);

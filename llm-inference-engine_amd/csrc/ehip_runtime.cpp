@@ -671,6 +671,35 @@ int ehip_step_kv_append(ehip_ctx* ctx, const float* d_src_k, const float* d_src_
   return EHIP_OK;
 }
 
+int ehip_step_rope_kv_append(ehip_ctx* ctx, float* d_q, const float* d_src_k,
+                             const float* d_src_v, const float* d_cos, const float* d_sin,
+                             int64_t table_positions, void* d_k_slab, void* d_v_slab) {
+  if (int rc = CheckCtx(ctx)) return rc;
+  if (!ctx->have_step) return SetError(ctx, EHIP_FAILED_PRECONDITION, "no step uploaded");
+  const Plan& plan = ctx->plan;
+  if (plan.rows.empty()) return EHIP_OK;
+  if (plan.slots.empty())
+    return SetError(ctx, EHIP_FAILED_PRECONDITION, "the uploaded step has no slot mapping");
+  if (!d_q || !d_src_k || !d_src_v || !d_cos || !d_sin || !d_k_slab || !d_v_slab)
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "null rope/append operand");
+  const ehip_geometry& g = ctx->geom;
+  if (g.head_dim % 2 != 0)
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "RoPE needs an even head_dim (got %d)",
+                    g.head_dim);
+  if (plan.max_length > table_positions)
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "position %lld outside the RoPE tables [0, %lld)",
+                    static_cast<long long>(plan.max_length - 1),
+                    static_cast<long long>(table_positions));
+  if (ehip::BlockStride(g) != int64_t{g.kv_heads} * g.block_size * g.head_dim)
+    return SetError(ctx, EHIP_UNIMPLEMENTED, "append needs the dense Hkv*bs*d block stride");
+  EHIP_HIP(ctx, ehip::LaunchRopeKvAppend(d_q, d_src_k, d_src_v, ctx->d_rows, d_cos, d_sin,
+                                         ctx->d_slots, static_cast<int64_t>(plan.rows.size()),
+                                         g.heads, g.kv_heads, g.head_dim, g.block_size,
+                                         g.slab_blocks, d_k_slab, d_v_slab, g.kv_dtype,
+                                         ctx->d_err, ctx->stream));
+  return EHIP_OK;
+}
+
 int ehip_step_attention(ehip_ctx* ctx, const float* d_q, const void* d_k_slab,
                         const void* d_v_slab, float* d_out) {
   if (int rc = CheckCtx(ctx)) return rc;

@@ -94,6 +94,14 @@ hipError_t LaunchKvGather(const float* k_slab, const float* v_slab, const int32_
                           int64_t slab_blocks, float* out_k, float* out_v, int32_t* err,
                           hipStream_t stream);
 
+// Fused RoPE + KV append of one step's rows (q rotated in place; rotated K and
+// V scattered at the rows' slots; row r at position rows[r].length - 1).
+hipError_t LaunchRopeKvAppend(float* q, const float* src_k, const float* src_v,
+                              const RowDesc* rows, const float* cos_t, const float* sin_t,
+                              const int64_t* slots, int64_t n_rows, int heads, int kv_heads,
+                              int d, int bs, int64_t slab_blocks, void* k_slab, void* v_slab,
+                              int kv_dtype, int32_t* err, hipStream_t stream);
+
 // Measurement probes (probe.hip): a streaming read of a buffer below 4 GiB,
 // and the decode access pattern without arithmetic.
 hipError_t LaunchStreamRead(const void* p, int64_t bytes, bool nt, uint32_t* sink,

@@ -90,6 +90,97 @@ __global__ __launch_bounds__(256) void KvScatterScalar(const float* __restrict__
   }
 }
 
+// Fused RoPE + KV append for the rows of one step: kernels::RopeApplyF32
+// (src/kernels/rope.h:13-36, HF half rotation) on q in place and on each
+// appended K row on its way into the slab (src/model/optimized_model.cpp
+// applies RoPE to q and k, then PagedKvCache::append scatters k and v).
+// Row r sits at position rows[r].length - 1. The pair (x[j], x[j + d/2]) is
+// rotated as the reference's AVX2 row kernel does it:
+//   out[j]       = fma(-x[j + d/2], sin, x[j] * cos)
+//   out[j + d/2] = fma(x[j], sin, x[j + d/2] * cos)
+// for the pairs in whole groups of 8, and as the compiled scalar tail of that
+// kernel, fma(x[j], cos, -(x[j + d/2] * sin)) and fma(x[j + d/2], cos,
+// x[j] * sin), for the rest, so q and the K slab match the reference
+// bit for bit (the bf16 slab after its round-to-nearest-even). One thread handles W
+// consecutive pairs of one (row, head): heads [0, H) are q, [H, H + Hkv) the
+// k/v rows, whose v is copied unrotated. The source K rows are left as they
+// were (the rotated rows live in the slab).
+template <class KV, int W>
+__global__ __launch_bounds__(256) void RopeKvAppend(
+    float* __restrict__ q, const float* __restrict__ src_k, const float* __restrict__ src_v,
+    const RowDesc* __restrict__ rows, const float* __restrict__ cos_t,
+    const float* __restrict__ sin_t, const int64_t* __restrict__ slots, int64_t n_rows, int heads,
+    int kv_heads, int d, int bs, int64_t slab_blocks, KV* k_slab, KV* v_slab, int32_t* err) {
+  const int half = d >> 1;
+  const int fused = half & ~7;  // pairs the AVX2 kernel handles 8 at a time
+  const int gpr = half / W;     // pair groups per head row
+  const int64_t per_row = int64_t{heads + kv_heads} * gpr;
+  const int64_t n = n_rows * per_row;
+  for (int64_t i = blockIdx.x * int64_t{blockDim.x} + threadIdx.x; i < n;
+       i += int64_t{gridDim.x} * blockDim.x) {
+    const int64_t r = i / per_row;
+    const int rem = static_cast<int>(i - r * per_row);
+    const int hh = rem / gpr;
+    const int j = (rem - hh * gpr) * W;
+    const int64_t p = rows[r].length - 1;
+    const float* cr = cos_t + p * half + j;
+    const float* sr = sin_t + p * half + j;
+    float lo[W], hi[W], c[W], s[W];
+    const float* x = hh < heads ? q + (r * heads + hh) * d
+                                : src_k + (r * kv_heads + (hh - heads)) * d;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      lo[w] = x[j + w];
+      hi[w] = x[j + half + w];
+      c[w] = cr[w];
+      s[w] = sr[w];
+    }
+    float ro[W], rh[W];
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      if (j + w < fused) {
+        ro[w] = fmaf(-hi[w], s[w], lo[w] * c[w]);
+        rh[w] = fmaf(lo[w], s[w], hi[w] * c[w]);
+      } else {
+        ro[w] = fmaf(lo[w], c[w], -(hi[w] * s[w]));
+        rh[w] = fmaf(hi[w], c[w], lo[w] * s[w]);
+      }
+    }
+    if (hh < heads) {
+      float* xq = q + (r * heads + hh) * d;
+#pragma unroll
+      for (int w = 0; w < W; ++w) {
+        xq[j + w] = ro[w];
+        xq[j + half + w] = rh[w];
+      }
+      continue;
+    }
+    const int h = hh - heads;
+    const int64_t slot = slots[r];
+    if (slot < 0 || slot >= slab_blocks * bs) {
+      atomicOr(err, kErrSlotRange);
+      continue;
+    }
+    const int64_t block = slot / bs;
+    const int64_t dst = ((block * kv_heads + h) * bs + (slot - block * bs)) * d;
+    const float* xv = src_v + (r * kv_heads + h) * d;
+    if constexpr (W == 4) {
+      Store4<KV>(k_slab + dst + j, make_float4(ro[0], ro[1], ro[2], ro[3]));
+      Store4<KV>(k_slab + dst + j + half, make_float4(rh[0], rh[1], rh[2], rh[3]));
+      Store4<KV>(v_slab + dst + j, *reinterpret_cast<const float4*>(xv + j));
+      Store4<KV>(v_slab + dst + j + half, *reinterpret_cast<const float4*>(xv + j + half));
+    } else {
+#pragma unroll
+      for (int w = 0; w < W; ++w) {
+        Store1(k_slab + dst + j + w, ro[w]);
+        Store1(k_slab + dst + j + half + w, rh[w]);
+        Store1(v_slab + dst + j + w, xv[j + w]);
+        Store1(v_slab + dst + j + half + w, xv[j + half + w]);
+      }
+    }
+  }
+}
+
 // kernels::KvGatherF32 (src/kernels/kv_gather.cpp:42-89): out[h, j, :] is
 // token j of kv head h, read through the table.
 __global__ __launch_bounds__(256) void KvGather(const float* __restrict__ k_slab,
@@ -145,6 +236,37 @@ int GridFor(int64_t work, int block) {
 }
 
 }  // namespace
+
+hipError_t LaunchRopeKvAppend(float* q, const float* src_k, const float* src_v,
+                              const RowDesc* rows, const float* cos_t, const float* sin_t,
+                              const int64_t* slots, int64_t n_rows, int heads, int kv_heads,
+                              int d, int bs, int64_t slab_blocks, void* k_slab, void* v_slab,
+                              int kv_dtype, int32_t* err, hipStream_t stream) {
+  const bool vec = (d % 8) == 0 && reinterpret_cast<uintptr_t>(q) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(src_k) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(src_v) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(cos_t) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(sin_t) % 16 == 0;
+  const int64_t n = n_rows * (heads + kv_heads) * (d / 2) / (vec ? 4 : 1);
+  const dim3 grid(GridFor(n, 256)), block(256);
+#define EHIP_ROPE_LAUNCH(KV, W)                                                               \
+  hipLaunchKernelGGL((RopeKvAppend<KV, W>), grid, block, 0, stream, q, src_k, src_v, rows,   \
+                     cos_t, sin_t, slots, n_rows, heads, kv_heads, d, bs, slab_blocks,        \
+                     static_cast<KV*>(k_slab), static_cast<KV*>(v_slab), err)
+  if (kv_dtype == EHIP_KV_BF16) {
+    if (vec)
+      EHIP_ROPE_LAUNCH(uint16_t, 4);
+    else
+      EHIP_ROPE_LAUNCH(uint16_t, 1);
+  } else {
+    if (vec)
+      EHIP_ROPE_LAUNCH(float, 4);
+    else
+      EHIP_ROPE_LAUNCH(float, 1);
+  }
+#undef EHIP_ROPE_LAUNCH
+  return hipGetLastError();
+}
 
 hipError_t LaunchKvScatter(const float* src_k, const float* src_v, const int64_t* slots,
                            int64_t t_dim, int32_t kv_heads, int32_t d, int32_t bs,

@@ -219,6 +219,7 @@ int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::
   plan->table_ids.clear();
   plan->slots.clear();
   plan->partials = 0;
+  plan->max_length = 0;
   const int32_t B = s.num_seqs;
   if (B == 0) {
     FinishPlan(g, plan, false);
@@ -263,6 +264,7 @@ int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::
     const int64_t P = L - T;
     for (int32_t t = 0; t < T; ++t)
       plan->rows.push_back(RowDesc{s.h_table_offsets[b], static_cast<int32_t>(P + t + 1), 0, 0});
+    plan->max_length = std::max(plan->max_length, L);
   }
   if (s.h_slot_mapping) {
     const int64_t cap = g.slab_blocks * g.block_size;

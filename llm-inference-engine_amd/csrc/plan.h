@@ -89,6 +89,7 @@ struct Plan {
   std::vector<int64_t> slots;       // slot mapping of appended tokens (may be empty)
   std::vector<int32_t> merge_rows;  // rows with more than one split, ascending
   int64_t partials = 0;             // sum over rows of nsplit * Hkv
+  int64_t max_length = 0;           // longest visible length (largest position + 1)
   int32_t split_tokens = 0;         // base split length chosen for this step
   int64_t joint_items = 0;
   int64_t shared_tokens = 0;        // sum over groups of the jointly read prefix

@@ -146,25 +146,49 @@ Status BatchedAttention::Upload(const BatchInputs& in) {
   return Status::Ok();
 }
 
-Status BatchedAttention::ForwardLayer(int layer, const float* d_q, const float* d_k_new,
-                                      const float* d_v_new, float* d_out) {
-  const int layers = pool_->geometry().num_layers;
+Status BatchedAttention::CheckLayer(int layer) const {
   if (!uploaded_)
     return Error(StatusCode::kFailedPrecondition, "BatchedAttention: no step uploaded");
   if (layer != next_layer_)
     return Error(StatusCode::kInvalidArgument,
                  Format("BatchedAttention: expected layer %d next, got %d", next_layer_, layer));
+  return Status::Ok();
+}
+
+Status BatchedAttention::Attend(int layer, const float* d_q, float* d_out) {
+  if (Status s = FromRc(ctx_, ehip_step_attention(ctx_, d_q, pool_->k_slab(layer),
+                                                  pool_->v_slab(layer), d_out));
+      !s.ok())
+    return s;
+  next_layer_ = (layer + 1) % pool_->geometry().num_layers;
+  return Status::Ok();
+}
+
+Status BatchedAttention::ForwardLayer(int layer, const float* d_q, const float* d_k_new,
+                                      const float* d_v_new, float* d_out) {
+  if (Status s = CheckLayer(layer); !s.ok()) return s;
   if (has_slots_)
     if (Status s = FromRc(ctx_, ehip_step_kv_append(ctx_, d_k_new, d_v_new, pool_->k_slab(layer),
                                                     pool_->v_slab(layer)));
         !s.ok())
       return s;
-  if (Status s = FromRc(ctx_, ehip_step_attention(ctx_, d_q, pool_->k_slab(layer),
-                                                  pool_->v_slab(layer), d_out));
+  return Attend(layer, d_q, d_out);
+}
+
+Status BatchedAttention::ForwardLayerRope(int layer, float* d_q, const float* d_k_new,
+                                          const float* d_v_new, const RopeTables& rope,
+                                          float* d_out) {
+  if (Status s = CheckLayer(layer); !s.ok()) return s;
+  if (!has_slots_)
+    return Error(StatusCode::kFailedPrecondition,
+                 "BatchedAttention: RoPE needs the step's slot mapping");
+  if (Status s = FromRc(ctx_, ehip_step_rope_kv_append(ctx_, d_q, d_k_new, d_v_new, rope.d_cos,
+                                                       rope.d_sin, rope.positions,
+                                                       pool_->k_slab(layer),
+                                                       pool_->v_slab(layer)));
       !s.ok())
     return s;
-  next_layer_ = (layer + 1) % layers;
-  return Status::Ok();
+  return Attend(layer, d_q, d_out);
 }
 
 }  // namespace ehip::host

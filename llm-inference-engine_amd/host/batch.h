@@ -85,6 +85,18 @@ class BatchedAttention {
   // [ΣT_b, H, d] fp32. Layers come in order 0..L-1 once per step.
   Status ForwardLayer(int layer, const float* d_q, const float* d_k_new, const float* d_v_new,
                       float* d_out);
+  // The same with RoPE fused into the append: d_q is rotated in place and the
+  // new K rows on their way into the slabs, at each row's absolute position
+  // (the rows' context position), as OptimizedModel's layer forward does with
+  // kernels::RopeApplyF32 before the append (src/model/optimized_model.cpp:284-291).
+  // d_cos/d_sin are the [positions, d/2] fp32 tables (Rope::cos()/sin()).
+  struct RopeTables {
+    const float* d_cos = nullptr;
+    const float* d_sin = nullptr;
+    int64_t positions = 0;
+  };
+  Status ForwardLayerRope(int layer, float* d_q, const float* d_k_new, const float* d_v_new,
+                          const RopeTables& rope, float* d_out);
 
   const ehip_geometry& geometry() const { return geom_; }
   float scale() const { return geom_.scale; }
@@ -93,6 +105,9 @@ class BatchedAttention {
   ehip_ctx* ctx_;
   const BlockPool* pool_;
   ehip_geometry geom_{};
+  Status CheckLayer(int layer) const;
+  Status Attend(int layer, const float* d_q, float* d_out);
+
   bool uploaded_ = false;
   bool has_slots_ = false;
   int next_layer_ = 0;

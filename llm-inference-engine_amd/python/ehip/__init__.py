@@ -93,6 +93,7 @@ def lib():
                                                          C.c_float, _vp],
             "ehip_step_upload": [_vp, C.POINTER(Geometry), C.POINTER(StepDesc)],
             "ehip_step_kv_append": [_vp, _vp, _vp, _vp, _vp],
+            "ehip_step_rope_kv_append": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp],
             "ehip_step_attention": [_vp, _vp, _vp, _vp, _vp],
             "ehip_step_info": [_vp, _I64P, _I64P, _I64P],
             "ehip_plan_counts": [C.POINTER(Geometry), C.POINTER(StepDesc), _I64P, _I64P, _I64P,
@@ -305,6 +306,11 @@ class Context:
 
     def step_kv_append(self, src_k, src_v, k_slab, v_slab) -> int:
         return lib().ehip_step_kv_append(self.h, src_k.ptr, src_v.ptr, k_slab.ptr, v_slab.ptr)
+
+    def step_rope_kv_append(self, q, src_k, src_v, cos, sin, table_positions, k_slab,
+                            v_slab) -> int:
+        return lib().ehip_step_rope_kv_append(self.h, q.ptr, src_k.ptr, src_v.ptr, cos.ptr,
+                                              sin.ptr, table_positions, k_slab.ptr, v_slab.ptr)
 
     def step_attention(self, q, k_slab, v_slab, out) -> int:
         return lib().ehip_step_attention(self.h, q.ptr, k_slab.ptr, v_slab.ptr, out.ptr)

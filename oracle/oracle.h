@@ -95,6 +95,15 @@ void orc_prefill_varlen_f32(int isa, const float* q, const int32_t* cu_seqlens,
                             float* out, int64_t heads, int64_t kv_heads,
                             int64_t d, float scale);
 
+/* ---- rotary position embedding, in place (src/kernels/rope.h:13-36;
+ *      src/kernels/scalar/rope.cpp, src/kernels/avx2/rope.cpp). x [t, hx, d]
+ *      fp32, cos/sin [P, d/2], positions [t]. isa 0: the scalar row kernel
+ *      (lo*c - hi*s with both products rounded); isa 1: the AVX2 row kernel
+ *      (fma(-hi, s, lo*c) and fma(lo, s, hi*c) over whole 8-wide groups of
+ *      the half; fma(lo, c, -(hi*s)) and fma(hi, c, lo*s) for the rest). ---- */
+void orc_rope_apply_f32(int isa, float* x, int64_t t, int64_t hx, int64_t d,
+                        const int32_t* positions, const float* cos, const float* sin);
+
 /* ---- KV scatter / gather (src/kernels/kv_scatter.cpp:27-61,
  *      src/kernels/kv_gather.cpp:42-89) ---- */
 void orc_kv_scatter_f32(const float* src_k, const float* src_v,

@@ -71,6 +71,8 @@ def lib():
                                           _u16p, _u16p]
         L.orc_kv_gather_f32.argtypes = [_f32p, _f32p, _i32p, _i64, _i64, _i64, _i64,
                                         _f32p, _f32p]
+        L.orc_rope_apply_f32.argtypes = [C.c_int, _f32p, _i64, _i64, _i64, _i32p, _f32p, _f32p]
+        L.orc_rope_apply_f32.restype = None
         L.orc_cpu_attention.argtypes = [_f32p, _f32p, _f32p, _i64, _i64, _i64, _i64, _i64,
                                         C.c_float, _f32p]
         L.orc_cpu_attention.restype = C.c_int
@@ -101,6 +103,8 @@ def ref():
                                      _i64, C.c_float]
         R.ref_kv_scatter_f32.argtypes = [_f32p, _f32p, _i64p, _i64, _i64, _i64, _i64,
                                          _f32p, _f32p]
+        R.ref_rope_apply_f32.argtypes = [C.c_int, _f32p, _i64, _i64, _i64, _i32p, _f32p, _f32p]
+        R.ref_rope_apply_f32.restype = None
         R.ref_kv_gather_f32.argtypes = [_f32p, _f32p, _i32p, _i64, _i64, _i64, _i64,
                                         _f32p, _f32p]
         _ref = R
@@ -256,6 +260,30 @@ def cpu_attention(q, k, v, heads, kv_heads, d, scale):
     if rc != 0:
         raise ValueError(f"orc_cpu_attention rejected the call (status {rc})")
     return out
+
+
+def rope_apply(x, positions, cos, sin, isa=1, use_ref=False):
+    """RopeApplyF32 on a copy of x [t, hx, d] (fp32); returns the rotated copy.
+    isa 1 = the AVX2 row kernel's FMA form, 0 = the scalar form."""
+    y = np.array(x, np.float32, copy=True, order="C")
+    t, hx, d = y.shape
+    pos = np.ascontiguousarray(positions, np.int32)
+    c = np.ascontiguousarray(cos, np.float32).reshape(-1)
+    s = np.ascontiguousarray(sin, np.float32).reshape(-1)
+    fn = ref().ref_rope_apply_f32 if use_ref else lib().orc_rope_apply_f32
+    fn(isa, y.reshape(-1), t, hx, d, pos, c, s)
+    return y
+
+
+def rope_tables(d, positions, theta=10000.0):
+    """cos/sin tables [P, d/2] the way the reference's Rope module builds them
+    for the default scaling (src/model/modules.cpp BaseInvFreq: inv_freq in
+    double, stored fp32; angle = position * inv_freq in fp32). Test data for
+    the RoPE kernels, which take the tables as inputs."""
+    half = d // 2
+    inv = (1.0 / np.power(float(theta), np.arange(half, dtype=np.float64) * 2.0 / d)).astype(np.float32)
+    ang = np.arange(positions, dtype=np.float32)[:, None] * inv[None, :]
+    return np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
 
 
 def kv_scatter(src_k, src_v, slot_mapping, kv_heads, d, bs, k_slab, v_slab, use_ref=False):

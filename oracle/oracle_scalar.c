@@ -565,3 +565,38 @@ int orc_cpu_attention(const float* q, const float* k, const float* v,
   orc_parallel_for(heads * t_dim, 1, attention_rows, &c);
   return 0;
 }
+
+
+/* RoPE row kernels (src/kernels/scalar/rope.cpp RopeRows and
+ * src/kernels/avx2/rope.cpp RopeRows). This file is built with
+ * -ffp-contract=off, so `lo * c - hi * s` rounds both products, as the
+ * reference's scalar kernel does; fmaf() spells out the AVX2 kernel's fused
+ * forms (bit-exact against the reference build for d = 10, 64, 72, 128, 130). */
+void orc_rope_apply_f32(int isa, float* x, int64_t t, int64_t hx, int64_t d,
+                        const int32_t* positions, const float* cos, const float* sin) {
+  const int64_t half = d / 2;
+  const int64_t fused = isa == 1 ? half / 8 * 8 : 0;  /* AVX2: whole 8-lane groups */
+  for (int64_t i = 0; i < t; ++i) {
+    const int64_t p = positions[i];
+    const float* cr = cos + p * half;
+    const float* sr = sin + p * half;
+    for (int64_t h = 0; h < hx; ++h) {
+      float* v = x + (i * hx + h) * d;
+      for (int64_t j = 0; j < half; ++j) {
+        const float c = cr[j], s = sr[j], lo = v[j], hi = v[j + half];
+        if (j < fused) {
+          v[j] = fmaf(-hi, s, lo * c);
+          v[j + half] = fmaf(lo, s, hi * c);
+        } else if (isa == 1) {
+          /* the AVX2 kernel's scalar tail, which its build contracts into
+           * fma(lo, c, -(hi*s)) and fma(hi, c, lo*s) */
+          v[j] = fmaf(lo, c, -(hi * s));
+          v[j + half] = fmaf(hi, c, lo * s);
+        } else {
+          v[j] = (lo * c) - (hi * s);
+          v[j + half] = (hi * c) + (lo * s);
+        }
+      }
+    }
+  }
+}

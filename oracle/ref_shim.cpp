@@ -18,6 +18,8 @@
 #include "kernels/kv_gather.h"
 #include "kernels/kv_scatter.h"
 #include "kernels/paged_attention.h"
+#include "kernels/internal/rope_impl.h"
+#include "kernels/rope.h"
 
 namespace k = engine::kernels;
 namespace ki = engine::kernels::internal;
@@ -31,6 +33,17 @@ extern "C" {
 int ref_selected_isa() { return static_cast<int>(k::SelectedIsa()); }
 
 float ref_exp_scalar(float x) { return ki::ExpF32Scalar(x); }
+
+// RoPE in place (src/kernels/rope.h:34-36): isa 0 / 1 runs that ISA's row
+// kernel through the detail seam, -1 the public threaded entry point.
+void ref_rope_apply_f32(int isa, float* x, std::int64_t t, std::int64_t hx, std::int64_t d,
+                        const std::int32_t* positions, const float* cos, const float* sin) {
+  if (isa < 0) {
+    k::RopeApplyF32(x, t, hx, d, positions, cos, sin);
+    return;
+  }
+  k::detail::RopeRowsVariant(ToIsa(isa))(x, t, hx, d, positions, cos, sin);
+}
 
 void ref_paged_decode_batched_f32(int isa, const float* q, const float* k_slab,
                                   const float* v_slab,

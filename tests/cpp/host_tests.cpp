@@ -804,6 +804,89 @@ TEST_GPU(GpuBatchedStepMixedBf16) {
   EXPECT_EQ(pool.refcount(caches[0].block_table().blocks()[0]), 2);
 }
 
+TEST_GPU(GpuBatchedStepRopeBf16) {
+  // ForwardLayerRope on a mixed step (decodes after a prompt step, plus a
+  // fresh 21-token chunk): q comes back rotated and the slabs hold rotated K
+  // and plain V, bit for bit the oracle's AVX2-form RoPE (at the positions
+  // BatchAssembler hands out) followed by its bf16 scatter.
+  Gpu gpu;
+  HbmSlabAllocator hbm(gpu.ctx);
+  const int L = 2, Hkv = 2, d = 72, bs = 16, H = 6;
+  StatusOr<std::unique_ptr<BlockPool>> pr =
+      BlockPool::Create(Geom(L, Hkv, d, KvDtype::kBFloat16), bs, 40, &hbm);
+  ASSERT_OK(pr.status());
+  BlockPool& pool = **pr;
+  BatchedAttention attn(gpu.ctx, &pool, H);
+  BatchAssembler asmb;
+  std::vector<PagedKvCache> caches;
+  caches.reserve(3);
+  for (int i = 0; i < 3; ++i) caches.emplace_back(&pool, gpu.ctx);
+  const int64_t n_pos = 256, half = d / 2;
+  std::vector<float> cs(static_cast<size_t>(n_pos * half)), sn(cs.size());
+  for (int64_t p = 0; p < n_pos; ++p)
+    for (int64_t j = 0; j < half; ++j) {
+      const float ang = static_cast<float>(p) * std::pow(10000.0f, -2.0f * j / d);
+      cs[static_cast<size_t>(p * half + j)] = std::cos(ang);
+      sn[static_cast<size_t>(p * half + j)] = std::sin(ang);
+    }
+  DeviceBuffer dcos = ToDevice(gpu.ctx, cs), dsin = ToDevice(gpu.ctx, sn);
+  const BatchedAttention::RopeTables rope{static_cast<const float*>(dcos.get()),
+                                          static_cast<const float*>(dsin.get()), n_pos};
+  const size_t slab_n = static_cast<size_t>(pool.slab_bytes() / 2);
+  std::vector<uint16_t> mk(slab_n * L, 0), mv(slab_n * L, 0);
+  uint64_t seed = 900;
+  const std::vector<std::vector<int>> steps = {{30, 70, 0}, {1, 1, 21}};
+  for (const std::vector<int>& lens : steps) {
+    std::vector<std::vector<int32_t>> toks;
+    std::vector<BatchSeqInput> seqs;
+    for (int s = 0; s < 3; ++s) toks.emplace_back(static_cast<size_t>(lens[static_cast<size_t>(s)]), 1);
+    for (int s = 0; s < 3; ++s)
+      if (!toks[static_cast<size_t>(s)].empty()) seqs.push_back({toks[static_cast<size_t>(s)], &caches[static_cast<size_t>(s)]});
+    ASSERT_OK(asmb.AssembleMixed(seqs));
+    const BatchInputs& in = asmb.inputs();
+    ASSERT_OK(attn.Upload(in));
+    const int64_t T = in.num_tokens();
+    for (int layer = 0; layer < L; ++layer) {
+      std::vector<float> q = Normal(T * H * d, seed++), k = Normal(T * Hkv * d, seed++),
+                         v = Normal(T * Hkv * d, seed++);
+      DeviceBuffer dq = ToDevice(gpu.ctx, q), dk = ToDevice(gpu.ctx, k), dv = ToDevice(gpu.ctx, v),
+                   dout;
+      ASSERT_OK(dout.Reserve(gpu.ctx, T * H * d * 4));
+      ASSERT_OK(attn.ForwardLayerRope(layer, static_cast<float*>(dq.get()),
+                                      static_cast<float*>(dk.get()), static_cast<float*>(dv.get()),
+                                      rope, static_cast<float*>(dout.get())));
+      ASSERT_OK(FromRc(gpu.ctx, ehip_sync(gpu.ctx)));
+      orc_rope_apply_f32(1, q.data(), T, H, d, in.positions.data(), cs.data(), sn.data());
+      orc_rope_apply_f32(1, k.data(), T, Hkv, d, in.positions.data(), cs.data(), sn.data());
+      const size_t off = static_cast<size_t>(layer) * slab_n;
+      orc_kv_scatter_bf16(k.data(), v.data(), in.slot_mapping.data(), T, Hkv, d, bs,
+                          mk.data() + off, mv.data() + off);
+      const std::vector<float> gq = ToHost<float>(gpu.ctx, dq.get(), T * H * d);
+      EXPECT(std::memcmp(gq.data(), q.data(), q.size() * 4) == 0);
+      const std::vector<uint16_t> gk = ToHost<uint16_t>(gpu.ctx, pool.k_slab(layer),
+                                                        static_cast<int64_t>(slab_n));
+      const std::vector<uint16_t> gv = ToHost<uint16_t>(gpu.ctx, pool.v_slab(layer),
+                                                        static_cast<int64_t>(slab_n));
+      EXPECT(std::memcmp(gk.data(), mk.data() + off, slab_n * 2) == 0);
+      EXPECT(std::memcmp(gv.data(), mv.data() + off, slab_n * 2) == 0);
+    }
+  }
+  // Tables one position short of the longest row: rejected, nothing launched.
+  ASSERT_OK(asmb.AssembleDecode(std::vector<BatchSeqInput>{{std::vector<int32_t>(1, 1), &caches[1]}}));
+  ASSERT_OK(attn.Upload(asmb.inputs()));
+  const int64_t need = asmb.inputs().context_lens[0];
+  DeviceBuffer q1, k1, v1, o1;
+  ASSERT_OK(q1.Reserve(gpu.ctx, H * d * 4));
+  ASSERT_OK(k1.Reserve(gpu.ctx, Hkv * d * 4));
+  ASSERT_OK(v1.Reserve(gpu.ctx, Hkv * d * 4));
+  ASSERT_OK(o1.Reserve(gpu.ctx, H * d * 4));
+  const BatchedAttention::RopeTables short_rope{rope.d_cos, rope.d_sin, need - 1};
+  EXPECT_CODE(attn.ForwardLayerRope(0, static_cast<float*>(q1.get()), static_cast<float*>(k1.get()),
+                                    static_cast<float*>(v1.get()), short_rope,
+                                    static_cast<float*>(o1.get())),
+              StatusCode::kInvalidArgument);
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {

@@ -317,3 +317,41 @@ def test_scatter_closed_form_and_round_trip(orc):
     vb = np.zeros_like(kb)
     orc.kv_scatter(sk, sv, slots, Hkv, d, bs, kb, vb)
     assert np.array_equal(kb, orc.to_bf16_bits(ksl) * (ksl != 0) + 0 * kb)
+
+
+# ------------------------------------------------------------------ RoPE (src/kernels/rope.h)
+@needs_ref
+@pytest.mark.parametrize("isa", [0, 1])
+@pytest.mark.parametrize("d", [10, 64, 72, 128, 130])
+def test_rope_bit_exact_vs_reference_build(orc, isa, d):
+    rng = np.random.default_rng(d + 100 * isa)
+    x = normal(rng, (11, 3, d))
+    c, s = orc.rope_tables(d, 4096, theta=500000.0)
+    pos = rng.integers(0, 4096, 11).astype(np.int32)
+    pos[3] = pos[4]  # repeated positions are allowed (rope.h:18-20)
+    ours = orc.rope_apply(x, pos, c, s, isa=isa)
+    theirs = orc.rope_apply(x, pos, c, s, isa=isa, use_ref=True)
+    assert np.array_equal(ours.view(np.uint32), theirs.view(np.uint32))
+
+
+@pytest.mark.parametrize("isa", [0, 1])
+def test_rope_closed_forms(orc, isa):
+    """Position 0 is the identity; each (j, j + d/2) pair is rotated by the
+    table angle (fp64 rotation within fp32 rounding); pair norms are kept."""
+    rng = np.random.default_rng(9)
+    d = 64
+    x = normal(rng, (6, 4, d))
+    c, s = orc.rope_tables(d, 1000)
+    pos = np.array([0, 1, 17, 999, 500, 0], np.int32)
+    y = orc.rope_apply(x, pos, c, s, isa=isa)
+    assert np.array_equal(y[0], x[0]) and np.array_equal(y[5], x[5])
+    lo, hi = x[..., : d // 2].astype(np.float64), x[..., d // 2:].astype(np.float64)
+    cc, ss = c[pos][:, None, :].astype(np.float64), s[pos][:, None, :].astype(np.float64)
+    want = np.concatenate([lo * cc - hi * ss, hi * cc + lo * ss], axis=-1)
+    assert np.abs(y - want).max() <= 4e-7 * max(1.0, np.abs(want).max())
+    n0 = lo ** 2 + hi ** 2
+    n1 = y[..., : d // 2].astype(np.float64) ** 2 + y[..., d // 2:].astype(np.float64) ** 2
+    assert np.allclose(n0, n1, rtol=2e-6, atol=1e-7)
+    # The FMA (AVX2) and two-rounding (scalar) forms differ by at most an ulp or so.
+    other = orc.rope_apply(x, pos, c, s, isa=1 - isa)
+    assert np.abs(y - other).max() <= 4e-7 * max(1.0, np.abs(y).max())
