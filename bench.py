@@ -173,6 +173,48 @@ def time_chunks(ctx, ehip, w, slabs, qs, outs, layers, reps=5):
                          "kernel": "causal prefill chunks (bf16 MFMA)"}}
 
 
+def time_rope_append(ctx, ehip, w, slabs, qs, kns, vns, layers, reps=5):
+    """The fused RoPE + KV append (ehip_step_rope_kv_append) against the plain
+    append, one launch per layer each, on the workload's own step. Bytes of
+    the fused kernel per launch: q read and written, new K/V rows read (fp32),
+    one cos and one sin row per query row, K/V written to the slab."""
+    H, Hkv, d, R = w.heads, w.kv_heads, w.head_dim, w.rows
+    n_pos = int(w.context_lens.max())
+    half = d // 2
+    pos = np.arange(n_pos, dtype=np.float32)[:, None]
+    inv = (1.0 / np.power(10000.0, np.arange(half, dtype=np.float64) * 2.0 / d)).astype(np.float32)
+    ang = pos * inv[None, :]
+    cos = ctx.to_device(np.cos(ang).astype(np.float32))
+    sin = ctx.to_device(np.sin(ang).astype(np.float32))
+    g = ehip.geometry(H, Hkv, d, w.block_size, w.kv_dtype, w.pool_blocks, w.scale)
+    ctx._check(ctx.step_upload(g, ehip.StepArrays(w.query_lens, w.context_lens, w.tables,
+                                                  w.slot_mapping)))
+    out = {}
+    for name in ("plain", "rope"):
+        ev = [(ctx.event(), ctx.event()) for _ in range(reps * layers)]
+        for r in range(reps + 1):
+            for layer in range(layers):
+                ks, vs = slabs[layer]
+                if r:
+                    ctx.record(ev[(r - 1) * layers + layer][0])
+                if name == "rope":
+                    ctx._check(ctx.step_rope_kv_append(qs[layer], kns[layer], vns[layer], cos,
+                                                       sin, n_pos, ks, vs))
+                else:
+                    ctx._check(ctx.step_kv_append(kns[layer], vns[layer], ks, vs))
+                if r:
+                    ctx.record(ev[(r - 1) * layers + layer][1])
+        ctx.sync()
+        out[name] = float(np.mean([ctx.elapsed_ms(a, b) for a, b in ev])) / 1e3
+    cos.free()
+    sin.free()
+    nbytes = R * (2 * H * d * 4 + 2 * Hkv * d * 4 + d * 4 + 2 * Hkv * d * w.kv_bytes)
+    return {"rows": R, "bytes_per_launch": nbytes,
+            "us_per_launch": round(out["rope"] * 1e6, 2),
+            "gbps": round(nbytes / out["rope"] / 1e9, 1),
+            "plain_append_us_per_launch": round(out["plain"] * 1e6, 2)}
+
+
 def c5_reprefill(ctx, ehip, w, slabs, layers, reps=3):
     """C5's preempt-and-recompute event: one evicted sequence re-prefilled as
     a 4096-token causal chunk (P = 0), per layer, on the C5 pools."""
@@ -348,6 +390,9 @@ def main():
     if pre is not None:
         result["prefill"] = pre
         log(f"[bench] prefill chunks: {pre['us_per_layer']} us/layer, {pre['tflops']} TFLOP/s")
+    ra = time_rope_append(ctx, ehip, w, slabs, qs, kns, vns, layers)
+    result["rope_append"] = ra
+    log(f"[bench] fused RoPE + append: {ra}")
     if w.name == "C5":
         ev = c5_reprefill(ctx, ehip, w, slabs, layers)
         result["reprefill_event"] = ev

@@ -105,58 +105,85 @@ __global__ __launch_bounds__(256) void KvScatterScalar(const float* __restrict__
 // consecutive pairs of one (row, head): heads [0, H) are q, [H, H + Hkv) the
 // k/v rows, whose v is copied unrotated. The source K rows are left as they
 // were (the rotated rows live in the slab).
+template <int W>
+struct Pairs {
+  float v[W];
+};
+
+template <int W>
+__device__ __forceinline__ Pairs<W> LoadPairs(const float* p) {
+  Pairs<W> r;
+  if constexpr (W == 4) {
+    const float4 x = *reinterpret_cast<const float4*>(p);
+    r.v[0] = x.x, r.v[1] = x.y, r.v[2] = x.z, r.v[3] = x.w;
+  } else {
+#pragma unroll
+    for (int w = 0; w < W; ++w) r.v[w] = p[w];
+  }
+  return r;
+}
+
+template <int W>
+__device__ __forceinline__ void StorePairs(float* p, const Pairs<W>& r) {
+  if constexpr (W == 4) {
+    *reinterpret_cast<float4*>(p) = make_float4(r.v[0], r.v[1], r.v[2], r.v[3]);
+  } else {
+#pragma unroll
+    for (int w = 0; w < W; ++w) p[w] = r.v[w];
+  }
+}
+
+template <class KV, int W>
+__device__ __forceinline__ void StorePairs(KV* p, const Pairs<W>& r) {
+  if constexpr (W == 4) {
+    Store4<KV>(p, make_float4(r.v[0], r.v[1], r.v[2], r.v[3]));
+  } else {
+#pragma unroll
+    for (int w = 0; w < W; ++w) Store1(p + w, r.v[w]);
+  }
+}
+
+// Grid: x = query row (its position, slot and table entry are wavefront-
+// uniform), y strides over the row's (head, pair group) items.
 template <class KV, int W>
 __global__ __launch_bounds__(256) void RopeKvAppend(
     float* __restrict__ q, const float* __restrict__ src_k, const float* __restrict__ src_v,
     const RowDesc* __restrict__ rows, const float* __restrict__ cos_t,
-    const float* __restrict__ sin_t, const int64_t* __restrict__ slots, int64_t n_rows, int heads,
-    int kv_heads, int d, int bs, int64_t slab_blocks, KV* k_slab, KV* v_slab, int32_t* err) {
+    const float* __restrict__ sin_t, const int64_t* __restrict__ slots, int heads, int kv_heads,
+    int d, int bs, int64_t slab_blocks, KV* k_slab, KV* v_slab, int32_t* err) {
   const int half = d >> 1;
   const int fused = half & ~7;  // pairs the AVX2 kernel handles 8 at a time
   const int gpr = half / W;     // pair groups per head row
-  const int64_t per_row = int64_t{heads + kv_heads} * gpr;
-  const int64_t n = n_rows * per_row;
-  for (int64_t i = blockIdx.x * int64_t{blockDim.x} + threadIdx.x; i < n;
-       i += int64_t{gridDim.x} * blockDim.x) {
-    const int64_t r = i / per_row;
-    const int rem = static_cast<int>(i - r * per_row);
+  const int per_row = (heads + kv_heads) * gpr;
+  const int64_t r = blockIdx.x;
+  const int64_t p = rows[r].length - 1;
+  const int64_t slot = slots[r];
+  for (int rem = blockIdx.y * blockDim.x + threadIdx.x; rem < per_row;
+       rem += gridDim.y * blockDim.x) {
     const int hh = rem / gpr;
     const int j = (rem - hh * gpr) * W;
-    const int64_t p = rows[r].length - 1;
-    const float* cr = cos_t + p * half + j;
-    const float* sr = sin_t + p * half + j;
-    float lo[W], hi[W], c[W], s[W];
-    const float* x = hh < heads ? q + (r * heads + hh) * d
-                                : src_k + (r * kv_heads + (hh - heads)) * d;
-#pragma unroll
-    for (int w = 0; w < W; ++w) {
-      lo[w] = x[j + w];
-      hi[w] = x[j + half + w];
-      c[w] = cr[w];
-      s[w] = sr[w];
-    }
-    float ro[W], rh[W];
+    const bool is_q = hh < heads;
+    const float* x = is_q ? q + (r * heads + hh) * d : src_k + (r * kv_heads + (hh - heads)) * d;
+    const Pairs<W> lo = LoadPairs<W>(x + j), hi = LoadPairs<W>(x + j + half);
+    const Pairs<W> c = LoadPairs<W>(cos_t + p * half + j), s = LoadPairs<W>(sin_t + p * half + j);
+    Pairs<W> ro, rh;
 #pragma unroll
     for (int w = 0; w < W; ++w) {
       if (j + w < fused) {
-        ro[w] = fmaf(-hi[w], s[w], lo[w] * c[w]);
-        rh[w] = fmaf(lo[w], s[w], hi[w] * c[w]);
+        ro.v[w] = fmaf(-hi.v[w], s.v[w], lo.v[w] * c.v[w]);
+        rh.v[w] = fmaf(lo.v[w], s.v[w], hi.v[w] * c.v[w]);
       } else {
-        ro[w] = fmaf(lo[w], c[w], -(hi[w] * s[w]));
-        rh[w] = fmaf(hi[w], c[w], lo[w] * s[w]);
+        ro.v[w] = fmaf(lo.v[w], c.v[w], -(hi.v[w] * s.v[w]));
+        rh.v[w] = fmaf(hi.v[w], c.v[w], lo.v[w] * s.v[w]);
       }
     }
-    if (hh < heads) {
+    if (is_q) {
       float* xq = q + (r * heads + hh) * d;
-#pragma unroll
-      for (int w = 0; w < W; ++w) {
-        xq[j + w] = ro[w];
-        xq[j + half + w] = rh[w];
-      }
+      StorePairs<W>(xq + j, ro);
+      StorePairs<W>(xq + j + half, rh);
       continue;
     }
     const int h = hh - heads;
-    const int64_t slot = slots[r];
     if (slot < 0 || slot >= slab_blocks * bs) {
       atomicOr(err, kErrSlotRange);
       continue;
@@ -164,20 +191,10 @@ __global__ __launch_bounds__(256) void RopeKvAppend(
     const int64_t block = slot / bs;
     const int64_t dst = ((block * kv_heads + h) * bs + (slot - block * bs)) * d;
     const float* xv = src_v + (r * kv_heads + h) * d;
-    if constexpr (W == 4) {
-      Store4<KV>(k_slab + dst + j, make_float4(ro[0], ro[1], ro[2], ro[3]));
-      Store4<KV>(k_slab + dst + j + half, make_float4(rh[0], rh[1], rh[2], rh[3]));
-      Store4<KV>(v_slab + dst + j, *reinterpret_cast<const float4*>(xv + j));
-      Store4<KV>(v_slab + dst + j + half, *reinterpret_cast<const float4*>(xv + j + half));
-    } else {
-#pragma unroll
-      for (int w = 0; w < W; ++w) {
-        Store1(k_slab + dst + j + w, ro[w]);
-        Store1(k_slab + dst + j + half + w, rh[w]);
-        Store1(v_slab + dst + j + w, xv[j + w]);
-        Store1(v_slab + dst + j + half + w, xv[j + half + w]);
-      }
-    }
+    StorePairs<KV, W>(k_slab + dst + j, ro);
+    StorePairs<KV, W>(k_slab + dst + j + half, rh);
+    StorePairs<KV, W>(v_slab + dst + j, LoadPairs<W>(xv + j));
+    StorePairs<KV, W>(v_slab + dst + j + half, LoadPairs<W>(xv + j + half));
   }
 }
 
@@ -247,11 +264,16 @@ hipError_t LaunchRopeKvAppend(float* q, const float* src_k, const float* src_v,
                    reinterpret_cast<uintptr_t>(src_v) % 16 == 0 &&
                    reinterpret_cast<uintptr_t>(cos_t) % 16 == 0 &&
                    reinterpret_cast<uintptr_t>(sin_t) % 16 == 0;
-  const int64_t n = n_rows * (heads + kv_heads) * (d / 2) / (vec ? 4 : 1);
-  const dim3 grid(GridFor(n, 256)), block(256);
+  if (n_rows <= 0) return hipSuccess;
+  if (n_rows > 0x7FFFFFFF) return hipErrorInvalidValue;
+  const int64_t per_row = int64_t{heads + kv_heads} * (d / 2) / (vec ? 4 : 1);
+  const int threads = per_row >= 256 ? 256 : static_cast<int>((per_row + 63) / 64 * 64);
+  const int64_t ys = (per_row + threads - 1) / threads;
+  const dim3 grid(static_cast<uint32_t>(n_rows), static_cast<uint32_t>(ys < 65535 ? ys : 65535)),
+      block(threads);
 #define EHIP_ROPE_LAUNCH(KV, W)                                                               \
   hipLaunchKernelGGL((RopeKvAppend<KV, W>), grid, block, 0, stream, q, src_k, src_v, rows,   \
-                     cos_t, sin_t, slots, n_rows, heads, kv_heads, d, bs, slab_blocks,        \
+                     cos_t, sin_t, slots, heads, kv_heads, d, bs, slab_blocks,                \
                      static_cast<KV*>(k_slab), static_cast<KV*>(v_slab), err)
   if (kv_dtype == EHIP_KV_BF16) {
     if (vec)
