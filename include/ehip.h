@@ -237,6 +237,11 @@ int ehip_step_info(const ehip_ctx* ctx, int64_t* rows, int64_t* items, int64_t* 
 int ehip_plan_counts(const ehip_geometry* geom, const ehip_step_desc* step, int64_t* rows,
                      int64_t* items, int64_t* partials, int32_t* split_tokens,
                      int64_t* joint_items, int64_t* shared_tokens);
+/* The work list of the same plan, in dispatch order, for tests of the host
+ * logic: six int32 per item {row, joint_row (-1 if none), key_begin, key_end,
+ * kv_head, split}. Writes at most cap items; *n gets the item count. */
+int ehip_plan_items(const ehip_geometry* geom, const ehip_step_desc* step, int32_t* out,
+                    int64_t cap, int64_t* n);
 
 #ifdef __cplusplus
 }

@@ -34,6 +34,9 @@ struct ehip_ctx {
   float* d_part = nullptr;
   size_t d_part_bytes = 0;
   int32_t* d_err = nullptr;
+  // Item-queue counters of the persistent decode kernel: two words of the
+  // error page (zeroed at creation), used in turn by successive launches.
+  ehip::QueueState queue{};
 
   // The uploaded step.
   bool have_step = false;
@@ -256,7 +259,7 @@ int LaunchAttention(ehip_ctx* ctx, const float* q, const void* k_slab, const voi
   p.d = g.head_dim;
   p.bs = g.block_size;
   p.scale_log2 = g.scale * 1.4426950408889634f;
-  EHIP_HIP(ctx, ehip::LaunchDecode(p, g.kv_dtype, ctx->stream));
+  EHIP_HIP(ctx, ehip::LaunchDecode(p, g.kv_dtype, &ctx->queue, ctx->stream));
   return EHIP_OK;
 }
 
@@ -294,6 +297,9 @@ int ehip_init(int device, ehip_ctx** out) {
     if (e != hipSuccess) { rc = HipFail(ctx, e, "hipMalloc(err)"); break; }
     e = hipMemset(ctx->d_err, 0, 256);
     if (e != hipSuccess) { rc = HipFail(ctx, e, "hipMemset(err)"); break; }
+    // Page words: 0 range flags, 32 probe sink, 48-49 decode item queue.
+    ctx->queue.d_pair = reinterpret_cast<uint32_t*>(ctx->d_err) + 48;
+    ctx->queue.parity = 0;
   } while (false);
   if (rc != EHIP_OK) {
     ehip_destroy(ctx);
@@ -731,6 +737,27 @@ int ehip_plan_counts(const ehip_geometry* geom, const ehip_step_desc* step, int6
   if (split_tokens) *split_tokens = plan.split_tokens;
   if (joint_items) *joint_items = plan.joint_items;
   if (shared_tokens) *shared_tokens = plan.shared_tokens;
+  return EHIP_OK;
+}
+
+int ehip_plan_items(const ehip_geometry* geom, const ehip_step_desc* step, int32_t* out,
+                    int64_t cap, int64_t* n) {
+  if (!geom || !step || !n || cap < 0 || (cap > 0 && !out)) return EHIP_INVALID_ARGUMENT;
+  Plan plan;
+  std::string err;
+  if (int rc = ehip::BuildPlan(*geom, *step, &plan, &err)) return rc;
+  *n = static_cast<int64_t>(plan.items.size());
+  const int64_t m = std::min<int64_t>(cap, *n);
+  for (int64_t i = 0; i < m; ++i) {
+    const ehip::WorkItem& w = plan.items[static_cast<size_t>(i)];
+    int32_t* o = out + 6 * i;
+    o[0] = w.row0;
+    o[1] = w.row1;
+    o[2] = w.tok_begin;
+    o[3] = w.tok_end;
+    o[4] = w.hk_split & ((1 << ehip::kHkBits) - 1);
+    o[5] = w.hk_split >> ehip::kHkBits;
+  }
   return EHIP_OK;
 }
 

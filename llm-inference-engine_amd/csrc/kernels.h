@@ -40,6 +40,15 @@ struct DecodeParams {
   int32_t d;
   int32_t bs;
   float scale_log2;         // scale * log2(e)
+  uint32_t* queue;          // this launch's item counter (zero at launch; MFMA kernel only)
+  uint32_t* queue_next;     // the counter of the next launch, cleared by this one
+};
+
+// Two item-queue counters of a context: a launch draws tickets from
+// d_pair[parity] and clears d_pair[1 - parity], then the parity flips.
+struct QueueState {
+  uint32_t* d_pair;
+  int parity;
 };
 
 struct PrefillParams {
@@ -77,11 +86,12 @@ int PrefillRowsPerItem(int kv_dtype, int d, int group, int bs, int64_t slab_byte
 // item; picks the specialised (dtype, d, g) kernel or the generic one), then,
 // if any row was split, the merge of the split partials. The kernel boundary
 // between the two publishes the partials: no device-wide fences or counters.
-hipError_t LaunchDecode(const DecodeParams& p, int kv_dtype, hipStream_t stream);
+hipError_t LaunchDecode(const DecodeParams& p, int kv_dtype, QueueState* queue, hipStream_t stream);
 
 // bf16-KV decode with QK^T on MFMA; returns false (nothing launched) when the
 // shape is not covered (d not 64/128, g not 1/2/4/8, bs < 16, misaligned).
-bool LaunchDecodeMfma(const DecodeParams& p, hipStream_t stream, hipError_t* err);
+bool LaunchDecodeMfma(const DecodeParams& p, QueueState* queue, hipStream_t stream,
+                      hipError_t* err);
 
 // KvScatter: rows [T, Hkv, d] fp32 into slabs (fp32 copy or bf16 RNE).
 hipError_t LaunchKvScatter(const float* src_k, const float* src_v, const int64_t* slots,

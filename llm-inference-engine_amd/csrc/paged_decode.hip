@@ -482,22 +482,24 @@ hipError_t LaunchTyped(const DecodeParams& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-hipError_t LaunchSplits(const DecodeParams& p, int kv_dtype, hipStream_t stream) {
+hipError_t LaunchSplits(const DecodeParams& p, int kv_dtype, QueueState* queue,
+                        hipStream_t stream) {
   if (kv_dtype != EHIP_KV_BF16) return LaunchTyped<float>(p, stream);
   // EHIP_DECODE_KERNEL=valu selects the all-VALU kernel for bf16 as well.
   const char* pick = std::getenv("EHIP_DECODE_KERNEL");
   if (!(pick && std::strcmp(pick, "valu") == 0)) {
     hipError_t err = hipSuccess;
-    if (LaunchDecodeMfma(p, stream, &err)) return err;
+    if (LaunchDecodeMfma(p, queue, stream, &err)) return err;
   }
   return LaunchTyped<uint16_t>(p, stream);
 }
 
 }  // namespace
 
-hipError_t LaunchDecode(const DecodeParams& p, int kv_dtype, hipStream_t stream) {
+hipError_t LaunchDecode(const DecodeParams& p, int kv_dtype, QueueState* queue,
+                        hipStream_t stream) {
   // Split rows may come from prefill key splits alone (no decode items).
-  hipError_t e = p.n_items > 0 ? LaunchSplits(p, kv_dtype, stream) : hipSuccess;
+  hipError_t e = p.n_items > 0 ? LaunchSplits(p, kv_dtype, queue, stream) : hipSuccess;
   if (e != hipSuccess || p.n_merge == 0) return e;
   // Only the rows that were split: a step dominated by prefill-chunk rows
   // (which need no merge) launches no idle merge blocks.

@@ -92,8 +92,20 @@ void DecodeMfmaBf16(DecodeParams p) {
   __shared__ uint4 q_lds[QL ? 2 * NC * 64 : 1];
 
   const int lane = threadIdx.x;
-  const int item_idx = blockIdx.x;
-  if (item_idx >= p.n_items) return;
+  // Persistent wavefronts: a workgroup's first item is its index; each later
+  // one is gridDim.x plus a ticket from the launch's queue counter. The ticket
+  // is drawn when at most kDrawAhead keys of the current item remain: late
+  // enough that items go to the wavefronts that free up first (longest-first
+  // list scheduling: the queue hands out the short items last, so the
+  // wavefronts finish together), early enough to hide the atomic's latency.
+  // The first wavefront clears the counter the next launch on the stream
+  // will use (this launch's own counter was cleared by the launch before it,
+  // or at context creation).
+  constexpr int kDrawAhead = 64;
+  if (blockIdx.x == 0 && lane == 0) *p.queue_next = 0u;
+  for (int item_idx = blockIdx.x; item_idx < p.n_items;) {
+  uint32_t ticket = 0;
+  bool drawn = false;
   const ItemRef it = DecodeItem(p.items[item_idx]);
   const int nrows = it.nrows;  // <= RMAX (the host launches RMAX = 2 only for joint plans)
   const int hk = it.hk;
@@ -200,6 +212,10 @@ void DecodeMfmaBf16(DecodeParams p) {
   for (int h = 0; h < GV; ++h) o[h][0] = o[h][1] = 0.f;
 
   auto process = [&](const T& t, int t0) {
+    if (!drawn && t0 + kDrawAhead >= te) {  // wavefront-uniform
+      drawn = true;
+      if (lane == 0) ticket = atomicAdd(p.queue, 1u);
+    }
     f32x4_t acc[TH];
 #pragma unroll
     for (int h2 = 0; h2 < TH; ++h2) {
@@ -363,29 +379,62 @@ void DecodeMfmaBf16(DecodeParams p) {
       }
     }
   }
+  item_idx = static_cast<int>(gridDim.x + __builtin_amdgcn_readfirstlane(ticket));
+  }
+}
+
+// Workgroups (one wavefront each) a launch keeps resident: the kernel's
+// occupancy per CU times the CU count.
+template <class K>
+int ResidentWaves(K kernel) {
+  int dev = 0, cus = 0, per_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 64, 0) != hipSuccess)
+    return 0;
+  return cus * per_cu;
+}
+
+template <class K>
+void LaunchPersistent(K kernel, const DecodeParams& p, hipStream_t stream, bool persist) {
+  int grid = p.n_items;
+  if (persist) {
+    // EHIP_DECODE_SLOTS caps the grid below the resident count (tests use it
+    // to make every wavefront take many items from the queue).
+    int slots = ResidentWaves(kernel);
+    if (const char* cap = std::getenv("EHIP_DECODE_SLOTS")) {
+      const long c = std::strtol(cap, nullptr, 10);
+      if (c > 0 && (slots <= 0 || c < slots)) slots = static_cast<int>(c);
+    }
+    if (slots > 0 && slots < grid) grid = slots;
+  }
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(64), 0, stream, p);
 }
 
 template <int D, int G, int RMAX>
-void LaunchShape(const DecodeParams& p, hipStream_t stream, bool wide, bool deep) {
+void LaunchShape(const DecodeParams& p, hipStream_t stream, bool wide, bool deep, bool persist) {
   // Two wavefronts per SIMD wherever the shape fits 256 registers without
   // spilling (the 16-virtual-head and triple-buffered 128-wide shapes do not).
   constexpr bool QL = D * G * RMAX >= 1024;
   constexpr int OCC = (D == 128 && G * RMAX >= 16) ? 1 : 2;
   constexpr int OCC3 = D == 128 ? 1 : 2;
-  const dim3 grid(p.n_items), block(64);
   if (wide && deep)
-    hipLaunchKernelGGL((DecodeMfmaBf16<D, G, RMAX, 2, 3, QL, OCC3>), grid, block, 0, stream, p);
+    LaunchPersistent(DecodeMfmaBf16<D, G, RMAX, 2, 3, QL, OCC3>, p, stream, persist);
   else if (wide)
-    hipLaunchKernelGGL((DecodeMfmaBf16<D, G, RMAX, 2, 2, QL, OCC>), grid, block, 0, stream, p);
+    LaunchPersistent(DecodeMfmaBf16<D, G, RMAX, 2, 2, QL, OCC>, p, stream, persist);
   else if (deep)
-    hipLaunchKernelGGL((DecodeMfmaBf16<D, G, RMAX, 1, 3, QL, OCC3>), grid, block, 0, stream, p);
+    LaunchPersistent(DecodeMfmaBf16<D, G, RMAX, 1, 3, QL, OCC3>, p, stream, persist);
   else
-    hipLaunchKernelGGL((DecodeMfmaBf16<D, G, RMAX, 1, 2, QL, OCC>), grid, block, 0, stream, p);
+    LaunchPersistent(DecodeMfmaBf16<D, G, RMAX, 1, 2, QL, OCC>, p, stream, persist);
 }
 
 }  // namespace
 
-bool LaunchDecodeMfma(const DecodeParams& p, hipStream_t stream, hipError_t* err) {
+bool LaunchDecodeMfma(const DecodeParams& params, QueueState* queue, hipStream_t stream,
+                      hipError_t* err) {
+  DecodeParams p = params;
+  p.queue = queue->d_pair + queue->parity;
+  p.queue_next = queue->d_pair + (1 - queue->parity);
   const bool aligned = (reinterpret_cast<uintptr_t>(p.k_slab) % 16 == 0) &&
                        (reinterpret_cast<uintptr_t>(p.v_slab) % 16 == 0) &&
                        (reinterpret_cast<uintptr_t>(p.q) % 16 == 0) &&
@@ -400,14 +449,21 @@ bool LaunchDecodeMfma(const DecodeParams& p, hipStream_t stream, hipError_t* err
   const char* bufs = std::getenv("EHIP_DECODE_BUFS");
   const bool deep = bufs && std::strcmp(bufs, "3") == 0;
   const bool joint = p.n_joint > 0;
-#define EHIP_MFMA_CASE(DD, GG)                          \
-  if (p.d == DD && p.group == GG) {                     \
-    if (joint)                                          \
-      LaunchShape<DD, GG, 2>(p, stream, wide, deep);    \
-    else                                                \
-      LaunchShape<DD, GG, 1>(p, stream, wide, deep);    \
-    *err = hipGetLastError();                           \
-    return true;                                        \
+  // EHIP_DECODE_PERSIST=0: one workgroup per item (the hardware dispatcher
+  // hands out the items instead of the queue).
+  const char* pers = std::getenv("EHIP_DECODE_PERSIST");
+  const bool persist = !(pers && std::strcmp(pers, "0") == 0);
+  // The counters swap roles only after a launch was enqueued, so the one the
+  // next launch uses is always the one this launch clears.
+#define EHIP_MFMA_CASE(DD, GG)                                   \
+  if (p.d == DD && p.group == GG) {                              \
+    if (joint)                                                   \
+      LaunchShape<DD, GG, 2>(p, stream, wide, deep, persist);    \
+    else                                                         \
+      LaunchShape<DD, GG, 1>(p, stream, wide, deep, persist);    \
+    *err = hipGetLastError();                                    \
+    if (*err == hipSuccess) queue->parity ^= 1;                  \
+    return true;                                                 \
   }
   EHIP_MFMA_CASE(128, 1)
   EHIP_MFMA_CASE(128, 2)

@@ -9,7 +9,10 @@ namespace ehip {
 namespace {
 
 constexpr int32_t kTile = 64;             // split lengths are whole 64-key units
-constexpr int64_t kTargetItems = 7680;    // ~7.5 wavefront work items per SIMD (1024 SIMDs)
+// ~2 work items per resident decode wavefront (2048 on MI355X): fewer, longer
+// items measured faster than ~7.5 per SIMD (each item pays its descriptor,
+// query and first-tile round trips).
+constexpr int64_t kTargetItems = 4096;
 constexpr int32_t kMinSplit = 128;
 constexpr int32_t kMaxSplitsPerRow = 64;  // bounds the merge a single wave performs
 
@@ -69,7 +72,12 @@ int32_t ChooseSplitTokens(const ehip_geometry& g, int64_t unit_tokens) {
     const long v = std::strtol(env, nullptr, 10);
     if (v > 0) return static_cast<int32_t>(std::min<int64_t>(RoundUp(v, kTile), max_split));
   }
-  int64_t s = (unit_tokens + kTargetItems - 1) / kTargetItems;
+  int64_t target = kTargetItems;
+  if (const char* env = std::getenv("EHIP_TARGET_ITEMS")) {
+    const long v = std::strtol(env, nullptr, 10);
+    if (v > 0) target = v;
+  }
+  int64_t s = (unit_tokens + target - 1) / target;
   s = RoundUp(std::max<int64_t>(s, kMinSplit), kTile);
   return static_cast<int32_t>(std::min<int64_t>(s, max_split));
 }
@@ -88,6 +96,11 @@ int32_t SharedFullBlocks(const Plan& plan, const RowDesc& a, const RowDesc& b, i
   while (c < limit && ta[c] == tb[c]) ++c;
   return c;
 }
+
+// One key range of a row (or of a joint pair a, b over their shared prefix).
+struct KeyRange {
+  int32_t a, b, tb, te;
+};
 
 // Pairs rows that share leading blocks (greedy over rows ordered by their
 // first block id and table), splits every row into whole-tile key ranges
@@ -152,14 +165,45 @@ void FinishPlan(const ehip_geometry& g, Plan* plan, bool allow_joint,
     split_len[a] = split_len[b] = std::max(split_len[a], split_len[b]);
   }
 
+  // Key ranges: a group's shared prefix [0, P) in joint ranges, then each
+  // row's own keys [P, L), in pieces of the row's split length. Every range
+  // becomes one work item per kv head.
+  std::vector<KeyRange> ranges;
+  for (size_t k = 0; k < plan->groups.size(); k += kMaxJointRows) {
+    const int32_t a = plan->groups[k];
+    const int32_t sl = split_len[a], P = joint_len[a];
+    for (int32_t t = 0; t < P; t += sl)
+      ranges.push_back(KeyRange{a, plan->groups[k + 1], t, std::min(P, t + sl)});
+  }
+  for (size_t r = 0; r < n; ++r) {
+    if (skipped(r)) continue;
+    const int32_t sl = split_len[r];
+    for (int32_t t = joint_len[r]; t < plan->rows[r].length; t += sl)
+      ranges.push_back(KeyRange{static_cast<int32_t>(r), -1, t,
+                                std::min(plan->rows[r].length, t + sl)});
+  }
+
+  // Split indices follow key order within a row. Joint ranges cover the
+  // leading keys of both members, so numbering them first (in key order)
+  // gives both members the same index for each.
+  std::stable_sort(ranges.begin(), ranges.end(), [](const KeyRange& x, const KeyRange& y) {
+    const bool jx = x.b >= 0, jy = y.b >= 0;
+    if (jx != jy) return jx;
+    return x.a != y.a ? x.a < y.a : x.tb < y.tb;
+  });
+  size_t n_joint_ranges = 0;
+  while (n_joint_ranges < ranges.size() && ranges[n_joint_ranges].b >= 0) ++n_joint_ranges;
+  std::vector<int32_t> nsplit(n, 0), split_of(ranges.size());
+  for (size_t i = 0; i < ranges.size(); ++i) {
+    split_of[i] = nsplit[ranges[i].a]++;
+    if (ranges[i].b >= 0) ++nsplit[ranges[i].b];
+  }
   int64_t split_base = 0;
   plan->any_split = false;
   plan->merge_rows.clear();
   for (size_t r = 0; r < n; ++r) {
     RowDesc& rd = plan->rows[r];
-    const int32_t sl = split_len[r], P = joint_len[r];
-    rd.nsplit = skipped(r) ? ((*skip)[r] > 1 ? (*skip)[r] : 0)
-                           : (P + sl - 1) / sl + (rd.length - P + sl - 1) / sl;
+    rd.nsplit = skipped(r) ? ((*skip)[r] > 1 ? (*skip)[r] : 0) : nsplit[r];
     rd.split_base = static_cast<int32_t>(split_base);
     split_base += rd.nsplit;
     plan->any_split = plan->any_split || rd.nsplit > 1;
@@ -168,25 +212,14 @@ void FinishPlan(const ehip_geometry& g, Plan* plan, bool allow_joint,
   plan->partials = split_base * g.kv_heads;
 
   plan->items.clear();
-  for (size_t k = 0; k < plan->groups.size(); k += kMaxJointRows) {
-    const int32_t a = plan->groups[k];
-    const int32_t sl = split_len[a], P = joint_len[a];
+  plan->items.reserve(ranges.size() * g.kv_heads);
+  for (size_t i = 0; i < ranges.size(); ++i) {
+    const KeyRange& kr = ranges[i];
     for (int32_t hk = 0; hk < g.kv_heads; ++hk)
-      for (int32_t s = 0, t = 0; t < P; ++s, t += sl)
-        plan->items.push_back(WorkItem{a, plan->groups[k + 1], t, std::min(P, t + sl),
-                                       PackHkSplit(hk, s), plan->rows[a].table_off, 0, 0});
+      plan->items.push_back(WorkItem{kr.a, kr.b, kr.tb, kr.te, PackHkSplit(hk, split_of[i]),
+                                     plan->rows[kr.a].table_off, 0, 0});
   }
-  plan->joint_items = static_cast<int64_t>(plan->items.size());
-  for (size_t r = 0; r < n; ++r) {
-    if (skipped(r)) continue;
-    const RowDesc& rd = plan->rows[r];
-    const int32_t sl = split_len[r], P = joint_len[r];
-    const int32_t s0 = (P + sl - 1) / sl;
-    for (int32_t hk = 0; hk < g.kv_heads; ++hk)
-      for (int32_t s = s0, t = P; t < rd.length; ++s, t += sl)
-        plan->items.push_back(WorkItem{static_cast<int32_t>(r), -1, t, std::min(rd.length, t + sl),
-                                       PackHkSplit(hk, s), rd.table_off, 0, 0});
-  }
+  plan->joint_items = static_cast<int64_t>(n_joint_ranges) * g.kv_heads;
   // Longest key range first, so the tail of the dispatch is short items.
   std::stable_sort(plan->items.begin(), plan->items.end(),
                    [](const WorkItem& x, const WorkItem& y) {

@@ -98,6 +98,7 @@ def lib():
             "ehip_step_info": [_vp, _I64P, _I64P, _I64P],
             "ehip_plan_counts": [C.POINTER(Geometry), C.POINTER(StepDesc), _I64P, _I64P, _I64P,
                                  C.POINTER(C.c_int32), _I64P, _I64P],
+            "ehip_plan_items": [C.POINTER(Geometry), C.POINTER(StepDesc), _vp, _i64, _I64P],
             "ehip_probe_stream_read": [_vp, _vp, _i64, _i32, _i32, C.POINTER(C.c_float)],
             "ehip_probe_tile_gather": [_vp, _vp, _vp, _i64, _vp, _i64, _i32, _i32, _i64, _i32,
                                        _i32, _i32, C.POINTER(C.c_float)],
@@ -160,6 +161,19 @@ def plan_counts(geom: Geometry, step: StepArrays, joint: bool = False):
                                 C.byref(p), C.byref(s), C.byref(j), C.byref(sh))
     out = (rc, r.value, i.value, p.value, s.value)
     return out + (j.value, sh.value) if joint else out
+
+
+def plan_items(geom: Geometry, step: StepArrays):
+    """Host-only planning: (status, items [n, 6] int32) with columns row,
+    joint_row, key_begin, key_end, kv_head, split, in dispatch order."""
+    n = C.c_int64()
+    rc = lib().ehip_plan_items(C.byref(geom), C.byref(step.desc), None, 0, C.byref(n))
+    if rc != 0:
+        return rc, np.zeros((0, 6), np.int32)
+    out = np.zeros((n.value, 6), np.int32)
+    rc = lib().ehip_plan_items(C.byref(geom), C.byref(step.desc), out.ctypes.data, n.value,
+                               C.byref(n))
+    return rc, out
 
 
 class DeviceBuffer:

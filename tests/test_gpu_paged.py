@@ -517,6 +517,25 @@ def test_prefill_key_splits(gctx, ehip_mod, orc, H, Hkv, T, P, monkeypatch):
     assert rel_norm(outs[0][rows], outs[1][rows]) <= PREFILL_REL
 
 
+@pytest.mark.parametrize("slots", ["1", "7", "300"])
+def test_persistent_decode_queue(gctx, ehip_mod, orc, slots, monkeypatch):
+    """The MFMA decode kernel's wavefronts take their later items from the
+    launch's queue counter. With the grid capped to a few wavefronts every
+    one of them runs many items, over several launches in a row (the
+    counters alternate between launches): outputs bit-identical to one
+    workgroup per item, and within the bars of the oracle."""
+    from ehip import workloads
+    w = workloads.c4(num_seqs=24, share_frac=0.3)
+    monkeypatch.setenv("EHIP_DECODE_PERSIST", "0")
+    base = run_step(gctx, ehip_mod, orc, w, 17, layers=3)
+    monkeypatch.setenv("EHIP_DECODE_PERSIST", "1")
+    monkeypatch.setenv("EHIP_DECODE_SLOTS", slots)
+    got = run_step(gctx, ehip_mod, orc, w, 17, layers=3)
+    for (g, ref, *_), (b, *_) in zip(got, base):
+        assert np.array_equal(g.view(np.uint32), b.view(np.uint32))
+        check_fp32(g, ref)
+
+
 @pytest.mark.parametrize("kernel", ["mfma", "valu"])
 def test_step_c4_shape_with_shared_prefix_blocks(gctx, ehip_mod, orc, kernel, monkeypatch):
     """C4 construction (log-uniform lengths, pair-shared prefix blocks, bf16)

@@ -224,3 +224,41 @@ def test_plan_chunk_rows_pair_up(ehip_mod, monkeypatch):
     assert shared == exp_shared
     assert joint == 8 * exp_joint
     assert items == 8 * (exp_joint + exp_private)
+
+
+def check_partition(items, lens, hkv):
+    """Every (row, kv head) has key ranges (its own and the joint ones it is a
+    member of) that tile [0, L) exactly, numbered 0..n-1 in key order."""
+    per = {}
+    for r0, r1, tb, te, hk, sp in items.tolist():
+        assert 0 <= tb < te
+        for r in (r0, r1):
+            if r >= 0:
+                per.setdefault((r, hk), []).append((tb, te, sp))
+    for r, L in enumerate(lens):
+        ns = None
+        for hk in range(hkv):
+            rs = sorted(per[(r, hk)])
+            assert rs[0][0] == 0 and rs[-1][1] == L
+            assert all(a[1] == b[0] for a, b in zip(rs, rs[1:]))
+            assert [sp for _, _, sp in rs] == list(range(len(rs)))
+            assert ns is None or ns == len(rs)  # the same splits for every head
+            ns = len(rs)
+
+
+def test_plan_items_partition_c4(ehip_mod):
+    """The work list of the C4 step (pair-shared prefixes, log-uniform
+    lengths) tiles every row exactly, with split indices in key order and
+    the same splits for every kv head; items are ordered longest first."""
+    from ehip import workloads
+    w = workloads.c4()
+    g = ehip_mod.geometry(w.heads, w.kv_heads, w.head_dim, w.block_size, w.kv_dtype,
+                          w.pool_blocks, w.scale)
+    st = ehip_mod.StepArrays(w.query_lens, w.context_lens, w.tables, w.slot_mapping)
+    rc, items = ehip_mod.plan_items(g, st)
+    assert rc == 0
+    check_partition(items, w.context_lens, w.kv_heads)
+    keys = items[:, 3] - items[:, 2]
+    assert (np.diff(keys) <= 0).all()
+    rc, rows, n, partials, split, joint, shared = ehip_mod.plan_counts(g, st, joint=True)
+    assert n == len(items) and joint == int((items[:, 1] >= 0).sum()) > 0
