@@ -52,7 +52,10 @@ enum {
   EHIP_INTERNAL = 11
 };
 
-enum { EHIP_KV_F32 = 0, EHIP_KV_BF16 = 1 };
+/* KV element types. INT8 slabs carry fp32 per-(block, kv head) scales in
+ * separate [slab_blocks, kv_heads] arrays (one for K, one for V): the format
+ * the reference reserves in docs/design/paged-kv-cache.md:219-231. */
+enum { EHIP_KV_F32 = 0, EHIP_KV_BF16 = 1, EHIP_KV_INT8 = 2 };
 
 typedef struct ehip_ctx ehip_ctx;
 
@@ -225,6 +228,21 @@ int ehip_step_rope_kv_append(ehip_ctx* ctx, float* d_q, const float* d_src_k,
 /* Attention for every row of the step: q/out [sum T_b, H, d] fp32. */
 int ehip_step_attention(ehip_ctx* ctx, const float* d_q, const void* d_k_slab,
                         const void* d_v_slab, float* d_out);
+/* INT8 KV (geometry kv_dtype EHIP_KV_INT8): the append quantises the step's
+ * new rows into int8 slabs with fp32 scales [slab_blocks, kv_heads] per slab
+ * (requantising a block's older rows when a new row exceeds its range; a row
+ * at offset 0 starts a fresh block), and the attention dequantises through
+ * the scales. The reference reserves this format
+ * (docs/design/paged-kv-cache.md:219-231: INT8 slabs plus per-block-per-head
+ * scales, dequantised inside the attention kernels) without implementing it;
+ * these entry points add the scale parameters to ehip_step_kv_append and
+ * ehip_step_attention as that design says. Covered shapes: head_dim 64 or
+ * 128, g in {1, 2, 4, 8}, block_size >= 16. */
+int ehip_step_kv_append_int8(ehip_ctx* ctx, const float* d_src_k, const float* d_src_v,
+                             void* d_k_slab, void* d_v_slab, float* d_k_scale, float* d_v_scale);
+int ehip_step_attention_int8(ehip_ctx* ctx, const float* d_q, const void* d_k_slab,
+                             const void* d_v_slab, const float* d_k_scale,
+                             const float* d_v_scale, float* d_out);
 /* Counts of the uploaded plan (rows, work items, split partials). */
 int ehip_step_info(const ehip_ctx* ctx, int64_t* rows, int64_t* items, int64_t* partials);
 

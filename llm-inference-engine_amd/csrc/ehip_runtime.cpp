@@ -47,6 +47,8 @@ struct ehip_ctx {
   const ehip::PrefillItem* d_prefill = nullptr;
   const int32_t* d_table = nullptr;
   const int64_t* d_slots = nullptr;
+  const ehip::Q8Group* d_q8_groups = nullptr;  // INT8 append groups of the step
+  const int32_t* d_q8_rows = nullptr;
   const int32_t* d_merge_rows = nullptr;
 };
 
@@ -135,8 +137,10 @@ int UploadPlan(ehip_ctx* ctx, const ehip_geometry& g, Plan&& plan, const int32_t
   const size_t table_b = Align256(plan.table_ids.size() * sizeof(int32_t));
   const size_t slots_b = Align256(plan.slots.size() * sizeof(int64_t));
   const size_t merge_b = Align256(plan.merge_rows.size() * sizeof(int32_t));
-  const size_t total =
-      std::max<size_t>(256, rows_b + items_b + prefill_b + table_b + slots_b + merge_b);
+  const size_t q8g_b = Align256(plan.q8_groups.size() * sizeof(ehip::Q8Group));
+  const size_t q8r_b = Align256(plan.q8_rows.size() * sizeof(int32_t));
+  const size_t total = std::max<size_t>(
+      256, rows_b + items_b + prefill_b + table_b + slots_b + merge_b + q8g_b + q8r_b);
 
   const int cur = ctx->stage_cur;
   ctx->stage_cur ^= 1;
@@ -170,6 +174,9 @@ int UploadPlan(ehip_ctx* ctx, const ehip_geometry& g, Plan&& plan, const int32_t
               plan.slots.size() * sizeof(int64_t));
   std::memcpy(h + rows_b + items_b + prefill_b + table_b + slots_b, plan.merge_rows.data(),
               plan.merge_rows.size() * sizeof(int32_t));
+  const size_t q8_at = rows_b + items_b + prefill_b + table_b + slots_b + merge_b;
+  std::memcpy(h + q8_at, plan.q8_groups.data(), plan.q8_groups.size() * sizeof(ehip::Q8Group));
+  std::memcpy(h + q8_at + q8g_b, plan.q8_rows.data(), plan.q8_rows.size() * sizeof(int32_t));
   EHIP_HIP(ctx, hipMemcpyAsync(ctx->d_desc, h, total, hipMemcpyHostToDevice, ctx->stream));
   if (!ctx->stage_done[cur]) EHIP_HIP(ctx, hipEventCreateWithFlags(&ctx->stage_done[cur],
                                                                    hipEventDisableTiming));
@@ -185,6 +192,8 @@ int UploadPlan(ehip_ctx* ctx, const ehip_geometry& g, Plan&& plan, const int32_t
   ctx->d_slots = reinterpret_cast<const int64_t*>(d + rows_b + items_b + prefill_b + table_b);
   ctx->d_merge_rows =
       reinterpret_cast<const int32_t*>(d + rows_b + items_b + prefill_b + table_b + slots_b);
+  ctx->d_q8_groups = reinterpret_cast<const ehip::Q8Group*>(d + q8_at);
+  ctx->d_q8_rows = reinterpret_cast<const int32_t*>(d + q8_at + q8g_b);
   if (int rc = EnsureWorkspace(ctx, g, plan)) return rc;
   ctx->geom = g;
   ctx->plan = std::move(plan);
@@ -193,7 +202,7 @@ int UploadPlan(ehip_ctx* ctx, const ehip_geometry& g, Plan&& plan, const int32_t
 }
 
 int LaunchAttention(ehip_ctx* ctx, const float* q, const void* k_slab, const void* v_slab,
-                    float* out) {
+                    float* out, const float* k_scale = nullptr, const float* v_scale = nullptr) {
   const ehip_geometry& g = ctx->geom;
   const Plan& plan = ctx->plan;
   if (plan.items.size() > static_cast<size_t>(INT32_MAX) ||
@@ -259,6 +268,8 @@ int LaunchAttention(ehip_ctx* ctx, const float* q, const void* k_slab, const voi
   p.d = g.head_dim;
   p.bs = g.block_size;
   p.scale_log2 = g.scale * 1.4426950408889634f;
+  p.k_scale = k_scale;
+  p.v_scale = v_scale;
   EHIP_HIP(ctx, ehip::LaunchDecode(p, g.kv_dtype, &ctx->queue, ctx->stream));
   return EHIP_OK;
 }
@@ -668,6 +679,9 @@ int ehip_step_kv_append(ehip_ctx* ctx, const float* d_src_k, const float* d_src_
   if (!d_src_k || !d_src_v || !d_k_slab || !d_v_slab)
     return SetError(ctx, EHIP_INVALID_ARGUMENT, "null append operand");
   const ehip_geometry& g = ctx->geom;
+  if (g.kv_dtype == EHIP_KV_INT8)
+    return SetError(ctx, EHIP_INVALID_ARGUMENT,
+                    "INT8 slabs carry scales: use ehip_step_kv_append_int8");
   if (ehip::BlockStride(g) != int64_t{g.kv_heads} * g.block_size * g.head_dim)
     return SetError(ctx, EHIP_UNIMPLEMENTED, "append needs the dense Hkv*bs*d block stride");
   EHIP_HIP(ctx, ehip::LaunchKvScatter(d_src_k, d_src_v, ctx->d_slots,
@@ -689,6 +703,8 @@ int ehip_step_rope_kv_append(ehip_ctx* ctx, float* d_q, const float* d_src_k,
   if (!d_q || !d_src_k || !d_src_v || !d_cos || !d_sin || !d_k_slab || !d_v_slab)
     return SetError(ctx, EHIP_INVALID_ARGUMENT, "null rope/append operand");
   const ehip_geometry& g = ctx->geom;
+  if (g.kv_dtype == EHIP_KV_INT8)
+    return SetError(ctx, EHIP_UNIMPLEMENTED, "fused RoPE + append covers fp32 and bf16 slabs");
   if (g.head_dim % 2 != 0)
     return SetError(ctx, EHIP_INVALID_ARGUMENT, "RoPE needs an even head_dim (got %d)",
                     g.head_dim);
@@ -713,7 +729,50 @@ int ehip_step_attention(ehip_ctx* ctx, const float* d_q, const void* d_k_slab,
   if (ctx->plan.rows.empty()) return EHIP_OK;
   if (!d_q || !d_k_slab || !d_v_slab || !d_out)
     return SetError(ctx, EHIP_INVALID_ARGUMENT, "null attention operand");
+  if (ctx->geom.kv_dtype == EHIP_KV_INT8)
+    return SetError(ctx, EHIP_INVALID_ARGUMENT,
+                    "INT8 slabs carry scales: use ehip_step_attention_int8");
   return LaunchAttention(ctx, d_q, d_k_slab, d_v_slab, d_out);
+}
+
+int ehip_step_kv_append_int8(ehip_ctx* ctx, const float* d_src_k, const float* d_src_v,
+                             void* d_k_slab, void* d_v_slab, float* d_k_scale, float* d_v_scale) {
+  if (int rc = CheckCtx(ctx)) return rc;
+  if (!ctx->have_step) return SetError(ctx, EHIP_FAILED_PRECONDITION, "no step uploaded");
+  const Plan& plan = ctx->plan;
+  const ehip_geometry& g = ctx->geom;
+  if (g.kv_dtype != EHIP_KV_INT8)
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "the uploaded geometry is not INT8 KV");
+  if (plan.slots.empty()) {
+    if (plan.rows.empty()) return EHIP_OK;
+    return SetError(ctx, EHIP_FAILED_PRECONDITION, "the uploaded step has no slot mapping");
+  }
+  if (!d_src_k || !d_src_v || !d_k_slab || !d_v_slab || !d_k_scale || !d_v_scale)
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "null append operand");
+  if (ehip::BlockStride(g) != int64_t{g.kv_heads} * g.block_size * g.head_dim)
+    return SetError(ctx, EHIP_UNIMPLEMENTED, "append needs the dense Hkv*bs*d block stride");
+  EHIP_HIP(ctx, ehip::LaunchAppendQ8(d_src_k, d_src_v, ctx->d_q8_groups,
+                                     static_cast<int64_t>(plan.q8_groups.size()), ctx->d_q8_rows,
+                                     g.kv_heads, g.head_dim, g.block_size, g.slab_blocks,
+                                     d_k_slab, d_v_slab, d_k_scale, d_v_scale, ctx->d_err,
+                                     ctx->stream));
+  return EHIP_OK;
+}
+
+int ehip_step_attention_int8(ehip_ctx* ctx, const float* d_q, const void* d_k_slab,
+                             const void* d_v_slab, const float* d_k_scale,
+                             const float* d_v_scale, float* d_out) {
+  if (int rc = CheckCtx(ctx)) return rc;
+  if (!ctx->have_step) return SetError(ctx, EHIP_FAILED_PRECONDITION, "no step uploaded");
+  const ehip_geometry& g = ctx->geom;
+  if (g.kv_dtype != EHIP_KV_INT8)
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "the uploaded geometry is not INT8 KV");
+  if (ctx->plan.rows.empty()) return EHIP_OK;
+  if (!d_q || !d_k_slab || !d_v_slab || !d_k_scale || !d_v_scale || !d_out)
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "null attention operand");
+  if (g.slab_blocks * g.kv_heads >= (int64_t{1} << 29))
+    return SetError(ctx, EHIP_UNIMPLEMENTED, "INT8 scale arrays above 2 GiB");
+  return LaunchAttention(ctx, d_q, d_k_slab, d_v_slab, d_out, d_k_scale, d_v_scale);
 }
 
 int ehip_step_info(const ehip_ctx* ctx, int64_t* rows, int64_t* items, int64_t* partials) {

@@ -40,6 +40,8 @@ struct DecodeParams {
   int32_t d;
   int32_t bs;
   float scale_log2;         // scale * log2(e)
+  const float* k_scale;     // INT8 KV: per-(block, kv head) scales [slab_blocks, Hkv]
+  const float* v_scale;
   uint32_t* queue;          // this launch's item counter (zero at launch; MFMA kernel only)
   uint32_t* queue_next;     // the counter of the next launch, cleared by this one
 };
@@ -92,6 +94,8 @@ hipError_t LaunchDecode(const DecodeParams& p, int kv_dtype, QueueState* queue, 
 // shape is not covered (d not 64/128, g not 1/2/4/8, bs < 16, misaligned).
 bool LaunchDecodeMfma(const DecodeParams& p, QueueState* queue, hipStream_t stream,
                       hipError_t* err);
+// INT8 KV decode (paged_decode_q8.hip); false when the shape is not covered.
+bool LaunchDecodeQ8(const DecodeParams& p, hipStream_t stream, hipError_t* err);
 
 // KvScatter: rows [T, Hkv, d] fp32 into slabs (fp32 copy or bf16 RNE).
 hipError_t LaunchKvScatter(const float* src_k, const float* src_v, const int64_t* slots,
@@ -103,6 +107,13 @@ hipError_t LaunchKvGather(const float* k_slab, const float* v_slab, const int32_
                           int32_t bs, int64_t length, int32_t kv_heads, int32_t d,
                           int64_t slab_blocks, float* out_k, float* out_v, int32_t* err,
                           hipStream_t stream);
+
+// INT8 append with per-(block, kv head) scales, one wavefront per
+// (append group, kv head).
+hipError_t LaunchAppendQ8(const float* src_k, const float* src_v, const Q8Group* groups,
+                          int64_t n_groups, const int32_t* rows, int kv_heads, int d, int bs,
+                          int64_t slab_blocks, void* k_slab, void* v_slab, float* k_scale,
+                          float* v_scale, int32_t* err, hipStream_t stream);
 
 // Fused RoPE + KV append of one step's rows (q rotated in place; rotated K and
 // V scattered at the rows' slots; row r at position rows[r].length - 1).

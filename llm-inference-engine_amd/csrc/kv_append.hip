@@ -198,6 +198,87 @@ __global__ __launch_bounds__(256) void RopeKvAppend(
   }
 }
 
+// INT8 append with per-(block, kv head) scales. One wavefront per (append
+// group, kv head): the group's rows land at consecutive offsets
+// [off0, off0 + n) of one block. For K, then V: m = max |x| over the new rows;
+// the stored scale counts only when off0 > 0 (offset 0 is a freshly allocated
+// block, whatever an earlier owner left); if m exceeds 127 times that scale,
+// the scale becomes m / 127 and the block's older rows are requantised. Each
+// value is quant(x, s) = 0 if s == 0, else clamp(rint(x * (1 / s)), -127, 127),
+// in fp32 with round-to-nearest-even throughout, so the slabs and scales are
+// bit-identical to the CPU restatement. Lanes handle 4 consecutive elements
+// (d % 4 == 0).
+__device__ __forceinline__ int32_t Q8(float x, float inv, bool zero) {
+  if (zero) return 0;
+  const float y = fminf(fmaxf(rintf(x * inv), -127.0f), 127.0f);
+  return static_cast<int32_t>(y);
+}
+
+__device__ __forceinline__ uint32_t Pack4(int32_t a, int32_t b, int32_t c, int32_t e) {
+  return (static_cast<uint32_t>(a) & 0xFFu) | ((static_cast<uint32_t>(b) & 0xFFu) << 8) |
+         ((static_cast<uint32_t>(c) & 0xFFu) << 16) | (static_cast<uint32_t>(e) << 24);
+}
+
+__global__ __launch_bounds__(64) void AppendQ8(const float* __restrict__ src_k,
+                                               const float* __restrict__ src_v,
+                                               const Q8Group* __restrict__ groups,
+                                               const int32_t* __restrict__ rows, int kv_heads,
+                                               int d, int bs, int64_t slab_blocks,
+                                               int8_t* k_slab, int8_t* v_slab, float* k_scale,
+                                               float* v_scale, int32_t* err) {
+  const int gi = blockIdx.x / kv_heads;
+  const int h = blockIdx.x - gi * kv_heads;
+  const int lane = threadIdx.x;
+  const Q8Group gr = groups[gi];
+  if (gr.block < 0 || gr.block >= slab_blocks || gr.off0 < 0 || gr.off0 + gr.n > bs) {
+    if (lane == 0) atomicOr(err, kErrSlotRange);
+    return;
+  }
+  const int64_t tile = (int64_t{gr.block} * kv_heads + h) * bs * d;
+  const int d4 = d >> 2;
+  const int ne4 = gr.n * d4;
+  for (int which = 0; which < 2; ++which) {
+    const float* src = which ? src_v : src_k;
+    uint32_t* dst = reinterpret_cast<uint32_t*>((which ? v_slab : k_slab) + tile);
+    float* sc = (which ? v_scale : k_scale) + int64_t{gr.block} * kv_heads + h;
+    auto src4 = [&](int i) {
+      const int r = rows[gr.row0 + i / d4];
+      return *reinterpret_cast<const float4*>(src + (int64_t{r} * kv_heads + h) * d +
+                                              (i % d4) * 4);
+    };
+    float m = 0.f;
+    for (int i = lane; i < ne4; i += 64) {
+      const float4 x = src4(i);
+      m = fmaxf(m, fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w))));
+    }
+    m = WaveMax(m);
+    const float s0 = gr.off0 > 0 ? *sc : 0.f;
+    float s1 = s0;
+    if (m > s0 * 127.0f) {
+      s1 = m / 127.0f;
+      const float inv = 1.0f / s1;
+      const bool zero = s1 == 0.0f;
+      for (int i = lane; i < gr.off0 * d4; i += 64) {
+        const uint32_t w = dst[i];
+        const float x0 = static_cast<float>(static_cast<int8_t>(w)) * s0;
+        const float x1 = static_cast<float>(static_cast<int8_t>(w >> 8)) * s0;
+        const float x2 = static_cast<float>(static_cast<int8_t>(w >> 16)) * s0;
+        const float x3 = static_cast<float>(static_cast<int8_t>(w >> 24)) * s0;
+        dst[i] = Pack4(Q8(x0, inv, zero), Q8(x1, inv, zero), Q8(x2, inv, zero),
+                       Q8(x3, inv, zero));
+      }
+    }
+    const float inv = 1.0f / s1;
+    const bool zero = s1 == 0.0f;
+    for (int i = lane; i < ne4; i += 64) {
+      const float4 x = src4(i);
+      dst[gr.off0 * d4 + i] =
+          Pack4(Q8(x.x, inv, zero), Q8(x.y, inv, zero), Q8(x.z, inv, zero), Q8(x.w, inv, zero));
+    }
+    if (lane == 0) *sc = s1;
+  }
+}
+
 // kernels::KvGatherF32 (src/kernels/kv_gather.cpp:42-89): out[h, j, :] is
 // token j of kv head h, read through the table.
 __global__ __launch_bounds__(256) void KvGather(const float* __restrict__ k_slab,
@@ -253,6 +334,19 @@ int GridFor(int64_t work, int block) {
 }
 
 }  // namespace
+
+hipError_t LaunchAppendQ8(const float* src_k, const float* src_v, const Q8Group* groups,
+                          int64_t n_groups, const int32_t* rows, int kv_heads, int d, int bs,
+                          int64_t slab_blocks, void* k_slab, void* v_slab, float* k_scale,
+                          float* v_scale, int32_t* err, hipStream_t stream) {
+  if (n_groups <= 0) return hipSuccess;
+  if (d % 4 != 0 || n_groups * kv_heads > 0x7FFFFFFF) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(AppendQ8, dim3(static_cast<uint32_t>(n_groups * kv_heads)), dim3(64), 0,
+                     stream, src_k, src_v, groups, rows, kv_heads, d, bs, slab_blocks,
+                     static_cast<int8_t*>(k_slab), static_cast<int8_t*>(v_slab), k_scale,
+                     v_scale, err);
+  return hipGetLastError();
+}
 
 hipError_t LaunchRopeKvAppend(float* q, const float* src_k, const float* src_v,
                               const RowDesc* rows, const float* cos_t, const float* sin_t,

@@ -484,6 +484,13 @@ hipError_t LaunchTyped(const DecodeParams& p, hipStream_t stream) {
 
 hipError_t LaunchSplits(const DecodeParams& p, int kv_dtype, QueueState* queue,
                         hipStream_t stream) {
+  if (kv_dtype == EHIP_KV_INT8) {
+    // No VALU fallback for INT8: the plan validation admits only the shapes
+    // the MFMA kernel covers.
+    hipError_t err = hipSuccess;
+    if (LaunchDecodeQ8(p, stream, &err)) return err;
+    return hipErrorInvalidValue;
+  }
   if (kv_dtype != EHIP_KV_BF16) return LaunchTyped<float>(p, stream);
   // EHIP_DECODE_KERNEL=valu selects the all-VALU kernel for bf16 as well.
   const char* pick = std::getenv("EHIP_DECODE_KERNEL");

@@ -51,9 +51,19 @@ int ValidateGeometry(const ehip_geometry& g, std::string* err) {
     return Fail(err, EHIP_INVALID_ARGUMENT,
                 "block_size=%lld must be one of 8, 16, 32, 64 (a power of two dividing 64)",
                 g.block_size);
-  if (g.kv_dtype != EHIP_KV_F32 && g.kv_dtype != EHIP_KV_BF16)
-    return Fail(err, EHIP_INVALID_ARGUMENT, "kv_dtype=%lld is not F32 (0) or BF16 (1)",
+  if (g.kv_dtype != EHIP_KV_F32 && g.kv_dtype != EHIP_KV_BF16 && g.kv_dtype != EHIP_KV_INT8)
+    return Fail(err, EHIP_INVALID_ARGUMENT, "kv_dtype=%lld is not F32 (0), BF16 (1) or INT8 (2)",
                 g.kv_dtype);
+  if (g.kv_dtype == EHIP_KV_INT8) {
+    // The INT8 kernels (MFMA QK^T over 16-token halves) cover these shapes.
+    const int64_t grp = g.heads / g.kv_heads;
+    if ((g.head_dim != 64 && g.head_dim != 128) ||
+        (grp != 1 && grp != 2 && grp != 4 && grp != 8) || g.block_size < 16)
+      return Fail(err, EHIP_UNIMPLEMENTED,
+                  "INT8 KV needs head_dim 64 or 128, g in {1,2,4,8} and block_size >= 16 "
+                  "(got d=%lld, g=%lld, bs=%lld)",
+                  g.head_dim, grp, g.block_size);
+  }
   if (g.reserved != 0) return Fail(err, EHIP_INVALID_ARGUMENT, "reserved field must be 0");
   if (g.slab_blocks < 1)
     return Fail(err, EHIP_INVALID_ARGUMENT, "slab_blocks=%lld must be >= 1", g.slab_blocks);
@@ -241,6 +251,40 @@ void FinishPlan(const ehip_geometry& g, Plan* plan, bool allow_joint,
 
 }  // namespace
 
+namespace {
+
+// INT8 append groups: the step's rows grouped by destination block, each
+// group's rows in offset order with consecutive offsets (tokens append in
+// order; a block takes rows of one sequence only).
+int BuildQ8Groups(const ehip_geometry& g, Plan* plan, std::string* err) {
+  const int64_t n = static_cast<int64_t>(plan->slots.size());
+  std::vector<int32_t> order(static_cast<size_t>(n));
+  for (int64_t i = 0; i < n; ++i) order[static_cast<size_t>(i)] = static_cast<int32_t>(i);
+  std::stable_sort(order.begin(), order.end(),
+                   [&](int32_t a, int32_t b) { return plan->slots[a] < plan->slots[b]; });
+  for (int64_t i = 0; i < n;) {
+    const int64_t block = plan->slots[order[i]] / g.block_size;
+    const int64_t off0 = plan->slots[order[i]] % g.block_size;
+    int64_t j = i;
+    while (j < n && plan->slots[order[j]] / g.block_size == block) {
+      if (plan->slots[order[j]] % g.block_size != off0 + (j - i))
+        return Fail(err, EHIP_INVALID_ARGUMENT,
+                    "INT8 append: rows landing in block %lld do not take consecutive slots "
+                    "(slot %lld)",
+                    block, plan->slots[order[j]]);
+      ++j;
+    }
+    plan->q8_groups.push_back(Q8Group{static_cast<int32_t>(block), static_cast<int32_t>(off0),
+                                      static_cast<int32_t>(j - i),
+                                      static_cast<int32_t>(plan->q8_rows.size())});
+    for (int64_t k = i; k < j; ++k) plan->q8_rows.push_back(order[k]);
+    i = j;
+  }
+  return EHIP_OK;
+}
+
+}  // namespace
+
 int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::string* err,
               int prefill_rows) {
   if (int rc = ValidateGeometry(g, err)) return rc;
@@ -251,6 +295,8 @@ int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::
   plan->prefill.clear();
   plan->table_ids.clear();
   plan->slots.clear();
+  plan->q8_groups.clear();
+  plan->q8_rows.clear();
   plan->partials = 0;
   plan->max_length = 0;
   const int32_t B = s.num_seqs;
@@ -308,6 +354,8 @@ int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::
                     slot, cap);
     }
     plan->slots.assign(s.h_slot_mapping, s.h_slot_mapping + total_rows);
+    if (g.kv_dtype == EHIP_KV_INT8)
+      if (int rc = BuildQ8Groups(g, plan, err)) return rc;
   }
   if (g.kv_heads >= (1 << kHkBits))
     return Fail(err, EHIP_UNIMPLEMENTED, "kv_heads=%lld >= 4096", g.kv_heads);
@@ -381,7 +429,8 @@ int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::
                                             s.h_table_offsets[bl.b], pc.kb, pc.ke});
     }
   }
-  FinishPlan(g, plan, true, &skip);
+  // The INT8 decode kernel serves one row per item (no joint items).
+  FinishPlan(g, plan, g.kv_dtype != EHIP_KV_INT8, &skip);
   return EHIP_OK;
 }
 

@@ -80,6 +80,16 @@ constexpr int kHkBits = 12;
 
 inline int32_t PackHkSplit(int32_t hk, int32_t split) { return hk | (split << kHkBits); }
 
+// Rows of one step landing in one block (INT8 append): the block, the first
+// new row's offset in it, the row count and where its row indices start in
+// Plan::q8_rows.
+struct Q8Group {
+  int32_t block;
+  int32_t off0;
+  int32_t n;
+  int32_t row0;
+};
+
 struct Plan {
   std::vector<RowDesc> rows;
   std::vector<WorkItem> items;
@@ -88,6 +98,8 @@ struct Plan {
   std::vector<int32_t> table_ids;   // CSR ids, copied
   std::vector<int64_t> slots;       // slot mapping of appended tokens (may be empty)
   std::vector<int32_t> merge_rows;  // rows with more than one split, ascending
+  std::vector<Q8Group> q8_groups;   // INT8 append groups (kv_dtype INT8 with slots)
+  std::vector<int32_t> q8_rows;     // row indices of the groups, in offset order
   int64_t partials = 0;             // sum over rows of nsplit * Hkv
   int64_t max_length = 0;           // longest visible length (largest position + 1)
   int32_t split_tokens = 0;         // base split length chosen for this step

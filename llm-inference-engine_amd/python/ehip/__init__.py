@@ -28,6 +28,7 @@ INTERNAL = 11
 
 KV_F32 = 0
 KV_BF16 = 1
+KV_INT8 = 2
 
 _i32 = C.c_int32
 _i64 = C.c_int64
@@ -94,6 +95,8 @@ def lib():
             "ehip_step_upload": [_vp, C.POINTER(Geometry), C.POINTER(StepDesc)],
             "ehip_step_kv_append": [_vp, _vp, _vp, _vp, _vp],
             "ehip_step_rope_kv_append": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp],
+            "ehip_step_kv_append_int8": [_vp, _vp, _vp, _vp, _vp, _vp, _vp],
+            "ehip_step_attention_int8": [_vp, _vp, _vp, _vp, _vp, _vp, _vp],
             "ehip_step_attention": [_vp, _vp, _vp, _vp, _vp],
             "ehip_step_info": [_vp, _I64P, _I64P, _I64P],
             "ehip_plan_counts": [C.POINTER(Geometry), C.POINTER(StepDesc), _I64P, _I64P, _I64P,
@@ -325,6 +328,14 @@ class Context:
                             v_slab) -> int:
         return lib().ehip_step_rope_kv_append(self.h, q.ptr, src_k.ptr, src_v.ptr, cos.ptr,
                                               sin.ptr, table_positions, k_slab.ptr, v_slab.ptr)
+
+    def step_kv_append_int8(self, src_k, src_v, k_slab, v_slab, k_scale, v_scale) -> int:
+        return lib().ehip_step_kv_append_int8(self.h, src_k.ptr, src_v.ptr, k_slab.ptr,
+                                              v_slab.ptr, k_scale.ptr, v_scale.ptr)
+
+    def step_attention_int8(self, q, k_slab, v_slab, k_scale, v_scale, out) -> int:
+        return lib().ehip_step_attention_int8(self.h, q.ptr, k_slab.ptr, v_slab.ptr,
+                                              k_scale.ptr, v_scale.ptr, out.ptr)
 
     def step_attention(self, q, k_slab, v_slab, out) -> int:
         return lib().ehip_step_attention(self.h, q.ptr, k_slab.ptr, v_slab.ptr, out.ptr)

@@ -14,7 +14,7 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-from . import KV_BF16, KV_F32
+from . import KV_BF16, KV_F32, KV_INT8
 
 
 @dataclass
@@ -51,7 +51,7 @@ class Workload:
 
     @property
     def kv_bytes(self) -> int:
-        return 2 if self.kv_dtype == KV_BF16 else 4
+        return {KV_BF16: 2, KV_INT8: 1}.get(self.kv_dtype, 4)
 
     def decode_rows(self) -> np.ndarray:
         return np.flatnonzero(self.query_lens == 1)

@@ -117,6 +117,30 @@ void orc_kv_scatter_bf16(const float* src_k, const float* src_v,
                          const int64_t* slot_mapping, int64_t t_dim,
                          int64_t kv_heads, int64_t d, int64_t block_size,
                          uint16_t* k_slab, uint16_t* v_slab);
+/* ---- INT8 KV with per-(block, kv head) scales ----
+ * The reference reserves this format (docs/design/paged-kv-cache.md:219-231:
+ * INT8 slabs [num_blocks, Hkv, bs, d] plus fp32 per-block-per-head scales
+ * beside them, dequantised inside the attention kernels) without implementing
+ * it, so these semantics are this build's; they are pinned by closed forms
+ * (round-trip error, requantisation bounds, fresh-block reset) in
+ * tests/test_oracle.py, not against a reference output.
+ *
+ * Append: the rows landing in one block in one call are quantised together.
+ * For each (block, kv head) and each of K and V: m = max |x| over the new
+ * rows; the block's old scale s0 counts only when the first new row's offset
+ * in the block is > 0 (offset 0 means a freshly allocated block). If
+ * m > s0 * 127 the scale becomes m / 127 and the block's older rows are
+ * requantised (x' = q * s0, then quantised with the new scale); otherwise the
+ * scale stays. quant(x, s) = 0 if s == 0, else clamp(rint(x * (1 / s)), -127,
+ * 127). All arithmetic is fp32 with round-to-nearest-even. Rows of one block
+ * must arrive with consecutive offsets (tokens append in order). */
+void orc_kv_append_int8(const float* src_k, const float* src_v, const int64_t* slot_mapping,
+                        int64_t t_dim, int64_t kv_heads, int64_t d, int64_t block_size,
+                        int8_t* k_slab, int8_t* v_slab, float* k_scale, float* v_scale);
+/* Dequantised fp32 copy of an INT8 slab: x = q * scale[block, head]. */
+void orc_int8_dequant(const int8_t* slab, const float* scale, int64_t num_blocks,
+                      int64_t kv_heads, int64_t block_size, int64_t d, float* out);
+
 void orc_kv_gather_f32(const float* k_slab, const float* v_slab,
                        const int32_t* block_table, int64_t block_size,
                        int64_t length, int64_t kv_heads, int64_t d,

@@ -25,6 +25,7 @@ _f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
 _u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
 _i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
 _i64p = np.ctypeslib.ndpointer(np.int64, flags="C_CONTIGUOUS")
+_i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
 _i64 = C.c_int64
 _PP = C.POINTER(C.c_void_p)
 
@@ -71,6 +72,11 @@ def lib():
                                           _u16p, _u16p]
         L.orc_kv_gather_f32.argtypes = [_f32p, _f32p, _i32p, _i64, _i64, _i64, _i64,
                                         _f32p, _f32p]
+        L.orc_kv_append_int8.argtypes = [_f32p, _f32p, _i64p, _i64, _i64, _i64, _i64, _i8p,
+                                         _i8p, _f32p, _f32p]
+        L.orc_kv_append_int8.restype = None
+        L.orc_int8_dequant.argtypes = [_i8p, _f32p, _i64, _i64, _i64, _i64, _f32p]
+        L.orc_int8_dequant.restype = None
         L.orc_rope_apply_f32.argtypes = [C.c_int, _f32p, _i64, _i64, _i64, _i32p, _f32p, _f32p]
         L.orc_rope_apply_f32.restype = None
         L.orc_cpu_attention.argtypes = [_f32p, _f32p, _f32p, _i64, _i64, _i64, _i64, _i64,
@@ -301,6 +307,29 @@ def kv_scatter(src_k, src_v, slot_mapping, kv_heads, d, bs, k_slab, v_slab, use_
     else:
         lib().orc_kv_scatter_f32(sk, sv, sm, t_dim, kv_heads, d, bs, k_slab.reshape(-1),
                                  v_slab.reshape(-1))
+
+
+def kv_append_int8(src_k, src_v, slot_mapping, kv_heads, d, bs, k_slab, v_slab, k_scale,
+                   v_scale):
+    """INT8 append in place: slabs int8 [blocks, Hkv, bs, d], scales fp32 [blocks, Hkv]."""
+    sm = np.ascontiguousarray(slot_mapping, np.int64)
+    for a, dt in ((k_slab, np.int8), (v_slab, np.int8), (k_scale, np.float32),
+                  (v_scale, np.float32)):
+        assert a.dtype == dt and a.flags.c_contiguous
+    lib().orc_kv_append_int8(np.ascontiguousarray(src_k, np.float32).reshape(-1),
+                             np.ascontiguousarray(src_v, np.float32).reshape(-1), sm, len(sm),
+                             kv_heads, d, bs, k_slab.reshape(-1), v_slab.reshape(-1),
+                             k_scale.reshape(-1), v_scale.reshape(-1))
+
+
+def int8_dequant(slab, scale):
+    """fp32 copy of an INT8 slab [blocks, Hkv, bs, d]: q * scale[block, head]."""
+    nb, hkv, bs, d = slab.shape
+    out = np.empty(slab.shape, np.float32)
+    lib().orc_int8_dequant(np.ascontiguousarray(slab).reshape(-1),
+                           np.ascontiguousarray(scale, np.float32).reshape(-1), nb, hkv, bs, d,
+                           out.reshape(-1))
+    return out
 
 
 def kv_gather(k_slab, v_slab, block_table, bs, length, kv_heads, d, use_ref=False):

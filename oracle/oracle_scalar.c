@@ -479,6 +479,83 @@ void orc_kv_scatter_bf16(const float* src_k, const float* src_v,
   }
 }
 
+static int8_t q8(float x, float s) {
+  if (s == 0.0f) return 0;
+  const float inv = 1.0f / s;
+  float y = rintf(x * inv);
+  if (y > 127.0f) y = 127.0f;
+  if (y < -127.0f) y = -127.0f;
+  return (int8_t)y;
+}
+
+/* One (block, kv head) of one slab: new rows at offsets [off0, off0 + n). */
+static void append_q8_tile(const float* src, int64_t src_row_stride, const int64_t* rows,
+                           int64_t n, int64_t off0, int64_t d, int8_t* tile, float* scale) {
+  float m = 0.0f;
+  for (int64_t i = 0; i < n; ++i)
+    for (int64_t e = 0; e < d; ++e) {
+      const float a = fabsf(src[rows[i] * src_row_stride + e]);
+      if (a > m) m = a;
+    }
+  const float s0 = off0 > 0 ? *scale : 0.0f;
+  float s1 = s0;
+  if (m > s0 * 127.0f) {
+    s1 = m / 127.0f;
+    for (int64_t r = 0; r < off0; ++r)
+      for (int64_t e = 0; e < d; ++e) {
+        const float x = (float)tile[r * d + e] * s0;
+        tile[r * d + e] = q8(x, s1);
+      }
+  }
+  for (int64_t i = 0; i < n; ++i)
+    for (int64_t e = 0; e < d; ++e)
+      tile[(off0 + i) * d + e] = q8(src[rows[i] * src_row_stride + e], s1);
+  *scale = s1;
+}
+
+void orc_kv_append_int8(const float* src_k, const float* src_v, const int64_t* slot_mapping,
+                        int64_t t_dim, int64_t kv_heads, int64_t d, int64_t block_size,
+                        int8_t* k_slab, int8_t* v_slab, float* k_scale, float* v_scale) {
+  int64_t* rows = (int64_t*)malloc(sizeof(int64_t) * (size_t)(block_size > 0 ? block_size : 1));
+  char* done = (char*)calloc((size_t)(t_dim > 0 ? t_dim : 1), 1);
+  for (int64_t t = 0; t < t_dim; ++t) {
+    if (done[t]) continue;
+    const int64_t block = slot_mapping[t] / block_size;
+    /* every row of this call landing in `block`, in offset order */
+    int64_t n = 0, off0 = block_size;
+    for (int64_t u = t; u < t_dim; ++u)
+      if (slot_mapping[u] / block_size == block) {
+        const int64_t off = slot_mapping[u] % block_size;
+        if (off < off0) off0 = off;
+        done[u] = 1;
+        rows[n++] = u;
+      }
+    /* order by offset (insertion sort; n <= block_size) */
+    for (int64_t i = 1; i < n; ++i)
+      for (int64_t j = i; j > 0 && slot_mapping[rows[j - 1]] > slot_mapping[rows[j]]; --j) {
+        const int64_t x = rows[j];
+        rows[j] = rows[j - 1];
+        rows[j - 1] = x;
+      }
+    for (int64_t h = 0; h < kv_heads; ++h) {
+      const int64_t tile = (block * kv_heads + h) * block_size * d;
+      append_q8_tile(src_k + h * d, kv_heads * d, rows, n, off0, d, k_slab + tile,
+                     k_scale + block * kv_heads + h);
+      append_q8_tile(src_v + h * d, kv_heads * d, rows, n, off0, d, v_slab + tile,
+                     v_scale + block * kv_heads + h);
+    }
+  }
+  free(rows);
+  free(done);
+}
+
+void orc_int8_dequant(const int8_t* slab, const float* scale, int64_t num_blocks,
+                      int64_t kv_heads, int64_t block_size, int64_t d, float* out) {
+  const int64_t tile = block_size * d;
+  for (int64_t u = 0; u < num_blocks * kv_heads; ++u)
+    for (int64_t i = 0; i < tile; ++i) out[u * tile + i] = (float)slab[u * tile + i] * scale[u];
+}
+
 void orc_kv_gather_f32(const float* k_slab, const float* v_slab,
                        const int32_t* block_table, int64_t block_size,
                        int64_t length, int64_t kv_heads, int64_t d,

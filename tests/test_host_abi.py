@@ -262,3 +262,31 @@ def test_plan_items_partition_c4(ehip_mod):
     assert (np.diff(keys) <= 0).all()
     rc, rows, n, partials, split, joint, shared = ehip_mod.plan_counts(g, st, joint=True)
     assert n == len(items) and joint == int((items[:, 1] >= 0).sum()) > 0
+
+
+def test_plan_int8_shapes_and_append_groups(ehip_mod):
+    """INT8 KV: shapes outside the kernels' coverage are Unimplemented (9);
+    rows landing in one block must take consecutive slots (2 otherwise); no
+    joint items are planned."""
+    E = ehip_mod
+    tabs = [np.arange(4, dtype=np.int32), np.arange(4, 8, dtype=np.int32)]
+    st = E.StepArrays(np.array([3, 1], np.int32), np.array([40, 20], np.int64), tabs,
+                      np.array([37, 38, 39, 4 * 16 + 19], np.int64))
+    ok = E.geometry(32, 8, 128, 16, E.KV_INT8, 16, 0.088)
+    assert E.plan_counts(ok, st, joint=True)[0] == 0
+    for bad in (E.geometry(14, 2, 64, 16, E.KV_INT8, 8, 0.125),   # g = 7
+                E.geometry(32, 8, 96, 16, E.KV_INT8, 8, 0.1),     # d = 96
+                E.geometry(32, 8, 128, 8, E.KV_INT8, 16, 0.088)):  # bs = 8
+        assert E.plan_counts(bad, st)[0] == 9
+    gap = E.StepArrays(np.array([3, 1], np.int32), np.array([40, 20], np.int64), tabs,
+                       np.array([36, 38, 39, 4 * 16 + 19], np.int64))
+    assert E.plan_counts(ok, gap)[0] == 2
+    # two sequences forked from one prefix would share leading blocks: still
+    # no joint items for INT8
+    shared = [np.arange(10, dtype=np.int32), np.array(list(range(8)) + [10, 11], np.int32)]
+    st2 = E.StepArrays(np.array([1, 1], np.int32), np.array([150, 150], np.int64), shared,
+                       np.array([9 * 16 + 5, 11 * 16 + 5], np.int64))
+    rc, rows, items, partials, split, joint, sh = E.plan_counts(ok, st2, joint=True)
+    assert rc == 0 and joint == 0
+    g16 = E.geometry(32, 8, 128, 16, E.KV_BF16, 16, 0.088)
+    assert E.plan_counts(g16, st2, joint=True)[5] > 0

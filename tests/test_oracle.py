@@ -355,3 +355,104 @@ def test_rope_closed_forms(orc, isa):
     # The FMA (AVX2) and two-rounding (scalar) forms differ by at most an ulp or so.
     other = orc.rope_apply(x, pos, c, s, isa=1 - isa)
     assert np.abs(y - other).max() <= 4e-7 * max(1.0, np.abs(y).max())
+
+
+# ------------------------------------------------------------ INT8 KV append
+def int8_case(rng, nb=6, hkv=2, bs=16, d=8):
+    k = np.zeros((nb, hkv, bs, d), np.int8)
+    v = np.zeros((nb, hkv, bs, d), np.int8)
+    return k, v, np.zeros((nb, hkv), np.float32), np.zeros((nb, hkv), np.float32)
+
+
+def test_int8_fresh_block_closed_form(orc):
+    """One call filling rows 0..n-1 of a fresh block: scale = max|x| / 127 in
+    fp32, the max element maps to +-127, every element is within half a step
+    of its value, and zero rows of a zero block give scale 0 and q = 0."""
+    rng = np.random.default_rng(1)
+    hkv, bs, d = 2, 16, 8
+    k, v, ks, vs = int8_case(rng, hkv=hkv, bs=bs, d=d)
+    n = 11
+    src_k = (rng.standard_normal((n, hkv, d)) * 3).astype(np.float32)
+    src_v = np.zeros((n, hkv, d), np.float32)
+    slots = 3 * bs + np.arange(n)
+    orc.kv_append_int8(src_k, src_v, slots, hkv, d, bs, k, v, ks, vs)
+    for h in range(hkv):
+        m = np.abs(src_k[:, h]).max()
+        assert ks[3, h] == np.float32(m) / np.float32(127)
+        q = k[3, h, :n]
+        assert np.abs(q).max() == 127
+        x = q.astype(np.float32) * ks[3, h]
+        assert np.abs(x - src_k[:, h]).max() <= 0.5 * ks[3, h] * (1 + 1e-6)
+        assert vs[3, h] == 0 and not v[3, h].any()
+    untouched = np.ones(6, bool)
+    untouched[3] = False
+    assert not k[untouched].any() and not ks[untouched].any()
+
+
+def test_int8_incremental_appends_requantise(orc):
+    """Decode-style appends one row at a time: the scale never decreases,
+    rises exactly when a row exceeds 127 * scale, and every stored value stays
+    within one step of its input (double rounding after requantisation)."""
+    rng = np.random.default_rng(2)
+    hkv, bs, d = 1, 16, 16
+    k, v, ks, vs = int8_case(rng, hkv=hkv, bs=bs, d=d)
+    amps = [0.5, 0.2, 2.0, 1.0, 7.5, 7.4, 0.1]
+    rows = []
+    prev = np.float32(0)
+    for off, a in enumerate(amps):
+        x = (rng.uniform(-1, 1, (1, hkv, d)) * a).astype(np.float32)
+        rows.append(x[0, 0])
+        orc.kv_append_int8(x, x, np.array([2 * bs + off]), hkv, d, bs, k, v, ks, vs)
+        m = np.abs(x).max()
+        if m > prev * np.float32(127):
+            assert ks[2, 0] == np.float32(m) / np.float32(127)
+        else:
+            assert ks[2, 0] == prev
+        assert ks[2, 0] >= prev
+        prev = ks[2, 0]
+    x = k[2, 0, :len(amps)].astype(np.float32) * ks[2, 0]
+    assert np.abs(x - np.array(rows)).max() <= ks[2, 0] * (1 + 1e-6)
+    assert np.array_equal(k, v) and np.array_equal(ks, vs)
+
+
+def test_int8_batched_equals_ordered_when_first_row_holds_the_max(orc):
+    """When the first appended row carries the block's maximum, the scale is
+    set once, no requantisation happens, and appending the rows one by one
+    stores exactly what one batched call stores."""
+    rng = np.random.default_rng(3)
+    hkv, bs, d = 2, 8, 8
+    x = rng.uniform(-1, 1, (bs, hkv, d)).astype(np.float32)
+    x[0] *= 4  # row 0 holds the max of every head
+    slots = 5 * bs + np.arange(bs)
+    a = int8_case(rng, hkv=hkv, bs=bs, d=d)
+    orc.kv_append_int8(x, x, slots, hkv, d, bs, *a)
+    b = int8_case(rng, hkv=hkv, bs=bs, d=d)
+    for i in range(bs):
+        orc.kv_append_int8(x[i:i + 1], x[i:i + 1], slots[i:i + 1], hkv, d, bs, *b)
+    for u, w in zip(a, b):
+        assert np.array_equal(u, w)
+
+
+def test_int8_fresh_block_ignores_a_stale_scale(orc):
+    """A block reused after release starts at offset 0: its old scale (and
+    rows) must not leak into the new contents."""
+    rng = np.random.default_rng(4)
+    hkv, bs, d = 2, 16, 8
+    x = rng.standard_normal((5, hkv, d)).astype(np.float32)
+    slots = 1 * bs + np.arange(5)
+    a = int8_case(rng, hkv=hkv, bs=bs, d=d)
+    b = int8_case(rng, hkv=hkv, bs=bs, d=d)
+    b[0][1] = 99
+    b[2][1] = 1e30  # stale state from a previous owner
+    orc.kv_append_int8(x, x, slots, hkv, d, bs, *a)
+    orc.kv_append_int8(x, x, slots, hkv, d, bs, *b)
+    assert np.array_equal(a[0][1, :, :5], b[0][1, :, :5])
+    assert np.array_equal(a[2][1], b[2][1])
+
+
+def test_int8_dequant_matches_closed_form(orc):
+    rng = np.random.default_rng(5)
+    q = rng.integers(-127, 128, (3, 2, 4, 8)).astype(np.int8)
+    s = rng.uniform(0.01, 1, (3, 2)).astype(np.float32)
+    x = orc.int8_dequant(q, s)
+    assert np.array_equal(x, q.astype(np.float32) * s[:, :, None, None])
