@@ -37,6 +37,7 @@ sys.path.insert(0, str(ROOT))
 import numpy as np  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+KV_NAMES = {0: "f32", 1: "bf16", 2: "int8"}
 
 
 def log(*a):
@@ -54,6 +55,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-ceiling-probe", action="store_true",
                     help="skip the read-bandwidth probes that price the practical ceiling")
+    ap.add_argument("--kv", default="auto", choices=["auto", "int8"],
+                    help="KV element type: the config's own (auto) or INT8 with "
+                         "per-(block, kv head) scales")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="run one device-to-device copy of this size first (a known-size "
                          "dispatch that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -259,6 +263,9 @@ def main():
     from ehip import workloads
 
     w = workloads.CONFIGS[args.config]()
+    q8 = args.kv == "int8"
+    if q8:
+        w.kv_dtype = ehip.KV_INT8
     layers = args.layers or w.layers
     H, Hkv, d, bs = w.heads, w.kv_heads, w.head_dim, w.block_size
     R = w.rows
@@ -276,11 +283,24 @@ def main():
         a.free()
         b.free()
         log(f"[bench] copy probe: {nbytes} bytes device-to-device")
-    slabs, qs, kns, vns, outs = [], [], [], [], []
+    slabs, scales, qs, kns, vns, outs = [], [], [], [], [], []
     for layer in range(layers):
         ks, vs = ctx.alloc(slab_bytes), ctx.alloc(slab_bytes)
-        ctx.fill_normal(ks, w.pool_blocks * Hkv * bs * d, w.kv_dtype, 0.0, w.qkv_std, 10 + layer)
-        ctx.fill_normal(vs, w.pool_blocks * Hkv * bs * d, w.kv_dtype, 0.0, w.qkv_std, 1000 + layer)
+        if q8:
+            # int8 slabs: random bytes (bf16 normals over the same memory);
+            # scales: fp32 normals, one per (block, kv head)
+            n16 = slab_bytes // 2
+            ctx.fill_normal(ks, n16, ehip.KV_BF16, 0.0, 1.0, 10 + layer)
+            ctx.fill_normal(vs, n16, ehip.KV_BF16, 0.0, 1.0, 1000 + layer)
+            kss, vss = ctx.alloc(w.pool_blocks * Hkv * 4), ctx.alloc(w.pool_blocks * Hkv * 4)
+            ctx.fill_normal(kss, w.pool_blocks * Hkv, ehip.KV_F32, 0.0, 0.01, 5000 + layer)
+            ctx.fill_normal(vss, w.pool_blocks * Hkv, ehip.KV_F32, 0.0, 0.01, 6000 + layer)
+            scales.append((kss, vss))
+        else:
+            ctx.fill_normal(ks, w.pool_blocks * Hkv * bs * d, w.kv_dtype, 0.0, w.qkv_std,
+                            10 + layer)
+            ctx.fill_normal(vs, w.pool_blocks * Hkv * bs * d, w.kv_dtype, 0.0, w.qkv_std,
+                            1000 + layer)
         slabs.append((ks, vs))
         q, kn, vn = ctx.alloc(R * H * d * 4), ctx.alloc(R * Hkv * d * 4), ctx.alloc(R * Hkv * d * 4)
         ctx.fill_normal(q, R * H * d, ehip.KV_F32, 0.0, w.qkv_std, 2000 + layer)
@@ -300,10 +320,17 @@ def main():
         ctx._check(ctx.step_upload(g, st))
         for layer in range(layers):
             ks, vs = slabs[layer]
-            ctx._check(ctx.step_kv_append(kns[layer], vns[layer], ks, vs))
+            if q8:
+                kss, vss = scales[layer]
+                ctx._check(ctx.step_kv_append_int8(kns[layer], vns[layer], ks, vs, kss, vss))
+            else:
+                ctx._check(ctx.step_kv_append(kns[layer], vns[layer], ks, vs))
             if evs is not None:
                 ctx.record(evs[layer][0])
-            ctx._check(ctx.step_attention(qs[layer], ks, vs, outs[layer]))
+            if q8:
+                ctx._check(ctx.step_attention_int8(qs[layer], ks, vs, kss, vss, outs[layer]))
+            else:
+                ctx._check(ctx.step_attention(qs[layer], ks, vs, outs[layer]))
             if evs is not None:
                 ctx.record(evs[layer][1])
 
@@ -359,9 +386,9 @@ def main():
         "data": "synthetic",
         "config": {
             "workload": (f"{w.name}: {w.num_seqs} sequences, {layers} layers, H={H} Hkv={Hkv} "
-                         f"d={d} bs={bs}, kv {'bf16' if w.kv_dtype else 'fp32'}, "
+                         f"d={d} bs={bs}, kv {KV_NAMES[w.kv_dtype]}, "
                          f"sum L={tok}, rows={R}"),
-            "kv_dtype": "bf16" if w.kv_dtype else "f32",
+            "kv_dtype": KV_NAMES[w.kv_dtype],
             "num_seqs": w.num_seqs, "layers": layers, "sum_context": tok,
             "work_items": items, "split_partials": partials,
             "parallelism": "single GPU",
@@ -386,14 +413,17 @@ def main():
     if not args.no_ceiling_probe:
         result["ceiling"] = ceiling_probe(ctx, w, slabs[0], slab_bytes)
         log(f"[bench] read ceiling: {result['ceiling']}")
-    pre = time_chunks(ctx, ehip, w, slabs, qs, outs, layers)
+    # The chunk, fused-RoPE and re-prefill measurements run the fp32/bf16
+    # entry points; an INT8 run reports the decode step alone.
+    pre = None if q8 else time_chunks(ctx, ehip, w, slabs, qs, outs, layers)
     if pre is not None:
         result["prefill"] = pre
         log(f"[bench] prefill chunks: {pre['us_per_layer']} us/layer, {pre['tflops']} TFLOP/s")
-    ra = time_rope_append(ctx, ehip, w, slabs, qs, kns, vns, layers)
-    result["rope_append"] = ra
-    log(f"[bench] fused RoPE + append: {ra}")
-    if w.name == "C5":
+    if not q8:
+        ra = time_rope_append(ctx, ehip, w, slabs, qs, kns, vns, layers)
+        result["rope_append"] = ra
+        log(f"[bench] fused RoPE + append: {ra}")
+    if w.name == "C5" and not q8:
         ev = c5_reprefill(ctx, ehip, w, slabs, layers)
         result["reprefill_event"] = ev
         # One 4096-token re-prefill every 50 decode steps, amortised per step.

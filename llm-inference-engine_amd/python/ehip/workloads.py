@@ -71,6 +71,9 @@ class Workload:
         q_o = 4 * R * H * d * 2
         bt = 4 * int(np.sum((L + bs - 1) // bs)) + 4 * (B + 1) + 4 * B
         append = R * self.kv_heads * d * 2 * (4 + s) if with_append else 0
+        if self.kv_dtype == KV_INT8:
+            # the K and V scales of every unique (block, kv head) tile
+            unique_kv += 8 * self.kv_heads * (int(np.sum((L + bs - 1) // bs)) - shared_extra)
         return {"unique_kv": unique_kv, "logical_kv": logical_kv, "q_o": q_o, "tables": bt,
                 "append": append, "total": unique_kv + q_o + bt + append}
 
