@@ -7,18 +7,20 @@
 // softmax over the dequantised values x = q * scale as the fp32/bf16 paths
 // (kernels::PagedDecodeAttentionBatchedF32, src/kernels/paged_attention.h:105-110):
 //
-//  * QK^T runs on v_mfma_f32_16x16x32_bf16. Lane (n, kq) loads D/4 bytes of
-//    key row n in one piece (16 or 32 contiguous bytes); its 8-element chunk c
-//    is bytes [8c, 8c + 8) of that piece, i.e. head-dim elements
-//    kq * D/4 + 8c .. + 8. The query operands use the same permutation of the
-//    head dimension, so the dot products are unchanged. int8 values widen to
-//    bf16 exactly (|q| <= 127 fits bf16's 8-bit significand); Q is split into
-//    bf16 hi + lo parts as in the bf16 kernel. The 16 keys of one MFMA half
-//    lie in one block, so that half's score is scaled by the block's K scale
-//    (times softmax scale and log2 e) after the MFMA.
+//  * QK^T runs on v_mfma_i32_16x16x64_i8 with the int8 keys as they sit in
+//    the slab: lane (n, kq) loads D/4 contiguous bytes of key row n, and its
+//    16-byte chunk c covers head-dim elements kq * D/4 + 16c .. + 16. Each
+//    query row is scaled by 127 / max|q| and split into three int8 digits,
+//    q ~ s_q * (d1 + d2 / 128 + d3 / 16384) with |error| <= s_q / 32768, over
+//    the same head-dim permutation, so three integer MFMAs per chunk give the
+//    dot products exactly in int32 up to that query rounding. The 16 keys of
+//    one MFMA half lie in one block: that half's scores are
+//    (a1 + a2 / 128 + a3 / 16384) * s_q * k_scale * softmax scale * log2 e.
 //  * PV runs on the VALU in fp32: lane owns elements 4 * (lane % (D/4)) .. +4
-//    of a token row (one 4-byte load), widened and multiplied by the half's V
-//    scale; token groups are summed across lanes at the end.
+//    of a token row (one 4-byte load). The bytes are read as unsigned after
+//    flipping their sign bits (u = q + 128, one v_cvt_f32_ubyte each), scaled
+//    by the half's V scale, and the 128 * sum(p * v_scale) offset is taken out
+//    once per item; token groups are summed across lanes at the end.
 //
 // Rows past a key range read as zeros through bounded buffer descriptors and
 // are masked; split results go through the same partial/merge path as the
@@ -34,8 +36,6 @@
 namespace ehip {
 namespace {
 
-typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
-typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 
 __device__ __forceinline__ float ReadLaneF(float x, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
@@ -49,23 +49,16 @@ __device__ __forceinline__ float Max16F(float x) {
   return x;
 }
 
-// Signed byte k of w as float (exact).
-__device__ __forceinline__ float ByteF(uint32_t w, int k) {
-  return static_cast<float>(static_cast<int8_t>(w >> (8 * k)));
+typedef __attribute__((ext_vector_type(4))) int i32x4_t;
+
+// Byte k of w as an unsigned integer in float (v_cvt_f32_ubyte).
+__device__ __forceinline__ float UByteF(uint32_t w, int k) {
+  return static_cast<float>((w >> (8 * k)) & 0xFFu);
 }
 
-// Eight int8 (two dwords) widened to bf16: the bf16 of a small integer is the
-// upper half of its fp32 bits (the lower half is zero), packed two per dword.
-__device__ __forceinline__ bf16x8_t WidenQ8(uint32_t lo, uint32_t hi) {
-  uint32_t w[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t src = i < 2 ? lo : hi;
-    const uint32_t a = __float_as_uint(ByteF(src, (2 * i) & 3));
-    const uint32_t b = __float_as_uint(ByteF(src, (2 * i + 1) & 3));
-    w[i] = __builtin_amdgcn_perm(b, a, 0x07060302u);
-  }
-  return __builtin_bit_cast(bf16x8_t, make_uint4(w[0], w[1], w[2], w[3]));
+__device__ __forceinline__ uint32_t PackDigits(const int* d) {
+  return (static_cast<uint32_t>(d[0]) & 0xFFu) | ((static_cast<uint32_t>(d[1]) & 0xFFu) << 8) |
+         ((static_cast<uint32_t>(d[2]) & 0xFFu) << 16) | (static_cast<uint32_t>(d[3]) << 24);
 }
 
 template <int D, int TH>
@@ -81,13 +74,12 @@ struct TileQ8 {
   int phys[TH];
 };
 
-// QL: Q operands in LDS rather than registers. OCC: waves per SIMD.
-template <int D, int G, int TH, bool QL, int OCC>
+// OCC: waves per SIMD.
+template <int D, int G, int TH, int OCC>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(OCC)))
 void DecodeMfmaQ8(DecodeParams p) {
   using T = TileQ8<D, TH>;
   constexpr int TT = 16 * TH;
-  constexpr int NC = D / 32;
   constexpr int KB = T::KB;
   constexpr int KL = T::KL;
   constexpr int VLPT = T::VLPT;
@@ -98,7 +90,6 @@ void DecodeMfmaQ8(DecodeParams p) {
   static_assert(G >= 1 && G <= 8 && (D == 64 || D == 128), "shape");
 
   __shared__ float p_lds[TT * HP];
-  __shared__ uint4 q_lds[QL ? 2 * NC * 64 : 1];
 
   const int lane = threadIdx.x;
   const int item_idx = blockIdx.x;
@@ -114,18 +105,29 @@ void DecodeMfmaQ8(DecodeParams p) {
   const int tv = lane / VLPT;
   const bool live = n < G;
 
-  float4 qraw[NC][2];
+  float qf[KB];  // this lane's query slice: head n, elements kq * KB .. + KB
   {
     const float* qp =
         p.q + (int64_t{row} * p.heads + int64_t{hk} * G + (live ? n : 0)) * D + kq * KB;
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      qraw[c][0] = *reinterpret_cast<const float4*>(qp + c * 8);
-      qraw[c][1] = *reinterpret_cast<const float4*>(qp + c * 8 + 4);
+    for (int i = 0; i < KB; i += 4) {
+      const float4 x = *reinterpret_cast<const float4*>(qp + i);
+      qf[i] = x.x;
+      qf[i + 1] = x.y;
+      qf[i + 2] = x.z;
+      qf[i + 3] = x.w;
     }
   }
+  // The range's table slice, two block ids per lane (ranges up to 128 blocks).
   const int lb0 = tb / bs;
-  const int tab = LoadRangeTable(p, it.table_off, tb, te, lane);
+  const int nblk = (te - 1) / bs - lb0 + 1;
+  auto table_at = [&](int j) {
+    const int raw = p.table[it.table_off + lb0 + min(j, nblk - 1)];
+    const bool bad = raw < 0 || raw >= p.slab_blocks;
+    return j < nblk ? (bad ? -2 : raw) : -1;
+  };
+  const int tab = table_at(lane);
+  const int tab2 = table_at(64 + lane);
   const int8_t* kbase = static_cast<const int8_t*>(p.k_slab) + int64_t{hk} * bs * D;
   const int8_t* vbase = static_cast<const int8_t*>(p.v_slab) + int64_t{hk} * bs * D;
   const int bmask = bs - 1;
@@ -142,8 +144,9 @@ void DecodeMfmaQ8(DecodeParams p) {
 #pragma unroll
     for (int h2 = 0; h2 < TH; ++h2) {
       const int th = t0 + 16 * h2;  // wavefront-uniform; a half lies in one block (bs >= 16)
+      const int bi = min(th, te - 1) / bs - lb0;  // wavefront-uniform, < 128
       const int phys = given ? it.first[h2 > 0 ? 1 : 0]
-                             : __builtin_amdgcn_readlane(tab, min(th, te - 1) / bs - lb0);
+                             : __builtin_amdgcn_readlane(bi < 64 ? tab : tab2, bi & 63);
       const bool ok = th < te && phys >= 0;
       t.phys[h2] = ok ? phys : -1;
       const int64_t boff = int64_t{ok ? phys : 0} * p.block_stride + (th & bmask) * D;
@@ -172,56 +175,79 @@ void DecodeMfmaQ8(DecodeParams p) {
   else
     load(bufA, tb, false);
 
-  bf16x8_t qa_hi[NC], qa_lo[NC];
+  // Query digits per 16-element chunk (KL chunks), three int8 digits each.
+  i32x4_t qd[KL][3];
+  float sq4[4];  // s_q of the heads 4 * kq + i (this lane's accumulator rows)
+  {
+    float amax = 0.f;
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    const float x[8] = {qraw[c][0].x, qraw[c][0].y, qraw[c][0].z, qraw[c][0].w,
-                        qraw[c][1].x, qraw[c][1].y, qraw[c][1].z, qraw[c][1].w};
+    for (int i = 0; i < KB; ++i) amax = fmaxf(amax, fabsf(qf[i]));
+    amax = fmaxf(amax, ShflXor(amax, 16));
+    amax = fmaxf(amax, ShflXor(amax, 32));
+    const float inv = (live && amax > 0.f) ? 127.0f / amax : 0.f;
+    const float sq = live ? amax * (1.0f / 127.0f) : 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float xv = live ? x[i] : 0.f;
-      const __bf16 hb = static_cast<__bf16>(xv);
-      qa_hi[c][i] = hb;
-      qa_lo[c][i] = static_cast<__bf16>(xv - static_cast<float>(hb));
+    for (int c = 0; c < KL; ++c) {
+      uint32_t w[3][4];
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        int d1[4], d2[4], d3[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float x = qf[c * 16 + g4 * 4 + j] * inv;
+          const float r1 = rintf(x);
+          const float x2 = (x - r1) * 128.0f;
+          const float r2 = rintf(x2);
+          const float r3 = rintf((x2 - r2) * 128.0f);
+          d1[j] = static_cast<int>(r1);
+          d2[j] = static_cast<int>(r2);
+          d3[j] = static_cast<int>(r3);
+        }
+        w[0][g4] = PackDigits(d1);
+        w[1][g4] = PackDigits(d2);
+        w[2][g4] = PackDigits(d3);
+      }
+#pragma unroll
+      for (int dg = 0; dg < 3; ++dg)
+        qd[c][dg] = i32x4_t{static_cast<int>(w[dg][0]), static_cast<int>(w[dg][1]),
+                            static_cast<int>(w[dg][2]), static_cast<int>(w[dg][3])};
     }
-    if constexpr (QL) {
-      q_lds[(2 * c) * 64 + lane] = __builtin_bit_cast(uint4, qa_hi[c]);
-      q_lds[(2 * c + 1) * 64 + lane] = __builtin_bit_cast(uint4, qa_lo[c]);
-    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      sq4[i] = __shfl(sq, 4 * kq + i);  // lane 4kq+i holds head 4kq+i (kq of that lane = 0)
   }
 
-  float m[4], lsum[4], o[G][4];
+  float m[4], lsum[4], cofs[4], o[G][4];  // cofs: sum of p * v_scale per head row
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     m[i] = -INFINITY;
     lsum[i] = 0.f;
+    cofs[i] = 0.f;
   }
 #pragma unroll
   for (int h = 0; h < G; ++h) o[h][0] = o[h][1] = o[h][2] = o[h][3] = 0.f;
 
   auto process = [&](const T& t, int t0) {
-    f32x4_t acc[TH];
-#pragma unroll
-    for (int h2 = 0; h2 < TH; ++h2) {
-      acc[h2] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const uint4 w = t.k[h2][c / 2];
-        const bf16x8_t kb = (c & 1) ? WidenQ8(w.z, w.w) : WidenQ8(w.x, w.y);
-        const bf16x8_t qh = QL ? __builtin_bit_cast(bf16x8_t, q_lds[(2 * c) * 64 + lane]) : qa_hi[c];
-        const bf16x8_t ql =
-            QL ? __builtin_bit_cast(bf16x8_t, q_lds[(2 * c + 1) * 64 + lane]) : qa_lo[c];
-        acc[h2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qh, kb, acc[h2], 0, 0, 0);
-        acc[h2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ql, kb, acc[h2], 0, 0, 0);
-      }
-    }
     float s[TH][4];
 #pragma unroll
     for (int h2 = 0; h2 < TH; ++h2) {
+      i32x4_t a1 = {0, 0, 0, 0}, a2 = {0, 0, 0, 0}, a3 = {0, 0, 0, 0};
+#pragma unroll
+      for (int c = 0; c < KL; ++c) {
+        const i32x4_t kb = __builtin_bit_cast(i32x4_t, t.k[h2][c]);
+        a1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(qd[c][0], kb, a1, 0, 0, 0);
+        a2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(qd[c][1], kb, a2, 0, 0, 0);
+        a3 = __builtin_amdgcn_mfma_i32_16x16x64_i8(qd[c][2], kb, a3, 0, 0, 0);
+      }
       const bool valid = t.phys[h2] >= 0 && t0 + 16 * h2 + n < te;
       const float sc = t.ks[h2] * p.scale_log2;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) s[h2][i] = valid ? acc[h2][i] * sc : -INFINITY;
+      for (int i = 0; i < 4; ++i) {
+        const float dot = fmaf(static_cast<float>(a3[i]), 1.0f / 16384.0f,
+                               fmaf(static_cast<float>(a2[i]), 1.0f / 128.0f,
+                                    static_cast<float>(a1[i])));
+        s[h2][i] = valid ? dot * (sq4[i] * sc) : -INFINITY;
+      }
     }
     float alpha[4];
 #pragma unroll
@@ -233,13 +259,15 @@ void DecodeMfmaQ8(DecodeParams p) {
       const float mn = fmaxf(m[i], mx);
       alpha[i] = mn == -INFINITY ? 1.f : Exp2(m[i] - mn);
       m[i] = mn;
-      float ps = 0.f;
+      float ps = 0.f, pc = 0.f;
 #pragma unroll
       for (int h2 = 0; h2 < TH; ++h2) {
         s[h2][i] = mn == -INFINITY ? 0.f : Exp2(s[h2][i] - mn);
         ps += s[h2][i];
+        pc = fmaf(s[h2][i], t.vs[h2], pc);
       }
       lsum[i] = lsum[i] * alpha[i] + ps;
+      cofs[i] = cofs[i] * alpha[i] + pc;
     }
     if (kq < HR) {
 #pragma unroll
@@ -263,9 +291,9 @@ void DecodeMfmaQ8(DecodeParams p) {
 #pragma unroll
       for (int j = 0; j < VJ; ++j) {
         const int tt = 16 * h2 + j * VT + tv;
-        const uint32_t r = t.v[h2][j];
-        const float v0 = ByteF(r, 0) * vsc, v1 = ByteF(r, 1) * vsc;
-        const float v2 = ByteF(r, 2) * vsc, v3 = ByteF(r, 3) * vsc;
+        const uint32_t r = t.v[h2][j] ^ 0x80808080u;  // u = q + 128
+        const float v0 = UByteF(r, 0) * vsc, v1 = UByteF(r, 1) * vsc;
+        const float v2 = UByteF(r, 2) * vsc, v3 = UByteF(r, 3) * vsc;
         float pv[HP];
 #pragma unroll
         for (int r4 = 0; r4 < HR; ++r4) {
@@ -297,6 +325,7 @@ void DecodeMfmaQ8(DecodeParams p) {
   }
 
   ReportRejectedBlocks(p, tab);
+  ReportRejectedBlocks(p, tab2);
   // Token groups of a V load hold partial sums of the same elements.
   if constexpr (VT > 1) {
 #pragma unroll
@@ -304,9 +333,20 @@ void DecodeMfmaQ8(DecodeParams p) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) o[h][e] = SumAcross<VLPT>(o[h][e]);
   }
-  float lrow[4];
+  float lrow[4], crow[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) lrow[i] = SumGroup16(lsum[i]);
+  for (int i = 0; i < 4; ++i) {
+    lrow[i] = SumGroup16(lsum[i]);
+    crow[i] = 128.0f * SumGroup16(cofs[i]);
+  }
+  // The unsigned bytes carried +128: take 128 * sum(p * v_scale) out of every
+  // element of each head.
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    const float c = ReadLaneF(crow[h & 3], 16 * (h >> 2));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[h][e] -= c;
+  }
 
   const RowDesc rd = p.rows[row];
   if (rd.nsplit == 1) {
@@ -341,8 +381,8 @@ void DecodeMfmaQ8(DecodeParams p) {
 
 template <int D, int G>
 void LaunchQ8Shape(const DecodeParams& p, hipStream_t stream) {
-  constexpr bool QL = D * G >= 512;
-  hipLaunchKernelGGL((DecodeMfmaQ8<D, G, 2, QL, 2>), dim3(p.n_items), dim3(64), 0, stream, p);
+  // 32-token tiles: 64-token tiles measured slower on C4 and C5.
+  hipLaunchKernelGGL((DecodeMfmaQ8<D, G, 2, 2>), dim3(p.n_items), dim3(64), 0, stream, p);
 }
 
 }  // namespace

@@ -76,13 +76,20 @@ int ValidateGeometry(const ehip_geometry& g, std::string* err) {
   return EHIP_OK;
 }
 
+int32_t MaxSplitTokens(const ehip_geometry& g) {
+  // A work item's table slice sits in the wavefront's lanes: one block id per
+  // lane (64 blocks), two per lane for the INT8 kernel (128 blocks), whose
+  // items carry half the bytes per key and so want longer ranges.
+  return (g.kv_dtype == EHIP_KV_INT8 ? 128 : 64) * g.block_size;
+}
+
 int32_t ChooseSplitTokens(const ehip_geometry& g, int64_t unit_tokens) {
-  const int32_t max_split = 64 * g.block_size;
+  const int32_t max_split = MaxSplitTokens(g);
   if (const char* env = std::getenv("EHIP_SPLIT_TOKENS")) {
     const long v = std::strtol(env, nullptr, 10);
     if (v > 0) return static_cast<int32_t>(std::min<int64_t>(RoundUp(v, kTile), max_split));
   }
-  int64_t target = kTargetItems;
+  int64_t target = g.kv_dtype == EHIP_KV_INT8 ? kTargetItems / 2 : kTargetItems;
   if (const char* env = std::getenv("EHIP_TARGET_ITEMS")) {
     const long v = std::strtol(env, nullptr, 10);
     if (v > 0) target = v;
@@ -120,7 +127,7 @@ struct KeyRange {
 void FinishPlan(const ehip_geometry& g, Plan* plan, bool allow_joint,
                 const std::vector<int32_t>* skip = nullptr) {
   const int32_t bs = g.block_size;
-  const int32_t max_split = 64 * bs;
+  const int32_t max_split = MaxSplitTokens(g);
   const size_t n = plan->rows.size();
   auto skipped = [&](size_t r) { return skip && (*skip)[r] > 0; };
   int64_t units = 0;

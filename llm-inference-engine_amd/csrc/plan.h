@@ -119,6 +119,8 @@ int64_t BlockStride(const ehip_geometry& g);
 // the chip (a few per SIMD) without drowning in partial-merge traffic.
 // EHIP_SPLIT_TOKENS overrides it (rounded to a multiple of 64).
 int32_t ChooseSplitTokens(const ehip_geometry& g, int64_t unit_tokens);
+// Longest key range of one decode work item.
+int32_t MaxSplitTokens(const ehip_geometry& g);
 
 // Validates the step (lengths, CSR offsets, every table id and slot in range)
 // and builds the plan. Chunks of at least kMinPrefillRows rows go to the MFMA

@@ -124,13 +124,15 @@ def test_int8_steps_bit_exact_append_and_attention(gctx, ehip_mod, orc, H, Hkv, 
     run.free()
 
 
-def test_int8_long_rows_split_and_merged(gctx, ehip_mod, orc, monkeypatch):
+@pytest.mark.parametrize("split", ["128", "2048"])
+def test_int8_long_rows_split_and_merged(gctx, ehip_mod, orc, monkeypatch, split):
     """Decode rows long enough to be split into several key ranges (the split
-    partials go through the shared merge)."""
-    monkeypatch.setenv("EHIP_SPLIT_TOKENS", "128")
+    partials go through the shared merge); 2048-key ranges span 128 blocks, the
+    longest an INT8 work item takes."""
+    monkeypatch.setenv("EHIP_SPLIT_TOKENS", split)
     rng = np.random.default_rng(7)
     H, Hkv, d, bs = 32, 8, 128, 16
-    lens = [1500, 2049, 17, 640]
+    lens = [1500, 2049, 17, 640, 4100]
     pool = sum((L + bs - 1) // bs for L in lens) + 5
     tabs = make_tables(rng, lens, bs, pool)
     run = Int8Run(gctx, ehip_mod, H, Hkv, d, bs, pool, seed=11)
