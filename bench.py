@@ -64,11 +64,13 @@ def parse():
     return ap.parse_args()
 
 
-def traffic_from_profiles(config: str):
+def traffic_from_profiles(config: str, kv: str = ""):
     """HBM bytes per attention launch from the committed rocprofv3 PMC summary
     (FETCH_SIZE / WRITE_SIZE per dispatch, each scaled by the same counter's
-    reading on a copy kernel of known size), or None."""
-    p = ROOT / "profiles" / f"decode_{config.lower()}_traffic.json"
+    reading on a copy kernel of known size), or None. kv: "" for the
+    config's own KV type, "int8" for the INT8 run."""
+    suffix = f"_{kv}" if kv else ""
+    p = ROOT / "profiles" / f"decode_{config.lower()}{suffix}_traffic.json"
     if not p.exists():
         return None
     t = json.loads(p.read_text())
@@ -369,7 +371,7 @@ def main():
     attn_avg = float(np.mean(attn_ms)) / 1e3
     achieved = attn_bytes / attn_avg / 1e9
     tok = int(w.context_lens.sum())
-    traffic = traffic_from_profiles(w.name)
+    traffic = traffic_from_profiles(w.name, "int8" if q8 else "")
 
     result = {
         "metric": "ragged paged-attn decode: HBM GB/s (% of 8 TB/s) + attended KV tok/s per step",
