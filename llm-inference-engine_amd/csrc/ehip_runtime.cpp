@@ -270,6 +270,8 @@ int LaunchAttention(ehip_ctx* ctx, const float* q, const void* k_slab, const voi
   p.scale_log2 = g.scale * 1.4426950408889634f;
   p.k_scale = k_scale;
   p.v_scale = v_scale;
+  p.max_length = plan.max_length;
+  p.has_prefill = plan.prefill.empty() ? 0 : 1;
   EHIP_HIP(ctx, ehip::LaunchDecode(p, g.kv_dtype, &ctx->queue, ctx->stream));
   return EHIP_OK;
 }

@@ -40,6 +40,8 @@ struct DecodeParams {
   int32_t d;
   int32_t bs;
   float scale_log2;         // scale * log2(e)
+  int64_t max_length;       // longest row (keys attended)
+  int32_t has_prefill;      // the step also has MFMA prefill items
   const float* k_scale;     // INT8 KV: per-(block, kv head) scales [slab_blocks, Hkv]
   const float* v_scale;
   uint32_t* queue;          // this launch's item counter (zero at launch; MFMA kernel only)

@@ -31,6 +31,14 @@ namespace ehip {
 namespace {
 
 constexpr int kWavesPerBlock = 4;
+// Steps with at most this many (row, kv head) units take the workgroup-per-unit
+// kernel (4 or 8 wavefronts each, 2048 wavefronts at most).
+constexpr int64_t kWgMaxUnits = 256;
+// ... and only when no row needs more than this many 32-key tiles per
+// wavefront: past that, the split-KV path (more wavefronts on a long row,
+// merged by a second kernel) measured faster (C2: rows up to 2049 keys,
+// 32.6 against 39.0 us per layer; C1: one 513-key row, 17.3 against 22.0 us).
+constexpr int kWgMaxTilesPerWave = 6;
 
 template <class KV>
 struct KvT;
@@ -73,7 +81,8 @@ __device__ __forceinline__ float KvAt(const uint16_t* p, int64_t i) {
 // Specialised kernel body: KV in {f32, bf16}, D in {64, 128}, G = g exactly.
 template <class KV, int D, int G>
 __device__ __forceinline__ void DecodeValuRow(const DecodeParams& p, int row, int hk, int tb,
-                                              int te, int split, int table_off) {
+                                              int te, int split, int table_off,
+                                              float* lds_o = nullptr, float* lds_ml = nullptr) {
   constexpr int EPV = KvT<KV>::EPV;
   constexpr int LPT = (G * D / 8 > 64) ? 16 : 8;  // lanes per token row
   constexpr int E = D / LPT;                      // elements per lane
@@ -238,6 +247,25 @@ __device__ __forceinline__ void DecodeValuRow(const DecodeParams& p, int row, in
     for (int e = 0; e < E; ++e) o[h][e] = SumAcross<LPT>(o[h][e]);
   }
 
+  if (lds_o) {  // a wavefront's share of a workgroup-wide range: unnormalised (o, m, l)
+    if (tl == 0) {
+      float* po = lds_o + sub * EPV;
+#pragma unroll
+      for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int v = 0; v < NV; ++v)
+#pragma unroll
+          for (int c = 0; c < EPV; ++c) po[h * D + v * VSPAN + c] = o[h][v * EPV + c];
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        lds_ml[h * 2 + 0] = m[h];
+        lds_ml[h * 2 + 1] = l[h];
+      }
+    }
+    return;
+  }
   if (rd.nsplit == 1) {
     if (tl == 0) {
       float* op = p.out + (int64_t{row} * p.heads + int64_t{hk} * G) * D + sub * EPV;
@@ -296,6 +324,57 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void DecodeValu(DecodeParams p
   const ItemRef it = DecodeItem(p.items[item_idx]);
   for (int r = 0; r < it.nrows; ++r)
     DecodeValuRow<KV, D, G>(p, it.rows[r], it.hk, it.tb, it.te, it.split, it.table_off);
+}
+
+// ----------------------------------------------------------------------------
+// Small steps (few (row, kv head) units, as in single-sequence and 32-row fp32
+// decode): one workgroup of NW wavefronts per unit. Each wavefront takes an
+// equal run of whole 32-key tiles of the row and leaves its unnormalised
+// (o, m, l) in LDS; after a barrier the workgroup merges them (the split
+// merge's log-sum-exp, in wavefront order) and writes the row's output. One
+// launch, no global partials and no merge kernel, and NW times the bytes in
+// flight per row of the one-item-per-wavefront kernel.
+template <class KV, int D, int G, int NW>
+__global__ __launch_bounds__(NW * 64) void DecodeValuWg(DecodeParams p) {
+  __shared__ float lds_o[NW * G * D];
+  __shared__ float lds_ml[NW * G * 2];
+  const int unit = blockIdx.x;
+  const int row = unit / p.kv_heads;
+  const int hk = unit - row * p.kv_heads;
+  const RowDesc rd = p.rows[row];
+  const int len = rd.length;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tiles = (len + 31) / 32;
+  const int tb = (tiles * w) / NW * 32;
+  const int te = min(len, (tiles * (w + 1)) / NW * 32);
+  if (tb < te) {
+    DecodeValuRow<KV, D, G>(p, row, hk, tb, te, 0, rd.table_off, lds_o + w * G * D,
+                            lds_ml + w * G * 2);
+  } else {
+    const int lane = threadIdx.x & 63;
+    for (int j = lane; j < G * D; j += 64) lds_o[w * G * D + j] = 0.f;
+    if (lane < G) {
+      lds_ml[(w * G + lane) * 2 + 0] = -INFINITY;
+      lds_ml[(w * G + lane) * 2 + 1] = 0.f;
+    }
+  }
+  __syncthreads();
+  float* out = p.out + (int64_t{row} * p.heads + int64_t{hk} * G) * D;
+  for (int j = threadIdx.x; j < G * D; j += NW * 64) {
+    const int h = j / D;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < NW; ++u) mx = fmaxf(mx, lds_ml[(u * G + h) * 2]);
+    float lsum = 0.f, acc = 0.f;
+#pragma unroll
+    for (int u = 0; u < NW; ++u) {
+      const float mu = lds_ml[(u * G + h) * 2];
+      const float wt = mu == -INFINITY ? 0.f : Exp2(mu - mx);
+      lsum += lds_ml[(u * G + h) * 2 + 1] * wt;
+      acc += wt * lds_o[u * G * D + j];
+    }
+    out[j] = acc * (1.0f / lsum);
+  }
 }
 
 // ----------------------------------------------------------------------------
@@ -482,6 +561,47 @@ hipError_t LaunchTyped(const DecodeParams& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// Workgroup-per-unit decode for small fp32 steps; false when it does not
+// apply (too many units, a row longer than NW wavefronts' table slices, or a
+// shape without a specialised kernel). EHIP_DECODE_WG=0 turns it off.
+bool LaunchSmallStep(const DecodeParams& p, hipStream_t stream, hipError_t* err) {
+  const char* env = std::getenv("EHIP_DECODE_WG");
+  if (env && env[0] == '0') return false;
+  const int64_t units = int64_t{p.n_rows} * p.kv_heads;
+  if (units < 1 || units > kWgMaxUnits) return false;
+  const bool aligned = (reinterpret_cast<uintptr_t>(p.k_slab) % 16 == 0) &&
+                       (reinterpret_cast<uintptr_t>(p.v_slab) % 16 == 0) &&
+                       (reinterpret_cast<uintptr_t>(p.q) % 16 == 0) &&
+                       (reinterpret_cast<uintptr_t>(p.out) % 16 == 0) &&
+                       (p.block_stride % 4 == 0);
+  if (!aligned) return false;
+  const dim3 grid(static_cast<uint32_t>(units));
+  // A wavefront's run (at most len / NW + 32 keys, starting on a 32-key
+  // boundary) must fit its 64-entry table slice.
+#define EHIP_WG_CASE(DD, GG, NW)                                                           \
+  if (p.d == DD && p.group == GG) {                                                        \
+    if (p.max_length > int64_t{NW} * std::min(64 * p.bs - 32 - p.bs, kWgMaxTilesPerWave * 32)) \
+      return false;                                                                        \
+    hipLaunchKernelGGL((DecodeValuWg<float, DD, GG, NW>), grid, dim3(NW * 64), 0, stream, p); \
+    *err = hipGetLastError();                                                              \
+    return true;                                                                           \
+  }
+  // Eight wavefronts per workgroup keep the register budget of the
+  // one-item kernels (two workgroup wavefronts per SIMD); the shapes that
+  // would spill there take four.
+  EHIP_WG_CASE(64, 1, 8)
+  EHIP_WG_CASE(64, 2, 8)
+  EHIP_WG_CASE(64, 4, 8)
+  EHIP_WG_CASE(64, 7, 8)
+  EHIP_WG_CASE(64, 8, 4)
+  EHIP_WG_CASE(128, 1, 8)
+  EHIP_WG_CASE(128, 2, 8)
+  EHIP_WG_CASE(128, 7, 8)
+  EHIP_WG_CASE(128, 8, 4)
+#undef EHIP_WG_CASE
+  return false;
+}
+
 hipError_t LaunchSplits(const DecodeParams& p, int kv_dtype, QueueState* queue,
                         hipStream_t stream) {
   if (kv_dtype == EHIP_KV_INT8) {
@@ -505,6 +625,12 @@ hipError_t LaunchSplits(const DecodeParams& p, int kv_dtype, QueueState* queue,
 
 hipError_t LaunchDecode(const DecodeParams& p, int kv_dtype, QueueState* queue,
                         hipStream_t stream) {
+  // Small fp32 steps without prefill chunks: one workgroup per (row, kv head),
+  // merged in LDS (the plan's split partials are not used).
+  if (kv_dtype == EHIP_KV_F32 && p.n_items > 0 && !p.has_prefill) {
+    hipError_t e = hipSuccess;
+    if (LaunchSmallStep(p, stream, &e)) return e;
+  }
   // Split rows may come from prefill key splits alone (no decode items).
   hipError_t e = p.n_items > 0 ? LaunchSplits(p, kv_dtype, queue, stream) : hipSuccess;
   if (e != hipSuccess || p.n_merge == 0) return e;

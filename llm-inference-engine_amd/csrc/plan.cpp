@@ -450,6 +450,7 @@ int BuildSingleRowPlan(const ehip_geometry& g, int64_t length, int64_t num_block
     return Fail(err, EHIP_INVALID_ARGUMENT, "ceil(length/bs) exceeds num_blocks=%lld",
                 num_blocks);
   plan->rows.assign(1, RowDesc{0, static_cast<int32_t>(length), 0, 0});
+  plan->max_length = length;
   plan->table_ids.clear();
   plan->slots.clear();
   FinishPlan(g, plan, false);

@@ -340,8 +340,10 @@ def test_bf16_decode_gqa_sweep(gctx, orc, H, Hkv, d):
 
 @pytest.mark.parametrize("split", ["64", "128", "512", "1024"])
 def test_split_count_independence(gctx, orc, split, monkeypatch):
-    # The merged result must not depend on how the keys were split.
+    # The merged result must not depend on how the keys were split (the
+    # split-KV path: the workgroup-per-row kernel for small steps is off).
     monkeypatch.setenv("EHIP_SPLIT_TOKENS", split)
+    monkeypatch.setenv("EHIP_DECODE_WG", "0")
     rng = np.random.default_rng(3)
     lengths = [4000, 17, 1025, 2048, 64]
     H, Hkv, d, bs = 32, 8, 128, 16
@@ -406,9 +408,11 @@ def run_step(gctx, ehip_mod, orc, w, seed, layers=1):
     return results
 
 
-def test_step_c2_ragged_decode(gctx, ehip_mod, orc):
+@pytest.mark.parametrize("wg", ["1", "0"])
+def test_step_c2_ragged_decode(gctx, ehip_mod, orc, wg, monkeypatch):
     """C2 shape (B=32, L~U[64,2048]+1, fp32 pool 1.25x need): two layers of
     append + attention through the per-step descriptor."""
+    monkeypatch.setenv("EHIP_DECODE_WG", wg)  # workgroup per (row, kv head), or split-KV
     from ehip import workloads
     w = workloads.c2()
     for got, ref, *_ in run_step(gctx, ehip_mod, orc, w, 7, layers=2):
@@ -550,6 +554,7 @@ def test_step_c4_shape_with_shared_prefix_blocks(gctx, ehip_mod, orc, kernel, mo
 
 @pytest.mark.parametrize("joint", ["1", "0"])
 def test_step_shared_prefix_fp32_valu(gctx, ehip_mod, orc, joint, monkeypatch):
+    monkeypatch.setenv("EHIP_DECODE_WG", "0")  # joint items live in the split-KV path
     """Pair-shared prefix blocks through the fp32 VALU kernel, with and without
     joint work items (joint items are processed row by row there)."""
     monkeypatch.setenv("EHIP_NO_JOINT", "0" if joint == "1" else "1")
@@ -604,3 +609,29 @@ def test_bandwidth_probes(gctx, ehip_mod):
     assert rc == ehip_mod.INVALID_ARGUMENT
     assert ehip_mod.lib().ehip_probe_stream_read(gctx.h, k.ptr, 8, 0, 1,
                                                  C.byref(out)) == ehip_mod.INVALID_ARGUMENT
+
+
+@pytest.mark.parametrize("H,Hkv,d", [(14, 2, 64), (32, 8, 128), (8, 8, 128), (28, 4, 64),
+                                     (8, 1, 128), (24, 3, 64)])
+@pytest.mark.parametrize("lens", [[1, 17, 33, 1500, 513], [1024, 1536, 1], [32, 64, 96],
+                                  [4000, 17]])
+def test_small_step_workgroup_per_row(gctx, orc, H, Hkv, d, lens, monkeypatch):
+    """Small fp32 steps with short rows take one workgroup per (row, kv head),
+    its wavefronts splitting the row's tiles and merging in LDS (a 4000-key
+    row goes to the split-KV path instead): against the oracle, and against
+    the split-KV path on the same inputs (both within the fp32 bar)."""
+    rng = np.random.default_rng(H + 7 * d + len(lens))
+    bs = 16
+    q, ks, vs, tables = batched_case(orc, rng, lens, H, Hkv, d, bs)
+    ref = orc.paged_decode_batched(q, ks, vs, tables, lens, H, Hkv, d, bs, scale_for(d))
+    outs = []
+    for wg in ("1", "0"):
+        monkeypatch.setenv("EHIP_DECODE_WG", wg)
+        out = gctx.alloc(q.nbytes)
+        assert gctx.paged_decode_batched(gctx.to_device(q), gctx.to_device(ks),
+                                         gctx.to_device(vs), tables, lens, H, Hkv, d, bs, 0,
+                                         ks.shape[0], scale_for(d), out) == 0
+        gctx.sync()
+        outs.append(out.download(np.float32, q.shape))
+        check_fp32(outs[-1], ref)
+    assert rel_norm(outs[0], outs[1]) <= FP32_REL
