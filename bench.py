@@ -58,6 +58,10 @@ def parse():
     ap.add_argument("--kv", default="auto", choices=["auto", "int8"],
                     help="KV element type: the config's own (auto) or INT8 with "
                          "per-(block, kv head) scales")
+    ap.add_argument("--graph", action="store_true",
+                    help="time the step as one eager descriptor upload plus one replay of a "
+                         "captured HIP graph of the per-layer launches (stream capture on a "
+                         "stream handed to the context with ehip_set_stream)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="run one device-to-device copy of this size first (a known-size "
                          "dispatch that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -364,6 +368,48 @@ def main():
     log("[bench] sampled-step mean us: " + " ".join(f"{x:.0f}" for x in a.mean(axis=1)))
 
     t_step = max(wall, gpu_ms / 1e3) / K
+    graph_info = None
+    if args.graph:
+        # The per-layer launches of the uploaded step, captured once and
+        # replayed per step (the step's plan is the same every step here); the
+        # descriptor upload stays eager. Per-launch events above came from the
+        # eager steps.
+        from ehip import hipgraph
+        gs = hipgraph.Stream()
+        ctx._check(ehip.lib().ehip_set_stream(ctx.h, gs.h))
+        ctx._check(ctx.step_upload(g, st))
+        ctx.sync()
+        graph = hipgraph.Graph()
+
+        def layer_launches():
+            for layer in range(layers):
+                ks, vs = slabs[layer]
+                if q8:
+                    kss, vss = scales[layer]
+                    ctx._check(ctx.step_kv_append_int8(kns[layer], vns[layer], ks, vs, kss, vss))
+                    ctx._check(ctx.step_attention_int8(qs[layer], ks, vs, kss, vss, outs[layer]))
+                else:
+                    ctx._check(ctx.step_kv_append(kns[layer], vns[layer], ks, vs))
+                    ctx._check(ctx.step_attention(qs[layer], ks, vs, outs[layer]))
+
+        graph.capture(gs, layer_launches)
+        for _ in range(args.warmup):
+            ctx._check(ctx.step_upload(g, st))
+            graph.replay(gs)
+        ctx.sync()
+        t0 = time.perf_counter()
+        for _ in range(K):
+            ctx._check(ctx.step_upload(g, st))
+            graph.replay(gs)
+        ctx.sync()
+        t_graph = (time.perf_counter() - t0) / K
+        log(f"[bench] graph replay: {t_graph * 1e3:.3f} ms/step (eager {t_step * 1e3:.3f})")
+        graph_info = {"eager_ms_per_step": round(t_step * 1e3, 4),
+                      "graph_ms_per_step": round(t_graph * 1e3, 4)}
+        t_step = t_graph
+        ctx._check(ehip.lib().ehip_set_stream(ctx.h, None))
+        graph.close()
+        gs.close()
     per_layer = w.bytes_per_layer(with_append=True)
     step_bytes = per_layer["total"] * layers
     value = step_bytes / t_step / 1e9
@@ -412,6 +458,8 @@ def main():
             "timed_steps_sampled": len(sampled),
         },
     }
+    if graph_info is not None:
+        result["launch"] = dict(graph_info, mode="captured graph of the per-layer launches")
     if not args.no_ceiling_probe:
         result["ceiling"] = ceiling_probe(ctx, w, slabs[0], slab_bytes)
         log(f"[bench] read ceiling: {result['ceiling']}")

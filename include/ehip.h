@@ -101,6 +101,16 @@ int ehip_device_count(int* out);
 /* Waits for all enqueued work; returns InvalidArgument if a kernel skipped an
  * out-of-range slot or block id since the previous ehip_sync. */
 int ehip_sync(ehip_ctx* ctx);
+/* Enqueue the context's work on a caller's HIP stream (a hipStream_t passed
+ * as void*), or back on the context's own stream when NULL. The per-layer
+ * calls (ehip_step_kv_append*, ehip_step_rope_kv_append,
+ * ehip_step_attention*) then record into a graph the caller captures on that
+ * stream: they enqueue kernels only (no allocation, copy, memset or
+ * synchronisation), and the persistent decode kernel leaves its queue
+ * counters zero, so a captured layer sequence replays without host work.
+ * ehip_step_upload copies the step descriptor and is not captured. No
+ * counterpart in the reference (its kernels run on the calling thread). */
+int ehip_set_stream(ehip_ctx* ctx, void* stream);
 
 /* ------------------------------------------------------------ memory ----- */
 /* HBM allocation, 256-byte aligned, zero-filled (the reference BlockPool

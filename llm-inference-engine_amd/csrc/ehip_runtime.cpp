@@ -17,7 +17,8 @@
 
 struct ehip_ctx {
   int device = 0;
-  hipStream_t stream = nullptr;
+  hipStream_t stream = nullptr;      // the stream every call enqueues on
+  hipStream_t own_stream = nullptr;  // the context's own (created at init)
   std::string last_error;
 
   // Step descriptor: host staging (pinned, double-buffered so building step
@@ -35,7 +36,7 @@ struct ehip_ctx {
   size_t d_part_bytes = 0;
   int32_t* d_err = nullptr;
   // Item-queue counters of the persistent decode kernel: two words of the
-  // error page (zeroed at creation), used in turn by successive launches.
+  // error page (zeroed at creation; every launch leaves them zero).
   ehip::QueueState queue{};
 
   // The uploaded step.
@@ -304,7 +305,8 @@ int ehip_init(int device, ehip_ctx** out) {
     hipError_t e = hipSetDevice(device);
     if (e != hipSuccess) { rc = HipFail(ctx, e, "hipSetDevice"); break; }
     // Default priority (a non-default priority stream has hung on this pool).
-    e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    e = hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking);
+    ctx->stream = ctx->own_stream;
     if (e != hipSuccess) { rc = HipFail(ctx, e, "hipStreamCreate"); break; }
     e = hipMalloc(&ctx->d_err, 256);
     if (e != hipSuccess) { rc = HipFail(ctx, e, "hipMalloc(err)"); break; }
@@ -312,7 +314,6 @@ int ehip_init(int device, ehip_ctx** out) {
     if (e != hipSuccess) { rc = HipFail(ctx, e, "hipMemset(err)"); break; }
     // Page words: 0 range flags, 32 probe sink, 48-49 decode item queue.
     ctx->queue.d_pair = reinterpret_cast<uint32_t*>(ctx->d_err) + 48;
-    ctx->queue.parity = 0;
   } while (false);
   if (rc != EHIP_OK) {
     ehip_destroy(ctx);
@@ -333,7 +334,7 @@ int ehip_destroy(ehip_ctx* ctx) {
   if (ctx->d_desc) (void)hipFree(ctx->d_desc);
   if (ctx->d_part) (void)hipFree(ctx->d_part);
   if (ctx->d_err) (void)hipFree(ctx->d_err);
-  if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+  if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
   delete ctx;
   return EHIP_OK;
 }
@@ -356,6 +357,12 @@ int ehip_sync(ehip_ctx* ctx) {
                     flags, (flags & ehip::kErrSlotRange) ? "slot outside slab " : "",
                     (flags & ehip::kErrBlockRange) ? "block id outside slab" : "");
   }
+  return EHIP_OK;
+}
+
+int ehip_set_stream(ehip_ctx* ctx, void* stream) {
+  if (int rc = CheckCtx(ctx)) return rc;
+  ctx->stream = stream ? static_cast<hipStream_t>(stream) : ctx->own_stream;
   return EHIP_OK;
 }
 

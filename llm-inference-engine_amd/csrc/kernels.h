@@ -44,15 +44,16 @@ struct DecodeParams {
   int32_t has_prefill;      // the step also has MFMA prefill items
   const float* k_scale;     // INT8 KV: per-(block, kv head) scales [slab_blocks, Hkv]
   const float* v_scale;
-  uint32_t* queue;          // this launch's item counter (zero at launch; MFMA kernel only)
-  uint32_t* queue_next;     // the counter of the next launch, cleared by this one
+  uint32_t* queue;          // item tickets (zero at launch; MFMA kernel only)
+  uint32_t* queue_done;     // wavefronts finished (zero at launch)
 };
 
-// Two item-queue counters of a context: a launch draws tickets from
-// d_pair[parity] and clears d_pair[1 - parity], then the parity flips.
+// The item-queue counters of a context ({tickets, wavefronts done}); each
+// persistent decode launch leaves them zero, so launches on the context's
+// stream, eager or replayed from a captured graph, need no clearing between
+// them.
 struct QueueState {
   uint32_t* d_pair;
-  int parity;
 };
 
 struct PrefillParams {

@@ -98,11 +98,10 @@ void DecodeMfmaBf16(DecodeParams p) {
   // enough that items go to the wavefronts that free up first (longest-first
   // list scheduling: the queue hands out the short items last, so the
   // wavefronts finish together), early enough to hide the atomic's latency.
-  // The first wavefront clears the counter the next launch on the stream
-  // will use (this launch's own counter was cleared by the launch before it,
-  // or at context creation).
+  // On its way out each wavefront counts itself in; the last one (which then
+  // knows every ticket has been drawn) clears both counters for the next
+  // launch, so a launch leaves them as it found them: zero.
   constexpr int kDrawAhead = 64;
-  if (blockIdx.x == 0 && lane == 0) *p.queue_next = 0u;
   for (int item_idx = blockIdx.x; item_idx < p.n_items;) {
   uint32_t ticket = 0;
   bool drawn = false;
@@ -381,6 +380,10 @@ void DecodeMfmaBf16(DecodeParams p) {
   }
   item_idx = static_cast<int>(gridDim.x + __builtin_amdgcn_readfirstlane(ticket));
   }
+  if (lane == 0 && atomicAdd(p.queue_done, 1u) == gridDim.x - 1) {
+    atomicExch(p.queue, 0u);
+    atomicExch(p.queue_done, 0u);
+  }
 }
 
 // Workgroups (one wavefront each) a launch keeps resident: the kernel's
@@ -433,8 +436,8 @@ void LaunchShape(const DecodeParams& p, hipStream_t stream, bool wide, bool deep
 bool LaunchDecodeMfma(const DecodeParams& params, QueueState* queue, hipStream_t stream,
                       hipError_t* err) {
   DecodeParams p = params;
-  p.queue = queue->d_pair + queue->parity;
-  p.queue_next = queue->d_pair + (1 - queue->parity);
+  p.queue = queue->d_pair;
+  p.queue_done = queue->d_pair + 1;
   const bool aligned = (reinterpret_cast<uintptr_t>(p.k_slab) % 16 == 0) &&
                        (reinterpret_cast<uintptr_t>(p.v_slab) % 16 == 0) &&
                        (reinterpret_cast<uintptr_t>(p.q) % 16 == 0) &&
@@ -453,8 +456,6 @@ bool LaunchDecodeMfma(const DecodeParams& params, QueueState* queue, hipStream_t
   // hands out the items instead of the queue).
   const char* pers = std::getenv("EHIP_DECODE_PERSIST");
   const bool persist = !(pers && std::strcmp(pers, "0") == 0);
-  // The counters swap roles only after a launch was enqueued, so the one the
-  // next launch uses is always the one this launch clears.
 #define EHIP_MFMA_CASE(DD, GG)                                   \
   if (p.d == DD && p.group == GG) {                              \
     if (joint)                                                   \
@@ -462,7 +463,6 @@ bool LaunchDecodeMfma(const DecodeParams& params, QueueState* queue, hipStream_t
     else                                                         \
       LaunchShape<DD, GG, 1>(p, stream, wide, deep, persist);    \
     *err = hipGetLastError();                                    \
-    if (*err == hipSuccess) queue->parity ^= 1;                  \
     return true;                                                 \
   }
   EHIP_MFMA_CASE(128, 1)

@@ -92,6 +92,7 @@ def lib():
             "ehip_paged_decode_attention_batched_bf16": [_vp, _vp, _vp, _vp, _vp, _vp, _i64,
                                                          _i64, _i64, _i64, _i64, _i64, _i64,
                                                          C.c_float, _vp],
+            "ehip_set_stream": [_vp, _vp],
             "ehip_step_upload": [_vp, C.POINTER(Geometry), C.POINTER(StepDesc)],
             "ehip_step_kv_append": [_vp, _vp, _vp, _vp, _vp],
             "ehip_step_rope_kv_append": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp],

@@ -21,6 +21,8 @@
 #include <string>
 #include <vector>
 
+#include <hip/hip_runtime_api.h>
+
 #include "batch.h"
 #include "block_pool.h"
 #include "block_table.h"
@@ -89,6 +91,14 @@ struct Register {
       ++g_failures;                                                                       \
       return;                                                                             \
     }                                                                                     \
+  } while (0)
+#define ASSERT(cond)                                                          \
+  do {                                                                        \
+    if (!(cond)) {                                                            \
+      std::fprintf(stderr, "  %s:%d: ASSERT(%s) failed\n", __FILE__, __LINE__, #cond); \
+      ++g_failures;                                                           \
+      return;                                                                 \
+    }                                                                         \
   } while (0)
 #define EXPECT_CODE(expr, c) EXPECT_EQ(static_cast<int>((expr).code()), static_cast<int>(c))
 
@@ -885,6 +895,132 @@ TEST_GPU(GpuBatchedStepRopeBf16) {
                                     static_cast<float*>(v1.get()), short_rope,
                                     static_cast<float*>(o1.get())),
               StatusCode::kInvalidArgument);
+}
+
+TEST_GPU(GpuCapturedLayersReplay) {
+  // The per-layer calls of one step (append + attention, bf16 pool, decodes
+  // and a 40-row chunk) captured on a caller stream into a HIP graph and
+  // replayed four times, the slabs restored (eagerly) before each replay:
+  // every replay's outputs and slabs bit-identical to the eager run. The
+  // persistent decode kernel runs on 3 wavefronts so each takes many items
+  // from its queue, whose counters each launch must leave zero.
+  setenv("EHIP_DECODE_SLOTS", "3", 1);
+  Gpu gpu;
+  HbmSlabAllocator hbm(gpu.ctx);
+  const int L = 3, Hkv = 2, d = 128, bs = 16, H = 8;
+  StatusOr<std::unique_ptr<BlockPool>> pr =
+      BlockPool::Create(Geom(L, Hkv, d, KvDtype::kBFloat16), bs, 96, &hbm);
+  ASSERT_OK(pr.status());
+  BlockPool& pool = **pr;
+  BatchedAttention attn(gpu.ctx, &pool, H);
+  BatchAssembler asmb;
+  std::vector<PagedKvCache> caches;
+  caches.reserve(5);
+  for (int i = 0; i < 5; ++i) caches.emplace_back(&pool, gpu.ctx);
+  // Prompts first (eager), then the step under test.
+  std::vector<std::vector<int32_t>> toks = {std::vector<int32_t>(300, 1), std::vector<int32_t>(90, 1),
+                                            std::vector<int32_t>(17, 1), std::vector<int32_t>(500, 1)};
+  std::vector<BatchSeqInput> seqs;
+  for (int s = 0; s < 4; ++s) seqs.push_back({toks[static_cast<size_t>(s)], &caches[static_cast<size_t>(s)]});
+  ASSERT_OK(asmb.AssembleMixed(seqs));
+  ASSERT_OK(attn.Upload(asmb.inputs()));
+  uint64_t seed = 7000;
+  {
+    const int64_t T = asmb.inputs().num_tokens();
+    for (int layer = 0; layer < L; ++layer) {
+      DeviceBuffer dq = ToDevice(gpu.ctx, Normal(T * H * d, seed++));
+      DeviceBuffer dk = ToDevice(gpu.ctx, Normal(T * Hkv * d, seed++));
+      DeviceBuffer dv = ToDevice(gpu.ctx, Normal(T * Hkv * d, seed++));
+      DeviceBuffer dout;
+      ASSERT_OK(dout.Reserve(gpu.ctx, T * H * d * 4));
+      ASSERT_OK(attn.ForwardLayer(layer, static_cast<float*>(dq.get()), static_cast<float*>(dk.get()),
+                                  static_cast<float*>(dv.get()), static_cast<float*>(dout.get())));
+    }
+    ASSERT_OK(FromRc(gpu.ctx, ehip_sync(gpu.ctx)));
+  }
+  std::vector<std::vector<int32_t>> step = {std::vector<int32_t>(1, 1), std::vector<int32_t>(1, 1),
+                                            std::vector<int32_t>(1, 1), std::vector<int32_t>(1, 1),
+                                            std::vector<int32_t>(40, 1)};
+  seqs.clear();
+  for (int s = 0; s < 5; ++s) seqs.push_back({step[static_cast<size_t>(s)], &caches[static_cast<size_t>(s)]});
+  ASSERT_OK(asmb.AssembleMixed(seqs));
+  const BatchInputs& in = asmb.inputs();
+  const int64_t T = in.num_tokens();
+  std::vector<DeviceBuffer> dq(L), dk(L), dv(L), dout(L);
+  for (int layer = 0; layer < L; ++layer) {
+    dq[layer] = ToDevice(gpu.ctx, Normal(T * H * d, seed++));
+    dk[layer] = ToDevice(gpu.ctx, Normal(T * Hkv * d, seed++));
+    dv[layer] = ToDevice(gpu.ctx, Normal(T * Hkv * d, seed++));
+    ASSERT_OK(dout[layer].Reserve(gpu.ctx, T * H * d * 4));
+  }
+  const int64_t slab_n = pool.slab_bytes() / 2;
+  // The slabs before the step, to restore before each run.
+  std::vector<std::vector<uint16_t>> k0(L), v0(L);
+  for (int layer = 0; layer < L; ++layer) {
+    k0[layer] = ToHost<uint16_t>(gpu.ctx, pool.k_slab(layer), slab_n);
+    v0[layer] = ToHost<uint16_t>(gpu.ctx, pool.v_slab(layer), slab_n);
+  }
+  auto restore = [&]() {
+    for (int layer = 0; layer < L; ++layer) {
+      if (ehip_copy_to_device(gpu.ctx, pool.k_slab(layer), k0[layer].data(), pool.slab_bytes()) != EHIP_OK ||
+          ehip_copy_to_device(gpu.ctx, pool.v_slab(layer), v0[layer].data(), pool.slab_bytes()) != EHIP_OK)
+        std::abort();
+    }
+  };
+  auto forward = [&]() -> Status {
+    for (int layer = 0; layer < L; ++layer)
+      if (Status st = attn.ForwardLayer(layer, static_cast<float*>(dq[layer].get()),
+                                        static_cast<float*>(dk[layer].get()),
+                                        static_cast<float*>(dv[layer].get()),
+                                        static_cast<float*>(dout[layer].get()));
+          !st.ok())
+        return st;
+    return Status::Ok();
+  };
+  ASSERT_OK(attn.Upload(in));
+  ASSERT_OK(forward());
+  ASSERT_OK(FromRc(gpu.ctx, ehip_sync(gpu.ctx)));
+  std::vector<std::vector<float>> out_e(L);
+  std::vector<std::vector<uint16_t>> k_e(L), v_e(L);
+  for (int layer = 0; layer < L; ++layer) {
+    out_e[layer] = ToHost<float>(gpu.ctx, dout[layer].get(), T * H * d);
+    k_e[layer] = ToHost<uint16_t>(gpu.ctx, pool.k_slab(layer), slab_n);
+    v_e[layer] = ToHost<uint16_t>(gpu.ctx, pool.v_slab(layer), slab_n);
+  }
+
+  hipStream_t s = nullptr;
+  ASSERT(hipStreamCreateWithFlags(&s, hipStreamNonBlocking) == hipSuccess);
+  ASSERT_OK(FromRc(gpu.ctx, ehip_set_stream(gpu.ctx, s)));
+  ASSERT_OK(attn.Upload(in));  // the descriptor copy stays outside the graph
+  ASSERT(hipStreamSynchronize(s) == hipSuccess);
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  ASSERT(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) == hipSuccess);
+  const Status captured = forward();
+  ASSERT(hipStreamEndCapture(s, &graph) == hipSuccess);
+  ASSERT_OK(captured);
+  ASSERT(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) == hipSuccess);
+  for (int rep = 0; rep < 4; ++rep) {
+    restore();
+    for (int layer = 0; layer < L; ++layer)
+      if (ehip_copy_to_device(gpu.ctx, dout[layer].get(), std::vector<float>(static_cast<size_t>(T * H * d), -1.0f).data(),
+                              T * H * d * 4) != EHIP_OK)
+        std::abort();
+    ASSERT(hipGraphLaunch(exec, s) == hipSuccess);
+    ASSERT(hipStreamSynchronize(s) == hipSuccess);
+    ASSERT_OK(FromRc(gpu.ctx, ehip_sync(gpu.ctx)));
+    for (int layer = 0; layer < L; ++layer) {
+      const std::vector<float> o = ToHost<float>(gpu.ctx, dout[layer].get(), T * H * d);
+      EXPECT(std::memcmp(o.data(), out_e[layer].data(), o.size() * 4) == 0);
+      EXPECT(ToHost<uint16_t>(gpu.ctx, pool.k_slab(layer), slab_n) == k_e[layer]);
+      EXPECT(ToHost<uint16_t>(gpu.ctx, pool.v_slab(layer), slab_n) == v_e[layer]);
+    }
+  }
+  ASSERT(hipGraphExecDestroy(exec) == hipSuccess);
+  ASSERT(hipGraphDestroy(graph) == hipSuccess);
+  ASSERT_OK(FromRc(gpu.ctx, ehip_set_stream(gpu.ctx, nullptr)));
+  ASSERT(hipStreamDestroy(s) == hipSuccess);
+  unsetenv("EHIP_DECODE_SLOTS");
 }
 
 }  // namespace

@@ -1,0 +1,123 @@
+"""Captured-graph replay of the per-layer step launches.
+
+A caller hands its stream to the context (ehip_set_stream) and captures the
+per-layer append + attention launches of an uploaded step into a HIP graph
+(stream capture through the HIP runtime the library uses). Each replay, with the slabs restored and the outputs
+poisoned by eager copies in between, must reproduce the eager run bit for bit
+(slabs and outputs): the launches record kernels only, and the persistent
+decode kernel leaves its queue counters as it found them.
+"""
+import numpy as np
+import pytest
+
+from gpu_util import new_rows, seeded_pool
+
+pytestmark = pytest.mark.gpu
+
+
+def run_case(gctx, ehip_mod, orc, w, layers, int8=False):
+    from ehip import hipgraph
+    E = ehip_mod
+    H, Hkv, d, bs = w.heads, w.kv_heads, w.head_dim, w.block_size
+    g = E.geometry(H, Hkv, d, bs, w.kv_dtype, w.pool_blocks, w.scale)
+    st = E.StepArrays(w.query_lens, w.context_lens, w.tables, w.slot_mapping)
+    bufs = []
+    for layer in range(layers):
+        kp, vp = seeded_pool(orc, w, 100 + layer, poison=False)
+        if int8:
+            k8 = np.clip(np.rint(kp * 40), -127, 127).astype(np.int8)
+            v8 = np.clip(np.rint(vp * 40), -127, 127).astype(np.int8)
+            sc = np.full((w.pool_blocks, Hkv), 1 / 40, np.float32)
+            slab_k, slab_v = k8, v8
+            extra = (gctx.to_device(sc), gctx.to_device(sc.copy()))
+        else:
+            slab_k = orc.to_bf16_bits(kp) if w.kv_dtype == E.KV_BF16 else kp
+            slab_v = orc.to_bf16_bits(vp) if w.kv_dtype == E.KV_BF16 else vp
+            extra = None
+        kn, vn, q = new_rows(orc, w, 300 + layer)
+        bufs.append(dict(k0=slab_k, v0=slab_v, dk=gctx.to_device(slab_k),
+                         dv=gctx.to_device(slab_v), dkn=gctx.to_device(kn),
+                         dvn=gctx.to_device(vn), dq=gctx.to_device(q),
+                         out=gctx.alloc(q.nbytes), shape=q.shape, scales=extra))
+
+    def launches():
+        for b in bufs:
+            if int8:
+                ks, vs = b["scales"]
+                assert gctx.step_kv_append_int8(b["dkn"], b["dvn"], b["dk"], b["dv"], ks, vs) == 0
+                assert gctx.step_attention_int8(b["dq"], b["dk"], b["dv"], ks, vs, b["out"]) == 0
+            else:
+                assert gctx.step_kv_append(b["dkn"], b["dvn"], b["dk"], b["dv"]) == 0
+                assert gctx.step_attention(b["dq"], b["dk"], b["dv"], b["out"]) == 0
+
+    def restore():
+        for b in bufs:
+            b["dk"].upload(b["k0"])
+            b["dv"].upload(b["v0"])
+            b["out"].upload(np.full(b["shape"], -7.0, np.float32))
+            if int8:
+                sc = np.full((w.pool_blocks, Hkv), 1 / 40, np.float32)
+                b["scales"][0].upload(sc)
+                b["scales"][1].upload(sc)
+
+    def snapshot():
+        return [(b["out"].download(np.float32, b["shape"]).copy(),
+                 b["dk"].download(b["k0"].dtype, b["k0"].shape).copy(),
+                 b["dv"].download(b["v0"].dtype, b["v0"].shape).copy()) for b in bufs]
+
+    s = hipgraph.Stream()
+    graph = hipgraph.Graph()
+    assert ehip_mod.lib().ehip_set_stream(gctx.h, s.h) == 0
+    try:
+        assert gctx.step_upload(g, st) == 0, gctx.last_error()
+        restore()
+        launches()
+        gctx.sync()
+        eager = snapshot()
+        graph.capture(s, launches)
+        for _ in range(3):
+            restore()
+            graph.replay(s)
+            gctx.sync()
+            for (o, k, v), (eo, ek, ev) in zip(snapshot(), eager):
+                assert np.array_equal(o.view(np.uint32), eo.view(np.uint32))
+                assert np.array_equal(k.view(np.uint8), ek.view(np.uint8))
+                assert np.array_equal(v.view(np.uint8), ev.view(np.uint8))
+    finally:
+        assert ehip_mod.lib().ehip_set_stream(gctx.h, None) == 0
+        graph.close()
+        s.close()
+    for b in bufs:
+        for key in ("dk", "dv", "dkn", "dvn", "dq", "out"):
+            b[key].free()
+        if b["scales"]:
+            for x in b["scales"]:
+                x.free()
+
+
+def test_graph_replay_bf16_persistent_decode(gctx, ehip_mod, orc, monkeypatch):
+    """bf16 C4 shape at 24 sequences (joint items), the persistent decode
+    kernel on 5 wavefronts so each drains the queue, three layers."""
+    monkeypatch.setenv("EHIP_DECODE_SLOTS", "5")
+    from ehip import workloads
+    run_case(gctx, ehip_mod, orc, workloads.c4(num_seqs=24, share_frac=0.3), layers=3)
+
+
+def test_graph_replay_fp32_small_step(gctx, ehip_mod, orc):
+    """The C1 shape: the workgroup-per-row kernel (no merge launch)."""
+    from ehip import workloads
+    run_case(gctx, ehip_mod, orc, workloads.c1(), layers=2)
+
+
+def test_graph_replay_fp32_split_kv(gctx, ehip_mod, orc):
+    """C2: split-KV decode plus the merge kernel per layer."""
+    from ehip import workloads
+    run_case(gctx, ehip_mod, orc, workloads.c2(layers=2), layers=2)
+
+
+def test_graph_replay_int8(gctx, ehip_mod, orc):
+    """INT8 append (requantising growing blocks) and INT8 decode."""
+    from ehip import workloads
+    w = workloads.c4(num_seqs=16, share_frac=0.0)
+    w.kv_dtype = ehip_mod.KV_INT8
+    run_case(gctx, ehip_mod, orc, w, layers=2, int8=True)

@@ -525,8 +525,8 @@ def test_prefill_key_splits(gctx, ehip_mod, orc, H, Hkv, T, P, monkeypatch):
 def test_persistent_decode_queue(gctx, ehip_mod, orc, slots, monkeypatch):
     """The MFMA decode kernel's wavefronts take their later items from the
     launch's queue counter. With the grid capped to a few wavefronts every
-    one of them runs many items, over several launches in a row (the
-    counters alternate between launches): outputs bit-identical to one
+    one of them runs many items, over several launches in a row (each launch
+    must leave the counters zero for the next): outputs bit-identical to one
     workgroup per item, and within the bars of the oracle."""
     from ehip import workloads
     w = workloads.c4(num_seqs=24, share_frac=0.3)
