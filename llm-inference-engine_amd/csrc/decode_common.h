@@ -32,6 +32,20 @@ __device__ __forceinline__ int LoadRangeTable(const DecodeParams& p, int table_o
   return lane < nblk ? (bad ? -2 : raw) : -1;
 }
 
+// Work-item and row descriptors are read-only for a launch. Read through the
+// constant address space at a wavefront-uniform index they become scalar
+// loads (s_load, counted by lgkmcnt): they land in scalar registers and do not
+// wait behind the wavefront's outstanding vector loads and stores, which a
+// vector load would (vmcnt retires in issue order).
+template <class R>
+__device__ __forceinline__ R ScalarRead(const R* base, int i) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return ((const __attribute__((address_space(4))) R*)base)[i];
+#else
+  return base[i];  // the host pass only type-checks device code
+#endif
+}
+
 __device__ __forceinline__ void ReportRejectedBlocks(const DecodeParams& p, int tab) {
   if (__any(tab == -2) && (threadIdx.x & 63) == 0) atomicOr(p.err, kErrBlockRange);
 }

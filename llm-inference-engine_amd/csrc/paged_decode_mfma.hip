@@ -101,11 +101,18 @@ void DecodeMfmaBf16(DecodeParams p) {
   // On its way out each wavefront counts itself in; the last one (which then
   // knows every ticket has been drawn) clears both counters for the next
   // launch, so a launch leaves them as it found them: zero.
+  // Descriptors come through the scalar unit: the rows' split slots and the
+  // next item are requested together before the item's results are stored,
+  // so neither waits behind outstanding vector memory operations (vmcnt
+  // retires loads and stores in issue order).
   constexpr int kDrawAhead = 64;
-  for (int item_idx = blockIdx.x; item_idx < p.n_items;) {
+  int item_idx = blockIdx.x;
+  WorkItem wi;
+  if (item_idx < p.n_items) wi = ScalarRead(p.items, item_idx);
+  while (item_idx < p.n_items) {
   uint32_t ticket = 0;
   bool drawn = false;
-  const ItemRef it = DecodeItem(p.items[item_idx]);
+  const ItemRef it = DecodeItem(wi);
   const int nrows = it.nrows;  // <= RMAX (the host launches RMAX = 2 only for joint plans)
   const int hk = it.hk;
   const int tb = it.tb, te = it.te;
@@ -341,11 +348,16 @@ void DecodeMfmaBf16(DecodeParams p) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) lrow[i] = SumGroup16(lsum[i]);
 
+  RowDesc rds[RMAX];
+#pragma unroll
+  for (int rr = 0; rr < RMAX; ++rr) rds[rr] = ScalarRead(p.rows, it.rows[rr]);
+  item_idx = static_cast<int>(gridDim.x + __builtin_amdgcn_readfirstlane(ticket));
+  if (item_idx < p.n_items) wi = ScalarRead(p.items, item_idx);
 #pragma unroll
   for (int rr = 0; rr < RMAX; ++rr) {
     if (rr >= nrows) break;
     const int row = it.rows[rr];
-    const RowDesc rd = p.rows[row];
+    const RowDesc rd = rds[rr];
     if (rd.nsplit == 1) {
       if (lane < VLPT) {
         float* op = p.out + (int64_t{row} * p.heads + int64_t{hk} * G) * D + ev;
@@ -378,7 +390,6 @@ void DecodeMfmaBf16(DecodeParams p) {
       }
     }
   }
-  item_idx = static_cast<int>(gridDim.x + __builtin_amdgcn_readfirstlane(ticket));
   }
   if (lane == 0 && atomicAdd(p.queue_done, 1u) == gridDim.x - 1) {
     atomicExch(p.queue, 0u);

@@ -237,11 +237,17 @@ void FinishPlan(const ehip_geometry& g, Plan* plan, bool allow_joint,
                                      plan->rows[kr.a].table_off, 0, 0});
   }
   plan->joint_items = static_cast<int64_t>(n_joint_ranges) * g.kv_heads;
-  // Longest key range first, so the tail of the dispatch is short items.
+  // Costliest first, so the tail of the dispatch is short items. A joint
+  // item reads its keys once but does the arithmetic of both rows; counting
+  // it as its keys times its rows starts the joint items with the first
+  // wave of the queue instead of behind every full-length single-row item
+  // (C4: 440 -> 428 us per launch on MI355X; weights 1.5 to 3 measured
+  // alike, 1 left the joint items in the tail).
+  auto cost = [](const WorkItem& x) {
+    return int64_t{x.tok_end - x.tok_begin} * (x.row1 >= 0 ? kMaxJointRows : 1);
+  };
   std::stable_sort(plan->items.begin(), plan->items.end(),
-                   [](const WorkItem& x, const WorkItem& y) {
-                     return x.tok_end - x.tok_begin > y.tok_end - y.tok_begin;
-                   });
+                   [&](const WorkItem& x, const WorkItem& y) { return cost(x) > cost(y); });
   // The block ids of each item's first two 16-token halves ride in the item,
   // so a wavefront can issue its first K/V loads without waiting for its
   // table slice (-1 when the table is device-resident and unknown here).

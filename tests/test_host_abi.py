@@ -249,7 +249,8 @@ def check_partition(items, lens, hkv):
 def test_plan_items_partition_c4(ehip_mod):
     """The work list of the C4 step (pair-shared prefixes, log-uniform
     lengths) tiles every row exactly, with split indices in key order and
-    the same splits for every kv head; items are ordered longest first."""
+    the same splits for every kv head; items are ordered costliest first
+    (keys times rows served)."""
     from ehip import workloads
     w = workloads.c4()
     g = ehip_mod.geometry(w.heads, w.kv_heads, w.head_dim, w.block_size, w.kv_dtype,
@@ -258,8 +259,9 @@ def test_plan_items_partition_c4(ehip_mod):
     rc, items = ehip_mod.plan_items(g, st)
     assert rc == 0
     check_partition(items, w.context_lens, w.kv_heads)
-    keys = items[:, 3] - items[:, 2]
-    assert (np.diff(keys) <= 0).all()
+    # costliest first: keys times the rows an item serves
+    cost = (items[:, 3] - items[:, 2]) * np.where(items[:, 1] >= 0, 2, 1)
+    assert (np.diff(cost) <= 0).all()
     rc, rows, n, partials, split, joint, shared = ehip_mod.plan_counts(g, st, joint=True)
     assert n == len(items) and joint == int((items[:, 1] >= 0).sum()) > 0
 
