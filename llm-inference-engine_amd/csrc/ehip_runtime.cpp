@@ -35,8 +35,8 @@ struct ehip_ctx {
   float* d_part = nullptr;
   size_t d_part_bytes = 0;
   int32_t* d_err = nullptr;
-  // Item-queue counters of the persistent decode kernel: two words of the
-  // error page (zeroed at creation; every launch leaves them zero).
+  // Item-queue counters of the persistent decode kernel, in the error page
+  // (zeroed at creation; every launch leaves them zero).
   ehip::QueueState queue{};
 
   // The uploaded step.
@@ -308,12 +308,19 @@ int ehip_init(int device, ehip_ctx** out) {
     e = hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking);
     ctx->stream = ctx->own_stream;
     if (e != hipSuccess) { rc = HipFail(ctx, e, "hipStreamCreate"); break; }
-    e = hipMalloc(&ctx->d_err, 256);
+    // Words 0 range flags, 32 probe sink; from word 1024 the decode item
+    // queue: kItemQueues ticket counters kQueueStride words apart, then the
+    // wavefronts-done counter.
+    constexpr size_t kQueueWord = 1024;
+    constexpr size_t kPageBytes =
+        4 * (kQueueWord + (ehip::kItemQueues + 1) * size_t{ehip::kQueueStride});
+    e = hipMalloc(&ctx->d_err, kPageBytes);
     if (e != hipSuccess) { rc = HipFail(ctx, e, "hipMalloc(err)"); break; }
-    e = hipMemset(ctx->d_err, 0, 256);
+    e = hipMemset(ctx->d_err, 0, kPageBytes);
     if (e != hipSuccess) { rc = HipFail(ctx, e, "hipMemset(err)"); break; }
-    // Page words: 0 range flags, 32 probe sink, 48-49 decode item queue.
-    ctx->queue.d_pair = reinterpret_cast<uint32_t*>(ctx->d_err) + 48;
+    uint32_t* words = reinterpret_cast<uint32_t*>(ctx->d_err);
+    ctx->queue.d_counters = words + kQueueWord;
+    ctx->queue.d_done = words + kQueueWord + size_t{ehip::kItemQueues} * ehip::kQueueStride;
   } while (false);
   if (rc != EHIP_OK) {
     ehip_destroy(ctx);

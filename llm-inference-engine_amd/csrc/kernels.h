@@ -44,16 +44,27 @@ struct DecodeParams {
   int32_t has_prefill;      // the step also has MFMA prefill items
   const float* k_scale;     // INT8 KV: per-(block, kv head) scales [slab_blocks, Hkv]
   const float* v_scale;
-  uint32_t* queue;          // item tickets (zero at launch; MFMA kernel only)
+  uint32_t* queue;          // kItemQueues ticket counters, kQueueStride words apart
+                            // (zero at launch; MFMA kernel only)
   uint32_t* queue_done;     // wavefronts finished (zero at launch)
 };
 
-// The item-queue counters of a context ({tickets, wavefronts done}); each
-// persistent decode launch leaves them zero, so launches on the context's
-// stream, eager or replayed from a captured graph, need no clearing between
-// them.
+// The persistent decode kernel's item queue is split into kItemQueues
+// sub-queues: sub-queue q serves the items whose index is q modulo the
+// sub-queue count, to the wavefronts whose index is q modulo it. One counter
+// takes every ticket of a launch through one memory channel's atomic unit,
+// which serialises them (about 12 ns apiece on MI355X); 32 counters in
+// separate 256-byte lines draw in parallel.
+constexpr int kItemQueues = 32;
+constexpr int kQueueStride = 64;  // words between counters
+
+// The item-queue counters of a context (kItemQueues ticket counters and the
+// wavefronts-done counter); each persistent decode launch leaves them zero,
+// so launches on the context's stream, eager or replayed from a captured
+// graph, need no clearing between them.
 struct QueueState {
-  uint32_t* d_pair;
+  uint32_t* d_counters;
+  uint32_t* d_done;
 };
 
 struct PrefillParams {

@@ -93,19 +93,26 @@ void DecodeMfmaBf16(DecodeParams p) {
 
   const int lane = threadIdx.x;
   // Persistent wavefronts: a workgroup's first item is its index; each later
-  // one is gridDim.x plus a ticket from the launch's queue counter. The ticket
+  // one comes by ticket from the workgroup's sub-queue. The ticket
   // is drawn when at most kDrawAhead keys of the current item remain: late
   // enough that items go to the wavefronts that free up first (longest-first
   // list scheduling: the queue hands out the short items last, so the
   // wavefronts finish together), early enough to hide the atomic's latency.
   // On its way out each wavefront counts itself in; the last one (which then
-  // knows every ticket has been drawn) clears both counters for the next
+  // knows every ticket has been drawn) clears every counter for the next
   // launch, so a launch leaves them as it found them: zero.
   // Descriptors come through the scalar unit: the rows' split slots and the
   // next item are requested together before the item's results are stored,
   // so neither waits behind outstanding vector memory operations (vmcnt
   // retires loads and stores in issue order).
   constexpr int kDrawAhead = 64;
+  // Sub-queue q of nq serves items q, q + nq, ... in list order: the ones
+  // below gridDim.x are first items (workgroup i starts with item i), the
+  // rest go out by ticket, from the first such index at or above gridDim.x.
+  const int nq = min(kItemQueues, static_cast<int>(gridDim.x));
+  const int q = static_cast<int>(blockIdx.x) % nq;
+  const int first_queued = q + nq * ((static_cast<int>(gridDim.x) - q + nq - 1) / nq);
+  uint32_t* const my_queue = p.queue + q * kQueueStride;
   int item_idx = blockIdx.x;
   WorkItem wi;
   if (item_idx < p.n_items) wi = ScalarRead(p.items, item_idx);
@@ -220,7 +227,7 @@ void DecodeMfmaBf16(DecodeParams p) {
   auto process = [&](const T& t, int t0) {
     if (!drawn && t0 + kDrawAhead >= te) {  // wavefront-uniform
       drawn = true;
-      if (lane == 0) ticket = atomicAdd(p.queue, 1u);
+      if (lane == 0) ticket = atomicAdd(my_queue, 1u);
     }
     f32x4_t acc[TH];
 #pragma unroll
@@ -351,7 +358,7 @@ void DecodeMfmaBf16(DecodeParams p) {
   RowDesc rds[RMAX];
 #pragma unroll
   for (int rr = 0; rr < RMAX; ++rr) rds[rr] = ScalarRead(p.rows, it.rows[rr]);
-  item_idx = static_cast<int>(gridDim.x + __builtin_amdgcn_readfirstlane(ticket));
+  item_idx = first_queued + nq * static_cast<int>(__builtin_amdgcn_readfirstlane(ticket));
   if (item_idx < p.n_items) wi = ScalarRead(p.items, item_idx);
 #pragma unroll
   for (int rr = 0; rr < RMAX; ++rr) {
@@ -392,7 +399,7 @@ void DecodeMfmaBf16(DecodeParams p) {
   }
   }
   if (lane == 0 && atomicAdd(p.queue_done, 1u) == gridDim.x - 1) {
-    atomicExch(p.queue, 0u);
+    for (int k = 0; k < nq; ++k) atomicExch(p.queue + k * kQueueStride, 0u);
     atomicExch(p.queue_done, 0u);
   }
 }
@@ -447,8 +454,8 @@ void LaunchShape(const DecodeParams& p, hipStream_t stream, bool wide, bool deep
 bool LaunchDecodeMfma(const DecodeParams& params, QueueState* queue, hipStream_t stream,
                       hipError_t* err) {
   DecodeParams p = params;
-  p.queue = queue->d_pair;
-  p.queue_done = queue->d_pair + 1;
+  p.queue = queue->d_counters;
+  p.queue_done = queue->d_done;
   const bool aligned = (reinterpret_cast<uintptr_t>(p.k_slab) % 16 == 0) &&
                        (reinterpret_cast<uintptr_t>(p.v_slab) % 16 == 0) &&
                        (reinterpret_cast<uintptr_t>(p.q) % 16 == 0) &&

@@ -521,13 +521,15 @@ def test_prefill_key_splits(gctx, ehip_mod, orc, H, Hkv, T, P, monkeypatch):
     assert rel_norm(outs[0][rows], outs[1][rows]) <= PREFILL_REL
 
 
-@pytest.mark.parametrize("slots", ["1", "7", "300"])
+@pytest.mark.parametrize("slots", ["1", "7", "40", "64", "300"])
 def test_persistent_decode_queue(gctx, ehip_mod, orc, slots, monkeypatch):
     """The MFMA decode kernel's wavefronts take their later items from the
-    launch's queue counter. With the grid capped to a few wavefronts every
-    one of them runs many items, over several launches in a row (each launch
-    must leave the counters zero for the next): outputs bit-identical to one
-    workgroup per item, and within the bars of the oracle."""
+    launch's sub-queue counters (up to 32, one per wavefront index modulo
+    their count). With the grid capped to a few wavefronts every one of them
+    runs many items, over several launches in a row (each launch must leave
+    the counters zero for the next); 40 leaves the sub-queues with unequal
+    numbers of wavefronts. Outputs bit-identical to one workgroup per item,
+    and within the bars of the oracle."""
     from ehip import workloads
     w = workloads.c4(num_seqs=24, share_frac=0.3)
     monkeypatch.setenv("EHIP_DECODE_PERSIST", "0")
