@@ -9,10 +9,12 @@ namespace ehip {
 namespace {
 
 constexpr int32_t kTile = 64;             // split lengths are whole 64-key units
-// ~2 work items per resident decode wavefront (2048 on MI355X): fewer, longer
-// items measured faster than ~7.5 per SIMD (each item pays its descriptor,
-// query and first-tile round trips).
-constexpr int64_t kTargetItems = 4096;
+// About one work item per resident decode wavefront (2048 on MI355X) before
+// the per-item length cap: each item pays its descriptor, query and
+// first-tile round trips plus a partial slot, and the queue balances the
+// rest (with 32 item sub-queues, 2048 measured faster than 4096 on C3,
+// 150 -> 141 us, and C5, 268 -> 262 us; C4's items are all at the cap).
+constexpr int64_t kTargetItems = 2048;
 constexpr int32_t kMinSplit = 128;
 constexpr int32_t kMaxSplitsPerRow = 64;  // bounds the merge a single wave performs
 
