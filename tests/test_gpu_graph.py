@@ -121,3 +121,20 @@ def test_graph_replay_int8(gctx, ehip_mod, orc):
     w = workloads.c4(num_seqs=16, share_frac=0.0)
     w.kv_dtype = ehip_mod.KV_INT8
     run_case(gctx, ehip_mod, orc, w, layers=2, int8=True)
+
+
+def test_graph_replay_mixed_prefill_and_decode(gctx, ehip_mod, orc):
+    """A step with causal prefill chunks (one from position 0, one after a
+    cached prefix) and decode rows: the prefill kernel, the persistent decode
+    kernel and the split merge (which also reduces the chunks' key splits)
+    are all captured and replayed."""
+    from ehip import workloads
+    rng = np.random.default_rng(11)
+    qlens = np.array([64, 96] + [1] * 8, np.int32)
+    ctx_lens = np.concatenate([[64, 296], rng.integers(100, 700, 8) + 1]).astype(np.int64)
+    need = (ctx_lens + 15) // 16
+    pool = int(np.ceil(1.25 * need.sum()))
+    tables, _ = workloads._tables_from_pool(need, pool, rng)
+    w = workloads._finish("mixed", 32, 8, 128, 16, ehip_mod.KV_BF16, 2, qlens, ctx_lens, tables,
+                          pool, 0.5)
+    run_case(gctx, ehip_mod, orc, w, layers=2)
