@@ -18,9 +18,11 @@
 //    (a1 + a2 / 128 + a3 / 16384) * s_q * k_scale * softmax scale * log2 e.
 //  * PV runs on the VALU in fp32: lane owns elements 4 * (lane % (D/4)) .. +4
 //    of a token row (one 4-byte load). The bytes are read as unsigned after
-//    flipping their sign bits (u = q + 128, one v_cvt_f32_ubyte each), scaled
-//    by the half's V scale, and the 128 * sum(p * v_scale) offset is taken out
-//    once per item; token groups are summed across lanes at the end.
+//    flipping their sign bits (u = q + 128, one v_cvt_f32_ubyte each) and
+//    multiplied by p * v_scale (the half's V scale is folded into the
+//    probability when it is written for the PV layout); the
+//    128 * sum(p * v_scale) offset is taken out once per item; token groups
+//    are summed across lanes at the end.
 //
 // Rows past a key range read as zeros through bounded buffer descriptors and
 // are masked; split results go through the same partial/merge path as the
@@ -262,9 +264,12 @@ void DecodeMfmaQ8(DecodeParams p) {
       float ps = 0.f, pc = 0.f;
 #pragma unroll
       for (int h2 = 0; h2 < TH; ++h2) {
-        s[h2][i] = mn == -INFINITY ? 0.f : Exp2(s[h2][i] - mn);
-        ps += s[h2][i];
-        pc = fmaf(s[h2][i], t.vs[h2], pc);
+        const float pr = mn == -INFINITY ? 0.f : Exp2(s[h2][i] - mn);
+        ps += pr;
+        // The half's V scale rides on the probability (one multiply per
+        // score here instead of one per V element in the PV loop).
+        s[h2][i] = pr * t.vs[h2];
+        pc += s[h2][i];
       }
       lsum[i] = lsum[i] * alpha[i] + ps;
       cofs[i] = cofs[i] * alpha[i] + pc;
@@ -287,13 +292,12 @@ void DecodeMfmaQ8(DecodeParams p) {
 #pragma unroll
     for (int h2 = 0; h2 < TH; ++h2) {
       if (t.phys[h2] < 0) continue;
-      const float vsc = t.vs[h2];
 #pragma unroll
       for (int j = 0; j < VJ; ++j) {
         const int tt = 16 * h2 + j * VT + tv;
         const uint32_t r = t.v[h2][j] ^ 0x80808080u;  // u = q + 128
-        const float v0 = UByteF(r, 0) * vsc, v1 = UByteF(r, 1) * vsc;
-        const float v2 = UByteF(r, 2) * vsc, v3 = UByteF(r, 3) * vsc;
+        const float v0 = UByteF(r, 0), v1 = UByteF(r, 1);
+        const float v2 = UByteF(r, 2), v3 = UByteF(r, 3);
         float pv[HP];
 #pragma unroll
         for (int r4 = 0; r4 < HR; ++r4) {
