@@ -27,8 +27,15 @@
  *     blk*block_stride elements, kv head `hk` at +hk*bs*d, slot p at +p*d.
  *     KV element type is fp32 or bf16 (bf16 = the reference's
  *     Fp32ToBf16Bits round-to-nearest-even, src/tensor/half.h:112-124).
- *   - Queries and outputs are fp32, [rows, H, d] contiguous; arithmetic is
- *     fp32 throughout (bf16 K/V are widened exactly).
+ *   - Queries and outputs are fp32, [rows, H, d] contiguous. Softmax,
+ *     running sums and accumulation are fp32 everywhere. The products differ
+ *     by kernel: fp32 KV is all-fp32 on the vector ALUs; bf16-KV decode
+ *     multiplies bf16 K by q split into bf16 hi + lo parts (q = hi + lo to
+ *     about 2^-17 relative) on the matrix cores, and P.V in fp32; the causal
+ *     prefill-chunk kernel rounds q and the probabilities P to bf16 for its
+ *     matrix-core products (fp32 accumulate); INT8 KV forms exact integer
+ *     q.k products of a three-digit int8 split of q. The parity bars these
+ *     give are stated beside each test.
  *   - A context is used from one host thread at a time (the reference's
  *     single engine thread, src/runtime/engine.h:27-33).
  */
@@ -99,7 +106,9 @@ int ehip_last_error(const ehip_ctx* ctx, char* buf, size_t n);
 /* Device count, without creating a context (0 when no GPU is visible). */
 int ehip_device_count(int* out);
 /* Waits for all enqueued work; returns InvalidArgument if a kernel skipped an
- * out-of-range slot or block id since the previous ehip_sync. */
+ * out-of-range slot or block id since the previous ehip_sync, and Internal
+ * (after clearing them) if the persistent decode kernel's item-queue counters
+ * were left non-zero, which only overlapping launches on one context cause. */
 int ehip_sync(ehip_ctx* ctx);
 /* Enqueue the context's work on a caller's HIP stream (a hipStream_t passed
  * as void*), or back on the context's own stream when NULL. The per-layer
@@ -108,8 +117,13 @@ int ehip_sync(ehip_ctx* ctx);
  * stream: they enqueue kernels only (no allocation, copy, memset or
  * synchronisation), and the persistent decode kernel leaves its queue
  * counters zero, so a captured layer sequence replays without host work.
- * ehip_step_upload copies the step descriptor and is not captured. No
- * counterpart in the reference (its kernels run on the calling thread). */
+ * ehip_step_upload copies the step descriptor and is not captured.
+ * Switching streams first waits (on the host) for the work already queued on
+ * the current stream: a context has one descriptor arena, one split
+ * workspace and one set of queue counters, so its launches must never run on
+ * two streams at once. FailedPrecondition if the current stream is being
+ * captured (end the capture first). No counterpart in the reference (its
+ * kernels run on the calling thread). */
 int ehip_set_stream(ehip_ctx* ctx, void* stream);
 
 /* ------------------------------------------------------------ memory ----- */
@@ -126,6 +140,22 @@ int ehip_copy_device(ehip_ctx* ctx, void* d_dst, const void* d_src, int64_t byte
  * dtype: EHIP_KV_F32 writes float, EHIP_KV_BF16 writes RNE bf16 bits. */
 int ehip_fill_normal(ehip_ctx* ctx, void* d_dst, int64_t n, int32_t dtype, float mean,
                      float stddev, uint64_t seed);
+
+/* ---------------------------------------------------- seeded host fills --
+ * The reference's deterministic fills (src/tensor/ops.h:88-109): engine
+ * std::mt19937_64(seed), whose output sequence the C++ standard fixes.
+ * Host memory only; no context needed. */
+/* Outputs skip .. skip+n-1 of std::mt19937_64(seed) (raw 64-bit values; the
+ * reference's uniforms are (x >> 11) * 2^-53, src/tensor/ops.cpp:205-224). */
+int ehip_rng_u64(uint64_t seed, uint64_t skip, uint64_t* h_out, int64_t n);
+/* tensor::fill_normal (src/tensor/ops.cpp:451-477) on n fp32 elements:
+ * Box-Muller on consecutive engine outputs, u1 = ((x >> 11) + 1) * 2^-53,
+ * u2 = (x >> 11) * 2^-53, z0 = r cos(2 pi u2), z1 = r sin(2 pi u2),
+ * element = (float)(mean + stddev * z); an odd n drops the last z1. Filled on
+ * several threads; the values do not depend on their number. */
+int ehip_host_fill_normal(float* h_dst, int64_t n, double mean, double stddev, uint64_t seed);
+/* Fp32ToBf16Bits (src/tensor/half.h:112-124) over n host elements. */
+int ehip_host_fp32_to_bf16(const float* h_src, uint16_t* h_dst, int64_t n);
 
 /* ------------------------------------------------------------ timing ----- */
 /* HIP events on the context's stream (the stream every kernel runs on). */
@@ -187,22 +217,6 @@ int ehip_paged_decode_attention_batched_bf16(
     const int32_t* const* h_block_tables, const int64_t* h_lengths, int64_t num_seqs,
     int64_t heads, int64_t kv_heads, int64_t d, int64_t block_size, int64_t block_stride,
     int64_t slab_blocks, float scale, float* d_out);
-
-/* ------------------------------------------- measurement probes -------
- * Read-bandwidth probes that price the attention kernels' roofline on the
- * running device (not part of the attention path): a streaming pass over
- * d_buf (16 <= bytes < 4 GiB), and the decode access pattern alone, in which
- * each of (n_blocks / tiles_per_item) * kv_heads wavefronts reads
- * tiles_per_item (block, head) tiles of tile_bytes from both slabs, at the
- * block ids h_blocks (each < slab_blocks; a block is block_bytes long).
- * nt selects the non-temporal load policy the decode kernels use. Each runs
- * reps times; *gbps gets the best rate in GB/s (bytes read / time). */
-int ehip_probe_stream_read(ehip_ctx* ctx, const void* d_buf, int64_t bytes, int32_t nt,
-                           int32_t reps, float* gbps);
-int ehip_probe_tile_gather(ehip_ctx* ctx, const void* d_k_slab, const void* d_v_slab,
-                           int64_t slab_blocks, const int32_t* h_blocks, int64_t n_blocks,
-                           int32_t tiles_per_item, int32_t kv_heads, int64_t block_bytes,
-                           int32_t tile_bytes, int32_t nt, int32_t reps, float* gbps);
 
 /* ------------------------------------------------ step path (hot path) ----
  * One descriptor upload per scheduler step, then per layer one append and one
@@ -270,6 +284,13 @@ int ehip_plan_counts(const ehip_geometry* geom, const ehip_step_desc* step, int6
  * kv_head, split}. Writes at most cap items; *n gets the item count. */
 int ehip_plan_items(const ehip_geometry* geom, const ehip_step_desc* step, int32_t* out,
                     int64_t cap, int64_t* n);
+/* The causal prefill-chunk items of the plan ehip_step_upload would build
+ * (chunks of >= 16 rows on the matrix-core kernel), in dispatch order: nine
+ * int32 per item {row_base, chunk_rows, past, q0, kv_head, split, key_begin,
+ * key_end, nsplit of the item's rows (0: unsplit)}. Writes at most cap items;
+ * *n gets the item count. */
+int ehip_plan_prefill_items(const ehip_geometry* geom, const ehip_step_desc* step, int32_t* out,
+                            int64_t cap, int64_t* n);
 
 #ifdef __cplusplus
 }

@@ -72,30 +72,6 @@ int HipFail(ehip_ctx* ctx, hipError_t e, const char* what) {
   return SetError(ctx, code, "%s: %s", what, hipGetErrorString(e));
 }
 
-// Best-of-reps rate of `launch` over `bytes` bytes, timed with events on the
-// context stream.
-template <class F>
-int TimeProbe(ehip_ctx* ctx, double bytes, int32_t reps, F launch, float* gbps) {
-  hipEvent_t a = nullptr, b = nullptr;
-  hipError_t e = hipEventCreate(&a);
-  if (e == hipSuccess) e = hipEventCreate(&b);
-  float best = 0.f;
-  for (int r = 0; e == hipSuccess && r < reps; ++r) {
-    e = hipEventRecord(a, ctx->stream);
-    if (e == hipSuccess) e = launch();
-    if (e == hipSuccess) e = hipEventRecord(b, ctx->stream);
-    if (e == hipSuccess) e = hipEventSynchronize(b);
-    float ms = 0.f;
-    if (e == hipSuccess) e = hipEventElapsedTime(&ms, a, b);
-    if (e == hipSuccess && ms > 0.f) best = std::max(best, static_cast<float>(bytes / ms / 1e6));
-  }
-  if (a) (void)hipEventDestroy(a);
-  if (b) (void)hipEventDestroy(b);
-  if (e != hipSuccess) return HipFail(ctx, e, "probe");
-  *gbps = best;
-  return EHIP_OK;
-}
-
 #define EHIP_HIP(ctx, expr)                                  \
   do {                                                       \
     hipError_t e_ = (expr);                                  \
@@ -308,7 +284,7 @@ int ehip_init(int device, ehip_ctx** out) {
     e = hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking);
     ctx->stream = ctx->own_stream;
     if (e != hipSuccess) { rc = HipFail(ctx, e, "hipStreamCreate"); break; }
-    // Words 0 range flags, 32 probe sink; from word 1024 the decode item
+    // Word 0 holds the range flags; from word 1024 the decode item
     // queue: kItemQueues ticket counters kQueueStride words apart, then the
     // wavefronts-done counter.
     constexpr size_t kQueueWord = 1024;
@@ -357,6 +333,21 @@ int ehip_sync(ehip_ctx* ctx) {
   EHIP_HIP(ctx, hipStreamSynchronize(ctx->stream));
   int32_t flags = 0;
   EHIP_HIP(ctx, hipMemcpy(&flags, ctx->d_err, sizeof(flags), hipMemcpyDeviceToHost));
+  // Every persistent decode launch leaves its queue counters zero. Non-zero
+  // counters after the stream drained mean two launches on this context
+  // overlapped (or one was cut short): later launches would skip items, so
+  // the counters are cleared and the step reported as failed.
+  const size_t queue_bytes = sizeof(uint32_t) * (size_t{ehip::kItemQueues} + 1) * ehip::kQueueStride;
+  std::vector<uint32_t> queue(queue_bytes / sizeof(uint32_t));
+  EHIP_HIP(ctx, hipMemcpy(queue.data(), ctx->queue.d_counters, queue_bytes, hipMemcpyDeviceToHost));
+  bool dirty = false;
+  for (int k = 0; k <= ehip::kItemQueues; ++k) dirty = dirty || queue[size_t{k} * ehip::kQueueStride];
+  if (dirty) {
+    EHIP_HIP(ctx, hipMemset(ctx->queue.d_counters, 0, queue_bytes));
+    return SetError(ctx, EHIP_INTERNAL,
+                    "decode item-queue counters were left non-zero (overlapping launches on one "
+                    "context?); cleared, and the outputs since the last sync are suspect");
+  }
   if (flags != 0) {
     EHIP_HIP(ctx, hipMemset(ctx->d_err, 0, sizeof(flags)));
     return SetError(ctx, EHIP_INVALID_ARGUMENT,
@@ -369,7 +360,18 @@ int ehip_sync(ehip_ctx* ctx) {
 
 int ehip_set_stream(ehip_ctx* ctx, void* stream) {
   if (int rc = CheckCtx(ctx)) return rc;
-  ctx->stream = stream ? static_cast<hipStream_t>(stream) : ctx->own_stream;
+  hipStream_t next = stream ? static_cast<hipStream_t>(stream) : ctx->own_stream;
+  if (next == ctx->stream) return EHIP_OK;
+  // The context owns one descriptor arena, one split workspace and one set of
+  // queue counters: work still queued on the old stream must finish before
+  // anything runs on the new one, or two launches would share them.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  EHIP_HIP(ctx, hipStreamIsCapturing(ctx->stream, &cap));
+  if (cap != hipStreamCaptureStatusNone)
+    return SetError(ctx, EHIP_FAILED_PRECONDITION,
+                    "the context's stream is being captured: end the capture before switching");
+  EHIP_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  ctx->stream = next;
   return EHIP_OK;
 }
 
@@ -436,54 +438,6 @@ int ehip_fill_normal(ehip_ctx* ctx, void* d_dst, int64_t n, int32_t dtype, float
   return EHIP_OK;
 }
 
-
-int ehip_probe_stream_read(ehip_ctx* ctx, const void* d_buf, int64_t bytes, int32_t nt,
-                           int32_t reps, float* gbps) {
-  if (int rc = CheckCtx(ctx)) return rc;
-  if (!d_buf || !gbps || reps < 1 || bytes < 16 || bytes >= (int64_t{1} << 32))
-    return SetError(ctx, EHIP_INVALID_ARGUMENT, "probe needs 16 <= bytes < 4 GiB and reps >= 1");
-  uint32_t* sink = reinterpret_cast<uint32_t*>(ctx->d_err) + 32;  // a spare word of the err page
-  const int64_t used = bytes / 16 * 16;
-  return TimeProbe(ctx, static_cast<double>(used), reps, [&] {
-    return ehip::LaunchStreamRead(d_buf, used, nt != 0, sink, ctx->stream);
-  }, gbps);
-}
-
-int ehip_probe_tile_gather(ehip_ctx* ctx, const void* d_k_slab, const void* d_v_slab,
-                           int64_t slab_blocks, const int32_t* h_blocks, int64_t n_blocks,
-                           int32_t tiles_per_item, int32_t kv_heads, int64_t block_bytes,
-                           int32_t tile_bytes, int32_t nt, int32_t reps, float* gbps) {
-  if (int rc = CheckCtx(ctx)) return rc;
-  if (!d_k_slab || !d_v_slab || !h_blocks || !gbps || reps < 1 || tiles_per_item < 1 ||
-      kv_heads < 1 || tile_bytes < 16 || tile_bytes % 16 != 0 ||
-      int64_t{tile_bytes} * kv_heads > block_bytes || n_blocks < tiles_per_item ||
-      n_blocks / tiles_per_item * kv_heads > INT32_MAX)
-    return SetError(ctx, EHIP_INVALID_ARGUMENT, "bad tile-gather probe arguments");
-  for (int64_t i = 0; i < n_blocks; ++i)
-    if (h_blocks[i] < 0 || h_blocks[i] >= slab_blocks)
-      return SetError(ctx, EHIP_INVALID_ARGUMENT, "probe block id %d out of range",
-                      static_cast<int>(h_blocks[i]));
-  const int32_t items = static_cast<int32_t>(n_blocks / tiles_per_item * kv_heads);
-  void* d_blocks = nullptr;
-  EHIP_HIP(ctx, hipMalloc(&d_blocks, static_cast<size_t>(n_blocks) * 4));
-  hipError_t e = hipMemcpyAsync(d_blocks, h_blocks, static_cast<size_t>(n_blocks) * 4,
-                                hipMemcpyHostToDevice, ctx->stream);
-  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
-  if (e != hipSuccess) {
-    (void)hipFree(d_blocks);
-    return HipFail(ctx, e, "probe upload");
-  }
-  uint32_t* sink = reinterpret_cast<uint32_t*>(ctx->d_err) + 32;
-  const double bytes = 2.0 * items * tiles_per_item * tile_bytes;
-  const int rc = TimeProbe(ctx, bytes, reps, [&] {
-    return ehip::LaunchTileGather(d_k_slab, d_v_slab, static_cast<const int32_t*>(d_blocks), items,
-                                  tiles_per_item, kv_heads, block_bytes, tile_bytes, nt != 0, sink,
-                                  ctx->stream);
-  }, gbps);
-  (void)hipStreamSynchronize(ctx->stream);
-  (void)hipFree(d_blocks);
-  return rc;
-}
 
 int ehip_event_create(ehip_ctx* ctx, void** ev_out) {
   if (int rc = CheckCtx(ctx)) return rc;
@@ -665,20 +619,27 @@ int ehip_paged_decode_attention_batched_bf16(
 
 // ------------------------------------------------------------ step path --
 
+namespace {
+// Query rows per MFMA prefill item for the geometry (0: chunks stay on the
+// decode kernels).
+int StepPrefillRows(const ehip_geometry& g) {
+  const int64_t stride = ehip::BlockStride(g);
+  const int64_t slab_bytes = g.slab_blocks > 0 && stride > 0 &&
+                                     g.slab_blocks <= INT64_MAX / stride / 2
+                                 ? g.slab_blocks * stride * 2
+                                 : INT64_MAX;
+  return ehip::PrefillRowsPerItem(g.kv_dtype, g.head_dim,
+                                  g.kv_heads > 0 ? g.heads / g.kv_heads : 0, g.block_size,
+                                  slab_bytes);
+}
+}  // namespace
+
 int ehip_step_upload(ehip_ctx* ctx, const ehip_geometry* geom, const ehip_step_desc* step) {
   if (int rc = CheckCtx(ctx)) return rc;
   if (!geom || !step) return SetError(ctx, EHIP_INVALID_ARGUMENT, "null geometry or step");
   Plan plan;
   std::string err;
-  const int64_t stride = ehip::BlockStride(*geom);
-  const int64_t slab_bytes =
-      geom->slab_blocks > 0 && stride > 0 && geom->slab_blocks <= INT64_MAX / stride / 2
-          ? geom->slab_blocks * stride * 2
-          : INT64_MAX;
-  const int prefill_rows = ehip::PrefillRowsPerItem(
-      geom->kv_dtype, geom->head_dim, geom->kv_heads > 0 ? geom->heads / geom->kv_heads : 0,
-      geom->block_size, slab_bytes);
-  if (int rc = ehip::BuildPlan(*geom, *step, &plan, &err, prefill_rows))
+  if (int rc = ehip::BuildPlan(*geom, *step, &plan, &err, StepPrefillRows(*geom)))
     return SetError(ctx, rc, "%s", err.c_str());
   return UploadPlan(ctx, *geom, std::move(plan), nullptr);
 }
@@ -832,6 +793,30 @@ int ehip_plan_items(const ehip_geometry* geom, const ehip_step_desc* step, int32
     o[3] = w.tok_end;
     o[4] = w.hk_split & ((1 << ehip::kHkBits) - 1);
     o[5] = w.hk_split >> ehip::kHkBits;
+  }
+  return EHIP_OK;
+}
+
+int ehip_plan_prefill_items(const ehip_geometry* geom, const ehip_step_desc* step, int32_t* out,
+                            int64_t cap, int64_t* n) {
+  if (!geom || !step || !n || cap < 0 || (cap > 0 && !out)) return EHIP_INVALID_ARGUMENT;
+  Plan plan;
+  std::string err;
+  if (int rc = ehip::BuildPlan(*geom, *step, &plan, &err, StepPrefillRows(*geom))) return rc;
+  *n = static_cast<int64_t>(plan.prefill.size());
+  const int64_t m = std::min<int64_t>(cap, *n);
+  for (int64_t i = 0; i < m; ++i) {
+    const ehip::PrefillItem& w = plan.prefill[static_cast<size_t>(i)];
+    int32_t* o = out + 9 * i;
+    o[0] = w.row_base;
+    o[1] = w.chunk;
+    o[2] = w.past;
+    o[3] = w.q0;
+    o[4] = w.hk_split & ((1 << ehip::kHkBits) - 1);
+    o[5] = w.hk_split >> ehip::kHkBits;
+    o[6] = w.key_begin;
+    o[7] = w.key_end;
+    o[8] = plan.rows[static_cast<size_t>(w.row_base + w.q0)].nsplit;
   }
   return EHIP_OK;
 }

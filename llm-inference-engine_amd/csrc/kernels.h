@@ -137,14 +137,6 @@ hipError_t LaunchRopeKvAppend(float* q, const float* src_k, const float* src_v,
                               int d, int bs, int64_t slab_blocks, void* k_slab, void* v_slab,
                               int kv_dtype, int32_t* err, hipStream_t stream);
 
-// Measurement probes (probe.hip): a streaming read of a buffer below 4 GiB,
-// and the decode access pattern without arithmetic.
-hipError_t LaunchStreamRead(const void* p, int64_t bytes, bool nt, uint32_t* sink,
-                            hipStream_t stream);
-hipError_t LaunchTileGather(const void* k, const void* v, const int32_t* blocks, int32_t n_items,
-                            int32_t tiles, int32_t kv_heads, int64_t block_bytes,
-                            int32_t tile_bytes, bool nt, uint32_t* sink, hipStream_t stream);
-
 hipError_t LaunchFillNormal(void* dst, int64_t n, int dtype, float mean, float stddev,
                             uint64_t seed, hipStream_t stream);
 

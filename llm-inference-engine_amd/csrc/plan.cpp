@@ -409,11 +409,17 @@ int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::
     const int64_t share = std::max<int64_t>(
         kMinPrefillSplitTiles,
         (total_tiles * g.kv_heads + kPrefillSlots - 1) / kPrefillSlots);
-    auto block_splits = [&](const Block& bl) {
+    // Tiles per key split of a block. The split count a row records must be
+    // the number of pieces actually cut: with the cap on splits, ceil(tiles /
+    // per) can fall below the count asked for (e.g. 626 tiles asked in 64
+    // pieces take 10 tiles each, i.e. 63 pieces), and a recorded count above
+    // it would make the merge read partial slots nothing wrote.
+    auto block_tiles_per_split = [&](const Block& bl) {
       const int64_t tiles = (bl.keys + kPrefillTile - 1) / kPrefillTile;
       if (!split_ok || static_cast<double>(tiles) <= split_mult * static_cast<double>(share))
-        return int64_t{1};
-      return std::min<int64_t>((tiles + share - 1) / share, kMaxSplitsPerRow);
+        return tiles;
+      const int64_t want = std::min<int64_t>((tiles + share - 1) / share, kMaxSplitsPerRow);
+      return (tiles + want - 1) / want;
     };
     // Most keys first; kv head fastest, so the blocks of one kv head are
     // dispatched 8 workgroups apart and land on one XCD's L2 together.
@@ -424,12 +430,12 @@ int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::
     for (size_t i = 0; i < blocks.size(); ++i) {
       const Block& bl = blocks[i];
       const int32_t T = s.h_query_lens[bl.b];
-      const int32_t ns = static_cast<int32_t>(block_splits(bl));
+      const int32_t tiles = (bl.keys + kPrefillTile - 1) / kPrefillTile;
+      const int32_t per = static_cast<int32_t>(block_tiles_per_split(bl));
+      const int32_t ns = (tiles + per - 1) / per;  // pieces cut below, one per split slot
       const int32_t r0 = row_base[bl.b] + bl.q0;
       const int32_t r1 = row_base[bl.b] + std::min(T, bl.q0 + prefill_rows);
       std::fill(skip.begin() + r0, skip.begin() + r1, ns);
-      const int32_t tiles = (bl.keys + kPrefillTile - 1) / kPrefillTile;
-      const int32_t per = (tiles + ns - 1) / ns;
       for (int32_t sp = 0, kb = 0; kb < bl.keys; ++sp, kb += per * kPrefillTile)
         pieces.push_back({static_cast<int32_t>(i), sp, kb,
                           std::min(bl.keys, kb + per * kPrefillTile)});

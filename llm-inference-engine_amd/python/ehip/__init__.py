@@ -103,9 +103,11 @@ def lib():
             "ehip_plan_counts": [C.POINTER(Geometry), C.POINTER(StepDesc), _I64P, _I64P, _I64P,
                                  C.POINTER(C.c_int32), _I64P, _I64P],
             "ehip_plan_items": [C.POINTER(Geometry), C.POINTER(StepDesc), _vp, _i64, _I64P],
-            "ehip_probe_stream_read": [_vp, _vp, _i64, _i32, _i32, C.POINTER(C.c_float)],
-            "ehip_probe_tile_gather": [_vp, _vp, _vp, _i64, _vp, _i64, _i32, _i32, _i64, _i32,
-                                       _i32, _i32, C.POINTER(C.c_float)],
+            "ehip_rng_u64": [C.c_uint64, C.c_uint64, _vp, _i64],
+            "ehip_host_fill_normal": [_vp, _i64, C.c_double, C.c_double, C.c_uint64],
+            "ehip_host_fp32_to_bf16": [_vp, _vp, _i64],
+            "ehip_plan_prefill_items": [C.POINTER(Geometry), C.POINTER(StepDesc), _vp, _i64,
+                                        _I64P],
         }
         for name, args in sig.items():
             f = getattr(L, name)
@@ -268,23 +270,6 @@ class Context:
         ms = C.c_float()
         self._check(lib().ehip_event_elapsed_ms(self.h, e0, e1, C.byref(ms)))
         return float(ms.value)
-
-    # ---------------------------------------------------------- probes
-    def probe_stream_read(self, buf: DeviceBuffer, nbytes: int, nt: bool, reps: int = 3) -> float:
-        g = C.c_float()
-        self._check(lib().ehip_probe_stream_read(self.h, buf.ptr, nbytes, int(nt), reps,
-                                                 C.byref(g)))
-        return float(g.value)
-
-    def probe_tile_gather(self, k_slab: DeviceBuffer, v_slab: DeviceBuffer, slab_blocks: int,
-                          blocks: np.ndarray, tiles_per_item: int, kv_heads: int,
-                          block_bytes: int, tile_bytes: int, nt: bool, reps: int = 3) -> float:
-        b = np.ascontiguousarray(blocks, np.int32)
-        g = C.c_float()
-        self._check(lib().ehip_probe_tile_gather(
-            self.h, k_slab.ptr, v_slab.ptr, slab_blocks, b.ctypes.data, b.size, tiles_per_item,
-            kv_heads, block_bytes, tile_bytes, int(nt), reps, C.byref(g)))
-        return float(g.value)
 
     # ------------------------------------------------- reference kernels
     def kv_scatter(self, src_k, src_v, slots, t_dim, kv_heads, d, bs, slab_blocks, k_slab,

@@ -592,25 +592,29 @@ def test_step_requires_upload_and_validates(gctx, ehip_mod):
 
 
 def test_bandwidth_probes(gctx, ehip_mod):
-    """The measurement probes run and validate their arguments (ids out of
-    range, bytes below one vector) without launching."""
+    """The benchmark's read-bandwidth probes (lib/libehip_probe.so, apart from
+    the attention library) run and validate their arguments (ids out of range,
+    bytes below one vector) without launching."""
+    from ehip import probe
     nb, hkv, tile = 64, 2, 16 * 64 * 2
     k, v = gctx.alloc(nb * hkv * tile), gctx.alloc(nb * hkv * tile)
-    g = gctx.probe_stream_read(k, nb * hkv * tile, nt=True, reps=2)
+    g = probe.stream_read(k, nb * hkv * tile, nt=True, reps=2)
     assert np.isfinite(g) and g > 0
     blocks = np.random.default_rng(0).permutation(nb).astype(np.int32)
     for nt in (False, True):
-        g = gctx.probe_tile_gather(k, v, nb, blocks, 8, hkv, hkv * tile, tile, nt=nt, reps=2)
+        g = probe.tile_gather(k, v, nb, blocks, 8, hkv, hkv * tile, tile, nt=nt, reps=2)
         assert np.isfinite(g) and g > 0
     import ctypes as C
     out = C.c_float()
     bad = blocks.copy()
     bad[3] = nb
-    rc = ehip_mod.lib().ehip_probe_tile_gather(gctx.h, k.ptr, v.ptr, nb, bad.ctypes.data, bad.size,
-                                               8, hkv, hkv * tile, tile, 1, 1, C.byref(out))
+    rc = probe.plib().ehip_probe_tile_gather(k.ptr, v.ptr, nb, bad.ctypes.data, bad.size, 8, hkv,
+                                             hkv * tile, tile, 1, 1, C.byref(out))
     assert rc == ehip_mod.INVALID_ARGUMENT
-    assert ehip_mod.lib().ehip_probe_stream_read(gctx.h, k.ptr, 8, 0, 1,
-                                                 C.byref(out)) == ehip_mod.INVALID_ARGUMENT
+    assert probe.plib().ehip_probe_stream_read(k.ptr, 8, 0, 1,
+                                               C.byref(out)) == ehip_mod.INVALID_ARGUMENT
+    k.free()
+    v.free()
 
 
 @pytest.mark.parametrize("H,Hkv,d", [(14, 2, 64), (32, 8, 128), (8, 8, 128), (28, 4, 64),

@@ -292,3 +292,51 @@ def test_plan_int8_shapes_and_append_groups(ehip_mod):
     assert rc == 0 and joint == 0
     g16 = E.geometry(32, 8, 128, 16, E.KV_BF16, 16, 0.088)
     assert E.plan_counts(g16, st2, joint=True)[5] > 0
+
+
+def prefill_items(ehip_mod, g, st):
+    n = C.c_int64()
+    L = ehip_mod.lib()
+    assert L.ehip_plan_prefill_items(C.byref(g), C.byref(st.desc), None, 0, C.byref(n)) == 0
+    out = np.zeros((max(n.value, 1), 9), np.int32)
+    assert L.ehip_plan_prefill_items(C.byref(g), C.byref(st.desc), out.ctypes.data, n.value,
+                                     C.byref(n)) == 0
+    return out[:n.value]
+
+
+@pytest.mark.parametrize("H,Hkv,T,P", [(8, 2, 16, 20000), (8, 2, 16, 40000), (32, 8, 4096, 0),
+                                       (64, 8, 37, 60000), (16, 2, 300, 9000)])
+def test_plan_prefill_split_ids_cover_recorded_splits(ehip_mod, H, Hkv, T, P):
+    """Every MFMA prefill block cut into key splits writes exactly the split
+    slots its rows record (ids 0 .. nsplit-1, once per kv head), and its
+    pieces tile the block's keys [0, P + last row + 1) without gaps. A count
+    above the pieces cut would make the merge read slots nothing wrote (the
+    split cap of 64 per row forces fewer, longer pieces on long contexts)."""
+    bs = 16
+    L = P + T
+    st = simple_step(ehip_mod, [L], qlens=np.array([T], np.int32))
+    g = geom(ehip_mod, heads=H, kv_heads=Hkv, slab_blocks=(L + bs - 1) // bs + 8)
+    items = prefill_items(ehip_mod, g, st)
+    assert len(items) > 0
+    blocks = {}
+    for row_base, chunk, past, q0, hk, split, kb, ke, nsplit in items:
+        assert (chunk, past) == (T, P)
+        blocks.setdefault((q0, hk), []).append((split, kb, ke, nsplit))
+    m = min(q0 for q0, _ in blocks if q0 > 0) if len({q0 for q0, _ in blocks}) > 1 else T
+    for (q0, hk), pieces in blocks.items():
+        keys = P + min(T, q0 + m)
+        ns = {p[3] for p in pieces}
+        assert len(ns) == 1, pieces
+        nsplit = ns.pop()
+        ids = sorted(p[0] for p in pieces)
+        if nsplit == 0:
+            assert ids == [0] and pieces[0][1:3] == (0, keys)
+        else:
+            assert ids == list(range(nsplit)), (q0, hk, nsplit, ids)
+            spans = sorted((kb, ke) for _, kb, ke, _ in pieces)
+            assert spans[0][0] == 0 and spans[-1][1] == keys
+            assert all(a[1] == b[0] for a, b in zip(spans, spans[1:]))
+    # The first case is the one that exposed the cap: 626 key tiles cut in 64
+    # requested pieces of 10 tiles make 63 pieces.
+    if (H, Hkv, T, P) == (8, 2, 16, 20000):
+        assert {p[3] for v in blocks.values() for p in v} == {63}
