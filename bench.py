@@ -4,20 +4,31 @@
 One step = one scheduler step of the configured workload (default C4: the
 Llama-3-8B-shape 256-sequence ragged bf16-KV decode, 32 layers): one step
 descriptor upload (host packing + one async copy), then per layer the
-KV-append of the step's new token rows and one attention launch over every
+KV-append of the step's new token rows and one attention call over every
 sequence. All K/V pools, queries and new rows are resident in HBM before the
-timed region (synthetic N(0, 0.5) data from a device-side generator).
+timed region.
+
+Data: the step's structure (lengths, block tables, shared prefixes) is the
+config's seeded mt19937_64 draw (ehip.workloads). Layer 0's queries, K/V
+pools and new rows are the reference's fill_normal streams of their seeds,
+generated on the host (they are what the parity check re-computes); the other
+layers' pools come from a device-side generator of the same distribution.
 
 Prints ONE JSON line (metric/value/unit as BASELINE.json names them):
-  value      = algorithmic HBM bytes of the step (unique K/V + Q + O + tables
-               + append) / step time, in GB/s;
-  roofline   = the attention kernel alone: its algorithmic bytes per launch /
-               its average launch duration (HIP events on the launch stream,
-               bracketing every layer's attention call of every SAMPLE-th
-               timed step: an event pair per launch on every step perturbs
-               the stream enough to cost ~2% of the step time);
+  value        = algorithmic HBM bytes of the step (unique K/V + Q + O +
+                 tables + append) / the median step time, in GB/s (each timed
+                 step is bracketed by its own pair of HIP events);
+  roofline     = the attention call alone (decode kernel + split merge): its
+                 algorithmic bytes per launch / its average duration (HIP
+                 events on the launch stream around every layer's attention
+                 call of every EVENT_SAMPLE-th timed step);
   cpu_baseline = the oracle's AVX2 restatement of the reference's batched
-               paged decode, timed on this host on a bounded fp32 sample.
+                 paged decode, timed on this host on the benched step's layer
+                 0 (fp32 K/V); its outputs are also the parity checker;
+  parity       = the benched step's layer 0 against that oracle: the append
+                 (bit-exact slabs), the outputs against the reference run on
+                 the bf16-rounded K/V (max_rel, allclose) and on the original
+                 fp32 K/V (max_abs).
 """
 from __future__ import annotations
 
@@ -25,6 +36,7 @@ import argparse
 import json
 import math
 import os
+import subprocess
 import sys
 import time
 from pathlib import Path
@@ -37,7 +49,9 @@ sys.path.insert(0, str(ROOT))
 import numpy as np  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 KV_NAMES = {0: "f32", 1: "bf16", 2: "int8"}
+CPU_SHARE_PER_GPU = 16  # host threads one GPU's job may use on a shared node
 
 
 def log(*a):
@@ -50,11 +64,15 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="C4", choices=["C1", "C2", "C3", "C4", "C5"])
+    ap.add_argument("--seed", type=int, default=0, help="structure seed (0: the config's own)")
     ap.add_argument("--layers", type=int, default=0, help="override the config's layer count")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true",
+                    help="skip the CPU baseline and the parity check it carries")
     ap.add_argument("--no-ceiling-probe", action="store_true",
                     help="skip the read-bandwidth probes that price the practical ceiling")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the prefill, fused RoPE and re-prefill side measurements")
     ap.add_argument("--kv", default="auto", choices=["auto", "int8"],
                     help="KV element type: the config's own (auto) or INT8 with "
                          "per-(block, kv head) scales")
@@ -68,84 +86,158 @@ def parse():
     return ap.parse_args()
 
 
+def host_cpu():
+    """(physical cores, model name) from lscpu, or (None, None)."""
+    try:
+        rows = subprocess.run(["lscpu", "-p=CORE,SOCKET"], capture_output=True, text=True,
+                              timeout=10).stdout
+        cores = len({ln for ln in rows.splitlines() if ln and not ln.startswith("#")})
+        info = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        model = next((ln.split(":", 1)[1].strip() for ln in info.splitlines()
+                      if ln.startswith("Model name")), None)
+        return cores or None, model
+    except (OSError, subprocess.SubprocessError):
+        return None, None
+
+
 def traffic_from_profiles(config: str, kv: str = ""):
     """HBM bytes per attention launch from the committed rocprofv3 PMC summary
     (FETCH_SIZE / WRITE_SIZE per dispatch, each scaled by the same counter's
-    reading on a copy kernel of known size), or None. kv: "" for the
-    config's own KV type, "int8" for the INT8 run."""
+    reading on a copy kernel of known size), or None when no summary exists
+    for this workload draw. kv: "" for the config's own KV type, "int8"."""
     suffix = f"_{kv}" if kv else ""
     p = ROOT / "profiles" / f"decode_{config.lower()}{suffix}_traffic.json"
     if not p.exists():
         return None
     t = json.loads(p.read_text())
     return (t["fetch_kib_per_dispatch"] * t["fetch_scale"]
-            + t["write_kib_per_dispatch"] * t["write_scale"]) * 1024.0
+            + t["write_kib_per_dispatch"] * t["write_scale"]) * 1024.0, t.get("sum_context")
 
 
-def cpu_baseline(w, seconds: float):
-    """Oracle AVX2 batched paged decode (bit-identical restatement of the
-    reference's PagedDecodeAttentionBatchedF32) on a bounded fp32 sample of
-    the workload: its first 32 sequences, one layer."""
+def parity_metrics(got, ref) -> dict:
+    """max_abs; max_rel = max|a-b| / max(|b|, 1e-6 max|b|); the reference's
+    allclose criterion |a-b| <= 1e-5 + 1e-4 |b| (src/tensor/ops.h:207)."""
+    a = np.asarray(got, np.float64)
+    b = np.asarray(ref, np.float64)
+    diff = np.abs(a - b)
+    floor = 1e-6 * float(np.abs(b).max())
+    den = np.maximum(np.abs(b), floor)
+    den[den == 0] = 1.0
+    fails = int(np.count_nonzero(~(diff <= 1e-5 + 1e-4 * np.abs(b))))
+    return {"max_abs": float(diff.max()), "max_rel": float((diff / den).max()),
+            "allclose_rtol1e-4_atol1e-5": fails == 0, "allclose_failures": fails,
+            "elements": int(a.size)}
+
+
+def cpu_baseline_and_parity(w, layer0, seconds: float):
+    """The CPU leg: the oracle's AVX2 restatement of the reference's
+    PagedDecodeAttentionBatchedF32 timed on this host over the benched step's
+    layer 0 (all sequences, fp32 K/V), and the same oracle as the parity
+    checker of the GPU's layer-0 results."""
     from oracle import oracle as orc
-    threads = max(1, min(16, os.cpu_count() or 1))
+    phys, model = host_cpu()
+    allowed = len(os.sched_getaffinity(0))
+    threads = max(1, min(phys or allowed, allowed, CPU_SHARE_PER_GPU))
     orc.set_threads(threads)
-    B = min(32, w.num_seqs)
-    lens = [int(x) for x in w.context_lens[:B]]
     H, Hkv, d, bs = w.heads, w.kv_heads, w.head_dim, w.block_size
-    need = [(L + bs - 1) // bs for L in lens]
-    nb = sum(need)
-    rng = np.random.default_rng(0)
-    k = (rng.standard_normal((nb, Hkv, bs, d), dtype=np.float32) * 0.5)
-    v = (rng.standard_normal((nb, Hkv, bs, d), dtype=np.float32) * 0.5)
-    perm = rng.permutation(nb).astype(np.int32)
-    tables, off = [], 0
-    for n in need:
-        tables.append(perm[off:off + n].copy())
-        off += n
-    q = (rng.standard_normal((B, H, d), dtype=np.float32) * 0.5)
+    lens = [int(x) for x in w.context_lens]
+    k32, v32 = layer0["k32"], layer0["v32"]
+    q, kn, vn = layer0["q"], layer0["kn"], layer0["vn"]
+    par = {"layer": 0}
+    bf16 = w.kv_dtype == 1
+    if bf16:
+        # The append, bit for bit: the oracle narrows the pre-append fp32
+        # pool and scatters the new rows (RNE), the GPU slabs must equal it.
+        kb, vb = orc.to_bf16_bits(k32), orc.to_bf16_bits(v32)
+        orc.kv_scatter(kn, vn, w.slot_mapping, Hkv, d, bs, kb, vb)
+        par["append_slabs_bit_exact"] = bool(np.array_equal(kb, layer0["k_dev"]) and
+                                             np.array_equal(vb, layer0["v_dev"]))
+        del kb, vb
+        kr = orc.bf16_bits_to_f32(layer0["k_dev"])
+        vr = orc.bf16_bits_to_f32(layer0["v_dev"])
+        ref_r = orc.paged_decode_batched(q, kr, vr, w.tables, lens, H, Hkv, d, bs, w.scale,
+                                         isa=orc.ISA_AVX2)
+        del kr, vr
+        par["vs_reference_on_bf16_kv"] = parity_metrics(layer0["out"], ref_r)
+    # The fp32 reference cache after the step's append, timed as the baseline.
+    orc.kv_scatter(kn, vn, w.slot_mapping, Hkv, d, bs, k32, v32)
+    if not bf16:
+        par["append_slabs_bit_exact"] = bool(
+            np.array_equal(k32.view(np.uint32), layer0["k_dev"].view(np.uint32)) and
+            np.array_equal(v32.view(np.uint32), layer0["v_dev"].view(np.uint32)))
     times = []
     t_end = time.perf_counter() + seconds
+    ref32 = None
     while len(times) < 3 or time.perf_counter() < t_end:
         t0 = time.perf_counter()
-        orc.paged_decode_batched(q, k, v, tables, lens, H, Hkv, d, bs, w.scale, isa=orc.ISA_AVX2)
+        ref32 = orc.paged_decode_batched(q, k32, v32, w.tables, lens, H, Hkv, d, bs, w.scale,
+                                         isa=orc.ISA_AVX2)
         times.append(time.perf_counter() - t0)
-        if len(times) >= 200:
+        if len(times) >= 500:
             break
     t = float(np.median(times))
     kv_bytes = Hkv * d * 4 * 2 * sum(lens)
-    bytes_ = kv_bytes + 4 * B * H * d * 2 + 4 * nb + 8 * B
-    return {"value": round(bytes_ / t / 1e9, 3), "unit": "GB/s", "cores": threads,
+    nblk = sum((L + bs - 1) // bs for L in lens)
+    bytes_ = kv_bytes + 4 * w.rows * H * d * 2 + 4 * nblk + 8 * w.num_seqs
+    base = {"value": round(bytes_ / t / 1e9, 3), "unit": "GB/s", "cores": threads,
             "kind": "port",
-            "sample": (f"oracle AVX2 PagedDecodeAttentionBatchedF32 restatement, fp32 K/V, "
-                       f"first {B} sequences of {w.name} (sum L={sum(lens)}), 1 layer, median of "
-                       f"{len(times)} calls"),
-            "attended_kv_tok_per_s": round(sum(lens) / t, 1),
-            "ms_per_call": round(t * 1e3, 3)}
+            "sample": (f"oracle AVX2 PagedDecodeAttentionBatchedF32 restatement on {threads} "
+                       f"threads, fp32 K/V, layer 0 of the benched {w.name} step (all "
+                       f"{w.num_seqs} sequences, sum L={sum(lens)}), median of {len(times)} "
+                       f"calls"),
+            "host_physical_cores": phys, "host_cpus_allowed": allowed, "cpu_model": model,
+            "attended_kv_tok_per_s": round(sum(lens) / t, 1), "ms_per_call": round(t * 1e3, 3)}
+    if bf16:
+        par["vs_reference_on_fp32_kv"] = parity_metrics(layer0["out"], ref32)
+        par["bars"] = {"append": "bit-exact", "vs_reference_on_bf16_kv": "max_rel <= 1e-4",
+                       "vs_reference_on_fp32_kv": "max_abs <= 2e-2"}
+        par["pass"] = bool(par["append_slabs_bit_exact"] and
+                           par["vs_reference_on_bf16_kv"]["max_rel"] <= 1e-4 and
+                           par["vs_reference_on_fp32_kv"]["max_abs"] <= 2e-2)
+    else:
+        par["vs_reference"] = parity_metrics(layer0["out"], ref32)
+        par["bars"] = {"append": "bit-exact", "vs_reference": "max_rel <= 1e-4"}
+        par["pass"] = bool(par["append_slabs_bit_exact"] and
+                           par["vs_reference"]["max_rel"] <= 1e-4)
+    return base, par
 
 
-MFMA_BF16_PEAK_TFLOPS = 2500.0
-
-
-def ceiling_probe(ctx, w, slab_pair, slab_bytes):
-    """Practical read ceilings on this device (libehip's probes, no
+def ceiling_probe(w, slab_pair, slab_bytes):
+    """Practical read ceilings on this device (lib/libehip_probe.so, no
     arithmetic): a streaming read of one K slab, and the decode access pattern
     (random (block, kv head) tiles of K and V, 36 per wavefront) with the
     default and the non-temporal load policy."""
+    from ehip import probe
     ks, vs = slab_pair
     tile = w.block_size * w.head_dim * w.kv_bytes
     rng = np.random.default_rng(5)
     blocks = rng.permutation(w.pool_blocks).astype(np.int32)
     tiles = 36
     blocks = blocks[: blocks.size // tiles * tiles]
-    out = {"stream_read_gbps": round(ctx.probe_stream_read(ks, min(slab_bytes, (1 << 32) - 16),
-                                                           nt=False), 1)}
+    out = {"stream_read_gbps": round(probe.stream_read(ks, min(slab_bytes, (1 << 32) - 16),
+                                                       nt=False), 1)}
     for nt in (False, True):
-        g = ctx.probe_tile_gather(ks, vs, w.pool_blocks, blocks, tiles, w.kv_heads,
-                                  w.kv_heads * tile, tile, nt=nt)
+        g = probe.tile_gather(ks, vs, w.pool_blocks, blocks, tiles, w.kv_heads,
+                              w.kv_heads * tile, tile, nt=nt)
         out["tile_gather_nt_gbps" if nt else "tile_gather_gbps"] = round(g, 1)
     out["note"] = ("best of 3; tile gather = the decode kernels' access pattern alone, "
                    f"{tile}-byte (block, head) tiles of both slabs")
     return out
+
+
+def time_calls(ctx, layers, reps, call):
+    """Mean seconds of call(layer) over reps passes of every layer (HIP
+    events around each call, after one untimed pass)."""
+    ev = [(ctx.event(), ctx.event()) for _ in range(reps * layers)]
+    for r in range(reps + 1):
+        for layer in range(layers):
+            if r:
+                ctx.record(ev[(r - 1) * layers + layer][0])
+            call(layer)
+            if r:
+                ctx.record(ev[(r - 1) * layers + layer][1])
+    ctx.sync()
+    return float(np.mean([ctx.elapsed_ms(a, b) for a, b in ev])) / 1e3
 
 
 def time_chunks(ctx, ehip, w, slabs, qs, outs, layers, reps=5):
@@ -160,17 +252,8 @@ def time_chunks(ctx, ehip, w, slabs, qs, outs, layers, reps=5):
     g = ehip.geometry(w.heads, w.kv_heads, w.head_dim, w.block_size, w.kv_dtype,
                       w.pool_blocks, w.scale)
     ctx._check(ctx.step_upload(g, st))
-    ev = [(ctx.event(), ctx.event()) for _ in range(reps * layers)]
-    for r in range(reps + 1):
-        for layer in range(layers):
-            ks, vs = slabs[layer]
-            if r:
-                ctx.record(ev[(r - 1) * layers + layer][0])
-            ctx._check(ctx.step_attention(qs[layer], ks, vs, outs[layer]))
-            if r:
-                ctx.record(ev[(r - 1) * layers + layer][1])
-    ctx.sync()
-    t = float(np.mean([ctx.elapsed_ms(a, b) for a, b in ev])) / 1e3
+    t = time_calls(ctx, layers, reps, lambda layer: ctx._check(
+        ctx.step_attention(qs[layer], slabs[layer][0], slabs[layer][1], outs[layer])))
     flops = 0
     for T, L in zip(qlens, w.context_lens[idx]):
         P = int(L) - int(T)
@@ -199,30 +282,17 @@ def time_rope_append(ctx, ehip, w, slabs, qs, kns, vns, layers, reps=5):
     g = ehip.geometry(H, Hkv, d, w.block_size, w.kv_dtype, w.pool_blocks, w.scale)
     ctx._check(ctx.step_upload(g, ehip.StepArrays(w.query_lens, w.context_lens, w.tables,
                                                   w.slot_mapping)))
-    out = {}
-    for name in ("plain", "rope"):
-        ev = [(ctx.event(), ctx.event()) for _ in range(reps * layers)]
-        for r in range(reps + 1):
-            for layer in range(layers):
-                ks, vs = slabs[layer]
-                if r:
-                    ctx.record(ev[(r - 1) * layers + layer][0])
-                if name == "rope":
-                    ctx._check(ctx.step_rope_kv_append(qs[layer], kns[layer], vns[layer], cos,
-                                                       sin, n_pos, ks, vs))
-                else:
-                    ctx._check(ctx.step_kv_append(kns[layer], vns[layer], ks, vs))
-                if r:
-                    ctx.record(ev[(r - 1) * layers + layer][1])
-        ctx.sync()
-        out[name] = float(np.mean([ctx.elapsed_ms(a, b) for a, b in ev])) / 1e3
+    t_plain = time_calls(ctx, layers, reps, lambda layer: ctx._check(
+        ctx.step_kv_append(kns[layer], vns[layer], slabs[layer][0], slabs[layer][1])))
+    t_rope = time_calls(ctx, layers, reps, lambda layer: ctx._check(
+        ctx.step_rope_kv_append(qs[layer], kns[layer], vns[layer], cos, sin, n_pos,
+                                slabs[layer][0], slabs[layer][1])))
     cos.free()
     sin.free()
     nbytes = R * (2 * H * d * 4 + 2 * Hkv * d * 4 + d * 4 + 2 * Hkv * d * w.kv_bytes)
-    return {"rows": R, "bytes_per_launch": nbytes,
-            "us_per_launch": round(out["rope"] * 1e6, 2),
-            "gbps": round(nbytes / out["rope"] / 1e9, 1),
-            "plain_append_us_per_launch": round(out["plain"] * 1e6, 2)}
+    return {"rows": R, "bytes_per_launch": nbytes, "us_per_launch": round(t_rope * 1e6, 2),
+            "gbps": round(nbytes / t_rope / 1e9, 1),
+            "plain_append_us_per_launch": round(t_plain * 1e6, 2)}
 
 
 def c5_reprefill(ctx, ehip, w, slabs, layers, reps=3):
@@ -237,17 +307,8 @@ def c5_reprefill(ctx, ehip, w, slabs, layers, reps=3):
     out = ctx.alloc(T * w.heads * w.head_dim * 4)
     ctx.fill_normal(q, T * w.heads * w.head_dim, ehip.KV_F32, 0.0, w.qkv_std, 77)
     ctx._check(ctx.step_upload(g, st))
-    ev = [(ctx.event(), ctx.event()) for _ in range(reps * layers)]
-    for r in range(reps + 1):
-        for layer in range(layers):
-            ks, vs = slabs[layer]
-            if r:
-                ctx.record(ev[(r - 1) * layers + layer][0])
-            ctx._check(ctx.step_attention(q, ks, vs, out))
-            if r:
-                ctx.record(ev[(r - 1) * layers + layer][1])
-    ctx.sync()
-    t = float(np.mean([ctx.elapsed_ms(a, b) for a, b in ev])) / 1e3
+    t = time_calls(ctx, layers, reps, lambda layer: ctx._check(
+        ctx.step_attention(q, slabs[layer][0], slabs[layer][1], out)))
     flops = 4 * w.heads * w.head_dim * (T * (T + 1) // 2)
     q.free()
     out.free()
@@ -259,6 +320,130 @@ def c5_reprefill(ctx, ehip, w, slabs, layers, reps=3):
                          "kernel": "causal prefill chunk (bf16 MFMA)"}}
 
 
+class Bench:
+    """Device state of one workload draw: pools, queries, new rows, outputs
+    for every layer, and the step loop."""
+
+    def __init__(self, ctx, ehip, w, layers, q8, host_layer0):
+        self.ctx, self.ehip, self.w, self.layers, self.q8 = ctx, ehip, w, layers, q8
+        H, Hkv, d, bs = w.heads, w.kv_heads, w.head_dim, w.block_size
+        R = w.rows
+        self.slab_bytes = w.pool_blocks * Hkv * bs * d * w.kv_bytes
+        self.slabs, self.scales, self.qs, self.kns, self.vns, self.outs = [], [], [], [], [], []
+        self.layer0 = None
+        for layer in range(layers):
+            ks, vs = ctx.alloc(self.slab_bytes), ctx.alloc(self.slab_bytes)
+            q, kn, vn = ctx.alloc(R * H * d * 4), ctx.alloc(R * Hkv * d * 4), ctx.alloc(R * Hkv * d * 4)
+            if q8:
+                # int8 slabs: random bytes (bf16 normals over the same memory);
+                # scales: fp32 normals, one per (block, kv head)
+                n16 = self.slab_bytes // 2
+                ctx.fill_normal(ks, n16, ehip.KV_BF16, 0.0, 1.0, 10 + layer)
+                ctx.fill_normal(vs, n16, ehip.KV_BF16, 0.0, 1.0, 1000 + layer)
+                kss, vss = ctx.alloc(w.pool_blocks * Hkv * 4), ctx.alloc(w.pool_blocks * Hkv * 4)
+                ctx.fill_normal(kss, w.pool_blocks * Hkv, ehip.KV_F32, 0.0, 0.01, 5000 + layer)
+                ctx.fill_normal(vss, w.pool_blocks * Hkv, ehip.KV_F32, 0.0, 0.01, 6000 + layer)
+                self.scales.append((kss, vss))
+            elif layer == 0 and host_layer0:
+                self.layer0 = self._host_layer0(ks, vs, q, kn, vn)
+            else:
+                n = w.pool_blocks * Hkv * bs * d
+                ctx.fill_normal(ks, n, w.kv_dtype, 0.0, w.qkv_std, 10 + layer)
+                ctx.fill_normal(vs, n, w.kv_dtype, 0.0, w.qkv_std, 1000 + layer)
+            if not (layer == 0 and self.layer0 is not None):
+                ctx.fill_normal(q, R * H * d, ehip.KV_F32, 0.0, w.qkv_std, 2000 + layer)
+                ctx.fill_normal(kn, R * Hkv * d, ehip.KV_F32, 0.0, w.qkv_std, 3000 + layer)
+                ctx.fill_normal(vn, R * Hkv * d, ehip.KV_F32, 0.0, w.qkv_std, 4000 + layer)
+            self.slabs.append((ks, vs))
+            self.qs.append(q)
+            self.kns.append(kn)
+            self.vns.append(vn)
+            self.outs.append(ctx.alloc(R * H * d * 4))
+        ctx.sync()
+        self.geom = ehip.geometry(H, Hkv, d, bs, w.kv_dtype, w.pool_blocks, w.scale)
+        self.st = ehip.StepArrays(w.query_lens, w.context_lens, w.tables, w.slot_mapping)
+
+    def _host_layer0(self, ks, vs, q, kn, vn):
+        """Layer 0 from the workload's seeded fill_normal streams (host)."""
+        from ehip import workloads
+        w = self.w
+        t0 = time.perf_counter()
+        k32, v32 = w.pool(0)
+        qh = w.q(0)
+        knh, vnh = w.new_kv(0)
+        if w.kv_dtype == self.ehip.KV_BF16:
+            ks.upload(workloads.to_bf16_bits(k32))
+            vs.upload(workloads.to_bf16_bits(v32))
+        else:
+            ks.upload(k32)
+            vs.upload(v32)
+        q.upload(qh)
+        kn.upload(knh)
+        vn.upload(vnh)
+        log(f"[bench] layer 0 from the seeded host streams in {time.perf_counter() - t0:.1f} s")
+        return {"k32": k32, "v32": v32, "q": qh, "kn": knh, "vn": vnh}
+
+    def step(self, evs=None):
+        ctx = self.ctx
+        ctx._check(ctx.step_upload(self.geom, self.st))
+        for layer in range(self.layers):
+            ks, vs = self.slabs[layer]
+            if self.q8:
+                kss, vss = self.scales[layer]
+                ctx._check(ctx.step_kv_append_int8(self.kns[layer], self.vns[layer], ks, vs, kss,
+                                                   vss))
+            else:
+                ctx._check(ctx.step_kv_append(self.kns[layer], self.vns[layer], ks, vs))
+            if evs is not None:
+                ctx.record(evs[layer][0])
+            if self.q8:
+                kss, vss = self.scales[layer]
+                ctx._check(ctx.step_attention_int8(self.qs[layer], ks, vs, kss, vss,
+                                                   self.outs[layer]))
+            else:
+                ctx._check(ctx.step_attention(self.qs[layer], ks, vs, self.outs[layer]))
+            if evs is not None:
+                ctx.record(evs[layer][1])
+
+    def time_steps(self, steps, warmup):
+        """Per-step seconds (HIP events at every step boundary), per-launch
+        attention seconds of the sampled steps, and the wall time."""
+        ctx = self.ctx
+        for _ in range(warmup):
+            self.step()
+        ctx.sync()
+        sampled = [s for s in range(steps) if s % EVENT_SAMPLE == EVENT_SAMPLE // 2] or [0]
+        evs = {s: [(ctx.event(), ctx.event()) for _ in range(self.layers)] for s in sampled}
+        marks = [ctx.event() for _ in range(steps + 1)]
+        ctx.sync()
+        t0 = time.perf_counter()
+        ctx.record(marks[0])
+        for s in range(steps):
+            self.step(evs.get(s))
+            ctx.record(marks[s + 1])
+        ctx.sync()
+        wall = time.perf_counter() - t0
+        per_step = np.array([ctx.elapsed_ms(marks[s], marks[s + 1]) for s in range(steps)]) / 1e3
+        attn = np.array([ctx.elapsed_ms(a, b) for s in sampled for (a, b) in evs[s]]) / 1e3
+        return per_step, attn.reshape(len(sampled), self.layers), wall
+
+    def capture_layer0(self):
+        """Layer 0's post-step slabs and outputs, downloaded (before any side
+        measurement reuses the buffers)."""
+        w = self.w
+        shape = (w.pool_blocks, w.kv_heads, w.block_size, w.head_dim)
+        dt = np.uint16 if w.kv_dtype == self.ehip.KV_BF16 else np.float32
+        ks, vs = self.slabs[0]
+        self.layer0["k_dev"] = ks.download(dt, shape)
+        self.layer0["v_dev"] = vs.download(dt, shape)
+        self.layer0["out"] = self.outs[0].download(np.float32, (w.rows, w.heads, w.head_dim))
+
+    def free(self):
+        for b in [x for pair in self.slabs for x in pair] + self.qs + self.kns + self.vns + \
+                self.outs + [x for pair in self.scales for x in pair]:
+            b.free()
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -268,17 +453,23 @@ def main():
     import ehip
     from ehip import workloads
 
-    w = workloads.CONFIGS[args.config]()
+    make = workloads.CONFIGS[args.config]
+    w = make(seed=args.seed) if args.seed else make()
     q8 = args.kv == "int8"
     if q8:
         w.kv_dtype = ehip.KV_INT8
     layers = args.layers or w.layers
     H, Hkv, d, bs = w.heads, w.kv_heads, w.head_dim, w.block_size
-    R = w.rows
-    kvb = w.kv_bytes
-    slab_bytes = w.pool_blocks * Hkv * bs * d * kvb
-    log(f"[bench] {w.name}: B={w.num_seqs} rows={R} sumL={int(w.context_lens.sum())} "
-        f"pool={w.pool_blocks} blocks, {layers} layers, slabs {2 * layers * slab_bytes / 2**30:.1f} GiB")
+    tok = int(w.context_lens.sum())
+    draw = {"seed": w.seed, "sum_context": tok}
+    seeds = [w.seed]
+    if w.name == "C4":
+        mean, sd = workloads.c4_sum_context_stats(w.num_seqs)
+        draw.update(expected_sum_context=round(mean), sd=round(sd), z=round((tok - mean) / sd, 3))
+        if abs(tok - mean) > sd:  # an atypical draw: report the median of three seeds
+            seeds = [w.seed, w.seed + 1, w.seed + 2]
+    log(f"[bench] {w.name}: B={w.num_seqs} rows={w.rows} sumL={tok} pool={w.pool_blocks} blocks, "
+        f"{layers} layers, draw {draw}")
 
     ctx = ehip.Context(0)
     if args.copy_probe_mib:
@@ -289,160 +480,135 @@ def main():
         a.free()
         b.free()
         log(f"[bench] copy probe: {nbytes} bytes device-to-device")
-    slabs, scales, qs, kns, vns, outs = [], [], [], [], [], []
-    for layer in range(layers):
-        ks, vs = ctx.alloc(slab_bytes), ctx.alloc(slab_bytes)
-        if q8:
-            # int8 slabs: random bytes (bf16 normals over the same memory);
-            # scales: fp32 normals, one per (block, kv head)
-            n16 = slab_bytes // 2
-            ctx.fill_normal(ks, n16, ehip.KV_BF16, 0.0, 1.0, 10 + layer)
-            ctx.fill_normal(vs, n16, ehip.KV_BF16, 0.0, 1.0, 1000 + layer)
-            kss, vss = ctx.alloc(w.pool_blocks * Hkv * 4), ctx.alloc(w.pool_blocks * Hkv * 4)
-            ctx.fill_normal(kss, w.pool_blocks * Hkv, ehip.KV_F32, 0.0, 0.01, 5000 + layer)
-            ctx.fill_normal(vss, w.pool_blocks * Hkv, ehip.KV_F32, 0.0, 0.01, 6000 + layer)
-            scales.append((kss, vss))
-        else:
-            ctx.fill_normal(ks, w.pool_blocks * Hkv * bs * d, w.kv_dtype, 0.0, w.qkv_std,
-                            10 + layer)
-            ctx.fill_normal(vs, w.pool_blocks * Hkv * bs * d, w.kv_dtype, 0.0, w.qkv_std,
-                            1000 + layer)
-        slabs.append((ks, vs))
-        q, kn, vn = ctx.alloc(R * H * d * 4), ctx.alloc(R * Hkv * d * 4), ctx.alloc(R * Hkv * d * 4)
-        ctx.fill_normal(q, R * H * d, ehip.KV_F32, 0.0, w.qkv_std, 2000 + layer)
-        ctx.fill_normal(kn, R * Hkv * d, ehip.KV_F32, 0.0, w.qkv_std, 3000 + layer)
-        ctx.fill_normal(vn, R * Hkv * d, ehip.KV_F32, 0.0, w.qkv_std, 4000 + layer)
-        qs.append(q)
-        kns.append(kn)
-        vns.append(vn)
-        outs.append(ctx.alloc(R * H * d * 4))
-    ctx.sync()
-    log("[bench] pools resident")
+    want_cpu = not args.no_cpu_baseline and not q8
+    bench = Bench(ctx, ehip, w, layers, q8, host_layer0=want_cpu)
+    log(f"[bench] pools resident ({2 * layers * bench.slab_bytes / 2**30:.1f} GiB of slabs)")
 
-    g = ehip.geometry(H, Hkv, d, bs, w.kv_dtype, w.pool_blocks, w.scale)
-    st = ehip.StepArrays(w.query_lens, w.context_lens, w.tables, w.slot_mapping)
-
-    def step(evs=None):
-        ctx._check(ctx.step_upload(g, st))
-        for layer in range(layers):
-            ks, vs = slabs[layer]
-            if q8:
-                kss, vss = scales[layer]
-                ctx._check(ctx.step_kv_append_int8(kns[layer], vns[layer], ks, vs, kss, vss))
-            else:
-                ctx._check(ctx.step_kv_append(kns[layer], vns[layer], ks, vs))
-            if evs is not None:
-                ctx.record(evs[layer][0])
-            if q8:
-                ctx._check(ctx.step_attention_int8(qs[layer], ks, vs, kss, vss, outs[layer]))
-            else:
-                ctx._check(ctx.step_attention(qs[layer], ks, vs, outs[layer]))
-            if evs is not None:
-                ctx.record(evs[layer][1])
-
-    for _ in range(args.warmup):
-        step()
-    ctx.sync()
-    log("[bench] warmup done")
+    per_step, attn, wall = bench.time_steps(args.steps, args.warmup)
     rows, items, partials = ctx.step_info()
+    log(f"[bench] timed {args.steps} steps: wall {wall * 1e3:.2f} ms, step median "
+        f"{np.median(per_step) * 1e3:.3f} ms, mean {per_step.mean() * 1e3:.3f} ms")
+    qs = np.percentile(attn * 1e6, [0, 10, 50, 90, 100])
+    log("[bench] attention us per launch: min %.1f p10 %.1f p50 %.1f p90 %.1f max %.1f" % tuple(qs))
+    per_layer = w.bytes_per_layer(with_append=True)
+    step_bytes = per_layer["total"] * layers
+    runs = [{"seed": w.seed, "sum_context": tok, "ms_per_step": float(np.median(per_step)) * 1e3,
+             "gbps": step_bytes / float(np.median(per_step)) / 1e9}]
+    if bench.layer0 is not None:
+        bench.capture_layer0()
 
-    K = args.steps
-    sampled = [s for s in range(K) if s % EVENT_SAMPLE == EVENT_SAMPLE // 2] or [0]
-    evs = {s: [(ctx.event(), ctx.event()) for _ in range(layers)] for s in sampled}
-    e_start, e_end = ctx.event(), ctx.event()
-    ctx.sync()
-    t0 = time.perf_counter()
-    ctx.record(e_start)
-    for s in range(K):
-        step(evs.get(s))
-    ctx.record(e_end)
-    ctx.sync()
-    wall = time.perf_counter() - t0
-    gpu_ms = ctx.elapsed_ms(e_start, e_end)
-    attn_ms = [ctx.elapsed_ms(a, b) for s in sampled for (a, b) in evs[s]]
-    log(f"[bench] timed {K} steps: wall {wall * 1e3:.2f} ms, events {gpu_ms:.2f} ms")
-    a = np.array(attn_ms).reshape(len(sampled), layers) * 1e3
-    q = np.percentile(a, [0, 10, 50, 90, 100])
-    log("[bench] attention us per launch: min %.1f p10 %.1f p50 %.1f p90 %.1f max %.1f" % tuple(q))
-    log("[bench] per-layer mean us: " + " ".join(f"{x:.0f}" for x in a.mean(axis=0)))
-    log("[bench] sampled-step mean us: " + " ".join(f"{x:.0f}" for x in a.mean(axis=1)))
-
-    t_step = max(wall, gpu_ms / 1e3) / K
     graph_info = None
     if args.graph:
         # The per-layer launches of the uploaded step, captured once and
         # replayed per step (the step's plan is the same every step here); the
-        # descriptor upload stays eager. Per-launch events above came from the
-        # eager steps.
+        # descriptor upload stays eager.
         from ehip import hipgraph
         gs = hipgraph.Stream()
         ctx._check(ehip.lib().ehip_set_stream(ctx.h, gs.h))
-        ctx._check(ctx.step_upload(g, st))
+        ctx._check(ctx.step_upload(bench.geom, bench.st))
         ctx.sync()
         graph = hipgraph.Graph()
 
         def layer_launches():
             for layer in range(layers):
-                ks, vs = slabs[layer]
-                if q8:
-                    kss, vss = scales[layer]
-                    ctx._check(ctx.step_kv_append_int8(kns[layer], vns[layer], ks, vs, kss, vss))
-                    ctx._check(ctx.step_attention_int8(qs[layer], ks, vs, kss, vss, outs[layer]))
-                else:
-                    ctx._check(ctx.step_kv_append(kns[layer], vns[layer], ks, vs))
-                    ctx._check(ctx.step_attention(qs[layer], ks, vs, outs[layer]))
+                ks, vs = bench.slabs[layer]
+                ctx._check(ctx.step_kv_append(bench.kns[layer], bench.vns[layer], ks, vs))
+                ctx._check(ctx.step_attention(bench.qs[layer], ks, vs, bench.outs[layer]))
 
         graph.capture(gs, layer_launches)
         for _ in range(args.warmup):
-            ctx._check(ctx.step_upload(g, st))
+            ctx._check(ctx.step_upload(bench.geom, bench.st))
             graph.replay(gs)
         ctx.sync()
         t0 = time.perf_counter()
-        for _ in range(K):
-            ctx._check(ctx.step_upload(g, st))
+        for _ in range(args.steps):
+            ctx._check(ctx.step_upload(bench.geom, bench.st))
             graph.replay(gs)
         ctx.sync()
-        t_graph = (time.perf_counter() - t0) / K
-        log(f"[bench] graph replay: {t_graph * 1e3:.3f} ms/step (eager {t_step * 1e3:.3f})")
-        graph_info = {"eager_ms_per_step": round(t_step * 1e3, 4),
+        t_graph = (time.perf_counter() - t0) / args.steps
+        log(f"[bench] graph replay: {t_graph * 1e3:.3f} ms/step")
+        graph_info = {"eager_ms_per_step_median": round(runs[0]["ms_per_step"], 4),
                       "graph_ms_per_step": round(t_graph * 1e3, 4)}
-        t_step = t_graph
         ctx._check(ehip.lib().ehip_set_stream(ctx.h, None))
         graph.close()
         gs.close()
-    per_layer = w.bytes_per_layer(with_append=True)
-    step_bytes = per_layer["total"] * layers
-    value = step_bytes / t_step / 1e9
+
+    result_extra = {}
+    if not args.no_ceiling_probe:
+        result_extra["ceiling"] = ceiling_probe(w, bench.slabs[0], bench.slab_bytes)
+        log(f"[bench] read ceiling: {result_extra['ceiling']}")
+    # The chunk, fused-RoPE and re-prefill measurements run the fp32/bf16
+    # entry points; an INT8 run reports the decode step alone.
+    if not q8 and not args.no_extras:
+        pre = time_chunks(ctx, ehip, w, bench.slabs, bench.qs, bench.outs, layers)
+        if pre is not None:
+            result_extra["prefill"] = pre
+            log(f"[bench] prefill chunks: {pre['us_per_layer']} us/layer, {pre['tflops']} TFLOP/s")
+        ra = time_rope_append(ctx, ehip, w, bench.slabs, bench.qs, bench.kns, bench.vns, layers)
+        result_extra["rope_append"] = ra
+        log(f"[bench] fused RoPE + append: {ra}")
+        if w.name == "C5":
+            ev = c5_reprefill(ctx, ehip, w, bench.slabs, layers)
+            result_extra["reprefill_event"] = ev
+            # One 4096-token re-prefill every 50 decode steps, amortised per step.
+            result_extra["ms_per_step_with_reprefill"] = round(runs[0]["ms_per_step"] +
+                                                               ev["event_ms"] / 50, 4)
+            log(f"[bench] C5 re-prefill: {ev['us_per_layer']} us/layer, {ev['tflops']} TFLOP/s")
+    layer0 = bench.layer0
+    bench.free()
+
+    # Further seeds of an atypical draw (timing only).
+    for seed in seeds[1:]:
+        wx = make(seed=seed)
+        bx = Bench(ctx, ehip, wx, layers, q8, host_layer0=False)
+        ps, _, _ = bx.time_steps(args.steps, args.warmup)
+        bx.free()
+        bx_bytes = wx.bytes_per_layer(with_append=True)["total"] * layers
+        runs.append({"seed": seed, "sum_context": int(wx.context_lens.sum()),
+                     "ms_per_step": float(np.median(ps)) * 1e3,
+                     "gbps": bx_bytes / float(np.median(ps)) / 1e9})
+        log(f"[bench] seed {seed}: {runs[-1]}")
+    headline = sorted(runs, key=lambda r: r["gbps"])[len(runs) // 2]
+
+    t_step = float(np.median(per_step))
     attn_bytes = per_layer["unique_kv"] + per_layer["q_o"] + per_layer["tables"]
-    attn_avg = float(np.mean(attn_ms)) / 1e3
+    attn_avg = float(attn.mean())
     achieved = attn_bytes / attn_avg / 1e9
-    tok = int(w.context_lens.sum())
-    traffic = traffic_from_profiles(w.name, "int8" if q8 else "")
+    tr = traffic_from_profiles(w.name, "int8" if q8 else "")
+    traffic = tr[0] if tr is not None and tr[1] == tok else None  # measured on this draw
 
     result = {
         "metric": "ragged paged-attn decode: HBM GB/s (% of 8 TB/s) + attended KV tok/s per step",
-        "value": round(value, 2),
+        "value": round(headline["gbps"], 2),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": K,
+        "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(t_step * 1e3, 4),
+        "ms_per_step": round(headline["ms_per_step"], 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic",
+        "data": ("synthetic: structure from the config's seeded mt19937_64 draw; layer 0 "
+                 "values from the reference fill_normal streams, other layers from a device "
+                 "generator of the same N(0, std)"),
         "config": {
             "workload": (f"{w.name}: {w.num_seqs} sequences, {layers} layers, H={H} Hkv={Hkv} "
-                         f"d={d} bs={bs}, kv {KV_NAMES[w.kv_dtype]}, "
-                         f"sum L={tok}, rows={R}"),
+                         f"d={d} bs={bs}, kv {KV_NAMES[w.kv_dtype]}, sum L={tok}, "
+                         f"rows={w.rows}"),
             "kv_dtype": KV_NAMES[w.kv_dtype],
             "num_seqs": w.num_seqs, "layers": layers, "sum_context": tok,
-            "work_items": items, "split_partials": partials,
+            "draw": draw, "work_items": items, "split_partials": partials,
             "parallelism": "single GPU",
         },
-        "hbm_frac": round(value / HBM_PEAK_GBS, 4),
-        "attended_kv_tok_per_s": round(tok * layers / t_step, 1),
+        "step_time": {"median_ms": round(t_step * 1e3, 4),
+                      "mean_ms": round(float(per_step.mean()) * 1e3, 4),
+                      "min_ms": round(float(per_step.min()) * 1e3, 4),
+                      "max_ms": round(float(per_step.max()) * 1e3, 4),
+                      "wall_ms_per_step": round(wall / args.steps * 1e3, 4)},
+        "hbm_frac": round(headline["gbps"] / HBM_PEAK_GBS, 4),
+        "attended_kv_tok_per_s": round(headline["sum_context"] * layers /
+                                       (headline["ms_per_step"] / 1e3), 1),
         "bytes_per_step": step_bytes,
         "roofline": {
             "bound": "hbm",
@@ -451,37 +617,24 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "kernel": "paged decode attention (one launch per layer)",
+            "kernel": "paged decode attention call (decode kernel + split merge)",
             "algorithmic_bytes_per_launch": attn_bytes,
             "avg_launch_us": round(attn_avg * 1e6, 3),
-            "launches_timed": len(attn_ms),
-            "timed_steps_sampled": len(sampled),
+            "launches_timed": int(attn.size),
+            "timed_steps_sampled": int(attn.shape[0]),
         },
     }
+    if len(runs) > 1:
+        result["seeds"] = runs
     if graph_info is not None:
         result["launch"] = dict(graph_info, mode="captured graph of the per-layer launches")
-    if not args.no_ceiling_probe:
-        result["ceiling"] = ceiling_probe(ctx, w, slabs[0], slab_bytes)
-        log(f"[bench] read ceiling: {result['ceiling']}")
-    # The chunk, fused-RoPE and re-prefill measurements run the fp32/bf16
-    # entry points; an INT8 run reports the decode step alone.
-    pre = None if q8 else time_chunks(ctx, ehip, w, slabs, qs, outs, layers)
-    if pre is not None:
-        result["prefill"] = pre
-        log(f"[bench] prefill chunks: {pre['us_per_layer']} us/layer, {pre['tflops']} TFLOP/s")
-    if not q8:
-        ra = time_rope_append(ctx, ehip, w, slabs, qs, kns, vns, layers)
-        result["rope_append"] = ra
-        log(f"[bench] fused RoPE + append: {ra}")
-    if w.name == "C5" and not q8:
-        ev = c5_reprefill(ctx, ehip, w, slabs, layers)
-        result["reprefill_event"] = ev
-        # One 4096-token re-prefill every 50 decode steps, amortised per step.
-        result["ms_per_step_with_reprefill"] = round(t_step * 1e3 + ev["event_ms"] / 50, 4)
-        log(f"[bench] C5 re-prefill: {ev['us_per_layer']} us/layer, {ev['tflops']} TFLOP/s")
-    if not args.no_cpu_baseline:
-        log("[bench] cpu baseline ...")
-        result["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
+    result.update(result_extra)
+    if want_cpu and layer0 is not None:
+        log("[bench] cpu baseline + parity ...")
+        base, par = cpu_baseline_and_parity(w, layer0, args.cpu_seconds)
+        result["cpu_baseline"] = base
+        result["parity"] = par
+        log(f"[bench] parity: {par}")
     ctx.close()
     print(json.dumps(result), flush=True)
 
