@@ -115,8 +115,10 @@ def traffic_from_profiles(config: str, kv: str = ""):
 
 
 def parity_metrics(got, ref) -> dict:
-    """max_abs; max_rel = max|a-b| / max(|b|, 1e-6 max|b|); the reference's
-    allclose criterion |a-b| <= 1e-5 + 1e-4 |b| (src/tensor/ops.h:207)."""
+    """max_abs; max_rel = max over elements of |a-b| / max(|b|, 1e-6 max|b|)
+    (the elementwise form); max_rel_vector = max over (row, head) vectors of
+    max|a-b| / max|b|; the reference's allclose criterion
+    |a-b| <= 1e-5 + 1e-4 |b| (src/tensor/ops.h:207)."""
     a = np.asarray(got, np.float64)
     b = np.asarray(ref, np.float64)
     diff = np.abs(a - b)
@@ -124,7 +126,9 @@ def parity_metrics(got, ref) -> dict:
     den = np.maximum(np.abs(b), floor)
     den[den == 0] = 1.0
     fails = int(np.count_nonzero(~(diff <= 1e-5 + 1e-4 * np.abs(b))))
+    vec_den = np.maximum(np.abs(b).reshape(-1, b.shape[-1]).max(axis=1), 1e-30)
     return {"max_abs": float(diff.max()), "max_rel": float((diff / den).max()),
+            "max_rel_vector": float((diff.reshape(-1, b.shape[-1]).max(axis=1) / vec_den).max()),
             "allclose_rtol1e-4_atol1e-5": fails == 0, "allclose_failures": fails,
             "elements": int(a.size)}
 
@@ -187,18 +191,27 @@ def cpu_baseline_and_parity(w, layer0, seconds: float):
                        f"calls"),
             "host_physical_cores": phys, "host_cpus_allowed": allowed, "cpu_model": model,
             "attended_kv_tok_per_s": round(sum(lens) / t, 1), "ms_per_call": round(t * 1e3, 3)}
+    # How far the reference's own two backends (scalar and AVX2, both
+    # bit-identical to the reference build) are apart on the same fp32 cache:
+    # the elementwise max_rel of near-zero outputs (sums that cancel) is set
+    # by summation order, not by correctness.
+    ref_scalar = orc.paged_decode_batched(q, k32, v32, w.tables, lens, H, Hkv, d, bs, w.scale,
+                                          isa=orc.ISA_SCALAR)
+    par["reference_scalar_vs_avx2"] = parity_metrics(ref_scalar, ref32)
+    del ref_scalar
+    gate = "vs_reference_on_bf16_kv" if bf16 else "vs_reference"
     if bf16:
         par["vs_reference_on_fp32_kv"] = parity_metrics(layer0["out"], ref32)
-        par["bars"] = {"append": "bit-exact", "vs_reference_on_bf16_kv": "max_rel <= 1e-4",
-                       "vs_reference_on_fp32_kv": "max_abs <= 2e-2"}
-        par["pass"] = bool(par["append_slabs_bit_exact"] and
-                           par["vs_reference_on_bf16_kv"]["max_rel"] <= 1e-4 and
-                           par["vs_reference_on_fp32_kv"]["max_abs"] <= 2e-2)
     else:
         par["vs_reference"] = parity_metrics(layer0["out"], ref32)
-        par["bars"] = {"append": "bit-exact", "vs_reference": "max_rel <= 1e-4"}
-        par["pass"] = bool(par["append_slabs_bit_exact"] and
-                           par["vs_reference"]["max_rel"] <= 1e-4)
+    par["bars"] = {"append": "bit-exact",
+                   gate: "max_rel_vector <= 1e-4 and the reference allclose (rtol 1e-4, atol 1e-5)"}
+    ok = (par["append_slabs_bit_exact"] and par[gate]["max_rel_vector"] <= 1e-4 and
+          par[gate]["allclose_rtol1e-4_atol1e-5"])
+    if bf16:
+        par["bars"]["vs_reference_on_fp32_kv"] = "max_abs <= 2e-2"
+        ok = ok and par["vs_reference_on_fp32_kv"]["max_abs"] <= 2e-2
+    par["pass"] = bool(ok)
     return base, par
 
 
