@@ -201,6 +201,23 @@ int ehip_paged_decode_attention_f32(ehip_ctx* ctx, const float* d_q, const float
                                     int64_t block_stride, int64_t slab_blocks, float scale,
                                     float* d_out);
 
+/* No counterpart in the reference: the allocation-free variant of
+ * ehip_paged_decode_attention_f32 (same arguments and results), for callers
+ * that cannot allocate device memory — code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc. Its one-row plan and split
+ * partials live in a static per-device scratch array of 4 MiB, written by a
+ * kernel (no allocation, copy or host staging per call); rows that would need
+ * more (key splits x H x (d + 2) x 4 bytes of partials, plus the plan) get
+ * ResourceExhausted. Every call on a device shares that device's array:
+ * calls that overlap on one device (two streams, two contexts) race and must
+ * be ordered by the caller. */
+int ehip_paged_decode_attention_f32_noalloc(ehip_ctx* ctx, const float* d_q,
+                                            const float* d_k_slab, const float* d_v_slab,
+                                            const int32_t* d_block_table, int64_t num_blocks,
+                                            int64_t length, int64_t heads, int64_t kv_heads,
+                                            int64_t d, int64_t block_size, int64_t block_stride,
+                                            int64_t slab_blocks, float scale, float* d_out);
+
 /* kernels::PagedDecodeAttentionBatchedF32 (src/kernels/paged_attention.h:105-110):
  * B sequences over one shared slab pair. Like the reference, the tables are
  * host arrays of per-sequence pointers (h_block_tables[b] has

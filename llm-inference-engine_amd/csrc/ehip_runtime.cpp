@@ -19,7 +19,7 @@ struct ehip_ctx {
   int device = 0;
   hipStream_t stream = nullptr;      // the stream every call enqueues on
   hipStream_t own_stream = nullptr;  // the context's own (created at init)
-  std::string last_error;
+  char last_error[512] = {};  // fixed storage: reporting an error allocates nothing
 
   // Step descriptor: host staging (pinned, double-buffered so building step
   // n+1 never overwrites a buffer whose copy is still queued) and its device
@@ -58,12 +58,11 @@ namespace {
 using ehip::Plan;
 
 int SetError(ehip_ctx* ctx, int code, const char* fmt, ...) {
-  char buf[512];
+  if (!ctx) return code;
   va_list ap;
   va_start(ap, fmt);
-  std::vsnprintf(buf, sizeof(buf), fmt, ap);
+  std::vsnprintf(ctx->last_error, sizeof(ctx->last_error), fmt, ap);
   va_end(ap);
-  if (ctx) ctx->last_error = buf;
   return code;
 }
 
@@ -297,6 +296,10 @@ int ehip_init(int device, ehip_ctx** out) {
     uint32_t* words = reinterpret_cast<uint32_t*>(ctx->d_err);
     ctx->queue.d_counters = words + kQueueWord;
     ctx->queue.d_done = words + kQueueWord + size_t{ehip::kItemQueues} * ehip::kQueueStride;
+    // The device address of the allocation-free entry point's static scratch
+    // (fetched once per device, with the device current).
+    e = ehip::InitStaticScratch(device);
+    if (e != hipSuccess) { rc = HipFail(ctx, e, "hipGetSymbolAddress(scratch)"); break; }
   } while (false);
   if (rc != EHIP_OK) {
     ehip_destroy(ctx);
@@ -324,7 +327,7 @@ int ehip_destroy(ehip_ctx* ctx) {
 
 int ehip_last_error(const ehip_ctx* ctx, char* buf, size_t n) {
   if (!ctx || !buf || n == 0) return EHIP_INVALID_ARGUMENT;
-  std::snprintf(buf, n, "%s", ctx->last_error.c_str());
+  std::snprintf(buf, n, "%s", ctx->last_error);
   return EHIP_OK;
 }
 
@@ -341,7 +344,7 @@ int ehip_sync(ehip_ctx* ctx) {
   std::vector<uint32_t> queue(queue_bytes / sizeof(uint32_t));
   EHIP_HIP(ctx, hipMemcpy(queue.data(), ctx->queue.d_counters, queue_bytes, hipMemcpyDeviceToHost));
   bool dirty = false;
-  for (int k = 0; k <= ehip::kItemQueues; ++k) dirty = dirty || queue[size_t{k} * ehip::kQueueStride];
+  for (int k = 0; k <= ehip::kItemQueues; ++k) dirty = dirty || queue[static_cast<size_t>(k) * ehip::kQueueStride];
   if (dirty) {
     EHIP_HIP(ctx, hipMemset(ctx->queue.d_counters, 0, queue_bytes));
     return SetError(ctx, EHIP_INTERNAL,
@@ -549,6 +552,64 @@ int ehip_paged_decode_attention_f32(ehip_ctx* ctx, const float* d_q, const float
     return SetError(ctx, rc, "%s", err.c_str());
   if (int rc = UploadPlan(ctx, g, std::move(plan), d_block_table)) return rc;
   return LaunchAttention(ctx, d_q, d_k_slab, d_v_slab, d_out);
+}
+
+int ehip_paged_decode_attention_f32_noalloc(ehip_ctx* ctx, const float* d_q,
+                                            const float* d_k_slab, const float* d_v_slab,
+                                            const int32_t* d_block_table, int64_t num_blocks,
+                                            int64_t length, int64_t heads, int64_t kv_heads,
+                                            int64_t d, int64_t block_size, int64_t block_stride,
+                                            int64_t slab_blocks, float scale, float* d_out) {
+  if (int rc = CheckCtx(ctx)) return rc;
+  if (heads > INT32_MAX || kv_heads > INT32_MAX || d > INT32_MAX || block_size > INT32_MAX)
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "geometry out of range");
+  const ehip_geometry g{static_cast<int32_t>(heads), static_cast<int32_t>(kv_heads),
+                        static_cast<int32_t>(d),     static_cast<int32_t>(block_size),
+                        EHIP_KV_F32,                 0,
+                        slab_blocks,                 block_stride,
+                        scale};
+  // The same checks as the allocating entry point, without building a plan
+  // on the host or a message string.
+  if (int rc = ehip::ValidateGeometry(g, nullptr))
+    return SetError(ctx, rc, "invalid geometry (heads=%d kv_heads=%d d=%d block_size=%d)", g.heads,
+                    g.kv_heads, g.head_dim, g.block_size);
+  if (!NonNull(d_q) || !NonNull(d_k_slab) || !NonNull(d_v_slab) || !NonNull(d_block_table) ||
+      !NonNull(d_out))
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "null decode operand");
+  if (length < 1 || length > (int64_t{1} << 30))
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "length=%lld out of range",
+                    static_cast<long long>(length));
+  if ((length + block_size - 1) / block_size > num_blocks)
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "ceil(length/bs) exceeds num_blocks=%lld",
+                    static_cast<long long>(num_blocks));
+  const int32_t split_len = ehip::SingleRowSplitTokens(g, length);
+  const int64_t nsplit = (length + split_len - 1) / split_len;
+  const int group = g.heads / g.kv_heads;
+  const size_t need = ehip::StaticScratchNeed(nsplit, g.kv_heads, group, g.head_dim);
+  if (need > ehip::kStaticScratchBytes)
+    return SetError(ctx, EHIP_RESOURCE_EXHAUSTED,
+                    "the row needs %zu bytes of scratch (%lld key splits x %d query heads); the "
+                    "static scratch holds %zu: use ehip_paged_decode_attention_f32",
+                    need, static_cast<long long>(nsplit), g.heads, ehip::kStaticScratchBytes);
+  ehip::DecodeParams p{};
+  p.q = d_q;
+  p.k_slab = d_k_slab;
+  p.v_slab = d_v_slab;
+  p.out = d_out;
+  p.table = d_block_table;
+  p.err = ctx->d_err;
+  p.block_stride = ehip::BlockStride(g);
+  p.slab_blocks = g.slab_blocks;
+  p.heads = g.heads;
+  p.kv_heads = g.kv_heads;
+  p.group = group;
+  p.d = g.head_dim;
+  p.bs = g.block_size;
+  p.scale_log2 = g.scale * 1.4426950408889634f;
+  EHIP_HIP(ctx, ehip::LaunchSingleRowStatic(p, ctx->device, static_cast<int32_t>(length),
+                                            split_len, static_cast<int32_t>(nsplit), &ctx->queue,
+                                            ctx->stream));
+  return EHIP_OK;
 }
 
 namespace {

@@ -137,6 +137,23 @@ hipError_t LaunchRopeKvAppend(float* q, const float* src_k, const float* src_v,
                               int d, int bs, int64_t slab_blocks, void* k_slab, void* v_slab,
                               int kv_dtype, int32_t* err, hipStream_t stream);
 
+// Allocation-free single-sequence decode (decode_static.hip): the one-row
+// plan and its split partials live in a per-device static scratch array of
+// kStaticScratchBytes. InitStaticScratch fetches the array's address on the
+// current device (once per device; called at context creation).
+constexpr size_t kStaticScratchBytes = size_t{4} << 20;
+hipError_t InitStaticScratch(int device);
+// Scratch bytes a row cut into nsplit key splits needs (plan + partials).
+size_t StaticScratchNeed(int64_t nsplit, int kv_heads, int group, int d);
+// Writes the plan of one row of `length` keys, cut into nsplit splits of
+// split_len keys, into the device's scratch and runs the fp32 decode (and the
+// split merge) on it; base carries everything else (q, slabs, table, out,
+// geometry). hipErrorNotInitialized if the device's address was not fetched,
+// hipErrorInvalidValue if the plan does not fit.
+hipError_t LaunchSingleRowStatic(const DecodeParams& base, int device, int32_t length,
+                                 int32_t split_len, int32_t nsplit, QueueState* queue,
+                                 hipStream_t stream);
+
 hipError_t LaunchFillNormal(void* dst, int64_t n, int dtype, float mean, float stddev,
                             uint64_t seed, hipStream_t stream);
 

@@ -101,6 +101,20 @@ int32_t ChooseSplitTokens(const ehip_geometry& g, int64_t unit_tokens) {
   return static_cast<int32_t>(std::min<int64_t>(s, max_split));
 }
 
+int32_t RowSplitTokens(const ehip_geometry& g, int32_t base, int32_t len) {
+  int32_t sl = base;
+  if ((len + sl - 1) / sl > kMaxSplitsPerRow) {
+    const int64_t want = RoundUp((len + kMaxSplitsPerRow - 1) / kMaxSplitsPerRow, kTile);
+    sl = static_cast<int32_t>(std::min<int64_t>(want, MaxSplitTokens(g)));
+  }
+  return sl;
+}
+
+int32_t SingleRowSplitTokens(const ehip_geometry& g, int64_t length) {
+  const int32_t base = ChooseSplitTokens(g, length * g.kv_heads);
+  return RowSplitTokens(g, base, static_cast<int32_t>(length));
+}
+
 namespace {
 
 constexpr int32_t kMinJointTokens = 128;  // shorter shared runs are not worth a joint pass
@@ -129,7 +143,6 @@ struct KeyRange {
 void FinishPlan(const ehip_geometry& g, Plan* plan, bool allow_joint,
                 const std::vector<int32_t>* skip = nullptr) {
   const int32_t bs = g.block_size;
-  const int32_t max_split = MaxSplitTokens(g);
   const size_t n = plan->rows.size();
   auto skipped = [&](size_t r) { return skip && (*skip)[r] > 0; };
   int64_t units = 0;
@@ -169,16 +182,8 @@ void FinishPlan(const ehip_geometry& g, Plan* plan, bool allow_joint,
   }
 
   // Split length per row (a group's members use the larger of the two).
-  auto row_split = [&](int32_t len) {
-    int32_t sl = base;
-    if ((len + sl - 1) / sl > kMaxSplitsPerRow) {
-      const int64_t want = RoundUp((len + kMaxSplitsPerRow - 1) / kMaxSplitsPerRow, kTile);
-      sl = static_cast<int32_t>(std::min<int64_t>(want, max_split));
-    }
-    return sl;
-  };
   std::vector<int32_t> split_len(n);
-  for (size_t r = 0; r < n; ++r) split_len[r] = row_split(plan->rows[r].length);
+  for (size_t r = 0; r < n; ++r) split_len[r] = RowSplitTokens(g, base, plan->rows[r].length);
   for (size_t k = 0; k < plan->groups.size(); k += kMaxJointRows) {
     const int32_t a = plan->groups[k], b = plan->groups[k + 1];
     split_len[a] = split_len[b] = std::max(split_len[a], split_len[b]);

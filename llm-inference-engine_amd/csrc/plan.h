@@ -121,6 +121,13 @@ int64_t BlockStride(const ehip_geometry& g);
 int32_t ChooseSplitTokens(const ehip_geometry& g, int64_t unit_tokens);
 // Longest key range of one decode work item.
 int32_t MaxSplitTokens(const ehip_geometry& g);
+// Split length of one row of `len` keys given the step's base length: the
+// base, grown (in whole 64-key units, up to MaxSplitTokens) so the row has at
+// most 64 splits while the cap allows.
+int32_t RowSplitTokens(const ehip_geometry& g, int32_t base, int32_t len);
+// The split length BuildSingleRowPlan gives a row of `length` keys (the
+// single-sequence decode's partition), without building the plan.
+int32_t SingleRowSplitTokens(const ehip_geometry& g, int64_t length);
 
 // Validates the step (lengths, CSR offsets, every table id and slot in range)
 // and builds the plan. Chunks of at least kMinPrefillRows rows go to the MFMA
