@@ -1,15 +1,21 @@
 // BlockPool: the paged KV cache's block allocator over per-layer K/V slabs.
 //
-// Same interface and semantics as the reference's kvcache::BlockPool
-// (src/kvcache/block_pool.h:62-199, .cpp:28-339): 2·L slabs of
-// [num_blocks, Hkv, bs, d], 256-byte aligned and zero-filled; a LIFO free
-// list seeded so the first Allocate returns block 0; refcounts with Share /
-// Release (sharing a free block or releasing one twice aborts); occupancy
-// stats; the capacity arithmetic the engine sizes the pool with. Two
-// differences: the slabs may be bf16 (the reference pool is fp32-only,
-// block_pool.cpp:41-46; bf16 storage follows its Fp32ToBf16Bits rounding), and
-// Create returns a heap-pinned pool (unique_ptr) instead of a move-once value,
-// because a BlockTable holds a raw pointer to its pool.
+// Interface and observable behaviour follow the reference's kvcache::BlockPool
+// (src/kvcache/block_pool.h:62-199; semantics in
+// docs/design/paged-kv-cache.md): 2·L slabs of [num_blocks, Hkv, bs, d],
+// 256-byte aligned and zero-filled; allocation is last-freed-first with the
+// first allocation returning block 0; blocks carry reference counts
+// (Share/Release; sharing a free block, releasing a free one or naming a
+// block outside the pool aborts); occupancy statistics; the capacity
+// arithmetic the engine sizes a pool with.
+//
+// This pool is built for HBM: every slab of every layer lives in one arena
+// (one device allocation, slab i at i·slab_stride), and the free blocks form
+// an intrusive chain through a per-block link array rather than a separate
+// stack. AllocateRun takes several blocks all-or-nothing for a table's
+// growth. Slabs may be bf16 (stored with the reference's Fp32ToBf16Bits
+// rounding); the reference pool is fp32-only. Create returns the pool on the
+// heap (unique_ptr), because tables keep a raw pointer to it.
 #pragma once
 
 #include <cstdint>
@@ -34,14 +40,14 @@ struct CacheGeometry {
   KvDtype dtype = KvDtype::kFloat32;
 };
 
-// kvcache::BlockPoolStats (block_pool.h:52-60): used + free == total.
+// kvcache::BlockPoolStats (src/kvcache/block_pool.h:52-60): used + free == total.
 struct BlockPoolStats {
   int64_t total = 0;
   int64_t used = 0;
   int64_t free = 0;
   double utilization = 0.0;  // used / total
-  int64_t peak_used = 0;     // high-water mark of used since Create
-  int64_t exhaustions = 0;   // Allocate() calls that found the free list empty
+  int64_t peak_used = 0;     // most blocks ever held at once since Create
+  int64_t exhaustions = 0;   // allocation requests refused for lack of blocks
   int block_size = 0;
 };
 
@@ -57,9 +63,9 @@ class BlockPool {
   static StatusOr<int64_t> NumBlocksForBudget(const CacheGeometry& geom, int block_size,
                                               int64_t kv_budget_bytes);
 
-  // Allocates the 2·L slabs from `allocator` (non-null; the pool does not own
-  // it and it must outlive the pool). block_size ∈ {8,16,32,64}; num_blocks in
-  // [1, 2^31) because block ids are int32.
+  // Takes the slab arena from `allocator` (non-null; not owned, must outlive
+  // the pool). block_size in {8, 16, 32, 64}; num_blocks in [1, 2^31) (block
+  // ids are int32).
   static StatusOr<std::unique_ptr<BlockPool>> Create(CacheGeometry geom, int block_size,
                                                      int64_t num_blocks,
                                                      SlabAllocator* allocator);
@@ -68,26 +74,30 @@ class BlockPool {
   BlockPool& operator=(const BlockPool&) = delete;
   ~BlockPool();
 
-  // Pops the free list (LIFO), refcount 1. ResourceExhausted when empty.
+  // One block, refcount 1; ResourceExhausted when none is free.
   StatusOr<int32_t> Allocate();
-  // refcount += 1; aborts on an out-of-range or free block.
+  // n >= 0 blocks appended to *out (each refcount 1, in the order Allocate
+  // would return them), or none at all and ResourceExhausted.
+  Status AllocateRun(int64_t n, std::vector<int32_t>* out);
+  // refcount + 1; aborts on a block outside the pool or a free block.
   void Share(int32_t block);
-  // refcount -= 1, 1 -> 0 returns the block to the free list; aborts on an
-  // out-of-range or free block (double free).
+  // refcount - 1; at 0 the block becomes the next one handed out. Aborts on a
+  // block outside the pool or a free block.
   void Release(int32_t block);
 
   int32_t refcount(int32_t block) const;
   BlockPoolStats stats() const;
   int64_t free_blocks() const;
-  // ceil((cur+add)/bs) - ceil(cur/bs); aborts on negative arguments.
+  // Blocks a sequence of cur tokens must add to hold add more:
+  // ceil((cur + add) / bs) - ceil(cur / bs). Aborts on negative counts.
   int64_t blocks_needed(int64_t cur_tokens, int64_t add_tokens) const;
 
   // Slab base pointers (device memory for an HBM allocator).
   void* k_slab(int layer) const;
   void* v_slab(int layer) const;
-  int64_t block_stride() const { return block_stride_; }  // Hkv·bs·d elements
-  int64_t head_stride() const { return head_stride_; }    // bs·d
-  int64_t row_stride() const { return row_stride_; }      // d
+  int64_t block_stride() const { return int64_t{geom_.num_kv_heads} * block_size_ * geom_.head_dim; }
+  int64_t head_stride() const { return int64_t{block_size_} * geom_.head_dim; }
+  int64_t row_stride() const { return geom_.head_dim; }
 
   const CacheGeometry& geometry() const { return geom_; }
   int block_size() const { return block_size_; }
@@ -97,27 +107,31 @@ class BlockPool {
   bool device_resident() const { return allocator_->device(); }
 
  private:
+  static constexpr int32_t kNoBlock = -1;
+
   BlockPool(CacheGeometry geom, int block_size, int64_t num_blocks, int64_t slab_bytes,
             SlabAllocator* allocator);
-  bool in_range(int32_t block) const { return block >= 0 && block < num_blocks_; }
+  void* slab(int index) const;
+  void CheckHeld(int32_t block, const char* op) const;  // mu_ held
+  int32_t PopFree();                                    // mu_ held, chain non-empty
+  void PushFree(int32_t block);                         // mu_ held
 
-  CacheGeometry geom_;
-  int block_size_;
-  int64_t num_blocks_;
-  int64_t slab_bytes_;
-  int64_t block_stride_;
-  int64_t head_stride_;
-  int64_t row_stride_;
-  SlabAllocator* allocator_;
-  std::vector<void*> k_slabs_;
-  std::vector<void*> v_slabs_;
+  const CacheGeometry geom_;
+  const int block_size_;
+  const int64_t num_blocks_;
+  const int64_t slab_bytes_;
+  const int64_t slab_stride_;  // slab_bytes_ rounded up to kSlabAlignment
+  SlabAllocator* const allocator_;
+  void* arena_ = nullptr;
 
   mutable std::mutex mu_;
-  std::vector<int32_t> refcount_;
-  std::vector<int32_t> free_list_;  // top = back
-  int64_t used_ = 0;
-  int64_t peak_used_ = 0;
-  int64_t exhaustions_ = 0;
+  // Per block: holders (0 = free) and, for a free block, the next free block.
+  std::vector<int32_t> holders_;
+  std::vector<int32_t> next_free_;
+  int32_t free_head_ = kNoBlock;
+  int64_t free_count_ = 0;
+  int64_t high_water_ = 0;
+  int64_t refused_ = 0;
 };
 
 }  // namespace ehip::host

@@ -8,74 +8,71 @@
 namespace ehip::host {
 
 PagedKvCache::PagedKvCache(BlockPool* pool, ehip_ctx* ctx) : pool_(pool), ctx_(ctx), table_(pool) {
-  EHIP_CHECK(pool_ != nullptr, "PagedKvCache: pool must not be null");
+  EHIP_CHECK(pool_ != nullptr, "a paged cache needs a pool");
 }
 
 int64_t PagedKvCache::capacity() const {
-  const int64_t bs = pool_->block_size();
-  return table_.num_blocks() * bs + pool_->free_blocks() * bs;
+  return (table_.num_blocks() + pool_->free_blocks()) * pool_->block_size();
 }
 
 Status PagedKvCache::RequireDevice(const char* what) const {
-  if (!pool_->device_resident() || ctx_ == nullptr)
-    return Error(StatusCode::kFailedPrecondition,
-                 Format("PagedKvCache::%s: needs an HBM-resident pool and a device context", what));
-  return Status::Ok();
+  if (pool_->device_resident() && ctx_ != nullptr) return Status::Ok();
+  return Error(StatusCode::kFailedPrecondition,
+               Format("%s runs on the device: the pool must be in HBM and a context given", what));
 }
 
 Status PagedKvCache::append(int layer, const float* d_k, const float* d_v, int64_t t_dim) {
   const CacheGeometry& g = pool_->geometry();
   if (!layer_in_range(layer))
     return Error(StatusCode::kInvalidArgument,
-                 Format("PagedKvCache::append: layer %d out of range [0, %d)", layer,
-                        g.num_layers));
+                 Format("append: the cache has layers 0..%d, not %d", g.num_layers - 1, layer));
   if (d_k == nullptr || d_v == nullptr || t_dim < 1)
     return Error(StatusCode::kInvalidArgument,
-                 Format("PagedKvCache::append: k/v must be non-null [T>=1, %d, %d] rows, T=%lld",
-                        g.num_kv_heads, g.head_dim, static_cast<long long>(t_dim)));
+                 Format("append: needs K and V rows of at least one token (T=%lld)",
+                        static_cast<long long>(t_dim)));
   if (Status s = RequireDevice("append"); !s.ok()) return s;
-  if (layer != next_layer_)
+  if (layer != fwd_.layers_written)
     return Error(StatusCode::kInvalidArgument,
-                 Format("PagedKvCache::append: expected layer %d next (append in layer order, "
-                        "once per layer per forward), got %d",
-                        next_layer_, layer));
+                 Format("append: layer %d arrived while this forward expects layer %d (each "
+                        "forward writes layers 0, 1, ... once each)",
+                        layer, fwd_.layers_written));
   if (layer == 0) {
+    // A new forward: grow the table (all-or-nothing) and publish its slots.
     StatusOr<std::vector<int64_t>> grown = table_.AppendTokens(t_dim);
     if (!grown.ok()) {
-      pending_slots_.clear();
+      fwd_ = Forward{};
       return grown.status();
     }
-    pending_slots_ = std::move(*grown);
+    fwd_.slots = std::move(*grown);
     table_dirty_ = true;
-    if (Status s = d_slots_.Upload(ctx_, pending_slots_.data(),
+    if (Status s = d_slots_.Upload(ctx_, fwd_.slots.data(),
                                    t_dim * static_cast<int64_t>(sizeof(int64_t)));
         !s.ok())
       return s;
-  } else if (t_dim != static_cast<int64_t>(pending_slots_.size())) {
+  } else if (t_dim != static_cast<int64_t>(fwd_.slots.size())) {
     return Error(StatusCode::kInvalidArgument,
-                 Format("PagedKvCache::append: layer %d T (%lld) must match this forward's token "
-                        "batch (%zu from layer 0)",
-                        layer, static_cast<long long>(t_dim), pending_slots_.size()));
+                 Format("append: layer %d brings %lld tokens but this forward appends %zu",
+                        layer, static_cast<long long>(t_dim), fwd_.slots.size()));
   }
   const auto* slots = static_cast<const int64_t*>(d_slots_.get());
+  const int bs = pool_->block_size();
   Status s = g.dtype == KvDtype::kBFloat16
                  ? kernels::KvScatterBf16(ctx_, d_k, d_v, slots, t_dim, g.num_kv_heads, g.head_dim,
-                                          pool_->block_size(), pool_->num_blocks(),
+                                          bs, pool_->num_blocks(),
                                           static_cast<uint16_t*>(pool_->k_slab(layer)),
                                           static_cast<uint16_t*>(pool_->v_slab(layer)))
                  : kernels::KvScatterF32(ctx_, d_k, d_v, slots, t_dim, g.num_kv_heads, g.head_dim,
-                                         pool_->block_size(), pool_->num_blocks(),
+                                         bs, pool_->num_blocks(),
                                          static_cast<float*>(pool_->k_slab(layer)),
                                          static_cast<float*>(pool_->v_slab(layer)));
   if (!s.ok()) return s;
-  next_layer_ = (layer + 1) % g.num_layers;
+  if (++fwd_.layers_written == g.num_layers) fwd_.layers_written = 0;  // forward complete
   return Status::Ok();
 }
 
 int64_t PagedKvCache::visible_length(int layer) const {
-  const int64_t committed = table_.num_tokens();
-  const bool written = next_layer_ == 0 || layer < next_layer_;
-  return written ? committed : committed - static_cast<int64_t>(pending_slots_.size());
+  const bool pending = fwd_.layers_written > 0 && layer >= fwd_.layers_written;
+  return table_.num_tokens() - (pending ? static_cast<int64_t>(fwd_.slots.size()) : 0);
 }
 
 Status PagedKvCache::SyncDeviceTable() const {
@@ -93,12 +90,11 @@ Status PagedKvCache::SyncDeviceTable() const {
 
 Status PagedKvCache::view(int layer, float* d_out_k, float* d_out_v) const {
   if (!layer_in_range(layer))
-    return Error(StatusCode::kInvalidArgument,
-                 Format("PagedKvCache::view: layer %d out of range", layer));
+    return Error(StatusCode::kInvalidArgument, Format("view: no layer %d", layer));
   if (Status s = RequireDevice("view"); !s.ok()) return s;
   const CacheGeometry& g = pool_->geometry();
   if (g.dtype != KvDtype::kFloat32)
-    return Error(StatusCode::kUnimplemented, "PagedKvCache::view: the gather reads f32 slabs");
+    return Error(StatusCode::kUnimplemented, "view: the contiguous gather reads f32 slabs");
   const int64_t len = visible_length(layer);
   if (len == 0) return Status::Ok();
   if (Status s = SyncDeviceTable(); !s.ok()) return s;
@@ -111,8 +107,7 @@ Status PagedKvCache::view(int layer, float* d_out_k, float* d_out_v) const {
 
 StatusOr<PagedKvView> PagedKvCache::paged_view(int layer) const {
   if (!layer_in_range(layer))
-    return Error(StatusCode::kInvalidArgument,
-                 Format("PagedKvCache::paged_view: layer %d out of range", layer));
+    return Error(StatusCode::kInvalidArgument, Format("paged_view: no layer %d", layer));
   PagedKvView v;
   if (pool_->device_resident() && ctx_ != nullptr) {
     if (Status s = SyncDeviceTable(); !s.ok()) return s;
@@ -132,22 +127,21 @@ StatusOr<PagedKvView> PagedKvCache::paged_view(int layer) const {
 
 Status PagedKvCache::truncate(int64_t new_length) {
   if (Status s = table_.Truncate(new_length); !s.ok()) return s;
-  pending_slots_.clear();
-  next_layer_ = 0;
+  fwd_ = Forward{};
   table_dirty_ = true;
   return Status::Ok();
 }
 
 StatusOr<const std::vector<int64_t>*> PagedKvCache::Grow(int64_t t_dim) {
-  if (next_layer_ != 0)
+  if (fwd_.layers_written != 0)
     return Error(StatusCode::kFailedPrecondition,
-                 Format("PagedKvCache::Grow: a per-layer forward is in progress (next layer %d)",
-                        next_layer_));
+                 Format("Grow: a layer-by-layer forward is open (%d layers written)",
+                        fwd_.layers_written));
   StatusOr<std::vector<int64_t>> grown = table_.AppendTokens(t_dim);
   if (!grown.ok()) return grown.status();
-  pending_slots_ = std::move(*grown);
+  fwd_.slots = std::move(*grown);
   table_dirty_ = true;
-  return &pending_slots_;
+  return &fwd_.slots;
 }
 
 Status PagedKvCache::ForkFrom(const PagedKvCache& parent, int64_t tokens) {

@@ -1,17 +1,18 @@
 // PagedKvCache: one sequence's KV cache over a device-resident BlockPool.
 //
-// The reference's kvcache::PagedKvCache (src/kvcache/paged_cache.h:47-129,
-// .cpp:62-168) and its per-forward layer protocol: append(layer, k, v) must
-// come in layer order once per layer; layer 0 grows the block table by T
-// tokens and every later layer of the same forward writes the same slots.
-// paged_view(layer) exposes the slab pointers, the table, its length and the
-// block stride; view(layer) gathers a contiguous [Hkv, len, d] copy (only the
-// layers already written in the current forward see its new tokens).
+// The per-forward layer protocol of the reference's kvcache::PagedKvCache
+// (src/kvcache/paged_cache.h:47-129): a forward appends its T new tokens to
+// every layer, in layer order, once per layer. The first layer's append grows
+// the block table by T tokens; the later layers write the same slots. Until a
+// layer has been written in the current forward, it does not see the new
+// tokens (visible_length). paged_view(layer) exposes the slab pointers, the
+// table, its length and the block stride; view(layer) gathers a contiguous
+// [Hkv, len, d] copy.
 //
 // K/V rows arrive as device pointers ([T, Hkv, d] fp32, token-major) and are
 // written by the device scatter kernel; bf16 slabs store RNE-narrowed bits.
-// The batched step path (BatchAssembler) grows every sequence of a step before
-// layer 0 through Grow(); the cache's own append then stays unused for it.
+// The batched step path (BatchAssembler) grows every sequence of a step once
+// through Grow(), and the step's own append kernel writes all layers.
 #pragma once
 
 #include <cstdint>
@@ -76,17 +77,22 @@ class PagedKvCache {
   BlockPool* pool() const { return pool_; }
 
  private:
-  bool layer_in_range(int layer) const {
-    return layer >= 0 && layer < pool_->geometry().num_layers;
-  }
+  int num_layers() const { return pool_->geometry().num_layers; }
+  bool layer_in_range(int layer) const { return layer >= 0 && layer < num_layers(); }
   Status RequireDevice(const char* what) const;
   Status SyncDeviceTable() const;
+  // The forward in progress: the slots its layer-0 append took, and how many
+  // layers (from layer 0 up) it has written. layers_written == 0: no forward
+  // is open (a finished forward closes itself).
+  struct Forward {
+    std::vector<int64_t> slots;
+    int layers_written = 0;
+  };
 
   BlockPool* pool_;
   ehip_ctx* ctx_;
   BlockTable table_;
-  std::vector<int64_t> pending_slots_;
-  int next_layer_ = 0;
+  Forward fwd_;
   DeviceBuffer d_slots_;
   mutable DeviceBuffer d_table_;
   mutable bool table_dirty_ = true;

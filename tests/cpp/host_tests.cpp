@@ -297,11 +297,11 @@ TEST_CPU(AppendTokensAllOrNothing) {
   EXPECT_EQ(after.exhaustions, before.exhaustions + 1);
   EXPECT_EQ(t.num_tokens(), 20);
   EXPECT(t.blocks() == blocks);
-  // The blocks taken (2, then 3) were released in that order, so the stack
-  // now yields 3 first.
+  // The refused growth took nothing from the pool, so the free order is the
+  // one before it: 2, then 3.
   ASSERT_OK(t.AppendTokens(44).status());  // exactly 4 blocks
-  EXPECT_EQ(t.blocks()[2], 3);
-  EXPECT_EQ(t.blocks()[3], 2);
+  EXPECT_EQ(t.blocks()[2], 2);
+  EXPECT_EQ(t.blocks()[3], 3);
 }
 
 TEST_CPU(TruncateKeepsPartialTailReleasesTailFirst) {
