@@ -201,6 +201,19 @@ int ehip_paged_decode_attention_f32(ehip_ctx* ctx, const float* d_q, const float
                                     int64_t block_stride, int64_t slab_blocks, float scale,
                                     float* d_out);
 
+/* kernels::PrefillAttentionF32 (src/kernels/attention.h:40-43): causal
+ * attention of T query rows at positions L-T .. L-1 over a contiguous cache,
+ * q/out [T, H, d], k/v [Hkv, L, d] head-major (kv head hk at hk*L*d). fp32. */
+int ehip_prefill_attention_f32(ehip_ctx* ctx, const float* d_q, const float* d_k,
+                               const float* d_v, float* d_out, int64_t t_dim, int64_t heads,
+                               int64_t kv_heads, int64_t d, int64_t l_dim, float scale);
+/* kernels::DecodeAttentionF32 (src/kernels/attention.h:71-73): the T = 1 case,
+ * q/out [H, d], k/v [Hkv, L, d]. fp32. Both read the contiguous cache through
+ * the paged kernels (an identity table over 16-key runs of each kv head). */
+int ehip_decode_attention_f32(ehip_ctx* ctx, const float* d_q, const float* d_k, const float* d_v,
+                              float* d_out, int64_t heads, int64_t kv_heads, int64_t d,
+                              int64_t l_dim, float scale);
+
 /* No counterpart in the reference: the allocation-free variant of
  * ehip_paged_decode_attention_f32 (same arguments and results), for callers
  * that cannot allocate device memory — code under HIP graph capture, tight

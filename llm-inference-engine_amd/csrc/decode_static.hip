@@ -101,6 +101,7 @@ hipError_t LaunchSingleRowStatic(const DecodeParams& base, int device, int32_t l
   p.n_joint = 0;
   p.max_length = length;
   p.has_prefill = 0;
+  p.head_stride = int64_t{base.bs} * base.d;
   return LaunchDecode(p, EHIP_KV_F32, queue, stream);
 }
 

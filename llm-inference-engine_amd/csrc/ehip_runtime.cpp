@@ -41,6 +41,7 @@ struct ehip_ctx {
 
   // The uploaded step.
   bool have_step = false;
+  int64_t head_stride = 0;  // kv-head stride inside a block (0: bs * d)
   ehip_geometry geom{};
   ehip::Plan plan;
   const ehip::RowDesc* d_rows = nullptr;
@@ -106,7 +107,8 @@ int EnsureWorkspace(ehip_ctx* ctx, const ehip_geometry& g, const Plan& plan) {
 
 // Packs rows | items | table ids | slots into one pinned staging buffer and
 // uploads it with one async copy; records the device pointers of each part.
-int UploadPlan(ehip_ctx* ctx, const ehip_geometry& g, Plan&& plan, const int32_t* d_user_table) {
+int UploadPlan(ehip_ctx* ctx, const ehip_geometry& g, Plan&& plan, const int32_t* d_user_table,
+               int64_t head_stride = 0) {
   const size_t rows_b = Align256(plan.rows.size() * sizeof(ehip::RowDesc));
   const size_t items_b = Align256(plan.items.size() * sizeof(ehip::WorkItem));
   const size_t prefill_b = Align256(plan.prefill.size() * sizeof(ehip::PrefillItem));
@@ -174,6 +176,7 @@ int UploadPlan(ehip_ctx* ctx, const ehip_geometry& g, Plan&& plan, const int32_t
   ctx->geom = g;
   ctx->plan = std::move(plan);
   ctx->have_step = true;
+  ctx->head_stride = head_stride != 0 ? head_stride : int64_t{g.block_size} * g.head_dim;
   return EHIP_OK;
 }
 
@@ -232,6 +235,7 @@ int LaunchAttention(ehip_ctx* ctx, const float* q, const void* k_slab, const voi
   p.part_ml = ctx->d_part + static_cast<size_t>(plan.partials) * grp * g.head_dim;
   p.err = ctx->d_err;
   p.block_stride = ehip::BlockStride(g);
+  p.head_stride = ctx->head_stride;
   p.slab_blocks = g.slab_blocks;
   p.n_items = static_cast<int32_t>(plan.items.size());
   p.n_rows = static_cast<int32_t>(plan.rows.size());
@@ -599,6 +603,7 @@ int ehip_paged_decode_attention_f32_noalloc(ehip_ctx* ctx, const float* d_q,
   p.table = d_block_table;
   p.err = ctx->d_err;
   p.block_stride = ehip::BlockStride(g);
+  p.head_stride = int64_t{g.block_size} * g.head_dim;
   p.slab_blocks = g.slab_blocks;
   p.heads = g.heads;
   p.kv_heads = g.kv_heads;
@@ -610,6 +615,55 @@ int ehip_paged_decode_attention_f32_noalloc(ehip_ctx* ctx, const float* d_q,
                                             split_len, static_cast<int32_t>(nsplit), &ctx->queue,
                                             ctx->stream));
   return EHIP_OK;
+}
+
+namespace {
+// kernels::PrefillAttentionF32 / DecodeAttentionF32 over a contiguous
+// [Hkv, L, d] cache: one sequence whose "blocks" are consecutive 16-row runs
+// of each kv head (identity table, block stride 16 d, kv-head stride L d),
+// planned and launched like any step with T rows at the end of L keys.
+int ContiguousAttention(ehip_ctx* ctx, const float* d_q, const float* d_k, const float* d_v,
+                        float* d_out, int64_t t_dim, int64_t heads, int64_t kv_heads, int64_t d,
+                        int64_t l_dim, float scale) {
+  if (int rc = CheckCtx(ctx)) return rc;
+  if (heads < 1 || kv_heads < 1 || d < 1 || heads > INT32_MAX || kv_heads > INT32_MAX ||
+      d > INT32_MAX || heads % kv_heads != 0)
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "heads=%lld kv_heads=%lld d=%lld invalid",
+                    static_cast<long long>(heads), static_cast<long long>(kv_heads),
+                    static_cast<long long>(d));
+  if (t_dim < 1 || l_dim < t_dim || l_dim > (int64_t{1} << 30))
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "need 1 <= T (%lld) <= L (%lld) <= 2^30",
+                    static_cast<long long>(t_dim), static_cast<long long>(l_dim));
+  if (!d_q || !d_k || !d_v || !d_out)
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "null attention operand");
+  constexpr int32_t kRun = 16;
+  const int64_t nblk = (l_dim + kRun - 1) / kRun;
+  const ehip_geometry g{static_cast<int32_t>(heads), static_cast<int32_t>(kv_heads),
+                        static_cast<int32_t>(d), kRun, EHIP_KV_F32, 0, nblk, kRun * d, scale};
+  std::vector<int32_t> ids(static_cast<size_t>(nblk));
+  for (int64_t i = 0; i < nblk; ++i) ids[static_cast<size_t>(i)] = static_cast<int32_t>(i);
+  const int32_t qlen = static_cast<int32_t>(t_dim);
+  const int32_t offsets[2] = {0, static_cast<int32_t>(nblk)};
+  const ehip_step_desc s{1, 0, &qlen, &l_dim, offsets, ids.data(), nullptr};
+  Plan plan;
+  std::string err;
+  if (int rc = ehip::BuildPlan(g, s, &plan, &err, 0, /*head_major=*/true))
+    return SetError(ctx, rc, "%s", err.c_str());
+  if (int rc = UploadPlan(ctx, g, std::move(plan), nullptr, l_dim * d)) return rc;
+  return LaunchAttention(ctx, d_q, d_k, d_v, d_out);
+}
+}  // namespace
+
+int ehip_prefill_attention_f32(ehip_ctx* ctx, const float* d_q, const float* d_k,
+                               const float* d_v, float* d_out, int64_t t_dim, int64_t heads,
+                               int64_t kv_heads, int64_t d, int64_t l_dim, float scale) {
+  return ContiguousAttention(ctx, d_q, d_k, d_v, d_out, t_dim, heads, kv_heads, d, l_dim, scale);
+}
+
+int ehip_decode_attention_f32(ehip_ctx* ctx, const float* d_q, const float* d_k, const float* d_v,
+                              float* d_out, int64_t heads, int64_t kv_heads, int64_t d,
+                              int64_t l_dim, float scale) {
+  return ContiguousAttention(ctx, d_q, d_k, d_v, d_out, 1, heads, kv_heads, d, l_dim, scale);
 }
 
 namespace {

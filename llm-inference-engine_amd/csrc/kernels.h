@@ -28,6 +28,9 @@ struct DecodeParams {
   float* part_ml;           // [partials, g, 2]
   int32_t* err;
   int64_t block_stride;     // elements
+  int64_t head_stride;      // elements between kv heads of a block (bs * d for slabs; L * d
+                            // for a contiguous [Hkv, L, d] cache read as one identity table);
+                            // the fp32 kernels honour it, the bf16/INT8 ones assume bs * d
   int64_t slab_blocks;
   int32_t n_items;
   int32_t n_rows;

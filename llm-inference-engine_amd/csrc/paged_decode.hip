@@ -117,8 +117,8 @@ __device__ __forceinline__ void DecodeValuRow(const DecodeParams& p, int row, in
 
   const int lb0 = tb / bs;
   const int tab = LoadRangeTable(p, table_off, tb, te, lane);
-  const KV* kbase = static_cast<const KV*>(p.k_slab) + int64_t{hk} * bs * D;
-  const KV* vbase = static_cast<const KV*>(p.v_slab) + int64_t{hk} * bs * D;
+  const KV* kbase = static_cast<const KV*>(p.k_slab) + int64_t{hk} * p.head_stride;
+  const KV* vbase = static_cast<const KV*>(p.v_slab) + int64_t{hk} * p.head_stride;
   const int lane_off = (tl * D + sub * EPV) * static_cast<int>(sizeof(KV));
 
   float m[G], l[G], o[G][E];
@@ -389,8 +389,8 @@ __device__ void DecodeGenericRow(const DecodeParams& p, int row, int hk, int tb,
   const int lane = threadIdx.x & 63;
   const RowDesc rd = p.rows[row];
   const int g = p.group, d = p.d, bs = p.bs;
-  const KV* kslab = static_cast<const KV*>(p.k_slab) + int64_t{hk} * bs * d;
-  const KV* vslab = static_cast<const KV*>(p.v_slab) + int64_t{hk} * bs * d;
+  const KV* kslab = static_cast<const KV*>(p.k_slab) + int64_t{hk} * p.head_stride;
+  const KV* vslab = static_cast<const KV*>(p.v_slab) + int64_t{hk} * p.head_stride;
   const int64_t pidx = PartialIndex(rd, p.kv_heads, hk, split);
 
   for (int h0 = 0; h0 < g; h0 += HC) {

@@ -306,8 +306,14 @@ int BuildQ8Groups(const ehip_geometry& g, Plan* plan, std::string* err) {
 }  // namespace
 
 int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::string* err,
-              int prefill_rows) {
-  if (int rc = ValidateGeometry(g, err)) return rc;
+              int prefill_rows, bool head_major) {
+  ehip_geometry checked = g;
+  if (head_major) {
+    if (g.block_stride != int64_t{g.block_size} * g.head_dim)
+      return Fail(err, EHIP_INVALID_ARGUMENT, "a head-major cache has block_stride = bs * d");
+    checked.block_stride = 0;
+  }
+  if (int rc = ValidateGeometry(checked, err)) return rc;
   if (s.num_seqs < 0) return Fail(err, EHIP_INVALID_ARGUMENT, "num_seqs=%lld < 0", s.num_seqs);
   if (s.reserved != 0) return Fail(err, EHIP_INVALID_ARGUMENT, "reserved field must be 0");
   plan->rows.clear();

@@ -138,8 +138,11 @@ constexpr int32_t kMinPrefillRows = 16;
 constexpr int32_t kPrefillTile = 32;       // keys per prefill tile
 constexpr int32_t kPrefillSlots = 512;     // workgroups resident at once (2 per CU)
 constexpr int32_t kMinPrefillSplitTiles = 8;
+// head_major: K/V are one contiguous [Hkv, L, d] cache read through an
+// identity table (block_stride = bs * d, kv heads L * d apart), so the slab
+// rule block_stride >= Hkv * bs * d does not apply.
 int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::string* err,
-              int prefill_rows = 0);
+              int prefill_rows = 0, bool head_major = false);
 
 // Plan for one row reading a device-resident table (single-sequence paged
 // decode): one row of `length` keys, table offset 0.

@@ -86,6 +86,10 @@ def lib():
             "ehip_kv_gather_f32": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp],
             "ehip_paged_decode_attention_f32": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
                                                 _i64, _i64, _i64, _i64, C.c_float, _vp],
+            "ehip_prefill_attention_f32": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
+                                           _i64, C.c_float],
+            "ehip_decode_attention_f32": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
+                                          C.c_float],
             "ehip_paged_decode_attention_f32_noalloc": [_vp, _vp, _vp, _vp, _vp, _i64, _i64,
                                                         _i64, _i64, _i64, _i64, _i64, _i64,
                                                         C.c_float, _vp],

@@ -34,6 +34,7 @@ def hip():
         h.hipGraphLaunch.argtypes = [vp, vp]
         h.hipGraphExecDestroy.argtypes = [vp]
         h.hipGraphDestroy.argtypes = [vp]
+        h.hipGraphExecUpdate.argtypes = [vp, vp, C.POINTER(vp), C.POINTER(C.c_int)]
         _hip = h
     return _hip
 
@@ -74,6 +75,27 @@ class Graph:
             _ok(hip().hipStreamEndCapture(stream.h, C.byref(self.graph)), "hipStreamEndCapture")
         _ok(hip().hipGraphInstantiate(C.byref(self.exec), self.graph, None, None, 0),
             "hipGraphInstantiate")
+        return self
+
+    def update(self, stream: Stream, fn):
+        """Re-capture what fn enqueues (the same launch sequence for a new step
+        plan) and write its kernel parameters into the instantiated graph
+        (hipGraphExecUpdate): no re-instantiation. Raises if the launch
+        topology changed (then capture() a new graph instead)."""
+        g = C.c_void_p()
+        _ok(hip().hipStreamBeginCapture(stream.h, _CAPTURE_THREAD_LOCAL), "hipStreamBeginCapture")
+        try:
+            fn()
+        finally:
+            _ok(hip().hipStreamEndCapture(stream.h, C.byref(g)), "hipStreamEndCapture")
+        err_node, result = C.c_void_p(), C.c_int(-1)
+        rc = hip().hipGraphExecUpdate(self.exec, g, C.byref(err_node), C.byref(result))
+        if rc != 0:
+            hip().hipGraphDestroy(g)
+            raise RuntimeError(f"hipGraphExecUpdate failed: hipError {rc}, update result "
+                               f"{result.value}")
+        hip().hipGraphDestroy(self.graph)
+        self.graph = g
         return self
 
     def replay(self, stream: Stream):

@@ -26,6 +26,7 @@
 #include "batch.h"
 #include "block_pool.h"
 #include "block_table.h"
+#include "dispatch.h"
 #include "ehip.h"
 #include "kernels.h"
 #include "oracle.h"
@@ -611,6 +612,110 @@ TEST_CPU(AssembleStagingIsStableAfterWarmup) {
   EXPECT_EQ(asmb.inputs().context_lens[0], 42);
 }
 
+// ----------------------------------------------------------------- dispatch
+
+std::vector<float> Normal(int64_t n, uint64_t seed) {
+  std::vector<float> v(static_cast<size_t>(n));
+  orc_fill_normal(v.data(), n, 0.0, 1.0, seed);
+  return v;
+}
+
+// The oracle's kernels behind the reference signatures (the role the
+// engine's own kernels::* functions play when it registers its CPU table).
+void OrcBatched(const float* q, const float* k, const float* v, const int32_t* const* tables,
+                const int64_t* lens, int64_t b, int64_t h, int64_t hkv, int64_t d, int64_t bs,
+                int64_t stride, float scale, float* out) {
+  orc_paged_decode_batched_f32(ORC_ISA_AVX2, q, k, v, tables, lens, b, h, hkv, d, bs, stride,
+                               scale, out);
+}
+void OrcSingle(const float* q, const float* k, const float* v, const int32_t* table, int64_t nb,
+               int64_t len, int64_t h, int64_t hkv, int64_t d, int64_t bs, int64_t stride,
+               float scale, float* out) {
+  orc_paged_decode_f32(ORC_ISA_AVX2, q, k, v, table, nb, len, h, hkv, d, bs, stride, scale, out);
+}
+
+TEST_CPU(DispatchParsesForcedIsa) {
+  using dispatch::Device;
+  EXPECT(!dispatch::ParseForced(nullptr).set);
+  EXPECT(!dispatch::ParseForced("").set);
+  const dispatch::Forced hip = dispatch::ParseForced("hip");
+  EXPECT(hip.set && hip.device == Device::kHip);
+  for (const char* isa : {"scalar", "neon", "avx2"}) {
+    const dispatch::Forced f = dispatch::ParseForced(isa);
+    EXPECT(f.set && f.device == Device::kCpu);
+  }
+  EXPECT_DEATH((void)dispatch::ParseForced("cuda"));  // fatal, not a fallback
+  EXPECT_DEATH((void)dispatch::ParseForced("HIP"));
+}
+
+TEST_CPU(DispatchResolvesByResidency) {
+  using dispatch::Device;
+  EXPECT(dispatch::Resolve({}, false) == Device::kCpu);
+  EXPECT(dispatch::Resolve({}, true) == Device::kHip);
+  EXPECT(dispatch::Resolve({true, Device::kHip}, true) == Device::kHip);
+  EXPECT(dispatch::Resolve({true, Device::kCpu}, false) == Device::kCpu);
+  EXPECT_DEATH((void)dispatch::Resolve({true, Device::kHip}, false));  // GPU cannot read host slabs
+  EXPECT_DEATH((void)dispatch::Resolve({true, Device::kCpu}, true));   // CPU cannot read HBM
+  auto pool = HostPool(4);
+  EXPECT(dispatch::Select(*pool) == Device::kCpu);
+}
+
+TEST_CPU(DispatchProcessForcedIsReadOnce) {
+  // The first call fixes the process-wide choice; a later change of the
+  // variable does not move it. (host_tests --forced shows the parse of the
+  // variable a fresh process starts with.)
+  const dispatch::Forced first = dispatch::ProcessForced();
+  setenv("ENGINE_FORCE_ISA", first.set ? "" : "hip", 1);
+  const dispatch::Forced again = dispatch::ProcessForced();
+  unsetenv("ENGINE_FORCE_ISA");
+  EXPECT(first.set == again.set && first.device == again.device);
+}
+
+TEST_CPU(DispatchCpuRouteRunsRegisteredKernels) {
+  const int L = 2, Hkv = 2, d = 16, bs = 8, H = 6, nb = 12;
+  auto pool = HostPool(nb, bs, L, Hkv, d);
+  std::vector<float> kn = Normal(3 * Hkv * d, 5), vn = Normal(3 * Hkv * d, 6);
+  std::vector<int64_t> slots = {3 * bs + 0, 3 * bs + 1, 7 * bs + 4};
+  dispatch::RegisterCpuKernels({});
+  EXPECT_CODE(dispatch::KvScatter(nullptr, *pool, 1, kn.data(), vn.data(), slots.data(), 3),
+              StatusCode::kUnimplemented);
+  dispatch::CpuKernels cpu;
+  cpu.paged_decode_f32 = OrcSingle;
+  cpu.paged_decode_batched_f32 = OrcBatched;
+  cpu.kv_scatter_f32 = orc_kv_scatter_f32;
+  dispatch::RegisterCpuKernels(cpu);
+  // Fill layer 1 through the dispatcher, then attend through it.
+  const size_t n = static_cast<size_t>(pool->slab_bytes() / 4);
+  std::vector<float> k1 = Normal(static_cast<int64_t>(n), 7), v1 = Normal(static_cast<int64_t>(n), 8);
+  std::memcpy(pool->k_slab(1), k1.data(), n * 4);
+  std::memcpy(pool->v_slab(1), v1.data(), n * 4);
+  ASSERT_OK(dispatch::KvScatter(nullptr, *pool, 1, kn.data(), vn.data(), slots.data(), 3));
+  orc_kv_scatter_f32(kn.data(), vn.data(), slots.data(), 3, Hkv, d, bs, k1.data(), v1.data());
+  EXPECT(std::memcmp(pool->k_slab(1), k1.data(), n * 4) == 0);
+  EXPECT(std::memcmp(pool->v_slab(1), v1.data(), n * 4) == 0);
+  const std::vector<int32_t> t0 = {3, 7, 1}, t1 = {5, 2};
+  const int32_t* tables[2] = {t0.data(), t1.data()};
+  const int64_t lens[2] = {21, 9};
+  std::vector<float> q = Normal(2 * H * d, 9), got(q.size()), want(q.size());
+  const float scale = kernels::AttentionScale(d);
+  ASSERT_OK(dispatch::PagedDecodeBatched(nullptr, *pool, 1, q.data(), tables, lens, 2, H, scale,
+                                         got.data()));
+  orc_paged_decode_batched_f32(ORC_ISA_AVX2, q.data(), k1.data(), v1.data(), tables, lens, 2, H,
+                               Hkv, d, bs, pool->block_stride(), scale, want.data());
+  EXPECT(std::memcmp(got.data(), want.data(), got.size() * 4) == 0);
+  ASSERT_OK(dispatch::PagedDecode(nullptr, *pool, 1, q.data(), t0.data(), 3, 21, H, scale,
+                                  got.data()));
+  EXPECT(std::memcmp(got.data(), want.data(), static_cast<size_t>(H * d) * 4) == 0);
+  // bf16 slabs have no CPU kernels (the reference pool is fp32).
+  StatusOr<std::unique_ptr<BlockPool>> bp =
+      BlockPool::Create(Geom(1, Hkv, d, KvDtype::kBFloat16), bs, 4, &g_host_alloc);
+  ASSERT_OK(bp.status());
+  EXPECT_CODE(dispatch::PagedDecodeBatched(nullptr, **bp, 0, q.data(), tables, lens, 1, H, scale,
+                                           got.data()),
+              StatusCode::kUnimplemented);
+  dispatch::RegisterCpuKernels({});
+}
+
 // --------------------------------------------------------------------- GPU
 
 struct Gpu {
@@ -623,12 +728,6 @@ struct Gpu {
   }
   ~Gpu() { ehip_destroy(ctx); }
 };
-
-std::vector<float> Normal(int64_t n, uint64_t seed) {
-  std::vector<float> v(static_cast<size_t>(n));
-  orc_fill_normal(v.data(), n, 0.0, 1.0, seed);
-  return v;
-}
 
 template <class T>
 std::vector<T> ToHost(ehip_ctx* ctx, const void* d, int64_t n) {
@@ -1023,11 +1122,228 @@ TEST_GPU(GpuCapturedLayersReplay) {
   unsetenv("EHIP_DECODE_SLOTS");
 }
 
+TEST_GPU(GpuPreemptThenReprefillLongContext) {
+  // Scheduler + BatchAssembler + BatchedAttention over a full bf16 pool:
+  //   step 0  prompts of A (4096 tokens), B (100), C (64), D (40) fill all
+  //           270 blocks;
+  //   step 1  A (latest arrival) and C cross into a new block with none free:
+  //           the scheduler preempts A (evict and recompute,
+  //           src/runtime/engine.cpp:419-430), its blocks return to the pool,
+  //           and B, C, D decode;
+  //   step 2  B and D have finished; A is readmitted as a 4096-token causal
+  //           chunk beside C's decode row (one step, one launch per layer).
+  // Decode rows against the oracle on the widened bf16 mirror (1e-4 relative
+  // per output vector); A's re-prefill rows, sampled (first, last and every
+  // 64th), against a single-row oracle decode over keys [0, t] (1e-2: bf16 Q
+  // and P on the matrix cores).
+  Gpu gpu;
+  HbmSlabAllocator hbm(gpu.ctx);
+  const int Hkv = 8, d = 128, bs = 16, H = 32;
+  StatusOr<std::unique_ptr<BlockPool>> pr =
+      BlockPool::Create(Geom(1, Hkv, d, KvDtype::kBFloat16), bs, 270, &hbm);
+  ASSERT_OK(pr.status());
+  BlockPool& pool = **pr;
+  BatchedAttention attn(gpu.ctx, &pool, H);
+  BatchAssembler asmb;
+  std::vector<PagedKvCache> caches;
+  caches.reserve(4);
+  for (int i = 0; i < 4; ++i) caches.emplace_back(&pool, gpu.ctx);
+  enum { A = 0, B = 1, C = 2, D = 3 };
+  const size_t slab_n = static_cast<size_t>(pool.slab_bytes() / 2);
+  std::vector<uint16_t> mk(slab_n, 0), mv(slab_n, 0);
+  uint64_t seed = 900;
+
+  // Runs one assembled step on the GPU, mirrors its append, returns q and the
+  // output (host).
+  auto run = [&](std::vector<float>* q_out) {
+    const BatchInputs& in = asmb.inputs();
+    const int64_t T = in.num_tokens();
+    std::vector<float> q = Normal(T * H * d, seed++), k = Normal(T * Hkv * d, seed++),
+                       v = Normal(T * Hkv * d, seed++);
+    DeviceBuffer dq = ToDevice(gpu.ctx, q), dk = ToDevice(gpu.ctx, k), dv = ToDevice(gpu.ctx, v),
+                 dout;
+    if (!dout.Reserve(gpu.ctx, T * H * d * 4).ok()) std::abort();
+    if (!attn.Upload(in).ok()) std::abort();
+    if (!attn.ForwardLayer(0, static_cast<float*>(dq.get()), static_cast<float*>(dk.get()),
+                           static_cast<float*>(dv.get()), static_cast<float*>(dout.get())).ok())
+      std::abort();
+    orc_kv_scatter_bf16(k.data(), v.data(), in.slot_mapping.data(), T, Hkv, d, bs, mk.data(),
+                        mv.data());
+    std::vector<float> got = ToHost<float>(gpu.ctx, dout.get(), T * H * d);
+    if (ehip_sync(gpu.ctx) != EHIP_OK) std::abort();
+    *q_out = std::move(q);
+    return got;
+  };
+  auto widen = [&](std::vector<float>* wk, std::vector<float>* wv) {
+    wk->resize(slab_n);
+    wv->resize(slab_n);
+    orc_bf16_to_fp32_array(mk.data(), wk->data(), static_cast<int64_t>(slab_n));
+    orc_bf16_to_fp32_array(mv.data(), wv->data(), static_cast<int64_t>(slab_n));
+  };
+  auto rel_vec = [&](const float* got, const float* want) {
+    double num = 0, den = 0;
+    for (int e = 0; e < d; ++e) {
+      num = std::max(num, std::fabs(double(got[e]) - want[e]));
+      den = std::max(den, std::fabs(double(want[e])));
+    }
+    return num / den;
+  };
+  // One decode row of sequence `s` against the oracle.
+  auto check_decode = [&](const std::vector<float>& q, const std::vector<float>& got, int64_t row,
+                          PagedKvCache& c, const std::vector<float>& wk,
+                          const std::vector<float>& wv) {
+    std::vector<float> want(static_cast<size_t>(H * d));
+    const std::vector<int32_t>& t = c.block_table().blocks();
+    orc_paged_decode_f32(ORC_ISA_AVX2, q.data() + row * H * d, wk.data(), wv.data(), t.data(),
+                         static_cast<int64_t>(t.size()), c.length(), H, Hkv, d, bs,
+                         pool.block_stride(), attn.scale(), want.data());
+    double worst = 0;
+    for (int h = 0; h < H; ++h)
+      worst = std::max(worst, rel_vec(got.data() + (row * H + h) * d, want.data() + h * d));
+    return worst;
+  };
+
+  // Step 0: the four prompts.
+  const int64_t prompt[4] = {4096, 100, 64, 40};
+  std::vector<std::vector<int32_t>> toks(4);
+  std::vector<BatchSeqInput> seqs;
+  for (int s = 0; s < 4; ++s) {
+    toks[static_cast<size_t>(s)].assign(static_cast<size_t>(prompt[s]), 7);
+    seqs.push_back({toks[static_cast<size_t>(s)], &caches[static_cast<size_t>(s)]});
+  }
+  ASSERT_OK(asmb.AssemblePrefill(seqs));
+  std::vector<float> q;
+  (void)run(&q);
+  EXPECT_EQ(pool.free_blocks(), 0);
+
+  // Step 1: the scheduler evicts A.
+  scheduler::Scheduler sched;
+  std::vector<scheduler::SeqDesc> running = {
+      Seq(B, 0, 100, 0, caches[B].block_table().num_blocks()),
+      Seq(C, 1, 64, 0, caches[C].block_table().num_blocks()),
+      Seq(D, 2, 40, 0, caches[D].block_table().num_blocks()),
+      Seq(A, 3, 4096, 0, caches[A].block_table().num_blocks())};
+  scheduler::ScheduleInputs in1;
+  in1.running = running;
+  in1.pool = {pool.free_blocks(), pool.num_blocks(), bs};
+  const scheduler::SchedulerOutput out1 = sched.Schedule(in1);
+  ASSERT(out1.preempt.size() == 1 && out1.preempt[0] == A);
+  ASSERT(out1.decode == (std::vector<scheduler::RequestId>{B, C, D}));
+  caches[A].reset();  // evict: its 256 blocks go back to the pool
+  EXPECT_EQ(pool.free_blocks(), 256);
+  std::vector<int32_t> one = {7};
+  seqs.clear();
+  for (auto id : out1.decode) seqs.push_back({one, &caches[id]});
+  ASSERT_OK(asmb.AssembleDecode(seqs));
+  std::vector<float> got = run(&q), wk, wv;
+  widen(&wk, &wv);
+  for (size_t r = 0; r < out1.decode.size(); ++r) {
+    const double e = check_decode(q, got, static_cast<int64_t>(r), caches[out1.decode[r]], wk, wv);
+    if (e > 1e-4) std::fprintf(stderr, "  step 1 decode row %zu: rel %.3g\n", r, e);
+    EXPECT(e <= 1e-4);
+  }
+
+  // Step 2: B and D finish; A comes back as a 4096-token prefill.
+  caches[B].reset();
+  caches[D].reset();
+  scheduler::ScheduleInputs in2;
+  const std::vector<scheduler::SeqDesc> running2 = {
+      Seq(C, 1, caches[C].length(), 0, caches[C].block_table().num_blocks())};
+  const std::vector<scheduler::SeqDesc> waiting2 = {Seq(A, 3, 0, 4096, 0)};
+  in2.running = running2;
+  in2.waiting = waiting2;
+  in2.pool = {pool.free_blocks(), pool.num_blocks(), bs};
+  in2.config.max_num_seqs = 8;
+  in2.config.max_num_batched_tokens = 8192;
+  const scheduler::SchedulerOutput out2 = sched.Schedule(in2);
+  ASSERT(out2.preempt.empty() && out2.decode == (std::vector<scheduler::RequestId>{C}));
+  ASSERT(out2.prefill.size() == 1 && out2.prefill[0].id == A && out2.prefill[0].num_tokens == 4096);
+  seqs.clear();
+  seqs.push_back({one, &caches[C]});
+  seqs.push_back({toks[A], &caches[A]});
+  ASSERT_OK(asmb.AssembleMixed(seqs));
+  got = run(&q);
+  widen(&wk, &wv);
+  const double ec = check_decode(q, got, 0, caches[C], wk, wv);
+  if (ec > 1e-4) std::fprintf(stderr, "  step 2 decode row: rel %.3g\n", ec);
+  EXPECT(ec <= 1e-4);
+  const std::vector<int32_t>& ta = caches[A].block_table().blocks();
+  double worst = 0;
+  std::vector<float> want(static_cast<size_t>(H * d));
+  for (int64_t t = 0; t < 4096; t = (t == 0 ? 63 : t + 64)) {
+    const int64_t row = 1 + t;  // rows: C's decode, then A's chunk
+    orc_paged_decode_f32(ORC_ISA_AVX2, q.data() + row * H * d, wk.data(), wv.data(), ta.data(),
+                         static_cast<int64_t>(ta.size()), t + 1, H, Hkv, d, bs,
+                         pool.block_stride(), attn.scale(), want.data());
+    for (int h = 0; h < H; ++h)
+      worst = std::max(worst, rel_vec(got.data() + (row * H + h) * d, want.data() + h * d));
+  }
+  if (worst > 1e-2) std::fprintf(stderr, "  re-prefill rows: rel %.3g\n", worst);
+  EXPECT(worst <= 1e-2);
+  EXPECT_EQ(caches[A].length(), 4096);
+}
+
+TEST_GPU(GpuDispatchHbmPoolRunsHip) {
+  // An HBM pool routes to the HIP path: append and batched decode through the
+  // dispatcher, checked against the oracle on a host mirror.
+  Gpu gpu;
+  HbmSlabAllocator hbm(gpu.ctx);
+  const int L = 1, Hkv = 2, d = 64, bs = 16, H = 8, nb = 20;
+  StatusOr<std::unique_ptr<BlockPool>> pr = BlockPool::Create(Geom(L, Hkv, d), bs, nb, &hbm);
+  ASSERT_OK(pr.status());
+  BlockPool& pool = **pr;
+  EXPECT(dispatch::Select(pool) == dispatch::Device::kHip);
+  const size_t n = static_cast<size_t>(pool.slab_bytes() / 4);
+  std::vector<float> k = Normal(static_cast<int64_t>(n), 21), v = Normal(static_cast<int64_t>(n), 22);
+  ASSERT_OK(FromRc(gpu.ctx, ehip_copy_to_device(gpu.ctx, pool.k_slab(0), k.data(), n * 4)));
+  ASSERT_OK(FromRc(gpu.ctx, ehip_copy_to_device(gpu.ctx, pool.v_slab(0), v.data(), n * 4)));
+  std::vector<float> kn = Normal(2 * Hkv * d, 23), vn = Normal(2 * Hkv * d, 24);
+  std::vector<int64_t> slots = {4 * bs + 10, 9 * bs + 2};
+  DeviceBuffer dkn = ToDevice(gpu.ctx, kn), dvn = ToDevice(gpu.ctx, vn), dslots;
+  ASSERT_OK(dslots.Upload(gpu.ctx, slots.data(), 2 * 8));
+  ASSERT_OK(dispatch::KvScatter(gpu.ctx, pool, 0, static_cast<float*>(dkn.get()),
+                                static_cast<float*>(dvn.get()),
+                                static_cast<const int64_t*>(dslots.get()), 2));
+  orc_kv_scatter_f32(kn.data(), vn.data(), slots.data(), 2, Hkv, d, bs, k.data(), v.data());
+  const std::vector<int32_t> t0 = {4, 11, 0}, t1 = {9};
+  const int32_t* tables[2] = {t0.data(), t1.data()};
+  const int64_t lens[2] = {43, 3};
+  std::vector<float> q = Normal(2 * H * d, 25), want(q.size());
+  DeviceBuffer dq = ToDevice(gpu.ctx, q), dout;
+  ASSERT_OK(dout.Reserve(gpu.ctx, static_cast<int64_t>(q.size() * 4)));
+  const float scale = kernels::AttentionScale(d);
+  ASSERT_OK(dispatch::PagedDecodeBatched(gpu.ctx, pool, 0, static_cast<float*>(dq.get()), tables,
+                                         lens, 2, H, scale, static_cast<float*>(dout.get())));
+  ASSERT_OK(FromRc(gpu.ctx, ehip_sync(gpu.ctx)));
+  std::vector<float> gk = ToHost<float>(gpu.ctx, pool.k_slab(0), static_cast<int64_t>(n));
+  EXPECT(std::memcmp(gk.data(), k.data(), n * 4) == 0);
+  orc_paged_decode_batched_f32(ORC_ISA_SCALAR, q.data(), k.data(), v.data(), tables, lens, 2, H,
+                               Hkv, d, bs, pool.block_stride(), scale, want.data());
+  std::vector<float> got = ToHost<float>(gpu.ctx, dout.get(), static_cast<int64_t>(q.size()));
+  double worst = 0;
+  for (size_t row = 0; row < 2 * H; ++row) {
+    double num = 0, den = 0;
+    for (int e = 0; e < d; ++e) {
+      const size_t i = row * d + static_cast<size_t>(e);
+      num = std::max(num, std::fabs(double(got[i]) - want[i]));
+      den = std::max(den, std::fabs(double(want[i])));
+    }
+    worst = std::max(worst, num / den);
+  }
+  EXPECT(worst <= 1e-4);
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
   bool gpu = false;
   const char* only = nullptr;
+  if (argc > 1 && std::strcmp(argv[1], "--forced") == 0) {
+    // The process-wide device choice this process starts with.
+    const dispatch::Forced f = dispatch::ProcessForced();
+    std::printf("%s\n", f.set ? dispatch::DeviceName(f.device).data() : "unset");
+    return 0;
+  }
   for (int i = 1; i < argc; ++i) {
     if (std::strcmp(argv[i], "--gpu") == 0) gpu = true;
     else if (std::strcmp(argv[i], "--cpu") == 0) gpu = false;

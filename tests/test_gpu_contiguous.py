@@ -1,0 +1,72 @@
+"""The contiguous-cache entry points (ehip_decode_attention_f32,
+ehip_prefill_attention_f32 = the reference's DecodeAttentionF32 and
+PrefillAttentionF32, src/kernels/attention.h:40-73) against the oracle's
+restatements of the same functions: fp32, within 1e-4 relative per output
+vector and the reference allclose (rtol 1e-4, atol 1e-5)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from gpu_util import rel_norm
+from paged_util import allclose_ref, scale_for
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(gctx, *arrs):
+    return [gctx.to_device(np.ascontiguousarray(a, np.float32)) for a in arrs]
+
+
+def _check(got, ref):
+    assert rel_norm(got, ref) <= 1e-4, rel_norm(got, ref)
+    assert allclose_ref(got, ref, 1e-4, 1e-5)
+
+
+@pytest.mark.parametrize("H,Hkv,d,L", [(14, 2, 64, 513), (32, 8, 128, 2048), (8, 8, 128, 1),
+                                       (28, 4, 64, 1000), (6, 3, 18, 77), (64, 8, 128, 20000)])
+def test_decode_attention_contiguous(gctx, ehip_mod, orc, H, Hkv, d, L):
+    rng = np.random.default_rng(H * L + d)
+    q = rng.standard_normal((H, d)).astype(np.float32)
+    k = rng.standard_normal((Hkv, L, d)).astype(np.float32)
+    v = rng.standard_normal((Hkv, L, d)).astype(np.float32)
+    dq, dk, dv = _dev(gctx, q, k, v)
+    out = gctx.alloc(q.nbytes)
+    rc = ehip_mod.lib().ehip_decode_attention_f32(gctx.h, dq.ptr, dk.ptr, dv.ptr, out.ptr, H, Hkv,
+                                                  d, L, C.c_float(scale_for(d)))
+    assert rc == 0, gctx.last_error()
+    gctx.sync()
+    got = out.download(np.float32, q.shape)
+    _check(got, orc.decode_contig(q, k, v, H, Hkv, d, scale_for(d)))
+    if L == 1:  # one key: every head of group hk returns v[hk, 0]
+        assert np.array_equal(got, np.repeat(v[:, 0, :], H // Hkv, axis=0))
+
+
+@pytest.mark.parametrize("H,Hkv,d", [(32, 8, 128), (14, 2, 64)])
+@pytest.mark.parametrize("T,L", [(1, 1), (16, 16), (37, 100), (128, 128), (5, 300), (300, 301)])
+def test_prefill_attention_contiguous(gctx, ehip_mod, orc, H, Hkv, d, T, L):
+    rng = np.random.default_rng(T * 1000 + L + H)
+    q = rng.standard_normal((T, H, d)).astype(np.float32)
+    k = rng.standard_normal((Hkv, L, d)).astype(np.float32)
+    v = rng.standard_normal((Hkv, L, d)).astype(np.float32)
+    dq, dk, dv = _dev(gctx, q, k, v)
+    out = gctx.alloc(q.nbytes)
+    rc = ehip_mod.lib().ehip_prefill_attention_f32(gctx.h, dq.ptr, dk.ptr, dv.ptr, out.ptr, T, H,
+                                                   Hkv, d, L, C.c_float(scale_for(d)))
+    assert rc == 0, gctx.last_error()
+    gctx.sync()
+    got = out.download(np.float32, q.shape)
+    _check(got, orc.prefill(q, k, v, H, Hkv, d, scale_for(d)))
+
+
+def test_contiguous_entry_points_validate(gctx, ehip_mod):
+    buf = gctx.alloc(4096)
+    L_ = ehip_mod.lib()
+    s = C.c_float(0.125)
+    assert L_.ehip_prefill_attention_f32(gctx.h, buf.ptr, buf.ptr, buf.ptr, buf.ptr, 5, 8, 8, 16,
+                                         4, s) == ehip_mod.INVALID_ARGUMENT  # T > L
+    assert L_.ehip_decode_attention_f32(gctx.h, buf.ptr, buf.ptr, buf.ptr, buf.ptr, 6, 4, 16, 4,
+                                        s) == ehip_mod.INVALID_ARGUMENT  # H % Hkv
+    assert L_.ehip_decode_attention_f32(gctx.h, None, buf.ptr, buf.ptr, buf.ptr, 8, 8, 16, 4,
+                                        s) == ehip_mod.INVALID_ARGUMENT
+    buf.free()

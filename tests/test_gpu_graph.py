@@ -138,3 +138,110 @@ def test_graph_replay_mixed_prefill_and_decode(gctx, ehip_mod, orc):
     w = workloads._finish("mixed", 32, 8, 128, 16, ehip_mod.KV_BF16, 2, qlens, ctx_lens, tables,
                           pool, 0.5)
     run_case(gctx, ehip_mod, orc, w, layers=2)
+
+
+# ------------------------------------------------------- replay vs the oracle
+def _oracle_step(orc, w, kb, vb, kn, vn, q, slots, lens, tables):
+    """The oracle's append into the host bf16 slabs, then the reference
+    attention on the widened post-append cache (and on nothing else: the
+    caller compares)."""
+    H, Hkv, d, bs = w.heads, w.kv_heads, w.head_dim, w.block_size
+    orc.kv_scatter(kn, vn, slots, Hkv, d, bs, kb, vb)
+    kr, vr = orc.bf16_bits_to_f32(kb), orc.bf16_bits_to_f32(vb)
+    return orc.paged_decode_batched(q, kr, vr, tables, [int(x) for x in lens], H, Hkv, d, bs,
+                                    w.scale, isa=orc.ISA_AVX2)
+
+
+def _decode_steps(w, n_steps):
+    """The workload advanced one token per sequence per step: each step's
+    post-append lengths, tables (grown by a free block when a boundary is
+    crossed) and append slots."""
+    bs = w.block_size
+    used = set(int(b) for t in w.tables for b in t)
+    free = [b for b in range(w.pool_blocks) if b not in used]
+    tables = [list(map(int, t)) for t in w.tables]
+    steps = []
+    for s in range(n_steps):
+        lens = w.context_lens.astype(np.int64) + s
+        slots = []
+        for b, L in enumerate(lens):
+            while len(tables[b]) * bs < L:
+                tables[b].append(free.pop())
+            pos = int(L) - 1
+            slots.append(tables[b][pos // bs] * bs + pos % bs)
+        steps.append((lens.copy(), [np.array(t, np.int32) for t in tables],
+                      np.array(slots, np.int64)))
+    return steps
+
+
+def test_graph_replay_follows_a_changing_decode_plan(gctx, ehip_mod, orc):
+    """A decode loop under one instantiated graph: every step each sequence
+    grows by a token (new lengths, new slots, tables growing across block
+    boundaries), the step's plan is uploaded eagerly, the layer launches are
+    re-captured and written into the graph with hipGraphExecUpdate, and the
+    replay is checked against the oracle (append bit-exact, outputs within
+    1e-4 relative per vector on the same bf16 cache) and against an eager run
+    of the same plan (bit-identical)."""
+    from ehip import hipgraph, workloads
+    from gpu_util import rel_norm
+    E = ehip_mod
+    w = workloads.c4(num_seqs=16, share_frac=0.0)
+    H, Hkv, d, bs = w.heads, w.kv_heads, w.head_dim, w.block_size
+    g = E.geometry(H, Hkv, d, bs, w.kv_dtype, w.pool_blocks, w.scale)
+    layers, n_steps = 2, 4
+    steps = _decode_steps(w, n_steps)
+    host, dev = [], []
+    for layer in range(layers):
+        kp, vp = seeded_pool(orc, w, 500 + layer, poison=False)
+        kb, vb = orc.to_bf16_bits(kp), orc.to_bf16_bits(vp)
+        host.append([kb, vb])
+        dev.append([gctx.to_device(kb), gctx.to_device(vb)])
+    R = w.num_seqs
+    rows = [[new_rows(orc, w, 700 + 10 * s + layer) for layer in range(layers)]
+            for s in range(n_steps)]
+    drows = [[[gctx.to_device(x) for x in rows[s][layer]] for layer in range(layers)]
+             for s in range(n_steps)]
+    outs = [gctx.alloc(R * H * d * 4) for _ in range(layers)]
+
+    def launches(s):
+        def fn():
+            for layer in range(layers):
+                dkn, dvn, dq = drows[s][layer]
+                dk, dv = dev[layer]
+                assert gctx.step_kv_append(dkn, dvn, dk, dv) == 0, gctx.last_error()
+                assert gctx.step_attention(dq, dk, dv, outs[layer]) == 0, gctx.last_error()
+        return fn
+
+    gs = hipgraph.Stream()
+    graph = hipgraph.Graph()
+    assert E.lib().ehip_set_stream(gctx.h, gs.h) == 0
+    try:
+        for s, (lens, tables, slots) in enumerate(steps):
+            st = E.StepArrays(np.ones(R, np.int32), lens, tables, slots)
+            assert gctx.step_upload(g, st) == 0, gctx.last_error()
+            if s == 0:
+                graph.capture(gs, launches(0))
+            else:
+                graph.update(gs, launches(s))
+            graph.replay(gs)
+            gctx.sync()
+            got = [o.download(np.float32, (R, H, d)).copy() for o in outs]
+            for layer in range(layers):
+                kn, vn, q = rows[s][layer]
+                kb, vb = host[layer]
+                ref = _oracle_step(orc, w, kb, vb, kn, vn, q, slots, lens, tables)
+                dk, dv = dev[layer]
+                assert np.array_equal(dk.download(np.uint16, kb.shape), kb), (s, layer)
+                assert np.array_equal(dv.download(np.uint16, vb.shape), vb), (s, layer)
+                assert rel_norm(got[layer], ref) <= 1e-4, (s, layer, rel_norm(got[layer], ref))
+            launches(s)()  # eager, same plan: the append is idempotent
+            gctx.sync()
+            for layer in range(layers):
+                eager = outs[layer].download(np.float32, (R, H, d))
+                assert np.array_equal(eager.view(np.uint32), got[layer].view(np.uint32)), (s, layer)
+    finally:
+        assert E.lib().ehip_set_stream(gctx.h, None) == 0
+        graph.close()
+        gs.close()
+    for x in [b for pair in dev for b in pair] + [b for s in drows for l in s for b in l] + outs:
+        x.free()

@@ -31,3 +31,23 @@ def test_host_layer_cpu():
 @pytest.mark.gpu
 def test_host_layer_gpu():
     _run("--gpu")
+
+
+@pytest.mark.parametrize("value,want", [(None, "unset"), ("", "unset"), ("hip", "hip"),
+                                        ("avx2", "cpu"), ("scalar", "cpu"), ("neon", "cpu")])
+def test_process_device_choice_from_environment(value, want):
+    """ENGINE_FORCE_ISA as a fresh process reads it: a CPU ISA name pins the
+    CPU kernels, "hip" the GPU path, nothing leaves it to the pool."""
+    import os
+    env = {k: v for k, v in os.environ.items() if k != "ENGINE_FORCE_ISA"}
+    if value is not None:
+        env["ENGINE_FORCE_ISA"] = value
+    r = subprocess.run([str(BIN), "--forced"], capture_output=True, text=True, timeout=30, env=env)
+    assert r.returncode == 0 and r.stdout.strip() == want, (r.returncode, r.stdout, r.stderr)
+
+
+def test_unknown_forced_isa_is_fatal():
+    import os
+    env = dict(os.environ, ENGINE_FORCE_ISA="cuda")
+    r = subprocess.run([str(BIN), "--forced"], capture_output=True, text=True, timeout=30, env=env)
+    assert r.returncode == -6 and "names no kernel set" in r.stderr
