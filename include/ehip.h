@@ -282,6 +282,16 @@ int ehip_step_rope_kv_append(ehip_ctx* ctx, float* d_q, const float* d_src_k,
 /* Attention for every row of the step: q/out [sum T_b, H, d] fp32. */
 int ehip_step_attention(ehip_ctx* ctx, const float* d_q, const void* d_k_slab,
                         const void* d_v_slab, float* d_out);
+/* ehip_step_kv_append followed by ehip_step_attention, with the same results
+ * bit for bit (the append into the slabs, the outputs). When every row of the
+ * step is a decode row (T_b == 1) on bf16 slabs covered by the matrix-core
+ * decode kernel, both run in one launch (plus the split merge): the work item
+ * that ends at a row's last key stores that row's new K/V and uses them
+ * directly; otherwise the two launches run in order. Together they stand for
+ * PagedKvCache::append followed by the batched attention in the reference's
+ * layer forward (src/model/optimized_model.cpp:370-467). */
+int ehip_step_append_attention(ehip_ctx* ctx, const float* d_src_k, const float* d_src_v,
+                               const float* d_q, void* d_k_slab, void* d_v_slab, float* d_out);
 /* INT8 KV (geometry kv_dtype EHIP_KV_INT8): the append quantises the step's
  * new rows into int8 slabs with fp32 scales [slab_blocks, kv_heads] per slab
  * (requantising a block's older rows when a new row exceeds its range; a row

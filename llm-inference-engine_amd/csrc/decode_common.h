@@ -61,6 +61,7 @@ struct ItemRef {
   int te;
   int table_off;
   int first[2];  // block ids of the first two 16-token halves, or -1
+  bool last;     // the range ends at its row's last key
 };
 
 __device__ __forceinline__ ItemRef DecodeItem(const WorkItem& it) {
@@ -68,8 +69,9 @@ __device__ __forceinline__ ItemRef DecodeItem(const WorkItem& it) {
   r.rows[0] = it.row0;
   r.rows[1] = it.row1 >= 0 ? it.row1 : it.row0;
   r.nrows = it.row1 >= 0 ? 2 : 1;
-  r.hk = it.hk_split & ((1 << kHkBits) - 1);
-  r.split = it.hk_split >> kHkBits;
+  r.hk = UnpackHk(it.hk_split);
+  r.split = UnpackSplit(it.hk_split);
+  r.last = IsLastRange(it.hk_split);
   r.tb = it.tok_begin;
   r.te = it.tok_end;
   r.table_off = it.table_off;

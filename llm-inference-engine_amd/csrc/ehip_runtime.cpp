@@ -180,8 +180,14 @@ int UploadPlan(ehip_ctx* ctx, const ehip_geometry& g, Plan&& plan, const int32_t
   return EHIP_OK;
 }
 
+// The decode-side parameters of the uploaded step (everything but the
+// fused-append rows).
+ehip::DecodeParams StepDecodeParams(ehip_ctx* ctx, const float* q, const void* k_slab,
+                                    const void* v_slab, float* out);
+
 int LaunchAttention(ehip_ctx* ctx, const float* q, const void* k_slab, const void* v_slab,
-                    float* out, const float* k_scale = nullptr, const float* v_scale = nullptr) {
+                    float* out, const float* k_scale = nullptr, const float* v_scale = nullptr,
+                    const float* new_k = nullptr, const float* new_v = nullptr) {
   const ehip_geometry& g = ctx->geom;
   const Plan& plan = ctx->plan;
   if (plan.items.size() > static_cast<size_t>(INT32_MAX) ||
@@ -222,6 +228,19 @@ int LaunchAttention(ehip_ctx* ctx, const float* q, const void* k_slab, const voi
     EHIP_HIP(ctx, e);
   }
   if (plan.items.empty() && plan.merge_rows.empty()) return EHIP_OK;
+  ehip::DecodeParams p = StepDecodeParams(ctx, q, k_slab, v_slab, out);
+  p.k_scale = k_scale;
+  p.v_scale = v_scale;
+  p.new_k = new_k;
+  p.new_v = new_v;
+  EHIP_HIP(ctx, ehip::LaunchDecode(p, g.kv_dtype, &ctx->queue, ctx->stream));
+  return EHIP_OK;
+}
+
+ehip::DecodeParams StepDecodeParams(ehip_ctx* ctx, const float* q, const void* k_slab,
+                                    const void* v_slab, float* out) {
+  const ehip_geometry& g = ctx->geom;
+  const Plan& plan = ctx->plan;
   ehip::DecodeParams p{};
   p.q = q;
   p.k_slab = k_slab;
@@ -248,12 +267,10 @@ int LaunchAttention(ehip_ctx* ctx, const float* q, const void* k_slab, const voi
   p.d = g.head_dim;
   p.bs = g.block_size;
   p.scale_log2 = g.scale * 1.4426950408889634f;
-  p.k_scale = k_scale;
-  p.v_scale = v_scale;
   p.max_length = plan.max_length;
   p.has_prefill = plan.prefill.empty() ? 0 : 1;
-  EHIP_HIP(ctx, ehip::LaunchDecode(p, g.kv_dtype, &ctx->queue, ctx->stream));
-  return EHIP_OK;
+  p.slots = ctx->d_slots;
+  return p;
 }
 
 bool NonNull(const void* a) { return a != nullptr; }
@@ -827,6 +844,38 @@ int ehip_step_attention(ehip_ctx* ctx, const float* d_q, const void* d_k_slab,
   return LaunchAttention(ctx, d_q, d_k_slab, d_v_slab, d_out);
 }
 
+int ehip_step_append_attention(ehip_ctx* ctx, const float* d_src_k, const float* d_src_v,
+                               const float* d_q, void* d_k_slab, void* d_v_slab, float* d_out) {
+  if (int rc = CheckCtx(ctx)) return rc;
+  if (!ctx->have_step) return SetError(ctx, EHIP_FAILED_PRECONDITION, "no step uploaded");
+  const Plan& plan = ctx->plan;
+  const ehip_geometry& g = ctx->geom;
+  if (plan.rows.empty()) return EHIP_OK;
+  if (plan.slots.empty())
+    return SetError(ctx, EHIP_FAILED_PRECONDITION, "the uploaded step has no slot mapping");
+  if (!d_src_k || !d_src_v || !d_q || !d_k_slab || !d_v_slab || !d_out)
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "null append/attention operand");
+  if (g.kv_dtype == EHIP_KV_INT8)
+    return SetError(ctx, EHIP_INVALID_ARGUMENT,
+                    "INT8 slabs carry scales: use ehip_step_kv_append_int8 + ehip_step_attention_int8");
+  if (ehip::BlockStride(g) != int64_t{g.kv_heads} * g.block_size * g.head_dim)
+    return SetError(ctx, EHIP_UNIMPLEMENTED, "append needs the dense Hkv*bs*d block stride");
+  // One launch (plus the split merge) when every row is a decode row on the
+  // bf16 matrix-core kernel: the items ending at their rows' last keys append.
+  const char* env = std::getenv("EHIP_FUSED_APPEND");
+  const bool allowed = !(env && env[0] == '0');
+  if (allowed && plan.all_decode && g.kv_dtype == EHIP_KV_BF16 && !plan.items.empty() &&
+      reinterpret_cast<uintptr_t>(d_src_k) % 8 == 0 && reinterpret_cast<uintptr_t>(d_src_v) % 8 == 0 &&
+      ehip::DecodeMfmaCovers(StepDecodeParams(ctx, d_q, d_k_slab, d_v_slab, d_out)))
+    return LaunchAttention(ctx, d_q, d_k_slab, d_v_slab, d_out, nullptr, nullptr, d_src_k,
+                           d_src_v);
+  EHIP_HIP(ctx, ehip::LaunchKvScatter(d_src_k, d_src_v, ctx->d_slots,
+                                      static_cast<int64_t>(plan.slots.size()), g.kv_heads,
+                                      g.head_dim, g.block_size, g.slab_blocks, d_k_slab, d_v_slab,
+                                      g.kv_dtype, ctx->d_err, ctx->stream));
+  return LaunchAttention(ctx, d_q, d_k_slab, d_v_slab, d_out);
+}
+
 int ehip_step_kv_append_int8(ehip_ctx* ctx, const float* d_src_k, const float* d_src_v,
                              void* d_k_slab, void* d_v_slab, float* d_k_scale, float* d_v_scale) {
   if (int rc = CheckCtx(ctx)) return rc;
@@ -906,8 +955,8 @@ int ehip_plan_items(const ehip_geometry* geom, const ehip_step_desc* step, int32
     o[1] = w.row1;
     o[2] = w.tok_begin;
     o[3] = w.tok_end;
-    o[4] = w.hk_split & ((1 << ehip::kHkBits) - 1);
-    o[5] = w.hk_split >> ehip::kHkBits;
+    o[4] = ehip::UnpackHk(w.hk_split);
+    o[5] = ehip::UnpackSplit(w.hk_split);
   }
   return EHIP_OK;
 }
@@ -927,8 +976,8 @@ int ehip_plan_prefill_items(const ehip_geometry* geom, const ehip_step_desc* ste
     o[1] = w.chunk;
     o[2] = w.past;
     o[3] = w.q0;
-    o[4] = w.hk_split & ((1 << ehip::kHkBits) - 1);
-    o[5] = w.hk_split >> ehip::kHkBits;
+    o[4] = ehip::UnpackHk(w.hk_split);
+    o[5] = ehip::UnpackSplit(w.hk_split);
     o[6] = w.key_begin;
     o[7] = w.key_end;
     o[8] = plan.rows[static_cast<size_t>(w.row_base + w.q0)].nsplit;

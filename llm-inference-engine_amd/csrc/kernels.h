@@ -47,6 +47,13 @@ struct DecodeParams {
   int32_t has_prefill;      // the step also has MFMA prefill items
   const float* k_scale;     // INT8 KV: per-(block, kv head) scales [slab_blocks, Hkv]
   const float* v_scale;
+  // Fused append (bf16 MFMA decode of an all-decode step): the step's new K/V
+  // rows [rows, Hkv, d] fp32 and their slots. The item flagged as its row's
+  // last key range stores the row's new bf16 K/V at the slot and uses them for
+  // that key. Null: the rows were appended by a separate launch.
+  const float* new_k;
+  const float* new_v;
+  const int64_t* slots;
   uint32_t* queue;          // kItemQueues ticket counters, kQueueStride words apart
                             // (zero at launch; MFMA kernel only)
   uint32_t* queue_done;     // wavefronts finished (zero at launch)
@@ -107,6 +114,10 @@ int PrefillRowsPerItem(int kv_dtype, int d, int group, int bs, int64_t slab_byte
 // between the two publishes the partials: no device-wide fences or counters.
 hipError_t LaunchDecode(const DecodeParams& p, int kv_dtype, QueueState* queue, hipStream_t stream);
 
+// Whether the bf16 MFMA decode kernel covers p (d 64/128, g 1/2/4/8, bs >= 16,
+// 16-byte aligned operands, not forced to the VALU kernel by
+// EHIP_DECODE_KERNEL=valu). Only it performs the fused append.
+bool DecodeMfmaCovers(const DecodeParams& p);
 // bf16-KV decode with QK^T on MFMA; returns false (nothing launched) when the
 // shape is not covered (d not 64/128, g not 1/2/4/8, bs < 16, misaligned).
 bool LaunchDecodeMfma(const DecodeParams& p, QueueState* queue, hipStream_t stream,

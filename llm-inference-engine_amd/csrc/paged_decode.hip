@@ -613,11 +613,10 @@ hipError_t LaunchSplits(const DecodeParams& p, int kv_dtype, QueueState* queue,
   }
   if (kv_dtype != EHIP_KV_BF16) return LaunchTyped<float>(p, stream);
   // EHIP_DECODE_KERNEL=valu selects the all-VALU kernel for bf16 as well.
-  const char* pick = std::getenv("EHIP_DECODE_KERNEL");
-  if (!(pick && std::strcmp(pick, "valu") == 0)) {
-    hipError_t err = hipSuccess;
-    if (LaunchDecodeMfma(p, queue, stream, &err)) return err;
-  }
+  hipError_t err = hipSuccess;
+  if (LaunchDecodeMfma(p, queue, stream, &err)) return err;
+  // Only the MFMA kernel performs a fused append; the caller checked coverage.
+  if (p.new_k != nullptr) return hipErrorInvalidValue;
   return LaunchTyped<uint16_t>(p, stream);
 }
 

@@ -74,7 +74,9 @@ struct Tile {
 // QL: keep the Q operands in LDS (read per MFMA) instead of 8·NC registers,
 // so the wide shapes fit two wavefronts per SIMD.
 // OCC: wavefronts per SIMD the register allocation must allow.
-template <int D, int G, int RMAX, int TH, int NBUF, bool QL, int OCC>
+// FUSE: the launch carries the step's new K/V rows (fused append); the
+// instance without it has no append code at all.
+template <int D, int G, int RMAX, int TH, int NBUF, bool QL, int OCC, bool FUSE>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(OCC)))
 void DecodeMfmaBf16(DecodeParams p) {
   using T = Tile<D, TH>;
@@ -90,6 +92,9 @@ void DecodeMfmaBf16(DecodeParams p) {
 
   __shared__ float p_lds[TT * HP];
   __shared__ uint4 q_lds[QL ? 2 * NC * 64 : 1];
+  // Fused append: the row's new K and V as bf16 pairs (element 2i, 2i + 1).
+  __shared__ uint4 knew_lds[FUSE ? D / 8 : 1];
+  __shared__ uint32_t vnew_lds[FUSE ? D / 2 : 1];
 
   const int lane = threadIdx.x;
   // Persistent wavefronts: a workgroup's first item is its index; each later
@@ -155,6 +160,12 @@ void DecodeMfmaBf16(DecodeParams p) {
   // Per-lane byte offsets inside a (block, head) tile: loop-invariant.
   const int koff = (n * D + kq * 8) * 2;
   const int voff = (tv * D + ev) * 2;
+  // Fused append: the item ending at its row's last key (position te - 1)
+  // streams keys [tb, te - 1) from the slab and takes the new key from the
+  // step's new rows in one more step after the loop.
+  const bool fuse = FUSE && it.last;  // wavefront-uniform
+  const int newpos = te - 1;
+  const int kend = fuse ? newpos : te;  // keys the tile loop reads from the slab
 
   // Each half's descriptor starts at its first token row and covers only the
   // rows inside the range: rows past the range end read as zeros (so stale
@@ -166,12 +177,13 @@ void DecodeMfmaBf16(DecodeParams p) {
 #pragma unroll
     for (int h2 = 0; h2 < TH; ++h2) {
       const int th = t0 + 16 * h2;  // wavefront-uniform; a half lies in one block (bs >= 16)
-      const int phys = given ? it.first[h2 > 0 ? 1 : 0]
-                             : __builtin_amdgcn_readlane(tab, min(th, te - 1) / bs - lb0);
-      const bool ok = th < te && phys >= 0;
+      const int phys =
+          given ? it.first[h2 > 0 ? 1 : 0]
+                : __builtin_amdgcn_readlane(tab, max(0, min(th, kend - 1) / bs - lb0));
+      const bool ok = th < kend && phys >= 0;
       t.phys[h2] = ok ? phys : -1;
       const int64_t boff = int64_t{ok ? phys : 0} * p.block_stride + (th & bmask) * D;
-      const uint32_t range = ok ? static_cast<uint32_t>(min(16, te - th) * D * 2) : 0u;
+      const uint32_t range = ok ? static_cast<uint32_t>(min(16, kend - th) * D * 2) : 0u;
       const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
           const_cast<uint16_t*>(kbase + boff), 0, range, 0x00020000);
       const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
@@ -194,6 +206,37 @@ void DecodeMfmaBf16(DecodeParams p) {
   else
     load(bufA, tb, false);
   if constexpr (NBUF == 3) load(bufB, tb + TT, false);
+
+  // Fused append: the item ending at its row's last key narrows that key's
+  // new K/V rows (the reference's round-to-nearest-even), stores them at the
+  // row's slot for later steps, and keeps them in LDS for its last step (no
+  // other item reads that row, and this item never loads it from the slab).
+  if (fuse) {
+    const int row = it.rows[0];
+    const int pair = lane % (D / 2);
+    const int64_t src = (int64_t{row} * p.kv_heads + hk) * D + 2 * pair;
+    const float2 kx = *reinterpret_cast<const float2*>(p.new_k + src);
+    const float2 vx = *reinterpret_cast<const float2*>(p.new_v + src);
+    const uint32_t kp = Fp32ToBf16Bits(kx.x) | (Fp32ToBf16Bits(kx.y) << 16);
+    const uint32_t vp = Fp32ToBf16Bits(vx.x) | (Fp32ToBf16Bits(vx.y) << 16);
+    reinterpret_cast<uint32_t*>(knew_lds)[pair] = kp;
+    vnew_lds[pair] = vp;
+    const int64_t slot = p.slots[row];
+    if (slot >= 0 && slot < p.slab_blocks * bs) {
+      const int64_t blk = slot / bs;
+      const int64_t dst = blk * p.block_stride + int64_t{hk} * bs * D + (slot - blk * bs) * D +
+                          2 * pair;
+      if (lane < D / 2) {
+        uint16_t* kslab = static_cast<uint16_t*>(const_cast<void*>(p.k_slab));
+        uint16_t* vslab = static_cast<uint16_t*>(const_cast<void*>(p.v_slab));
+        *reinterpret_cast<uint32_t*>(kslab + dst) = kp;
+        *reinterpret_cast<uint32_t*>(vslab + dst) = vp;
+      }
+    } else if (lane == 0) {
+      atomicOr(p.err, kErrSlotRange);
+    }
+    __syncthreads();  // the LDS rows are read by the tile patch below
+  }
 
   // Q as MFMA A operands: q = hi + lo, both bf16 (round-to-nearest-even
   // narrowing, branch-free); padding virtual heads are zero.
@@ -224,8 +267,8 @@ void DecodeMfmaBf16(DecodeParams p) {
 #pragma unroll
   for (int h = 0; h < GV; ++h) o[h][0] = o[h][1] = 0.f;
 
-  auto process = [&](const T& t, int t0) {
-    if (!drawn && t0 + kDrawAhead >= te) {  // wavefront-uniform
+  auto process = [&](const T& t, int t0, int tend) {
+    if (!drawn && t0 + kDrawAhead >= tend) {  // wavefront-uniform
       drawn = true;
       if (lane == 0) ticket = atomicAdd(my_queue, 1u);
     }
@@ -245,7 +288,7 @@ void DecodeMfmaBf16(DecodeParams p) {
     float s[TH][4];
 #pragma unroll
     for (int h2 = 0; h2 < TH; ++h2) {
-      const bool valid = t.phys[h2] >= 0 && t0 + 16 * h2 + n < te;
+      const bool valid = t.phys[h2] >= 0 && t0 + 16 * h2 + n < tend;
 #pragma unroll
       for (int i = 0; i < 4; ++i) s[h2][i] = valid ? acc[h2][i] * p.scale_log2 : -INFINITY;
     }
@@ -319,27 +362,44 @@ void DecodeMfmaBf16(DecodeParams p) {
   // A work item's range is never empty (tb < te), so the loop has no entry
   // test for the compiler to sink the Q loads behind. NBUF - 1 tiles are in
   // flight while one is computed; loads past the range are empty.
+  // (For a fused item whose range is the new key alone the loop's one tile
+  // is empty: every score masked, the state unchanged.)
   if constexpr (NBUF == 2) {
     for (int t0 = tb;; t0 += 2 * TT) {
       load(bufB, t0 + TT, false);
-      process(bufA, t0);
-      if (t0 + TT >= te) break;
+      process(bufA, t0, kend);
+      if (t0 + TT >= kend) break;
       load(bufA, t0 + 2 * TT, false);
-      process(bufB, t0 + TT);
-      if (t0 + 2 * TT >= te) break;
+      process(bufB, t0 + TT, kend);
+      if (t0 + 2 * TT >= kend) break;
     }
   } else {
     for (int t0 = tb;; t0 += 3 * TT) {
       load(bufC, t0 + 2 * TT, false);
-      process(bufA, t0);
-      if (t0 + TT >= te) break;
+      process(bufA, t0, kend);
+      if (t0 + TT >= kend) break;
       load(bufA, t0 + 3 * TT, false);
-      process(bufB, t0 + TT);
-      if (t0 + 2 * TT >= te) break;
+      process(bufB, t0 + TT, kend);
+      if (t0 + 2 * TT >= kend) break;
       load(bufB, t0 + 4 * TT, false);
-      process(bufC, t0 + 2 * TT);
-      if (t0 + 3 * TT >= te) break;
+      process(bufC, t0 + 2 * TT, kend);
+      if (t0 + 3 * TT >= kend) break;
     }
+  }
+  if (fuse) {
+    // The new key as a one-row tile: row 0 of the first half, from LDS.
+    T tn;
+#pragma unroll
+    for (int h2 = 0; h2 < TH; ++h2) {
+      tn.phys[h2] = h2 == 0 ? 0 : -1;
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+        tn.k[h2][c] = (h2 == 0 && n == 0) ? knew_lds[c * 4 + kq] : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+      for (int j = 0; j < VJ; ++j)
+        tn.v[h2][j] = (h2 == 0 && j * VT + tv == 0) ? vnew_lds[lane % VLPT] : 0u;
+    }
+    process(tn, newpos, te);
   }
 
   ReportRejectedBlocks(p, tab);
@@ -405,14 +465,19 @@ void DecodeMfmaBf16(DecodeParams p) {
 }
 
 // Workgroups (one wavefront each) a launch keeps resident: the kernel's
-// occupancy per CU times the CU count.
+// occupancy per CU times the CU count, queried once per (kernel, device).
 template <class K>
 int ResidentWaves(K kernel) {
-  int dev = 0, cus = 0, per_cu = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+  constexpr int kDevices = 64;
+  static int cached[kDevices] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (dev >= 0 && dev < kDevices && cached[dev] > 0) return cached[dev];
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
       hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 64, 0) != hipSuccess)
     return 0;
+  if (dev >= 0 && dev < kDevices) cached[dev] = cus * per_cu;
   return cus * per_cu;
 }
 
@@ -432,7 +497,7 @@ void LaunchPersistent(K kernel, const DecodeParams& p, hipStream_t stream, bool 
   hipLaunchKernelGGL(kernel, dim3(grid), dim3(64), 0, stream, p);
 }
 
-template <int D, int G, int RMAX>
+template <int D, int G, int RMAX, bool FUSE>
 void LaunchShape(const DecodeParams& p, hipStream_t stream, bool wide, bool deep, bool persist) {
   // Two wavefronts per SIMD wherever the shape fits 256 registers without
   // spilling (the 16-virtual-head and triple-buffered 128-wide shapes do not).
@@ -440,28 +505,44 @@ void LaunchShape(const DecodeParams& p, hipStream_t stream, bool wide, bool deep
   constexpr int OCC = (D == 128 && G * RMAX >= 16) ? 1 : 2;
   constexpr int OCC3 = D == 128 ? 1 : 2;
   if (wide && deep)
-    LaunchPersistent(DecodeMfmaBf16<D, G, RMAX, 2, 3, QL, OCC3>, p, stream, persist);
+    LaunchPersistent(DecodeMfmaBf16<D, G, RMAX, 2, 3, QL, OCC3, FUSE>, p, stream, persist);
   else if (wide)
-    LaunchPersistent(DecodeMfmaBf16<D, G, RMAX, 2, 2, QL, OCC>, p, stream, persist);
+    LaunchPersistent(DecodeMfmaBf16<D, G, RMAX, 2, 2, QL, OCC, FUSE>, p, stream, persist);
   else if (deep)
-    LaunchPersistent(DecodeMfmaBf16<D, G, RMAX, 1, 3, QL, OCC3>, p, stream, persist);
+    LaunchPersistent(DecodeMfmaBf16<D, G, RMAX, 1, 3, QL, OCC3, FUSE>, p, stream, persist);
   else
-    LaunchPersistent(DecodeMfmaBf16<D, G, RMAX, 1, 2, QL, OCC>, p, stream, persist);
+    LaunchPersistent(DecodeMfmaBf16<D, G, RMAX, 1, 2, QL, OCC, FUSE>, p, stream, persist);
+}
+
+template <int D, int G, int RMAX>
+void LaunchShape(const DecodeParams& p, hipStream_t stream, bool wide, bool deep, bool persist) {
+  if (p.new_k != nullptr)
+    LaunchShape<D, G, RMAX, true>(p, stream, wide, deep, persist);
+  else
+    LaunchShape<D, G, RMAX, false>(p, stream, wide, deep, persist);
 }
 
 }  // namespace
+
+bool DecodeMfmaCovers(const DecodeParams& p) {
+  const bool aligned = (reinterpret_cast<uintptr_t>(p.k_slab) % 16 == 0) &&
+                       (reinterpret_cast<uintptr_t>(p.v_slab) % 16 == 0) &&
+                       (reinterpret_cast<uintptr_t>(p.q) % 16 == 0) &&
+                       (reinterpret_cast<uintptr_t>(p.out) % 16 == 0) &&
+                       (p.block_stride % 8 == 0);
+  const bool shape = (p.d == 64 || p.d == 128) &&
+                     (p.group == 1 || p.group == 2 || p.group == 4 || p.group == 8);
+  const char* pick = std::getenv("EHIP_DECODE_KERNEL");
+  const bool valu = pick && std::strcmp(pick, "valu") == 0;
+  return aligned && shape && p.bs >= 16 && !valu;
+}
 
 bool LaunchDecodeMfma(const DecodeParams& params, QueueState* queue, hipStream_t stream,
                       hipError_t* err) {
   DecodeParams p = params;
   p.queue = queue->d_counters;
   p.queue_done = queue->d_done;
-  const bool aligned = (reinterpret_cast<uintptr_t>(p.k_slab) % 16 == 0) &&
-                       (reinterpret_cast<uintptr_t>(p.v_slab) % 16 == 0) &&
-                       (reinterpret_cast<uintptr_t>(p.q) % 16 == 0) &&
-                       (reinterpret_cast<uintptr_t>(p.out) % 16 == 0) &&
-                       (p.block_stride % 8 == 0);
-  if (!aligned || p.bs < 16) return false;
+  if (!DecodeMfmaCovers(p)) return false;
   // 32-token tiles (two MFMA halves per tile, double-buffered) measured best
   // on C4; EHIP_DECODE_TILE=16 selects one half per tile (fewer registers).
   const char* tile = std::getenv("EHIP_DECODE_TILE");

@@ -109,8 +109,8 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
   const int hgi = wave / RG;  // and head group
 
   const PrefillItem it = p.items[blockIdx.x];
-  const int hk = it.hk_split & ((1 << kHkBits) - 1);
-  const int split = it.hk_split >> kHkBits;
+  const int hk = UnpackHk(it.hk_split);
+  const int split = UnpackSplit(it.hk_split);
   const int P = it.past;       // cached keys before the chunk
   const int T = it.chunk;      // chunk rows
   const int q0 = it.q0;        // first chunk row of this workgroup

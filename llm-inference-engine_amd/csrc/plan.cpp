@@ -234,13 +234,17 @@ void FinishPlan(const ehip_geometry& g, Plan* plan, bool allow_joint,
     if (rd.nsplit > 1) plan->merge_rows.push_back(static_cast<int32_t>(r));
   }
   plan->partials = split_base * g.kv_heads;
+  for (size_t r = 0; r < n; ++r)
+    if (plan->rows[r].nsplit >= (1 << kSplitBits)) plan->partials = -1;  // rejected by BuildPlan
 
   plan->items.clear();
   plan->items.reserve(ranges.size() * g.kv_heads);
   for (size_t i = 0; i < ranges.size(); ++i) {
     const KeyRange& kr = ranges[i];
+    const bool last = kr.b < 0 && kr.te == plan->rows[kr.a].length;
     for (int32_t hk = 0; hk < g.kv_heads; ++hk)
-      plan->items.push_back(WorkItem{kr.a, kr.b, kr.tb, kr.te, PackHkSplit(hk, split_of[i]),
+      plan->items.push_back(WorkItem{kr.a, kr.b, kr.tb, kr.te,
+                                     PackHkSplit(hk, split_of[i]) | (last ? kLastRangeFlag : 0),
                                      plan->rows[kr.a].table_off, 0, 0});
   }
   plan->joint_items = static_cast<int64_t>(n_joint_ranges) * g.kv_heads;
@@ -466,6 +470,10 @@ int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::
   }
   // The INT8 decode kernel serves one row per item (no joint items).
   FinishPlan(g, plan, g.kv_dtype != EHIP_KV_INT8, &skip);
+  if (plan->partials < 0)
+    return Fail(err, EHIP_UNIMPLEMENTED, "a row needs %lld or more key splits",
+                int64_t{1} << kSplitBits);
+  plan->all_decode = static_cast<int64_t>(plan->rows.size()) == B && plan->prefill.empty();
   return EHIP_OK;
 }
 

@@ -76,9 +76,18 @@ struct PrefillItem {
 };
 
 constexpr int kMaxJointRows = 2;
+// The packed (kv head, split) word of a work item: kv head in bits 0-11,
+// split in bits 12-28, and bit 30 set on the item whose key range ends at its
+// row's last key (the item that appends the row's new token in the fused
+// append + attention launch).
 constexpr int kHkBits = 12;
+constexpr int kSplitBits = 17;
+constexpr int32_t kLastRangeFlag = int32_t{1} << 30;
 
-inline int32_t PackHkSplit(int32_t hk, int32_t split) { return hk | (split << kHkBits); }
+constexpr int32_t PackHkSplit(int32_t hk, int32_t split) { return hk | (split << kHkBits); }
+constexpr int32_t UnpackHk(int32_t v) { return v & ((1 << kHkBits) - 1); }
+constexpr int32_t UnpackSplit(int32_t v) { return (v >> kHkBits) & ((1 << kSplitBits) - 1); }
+constexpr bool IsLastRange(int32_t v) { return (v & kLastRangeFlag) != 0; }
 
 // Rows of one step landing in one block (INT8 append): the block, the first
 // new row's offset in it, the row count and where its row indices start in
@@ -106,6 +115,7 @@ struct Plan {
   int64_t joint_items = 0;
   int64_t shared_tokens = 0;        // sum over groups of the jointly read prefix
   bool any_split = false;           // some decode row has more than one split (merge needed)
+  bool all_decode = false;          // every row is its sequence's only new token (T_b == 1)
 };
 
 // Geometry validation shared by every entry point. Returns a StatusCode and

@@ -106,6 +106,7 @@ def lib():
             "ehip_step_kv_append_int8": [_vp, _vp, _vp, _vp, _vp, _vp, _vp],
             "ehip_step_attention_int8": [_vp, _vp, _vp, _vp, _vp, _vp, _vp],
             "ehip_step_attention": [_vp, _vp, _vp, _vp, _vp],
+            "ehip_step_append_attention": [_vp, _vp, _vp, _vp, _vp, _vp, _vp],
             "ehip_step_info": [_vp, _I64P, _I64P, _I64P],
             "ehip_plan_counts": [C.POINTER(Geometry), C.POINTER(StepDesc), _I64P, _I64P, _I64P,
                                  C.POINTER(C.c_int32), _I64P, _I64P],
@@ -329,6 +330,10 @@ class Context:
     def step_attention_int8(self, q, k_slab, v_slab, k_scale, v_scale, out) -> int:
         return lib().ehip_step_attention_int8(self.h, q.ptr, k_slab.ptr, v_slab.ptr,
                                               k_scale.ptr, v_scale.ptr, out.ptr)
+
+    def step_append_attention(self, src_k, src_v, q, k_slab, v_slab, out) -> int:
+        return lib().ehip_step_append_attention(self.h, src_k.ptr, src_v.ptr, q.ptr, k_slab.ptr,
+                                                v_slab.ptr, out.ptr)
 
     def step_attention(self, q, k_slab, v_slab, out) -> int:
         return lib().ehip_step_attention(self.h, q.ptr, k_slab.ptr, v_slab.ptr, out.ptr)

@@ -1,0 +1,112 @@
+"""ehip_step_append_attention: the step's KV append and attention in one
+launch for all-decode bf16 steps (the item that ends at a row's last key
+stores the row's new K/V and uses them directly), and the two-launch order
+for every other step. Either way the slabs must equal the oracle's append bit
+for bit and the outputs meet the decode bar against the reference on the same
+bf16-rounded cache (1e-4 relative per output vector, the reference allclose);
+fused and separate launches agree to within that bar."""
+import numpy as np
+import pytest
+
+from gpu_util import max_abs, new_rows, rel_norm, seeded_pool
+from paged_util import allclose_ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _workload(ehip_mod, H, Hkv, d, bs, lens, seed, dtype=None, qlens=None):
+    from ehip import workloads
+    rng = np.random.default_rng(seed)
+    lens = np.asarray(lens, np.int64)
+    qlens = np.ones(len(lens), np.int32) if qlens is None else np.asarray(qlens, np.int32)
+    need = (lens + bs - 1) // bs
+    pool = int(np.ceil(1.25 * need.sum())) + 2
+    tables, _ = workloads._tables_from_pool(need, pool, rng)
+    return workloads._finish("fused", H, Hkv, d, bs, dtype if dtype is not None else ehip_mod.KV_BF16,
+                             1, qlens, lens, tables, pool, 0.5)
+
+
+def _run(gctx, ehip_mod, orc, w, fused, seed=13):
+    H, Hkv, d, bs = w.heads, w.kv_heads, w.head_dim, w.block_size
+    bf16 = w.kv_dtype == ehip_mod.KV_BF16
+    g = ehip_mod.geometry(H, Hkv, d, bs, w.kv_dtype, w.pool_blocks, w.scale)
+    st = ehip_mod.StepArrays(w.query_lens, w.context_lens, w.tables, w.slot_mapping)
+    assert gctx.step_upload(g, st) == 0, gctx.last_error()
+    kp, vp = seeded_pool(orc, w, seed)
+    kn, vn, q = new_rows(orc, w, seed + 100)
+    k0 = orc.to_bf16_bits(kp) if bf16 else kp
+    v0 = orc.to_bf16_bits(vp) if bf16 else vp
+    dk, dv = gctx.to_device(k0), gctx.to_device(v0)
+    dq, dkn, dvn = gctx.to_device(q), gctx.to_device(kn), gctx.to_device(vn)
+    out = gctx.alloc(q.nbytes)
+    if fused:
+        assert gctx.step_append_attention(dkn, dvn, dq, dk, dv, out) == 0, gctx.last_error()
+    else:
+        assert gctx.step_kv_append(dkn, dvn, dk, dv) == 0
+        assert gctx.step_attention(dq, dk, dv, out) == 0
+    gctx.sync()
+    got = out.download(np.float32, q.shape)
+    kd, vd = dk.download(k0.dtype, k0.shape), dv.download(v0.dtype, v0.shape)
+    # Oracle: the append bit for bit, then the reference on that cache.
+    orc.kv_scatter(kn, vn, w.slot_mapping, Hkv, d, bs, k0, v0)
+    assert np.array_equal(kd.view(np.uint8), k0.view(np.uint8))
+    assert np.array_equal(vd.view(np.uint8), v0.view(np.uint8))
+    kr = orc.bf16_bits_to_f32(kd) if bf16 else kd
+    vr = orc.bf16_bits_to_f32(vd) if bf16 else vd
+    cu = np.concatenate([[0], np.cumsum(w.query_lens)]).astype(np.int32)
+    kseq = [orc.paged_to_contig(kr, t, int(L), Hkv, d, bs) for t, L in zip(w.tables, w.context_lens)]
+    vseq = [orc.paged_to_contig(vr, t, int(L), Hkv, d, bs) for t, L in zip(w.tables, w.context_lens)]
+    ref = orc.prefill_varlen(q, cu, kseq, vseq, H, Hkv, d, w.scale, isa=orc.ISA_AVX2)
+    for b in (dk, dv, dq, dkn, dvn, out):
+        b.free()
+    return got, ref
+
+
+def _check(got, ref):
+    assert rel_norm(got, ref) <= 1e-4, rel_norm(got, ref)
+    assert allclose_ref(got, ref, 1e-4, 1e-5)
+
+
+@pytest.mark.parametrize("H,Hkv,d,bs", [(32, 8, 128, 16), (64, 8, 128, 16), (14, 2, 64, 16),
+                                        (8, 8, 128, 32), (16, 2, 64, 64), (8, 1, 128, 16)])
+def test_fused_append_decode_step(gctx, ehip_mod, orc, H, Hkv, d, bs):
+    """Ragged decode rows, including rows of one key (only the new token),
+    rows whose last key range holds just the new key, and long split rows."""
+    lens = [1, 2, 17, 33, 129, 1025, 1026, 2049, 4000, 64, 65, 8193]
+    w = _workload(ehip_mod, H, Hkv, d, bs, lens, seed=H + d + bs)
+    fused, ref = _run(gctx, ehip_mod, orc, w, fused=True)
+    _check(fused, ref)
+    separate, _ = _run(gctx, ehip_mod, orc, w, fused=False)
+    assert rel_norm(fused, separate) <= 1e-5
+
+
+def test_fused_append_with_joint_items(gctx, ehip_mod, orc):
+    """The C4 shape with pair-shared prefixes (joint items never cover a row's
+    last key: only the rows' own items append)."""
+    from ehip import workloads
+    w = workloads.c4(num_seqs=24, share_frac=0.3)
+    rc, rows, items, partials, split, joint, shared = ehip_mod.plan_counts(
+        ehip_mod.geometry(w.heads, w.kv_heads, w.head_dim, w.block_size, w.kv_dtype,
+                          w.pool_blocks, w.scale),
+        ehip_mod.StepArrays(w.query_lens, w.context_lens, w.tables, w.slot_mapping), joint=True)
+    assert rc == 0 and joint > 0
+    fused, ref = _run(gctx, ehip_mod, orc, w, fused=True, seed=41)
+    _check(fused, ref)
+
+
+@pytest.mark.parametrize("case", ["fp32", "chunk", "valu"])
+def test_append_attention_falls_back_to_two_launches(gctx, ehip_mod, orc, case, monkeypatch):
+    """fp32 slabs, a step with a prefill chunk, and the VALU decode kernel take
+    the append launch then the attention launch, with the same results."""
+    if case == "fp32":
+        w = _workload(ehip_mod, 14, 2, 64, 16, [513, 17, 1], seed=5, dtype=ehip_mod.KV_F32)
+    elif case == "chunk":
+        w = _workload(ehip_mod, 32, 8, 128, 16, [300, 40, 1000], seed=6, qlens=[1, 20, 1])
+    else:
+        monkeypatch.setenv("EHIP_DECODE_KERNEL", "valu")
+        w = _workload(ehip_mod, 32, 8, 128, 16, [300, 40, 1000], seed=7)
+    got, ref = _run(gctx, ehip_mod, orc, w, fused=True)
+    rows = np.repeat(w.query_lens, w.query_lens) == 1
+    _check(got[rows], ref[rows])
+    if (~rows).any():  # chunk rows: bf16 Q and P on the matrix cores
+        assert rel_norm(got[~rows], ref[~rows]) <= 1e-2
