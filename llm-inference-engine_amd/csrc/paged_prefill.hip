@@ -15,13 +15,16 @@
 // groups x two head groups). Each wavefront keeps 4 (row block, head)
 // accumulator blocks, so every K and V operand read from LDS feeds four
 // MFMAs and every 16 KiB K/V tile staged in LDS serves 4M (row, head) pairs.
-// Keys stream in 32-token tiles staged in LDS (double-buffered, loaded one
-// tile ahead into registers):
-//   - K row-major [token][d], rows padded by 16 bytes, so the MFMA A operand
-//     (16 tokens x 8 elements per lane) is one conflict-free 16-byte read;
-//   - V transposed [d][token'], token' a permutation that puts the 8 tokens a
-//     lane contracts over next to each other, rows padded to 80 bytes, so
-//     the PV B operand is one 16-byte read as well.
+// Keys stream in 32-token tiles staged in LDS (double-buffered, loaded two
+// tiles ahead into registers). K and V tiles are both row-major
+// [token][d] with rows padded to 288 bytes (256 + 32), written with 16-byte
+// stores. The gfx950 LDS has 64 banks for reads and serves a 16-byte read in
+// passes of 16 lanes: with a row stride of 72 dwords (8 mod 64) the MFMA A
+// operand of K (16 tokens x 8 elements per lane, one 16-byte read) and the
+// PV B operand of V read with ds_read_b64_tr_b16 (two transposed 8-byte reads
+// per lane: 4 tokens x 16 columns of 4 rows per 16-lane group) are both free
+// of bank conflicts, and the 16-byte stores (8 lanes per pass on 32 banks)
+// write 128 contiguous bytes per pass.
 // S^T = K Q^T (v_mfma_f32_16x16x32_bf16, A = K, B = Q^T): lane l holds
 // scores of tokens 4*(l/16) + i of each 16-token half for query row l % 16,
 // which is exactly the A-operand layout P needs for O = P V once the two
@@ -39,9 +42,14 @@ namespace ehip {
 namespace {
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 
 constexpr int kTile = 32;    // keys per tile
+// Block ids of an item's key range staged in LDS at item start (2 KiB): tile
+// addresses then come from LDS instead of a global table read issued right
+// before each tile's K/V loads. Ids past the window are read from the table.
+constexpr int kTabWindow = 512;
 constexpr float kRefSlack = 8.f;
 constexpr int kWaves = 4;
 
@@ -58,28 +66,32 @@ int PrefillHeadsPerWave() {
   return hb;
 }
 
+// ds_read_b64_tr_b16: lane i of each 16-lane group receives element i % 4 of
+// the 8 bytes addressed by lanes 4j + i / 4 of the group, for j = 0..3.
+__device__ __forceinline__ bf16x4_t TransposedRead(const unsigned char* p) {
+  typedef __attribute__((ext_vector_type(4))) short s16x4_t;
+  const s16x4_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4_t*)(p));
+  return __builtin_bit_cast(bf16x4_t, r);
+}
+
 __device__ __forceinline__ float ShflF(float x, int src_lane) {
   return __int_as_float(__builtin_amdgcn_ds_bpermute(src_lane << 2, __float_as_int(x)));
 }
 
-// Position of token t (0..31) of a tile in the transposed V rows: the MFMA
-// contraction index k = 8*kq + i of lane group kq covers tokens 4kq+i (i < 4)
-// of the first half and 16+4kq+i-4 (i >= 4) of the second.
-__device__ __forceinline__ int VPerm(int t) {
-  return t < 16 ? (t >> 2) * 8 + (t & 3) : ((t - 16) >> 2) * 8 + 4 + (t & 3);
-}
-
 template <int D>
 struct PrefillSmem {
-  static constexpr int KROW = D * 2 + 16;      // bytes per K row (padded)
-  static constexpr int VROW = kTile * 2 + 16;  // bytes per transposed V row (padded)
-  static constexpr int KBYTES = kTile * KROW;
-  static constexpr int VBYTES = D * VROW;
-  static constexpr int BYTES = 2 * (KBYTES + VBYTES);  // double-buffered
+  static constexpr int ROW = D * 2 + 32;  // bytes per K or V row (padded)
+  static constexpr int TILE = kTile * ROW;
+  static constexpr int BYTES = 2 * 2 * TILE;  // K and V, double-buffered
   // Q^T operands of every wavefront (when kept in LDS):
   // [wave][head][chunk][lane] x 16 bytes.
   static constexpr int QBYTES = kWaves * 4 * (D / 32) * 64 * 16;
-  static constexpr int TOTAL = BYTES + QBYTES;
+  // The item's block-table slice (up to kTabWindow ids), after the tiles (and
+  // the Q^T operands when those are in LDS).
+  static constexpr int TAB_BYTES = kTabWindow * 4;
+  static constexpr int SMALL = BYTES + TAB_BYTES;           // Q^T in registers
+  static constexpr int TOTAL = BYTES + QBYTES + TAB_BYTES;  // Q^T in LDS
 };
 
 template <int D, int G, int HB>
@@ -151,8 +163,8 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
     }
   }
 
-  // Tile loads: thread -> (token pair, 8-element group) for V and (token,
-  // 8-element group) for K, two of each per tile.
+  // Tile loads: thread -> (token, 8-element group), two K and two V vectors
+  // per tile, at the same slab offsets.
   const uint16_t* kslab = static_cast<const uint16_t*>(p.k_slab) + int64_t{hk} * bs * D;
   const uint16_t* vslab = static_cast<const uint16_t*>(p.v_slab) + int64_t{hk} * bs * D;
   constexpr int EG = D / 8;  // 8-element groups per row
@@ -160,10 +172,8 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
   // of V (K0, K1, V0, V1), so global loads run two tiles ahead of compute.
   uint4 stA0, stA1, stA2, stA3, stB0, stB1, stB2, stB3;
   bool bad = false;
-  // Thread -> K vectors u = tid and tid + 256 (token u / EG, group u % EG);
-  // V token pair vp = tid % 16 (tokens 2vp, 2vp + 1), group tid / 16.
+  // Thread -> K and V vectors u = tid and tid + 256 (token u / EG, group u % EG).
   const int tk0 = tid / EG, tk1 = (tid + kWaves * 64) / EG, ek = tid % EG;
-  const int vp = tid % 16, ev = tid / 16;
   // bs is a power of two: block index and slot by shift and mask. A 32-key
   // tile spans at most two blocks (bs >= 16, tiles start at multiples of
   // 32): their two ids are read once per wavefront and selected per thread,
@@ -171,6 +181,8 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
   // (the host routes slabs of 4 GiB or more away from this kernel).
   const int bsh = __builtin_ctz(bs), bmask = bs - 1;
   const int32_t* tab = p.table + it.table_off;
+  int32_t* tab_lds = reinterpret_cast<int32_t*>(smem + SM::BYTES + (QL ? SM::QBYTES : 0));
+  const int kb_first = key0 >> __builtin_ctz(bs);
   const uint32_t nblk = static_cast<uint32_t>(p.slab_blocks);
   const int last_blk = (key1 - 1) >> bsh;
   const uint32_t stride_b = static_cast<uint32_t>(p.block_stride) * 2u;
@@ -178,30 +190,28 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kslab), 0, 0xFFFFFFFFu, 0x00020000);
   const __amdgpu_buffer_rsrc_t rv =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vslab), 0, 0xFFFFFFFFu, 0x00020000);
-  const uint32_t ko = static_cast<uint32_t>(ek * 16), vo = static_cast<uint32_t>(ev * 16);
+  const uint32_t ko = static_cast<uint32_t>(ek * 16);
 #define EHIP_PF_GLOAD(ST, K0)                                                                  \
   do {                                                                                      \
     const int kb0 = (K0) >> bsh;                                                            \
-    int id0 = __builtin_amdgcn_readfirstlane(tab[kb0]);                                     \
-    int id1 = __builtin_amdgcn_readfirstlane(tab[min(kb0 + 1, last_blk)]);                   \
+    const int kb1 = min(kb0 + 1, last_blk);                                                 \
+    int id0 = __builtin_amdgcn_readfirstlane(kb0 - kb_first < kTabWindow ? tab_lds[kb0 - kb_first] \
+                                                                         : tab[kb0]);        \
+    int id1 = __builtin_amdgcn_readfirstlane(kb1 - kb_first < kTabWindow ? tab_lds[kb1 - kb_first] \
+                                                                         : tab[kb1]);        \
     const bool okb = static_cast<uint32_t>(id0) < nblk && static_cast<uint32_t>(id1) < nblk; \
     bad = bad | !okb;                                                                        \
     id0 = okb ? id0 : 0;                                                                     \
     id1 = okb ? id1 : 0;                                                                     \
     const int pk0 = min((K0) + tk0, key1 - 1), pk1 = min((K0) + tk1, key1 - 1);             \
-    const int pv0 = min((K0) + 2 * vp, key1 - 1), pv1 = min((K0) + 2 * vp + 1, key1 - 1);    \
     const uint32_t a0 = static_cast<uint32_t>((pk0 >> bsh) != kb0 ? id1 : id0) * stride_b +  \
                         static_cast<uint32_t>((pk0 & bmask) * D * 2) + ko;                   \
     const uint32_t a1 = static_cast<uint32_t>((pk1 >> bsh) != kb0 ? id1 : id0) * stride_b +  \
                         static_cast<uint32_t>((pk1 & bmask) * D * 2) + ko;                   \
-    const uint32_t a2 = static_cast<uint32_t>((pv0 >> bsh) != kb0 ? id1 : id0) * stride_b +  \
-                        static_cast<uint32_t>((pv0 & bmask) * D * 2) + vo;                   \
-    const uint32_t a3 = static_cast<uint32_t>((pv1 >> bsh) != kb0 ? id1 : id0) * stride_b +  \
-                        static_cast<uint32_t>((pv1 & bmask) * D * 2) + vo;                   \
     ST##0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, a0, 0, 0)); \
     ST##1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, a1, 0, 0)); \
-    ST##2 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, a2, 0, 0)); \
-    ST##3 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, a3, 0, 0)); \
+    ST##2 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, a0, 0, 0)); \
+    ST##3 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, a1, 0, 0)); \
   } while (0)
 
   // Per head state. Scores/probabilities live in the S^T layout (row n =
@@ -220,34 +230,23 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
   const float slack = kRefSlack / sl2;     // the rescale slack in raw score units
 
   const int ntiles = (key1 - key0 + kTile - 1) / kTile;
-  const int vtp = VPerm(2 * vp);
-  // Writes a staged tile into LDS buffer BUF: K row-major; V packed into
-  // (t, t+1) dwords (lo: element 2w, hi: element 2w + 1 of the pair) and
-  // written transposed, V^T[e][perm(t)], with perm(2vp + 1) = perm(2vp) + 1.
-#define EHIP_PF_STORE(ST, BUF)                                                     \
-  do {                                                                           \
-    unsigned char* kw = smem + (BUF) * (SM::KBYTES + SM::VBYTES);                 \
-    unsigned char* vw = kw + SM::KBYTES;                                          \
-    *reinterpret_cast<uint4*>(kw + tk0 * SM::KROW + ek * 16) = ST##0;             \
-    *reinterpret_cast<uint4*>(kw + tk1 * SM::KROW + ek * 16) = ST##1;             \
-    const uint4 va = ST##2, vb2 = ST##3;                                          \
-    const uint32_t a[4] = {va.x, va.y, va.z, va.w};                               \
-    const uint32_t b[4] = {vb2.x, vb2.y, vb2.z, vb2.w};                           \
-    _Pragma("unroll") for (int w = 0; w < 4; ++w) {                               \
-      const uint32_t lo = (a[w] & 0xFFFFu) | (b[w] << 16);                        \
-      const uint32_t hi = (a[w] >> 16) | (b[w] & 0xFFFF0000u);                    \
-      const int e = ev * 8 + 2 * w;                                               \
-      *reinterpret_cast<uint32_t*>(vw + e * SM::VROW + vtp * 2) = lo;             \
-      *reinterpret_cast<uint32_t*>(vw + (e + 1) * SM::VROW + vtp * 2) = hi;       \
-    }                                                                             \
+  // Writes a staged tile into LDS buffer BUF (K then V, both row-major).
+#define EHIP_PF_STORE(ST, BUF)                                            \
+  do {                                                                  \
+    unsigned char* kw = smem + (BUF) * (2 * SM::TILE);                   \
+    unsigned char* vw = kw + SM::TILE;                                   \
+    *reinterpret_cast<uint4*>(kw + tk0 * SM::ROW + ek * 16) = ST##0;     \
+    *reinterpret_cast<uint4*>(kw + tk1 * SM::ROW + ek * 16) = ST##1;     \
+    *reinterpret_cast<uint4*>(vw + tk0 * SM::ROW + ek * 16) = ST##2;     \
+    *reinterpret_cast<uint4*>(vw + tk1 * SM::ROW + ek * 16) = ST##3;     \
   } while (0)
   auto compute_tile = [&](int tile, int buf) __attribute__((always_inline)) {
     const int k0 = key0 + tile * kTile;
     // Wavefront-uniform: a tile wholly past this wavefront's last row (the
     // other row groups' diagonal) is skipped.
     if (k0 < wend) {
-      const unsigned char* kb = smem + buf * (SM::KBYTES + SM::VBYTES);
-      const unsigned char* vb = kb + SM::KBYTES;
+      const unsigned char* kb = smem + buf * (2 * SM::TILE);
+      const unsigned char* vb = kb + SM::TILE;
       // Keys past this lane's query position (or past the workgroup's last
       // key) are masked.
       const bool diag = k0 + kTile > P + r0 || k0 + kTile > key1;
@@ -264,7 +263,7 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
 #pragma unroll
         for (int h2 = 0; h2 < 2; ++h2)
           ka[h2] = __builtin_bit_cast(
-              bf16x8_t, *reinterpret_cast<const uint4*>(kb + (16 * h2 + n) * SM::KROW +
+              bf16x8_t, *reinterpret_cast<const uint4*>(kb + (16 * h2 + n) * SM::ROW +
                                                         (c * 32 + kq * 8) * 2));
 #pragma unroll
         for (int hh = 0; hh < HB; ++hh) {
@@ -329,11 +328,18 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
             for (int nb = 0; nb < NB; ++nb) o[hh][nb][i] *= ar;
           }
       }
-      // O += P V: each V operand read once, HB MFMAs.
+      // O += P V: each V operand read once, HB MFMAs. The B operand of lane
+      // (n, kq) is V[token][16nb + n] over tokens 4kq..4kq+3 and
+      // 16+4kq..16+4kq+3 (the tokens its P values cover): two transposed
+      // reads, in which lane s of each 16-lane group addresses token row
+      // 4kq + s/4 (+16), columns 16nb + 4(s%4) .. +3, and lane n receives
+      // column 16nb + n of the group's 4 rows.
+      const unsigned char* vl = vb + (4 * kq + (n >> 2)) * SM::ROW + (n & 3) * 8;
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
-        const bf16x8_t vbv = __builtin_bit_cast(
-            bf16x8_t, *reinterpret_cast<const uint4*>(vb + (16 * nb + n) * SM::VROW + kq * 16));
+        const bf16x4_t v0 = TransposedRead(vl + nb * 32);
+        const bf16x4_t v1 = TransposedRead(vl + 16 * SM::ROW + nb * 32);
+        const bf16x8_t vbv = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
         for (int hh = 0; hh < HB; ++hh)
           o[hh][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[hh], vbv, o[hh][nb], 0, 0, 0);
@@ -342,6 +348,11 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
   };
   // Tile t is staged in slot t % 2 and LDS buffer t % 2; its slot is
   // refilled with tile t + 2 right after it is written to LDS.
+  {
+    const int nwin = min(last_blk - kb_first + 1, kTabWindow);
+    for (int i = tid; i < nwin; i += kWaves * 64) tab_lds[i] = tab[kb_first + i];
+    __syncthreads();
+  }
   EHIP_PF_GLOAD(stA, key0);
   if (ntiles > 1) EHIP_PF_GLOAD(stB, key0 + kTile);
   for (int tile = 0; tile < ntiles; tile += 2) {
@@ -418,7 +429,7 @@ bool LaunchPrefillMfma(const PrefillParams& p, hipStream_t stream, hipError_t* e
       hipLaunchKernelGGL((PrefillMfmaBf16<DD, GG, 4>), grid, block,                       \
                          PrefillSmem<DD>::TOTAL, stream, p);                              \
     else                                                                                  \
-      hipLaunchKernelGGL((PrefillMfmaBf16<DD, GG, 2>), grid, block, PrefillSmem<DD>::BYTES, \
+      hipLaunchKernelGGL((PrefillMfmaBf16<DD, GG, 2>), grid, block, PrefillSmem<DD>::SMALL, \
                          stream, p);                                                      \
     *err = hipGetLastError();                                                             \
     return true;                                                                          \
