@@ -46,10 +46,6 @@ typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 
 constexpr int kTile = 32;    // keys per tile
-// Block ids of an item's key range staged in LDS at item start (2 KiB): tile
-// addresses then come from LDS instead of a global table read issued right
-// before each tile's K/V loads. Ids past the window are read from the table.
-constexpr int kTabWindow = 512;
 constexpr float kRefSlack = 8.f;
 constexpr int kWaves = 4;
 
@@ -75,8 +71,25 @@ __device__ __forceinline__ bf16x4_t TransposedRead(const unsigned char* p) {
   return __builtin_bit_cast(bf16x4_t, r);
 }
 
-__device__ __forceinline__ float ShflF(float x, int src_lane) {
-  return __int_as_float(__builtin_amdgcn_ds_bpermute(src_lane << 2, __float_as_int(x)));
+// Reductions over the 4 lanes of a row (l, l ^ 16, l ^ 32, l ^ 48) with the
+// gfx950 swap permutes, without an LDS round trip. With both operands set to
+// x, v_permlane32_swap leaves (x[l % 32], x[32 + l % 32]) in lane l and
+// v_permlane16_swap leaves (x of the even row, x of the odd row) of the
+// lane's row pair; combining the two gives every lane the same value.
+template <typename Op>
+__device__ __forceinline__ float RowReduce(float x, Op op) {
+  const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  x = op(__uint_as_float(h[0]), __uint_as_float(h[1]));
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float RowMax(float x) {
+  return RowReduce(x, [](float a, float b) { return fmaxf(a, b); });
+}
+__device__ __forceinline__ float RowSum(float x) {
+  return RowReduce(x, [](float a, float b) { return a + b; });
 }
 
 template <int D>
@@ -87,11 +100,8 @@ struct PrefillSmem {
   // Q^T operands of every wavefront (when kept in LDS):
   // [wave][head][chunk][lane] x 16 bytes.
   static constexpr int QBYTES = kWaves * 4 * (D / 32) * 64 * 16;
-  // The item's block-table slice (up to kTabWindow ids), after the tiles (and
-  // the Q^T operands when those are in LDS).
-  static constexpr int TAB_BYTES = kTabWindow * 4;
-  static constexpr int SMALL = BYTES + TAB_BYTES;           // Q^T in registers
-  static constexpr int TOTAL = BYTES + QBYTES + TAB_BYTES;  // Q^T in LDS
+  static constexpr int SMALL = BYTES;           // Q^T in registers
+  static constexpr int TOTAL = BYTES + QBYTES;  // Q^T in LDS
 };
 
 template <int D, int G, int HB>
@@ -180,9 +190,12 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
   // and K/V are read through buffer descriptors with 32-bit byte offsets
   // (the host routes slabs of 4 GiB or more away from this kernel).
   const int bsh = __builtin_ctz(bs), bmask = bs - 1;
-  const int32_t* tab = p.table + it.table_off;
-  int32_t* tab_lds = reinterpret_cast<int32_t*>(smem + SM::BYTES + (QL ? SM::QBYTES : 0));
-  const int kb_first = key0 >> __builtin_ctz(bs);
+  // The block table is read-only during the launch and every index into it
+  // is wavefront-uniform: scalar loads through the constant address space
+  // (a vector or flat load would make the wait for the ids also wait for
+  // the K/V loads still in flight for the other staging slot).
+  const __attribute__((address_space(4))) int32_t* tab =
+      (const __attribute__((address_space(4))) int32_t*)(p.table) + it.table_off;
   const uint32_t nblk = static_cast<uint32_t>(p.slab_blocks);
   const int last_blk = (key1 - 1) >> bsh;
   const uint32_t stride_b = static_cast<uint32_t>(p.block_stride) * 2u;
@@ -193,12 +206,10 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
   const uint32_t ko = static_cast<uint32_t>(ek * 16);
 #define EHIP_PF_GLOAD(ST, K0)                                                                  \
   do {                                                                                      \
-    const int kb0 = (K0) >> bsh;                                                            \
+    const int kb0 = min((K0) >> bsh, last_blk);                                             \
     const int kb1 = min(kb0 + 1, last_blk);                                                 \
-    int id0 = __builtin_amdgcn_readfirstlane(kb0 - kb_first < kTabWindow ? tab_lds[kb0 - kb_first] \
-                                                                         : tab[kb0]);        \
-    int id1 = __builtin_amdgcn_readfirstlane(kb1 - kb_first < kTabWindow ? tab_lds[kb1 - kb_first] \
-                                                                         : tab[kb1]);        \
+    int id0 = tab[kb0];                                                                      \
+    int id1 = tab[kb1];                                                                      \
     const bool okb = static_cast<uint32_t>(id0) < nblk && static_cast<uint32_t>(id1) < nblk; \
     bad = bad | !okb;                                                                        \
     id0 = okb ? id0 : 0;                                                                     \
@@ -293,8 +304,7 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
         float mx = fmaxf(s[hh][0][0], s[hh][1][0]);
 #pragma unroll
         for (int i = 1; i < 4; ++i) mx = fmaxf(mx, fmaxf(s[hh][0][i], s[hh][1][i]));
-        mx = fmaxf(mx, ShflF(mx, lane ^ 16));
-        mx = fmaxf(mx, ShflF(mx, lane ^ 32));
+        mx = RowMax(mx);
         // Lazy rescaling (FlashAttention-3, Shah et al. 2024): the running
         // reference (raw score units) moves only when the tile's max exceeds
         // it by more than kRefSlack in log2 units, so probabilities stay below
@@ -316,24 +326,23 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
           }
         l[hh] = l[hh] * alpha[hh] + ps;  // lane-partial over this lane's tokens
       }
-      // Rescale the output rows (D layout: row 4kq+i) by their row's alpha,
-      // which lives in lanes l % 16 == row; skipped when no max moved.
+      // Rescale the output (O^T: this lane's registers all belong to its
+      // row n) by the row's alpha; skipped when no max moved.
       if (__any(moved)) {
 #pragma unroll
         for (int hh = 0; hh < HB; ++hh)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float ar = ShflF(alpha[hh], 4 * kq + i);
+          for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-            for (int nb = 0; nb < NB; ++nb) o[hh][nb][i] *= ar;
-          }
+            for (int i = 0; i < 4; ++i) o[hh][nb][i] *= alpha[hh];
       }
-      // O += P V: each V operand read once, HB MFMAs. The B operand of lane
-      // (n, kq) is V[token][16nb + n] over tokens 4kq..4kq+3 and
+      // O^T += V^T P^T: each V operand read once, HB MFMAs. The A operand of
+      // lane (n, kq) is V[token][16nb + n] over tokens 4kq..4kq+3 and
       // 16+4kq..16+4kq+3 (the tokens its P values cover): two transposed
       // reads, in which lane s of each 16-lane group addresses token row
       // 4kq + s/4 (+16), columns 16nb + 4(s%4) .. +3, and lane n receives
-      // column 16nb + n of the group's 4 rows.
+      // column 16nb + n of the group's 4 rows. The B operand is P^T, which is
+      // this lane's P values as they are (row n, the same 8 tokens).
       const unsigned char* vl = vb + (4 * kq + (n >> 2)) * SM::ROW + (n & 3) * 8;
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
@@ -342,70 +351,64 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
         const bf16x8_t vbv = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
         for (int hh = 0; hh < HB; ++hh)
-          o[hh][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[hh], vbv, o[hh][nb], 0, 0, 0);
+          o[hh][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vbv, pa[hh], o[hh][nb], 0, 0, 0);
       }
     }
   };
   // Tile t is staged in slot t % 2 and LDS buffer t % 2; its slot is
   // refilled with tile t + 2 right after it is written to LDS.
-  {
-    const int nwin = min(last_blk - kb_first + 1, kTabWindow);
-    for (int i = tid; i < nwin; i += kWaves * 64) tab_lds[i] = tab[kb_first + i];
-    __syncthreads();
-  }
+  // The loop waits for one slot's loads while the other slot's are still in
+  // flight (vmcnt counts loads in issue order). That holds only if every path
+  // into the loop head has issued slot A's loads before slot B's: so the
+  // loads run unconditionally (tiles past the item's end re-read its last
+  // rows, clamped, and an odd last tile's partner is computed as an empty
+  // tile), and the prologue's two loads are kept in order (the scheduler
+  // may otherwise issue B's first, and every wait becomes a wait for all).
   EHIP_PF_GLOAD(stA, key0);
-  if (ntiles > 1) EHIP_PF_GLOAD(stB, key0 + kTile);
+  __builtin_amdgcn_sched_barrier(0);
+  EHIP_PF_GLOAD(stB, key0 + kTile);
   for (int tile = 0; tile < ntiles; tile += 2) {
     EHIP_PF_STORE(stA, 0);
     __syncthreads();
-    if (tile + 2 < ntiles) EHIP_PF_GLOAD(stA, key0 + (tile + 2) * kTile);
+    EHIP_PF_GLOAD(stA, key0 + (tile + 2) * kTile);
     compute_tile(tile, 0);
-    if (tile + 1 >= ntiles) break;
     EHIP_PF_STORE(stB, 1);
     __syncthreads();
-    if (tile + 3 < ntiles) EHIP_PF_GLOAD(stB, key0 + (tile + 3) * kTile);
-    compute_tile(tile + 1, 1);
+    EHIP_PF_GLOAD(stB, key0 + (tile + 3) * kTile);
+    compute_tile(tile + 1, 1);  // no work when tile + 1 == ntiles
   }
 
   // Row sums: each lane holds a partial over its tokens; the 4 lanes of a
-  // row (l % 16 equal) together hold the row total.
+  // row (l % 16 equal) together hold the row total. O^T puts output row n,
+  // columns 16nb + 4kq .. +3 in lane (n, kq): one 16-byte store per block.
 #pragma unroll
   for (int hh = 0; hh < HB; ++hh) {
-    float lt = l[hh];
-    lt += ShflF(lt, lane ^ 16);
-    lt += ShflF(lt, lane ^ 32);
+    const float lt = RowSum(l[hh]);
     const int hg = hgi * HB + hh;  // head within the kv head's group
     const int head = hk * G + hg;
-    if (whole) {
+    if (n < qnw) {
+      if (whole) {
+        const float inv = 1.0f / lt;
+        float* op = p.out + (int64_t{it.row_base + r0 + n} * p.heads + head) * D + 4 * kq;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = 4 * kq + i;  // D-layout row of register i
-        const float inv = 1.0f / ShflF(lt, r);
-        if (r < qnw) {
-          float* op = p.out + (int64_t{it.row_base + r0 + r} * p.heads + head) * D + n;
-#pragma unroll
-          for (int nb = 0; nb < NB; ++nb) op[16 * nb] = o[hh][nb][i] * inv;
-        }
-      }
-    } else {
-      // Split partials: unnormalised output, the reference in log2 units and
-      // the row sum, at the rows' split slots.
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = 4 * kq + i;
-        if (r < qnw) {
-          const RowDesc rd = p.rows[it.row_base + r0 + r];
-          const int64_t pidx = PartialIndex(rd, p.kv_heads, hk, split);
-          float* po = p.part_o + (pidx * G + hg) * D + n;
-#pragma unroll
-          for (int nb = 0; nb < NB; ++nb) po[16 * nb] = o[hh][nb][i];
-        }
-      }
-      if (kq == 0 && n < qnw) {
+        for (int nb = 0; nb < NB; ++nb)
+          *reinterpret_cast<float4*>(op + 16 * nb) =
+              make_float4(o[hh][nb][0] * inv, o[hh][nb][1] * inv, o[hh][nb][2] * inv,
+                          o[hh][nb][3] * inv);
+      } else {
+        // Split partials: unnormalised output, the reference in log2 units
+        // and the row sum, at the row's split slot.
         const RowDesc rd = p.rows[it.row_base + r0 + n];
         const int64_t pidx = PartialIndex(rd, p.kv_heads, hk, split);
-        const float ms = m[hh] == -INFINITY ? -INFINITY : m[hh] * sl2;
-        *reinterpret_cast<float2*>(p.part_ml + (pidx * G + hg) * 2) = make_float2(ms, lt);
+        float* po = p.part_o + (pidx * G + hg) * D + 4 * kq;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+          *reinterpret_cast<float4*>(po + 16 * nb) =
+              make_float4(o[hh][nb][0], o[hh][nb][1], o[hh][nb][2], o[hh][nb][3]);
+        if (kq == 0) {
+          const float ms = m[hh] == -INFINITY ? -INFINITY : m[hh] * sl2;
+          *reinterpret_cast<float2*>(p.part_ml + (pidx * G + hg) * 2) = make_float2(ms, lt);
+        }
       }
     }
   }
