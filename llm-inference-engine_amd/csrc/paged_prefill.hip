@@ -190,12 +190,12 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
   // and K/V are read through buffer descriptors with 32-bit byte offsets
   // (the host routes slabs of 4 GiB or more away from this kernel).
   const int bsh = __builtin_ctz(bs), bmask = bs - 1;
-  // The block table is read-only during the launch and every index into it
-  // is wavefront-uniform: scalar loads through the constant address space
-  // (a vector or flat load would make the wait for the ids also wait for
-  // the K/V loads still in flight for the other staging slot).
-  const __attribute__((address_space(4))) int32_t* tab =
-      (const __attribute__((address_space(4))) int32_t*)(p.table) + it.table_off;
+  // A tile's two block ids are loaded two tiles ahead of its K/V loads, by
+  // vector loads that share the K/V loads' in-order counter (a scalar load
+  // would be waited for right before the K/V loads, and while one is in
+  // flight every LDS wait becomes a wait for it too).
+  const __amdgpu_buffer_rsrc_t rt = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int32_t*>(p.table + it.table_off), 0, 0xFFFFFFFFu, 0x00020000);
   const uint32_t nblk = static_cast<uint32_t>(p.slab_blocks);
   const int last_blk = (key1 - 1) >> bsh;
   const uint32_t stride_b = static_cast<uint32_t>(p.block_stride) * 2u;
@@ -204,12 +204,18 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
   const __amdgpu_buffer_rsrc_t rv =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vslab), 0, 0xFFFFFFFFu, 0x00020000);
   const uint32_t ko = static_cast<uint32_t>(ek * 16);
-#define EHIP_PF_GLOAD(ST, K0)                                                                  \
+#define EHIP_PF_IDLOAD(ID, K0)                                                               \
   do {                                                                                      \
     const int kb0 = min((K0) >> bsh, last_blk);                                             \
-    const int kb1 = min(kb0 + 1, last_blk);                                                 \
-    int id0 = tab[kb0];                                                                      \
-    int id1 = tab[kb1];                                                                      \
+    ID##0 = __builtin_amdgcn_raw_buffer_load_b32(rt, static_cast<uint32_t>(kb0) * 4u, 0, 0); \
+    ID##1 = __builtin_amdgcn_raw_buffer_load_b32(                                            \
+        rt, static_cast<uint32_t>(min(kb0 + 1, last_blk)) * 4u, 0, 0);                      \
+  } while (0)
+#define EHIP_PF_GLOAD(ST, K0, ID)                                                              \
+  do {                                                                                      \
+    const int kb0 = min((K0) >> bsh, last_blk);                                             \
+    int id0 = __builtin_amdgcn_readfirstlane(ID##0);                                         \
+    int id1 = __builtin_amdgcn_readfirstlane(ID##1);                                         \
     const bool okb = static_cast<uint32_t>(id0) < nblk && static_cast<uint32_t>(id1) < nblk; \
     bad = bad | !okb;                                                                        \
     id0 = okb ? id0 : 0;                                                                     \
@@ -364,17 +370,24 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
   // rows, clamped, and an odd last tile's partner is computed as an empty
   // tile), and the prologue's two loads are kept in order (the scheduler
   // may otherwise issue B's first, and every wait becomes a wait for all).
-  EHIP_PF_GLOAD(stA, key0);
+  uint32_t idA0, idA1, idB0, idB1;  // block ids of each slot's next tile
+  EHIP_PF_IDLOAD(idA, key0);
+  EHIP_PF_IDLOAD(idB, key0 + kTile);
+  EHIP_PF_GLOAD(stA, key0, idA);
+  EHIP_PF_IDLOAD(idA, key0 + 2 * kTile);
   __builtin_amdgcn_sched_barrier(0);
-  EHIP_PF_GLOAD(stB, key0 + kTile);
+  EHIP_PF_GLOAD(stB, key0 + kTile, idB);
+  EHIP_PF_IDLOAD(idB, key0 + 3 * kTile);
   for (int tile = 0; tile < ntiles; tile += 2) {
     EHIP_PF_STORE(stA, 0);
     __syncthreads();
-    EHIP_PF_GLOAD(stA, key0 + (tile + 2) * kTile);
+    EHIP_PF_GLOAD(stA, key0 + (tile + 2) * kTile, idA);
+    EHIP_PF_IDLOAD(idA, key0 + (tile + 4) * kTile);
     compute_tile(tile, 0);
     EHIP_PF_STORE(stB, 1);
     __syncthreads();
-    EHIP_PF_GLOAD(stB, key0 + (tile + 3) * kTile);
+    EHIP_PF_GLOAD(stB, key0 + (tile + 3) * kTile, idB);
+    EHIP_PF_IDLOAD(idB, key0 + (tile + 5) * kTile);
     compute_tile(tile + 1, 1);  // no work when tile + 1 == ntiles
   }
 
@@ -414,6 +427,7 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
   }
   if (__any(bad) && lane == 0) atomicOr(p.err, kErrBlockRange);
 #undef EHIP_PF_GLOAD
+#undef EHIP_PF_IDLOAD
 #undef EHIP_PF_STORE
 }
 
