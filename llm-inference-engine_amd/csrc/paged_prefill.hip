@@ -234,17 +234,16 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
   // Per head state. Scores/probabilities live in the S^T layout (row n =
   // l % 16); the output accumulators in the MFMA D layout (rows 4kq+i).
   f32x4_t o[HB][NB];
-  float m[HB], l[HB];
+  float ref[HB], l[HB];
 #pragma unroll
   for (int hh = 0; hh < HB; ++hh) {
-    m[hh] = -INFINITY;
+    ref[hh] = -INFINITY;
     l[hh] = 0.f;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) o[hh][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
   const int qpos = P + r0 + n;  // this lane's query position (S^T layout)
   const float sl2 = p.scale_log2;          // scores -> log2 domain
-  const float slack = kRefSlack / sl2;     // the rescale slack in raw score units
 
   const int ntiles = (key1 - key0 + kTile - 1) / kTile;
   // Writes a staged tile into LDS buffer BUF (K then V, both row-major).
@@ -302,45 +301,65 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
             for (int i = 0; i < 4; ++i)
               if (k0 + 16 * h2 + 4 * kq + i > lim) s[hh][h2][i] = -INFINITY;
       }
-      bf16x8_t pa[HB];
-      float alpha[HB];
-      bool moved = false;
+      // Lazy rescaling (FlashAttention-3, Shah et al. 2024): each row keeps a
+      // reference ref (log2 units; -inf until the row meets a key) and the
+      // probabilities are exp2(score * scale * log2e - ref). The reference
+      // moves only when a tile's row max exceeds it by more than kRefSlack,
+      // so probabilities stay below 2^kRefSlack and, for most tiles, neither
+      // a row reduction nor an output rescale is needed: each lane checks its
+      // own scores and the wavefront takes the slow path when any lane must.
+      float t[HB][8], tmax[HB];
+      bool need = false;
 #pragma unroll
       for (int hh = 0; hh < HB; ++hh) {
-        float mx = fmaxf(s[hh][0][0], s[hh][1][0]);
+        const float r = ref[hh] == -INFINITY ? 0.f : ref[hh];
+        float tm = -INFINITY;
 #pragma unroll
-        for (int i = 1; i < 4; ++i) mx = fmaxf(mx, fmaxf(s[hh][0][i], s[hh][1][i]));
-        mx = RowMax(mx);
-        // Lazy rescaling (FlashAttention-3, Shah et al. 2024): the running
-        // reference (raw score units) moves only when the tile's max exceeds
-        // it by more than kRefSlack in log2 units, so probabilities stay below
-        // 2^kRefSlack and the output rescale is skipped for most tiles;
-        // O / l is unchanged.
-        const float mn = mx > m[hh] + slack ? mx : m[hh];
-        alpha[hh] = mn == -INFINITY ? 1.f : Exp2((m[hh] - mn) * sl2);
-        moved = moved || mn != m[hh];
-        m[hh] = mn;
-        const float mc = mn == -INFINITY ? 0.f : mn * sl2;  // masked scores give exp2(-inf) = 0
+        for (int j = 0; j < 8; ++j) {
+          t[hh][j] = fmaf(s[hh][j >> 2][j & 3], sl2, -r);  // masked scores stay -inf
+          tm = fmaxf(tm, t[hh][j]);
+        }
+        tmax[hh] = tm;
+        need = need || ref[hh] == -INFINITY || tm > kRefSlack;
+      }
+      if (__any(need)) {
+        bool moved = false;
+        float alpha[HB];
+#pragma unroll
+        for (int hh = 0; hh < HB; ++hh) {
+          const float tr = RowMax(tmax[hh]);  // the row's max over the tile, from its reference
+          const bool unset = ref[hh] == -INFINITY;
+          const bool mv = tr != -INFINITY && (unset || tr > kRefSlack);
+          const float d = mv ? tr : 0.f;
+          alpha[hh] = unset ? 1.f : Exp2(-d);
+          ref[hh] = mv ? (unset ? 0.f : ref[hh]) + tr : ref[hh];
+          moved = moved || mv;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) t[hh][j] -= d;
+          l[hh] *= alpha[hh];
+        }
+        // Rescale the output (O^T: this lane's registers all belong to its
+        // row n) by the row's alpha.
+        if (__any(moved)) {
+#pragma unroll
+          for (int hh = 0; hh < HB; ++hh)
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) o[hh][nb][i] *= alpha[hh];
+        }
+      }
+      bf16x8_t pa[HB];
+#pragma unroll
+      for (int hh = 0; hh < HB; ++hh) {
         float ps = 0.f;
 #pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float pv = Exp2(fmaf(s[hh][h2][i], sl2, -mc));
-            ps += pv;
-            pa[hh][4 * h2 + i] = static_cast<__bf16>(pv);
-          }
-        l[hh] = l[hh] * alpha[hh] + ps;  // lane-partial over this lane's tokens
-      }
-      // Rescale the output (O^T: this lane's registers all belong to its
-      // row n) by the row's alpha; skipped when no max moved.
-      if (__any(moved)) {
-#pragma unroll
-        for (int hh = 0; hh < HB; ++hh)
-#pragma unroll
-          for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) o[hh][nb][i] *= alpha[hh];
+        for (int j = 0; j < 8; ++j) {
+          const float pv = Exp2(t[hh][j]);
+          ps += pv;
+          pa[hh][j] = static_cast<__bf16>(pv);
+        }
+        l[hh] += ps;  // lane-partial over this lane's tokens
       }
       // O^T += V^T P^T: each V operand read once, HB MFMAs. The A operand of
       // lane (n, kq) is V[token][16nb + n] over tokens 4kq..4kq+3 and
@@ -419,8 +438,7 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
           *reinterpret_cast<float4*>(po + 16 * nb) =
               make_float4(o[hh][nb][0], o[hh][nb][1], o[hh][nb][2], o[hh][nb][3]);
         if (kq == 0) {
-          const float ms = m[hh] == -INFINITY ? -INFINITY : m[hh] * sl2;
-          *reinterpret_cast<float2*>(p.part_ml + (pidx * G + hg) * 2) = make_float2(ms, lt);
+          *reinterpret_cast<float2*>(p.part_ml + (pidx * G + hg) * 2) = make_float2(ref[hh], lt);
         }
       }
     }
