@@ -76,8 +76,11 @@ struct TileQ8 {
   int phys[TH];
 };
 
-// OCC: waves per SIMD.
-template <int D, int G, int TH, int OCC>
+// OCC: waves per SIMD. RMAX: rows per work item. A joint item (two rows over
+// their shared prefix) puts the second row's g heads in MFMA rows g..2g-1, so
+// its keys are read and multiplied once for both rows; only the PV work
+// grows with the virtual heads.
+template <int D, int G, int TH, int OCC, int RMAX>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(OCC)))
 void DecodeMfmaQ8(DecodeParams p) {
   using T = TileQ8<D, TH>;
@@ -87,17 +90,18 @@ void DecodeMfmaQ8(DecodeParams p) {
   constexpr int VLPT = T::VLPT;
   constexpr int VT = T::VT;
   constexpr int VJ = T::VJ;
-  constexpr int HR = (G + 3) / 4;
+  constexpr int GV = G * RMAX;  // virtual heads, row-major over the item's rows
+  constexpr int HR = (GV + 3) / 4;
   constexpr int HP = HR * 4;
-  static_assert(G >= 1 && G <= 8 && (D == 64 || D == 128), "shape");
+  static_assert(G >= 1 && G <= 8 && GV <= 16 && (D == 64 || D == 128), "shape");
 
   __shared__ float p_lds[TT * HP];
 
   const int lane = threadIdx.x;
   const int item_idx = blockIdx.x;
   if (item_idx >= p.n_items) return;
-  const ItemRef it = DecodeItem(p.items[item_idx]);  // one row per item (no joint plans)
-  const int row = it.rows[0];
+  const ItemRef it = DecodeItem(p.items[item_idx]);
+  const int nrows = RMAX == 1 ? 1 : it.nrows;  // the host launches RMAX = 2 for joint plans
   const int hk = it.hk;
   const int tb = it.tb, te = it.te;
   const int bs = p.bs;
@@ -105,12 +109,14 @@ void DecodeMfmaQ8(DecodeParams p) {
   const int kq = lane >> 4;
   const int ev = (lane % VLPT) * 4;
   const int tv = lane / VLPT;
-  const bool live = n < G;
+  const int vrow = n / G;  // this lane's row of the item (virtual head n)
+  const bool live = n < GV && vrow < nrows;
 
-  float qf[KB];  // this lane's query slice: head n, elements kq * KB .. + KB
+  float qf[KB];  // this lane's query slice: virtual head n, elements kq * KB .. + KB
   {
+    const int qrow = it.rows[live ? vrow : 0];
     const float* qp =
-        p.q + (int64_t{row} * p.heads + int64_t{hk} * G + (live ? n : 0)) * D + kq * KB;
+        p.q + (int64_t{qrow} * p.heads + int64_t{hk} * G + (live ? n % G : 0)) * D + kq * KB;
 #pragma unroll
     for (int i = 0; i < KB; i += 4) {
       const float4 x = *reinterpret_cast<const float4*>(qp + i);
@@ -219,7 +225,7 @@ void DecodeMfmaQ8(DecodeParams p) {
       sq4[i] = __shfl(sq, 4 * kq + i);  // lane 4kq+i holds head 4kq+i (kq of that lane = 0)
   }
 
-  float m[4], lsum[4], cofs[4], o[G][4];  // cofs: sum of p * v_scale per head row
+  float m[4], lsum[4], cofs[4], o[GV][4];  // cofs: sum of p * v_scale per head row
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     m[i] = -INFINITY;
@@ -227,7 +233,7 @@ void DecodeMfmaQ8(DecodeParams p) {
     cofs[i] = 0.f;
   }
 #pragma unroll
-  for (int h = 0; h < G; ++h) o[h][0] = o[h][1] = o[h][2] = o[h][3] = 0.f;
+  for (int h = 0; h < GV; ++h) o[h][0] = o[h][1] = o[h][2] = o[h][3] = 0.f;
 
   auto process = [&](const T& t, int t0) {
     float s[TH][4];
@@ -282,7 +288,8 @@ void DecodeMfmaQ8(DecodeParams p) {
     }
     __syncthreads();
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
+    for (int h = 0; h < GV; ++h) {
+      if (h / G >= nrows) break;
       const float a = ReadLaneF(alpha[h & 3], 16 * (h >> 2));
       o[h][0] *= a;
       o[h][1] *= a;
@@ -308,7 +315,8 @@ void DecodeMfmaQ8(DecodeParams p) {
           pv[4 * r4 + 3] = x.w;
         }
 #pragma unroll
-        for (int h = 0; h < G; ++h) {
+        for (int h = 0; h < GV; ++h) {
+          if (h / G >= nrows) break;
           o[h][0] = fmaf(pv[h], v0, o[h][0]);
           o[h][1] = fmaf(pv[h], v1, o[h][1]);
           o[h][2] = fmaf(pv[h], v2, o[h][2]);
@@ -333,7 +341,7 @@ void DecodeMfmaQ8(DecodeParams p) {
   // Token groups of a V load hold partial sums of the same elements.
   if constexpr (VT > 1) {
 #pragma unroll
-    for (int h = 0; h < G; ++h)
+    for (int h = 0; h < GV; ++h)
 #pragma unroll
       for (int e = 0; e < 4; ++e) o[h][e] = SumAcross<VLPT>(o[h][e]);
   }
@@ -346,39 +354,50 @@ void DecodeMfmaQ8(DecodeParams p) {
   // The unsigned bytes carried +128: take 128 * sum(p * v_scale) out of every
   // element of each head.
 #pragma unroll
-  for (int h = 0; h < G; ++h) {
+  for (int h = 0; h < GV; ++h) {
     const float c = ReadLaneF(crow[h & 3], 16 * (h >> 2));
 #pragma unroll
     for (int e = 0; e < 4; ++e) o[h][e] -= c;
   }
 
-  const RowDesc rd = p.rows[row];
-  if (rd.nsplit == 1) {
+  // Each of the item's rows: its g heads are virtual heads rr * g .. + g.
+#pragma unroll
+  for (int rr = 0; rr < RMAX; ++rr) {
+    if (rr >= nrows) break;
+    const int row = it.rows[rr];
+    const RowDesc rd = p.rows[row];
+    if (rd.nsplit == 1) {
+      if (lane < VLPT) {
+        float* op = p.out + (int64_t{row} * p.heads + int64_t{hk} * G) * D + ev;
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+          const int vh = rr * G + h;
+          const float inv = 1.0f / ReadLaneF(lrow[vh & 3], 16 * (vh >> 2));
+          *reinterpret_cast<float4*>(op + h * D) =
+              make_float4(o[vh][0] * inv, o[vh][1] * inv, o[vh][2] * inv, o[vh][3] * inv);
+        }
+      }
+      continue;
+    }
+    const int64_t pidx = PartialIndex(rd, p.kv_heads, hk, it.split);
     if (lane < VLPT) {
-      float* op = p.out + (int64_t{row} * p.heads + int64_t{hk} * G) * D + ev;
+      float* po = p.part_o + pidx * G * D + ev;
 #pragma unroll
       for (int h = 0; h < G; ++h) {
-        const float inv = 1.0f / ReadLaneF(lrow[h & 3], 16 * (h >> 2));
-        *reinterpret_cast<float4*>(op + h * D) =
-            make_float4(o[h][0] * inv, o[h][1] * inv, o[h][2] * inv, o[h][3] * inv);
+        const int vh = rr * G + h;
+        *reinterpret_cast<float4*>(po + h * D) =
+            make_float4(o[vh][0], o[vh][1], o[vh][2], o[vh][3]);
       }
     }
-    return;
-  }
-  const int64_t pidx = PartialIndex(rd, p.kv_heads, hk, it.split);
-  if (lane < VLPT) {
-    float* po = p.part_o + pidx * G * D + ev;
 #pragma unroll
-    for (int h = 0; h < G; ++h)
-      *reinterpret_cast<float4*>(po + h * D) = make_float4(o[h][0], o[h][1], o[h][2], o[h][3]);
-  }
-#pragma unroll
-  for (int h = 0; h < G; ++h) {
-    const float mh = ReadLaneF(m[h & 3], 16 * (h >> 2));
-    const float lh = ReadLaneF(lrow[h & 3], 16 * (h >> 2));
-    if (lane == 0) {
-      p.part_ml[(pidx * G + h) * 2 + 0] = mh;
-      p.part_ml[(pidx * G + h) * 2 + 1] = lh;
+    for (int h = 0; h < G; ++h) {
+      const int vh = rr * G + h;
+      const float mh = ReadLaneF(m[vh & 3], 16 * (vh >> 2));
+      const float lh = ReadLaneF(lrow[vh & 3], 16 * (vh >> 2));
+      if (lane == 0) {
+        p.part_ml[(pidx * G + h) * 2 + 0] = mh;
+        p.part_ml[(pidx * G + h) * 2 + 1] = lh;
+      }
     }
   }
 }
@@ -386,7 +405,14 @@ void DecodeMfmaQ8(DecodeParams p) {
 template <int D, int G>
 void LaunchQ8Shape(const DecodeParams& p, hipStream_t stream) {
   // 32-token tiles: 64-token tiles measured slower on C4 and C5.
-  hipLaunchKernelGGL((DecodeMfmaQ8<D, G, 2, 2>), dim3(p.n_items), dim3(64), 0, stream, p);
+  // Joint plans: 2g virtual heads (one wavefront per SIMD where 2g = 16 at
+  // d = 128, whose accumulators would spill at two).
+  if (p.n_joint > 0) {
+    constexpr int OCC = (D == 128 && 2 * G >= 16) ? 1 : 2;
+    hipLaunchKernelGGL((DecodeMfmaQ8<D, G, 2, OCC, 2>), dim3(p.n_items), dim3(64), 0, stream, p);
+    return;
+  }
+  hipLaunchKernelGGL((DecodeMfmaQ8<D, G, 2, 2, 1>), dim3(p.n_items), dim3(64), 0, stream, p);
 }
 
 }  // namespace
@@ -399,7 +425,7 @@ bool LaunchDecodeQ8(const DecodeParams& p, hipStream_t stream, hipError_t* err) 
                        (reinterpret_cast<uintptr_t>(p.k_scale) % 4 == 0) &&
                        (reinterpret_cast<uintptr_t>(p.v_scale) % 4 == 0) &&
                        (p.block_stride % 16 == 0);
-  if (!aligned || p.bs < 16 || p.n_joint > 0) return false;
+  if (!aligned || p.bs < 16) return false;
 #define EHIP_Q8_CASE(DD, GG)           \
   if (p.d == DD && p.group == GG) {    \
     LaunchQ8Shape<DD, GG>(p, stream);  \

@@ -468,8 +468,7 @@ int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::
                                             s.h_table_offsets[bl.b], pc.kb, pc.ke});
     }
   }
-  // The INT8 decode kernel serves one row per item (no joint items).
-  FinishPlan(g, plan, g.kv_dtype != EHIP_KV_INT8, &skip);
+  FinishPlan(g, plan, true, &skip);
   if (plan->partials < 0)
     return Fail(err, EHIP_UNIMPLEMENTED, "a row needs %lld or more key splits",
                 int64_t{1} << kSplitBits);

@@ -146,6 +146,57 @@ def test_int8_long_rows_split_and_merged(gctx, ehip_mod, orc, monkeypatch, split
     run.free()
 
 
+def shared_pair_tables(rng, pairs, bs, extra=7):
+    """Tables for row pairs that share leading blocks: pairs of (len_a, len_b,
+    shared_blocks); each row's remaining blocks (its last included) are its
+    own. Returns (tables, pool)."""
+    need = sum(sb + (la + bs - 1) // bs - sb + (lb + bs - 1) // bs - sb for la, lb, sb in pairs)
+    pool = need + extra
+    perm = rng.permutation(pool).astype(np.int32)
+    tabs, off = [], 0
+    for la, lb, sb in pairs:
+        shared = perm[off:off + sb]
+        off += sb
+        for L in (la, lb):
+            own = (L + bs - 1) // bs - sb
+            assert own >= 1
+            tabs.append(np.concatenate([shared, perm[off:off + own]]).astype(np.int32))
+            off += own
+    return tabs, pool
+
+
+@pytest.mark.parametrize("H,Hkv,d", [(32, 8, 128), (64, 8, 128), (8, 2, 64)])
+def test_int8_shared_prefix_joint_items(gctx, ehip_mod, orc, monkeypatch, H, Hkv, d):
+    """Pair-shared prefix blocks (the C4 construction's sharing) through the
+    INT8 kernel: with joint work items (one pass over a pair's shared blocks,
+    the second row's g heads in MFMA rows g..2g-1) and with the plain per-row
+    partition, each against the reference attention over the dequantised
+    K/V, and the two against each other."""
+    bs = 16
+    pairs = [(700, 530, 20), (1300, 2100, 33), (300, 900, 12), (260, 129, 8)]
+    lens = [L for la, lb, _ in pairs for L in (la, lb)]
+    outs = []
+    for flag in ("0", "1"):
+        monkeypatch.setenv("EHIP_NO_JOINT", flag)
+        rng = np.random.default_rng(H + d)
+        tabs, pool = shared_pair_tables(rng, pairs, bs)
+        geo = ehip_mod.geometry(H, Hkv, d, bs, ehip_mod.KV_INT8, pool,
+                                float(np.float32(1 / np.sqrt(d))))
+        st = ehip_mod.StepArrays(np.ones(len(lens), np.int32), np.asarray(lens, np.int64), tabs,
+                                 slots_for(tabs, [1] * len(lens), lens, bs))
+        rc, *_, joint_items, shared = ehip_mod.plan_counts(geo, st, joint=True)
+        assert rc == 0
+        assert (joint_items > 0) == (flag == "0"), joint_items
+        run = Int8Run(gctx, ehip_mod, H, Hkv, d, bs, pool, seed=H * d + 1)
+        q, got, _ = run.step(orc, tabs, [1] * len(lens), lens, rng, 1.0)
+        run.check_slabs()
+        ref = run.reference(orc, q, tabs, [1] * len(lens), lens)
+        assert rel_norm(got, ref) <= 1e-4, (flag, rel_norm(got, ref))
+        outs.append(got)
+        run.free()
+    assert rel_norm(outs[0], outs[1]) <= 1e-5
+
+
 def test_int8_entry_points_reject_other_geometries(gctx, ehip_mod):
     """The fp32/bf16 entry points refuse INT8 geometry (their element size
     would overrun the int8 slabs) and the INT8 ones refuse the others."""

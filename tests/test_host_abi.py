@@ -268,8 +268,8 @@ def test_plan_items_partition_c4(ehip_mod):
 
 def test_plan_int8_shapes_and_append_groups(ehip_mod):
     """INT8 KV: shapes outside the kernels' coverage are Unimplemented (9);
-    rows landing in one block must take consecutive slots (2 otherwise); no
-    joint items are planned."""
+    rows landing in one block must take consecutive slots (2 otherwise);
+    rows sharing leading blocks get joint items, as for bf16."""
     E = ehip_mod
     tabs = [np.arange(4, dtype=np.int32), np.arange(4, 8, dtype=np.int32)]
     st = E.StepArrays(np.array([3, 1], np.int32), np.array([40, 20], np.int64), tabs,
@@ -283,15 +283,15 @@ def test_plan_int8_shapes_and_append_groups(ehip_mod):
     gap = E.StepArrays(np.array([3, 1], np.int32), np.array([40, 20], np.int64), tabs,
                        np.array([36, 38, 39, 4 * 16 + 19], np.int64))
     assert E.plan_counts(ok, gap)[0] == 2
-    # two sequences forked from one prefix would share leading blocks: still
-    # no joint items for INT8
+    # two sequences forked from one prefix share 8 leading blocks (128 keys):
+    # one joint range per kv head, for INT8 as for bf16
     shared = [np.arange(10, dtype=np.int32), np.array(list(range(8)) + [10, 11], np.int32)]
     st2 = E.StepArrays(np.array([1, 1], np.int32), np.array([150, 150], np.int64), shared,
                        np.array([9 * 16 + 5, 11 * 16 + 5], np.int64))
     rc, rows, items, partials, split, joint, sh = E.plan_counts(ok, st2, joint=True)
-    assert rc == 0 and joint == 0
+    assert rc == 0 and joint == 8 and sh == 128
     g16 = E.geometry(32, 8, 128, 16, E.KV_BF16, 16, 0.088)
-    assert E.plan_counts(g16, st2, joint=True)[5] > 0
+    assert E.plan_counts(g16, st2, joint=True)[5:] == (joint, sh)
 
 
 def prefill_items(ehip_mod, g, st):
