@@ -313,15 +313,17 @@ int ehip_step_info(const ehip_ctx* ctx, int64_t* rows, int64_t* items, int64_t* 
 /* ------------------------------------------------ host-only planning ------
  * The work-list builder behind ehip_step_upload, callable without a GPU (for
  * tests of the host logic). Fills the counts the plan would have: query rows,
- * work items (of which joint_items serve two rows sharing leading blocks),
- * split partial slots, the base split length and the keys read jointly
- * (summed over row pairs). Any out pointer may be NULL. */
+ * work items (of which joint_items serve two to four rows sharing leading
+ * blocks), split partial slots, the base split length and the key re-reads
+ * the joint items save (each group's shared prefix times its members minus
+ * one). Any out pointer may be NULL. */
 int ehip_plan_counts(const ehip_geometry* geom, const ehip_step_desc* step, int64_t* rows,
                      int64_t* items, int64_t* partials, int32_t* split_tokens,
                      int64_t* joint_items, int64_t* shared_tokens);
 /* The work list of the same plan, in dispatch order, for tests of the host
- * logic: six int32 per item {row, joint_row (-1 if none), key_begin, key_end,
- * kv_head, split}. Writes at most cap items; *n gets the item count. */
+ * logic: eight int32 per item {row, joint rows 2..4 (-1 where absent),
+ * key_begin, key_end, kv_head, split}. Writes at most cap items; *n gets the
+ * item count. */
 int ehip_plan_items(const ehip_geometry* geom, const ehip_step_desc* step, int32_t* out,
                     int64_t cap, int64_t* n);
 /* The causal prefill-chunk items of the plan ehip_step_upload would build

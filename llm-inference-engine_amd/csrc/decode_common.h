@@ -50,8 +50,8 @@ __device__ __forceinline__ void ReportRejectedBlocks(const DecodeParams& p, int 
   if (__any(tab == -2) && (threadIdx.x & 63) == 0) atomicOr(p.err, kErrBlockRange);
 }
 
-// A work item decoded: its rows (one, or both of a joint pair), kv head, key
-// range and split slot.
+// A work item decoded: its rows (one, or the members of a joint group; slots
+// past nrows repeat row 0), kv head, key range and split slot.
 struct ItemRef {
   int rows[kMaxJointRows];
   int nrows;
@@ -68,7 +68,9 @@ __device__ __forceinline__ ItemRef DecodeItem(const WorkItem& it) {
   ItemRef r;
   r.rows[0] = it.row0;
   r.rows[1] = it.row1 >= 0 ? it.row1 : it.row0;
-  r.nrows = it.row1 >= 0 ? 2 : 1;
+  r.rows[2] = it.row2 >= 0 ? it.row2 : it.row0;
+  r.rows[3] = it.row3 >= 0 ? it.row3 : it.row0;
+  r.nrows = 1 + (it.row1 >= 0) + (it.row2 >= 0) + (it.row3 >= 0);
   r.hk = UnpackHk(it.hk_split);
   r.split = UnpackSplit(it.hk_split);
   r.last = IsLastRange(it.hk_split);
@@ -78,6 +80,12 @@ __device__ __forceinline__ ItemRef DecodeItem(const WorkItem& it) {
   r.first[0] = it.first_block0;
   r.first[1] = it.first_block1;
   return r;
+}
+
+// Row r of an item, by selects (a dynamic index into the rows array would
+// put it in scratch memory).
+__device__ __forceinline__ int ItemRow(const ItemRef& it, int r) {
+  return r == 0 ? it.rows[0] : r == 1 ? it.rows[1] : r == 2 ? it.rows[2] : it.rows[3];
 }
 
 // Sequential log-sum-exp merge of one (row, kv head) group's split partials

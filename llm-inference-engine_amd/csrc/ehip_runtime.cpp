@@ -261,6 +261,7 @@ ehip::DecodeParams StepDecodeParams(ehip_ctx* ctx, const float* q, const void* k
   p.merge_rows = ctx->d_merge_rows;
   p.n_merge = static_cast<int32_t>(plan.merge_rows.size());
   p.n_joint = static_cast<int32_t>(plan.joint_items);
+  p.joint_rows = plan.joint_rows;
   p.heads = g.heads;
   p.kv_heads = g.kv_heads;
   p.group = static_cast<int32_t>(grp);
@@ -950,13 +951,15 @@ int ehip_plan_items(const ehip_geometry* geom, const ehip_step_desc* step, int32
   const int64_t m = std::min<int64_t>(cap, *n);
   for (int64_t i = 0; i < m; ++i) {
     const ehip::WorkItem& w = plan.items[static_cast<size_t>(i)];
-    int32_t* o = out + 6 * i;
+    int32_t* o = out + 8 * i;
     o[0] = w.row0;
     o[1] = w.row1;
-    o[2] = w.tok_begin;
-    o[3] = w.tok_end;
-    o[4] = ehip::UnpackHk(w.hk_split);
-    o[5] = ehip::UnpackSplit(w.hk_split);
+    o[2] = w.row2;
+    o[3] = w.row3;
+    o[4] = w.tok_begin;
+    o[5] = w.tok_end;
+    o[6] = ehip::UnpackHk(w.hk_split);
+    o[7] = ehip::UnpackSplit(w.hk_split);
   }
   return EHIP_OK;
 }

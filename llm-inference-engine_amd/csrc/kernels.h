@@ -37,6 +37,7 @@ struct DecodeParams {
   const int32_t* merge_rows;  // [n_merge] rows with more than one split
   int32_t n_merge;
   int32_t n_joint;          // joint work items in the plan
+  int32_t joint_rows;       // rows of the plan's largest joint item (1: none)
   int32_t heads;
   int32_t kv_heads;
   int32_t group;            // g = H / Hkv

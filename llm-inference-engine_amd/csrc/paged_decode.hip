@@ -323,7 +323,7 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void DecodeValu(DecodeParams p
   if (item_idx >= p.n_items) return;
   const ItemRef it = DecodeItem(p.items[item_idx]);
   for (int r = 0; r < it.nrows; ++r)
-    DecodeValuRow<KV, D, G>(p, it.rows[r], it.hk, it.tb, it.te, it.split, it.table_off);
+    DecodeValuRow<KV, D, G>(p, ItemRow(it, r), it.hk, it.tb, it.te, it.split, it.table_off);
 }
 
 // ----------------------------------------------------------------------------
@@ -464,7 +464,7 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void DecodeGeneric(DecodeParam
   if (item_idx >= p.n_items) return;
   const ItemRef it = DecodeItem(p.items[item_idx]);
   for (int r = 0; r < it.nrows; ++r)
-    DecodeGenericRow<KV>(p, it.rows[r], it.hk, it.tb, it.te, it.split);
+    DecodeGenericRow<KV>(p, ItemRow(it, r), it.hk, it.tb, it.te, it.split);
 }
 
 // ----------------------------------------------------------------------------

@@ -125,7 +125,7 @@ void DecodeMfmaBf16(DecodeParams p) {
   uint32_t ticket = 0;
   bool drawn = false;
   const ItemRef it = DecodeItem(wi);
-  const int nrows = it.nrows;  // <= RMAX (the host launches RMAX = 2 only for joint plans)
+  const int nrows = it.nrows;  // <= RMAX (the host launches RMAX >= the plan's joint rows)
   const int hk = it.hk;
   const int tb = it.tb, te = it.te;
   const int bs = p.bs;
@@ -143,7 +143,10 @@ void DecodeMfmaBf16(DecodeParams p) {
   {
     // Every lane loads (padding lanes read a live head) and padding is
     // zeroed afterwards, so no branch sits around the loads.
-    const int qrow = (live && vrow == 1) ? it.rows[1] : it.rows[0];  // no dynamic indexing
+    // The lane's row by selects (no dynamic indexing of the item's rows).
+    int qrow = it.rows[0];
+#pragma unroll
+    for (int rr = 1; rr < RMAX; ++rr) qrow = (live && vrow == rr) ? it.rows[rr] : qrow;
     const int qh = live ? n % G : 0;
     const float* qp = p.q + (int64_t{qrow} * p.heads + int64_t{hk} * G + qh) * D + kq * 8;
 #pragma unroll
@@ -555,9 +558,20 @@ bool LaunchDecodeMfma(const DecodeParams& params, QueueState* queue, hipStream_t
   // hands out the items instead of the queue).
   const char* pers = std::getenv("EHIP_DECODE_PERSIST");
   const bool persist = !(pers && std::strcmp(pers, "0") == 0);
+  // Rows per item: 1, 2, or 4 for groups of three or four sharers (the plan
+  // caps a group at 16 / g rows, so 4 only for g <= 4).
+  const int rows = joint ? p.joint_rows : 1;
 #define EHIP_MFMA_CASE(DD, GG)                                   \
   if (p.d == DD && p.group == GG) {                              \
-    if (joint)                                                   \
+    if constexpr (GG <= 4) {                                     \
+      if (rows > 2) {                                            \
+        LaunchShape<DD, GG, 4>(p, stream, wide, deep, persist);  \
+        *err = hipGetLastError();                                \
+        return true;                                             \
+      }                                                          \
+    }                                                            \
+    if (rows > 2) return false;                                  \
+    if (rows == 2)                                               \
       LaunchShape<DD, GG, 2>(p, stream, wide, deep, persist);    \
     else                                                         \
       LaunchShape<DD, GG, 1>(p, stream, wide, deep, persist);    \

@@ -101,7 +101,7 @@ void DecodeMfmaQ8(DecodeParams p) {
   const int item_idx = blockIdx.x;
   if (item_idx >= p.n_items) return;
   const ItemRef it = DecodeItem(p.items[item_idx]);
-  const int nrows = RMAX == 1 ? 1 : it.nrows;  // the host launches RMAX = 2 for joint plans
+  const int nrows = RMAX == 1 ? 1 : it.nrows;  // the host launches RMAX >= the plan's joint rows
   const int hk = it.hk;
   const int tb = it.tb, te = it.te;
   const int bs = p.bs;
@@ -114,7 +114,9 @@ void DecodeMfmaQ8(DecodeParams p) {
 
   float qf[KB];  // this lane's query slice: virtual head n, elements kq * KB .. + KB
   {
-    const int qrow = it.rows[live ? vrow : 0];
+    int qrow = it.rows[0];  // the lane's row by selects (no dynamic indexing)
+#pragma unroll
+    for (int rr = 1; rr < RMAX; ++rr) qrow = (live && vrow == rr) ? it.rows[rr] : qrow;
     const float* qp =
         p.q + (int64_t{qrow} * p.heads + int64_t{hk} * G + (live ? n % G : 0)) * D + kq * KB;
 #pragma unroll
@@ -405,8 +407,16 @@ void DecodeMfmaQ8(DecodeParams p) {
 template <int D, int G>
 void LaunchQ8Shape(const DecodeParams& p, hipStream_t stream) {
   // 32-token tiles: 64-token tiles measured slower on C4 and C5.
-  // Joint plans: 2g virtual heads (one wavefront per SIMD where 2g = 16 at
-  // d = 128, whose accumulators would spill at two).
+  // Joint plans: 2g or 4g virtual heads (one wavefront per SIMD where they
+  // reach 16 at d = 128, whose accumulators would spill at two).
+  if (p.n_joint > 0 && p.joint_rows > 2) {
+    if constexpr (4 * G <= 16) {
+      constexpr int OCC = (D == 128 && 4 * G >= 16) ? 1 : 2;
+      hipLaunchKernelGGL((DecodeMfmaQ8<D, G, 2, OCC, 4>), dim3(p.n_items), dim3(64), 0, stream,
+                         p);
+    }
+    return;
+  }
   if (p.n_joint > 0) {
     constexpr int OCC = (D == 128 && 2 * G >= 16) ? 1 : 2;
     hipLaunchKernelGGL((DecodeMfmaQ8<D, G, 2, OCC, 2>), dim3(p.n_items), dim3(64), 0, stream, p);
@@ -426,6 +436,7 @@ bool LaunchDecodeQ8(const DecodeParams& p, hipStream_t stream, hipError_t* err) 
                        (reinterpret_cast<uintptr_t>(p.v_scale) % 4 == 0) &&
                        (p.block_stride % 16 == 0);
   if (!aligned || p.bs < 16) return false;
+  if (p.n_joint > 0 && p.joint_rows * p.group > 16) return false;  // the plan caps groups
 #define EHIP_Q8_CASE(DD, GG)           \
   if (p.d == DD && p.group == GG) {    \
     LaunchQ8Shape<DD, GG>(p, stream);  \

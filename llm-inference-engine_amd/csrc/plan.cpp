@@ -3,7 +3,9 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <climits>
 #include <cstdlib>
+#include <utility>
 
 namespace ehip {
 namespace {
@@ -130,12 +132,15 @@ int32_t SharedFullBlocks(const Plan& plan, const RowDesc& a, const RowDesc& b, i
   return c;
 }
 
-// One key range of a row (or of a joint pair a, b over their shared prefix).
+// One key range of a row, or of a joint group's rows over their shared
+// prefix (rows[1..] = -1 where absent).
 struct KeyRange {
-  int32_t a, b, tb, te;
+  int32_t rows[kMaxJointRows];
+  int32_t tb, te;
+  bool joint() const { return rows[1] >= 0; }
 };
 
-// Pairs rows that share leading blocks (greedy over rows ordered by their
+// Groups rows that share leading blocks (greedy over rows ordered by their
 // first block id and table), splits every row into whole-tile key ranges
 // (joint ranges first), assigns partial slots and orders the work longest
 // first.
@@ -151,12 +156,15 @@ void FinishPlan(const ehip_geometry& g, Plan* plan, bool allow_joint,
   const int32_t base = ChooseSplitTokens(g, units);
   plan->split_tokens = base;
   plan->groups.clear();
+  plan->group_start.assign(1, 0);
   plan->joint_items = 0;
+  plan->joint_rows = 1;
   plan->shared_tokens = 0;
 
   std::vector<int32_t> joint_len(n, 0);
   const char* no_joint = std::getenv("EHIP_NO_JOINT");
-  if (allow_joint && n >= 2 && !(no_joint && no_joint[0] == '1')) {
+  const int cap = JointRowsCap(g.heads / g.kv_heads);
+  if (allow_joint && cap >= 2 && n >= 2 && !(no_joint && no_joint[0] == '1')) {
     std::vector<int32_t> order;
     order.reserve(n);
     for (size_t i = 0; i < n; ++i)
@@ -169,58 +177,88 @@ void FinishPlan(const ehip_geometry& g, Plan* plan, bool allow_joint,
         return plan->rows[a].table_off < plan->rows[b].table_off;
       return a < b;
     });
-    for (size_t i = 0; i + 1 < order.size(); ++i) {
-      const int32_t a = order[i], b = order[i + 1];
-      const int32_t c = SharedFullBlocks(*plan, plan->rows[a], plan->rows[b], bs);
-      if (c * bs < kMinJointTokens) continue;
-      plan->groups.push_back(a);
-      plan->groups.push_back(b);
-      joint_len[a] = joint_len[b] = c * bs;
-      plan->shared_tokens += int64_t{c} * bs;
-      ++i;  // b is taken
+    // A group starts at a row and takes the following rows while that saves
+    // more re-read keys: with m members and common prefix C (full blocks), a
+    // member sharing c blocks with the first row makes the common prefix
+    // C' = min(C, c), and it joins if m * C' > (m - 1) * C (and C' spans at
+    // least kMinJointTokens keys).
+    for (size_t i = 0; i + 1 < order.size();) {
+      const int32_t a = order[i];
+      int32_t common = INT32_MAX;
+      size_t j = i + 1;
+      for (; j < order.size() && static_cast<int>(j - i) < cap; ++j) {
+        const int32_t c = std::min(common, SharedFullBlocks(*plan, plan->rows[a],
+                                                            plan->rows[order[j]], bs));
+        const int64_t m = static_cast<int64_t>(j - i);  // members before order[j] joins
+        if (c * bs < kMinJointTokens) break;
+        if (common != INT32_MAX && m * int64_t{c} <= (m - 1) * int64_t{common}) break;
+        common = c;
+      }
+      if (j - i < 2) {
+        ++i;
+        continue;
+      }
+      for (size_t k = i; k < j; ++k) {
+        plan->groups.push_back(order[k]);
+        joint_len[order[k]] = common * bs;
+      }
+      plan->group_start.push_back(static_cast<int32_t>(plan->groups.size()));
+      plan->shared_tokens += int64_t{common} * bs * static_cast<int64_t>(j - i - 1);
+      plan->joint_rows = std::max(plan->joint_rows, static_cast<int32_t>(j - i));
+      i = j;
     }
   }
+  const size_t n_groups = plan->group_start.size() - 1;
+  auto members = [&](size_t k) {
+    return std::pair<const int32_t*, const int32_t*>(plan->groups.data() + plan->group_start[k],
+                                                     plan->groups.data() + plan->group_start[k + 1]);
+  };
 
-  // Split length per row (a group's members use the larger of the two).
+  // Split length per row (a group's members use the largest of theirs).
   std::vector<int32_t> split_len(n);
   for (size_t r = 0; r < n; ++r) split_len[r] = RowSplitTokens(g, base, plan->rows[r].length);
-  for (size_t k = 0; k < plan->groups.size(); k += kMaxJointRows) {
-    const int32_t a = plan->groups[k], b = plan->groups[k + 1];
-    split_len[a] = split_len[b] = std::max(split_len[a], split_len[b]);
+  for (size_t k = 0; k < n_groups; ++k) {
+    const auto [b, e] = members(k);
+    int32_t sl = 0;
+    for (const int32_t* r = b; r != e; ++r) sl = std::max(sl, split_len[*r]);
+    for (const int32_t* r = b; r != e; ++r) split_len[*r] = sl;
   }
 
   // Key ranges: a group's shared prefix [0, P) in joint ranges, then each
   // row's own keys [P, L), in pieces of the row's split length. Every range
   // becomes one work item per kv head.
   std::vector<KeyRange> ranges;
-  for (size_t k = 0; k < plan->groups.size(); k += kMaxJointRows) {
-    const int32_t a = plan->groups[k];
-    const int32_t sl = split_len[a], P = joint_len[a];
-    for (int32_t t = 0; t < P; t += sl)
-      ranges.push_back(KeyRange{a, plan->groups[k + 1], t, std::min(P, t + sl)});
+  for (size_t k = 0; k < n_groups; ++k) {
+    const auto [b, e] = members(k);
+    const int32_t sl = split_len[*b], P = joint_len[*b];
+    for (int32_t t = 0; t < P; t += sl) {
+      KeyRange kr{{-1, -1, -1, -1}, t, std::min(P, t + sl)};
+      std::copy(b, e, kr.rows);
+      ranges.push_back(kr);
+    }
   }
   for (size_t r = 0; r < n; ++r) {
     if (skipped(r)) continue;
     const int32_t sl = split_len[r];
     for (int32_t t = joint_len[r]; t < plan->rows[r].length; t += sl)
-      ranges.push_back(KeyRange{static_cast<int32_t>(r), -1, t,
+      ranges.push_back(KeyRange{{static_cast<int32_t>(r), -1, -1, -1}, t,
                                 std::min(plan->rows[r].length, t + sl)});
   }
 
   // Split indices follow key order within a row. Joint ranges cover the
-  // leading keys of both members, so numbering them first (in key order)
-  // gives both members the same index for each.
+  // leading keys of every member, so numbering them first (in key order)
+  // gives all members the same index for each.
   std::stable_sort(ranges.begin(), ranges.end(), [](const KeyRange& x, const KeyRange& y) {
-    const bool jx = x.b >= 0, jy = y.b >= 0;
-    if (jx != jy) return jx;
-    return x.a != y.a ? x.a < y.a : x.tb < y.tb;
+    if (x.joint() != y.joint()) return x.joint();
+    return x.rows[0] != y.rows[0] ? x.rows[0] < y.rows[0] : x.tb < y.tb;
   });
   size_t n_joint_ranges = 0;
-  while (n_joint_ranges < ranges.size() && ranges[n_joint_ranges].b >= 0) ++n_joint_ranges;
+  while (n_joint_ranges < ranges.size() && ranges[n_joint_ranges].joint()) ++n_joint_ranges;
   std::vector<int32_t> nsplit(n, 0), split_of(ranges.size());
   for (size_t i = 0; i < ranges.size(); ++i) {
-    split_of[i] = nsplit[ranges[i].a]++;
-    if (ranges[i].b >= 0) ++nsplit[ranges[i].b];
+    split_of[i] = nsplit[ranges[i].rows[0]];
+    for (int32_t r : ranges[i].rows)
+      if (r >= 0) ++nsplit[r];
   }
   int64_t split_base = 0;
   plan->any_split = false;
@@ -241,11 +279,11 @@ void FinishPlan(const ehip_geometry& g, Plan* plan, bool allow_joint,
   plan->items.reserve(ranges.size() * g.kv_heads);
   for (size_t i = 0; i < ranges.size(); ++i) {
     const KeyRange& kr = ranges[i];
-    const bool last = kr.b < 0 && kr.te == plan->rows[kr.a].length;
+    const bool last = !kr.joint() && kr.te == plan->rows[kr.rows[0]].length;
     for (int32_t hk = 0; hk < g.kv_heads; ++hk)
-      plan->items.push_back(WorkItem{kr.a, kr.b, kr.tb, kr.te,
+      plan->items.push_back(WorkItem{kr.rows[0], kr.rows[1], kr.rows[2], kr.rows[3], kr.tb, kr.te,
                                      PackHkSplit(hk, split_of[i]) | (last ? kLastRangeFlag : 0),
-                                     plan->rows[kr.a].table_off, 0, 0});
+                                     plan->rows[kr.rows[0]].table_off, 0, 0});
   }
   plan->joint_items = static_cast<int64_t>(n_joint_ranges) * g.kv_heads;
   // Costliest first, so the tail of the dispatch is short items. A joint
@@ -255,7 +293,8 @@ void FinishPlan(const ehip_geometry& g, Plan* plan, bool allow_joint,
   // (C4: 440 -> 428 us per launch on MI355X; weights 1.5 to 3 measured
   // alike, 1 left the joint items in the tail).
   auto cost = [](const WorkItem& x) {
-    return int64_t{x.tok_end - x.tok_begin} * (x.row1 >= 0 ? kMaxJointRows : 1);
+    const int rows = 1 + (x.row1 >= 0) + (x.row2 >= 0) + (x.row3 >= 0);
+    return int64_t{x.tok_end - x.tok_begin} * rows;
   };
   std::stable_sort(plan->items.begin(), plan->items.end(),
                    [&](const WorkItem& x, const WorkItem& y) { return cost(x) > cost(y); });

@@ -39,15 +39,18 @@ struct RowDesc {
   int32_t nsplit;      // splits of this row (joint ones first)
 };
 
-// One work item = one wavefront: keys [tok_begin, tok_end) of row0 (and of
-// row1 too for a joint item, row1 = -1 otherwise), for the g query heads of
-// one kv head. `split` is the partial slot index inside each row's range.
-// The range's table slice starts at table_off (both rows read the same
-// blocks), so a kernel can fetch the table, the queries and the row
-// descriptors in parallel as soon as it has the item.
+// One work item = one wavefront: keys [tok_begin, tok_end) of row0 (and, for
+// a joint item, of up to three more rows reading the same blocks over the
+// range: row1..row3, -1 where absent), for the g query heads of one kv head.
+// `split` is the partial slot index inside each row's range (the same for
+// every row of a joint item). The range's table slice starts at table_off,
+// so a kernel can fetch the table, the queries and the row descriptors in
+// parallel as soon as it has the item.
 struct WorkItem {
   int32_t row0;
   int32_t row1;
+  int32_t row2;
+  int32_t row3;
   int32_t tok_begin;
   int32_t tok_end;
   int32_t hk_split;  // kv_head | split << 12
@@ -75,7 +78,13 @@ struct PrefillItem {
   int32_t key_end;
 };
 
-constexpr int kMaxJointRows = 2;
+// Rows per joint item: at most 4, and at most 16 / g, so that the item's
+// virtual heads (g per row) fill no more than the 16 rows of one MFMA block.
+constexpr int kMaxJointRows = 4;
+constexpr int JointRowsCap(int64_t group) {
+  return group <= 0 ? 1 : (16 / group >= kMaxJointRows ? kMaxJointRows
+                                                        : (16 / group < 1 ? 1 : int(16 / group)));
+}
 // The packed (kv head, split) word of a work item: kv head in bits 0-11,
 // split in bits 12-28, and bit 30 set on the item whose key range ends at its
 // row's last key (the item that appends the row's new token in the fused
@@ -103,7 +112,8 @@ struct Plan {
   std::vector<RowDesc> rows;
   std::vector<WorkItem> items;
   std::vector<PrefillItem> prefill;  // chunk rows served by the MFMA prefill kernel
-  std::vector<int32_t> groups;      // [n_groups * kMaxJointRows] member rows (host side)
+  std::vector<int32_t> groups;      // member rows of each joint group (host side) ...
+  std::vector<int32_t> group_start;  // ... group i is groups[group_start[i] .. group_start[i+1])
   std::vector<int32_t> table_ids;   // CSR ids, copied
   std::vector<int64_t> slots;       // slot mapping of appended tokens (may be empty)
   std::vector<int32_t> merge_rows;  // rows with more than one split, ascending
@@ -113,7 +123,10 @@ struct Plan {
   int64_t max_length = 0;           // longest visible length (largest position + 1)
   int32_t split_tokens = 0;         // base split length chosen for this step
   int64_t joint_items = 0;
-  int64_t shared_tokens = 0;        // sum over groups of the jointly read prefix
+  int32_t joint_rows = 1;           // rows of the largest joint item (1: none)
+  // Keys whose re-reads the joint items save: for each group, its shared
+  // prefix times (members - 1).
+  int64_t shared_tokens = 0;
   bool any_split = false;           // some decode row has more than one split (merge needed)
   bool all_decode = false;          // every row is its sequence's only new token (T_b == 1)
 };

@@ -178,13 +178,14 @@ def plan_counts(geom: Geometry, step: StepArrays, joint: bool = False):
 
 
 def plan_items(geom: Geometry, step: StepArrays):
-    """Host-only planning: (status, items [n, 6] int32) with columns row,
-    joint_row, key_begin, key_end, kv_head, split, in dispatch order."""
+    """Host-only planning: (status, items [n, 8] int32) with columns row, the
+    joint rows 2..4 (-1 where absent), key_begin, key_end, kv_head, split, in
+    dispatch order."""
     n = C.c_int64()
     rc = lib().ehip_plan_items(C.byref(geom), C.byref(step.desc), None, 0, C.byref(n))
     if rc != 0:
-        return rc, np.zeros((0, 6), np.int32)
-    out = np.zeros((n.value, 6), np.int32)
+        return rc, np.zeros((0, 8), np.int32)
+    out = np.zeros((n.value, 8), np.int32)
     rc = lib().ehip_plan_items(C.byref(geom), C.byref(step.desc), out.ctypes.data, n.value,
                                C.byref(n))
     return rc, out

@@ -146,18 +146,20 @@ def test_int8_long_rows_split_and_merged(gctx, ehip_mod, orc, monkeypatch, split
     run.free()
 
 
-def shared_pair_tables(rng, pairs, bs, extra=7):
+def shared_pair_tables(rng, pairs, bs, extra=7, groups=()):
     """Tables for row pairs that share leading blocks: pairs of (len_a, len_b,
-    shared_blocks); each row's remaining blocks (its last included) are its
-    own. Returns (tables, pool)."""
-    need = sum(sb + (la + bs - 1) // bs - sb + (lb + bs - 1) // bs - sb for la, lb, sb in pairs)
+    shared_blocks), then larger fork groups of (shared_blocks, [lengths]);
+    each row's remaining blocks (its last included) are its own. Returns
+    (tables, pool)."""
+    all_groups = [(sb, [la, lb]) for la, lb, sb in pairs] + list(groups)
+    need = sum(sb + sum((L + bs - 1) // bs - sb for L in ls) for sb, ls in all_groups)
     pool = need + extra
     perm = rng.permutation(pool).astype(np.int32)
     tabs, off = [], 0
-    for la, lb, sb in pairs:
+    for sb, ls in all_groups:
         shared = perm[off:off + sb]
         off += sb
-        for L in (la, lb):
+        for L in ls:
             own = (L + bs - 1) // bs - sb
             assert own >= 1
             tabs.append(np.concatenate([shared, perm[off:off + own]]).astype(np.int32))
@@ -165,21 +167,24 @@ def shared_pair_tables(rng, pairs, bs, extra=7):
     return tabs, pool
 
 
-@pytest.mark.parametrize("H,Hkv,d", [(32, 8, 128), (64, 8, 128), (8, 2, 64)])
+@pytest.mark.parametrize("H,Hkv,d", [(32, 8, 128), (64, 8, 128), (8, 2, 64), (8, 8, 128)])
 def test_int8_shared_prefix_joint_items(gctx, ehip_mod, orc, monkeypatch, H, Hkv, d):
-    """Pair-shared prefix blocks (the C4 construction's sharing) through the
-    INT8 kernel: with joint work items (one pass over a pair's shared blocks,
-    the second row's g heads in MFMA rows g..2g-1) and with the plain per-row
-    partition, each against the reference attention over the dequantised
-    K/V, and the two against each other."""
+    """Pair-shared prefix blocks (the C4 construction's sharing) and, for
+    g <= 4, a fork of four rows through the INT8 kernel: with joint work items
+    (one pass over the shared blocks, row r's g heads in MFMA rows
+    r*g..r*g+g-1) and with the plain per-row partition, each against the
+    reference attention over the dequantised K/V, and the two against each
+    other."""
     bs = 16
     pairs = [(700, 530, 20), (1300, 2100, 33), (300, 900, 12), (260, 129, 8)]
-    lens = [L for la, lb, _ in pairs for L in (la, lb)]
+    # g <= 4: forks of four rows share 20 blocks (joint items of four rows)
+    quads = [(20, [500, 700, 330, 900])] if H // Hkv <= 4 else []
     outs = []
     for flag in ("0", "1"):
         monkeypatch.setenv("EHIP_NO_JOINT", flag)
         rng = np.random.default_rng(H + d)
-        tabs, pool = shared_pair_tables(rng, pairs, bs)
+        tabs, pool = shared_pair_tables(rng, pairs, bs, groups=quads)
+        lens = [L for la, lb, _ in pairs for L in (la, lb)] + [L for _, ls in quads for L in ls]
         geo = ehip_mod.geometry(H, Hkv, d, bs, ehip_mod.KV_INT8, pool,
                                 float(np.float32(1 / np.sqrt(d))))
         st = ehip_mod.StepArrays(np.ones(len(lens), np.int32), np.asarray(lens, np.int64), tabs,

@@ -617,6 +617,83 @@ def test_bandwidth_probes(gctx, ehip_mod):
     v.free()
 
 
+def fork_group_case(rng, groups, Hkv, d, bs, H):
+    """Rows forked from shared prefixes: groups of (shared_blocks, [lengths]).
+    A group's members read the same physical blocks (the same K/V) over the
+    shared prefix; every other block, the last included, is a member's own.
+    Returns (q, k_slab, v_slab, tables, lengths)."""
+    need = sum(sb + sum((L + bs - 1) // bs - sb for L in lens) for sb, lens in groups)
+    nb = need + 9
+    perm = rng.permutation(nb).astype(np.int32)
+    k_slab = normal(rng, (nb, Hkv, bs, d))
+    v_slab = normal(rng, (nb, Hkv, bs, d))
+    tables, off = [], 0
+    for sb, lens in groups:
+        shared = perm[off:off + sb]
+        off += sb
+        for L in lens:
+            own = (L + bs - 1) // bs - sb
+            assert own >= 1
+            tables.append(np.concatenate([shared, perm[off:off + own]]).astype(np.int32))
+            off += own
+    lengths = [L for _, ls in groups for L in ls]
+    q = normal(rng, (len(lengths), H, d))
+    return q, k_slab, v_slab, tables, lengths
+
+
+FORK_GROUPS = [(20, [700, 530, 900, 400, 655]),  # five sharers of 320 keys
+               (12, [300, 900, 260]),            # three sharers of 192 keys
+               (30, [600, 610]),                 # a pair
+               (0, [129, 77, 1])]                # no sharing
+
+
+@pytest.mark.parametrize("H,Hkv,d,kv", [(32, 8, 128, "mfma"), (16, 8, 64, "mfma"),
+                                        (8, 8, 128, "mfma"), (64, 8, 128, "mfma"),
+                                        (32, 8, 128, "valu"), (14, 2, 64, "f32"),
+                                        (8, 8, 64, "f32")])
+def test_decode_fork_groups_beyond_pairs(gctx, ehip_mod, orc, H, Hkv, d, kv, monkeypatch):
+    """Joint work items of up to min(4, 16 / g) rows over fork groups' shared
+    prefixes (groups of five and three sharers, a pair, unshared rows),
+    through the bf16 MFMA kernel (its virtual heads: g per row, up to 16),
+    the bf16 VALU kernel and the fp32 VALU kernel (rows one after the other):
+    against the oracle, and against the plain per-row partition."""
+    monkeypatch.setenv("EHIP_DECODE_KERNEL", "valu" if kv == "valu" else "mfma")
+    monkeypatch.setenv("EHIP_DECODE_WG", "0")  # joint items live in the split-KV path
+    rng = np.random.default_rng(H + 3 * d)
+    bs = 16
+    q, ks, vs, tables, lengths = fork_group_case(rng, FORK_GROUPS, Hkv, d, bs, H)
+    bf16 = kv != "f32"
+    if bf16:
+        ks_b, vs_b = orc.to_bf16_bits(ks), orc.to_bf16_bits(vs)
+        kd, vd = gctx.to_device(ks_b), gctx.to_device(vs_b)
+        ks_r, vs_r = orc.bf16_bits_to_f32(ks_b), orc.bf16_bits_to_f32(vs_b)
+    else:
+        kd, vd = gctx.to_device(ks), gctx.to_device(vs)
+        ks_r, vs_r = ks, vs
+    geo = ehip_mod.geometry(H, Hkv, d, bs, ehip_mod.KV_BF16 if bf16 else ehip_mod.KV_F32,
+                            ks.shape[0], scale_for(d))
+    st = ehip_mod.StepArrays(np.ones(len(lengths), np.int32), np.asarray(lengths, np.int64),
+                             tables)
+    _, items = ehip_mod.plan_items(geo, st)
+    assert (items[:, :4] >= 0).sum(axis=1).max() == min(4, 16 // (H // Hkv))
+    ref = orc.paged_decode_batched(q, ks_r, vs_r, tables, lengths, H, Hkv, d, bs, scale_for(d))
+    qd = gctx.to_device(q)
+    outs = []
+    for flag in ("0", "1"):
+        monkeypatch.setenv("EHIP_NO_JOINT", flag)
+        out = gctx.alloc(q.nbytes)
+        assert gctx.paged_decode_batched(qd, kd, vd, tables, lengths, H, Hkv, d, bs, 0,
+                                         ks.shape[0], scale_for(d), out, bf16=bf16) == 0, \
+            gctx.last_error()
+        gctx.sync()
+        outs.append(out.download(np.float32, q.shape))
+        out.free()
+        check_fp32(outs[-1], ref)
+    assert rel_norm(outs[0], outs[1]) <= FP32_REL
+    for b in (qd, kd, vd):
+        b.free()
+
+
 @pytest.mark.parametrize("H,Hkv,d", [(14, 2, 64), (32, 8, 128), (8, 8, 128), (28, 4, 64),
                                      (8, 1, 128), (24, 3, 64)])
 @pytest.mark.parametrize("lens", [[1, 17, 33, 1500, 513], [1024, 1536, 1], [32, 64, 96],

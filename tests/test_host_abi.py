@@ -199,27 +199,48 @@ def test_plan_joint_items_for_shared_prefixes(ehip_mod):
     assert partials == sum(nsplit) * w.kv_heads
 
 
-def test_plan_chunk_rows_pair_up(ehip_mod, monkeypatch):
+def greedy_groups(order, shared_blocks, cap, bs=16, min_joint=128):
+    """The planner's grouping rule, restated: from each row in order, take
+    the following rows while the common prefix C' = min(C, shared with the
+    first row) keeps at least min_joint keys and saves more re-reads than
+    before (m * C' > (m - 1) * C), up to cap rows."""
+    groups, i = [], 0
+    while i + 1 < len(order):
+        common, j = None, i + 1
+        while j < len(order) and j - i < cap:
+            c = shared_blocks(order[i], order[j])
+            c = c if common is None else min(common, c)
+            m = j - i
+            if c * bs < min_joint or (common is not None and m * c <= (m - 1) * common):
+                break
+            common, j = c, j + 1
+        if j - i < 2:
+            i += 1
+            continue
+        groups.append((order[i:j], common))
+        i = j
+    return groups
+
+
+def test_plan_chunk_rows_group_up(ehip_mod, monkeypatch):
     monkeypatch.setenv("EHIP_SPLIT_TOKENS", "128")
     # A chunk of 300 rows over 100 cached keys: row t attends 101 + t keys;
-    # consecutive rows of one sequence read the same table.
+    # consecutive rows of one sequence read the same table, so they form
+    # joint groups of four (g = 4: 16 / 4 virtual-head rows).
     st = simple_step(ehip_mod, [400], qlens=np.array([300], np.int32))
     rc, rows, items, partials, split, joint, shared = ehip_mod.plan_counts(geom(ehip_mod), st,
                                                                            joint=True)
     assert rc == 0 and rows == 300
     lens = [101 + t for t in range(300)]
+    groups = greedy_groups(list(range(300)), lambda a, b: min(lens[a], lens[b]) // 16, cap=4)
+    assert max(len(m) for m, _ in groups) == 4
     joint_len = [0] * 300
     exp_joint = exp_shared = 0
-    i = 0
-    while i + 1 < 300:  # the planner's greedy pairing over one table
-        P = (min(lens[i], lens[i + 1]) // 16) * 16
-        if P >= 128:
-            joint_len[i] = joint_len[i + 1] = P
-            exp_shared += P
-            exp_joint += math.ceil(P / 128)
-            i += 2
-        else:
-            i += 1
+    for members, c in groups:
+        for r in members:
+            joint_len[r] = 16 * c
+        exp_shared += 16 * c * (len(members) - 1)
+        exp_joint += math.ceil(16 * c / 128)
     exp_private = sum(math.ceil((L - P) / 128) for L, P in zip(lens, joint_len))
     assert shared == exp_shared
     assert joint == 8 * exp_joint
@@ -230,9 +251,9 @@ def check_partition(items, lens, hkv):
     """Every (row, kv head) has key ranges (its own and the joint ones it is a
     member of) that tile [0, L) exactly, numbered 0..n-1 in key order."""
     per = {}
-    for r0, r1, tb, te, hk, sp in items.tolist():
+    for r0, r1, r2, r3, tb, te, hk, sp in items.tolist():
         assert 0 <= tb < te
-        for r in (r0, r1):
+        for r in (r0, r1, r2, r3):
             if r >= 0:
                 per.setdefault((r, hk), []).append((tb, te, sp))
     for r, L in enumerate(lens):
@@ -260,10 +281,89 @@ def test_plan_items_partition_c4(ehip_mod):
     assert rc == 0
     check_partition(items, w.context_lens, w.kv_heads)
     # costliest first: keys times the rows an item serves
-    cost = (items[:, 3] - items[:, 2]) * np.where(items[:, 1] >= 0, 2, 1)
+    cost = (items[:, 5] - items[:, 4]) * (items[:, :4] >= 0).sum(axis=1)
     assert (np.diff(cost) <= 0).all()
     rc, rows, n, partials, split, joint, shared = ehip_mod.plan_counts(g, st, joint=True)
     assert n == len(items) and joint == int((items[:, 1] >= 0).sum()) > 0
+
+
+def group_step(ehip_mod, groups, bs=16, seed=5):
+    """Rows forked from shared prefixes: groups of (shared_blocks, [lengths]);
+    every member's blocks after the shared ones are its own."""
+    rng = np.random.default_rng(seed)
+    need = sum(sb + sum((L + bs - 1) // bs - sb for L in lens) for sb, lens in groups)
+    perm = rng.permutation(need + 5).astype(np.int32)
+    tabs, off = [], 0
+    for sb, lens in groups:
+        shared = perm[off:off + sb]
+        off += sb
+        for L in lens:
+            own = (L + bs - 1) // bs - sb
+            tabs.append(np.concatenate([shared, perm[off:off + own]]).astype(np.int32))
+            off += own
+    lens = [L for _, ls in groups for L in ls]
+    st = ehip_mod.StepArrays(np.ones(len(lens), np.int32), np.asarray(lens, np.int64), tabs)
+    return st, lens, need + 5
+
+
+@pytest.mark.parametrize("H,Hkv,cap", [(32, 8, 4), (64, 8, 2), (8, 8, 4), (14, 2, 2)])
+def test_plan_joint_groups_beyond_pairs(ehip_mod, H, Hkv, cap):
+    """Rows forked from one prefix form joint groups of up to min(4, 16 / g)
+    rows: a group of five sharers of 20 blocks is cut into groups of the cap;
+    a member whose common prefix with the group is short joins only while it
+    saves more re-read keys (m * C' > (m - 1) * C). Every row's key ranges
+    still tile [0, L) with split indices in key order."""
+    groups = [(20, [700, 530, 900, 400, 655]),   # five sharers of 320 keys
+              (12, [300, 900, 260]),             # three sharers of 192 keys
+              (30, [600, 610]),                  # a pair
+              (0, [129, 77])]                    # no sharing
+    st, lens, pool = group_step(ehip_mod, groups)
+    g = ehip_mod.geometry(H, Hkv, 64, 16, ehip_mod.KV_BF16 if H % Hkv == 0 and (H // Hkv) in (1, 2, 4, 8) else ehip_mod.KV_F32, pool, 0.125)
+    rc, items = ehip_mod.plan_items(g, st)
+    assert rc == 0
+    check_partition(items, lens, Hkv)
+    sizes = (items[:, :4] >= 0).sum(axis=1)
+    assert sizes.max() == cap
+    # every joint item's rows are members of one fork group, over its shared prefix
+    first = np.cumsum([0] + [len(ls) for _, ls in groups])
+    group_of = {r: k for k in range(len(groups)) for r in range(first[k], first[k + 1])}
+    for it in items[sizes > 1]:
+        rows = [r for r in it[:4] if r >= 0]
+        assert len({group_of[r] for r in rows}) == 1
+        assert it[5] <= 16 * groups[group_of[rows[0]]][0]
+    rc, rows, n, partials, split, joint, shared = ehip_mod.plan_counts(g, st, joint=True)
+    # saved re-reads: the five sharers give groups of the cap (and a remainder
+    # pair when cap = 2: 2 + 2 + 1), the three give cap-limited groups, the pair one
+    exp = 0
+    for sb, ls in groups:
+        m = len(ls)
+        while m >= 2 and sb * 16 >= 128:
+            take = min(cap, m)
+            exp += 16 * sb * (take - 1)
+            m -= take
+    assert shared == exp
+
+
+def test_plan_joint_group_member_rule(ehip_mod):
+    """A third sharer whose common prefix is much shorter stays out of the
+    group (2 * 8 <= 1 * 30); one whose common prefix is close joins
+    (2 * 25 > 1 * 30)."""
+    bs = 16
+    # rows 0, 1 share 30 blocks; row 2 shares the first 8 of them
+    base = np.arange(40, dtype=np.int32)
+    t0 = base[:40]
+    t1 = np.concatenate([base[:30], np.arange(100, 110, dtype=np.int32)])
+    t2 = np.concatenate([base[:8], np.arange(200, 232, dtype=np.int32)])
+    g = ehip_mod.geometry(32, 8, 128, bs, ehip_mod.KV_BF16, 256, 0.088)
+    st = ehip_mod.StepArrays(np.ones(3, np.int32), np.array([640, 640, 640], np.int64),
+                             [t0, t1, t2])
+    rc, *_, joint, shared = ehip_mod.plan_counts(g, st, joint=True)
+    assert rc == 0 and shared == 30 * 16
+    t2 = np.concatenate([base[:25], np.arange(200, 215, dtype=np.int32)])
+    st = ehip_mod.StepArrays(np.ones(3, np.int32), np.array([640, 640, 640], np.int64),
+                             [t0, t1, t2])
+    rc, *_, joint, shared = ehip_mod.plan_counts(g, st, joint=True)
+    assert rc == 0 and shared == 2 * 25 * 16
 
 
 def test_plan_int8_shapes_and_append_groups(ehip_mod):
