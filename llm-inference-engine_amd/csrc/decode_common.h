@@ -68,9 +68,8 @@ __device__ __forceinline__ ItemRef DecodeItem(const WorkItem& it) {
   ItemRef r;
   r.rows[0] = it.row0;
   r.rows[1] = it.row1 >= 0 ? it.row1 : it.row0;
-  r.rows[2] = it.row2 >= 0 ? it.row2 : it.row0;
-  r.rows[3] = it.row3 >= 0 ? it.row3 : it.row0;
-  r.nrows = 1 + (it.row1 >= 0) + (it.row2 >= 0) + (it.row3 >= 0);
+  r.rows[2] = r.rows[3] = it.row0;
+  r.nrows = it.row1 >= 0 ? 2 : 1;
   r.hk = UnpackHk(it.hk_split);
   r.split = UnpackSplit(it.hk_split);
   r.last = IsLastRange(it.hk_split);
@@ -80,6 +79,21 @@ __device__ __forceinline__ ItemRef DecodeItem(const WorkItem& it) {
   r.first[0] = it.first_block0;
   r.first[1] = it.first_block1;
   return r;
+}
+
+// Rows 3 and 4 of a joint item of a plan with groups beyond pairs (the
+// kernels that serve such groups read them; p.items_x is null otherwise).
+__device__ __forceinline__ void AddItemRows(const DecodeParams& p, int64_t idx, ItemRef& r) {
+  if (p.items_x == nullptr) return;
+  const ItemRowsX x = p.items_x[idx];
+  if (x.row2 >= 0) {
+    r.rows[2] = x.row2;
+    r.nrows = 3;
+  }
+  if (x.row3 >= 0) {
+    r.rows[3] = x.row3;
+    r.nrows = 4;
+  }
 }
 
 // Row r of an item, by selects (a dynamic index into the rows array would

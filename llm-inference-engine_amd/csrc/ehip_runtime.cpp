@@ -52,6 +52,7 @@ struct ehip_ctx {
   const ehip::Q8Group* d_q8_groups = nullptr;  // INT8 append groups of the step
   const int32_t* d_q8_rows = nullptr;
   const int32_t* d_merge_rows = nullptr;
+  const ehip::ItemRowsX* d_items_x = nullptr;  // null unless the plan groups beyond pairs
 };
 
 namespace {
@@ -117,8 +118,9 @@ int UploadPlan(ehip_ctx* ctx, const ehip_geometry& g, Plan&& plan, const int32_t
   const size_t merge_b = Align256(plan.merge_rows.size() * sizeof(int32_t));
   const size_t q8g_b = Align256(plan.q8_groups.size() * sizeof(ehip::Q8Group));
   const size_t q8r_b = Align256(plan.q8_rows.size() * sizeof(int32_t));
+  const size_t itx_b = Align256(plan.items_x.size() * sizeof(ehip::ItemRowsX));
   const size_t total = std::max<size_t>(
-      256, rows_b + items_b + prefill_b + table_b + slots_b + merge_b + q8g_b + q8r_b);
+      256, rows_b + items_b + prefill_b + table_b + slots_b + merge_b + q8g_b + q8r_b + itx_b);
 
   const int cur = ctx->stage_cur;
   ctx->stage_cur ^= 1;
@@ -155,6 +157,8 @@ int UploadPlan(ehip_ctx* ctx, const ehip_geometry& g, Plan&& plan, const int32_t
   const size_t q8_at = rows_b + items_b + prefill_b + table_b + slots_b + merge_b;
   std::memcpy(h + q8_at, plan.q8_groups.data(), plan.q8_groups.size() * sizeof(ehip::Q8Group));
   std::memcpy(h + q8_at + q8g_b, plan.q8_rows.data(), plan.q8_rows.size() * sizeof(int32_t));
+  std::memcpy(h + q8_at + q8g_b + q8r_b, plan.items_x.data(),
+              plan.items_x.size() * sizeof(ehip::ItemRowsX));
   EHIP_HIP(ctx, hipMemcpyAsync(ctx->d_desc, h, total, hipMemcpyHostToDevice, ctx->stream));
   if (!ctx->stage_done[cur]) EHIP_HIP(ctx, hipEventCreateWithFlags(&ctx->stage_done[cur],
                                                                    hipEventDisableTiming));
@@ -172,6 +176,9 @@ int UploadPlan(ehip_ctx* ctx, const ehip_geometry& g, Plan&& plan, const int32_t
       reinterpret_cast<const int32_t*>(d + rows_b + items_b + prefill_b + table_b + slots_b);
   ctx->d_q8_groups = reinterpret_cast<const ehip::Q8Group*>(d + q8_at);
   ctx->d_q8_rows = reinterpret_cast<const int32_t*>(d + q8_at + q8g_b);
+  ctx->d_items_x = plan.items_x.empty()
+                       ? nullptr
+                       : reinterpret_cast<const ehip::ItemRowsX*>(d + q8_at + q8g_b + q8r_b);
   if (int rc = EnsureWorkspace(ctx, g, plan)) return rc;
   ctx->geom = g;
   ctx->plan = std::move(plan);
@@ -262,6 +269,7 @@ ehip::DecodeParams StepDecodeParams(ehip_ctx* ctx, const float* q, const void* k
   p.n_merge = static_cast<int32_t>(plan.merge_rows.size());
   p.n_joint = static_cast<int32_t>(plan.joint_items);
   p.joint_rows = plan.joint_rows;
+  p.items_x = ctx->d_items_x;
   p.heads = g.heads;
   p.kv_heads = g.kv_heads;
   p.group = static_cast<int32_t>(grp);
@@ -952,10 +960,11 @@ int ehip_plan_items(const ehip_geometry* geom, const ehip_step_desc* step, int32
   for (int64_t i = 0; i < m; ++i) {
     const ehip::WorkItem& w = plan.items[static_cast<size_t>(i)];
     int32_t* o = out + 8 * i;
+    const bool x = !plan.items_x.empty();
     o[0] = w.row0;
     o[1] = w.row1;
-    o[2] = w.row2;
-    o[3] = w.row3;
+    o[2] = x ? plan.items_x[static_cast<size_t>(i)].row2 : -1;
+    o[3] = x ? plan.items_x[static_cast<size_t>(i)].row3 : -1;
     o[4] = w.tok_begin;
     o[5] = w.tok_end;
     o[6] = ehip::UnpackHk(w.hk_split);

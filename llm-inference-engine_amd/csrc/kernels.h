@@ -38,6 +38,7 @@ struct DecodeParams {
   int32_t n_merge;
   int32_t n_joint;          // joint work items in the plan
   int32_t joint_rows;       // rows of the plan's largest joint item (1: none)
+  const ItemRowsX* items_x; // rows 3 and 4 per item when joint_rows > 2, else null
   int32_t heads;
   int32_t kv_heads;
   int32_t group;            // g = H / Hkv

@@ -321,7 +321,8 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void DecodeValu(DecodeParams p
   const int item_idx =
       blockIdx.x * kWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (item_idx >= p.n_items) return;
-  const ItemRef it = DecodeItem(p.items[item_idx]);
+  ItemRef it = DecodeItem(p.items[item_idx]);
+  AddItemRows(p, item_idx, it);
   for (int r = 0; r < it.nrows; ++r)
     DecodeValuRow<KV, D, G>(p, ItemRow(it, r), it.hk, it.tb, it.te, it.split, it.table_off);
 }
@@ -462,7 +463,8 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void DecodeGeneric(DecodeParam
   const int item_idx =
       blockIdx.x * kWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (item_idx >= p.n_items) return;
-  const ItemRef it = DecodeItem(p.items[item_idx]);
+  ItemRef it = DecodeItem(p.items[item_idx]);
+  AddItemRows(p, item_idx, it);
   for (int r = 0; r < it.nrows; ++r)
     DecodeGenericRow<KV>(p, ItemRow(it, r), it.hk, it.tb, it.te, it.split);
 }

@@ -124,7 +124,8 @@ void DecodeMfmaBf16(DecodeParams p) {
   while (item_idx < p.n_items) {
   uint32_t ticket = 0;
   bool drawn = false;
-  const ItemRef it = DecodeItem(wi);
+  ItemRef it = DecodeItem(wi);
+  if constexpr (RMAX > 2) AddItemRows(p, item_idx, it);
   const int nrows = it.nrows;  // <= RMAX (the host launches RMAX >= the plan's joint rows)
   const int hk = it.hk;
   const int tb = it.tb, te = it.te;

@@ -100,7 +100,8 @@ void DecodeMfmaQ8(DecodeParams p) {
   const int lane = threadIdx.x;
   const int item_idx = blockIdx.x;
   if (item_idx >= p.n_items) return;
-  const ItemRef it = DecodeItem(p.items[item_idx]);
+  ItemRef it = DecodeItem(p.items[item_idx]);
+  if constexpr (RMAX > 2) AddItemRows(p, item_idx, it);
   const int nrows = RMAX == 1 ? 1 : it.nrows;  // the host launches RMAX >= the plan's joint rows
   const int hk = it.hk;
   const int tb = it.tb, te = it.te;

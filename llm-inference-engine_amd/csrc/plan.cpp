@@ -276,14 +276,21 @@ void FinishPlan(const ehip_geometry& g, Plan* plan, bool allow_joint,
     if (plan->rows[r].nsplit >= (1 << kSplitBits)) plan->partials = -1;  // rejected by BuildPlan
 
   plan->items.clear();
-  plan->items.reserve(ranges.size() * g.kv_heads);
+  plan->items_x.clear();
+  struct Entry {
+    WorkItem w;
+    ItemRowsX x;
+  };
+  std::vector<Entry> entries;
+  entries.reserve(ranges.size() * g.kv_heads);
   for (size_t i = 0; i < ranges.size(); ++i) {
     const KeyRange& kr = ranges[i];
     const bool last = !kr.joint() && kr.te == plan->rows[kr.rows[0]].length;
     for (int32_t hk = 0; hk < g.kv_heads; ++hk)
-      plan->items.push_back(WorkItem{kr.rows[0], kr.rows[1], kr.rows[2], kr.rows[3], kr.tb, kr.te,
-                                     PackHkSplit(hk, split_of[i]) | (last ? kLastRangeFlag : 0),
-                                     plan->rows[kr.rows[0]].table_off, 0, 0});
+      entries.push_back(Entry{WorkItem{kr.rows[0], kr.rows[1], kr.tb, kr.te,
+                                       PackHkSplit(hk, split_of[i]) | (last ? kLastRangeFlag : 0),
+                                       plan->rows[kr.rows[0]].table_off, 0, 0},
+                              ItemRowsX{kr.rows[2], kr.rows[3]}});
   }
   plan->joint_items = static_cast<int64_t>(n_joint_ranges) * g.kv_heads;
   // Costliest first, so the tail of the dispatch is short items. A joint
@@ -292,12 +299,18 @@ void FinishPlan(const ehip_geometry& g, Plan* plan, bool allow_joint,
   // wave of the queue instead of behind every full-length single-row item
   // (C4: 440 -> 428 us per launch on MI355X; weights 1.5 to 3 measured
   // alike, 1 left the joint items in the tail).
-  auto cost = [](const WorkItem& x) {
-    const int rows = 1 + (x.row1 >= 0) + (x.row2 >= 0) + (x.row3 >= 0);
-    return int64_t{x.tok_end - x.tok_begin} * rows;
+  auto cost = [](const Entry& e) {
+    const int rows = 1 + (e.w.row1 >= 0) + (e.x.row2 >= 0) + (e.x.row3 >= 0);
+    return int64_t{e.w.tok_end - e.w.tok_begin} * rows;
   };
-  std::stable_sort(plan->items.begin(), plan->items.end(),
-                   [&](const WorkItem& x, const WorkItem& y) { return cost(x) > cost(y); });
+  std::stable_sort(entries.begin(), entries.end(),
+                   [&](const Entry& x, const Entry& y) { return cost(x) > cost(y); });
+  plan->items.reserve(entries.size());
+  for (const Entry& e : entries) plan->items.push_back(e.w);
+  if (plan->joint_rows > 2) {
+    plan->items_x.reserve(entries.size());
+    for (const Entry& e : entries) plan->items_x.push_back(e.x);
+  }
   // The block ids of each item's first two 16-token halves ride in the item,
   // so a wavefront can issue its first K/V loads without waiting for its
   // table slice (-1 when the table is device-resident and unknown here).

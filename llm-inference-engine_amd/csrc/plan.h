@@ -40,23 +40,29 @@ struct RowDesc {
 };
 
 // One work item = one wavefront: keys [tok_begin, tok_end) of row0 (and, for
-// a joint item, of up to three more rows reading the same blocks over the
-// range: row1..row3, -1 where absent), for the g query heads of one kv head.
-// `split` is the partial slot index inside each row's range (the same for
-// every row of a joint item). The range's table slice starts at table_off,
-// so a kernel can fetch the table, the queries and the row descriptors in
-// parallel as soon as it has the item.
+// a joint item, of the other rows reading the same blocks over the range:
+// row1, -1 otherwise; a group of three or four rows keeps rows 3 and 4 in the
+// plan's ItemRowsX array, read only by the kernels that serve such groups),
+// for the g query heads of one kv head. `split` is the partial slot index
+// inside each row's range (the same for every row of a joint item). The
+// range's table slice starts at table_off, so a kernel can fetch the table,
+// the queries and the row descriptors in parallel as soon as it has the item.
 struct WorkItem {
   int32_t row0;
   int32_t row1;
-  int32_t row2;
-  int32_t row3;
   int32_t tok_begin;
   int32_t tok_end;
   int32_t hk_split;  // kv_head | split << 12
   int32_t table_off;
   int32_t first_block0;  // block id of token tok_begin (-1: read the table)
   int32_t first_block1;  // block id of token min(tok_begin + 16, tok_end - 1)
+};
+
+// Rows 3 and 4 of a joint item (-1 where absent), parallel to the work list
+// when the plan has groups of more than two rows.
+struct ItemRowsX {
+  int32_t row2;
+  int32_t row3;
 };
 
 // One causal prefill block: query rows q0 .. q0+M-1 of a chunk of `chunk`
@@ -111,6 +117,7 @@ struct Q8Group {
 struct Plan {
   std::vector<RowDesc> rows;
   std::vector<WorkItem> items;
+  std::vector<ItemRowsX> items_x;   // empty unless joint_rows > 2; else one per item
   std::vector<PrefillItem> prefill;  // chunk rows served by the MFMA prefill kernel
   std::vector<int32_t> groups;      // member rows of each joint group (host side) ...
   std::vector<int32_t> group_start;  // ... group i is groups[group_start[i] .. group_start[i+1])
