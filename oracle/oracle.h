@@ -137,6 +137,23 @@ void orc_kv_scatter_bf16(const float* src_k, const float* src_v,
 void orc_kv_append_int8(const float* src_k, const float* src_v, const int64_t* slot_mapping,
                         int64_t t_dim, int64_t kv_heads, int64_t d, int64_t block_size,
                         int8_t* k_slab, int8_t* v_slab, float* k_scale, float* v_scale);
+/* FP8 KV (OCP E4M3, "e4m3fn": bias 7, 3 mantissa bits, no infinities,
+ * 0x7F/0xFF NaN, largest finite 448) with the INT8 layout and scale rule:
+ * the same append as orc_kv_append_int8 with 448 in place of 127 and
+ * quant(x, s) = 0 if s == 0, else e4m3(clamp(x * (1 / s), -448, 448)).
+ * e4m3(y) rounds to nearest, ties to even (subnormal steps of 2^-9 below
+ * 2^-6); |y| >= 448 saturates to 448 and NaN encodes as 0x7F. No reference
+ * implementation exists either; tests/test_oracle.py pins the conversions
+ * against torch.float8_e4m3fn over every code and every midpoint, and the
+ * append by closed forms. */
+float orc_e4m3_to_fp32(uint8_t c);
+uint8_t orc_fp32_to_e4m3(float x);
+void orc_kv_append_fp8(const float* src_k, const float* src_v, const int64_t* slot_mapping,
+                       int64_t t_dim, int64_t kv_heads, int64_t d, int64_t block_size,
+                       uint8_t* k_slab, uint8_t* v_slab, float* k_scale, float* v_scale);
+/* Dequantised fp32 copy of an FP8 slab: x = e4m3(q) * scale[block, head]. */
+void orc_fp8_dequant(const uint8_t* slab, const float* scale, int64_t num_blocks,
+                     int64_t kv_heads, int64_t block_size, int64_t d, float* out);
 /* Dequantised fp32 copy of an INT8 slab: x = q * scale[block, head]. */
 void orc_int8_dequant(const int8_t* slab, const float* scale, int64_t num_blocks,
                       int64_t kv_heads, int64_t block_size, int64_t d, float* out);

@@ -26,6 +26,7 @@ _u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
 _i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
 _i64p = np.ctypeslib.ndpointer(np.int64, flags="C_CONTIGUOUS")
 _i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
 _i64 = C.c_int64
 _PP = C.POINTER(C.c_void_p)
 
@@ -77,6 +78,15 @@ def lib():
         L.orc_kv_append_int8.restype = None
         L.orc_int8_dequant.argtypes = [_i8p, _f32p, _i64, _i64, _i64, _i64, _f32p]
         L.orc_int8_dequant.restype = None
+        L.orc_e4m3_to_fp32.argtypes = [C.c_uint8]
+        L.orc_e4m3_to_fp32.restype = C.c_float
+        L.orc_fp32_to_e4m3.argtypes = [C.c_float]
+        L.orc_fp32_to_e4m3.restype = C.c_uint8
+        L.orc_kv_append_fp8.argtypes = [_f32p, _f32p, _i64p, _i64, _i64, _i64, _i64, _u8p,
+                                        _u8p, _f32p, _f32p]
+        L.orc_kv_append_fp8.restype = None
+        L.orc_fp8_dequant.argtypes = [_u8p, _f32p, _i64, _i64, _i64, _i64, _f32p]
+        L.orc_fp8_dequant.restype = None
         L.orc_rope_apply_f32.argtypes = [C.c_int, _f32p, _i64, _i64, _i64, _i32p, _f32p, _f32p]
         L.orc_rope_apply_f32.restype = None
         L.orc_cpu_attention.argtypes = [_f32p, _f32p, _f32p, _i64, _i64, _i64, _i64, _i64,
@@ -320,6 +330,43 @@ def kv_append_int8(src_k, src_v, slot_mapping, kv_heads, d, bs, k_slab, v_slab, 
                              np.ascontiguousarray(src_v, np.float32).reshape(-1), sm, len(sm),
                              kv_heads, d, bs, k_slab.reshape(-1), v_slab.reshape(-1),
                              k_scale.reshape(-1), v_scale.reshape(-1))
+
+
+def e4m3_to_f32(codes):
+    """fp32 values of OCP E4M3 codes (uint8 array)."""
+    c = np.ascontiguousarray(codes, np.uint8)
+    return np.array([lib().orc_e4m3_to_fp32(int(x)) for x in c.reshape(-1)],
+                    np.float32).reshape(c.shape)
+
+
+def f32_to_e4m3(x):
+    """OCP E4M3 codes of fp32 values (round to nearest even, saturating)."""
+    a = np.ascontiguousarray(x, np.float32)
+    return np.array([lib().orc_fp32_to_e4m3(float(v)) for v in a.reshape(-1)],
+                    np.uint8).reshape(a.shape)
+
+
+def kv_append_fp8(src_k, src_v, slot_mapping, kv_heads, d, bs, k_slab, v_slab, k_scale,
+                  v_scale):
+    """FP8 (E4M3) append in place: slabs uint8 [blocks, Hkv, bs, d], scales fp32 [blocks, Hkv]."""
+    sm = np.ascontiguousarray(slot_mapping, np.int64)
+    for a, dt in ((k_slab, np.uint8), (v_slab, np.uint8), (k_scale, np.float32),
+                  (v_scale, np.float32)):
+        assert a.dtype == dt and a.flags.c_contiguous
+    lib().orc_kv_append_fp8(np.ascontiguousarray(src_k, np.float32).reshape(-1),
+                            np.ascontiguousarray(src_v, np.float32).reshape(-1), sm, len(sm),
+                            kv_heads, d, bs, k_slab.reshape(-1), v_slab.reshape(-1),
+                            k_scale.reshape(-1), v_scale.reshape(-1))
+
+
+def fp8_dequant(slab, scale):
+    """fp32 copy of an FP8 slab [blocks, Hkv, bs, d]: e4m3(q) * scale[block, head]."""
+    nb, hkv, bs, d = slab.shape
+    out = np.empty(slab.shape, np.float32)
+    lib().orc_fp8_dequant(np.ascontiguousarray(slab, np.uint8).reshape(-1),
+                          np.ascontiguousarray(scale, np.float32).reshape(-1), nb, hkv, bs, d,
+                          out.reshape(-1))
+    return out
 
 
 def int8_dequant(slab, scale):

@@ -549,6 +549,141 @@ void orc_kv_append_int8(const float* src_k, const float* src_v, const int64_t* s
   free(done);
 }
 
+/* OCP FP8 E4M3 ("e4m3fn"): sign, 4 exponent bits (bias 7), 3 mantissa bits;
+ * no infinities, 0x7F / 0xFF are NaN, 448 is the largest finite value. */
+float orc_e4m3_to_fp32(uint8_t c) {
+  const int e = (c >> 3) & 15, m = c & 7;
+  float v;
+  if (e == 15 && m == 7)
+    v = NAN;
+  else if (e == 0)
+    v = ldexpf((float)m, -9); /* subnormal: m * 2^-9 */
+  else
+    v = ldexpf((float)(8 + m), e - 10); /* (1 + m/8) * 2^(e-7) */
+  return (c & 0x80) ? -v : v;
+}
+
+uint8_t orc_fp32_to_e4m3(float x) {
+  if (isnan(x)) return 0x7F;
+  uint32_t bits;
+  memcpy(&bits, &x, 4);
+  const uint8_t sign = (uint8_t)((bits >> 24) & 0x80);
+  const float a = fabsf(x);
+  if (a >= 448.0f) return sign | 0x7E; /* saturate: [448, 464] rounds to 448 anyway */
+  if (a < 0.015625f) {                 /* below 2^-6: subnormal steps of 2^-9 */
+    /* a * 2^9 is exact; rint is round-to-nearest-even; 8 steps carry into the
+     * smallest normal, whose code (exponent 1, mantissa 0) is 8 as well. */
+    return sign | (uint8_t)rintf(a * 512.0f);
+  }
+  memcpy(&bits, &a, 4);
+  int e = (int)(bits >> 23) - 127; /* 2^e <= a < 2^(e+1), -6 <= e <= 8 */
+  uint32_t m = (bits & 0x7FFFFF) >> 20, rem = bits & 0xFFFFF;
+  if (rem > 0x80000u || (rem == 0x80000u && (m & 1u))) ++m; /* to nearest, ties to even */
+  if (m == 8u) {
+    m = 0u;
+    ++e;
+  }
+  return sign | (uint8_t)(((e + 7) << 3) | (int)m);
+}
+
+static uint8_t qf8(float x, float s) {
+  if (s == 0.0f) return 0;
+  const float inv = 1.0f / s;
+  float y = x * inv;
+  if (y > 448.0f) y = 448.0f;
+  if (y < -448.0f) y = -448.0f;
+  return orc_fp32_to_e4m3(y);
+}
+
+/* One (block, kv head) of one FP8 slab: new rows at offsets [off0, off0 + n). */
+static void append_f8_tile(const float* src, int64_t src_row_stride, const int64_t* rows,
+                           int64_t n, int64_t off0, int64_t d, uint8_t* tile, float* scale) {
+  float m = 0.0f;
+  for (int64_t i = 0; i < n; ++i)
+    for (int64_t e = 0; e < d; ++e) {
+      const float a = fabsf(src[rows[i] * src_row_stride + e]);
+      if (a > m) m = a;
+    }
+  const float s0 = off0 > 0 ? *scale : 0.0f;
+  float s1 = s0;
+  if (m > s0 * 448.0f) {
+    s1 = m / 448.0f;
+    for (int64_t r = 0; r < off0; ++r)
+      for (int64_t e = 0; e < d; ++e) {
+        const float x = orc_e4m3_to_fp32(tile[r * d + e]) * s0;
+        tile[r * d + e] = qf8(x, s1);
+      }
+  }
+  for (int64_t i = 0; i < n; ++i)
+    for (int64_t e = 0; e < d; ++e)
+      tile[(off0 + i) * d + e] = qf8(src[rows[i] * src_row_stride + e], s1);
+  *scale = s1;
+}
+
+/* The rows of one call grouped by destination block, in offset order (shared
+ * by the INT8 and FP8 appends). Calls fn(block, rows, n, off0). */
+static void for_each_block_group(const int64_t* slot_mapping, int64_t t_dim, int64_t block_size,
+                                 void (*fn)(void*, int64_t, const int64_t*, int64_t, int64_t),
+                                 void* ctx) {
+  int64_t* rows = (int64_t*)malloc(sizeof(int64_t) * (size_t)(block_size > 0 ? block_size : 1));
+  char* done = (char*)calloc((size_t)(t_dim > 0 ? t_dim : 1), 1);
+  for (int64_t t = 0; t < t_dim; ++t) {
+    if (done[t]) continue;
+    const int64_t block = slot_mapping[t] / block_size;
+    int64_t n = 0, off0 = block_size;
+    for (int64_t u = t; u < t_dim; ++u)
+      if (slot_mapping[u] / block_size == block) {
+        const int64_t off = slot_mapping[u] % block_size;
+        if (off < off0) off0 = off;
+        done[u] = 1;
+        rows[n++] = u;
+      }
+    for (int64_t i = 1; i < n; ++i)
+      for (int64_t j = i; j > 0 && slot_mapping[rows[j - 1]] > slot_mapping[rows[j]]; --j) {
+        const int64_t x = rows[j];
+        rows[j] = rows[j - 1];
+        rows[j - 1] = x;
+      }
+    fn(ctx, block, rows, n, off0);
+  }
+  free(rows);
+  free(done);
+}
+
+struct f8_append_ctx {
+  const float *src_k, *src_v;
+  int64_t kv_heads, d, block_size;
+  uint8_t *k_slab, *v_slab;
+  float *k_scale, *v_scale;
+};
+
+static void f8_append_group(void* p, int64_t block, const int64_t* rows, int64_t n, int64_t off0) {
+  const struct f8_append_ctx* c = (const struct f8_append_ctx*)p;
+  for (int64_t h = 0; h < c->kv_heads; ++h) {
+    const int64_t tile = (block * c->kv_heads + h) * c->block_size * c->d;
+    append_f8_tile(c->src_k + h * c->d, c->kv_heads * c->d, rows, n, off0, c->d,
+                   c->k_slab + tile, c->k_scale + block * c->kv_heads + h);
+    append_f8_tile(c->src_v + h * c->d, c->kv_heads * c->d, rows, n, off0, c->d,
+                   c->v_slab + tile, c->v_scale + block * c->kv_heads + h);
+  }
+}
+
+void orc_kv_append_fp8(const float* src_k, const float* src_v, const int64_t* slot_mapping,
+                       int64_t t_dim, int64_t kv_heads, int64_t d, int64_t block_size,
+                       uint8_t* k_slab, uint8_t* v_slab, float* k_scale, float* v_scale) {
+  struct f8_append_ctx c = {src_k, src_v, kv_heads, d, block_size, k_slab, v_slab, k_scale,
+                            v_scale};
+  for_each_block_group(slot_mapping, t_dim, block_size, f8_append_group, &c);
+}
+
+void orc_fp8_dequant(const uint8_t* slab, const float* scale, int64_t num_blocks,
+                     int64_t kv_heads, int64_t block_size, int64_t d, float* out) {
+  const int64_t tile = block_size * d;
+  for (int64_t u = 0; u < num_blocks * kv_heads; ++u)
+    for (int64_t i = 0; i < tile; ++i)
+      out[u * tile + i] = orc_e4m3_to_fp32(slab[u * tile + i]) * scale[u];
+}
+
 void orc_int8_dequant(const int8_t* slab, const float* scale, int64_t num_blocks,
                       int64_t kv_heads, int64_t block_size, int64_t d, float* out) {
   const int64_t tile = block_size * d;

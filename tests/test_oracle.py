@@ -456,3 +456,127 @@ def test_int8_dequant_matches_closed_form(orc):
     s = rng.uniform(0.01, 1, (3, 2)).astype(np.float32)
     x = orc.int8_dequant(q, s)
     assert np.array_equal(x, q.astype(np.float32) * s[:, :, None, None])
+
+
+# ------------------------------------------------------------ FP8 (E4M3) KV
+def _torch_e4m3():
+    torch = pytest.importorskip("torch")
+    return torch
+
+
+def test_e4m3_decode_every_code_matches_torch(orc):
+    """The oracle's E4M3 decoder against torch.float8_e4m3fn on all 256 codes
+    (two independent implementations of the OCP format), and its closed form:
+    bias 7, 3 mantissa bits, subnormals m * 2^-9, 0x7F / 0xFF NaN, 448 max."""
+    torch = _torch_e4m3()
+    codes = np.arange(256, dtype=np.uint8)
+    got = orc.e4m3_to_f32(codes)
+    ref = torch.from_numpy(codes.copy()).view(torch.float8_e4m3fn).to(torch.float32).numpy()
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan) and set(np.where(nan)[0]) == {0x7F, 0xFF}
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+    assert got[0x7E] == 448.0 and got[0x01] == 2.0 ** -9 and got[0x08] == 2.0 ** -6
+    assert got[0x38] == 1.0 and got[0xB8] == -1.0
+
+
+def test_e4m3_encode_matches_torch_on_codes_midpoints_and_samples(orc):
+    """Round to nearest, ties to even: every finite code's value encodes to
+    itself, every midpoint between neighbouring codes goes to the even one,
+    and 20000 log-uniform samples in (2^-12, 464] agree with torch bit for
+    bit; beyond 448 the oracle saturates (torch gives NaN from 480 on)."""
+    torch = _torch_e4m3()
+    codes = np.array([c for c in range(256) if c & 0x7F != 0x7F], np.uint8)
+    vals = orc.e4m3_to_f32(codes)
+    assert np.array_equal(orc.f32_to_e4m3(vals), codes)
+    pos = np.sort(vals[vals > 0])
+    mids = ((pos[:-1].astype(np.float64) + pos[1:]) / 2).astype(np.float32)
+    rng = np.random.default_rng(8)
+    samp = (np.exp2(rng.uniform(-12, np.log2(464), 20000)) *
+            rng.choice([-1, 1], 20000)).astype(np.float32)
+    x = np.concatenate([mids, -mids, samp, np.float32([0.0, -0.0, 448.0, 460.0, 464.0])])
+    ref = torch.from_numpy(x.copy()).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(orc.f32_to_e4m3(x), ref)
+    # ties to even at a midpoint: 1 + 1/16 lies between codes 0x38 (1.0) and 0x39
+    assert orc.f32_to_e4m3(np.float32([1.0625]))[0] == 0x38
+    assert orc.f32_to_e4m3(np.float32([1.1875]))[0] == 0x3A
+    assert list(orc.f32_to_e4m3(np.float32([1000.0, -1e30, np.nan]))) == [0x7E, 0xFE, 0x7F]
+
+
+def fp8_case(nb=6, hkv=2, bs=16, d=8):
+    return (np.zeros((nb, hkv, bs, d), np.uint8), np.zeros((nb, hkv, bs, d), np.uint8),
+            np.zeros((nb, hkv), np.float32), np.zeros((nb, hkv), np.float32))
+
+
+def test_fp8_fresh_block_closed_form(orc):
+    """A fresh block: scale = max|x| / 448 in fp32, the max element maps to
+    +-448, each element is its value to within half an E4M3 step (relative
+    2^-4 of the element, or 2^-10 of the scale below the normal range), and
+    a zero V block gives scale 0 and zero codes."""
+    rng = np.random.default_rng(11)
+    hkv, bs, d = 2, 16, 8
+    k, v, ks, vs = fp8_case(hkv=hkv, bs=bs, d=d)
+    n = 11
+    src_k = (rng.standard_normal((n, hkv, d)) * 3).astype(np.float32)
+    src_v = np.zeros((n, hkv, d), np.float32)
+    orc.kv_append_fp8(src_k, src_v, 3 * bs + np.arange(n), hkv, d, bs, k, v, ks, vs)
+    for h in range(hkv):
+        m = np.abs(src_k[:, h]).max()
+        assert ks[3, h] == np.float32(m) / np.float32(448)
+        y = orc.e4m3_to_f32(k[3, h, :n])
+        assert np.abs(y).max() == 448.0
+        x = y * ks[3, h]
+        tol = np.maximum(np.abs(src_k[:, h]) * 2.0 ** -4, ks[3, h] * 2.0 ** -10) * (1 + 1e-6)
+        assert (np.abs(x - src_k[:, h]) <= tol).all()
+        assert vs[3, h] == 0 and not v[3, h].any()
+
+
+def test_fp8_incremental_appends_requantise(orc):
+    """One row at a time: the scale never decreases and rises exactly when a
+    row exceeds 448 * scale; older rows are requantised to the new scale."""
+    rng = np.random.default_rng(12)
+    hkv, bs, d = 1, 16, 16
+    k, v, ks, vs = fp8_case(hkv=hkv, bs=bs, d=d)
+    amps = [0.5, 0.2, 2.0, 1.0, 7.5, 7.4, 0.1]
+    rows, prev = [], np.float32(0)
+    for off, a in enumerate(amps):
+        x = (rng.uniform(-1, 1, (1, hkv, d)) * a).astype(np.float32)
+        rows.append(x[0, 0])
+        orc.kv_append_fp8(x, x, np.array([2 * bs + off]), hkv, d, bs, k, v, ks, vs)
+        m = np.abs(x).max()
+        exp = np.float32(m) / np.float32(448) if m > prev * np.float32(448) else prev
+        assert ks[2, 0] == exp and ks[2, 0] >= prev
+        prev = ks[2, 0]
+    x = orc.e4m3_to_f32(k[2, 0, :len(amps)]) * ks[2, 0]
+    r = np.array(rows)
+    # two roundings at most (the row's own, then a requantisation)
+    tol = np.maximum(np.abs(r) * 2.0 ** -3, ks[2, 0] * 2.0 ** -9) * (1 + 1e-6)
+    assert (np.abs(x - r) <= tol).all()
+    assert np.array_equal(k, v) and np.array_equal(ks, vs)
+
+
+def test_fp8_batched_equals_ordered_and_ignores_stale_state(orc):
+    """With the max in the first row, one batched call equals row-by-row
+    appends; a block reused at offset 0 ignores its stale scale and rows."""
+    rng = np.random.default_rng(13)
+    hkv, bs, d = 2, 8, 8
+    x = rng.uniform(-1, 1, (bs, hkv, d)).astype(np.float32)
+    x[0] *= 4
+    slots = 5 * bs + np.arange(bs)
+    a = fp8_case(hkv=hkv, bs=bs, d=d)
+    orc.kv_append_fp8(x, x, slots, hkv, d, bs, *a)
+    b = fp8_case(hkv=hkv, bs=bs, d=d)
+    b[0][5] = 77
+    b[2][5] = 1e30  # stale state from a previous owner
+    for i in range(bs):
+        orc.kv_append_fp8(x[i:i + 1], x[i:i + 1], slots[i:i + 1], hkv, d, bs, *b)
+    for u, w in zip(a, b):
+        assert np.array_equal(u, w)
+
+
+def test_fp8_dequant_matches_closed_form(orc):
+    rng = np.random.default_rng(14)
+    q = rng.integers(0, 256, (3, 2, 4, 8)).astype(np.uint8)
+    q[(q & 0x7F) == 0x7F] = 0x10
+    s = rng.uniform(0.01, 1, (3, 2)).astype(np.float32)
+    x = orc.fp8_dequant(q, s)
+    assert np.array_equal(x, orc.e4m3_to_f32(q) * s[:, :, None, None])
