@@ -50,7 +50,7 @@ import numpy as np  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
-KV_NAMES = {0: "f32", 1: "bf16", 2: "int8"}
+KV_NAMES = {0: "f32", 1: "bf16", 2: "int8", 3: "fp8"}
 CPU_SHARE_PER_GPU = 16  # host threads one GPU's job may use on a shared node
 
 
@@ -73,9 +73,9 @@ def parse():
                     help="skip the read-bandwidth probes that price the practical ceiling")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the prefill, fused RoPE and re-prefill side measurements")
-    ap.add_argument("--kv", default="auto", choices=["auto", "int8"],
-                    help="KV element type: the config's own (auto) or INT8 with "
-                         "per-(block, kv head) scales")
+    ap.add_argument("--kv", default="auto", choices=["auto", "int8", "fp8"],
+                    help="KV element type: the config's own (auto), or INT8 or FP8 (E4M3) "
+                         "with per-(block, kv head) scales")
     ap.add_argument("--graph", action="store_true",
                     help="time the step as one eager descriptor upload plus one replay of a "
                          "captured HIP graph of the per-layer launches (stream capture on a "
@@ -104,7 +104,7 @@ def traffic_from_profiles(config: str, kv: str = ""):
     """HBM bytes per attention launch from the committed rocprofv3 PMC summary
     (FETCH_SIZE / WRITE_SIZE per dispatch, each scaled by the same counter's
     reading on a copy kernel of known size), or None when no summary exists
-    for this workload draw. kv: "" for the config's own KV type, "int8"."""
+    for this workload draw. kv: "" for the config's own KV type, "int8", "fp8"."""
     suffix = f"_{kv}" if kv else ""
     p = ROOT / "profiles" / f"decode_{config.lower()}{suffix}_traffic.json"
     if not p.exists():
@@ -338,6 +338,7 @@ class Bench:
     for every layer, and the step loop."""
 
     def __init__(self, ctx, ehip, w, layers, q8, host_layer0):
+        # q8: "" for the config's own KV type, else "int8" or "fp8" (scaled slabs)
         self.ctx, self.ehip, self.w, self.layers, self.q8 = ctx, ehip, w, layers, q8
         H, Hkv, d, bs = w.heads, w.kv_heads, w.head_dim, w.block_size
         R = w.rows
@@ -347,12 +348,17 @@ class Bench:
         for layer in range(layers):
             ks, vs = ctx.alloc(self.slab_bytes), ctx.alloc(self.slab_bytes)
             q, kn, vn = ctx.alloc(R * H * d * 4), ctx.alloc(R * Hkv * d * 4), ctx.alloc(R * Hkv * d * 4)
-            if q8:
+            if q8 == "fp8":
+                # E4M3 slabs: N(0, 64) codes; scales: fp32 normals per (block, kv head)
+                ctx.fill_normal(ks, self.slab_bytes, ehip.KV_FP8, 0.0, 64.0, 10 + layer)
+                ctx.fill_normal(vs, self.slab_bytes, ehip.KV_FP8, 0.0, 64.0, 1000 + layer)
+            if q8 == "int8":
                 # int8 slabs: random bytes (bf16 normals over the same memory);
                 # scales: fp32 normals, one per (block, kv head)
                 n16 = self.slab_bytes // 2
                 ctx.fill_normal(ks, n16, ehip.KV_BF16, 0.0, 1.0, 10 + layer)
                 ctx.fill_normal(vs, n16, ehip.KV_BF16, 0.0, 1.0, 1000 + layer)
+            if q8:
                 kss, vss = ctx.alloc(w.pool_blocks * Hkv * 4), ctx.alloc(w.pool_blocks * Hkv * 4)
                 ctx.fill_normal(kss, w.pool_blocks * Hkv, ehip.KV_F32, 0.0, 0.01, 5000 + layer)
                 ctx.fill_normal(vss, w.pool_blocks * Hkv, ehip.KV_F32, 0.0, 0.01, 6000 + layer)
@@ -408,10 +414,10 @@ class Bench:
                 ctx.record(evs[layer][0])
             if self.q8:
                 kss, vss = self.scales[layer]
-                ctx._check(ctx.step_kv_append_int8(self.kns[layer], self.vns[layer], ks, vs, kss,
-                                                   vss))
-                ctx._check(ctx.step_attention_int8(self.qs[layer], ks, vs, kss, vss,
-                                                   self.outs[layer]))
+                append = getattr(ctx, f"step_kv_append_{self.q8}")
+                attention = getattr(ctx, f"step_attention_{self.q8}")
+                ctx._check(append(self.kns[layer], self.vns[layer], ks, vs, kss, vss))
+                ctx._check(attention(self.qs[layer], ks, vs, kss, vss, self.outs[layer]))
             else:
                 ctx._check(ctx.step_append_attention(self.kns[layer], self.vns[layer],
                                                      self.qs[layer], ks, vs, self.outs[layer]))
@@ -468,9 +474,9 @@ def main():
 
     make = workloads.CONFIGS[args.config]
     w = make(seed=args.seed) if args.seed else make()
-    q8 = args.kv == "int8"
+    q8 = args.kv if args.kv in ("int8", "fp8") else ""
     if q8:
-        w.kv_dtype = ehip.KV_INT8
+        w.kv_dtype = ehip.KV_FP8 if q8 == "fp8" else ehip.KV_INT8
     layers = args.layers or w.layers
     H, Hkv, d, bs = w.heads, w.kv_heads, w.head_dim, w.block_size
     tok = int(w.context_lens.sum())
@@ -589,7 +595,7 @@ def main():
     attn_bytes = per_layer["total"]
     attn_avg = float(attn.mean())
     achieved = attn_bytes / attn_avg / 1e9
-    tr = traffic_from_profiles(w.name, "int8" if q8 else "")
+    tr = traffic_from_profiles(w.name, q8)
     traffic = tr[0] if tr is not None and tr[1] == tok else None  # measured on this draw
 
     result = {

@@ -34,8 +34,10 @@
  *     about 2^-17 relative) on the matrix cores, and P.V in fp32; the causal
  *     prefill-chunk kernel rounds q and the probabilities P to bf16 for its
  *     matrix-core products (fp32 accumulate); INT8 KV forms exact integer
- *     q.k products of a three-digit int8 split of q. The parity bars these
- *     give are stated beside each test.
+ *     q.k products of a three-digit int8 split of q; FP8 KV multiplies the
+ *     E4M3 keys by a four-digit E4M3 split of q (about 2^-16 relative) on the
+ *     fp8 matrix cores. The parity bars these give are stated beside each
+ *     test.
  *   - A context is used from one host thread at a time (the reference's
  *     single engine thread, src/runtime/engine.h:27-33).
  */
@@ -59,10 +61,12 @@ enum {
   EHIP_INTERNAL = 11
 };
 
-/* KV element types. INT8 slabs carry fp32 per-(block, kv head) scales in
- * separate [slab_blocks, kv_heads] arrays (one for K, one for V): the format
- * the reference reserves in docs/design/paged-kv-cache.md:219-231. */
-enum { EHIP_KV_F32 = 0, EHIP_KV_BF16 = 1, EHIP_KV_INT8 = 2 };
+/* KV element types. INT8 and FP8 slabs carry fp32 per-(block, kv head) scales
+ * in separate [slab_blocks, kv_heads] arrays (one for K, one for V): the format
+ * the reference reserves in docs/design/paged-kv-cache.md:219-231. FP8 is the
+ * OCP E4M3 format (4 exponent bits with bias 7, 3 mantissa bits, largest
+ * finite value 448, codes 0x7F / 0xFF NaN). */
+enum { EHIP_KV_F32 = 0, EHIP_KV_BF16 = 1, EHIP_KV_INT8 = 2, EHIP_KV_FP8 = 3 };
 
 typedef struct ehip_ctx ehip_ctx;
 
@@ -74,7 +78,7 @@ typedef struct {
   int32_t kv_heads;     /* Hkv; H % Hkv == 0, group g = H / Hkv              */
   int32_t head_dim;     /* d                                                 */
   int32_t block_size;   /* bs in {8,16,32,64} (src/kvcache/block_pool.cpp:28-31) */
-  int32_t kv_dtype;     /* EHIP_KV_F32 or EHIP_KV_BF16                       */
+  int32_t kv_dtype;     /* EHIP_KV_F32, _BF16, _INT8 or _FP8                 */
   int32_t reserved;     /* must be 0                                         */
   int64_t slab_blocks;  /* blocks in each slab (bounds every block id)       */
   int64_t block_stride; /* elements per block id; 0 = Hkv*bs*d               */
@@ -137,7 +141,8 @@ int ehip_copy_to_host(ehip_ctx* ctx, void* h_dst, const void* d_src, int64_t byt
 int ehip_copy_device(ehip_ctx* ctx, void* d_dst, const void* d_src, int64_t bytes);
 /* Synthetic N(mean, std) fill on the device (counter-based hash + Box-Muller;
  * for benchmarks whose pools are too large to generate on the host).
- * dtype: EHIP_KV_F32 writes float, EHIP_KV_BF16 writes RNE bf16 bits. */
+ * dtype: EHIP_KV_F32 writes float, EHIP_KV_BF16 writes RNE bf16 bits,
+ * EHIP_KV_FP8 writes E4M3 codes (RNE, saturated to +-448). */
 int ehip_fill_normal(ehip_ctx* ctx, void* d_dst, int64_t n, int32_t dtype, float mean,
                      float stddev, uint64_t seed);
 
@@ -307,6 +312,18 @@ int ehip_step_kv_append_int8(ehip_ctx* ctx, const float* d_src_k, const float* d
 int ehip_step_attention_int8(ehip_ctx* ctx, const float* d_q, const void* d_k_slab,
                              const void* d_v_slab, const float* d_k_scale,
                              const float* d_v_scale, float* d_out);
+/* FP8 KV (geometry kv_dtype EHIP_KV_FP8): the same per-(block, kv head)
+ * scaled format and entry points as INT8, with E4M3 codes in place of int8:
+ * scale = max|x| / 448 when a block's range grows, code = E4M3(x / scale) with
+ * round to nearest even (NaN stays NaN, 0x7F). The reference reserves only
+ * the INT8 element type in that seam (docs/design/paged-kv-cache.md:219-231);
+ * FP8 is a second element type behind the same scale parameters. Covered
+ * shapes as for INT8. */
+int ehip_step_kv_append_fp8(ehip_ctx* ctx, const float* d_src_k, const float* d_src_v,
+                            void* d_k_slab, void* d_v_slab, float* d_k_scale, float* d_v_scale);
+int ehip_step_attention_fp8(ehip_ctx* ctx, const float* d_q, const void* d_k_slab,
+                            const void* d_v_slab, const float* d_k_scale, const float* d_v_scale,
+                            float* d_out);
 /* Counts of the uploaded plan (rows, work items, split partials). */
 int ehip_step_info(const ehip_ctx* ctx, int64_t* rows, int64_t* items, int64_t* partials);
 

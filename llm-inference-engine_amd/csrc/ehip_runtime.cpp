@@ -465,7 +465,8 @@ int ehip_copy_device(ehip_ctx* ctx, void* d_dst, const void* d_src, int64_t byte
 int ehip_fill_normal(ehip_ctx* ctx, void* d_dst, int64_t n, int32_t dtype, float mean,
                      float stddev, uint64_t seed) {
   if (int rc = CheckCtx(ctx)) return rc;
-  if (n < 0 || (n > 0 && !d_dst) || (dtype != EHIP_KV_F32 && dtype != EHIP_KV_BF16))
+  if (n < 0 || (n > 0 && !d_dst) ||
+      (dtype != EHIP_KV_F32 && dtype != EHIP_KV_BF16 && dtype != EHIP_KV_FP8))
     return SetError(ctx, EHIP_INVALID_ARGUMENT, "bad fill arguments");
   EHIP_HIP(ctx, ehip::LaunchFillNormal(d_dst, n, dtype, mean, stddev, seed, ctx->stream));
   return EHIP_OK;
@@ -797,9 +798,9 @@ int ehip_step_kv_append(ehip_ctx* ctx, const float* d_src_k, const float* d_src_
   if (!d_src_k || !d_src_v || !d_k_slab || !d_v_slab)
     return SetError(ctx, EHIP_INVALID_ARGUMENT, "null append operand");
   const ehip_geometry& g = ctx->geom;
-  if (g.kv_dtype == EHIP_KV_INT8)
+  if (ehip::ScaledKv(g.kv_dtype))
     return SetError(ctx, EHIP_INVALID_ARGUMENT,
-                    "INT8 slabs carry scales: use ehip_step_kv_append_int8");
+                    "INT8/FP8 slabs carry scales: use ehip_step_kv_append_int8 or _fp8");
   if (ehip::BlockStride(g) != int64_t{g.kv_heads} * g.block_size * g.head_dim)
     return SetError(ctx, EHIP_UNIMPLEMENTED, "append needs the dense Hkv*bs*d block stride");
   EHIP_HIP(ctx, ehip::LaunchKvScatter(d_src_k, d_src_v, ctx->d_slots,
@@ -821,7 +822,7 @@ int ehip_step_rope_kv_append(ehip_ctx* ctx, float* d_q, const float* d_src_k,
   if (!d_q || !d_src_k || !d_src_v || !d_cos || !d_sin || !d_k_slab || !d_v_slab)
     return SetError(ctx, EHIP_INVALID_ARGUMENT, "null rope/append operand");
   const ehip_geometry& g = ctx->geom;
-  if (g.kv_dtype == EHIP_KV_INT8)
+  if (ehip::ScaledKv(g.kv_dtype))
     return SetError(ctx, EHIP_UNIMPLEMENTED, "fused RoPE + append covers fp32 and bf16 slabs");
   if (g.head_dim % 2 != 0)
     return SetError(ctx, EHIP_INVALID_ARGUMENT, "RoPE needs an even head_dim (got %d)",
@@ -847,9 +848,9 @@ int ehip_step_attention(ehip_ctx* ctx, const float* d_q, const void* d_k_slab,
   if (ctx->plan.rows.empty()) return EHIP_OK;
   if (!d_q || !d_k_slab || !d_v_slab || !d_out)
     return SetError(ctx, EHIP_INVALID_ARGUMENT, "null attention operand");
-  if (ctx->geom.kv_dtype == EHIP_KV_INT8)
+  if (ehip::ScaledKv(ctx->geom.kv_dtype))
     return SetError(ctx, EHIP_INVALID_ARGUMENT,
-                    "INT8 slabs carry scales: use ehip_step_attention_int8");
+                    "INT8/FP8 slabs carry scales: use ehip_step_attention_int8 or _fp8");
   return LaunchAttention(ctx, d_q, d_k_slab, d_v_slab, d_out);
 }
 
@@ -864,9 +865,9 @@ int ehip_step_append_attention(ehip_ctx* ctx, const float* d_src_k, const float*
     return SetError(ctx, EHIP_FAILED_PRECONDITION, "the uploaded step has no slot mapping");
   if (!d_src_k || !d_src_v || !d_q || !d_k_slab || !d_v_slab || !d_out)
     return SetError(ctx, EHIP_INVALID_ARGUMENT, "null append/attention operand");
-  if (g.kv_dtype == EHIP_KV_INT8)
+  if (ehip::ScaledKv(g.kv_dtype))
     return SetError(ctx, EHIP_INVALID_ARGUMENT,
-                    "INT8 slabs carry scales: use ehip_step_kv_append_int8 + ehip_step_attention_int8");
+                    "INT8/FP8 slabs carry scales: use the _int8 / _fp8 append and attention");
   if (ehip::BlockStride(g) != int64_t{g.kv_heads} * g.block_size * g.head_dim)
     return SetError(ctx, EHIP_UNIMPLEMENTED, "append needs the dense Hkv*bs*d block stride");
   // One launch (plus the split merge) when every row is a decode row on the
@@ -885,14 +886,17 @@ int ehip_step_append_attention(ehip_ctx* ctx, const float* d_src_k, const float*
   return LaunchAttention(ctx, d_q, d_k_slab, d_v_slab, d_out);
 }
 
-int ehip_step_kv_append_int8(ehip_ctx* ctx, const float* d_src_k, const float* d_src_v,
-                             void* d_k_slab, void* d_v_slab, float* d_k_scale, float* d_v_scale) {
+namespace {
+
+int ScaledAppend(ehip_ctx* ctx, int kv_dtype, const float* d_src_k, const float* d_src_v,
+                 void* d_k_slab, void* d_v_slab, float* d_k_scale, float* d_v_scale) {
   if (int rc = CheckCtx(ctx)) return rc;
   if (!ctx->have_step) return SetError(ctx, EHIP_FAILED_PRECONDITION, "no step uploaded");
   const Plan& plan = ctx->plan;
   const ehip_geometry& g = ctx->geom;
-  if (g.kv_dtype != EHIP_KV_INT8)
-    return SetError(ctx, EHIP_INVALID_ARGUMENT, "the uploaded geometry is not INT8 KV");
+  if (g.kv_dtype != kv_dtype)
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "the uploaded geometry is not %s KV",
+                    kv_dtype == EHIP_KV_FP8 ? "FP8" : "INT8");
   if (plan.slots.empty()) {
     if (plan.rows.empty()) return EHIP_OK;
     return SetError(ctx, EHIP_FAILED_PRECONDITION, "the uploaded step has no slot mapping");
@@ -904,25 +908,52 @@ int ehip_step_kv_append_int8(ehip_ctx* ctx, const float* d_src_k, const float* d
   EHIP_HIP(ctx, ehip::LaunchAppendQ8(d_src_k, d_src_v, ctx->d_q8_groups,
                                      static_cast<int64_t>(plan.q8_groups.size()), ctx->d_q8_rows,
                                      g.kv_heads, g.head_dim, g.block_size, g.slab_blocks,
-                                     d_k_slab, d_v_slab, d_k_scale, d_v_scale, ctx->d_err,
-                                     ctx->stream));
+                                     d_k_slab, d_v_slab, d_k_scale, d_v_scale,
+                                     kv_dtype == EHIP_KV_FP8, ctx->d_err, ctx->stream));
   return EHIP_OK;
+}
+
+int ScaledAttention(ehip_ctx* ctx, int kv_dtype, const float* d_q, const void* d_k_slab,
+                    const void* d_v_slab, const float* d_k_scale, const float* d_v_scale,
+                    float* d_out) {
+  if (int rc = CheckCtx(ctx)) return rc;
+  if (!ctx->have_step) return SetError(ctx, EHIP_FAILED_PRECONDITION, "no step uploaded");
+  const ehip_geometry& g = ctx->geom;
+  if (g.kv_dtype != kv_dtype)
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "the uploaded geometry is not %s KV",
+                    kv_dtype == EHIP_KV_FP8 ? "FP8" : "INT8");
+  if (ctx->plan.rows.empty()) return EHIP_OK;
+  if (!d_q || !d_k_slab || !d_v_slab || !d_k_scale || !d_v_scale || !d_out)
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "null attention operand");
+  if (g.slab_blocks * g.kv_heads >= (int64_t{1} << 29))
+    return SetError(ctx, EHIP_UNIMPLEMENTED, "scale arrays above 2 GiB");
+  return LaunchAttention(ctx, d_q, d_k_slab, d_v_slab, d_out, d_k_scale, d_v_scale);
+}
+
+}  // namespace
+
+int ehip_step_kv_append_int8(ehip_ctx* ctx, const float* d_src_k, const float* d_src_v,
+                             void* d_k_slab, void* d_v_slab, float* d_k_scale, float* d_v_scale) {
+  return ScaledAppend(ctx, EHIP_KV_INT8, d_src_k, d_src_v, d_k_slab, d_v_slab, d_k_scale,
+                      d_v_scale);
 }
 
 int ehip_step_attention_int8(ehip_ctx* ctx, const float* d_q, const void* d_k_slab,
                              const void* d_v_slab, const float* d_k_scale,
                              const float* d_v_scale, float* d_out) {
-  if (int rc = CheckCtx(ctx)) return rc;
-  if (!ctx->have_step) return SetError(ctx, EHIP_FAILED_PRECONDITION, "no step uploaded");
-  const ehip_geometry& g = ctx->geom;
-  if (g.kv_dtype != EHIP_KV_INT8)
-    return SetError(ctx, EHIP_INVALID_ARGUMENT, "the uploaded geometry is not INT8 KV");
-  if (ctx->plan.rows.empty()) return EHIP_OK;
-  if (!d_q || !d_k_slab || !d_v_slab || !d_k_scale || !d_v_scale || !d_out)
-    return SetError(ctx, EHIP_INVALID_ARGUMENT, "null attention operand");
-  if (g.slab_blocks * g.kv_heads >= (int64_t{1} << 29))
-    return SetError(ctx, EHIP_UNIMPLEMENTED, "INT8 scale arrays above 2 GiB");
-  return LaunchAttention(ctx, d_q, d_k_slab, d_v_slab, d_out, d_k_scale, d_v_scale);
+  return ScaledAttention(ctx, EHIP_KV_INT8, d_q, d_k_slab, d_v_slab, d_k_scale, d_v_scale, d_out);
+}
+
+int ehip_step_kv_append_fp8(ehip_ctx* ctx, const float* d_src_k, const float* d_src_v,
+                            void* d_k_slab, void* d_v_slab, float* d_k_scale, float* d_v_scale) {
+  return ScaledAppend(ctx, EHIP_KV_FP8, d_src_k, d_src_v, d_k_slab, d_v_slab, d_k_scale,
+                      d_v_scale);
+}
+
+int ehip_step_attention_fp8(ehip_ctx* ctx, const float* d_q, const void* d_k_slab,
+                            const void* d_v_slab, const float* d_k_scale, const float* d_v_scale,
+                            float* d_out) {
+  return ScaledAttention(ctx, EHIP_KV_FP8, d_q, d_k_slab, d_v_slab, d_k_scale, d_v_scale, d_out);
 }
 
 int ehip_step_info(const ehip_ctx* ctx, int64_t* rows, int64_t* items, int64_t* partials) {

@@ -47,7 +47,7 @@ struct DecodeParams {
   float scale_log2;         // scale * log2(e)
   int64_t max_length;       // longest row (keys attended)
   int32_t has_prefill;      // the step also has MFMA prefill items
-  const float* k_scale;     // INT8 KV: per-(block, kv head) scales [slab_blocks, Hkv]
+  const float* k_scale;     // INT8/FP8 KV: per-(block, kv head) scales [slab_blocks, Hkv]
   const float* v_scale;
   // Fused append (bf16 MFMA decode of an all-decode step): the step's new K/V
   // rows [rows, Hkv, d] fp32 and their slots. The item flagged as its row's
@@ -124,8 +124,9 @@ bool DecodeMfmaCovers(const DecodeParams& p);
 // shape is not covered (d not 64/128, g not 1/2/4/8, bs < 16, misaligned).
 bool LaunchDecodeMfma(const DecodeParams& p, QueueState* queue, hipStream_t stream,
                       hipError_t* err);
-// INT8 KV decode (paged_decode_q8.hip); false when the shape is not covered.
-bool LaunchDecodeQ8(const DecodeParams& p, hipStream_t stream, hipError_t* err);
+// INT8 or FP8 (E4M3) KV decode (paged_decode_q8.hip); false when the shape
+// is not covered.
+bool LaunchDecodeQ8(const DecodeParams& p, bool fp8, hipStream_t stream, hipError_t* err);
 
 // KvScatter: rows [T, Hkv, d] fp32 into slabs (fp32 copy or bf16 RNE).
 hipError_t LaunchKvScatter(const float* src_k, const float* src_v, const int64_t* slots,
@@ -138,12 +139,12 @@ hipError_t LaunchKvGather(const float* k_slab, const float* v_slab, const int32_
                           int64_t slab_blocks, float* out_k, float* out_v, int32_t* err,
                           hipStream_t stream);
 
-// INT8 append with per-(block, kv head) scales, one wavefront per
-// (append group, kv head).
+// INT8 or FP8 (E4M3) append with per-(block, kv head) scales, one wavefront
+// per (append group, kv head).
 hipError_t LaunchAppendQ8(const float* src_k, const float* src_v, const Q8Group* groups,
                           int64_t n_groups, const int32_t* rows, int kv_heads, int d, int bs,
                           int64_t slab_blocks, void* k_slab, void* v_slab, float* k_scale,
-                          float* v_scale, int32_t* err, hipStream_t stream);
+                          float* v_scale, bool fp8, int32_t* err, hipStream_t stream);
 
 // Fused RoPE + KV append of one step's rows (q rotated in place; rotated K and
 // V scattered at the rows' slots; row r at position rows[r].length - 1).

@@ -33,6 +33,11 @@ __device__ __forceinline__ void Store1(float* dst, float x) { *dst = x; }
 __device__ __forceinline__ void Store1(uint16_t* dst, float x) {
   *dst = static_cast<uint16_t>(Fp32ToBf16Bits(x));
 }
+// E4M3 code of x saturated to +-448 (v_cvt_pk_fp8_f32 rounds to nearest even).
+__device__ __forceinline__ void Store1(uint8_t* dst, float x) {
+  const float c = fminf(fmaxf(x, -448.0f), 448.0f);
+  *dst = static_cast<uint8_t>(__builtin_amdgcn_cvt_pk_fp8_f32(c, c, 0, false) & 0xFF);
+}
 
 // d % 4 == 0 path.
 template <class KV>
@@ -198,16 +203,18 @@ __global__ __launch_bounds__(256) void RopeKvAppend(
   }
 }
 
-// INT8 append with per-(block, kv head) scales. One wavefront per (append
-// group, kv head): the group's rows land at consecutive offsets
+// INT8 / FP8 append with per-(block, kv head) scales. One wavefront per
+// (append group, kv head): the group's rows land at consecutive offsets
 // [off0, off0 + n) of one block. For K, then V: m = max |x| over the new rows;
 // the stored scale counts only when off0 > 0 (offset 0 is a freshly allocated
-// block, whatever an earlier owner left); if m exceeds 127 times that scale,
-// the scale becomes m / 127 and the block's older rows are requantised. Each
-// value is quant(x, s) = 0 if s == 0, else clamp(rint(x * (1 / s)), -127, 127),
-// in fp32 with round-to-nearest-even throughout, so the slabs and scales are
-// bit-identical to the CPU restatement. Lanes handle 4 consecutive elements
-// (d % 4 == 0).
+// block, whatever an earlier owner left); if m exceeds R times that scale (R =
+// 127 for int8, 448 for E4M3), the scale becomes m / R and the block's older
+// rows are requantised. Each value is quant(x, s) = 0 if s == 0, else the code
+// of y = x * (1 / s): int8 clamp(rint(y), -127, 127); E4M3 of clamp(y, -448,
+// 448) rounded to nearest even (v_cvt_pk_fp8_f32 is exact RNE there), NaN
+// giving 0x7F. All in fp32 with round-to-nearest-even, so the slabs and
+// scales are bit-identical to the CPU restatement. Lanes handle 4 consecutive
+// elements (d % 4 == 0).
 __device__ __forceinline__ int32_t Q8(float x, float inv, bool zero) {
   if (zero) return 0;
   const float y = fminf(fmaxf(rintf(x * inv), -127.0f), 127.0f);
@@ -219,13 +226,53 @@ __device__ __forceinline__ uint32_t Pack4(int32_t a, int32_t b, int32_t c, int32
          ((static_cast<uint32_t>(c) & 0xFFu) << 16) | (static_cast<uint32_t>(e) << 24);
 }
 
+// Four E4M3 codes of x * inv (zero: all 0).
+__device__ __forceinline__ uint32_t PackF8(float4 x, float inv, bool zero) {
+  const float y[4] = {x.x * inv, x.y * inv, x.z * inv, x.w * inv};
+  float c[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) c[i] = fminf(fmaxf(y[i], -448.0f), 448.0f);
+  uint32_t w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(c[0], c[1], 0, false));
+  w = static_cast<uint32_t>(
+      __builtin_amdgcn_cvt_pk_fp8_f32(c[2], c[3], static_cast<int>(w), true));
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (y[i] != y[i]) w = (w & ~(0xFFu << (8 * i))) | (0x7Fu << (8 * i));
+  return zero ? 0u : w;
+}
+
+// The four values a stored word holds, times s.
+template <bool F8>
+__device__ __forceinline__ float4 Unpack4(uint32_t w, float s) {
+  if constexpr (F8) {
+    const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), false);
+    const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), true);
+    return make_float4(lo[0] * s, lo[1] * s, hi[0] * s, hi[1] * s);
+  } else {
+    return make_float4(static_cast<float>(static_cast<int8_t>(w)) * s,
+                       static_cast<float>(static_cast<int8_t>(w >> 8)) * s,
+                       static_cast<float>(static_cast<int8_t>(w >> 16)) * s,
+                       static_cast<float>(static_cast<int8_t>(w >> 24)) * s);
+  }
+}
+
+template <bool F8>
+__device__ __forceinline__ uint32_t Quant4(float4 x, float inv, bool zero) {
+  if constexpr (F8)
+    return PackF8(x, inv, zero);
+  else
+    return Pack4(Q8(x.x, inv, zero), Q8(x.y, inv, zero), Q8(x.z, inv, zero), Q8(x.w, inv, zero));
+}
+
+template <bool F8>
 __global__ __launch_bounds__(64) void AppendQ8(const float* __restrict__ src_k,
                                                const float* __restrict__ src_v,
                                                const Q8Group* __restrict__ groups,
                                                const int32_t* __restrict__ rows, int kv_heads,
                                                int d, int bs, int64_t slab_blocks,
-                                               int8_t* k_slab, int8_t* v_slab, float* k_scale,
+                                               uint8_t* k_slab, uint8_t* v_slab, float* k_scale,
                                                float* v_scale, int32_t* err) {
+  constexpr float kRange = F8 ? 448.0f : 127.0f;
   const int gi = blockIdx.x / kv_heads;
   const int h = blockIdx.x - gi * kv_heads;
   const int lane = threadIdx.x;
@@ -254,27 +301,16 @@ __global__ __launch_bounds__(64) void AppendQ8(const float* __restrict__ src_k,
     m = WaveMax(m);
     const float s0 = gr.off0 > 0 ? *sc : 0.f;
     float s1 = s0;
-    if (m > s0 * 127.0f) {
-      s1 = m / 127.0f;
+    if (m > s0 * kRange) {
+      s1 = m / kRange;
       const float inv = 1.0f / s1;
       const bool zero = s1 == 0.0f;
-      for (int i = lane; i < gr.off0 * d4; i += 64) {
-        const uint32_t w = dst[i];
-        const float x0 = static_cast<float>(static_cast<int8_t>(w)) * s0;
-        const float x1 = static_cast<float>(static_cast<int8_t>(w >> 8)) * s0;
-        const float x2 = static_cast<float>(static_cast<int8_t>(w >> 16)) * s0;
-        const float x3 = static_cast<float>(static_cast<int8_t>(w >> 24)) * s0;
-        dst[i] = Pack4(Q8(x0, inv, zero), Q8(x1, inv, zero), Q8(x2, inv, zero),
-                       Q8(x3, inv, zero));
-      }
+      for (int i = lane; i < gr.off0 * d4; i += 64)
+        dst[i] = Quant4<F8>(Unpack4<F8>(dst[i], s0), inv, zero);
     }
     const float inv = 1.0f / s1;
     const bool zero = s1 == 0.0f;
-    for (int i = lane; i < ne4; i += 64) {
-      const float4 x = src4(i);
-      dst[gr.off0 * d4 + i] =
-          Pack4(Q8(x.x, inv, zero), Q8(x.y, inv, zero), Q8(x.z, inv, zero), Q8(x.w, inv, zero));
-    }
+    for (int i = lane; i < ne4; i += 64) dst[gr.off0 * d4 + i] = Quant4<F8>(src4(i), inv, zero);
     if (lane == 0) *sc = s1;
   }
 }
@@ -338,12 +374,13 @@ int GridFor(int64_t work, int block) {
 hipError_t LaunchAppendQ8(const float* src_k, const float* src_v, const Q8Group* groups,
                           int64_t n_groups, const int32_t* rows, int kv_heads, int d, int bs,
                           int64_t slab_blocks, void* k_slab, void* v_slab, float* k_scale,
-                          float* v_scale, int32_t* err, hipStream_t stream) {
+                          float* v_scale, bool fp8, int32_t* err, hipStream_t stream) {
   if (n_groups <= 0) return hipSuccess;
   if (d % 4 != 0 || n_groups * kv_heads > 0x7FFFFFFF) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(AppendQ8, dim3(static_cast<uint32_t>(n_groups * kv_heads)), dim3(64), 0,
-                     stream, src_k, src_v, groups, rows, kv_heads, d, bs, slab_blocks,
-                     static_cast<int8_t*>(k_slab), static_cast<int8_t*>(v_slab), k_scale,
+  hipLaunchKernelGGL(fp8 ? AppendQ8<true> : AppendQ8<false>,
+                     dim3(static_cast<uint32_t>(n_groups * kv_heads)), dim3(64), 0, stream,
+                     src_k, src_v, groups, rows, kv_heads, d, bs, slab_blocks,
+                     static_cast<uint8_t*>(k_slab), static_cast<uint8_t*>(v_slab), k_scale,
                      v_scale, err);
   return hipGetLastError();
 }
@@ -434,6 +471,9 @@ hipError_t LaunchFillNormal(void* dst, int64_t n, int dtype, float mean, float s
   if (dtype == EHIP_KV_BF16)
     hipLaunchKernelGGL(FillNormal<uint16_t>, dim3(GridFor(n, 256)), dim3(256), 0, stream,
                        static_cast<uint16_t*>(dst), n, mean, stddev, seed);
+  else if (dtype == EHIP_KV_FP8)
+    hipLaunchKernelGGL(FillNormal<uint8_t>, dim3(GridFor(n, 256)), dim3(256), 0, stream,
+                       static_cast<uint8_t*>(dst), n, mean, stddev, seed);
   else
     hipLaunchKernelGGL(FillNormal<float>, dim3(GridFor(n, 256)), dim3(256), 0, stream,
                        static_cast<float*>(dst), n, mean, stddev, seed);

@@ -606,11 +606,11 @@ bool LaunchSmallStep(const DecodeParams& p, hipStream_t stream, hipError_t* err)
 
 hipError_t LaunchSplits(const DecodeParams& p, int kv_dtype, QueueState* queue,
                         hipStream_t stream) {
-  if (kv_dtype == EHIP_KV_INT8) {
-    // No VALU fallback for INT8: the plan validation admits only the shapes
-    // the MFMA kernel covers.
+  if (ScaledKv(kv_dtype)) {
+    // No VALU fallback for INT8/FP8: the plan validation admits only the
+    // shapes the MFMA kernel covers.
     hipError_t err = hipSuccess;
-    if (LaunchDecodeQ8(p, stream, &err)) return err;
+    if (LaunchDecodeQ8(p, kv_dtype == EHIP_KV_FP8, stream, &err)) return err;
     return hipErrorInvalidValue;
   }
   if (kv_dtype != EHIP_KV_BF16) return LaunchTyped<float>(p, stream);

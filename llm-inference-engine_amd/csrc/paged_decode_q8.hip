@@ -1,7 +1,7 @@
-// INT8-KV paged decode for gfx950: per-(block, kv head) scales, one 64-lane
-// wavefront per work item (row, kv head, key range).
+// INT8- and FP8-KV paged decode for gfx950: per-(block, kv head) scales, one
+// 64-lane wavefront per work item (row, kv head, key range).
 //
-// The slabs hold int8 K/V [slab_blocks, Hkv, bs, d] with fp32 scales
+// The slabs hold int8 or E4M3 K/V [slab_blocks, Hkv, bs, d] with fp32 scales
 // [slab_blocks, Hkv] beside them (the layout the reference reserves for INT8
 // KV, docs/design/paged-kv-cache.md:219-231). Attention is the same online
 // softmax over the dequantised values x = q * scale as the fp32/bf16 paths
@@ -23,6 +23,19 @@
 //    probability when it is written for the PV layout); the
 //    128 * sum(p * v_scale) offset is taken out once per item; token groups
 //    are summed across lanes at the end.
+//
+// FP8 (E4M3) slabs take the same loads, tiles, softmax and outputs; two steps
+// differ:
+//  * QK^T runs on v_mfma_f32_16x16x32_bf16: the lane's D/4 key bytes (the
+//    same loads as INT8) are widened to bf16 with v_cvt_scalef32_pk_bf16_fp8
+//    (two per instruction, scale 1: every E4M3 value is a bf16 value), and q
+//    is split into bf16 hi + lo (q = hi + lo to ~2^-17 relative, as in the
+//    bf16 decode kernel). The fp8 matrix-core form
+//    (v_mfma_scale_f32_16x16x128_f8f6f4 over E4M3 digits of q) measured
+//    1e-4..2e-4 relative output error where a CPU model of the digit split
+//    alone gives ~1e-6, so it stays out.
+//  * PV converts the V bytes with v_cvt_pk_f32_fp8 (two per instruction);
+//    signed codes need no offset correction.
 //
 // Rows past a key range read as zeros through bounded buffer descriptors and
 // are masked; split results go through the same partial/merge path as the
@@ -80,7 +93,20 @@ struct TileQ8 {
 // their shared prefix) puts the second row's g heads in MFMA rows g..2g-1, so
 // its keys are read and multiplied once for both rows; only the PV work
 // grows with the virtual heads.
-template <int D, int G, int TH, int OCC, int RMAX>
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+
+// Eight E4M3 codes (two words) as eight bf16 values (exact).
+__device__ __forceinline__ bf16x8_t Fp8x8ToBf16(uint32_t w0, uint32_t w1) {
+  const bf16x2_t a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(static_cast<int>(w0), 1.0f, false);
+  const bf16x2_t b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(static_cast<int>(w0), 1.0f, true);
+  const bf16x2_t c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(static_cast<int>(w1), 1.0f, false);
+  const bf16x2_t d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(static_cast<int>(w1), 1.0f, true);
+  return bf16x8_t{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+template <int D, int G, int TH, int OCC, int RMAX, bool F8>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(OCC)))
 void DecodeMfmaQ8(DecodeParams p) {
   using T = TileQ8<D, TH>;
@@ -186,8 +212,12 @@ void DecodeMfmaQ8(DecodeParams p) {
   else
     load(bufA, tb, false);
 
-  // Query digits per 16-element chunk (KL chunks), three int8 digits each.
-  i32x4_t qd[KL][3];
+  // Query operands: int8, three digits per 16-element chunk (KL chunks);
+  // FP8 keys, bf16 hi + lo per 8-element chunk (KB / 8 chunks).
+  constexpr int NC8 = KB / 8;
+  constexpr float kQRange = 127.0f;
+  i32x4_t qd[KL][F8 ? 1 : 3];
+  bf16x8_t qh[F8 ? NC8 : 1], ql[F8 ? NC8 : 1];
   float sq4[4];  // s_q of the heads 4 * kq + i (this lane's accumulator rows)
   {
     float amax = 0.f;
@@ -195,33 +225,45 @@ void DecodeMfmaQ8(DecodeParams p) {
     for (int i = 0; i < KB; ++i) amax = fmaxf(amax, fabsf(qf[i]));
     amax = fmaxf(amax, ShflXor(amax, 16));
     amax = fmaxf(amax, ShflXor(amax, 32));
-    const float inv = (live && amax > 0.f) ? 127.0f / amax : 0.f;
-    const float sq = live ? amax * (1.0f / 127.0f) : 0.f;
+    const float inv = (live && amax > 0.f) ? kQRange / amax : 0.f;
+    const float sq = F8 ? 1.0f : (live ? amax * (1.0f / kQRange) : 0.f);
+    if constexpr (F8) {
 #pragma unroll
-    for (int c = 0; c < KL; ++c) {
-      uint32_t w[3][4];
+      for (int c = 0; c < NC8; ++c)
 #pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        int d1[4], d2[4], d3[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float x = qf[c * 16 + g4 * 4 + j] * inv;
-          const float r1 = rintf(x);
-          const float x2 = (x - r1) * 128.0f;
-          const float r2 = rintf(x2);
-          const float r3 = rintf((x2 - r2) * 128.0f);
-          d1[j] = static_cast<int>(r1);
-          d2[j] = static_cast<int>(r2);
-          d3[j] = static_cast<int>(r3);
+        for (int i = 0; i < 8; ++i) {
+          const float xv = live ? qf[8 * c + i] : 0.f;
+          const __bf16 hb = static_cast<__bf16>(xv);
+          qh[c][i] = hb;
+          ql[c][i] = static_cast<__bf16>(xv - static_cast<float>(hb));
         }
-        w[0][g4] = PackDigits(d1);
-        w[1][g4] = PackDigits(d2);
-        w[2][g4] = PackDigits(d3);
-      }
+    } else {
 #pragma unroll
-      for (int dg = 0; dg < 3; ++dg)
-        qd[c][dg] = i32x4_t{static_cast<int>(w[dg][0]), static_cast<int>(w[dg][1]),
-                            static_cast<int>(w[dg][2]), static_cast<int>(w[dg][3])};
+      for (int c = 0; c < KL; ++c) {
+        uint32_t w[3][4];
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          int d1[4], d2[4], d3[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float x = qf[c * 16 + g4 * 4 + j] * inv;
+            const float r1 = rintf(x);
+            const float x2 = (x - r1) * 128.0f;
+            const float r2 = rintf(x2);
+            const float r3 = rintf((x2 - r2) * 128.0f);
+            d1[j] = static_cast<int>(r1);
+            d2[j] = static_cast<int>(r2);
+            d3[j] = static_cast<int>(r3);
+          }
+          w[0][g4] = PackDigits(d1);
+          w[1][g4] = PackDigits(d2);
+          w[2][g4] = PackDigits(d3);
+        }
+#pragma unroll
+        for (int dg = 0; dg < 3; ++dg)
+          qd[c][dg] = i32x4_t{static_cast<int>(w[dg][0]), static_cast<int>(w[dg][1]),
+                              static_cast<int>(w[dg][2]), static_cast<int>(w[dg][3])};
+      }
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -242,23 +284,36 @@ void DecodeMfmaQ8(DecodeParams p) {
     float s[TH][4];
 #pragma unroll
     for (int h2 = 0; h2 < TH; ++h2) {
-      i32x4_t a1 = {0, 0, 0, 0}, a2 = {0, 0, 0, 0}, a3 = {0, 0, 0, 0};
+      float dot[4];
+      if constexpr (F8) {
+        f32x4_t a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int c = 0; c < KL; ++c) {
-        const i32x4_t kb = __builtin_bit_cast(i32x4_t, t.k[h2][c]);
-        a1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(qd[c][0], kb, a1, 0, 0, 0);
-        a2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(qd[c][1], kb, a2, 0, 0, 0);
-        a3 = __builtin_amdgcn_mfma_i32_16x16x64_i8(qd[c][2], kb, a3, 0, 0, 0);
+        for (int c = 0; c < NC8; ++c) {
+          const uint4 w = t.k[h2][c / 2];
+          const bf16x8_t kb = (c & 1) ? Fp8x8ToBf16(w.z, w.w) : Fp8x8ToBf16(w.x, w.y);
+          a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qh[c], kb, a, 0, 0, 0);
+          a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ql[c], kb, a, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dot[i] = a[i];
+      } else {
+        i32x4_t a1 = {0, 0, 0, 0}, a2 = {0, 0, 0, 0}, a3 = {0, 0, 0, 0};
+#pragma unroll
+        for (int c = 0; c < KL; ++c) {
+          const i32x4_t kb = __builtin_bit_cast(i32x4_t, t.k[h2][c]);
+          a1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(qd[c][0], kb, a1, 0, 0, 0);
+          a2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(qd[c][1], kb, a2, 0, 0, 0);
+          a3 = __builtin_amdgcn_mfma_i32_16x16x64_i8(qd[c][2], kb, a3, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          dot[i] = fmaf(static_cast<float>(a3[i]), 1.0f / 16384.0f,
+                        fmaf(static_cast<float>(a2[i]), 1.0f / 128.0f, static_cast<float>(a1[i])));
       }
       const bool valid = t.phys[h2] >= 0 && t0 + 16 * h2 + n < te;
       const float sc = t.ks[h2] * p.scale_log2;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float dot = fmaf(static_cast<float>(a3[i]), 1.0f / 16384.0f,
-                               fmaf(static_cast<float>(a2[i]), 1.0f / 128.0f,
-                                    static_cast<float>(a1[i])));
-        s[h2][i] = valid ? dot * (sq4[i] * sc) : -INFINITY;
-      }
+      for (int i = 0; i < 4; ++i) s[h2][i] = valid ? dot[i] * (sq4[i] * sc) : -INFINITY;
     }
     float alpha[4];
 #pragma unroll
@@ -278,10 +333,10 @@ void DecodeMfmaQ8(DecodeParams p) {
         // The half's V scale rides on the probability (one multiply per
         // score here instead of one per V element in the PV loop).
         s[h2][i] = pr * t.vs[h2];
-        pc += s[h2][i];
+        if constexpr (!F8) pc += s[h2][i];
       }
       lsum[i] = lsum[i] * alpha[i] + ps;
-      cofs[i] = cofs[i] * alpha[i] + pc;
+      if constexpr (!F8) cofs[i] = cofs[i] * alpha[i] + pc;
     }
     if (kq < HR) {
 #pragma unroll
@@ -305,9 +360,21 @@ void DecodeMfmaQ8(DecodeParams p) {
 #pragma unroll
       for (int j = 0; j < VJ; ++j) {
         const int tt = 16 * h2 + j * VT + tv;
-        const uint32_t r = t.v[h2][j] ^ 0x80808080u;  // u = q + 128
-        const float v0 = UByteF(r, 0), v1 = UByteF(r, 1);
-        const float v2 = UByteF(r, 2), v3 = UByteF(r, 3);
+        float v0, v1, v2, v3;
+        if constexpr (F8) {
+          const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(t.v[h2][j]), false);
+          const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(t.v[h2][j]), true);
+          v0 = lo[0];
+          v1 = lo[1];
+          v2 = hi[0];
+          v3 = hi[1];
+        } else {
+          const uint32_t r = t.v[h2][j] ^ 0x80808080u;  // u = q + 128
+          v0 = UByteF(r, 0);
+          v1 = UByteF(r, 1);
+          v2 = UByteF(r, 2);
+          v3 = UByteF(r, 3);
+        }
         float pv[HP];
 #pragma unroll
         for (int r4 = 0; r4 < HR; ++r4) {
@@ -348,19 +415,21 @@ void DecodeMfmaQ8(DecodeParams p) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) o[h][e] = SumAcross<VLPT>(o[h][e]);
   }
-  float lrow[4], crow[4];
+  float lrow[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    lrow[i] = SumGroup16(lsum[i]);
-    crow[i] = 128.0f * SumGroup16(cofs[i]);
-  }
-  // The unsigned bytes carried +128: take 128 * sum(p * v_scale) out of every
-  // element of each head.
+  for (int i = 0; i < 4; ++i) lrow[i] = SumGroup16(lsum[i]);
+  if constexpr (!F8) {
+    // The unsigned bytes carried +128: take 128 * sum(p * v_scale) out of
+    // every element of each head.
+    float crow[4];
 #pragma unroll
-  for (int h = 0; h < GV; ++h) {
-    const float c = ReadLaneF(crow[h & 3], 16 * (h >> 2));
+    for (int i = 0; i < 4; ++i) crow[i] = 128.0f * SumGroup16(cofs[i]);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) o[h][e] -= c;
+    for (int h = 0; h < GV; ++h) {
+      const float c = ReadLaneF(crow[h & 3], 16 * (h >> 2));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[h][e] -= c;
+    }
   }
 
   // Each of the item's rows: its g heads are virtual heads rr * g .. + g.
@@ -405,7 +474,7 @@ void DecodeMfmaQ8(DecodeParams p) {
   }
 }
 
-template <int D, int G>
+template <int D, int G, bool F8>
 void LaunchQ8Shape(const DecodeParams& p, hipStream_t stream) {
   // 32-token tiles: 64-token tiles measured slower on C4 and C5.
   // Joint plans: 2g or 4g virtual heads (one wavefront per SIMD where they
@@ -413,22 +482,23 @@ void LaunchQ8Shape(const DecodeParams& p, hipStream_t stream) {
   if (p.n_joint > 0 && p.joint_rows > 2) {
     if constexpr (4 * G <= 16) {
       constexpr int OCC = (D == 128 && 4 * G >= 16) ? 1 : 2;
-      hipLaunchKernelGGL((DecodeMfmaQ8<D, G, 2, OCC, 4>), dim3(p.n_items), dim3(64), 0, stream,
-                         p);
+      hipLaunchKernelGGL((DecodeMfmaQ8<D, G, 2, OCC, 4, F8>), dim3(p.n_items), dim3(64), 0,
+                         stream, p);
     }
     return;
   }
   if (p.n_joint > 0) {
     constexpr int OCC = (D == 128 && 2 * G >= 16) ? 1 : 2;
-    hipLaunchKernelGGL((DecodeMfmaQ8<D, G, 2, OCC, 2>), dim3(p.n_items), dim3(64), 0, stream, p);
+    hipLaunchKernelGGL((DecodeMfmaQ8<D, G, 2, OCC, 2, F8>), dim3(p.n_items), dim3(64), 0, stream,
+                       p);
     return;
   }
-  hipLaunchKernelGGL((DecodeMfmaQ8<D, G, 2, 2, 1>), dim3(p.n_items), dim3(64), 0, stream, p);
+  hipLaunchKernelGGL((DecodeMfmaQ8<D, G, 2, 2, 1, F8>), dim3(p.n_items), dim3(64), 0, stream, p);
 }
 
 }  // namespace
 
-bool LaunchDecodeQ8(const DecodeParams& p, hipStream_t stream, hipError_t* err) {
+bool LaunchDecodeQ8(const DecodeParams& p, bool fp8, hipStream_t stream, hipError_t* err) {
   const bool aligned = (reinterpret_cast<uintptr_t>(p.k_slab) % 16 == 0) &&
                        (reinterpret_cast<uintptr_t>(p.v_slab) % 16 == 0) &&
                        (reinterpret_cast<uintptr_t>(p.q) % 16 == 0) &&
@@ -438,11 +508,14 @@ bool LaunchDecodeQ8(const DecodeParams& p, hipStream_t stream, hipError_t* err) 
                        (p.block_stride % 16 == 0);
   if (!aligned || p.bs < 16) return false;
   if (p.n_joint > 0 && p.joint_rows * p.group > 16) return false;  // the plan caps groups
-#define EHIP_Q8_CASE(DD, GG)           \
-  if (p.d == DD && p.group == GG) {    \
-    LaunchQ8Shape<DD, GG>(p, stream);  \
-    *err = hipGetLastError();          \
-    return true;                       \
+#define EHIP_Q8_CASE(DD, GG)                                                      \
+  if (p.d == DD && p.group == GG) {                                               \
+    if (fp8)                                                                      \
+      LaunchQ8Shape<DD, GG, true>(p, stream);                                     \
+    else                                                                          \
+      LaunchQ8Shape<DD, GG, false>(p, stream);                                    \
+    *err = hipGetLastError();                                                     \
+    return true;                                                                  \
   }
   EHIP_Q8_CASE(128, 1)
   EHIP_Q8_CASE(128, 2)

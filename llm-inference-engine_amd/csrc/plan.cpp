@@ -55,16 +55,16 @@ int ValidateGeometry(const ehip_geometry& g, std::string* err) {
     return Fail(err, EHIP_INVALID_ARGUMENT,
                 "block_size=%lld must be one of 8, 16, 32, 64 (a power of two dividing 64)",
                 g.block_size);
-  if (g.kv_dtype != EHIP_KV_F32 && g.kv_dtype != EHIP_KV_BF16 && g.kv_dtype != EHIP_KV_INT8)
-    return Fail(err, EHIP_INVALID_ARGUMENT, "kv_dtype=%lld is not F32 (0), BF16 (1) or INT8 (2)",
-                g.kv_dtype);
-  if (g.kv_dtype == EHIP_KV_INT8) {
-    // The INT8 kernels (MFMA QK^T over 16-token halves) cover these shapes.
+  if (g.kv_dtype != EHIP_KV_F32 && g.kv_dtype != EHIP_KV_BF16 && !ScaledKv(g.kv_dtype))
+    return Fail(err, EHIP_INVALID_ARGUMENT,
+                "kv_dtype=%lld is not F32 (0), BF16 (1), INT8 (2) or FP8 (3)", g.kv_dtype);
+  if (ScaledKv(g.kv_dtype)) {
+    // The scaled-KV kernels (MFMA QK^T over 16-token halves) cover these shapes.
     const int64_t grp = g.heads / g.kv_heads;
     if ((g.head_dim != 64 && g.head_dim != 128) ||
         (grp != 1 && grp != 2 && grp != 4 && grp != 8) || g.block_size < 16)
       return Fail(err, EHIP_UNIMPLEMENTED,
-                  "INT8 KV needs head_dim 64 or 128, g in {1,2,4,8} and block_size >= 16 "
+                  "INT8/FP8 KV needs head_dim 64 or 128, g in {1,2,4,8} and block_size >= 16 "
                   "(got d=%lld, g=%lld, bs=%lld)",
                   g.head_dim, grp, g.block_size);
   }
@@ -82,9 +82,9 @@ int ValidateGeometry(const ehip_geometry& g, std::string* err) {
 
 int32_t MaxSplitTokens(const ehip_geometry& g) {
   // A work item's table slice sits in the wavefront's lanes: one block id per
-  // lane (64 blocks), two per lane for the INT8 kernel (128 blocks), whose
+  // lane (64 blocks), two per lane for the INT8/FP8 kernel (128 blocks), whose
   // items carry half the bytes per key and so want longer ranges.
-  return (g.kv_dtype == EHIP_KV_INT8 ? 128 : 64) * g.block_size;
+  return (ScaledKv(g.kv_dtype) ? 128 : 64) * g.block_size;
 }
 
 int32_t ChooseSplitTokens(const ehip_geometry& g, int64_t unit_tokens) {
@@ -93,7 +93,7 @@ int32_t ChooseSplitTokens(const ehip_geometry& g, int64_t unit_tokens) {
     const long v = std::strtol(env, nullptr, 10);
     if (v > 0) return static_cast<int32_t>(std::min<int64_t>(RoundUp(v, kTile), max_split));
   }
-  int64_t target = g.kv_dtype == EHIP_KV_INT8 ? kTargetItems / 2 : kTargetItems;
+  int64_t target = ScaledKv(g.kv_dtype) ? kTargetItems / 2 : kTargetItems;
   if (const char* env = std::getenv("EHIP_TARGET_ITEMS")) {
     const long v = std::strtol(env, nullptr, 10);
     if (v > 0) target = v;
@@ -329,7 +329,7 @@ void FinishPlan(const ehip_geometry& g, Plan* plan, bool allow_joint,
 
 namespace {
 
-// INT8 append groups: the step's rows grouped by destination block, each
+// INT8/FP8 append groups: the step's rows grouped by destination block, each
 // group's rows in offset order with consecutive offsets (tokens append in
 // order; a block takes rows of one sequence only).
 int BuildQ8Groups(const ehip_geometry& g, Plan* plan, std::string* err) {
@@ -345,7 +345,7 @@ int BuildQ8Groups(const ehip_geometry& g, Plan* plan, std::string* err) {
     while (j < n && plan->slots[order[j]] / g.block_size == block) {
       if (plan->slots[order[j]] % g.block_size != off0 + (j - i))
         return Fail(err, EHIP_INVALID_ARGUMENT,
-                    "INT8 append: rows landing in block %lld do not take consecutive slots "
+                    "scaled-KV append: rows landing in block %lld do not take consecutive slots "
                     "(slot %lld)",
                     block, plan->slots[order[j]]);
       ++j;
@@ -436,7 +436,7 @@ int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::
                     slot, cap);
     }
     plan->slots.assign(s.h_slot_mapping, s.h_slot_mapping + total_rows);
-    if (g.kv_dtype == EHIP_KV_INT8)
+    if (ScaledKv(g.kv_dtype))
       if (int rc = BuildQ8Groups(g, plan, err)) return rc;
   }
   if (g.kv_heads >= (1 << kHkBits))

@@ -104,7 +104,7 @@ constexpr int32_t UnpackHk(int32_t v) { return v & ((1 << kHkBits) - 1); }
 constexpr int32_t UnpackSplit(int32_t v) { return (v >> kHkBits) & ((1 << kSplitBits) - 1); }
 constexpr bool IsLastRange(int32_t v) { return (v & kLastRangeFlag) != 0; }
 
-// Rows of one step landing in one block (INT8 append): the block, the first
+// Rows of one step landing in one block (INT8/FP8 append): the block, the first
 // new row's offset in it, the row count and where its row indices start in
 // Plan::q8_rows.
 struct Q8Group {
@@ -124,7 +124,7 @@ struct Plan {
   std::vector<int32_t> table_ids;   // CSR ids, copied
   std::vector<int64_t> slots;       // slot mapping of appended tokens (may be empty)
   std::vector<int32_t> merge_rows;  // rows with more than one split, ascending
-  std::vector<Q8Group> q8_groups;   // INT8 append groups (kv_dtype INT8 with slots)
+  std::vector<Q8Group> q8_groups;   // scaled-KV append groups (INT8/FP8 with slots)
   std::vector<int32_t> q8_rows;     // row indices of the groups, in offset order
   int64_t partials = 0;             // sum over rows of nsplit * Hkv
   int64_t max_length = 0;           // longest visible length (largest position + 1)
@@ -144,6 +144,9 @@ int ValidateGeometry(const ehip_geometry& g, std::string* err);
 
 // Effective block stride in elements (geometry value or Hkv*bs*d).
 int64_t BlockStride(const ehip_geometry& g);
+
+// KV element types whose slabs carry per-(block, kv head) scales.
+inline bool ScaledKv(int kv_dtype) { return kv_dtype == EHIP_KV_INT8 || kv_dtype == EHIP_KV_FP8; }
 
 // Base split length: sized so that the step yields enough work items to fill
 // the chip (a few per SIMD) without drowning in partial-merge traffic.

@@ -29,6 +29,7 @@ INTERNAL = 11
 KV_F32 = 0
 KV_BF16 = 1
 KV_INT8 = 2
+KV_FP8 = 3
 
 _i32 = C.c_int32
 _i64 = C.c_int64
@@ -105,6 +106,8 @@ def lib():
             "ehip_step_rope_kv_append": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp],
             "ehip_step_kv_append_int8": [_vp, _vp, _vp, _vp, _vp, _vp, _vp],
             "ehip_step_attention_int8": [_vp, _vp, _vp, _vp, _vp, _vp, _vp],
+            "ehip_step_kv_append_fp8": [_vp, _vp, _vp, _vp, _vp, _vp, _vp],
+            "ehip_step_attention_fp8": [_vp, _vp, _vp, _vp, _vp, _vp, _vp],
             "ehip_step_attention": [_vp, _vp, _vp, _vp, _vp],
             "ehip_step_append_attention": [_vp, _vp, _vp, _vp, _vp, _vp, _vp],
             "ehip_step_info": [_vp, _I64P, _I64P, _I64P],
@@ -331,6 +334,14 @@ class Context:
     def step_attention_int8(self, q, k_slab, v_slab, k_scale, v_scale, out) -> int:
         return lib().ehip_step_attention_int8(self.h, q.ptr, k_slab.ptr, v_slab.ptr,
                                               k_scale.ptr, v_scale.ptr, out.ptr)
+
+    def step_kv_append_fp8(self, src_k, src_v, k_slab, v_slab, k_scale, v_scale) -> int:
+        return lib().ehip_step_kv_append_fp8(self.h, src_k.ptr, src_v.ptr, k_slab.ptr,
+                                             v_slab.ptr, k_scale.ptr, v_scale.ptr)
+
+    def step_attention_fp8(self, q, k_slab, v_slab, k_scale, v_scale, out) -> int:
+        return lib().ehip_step_attention_fp8(self.h, q.ptr, k_slab.ptr, v_slab.ptr,
+                                             k_scale.ptr, v_scale.ptr, out.ptr)
 
     def step_append_attention(self, src_k, src_v, q, k_slab, v_slab, out) -> int:
         return lib().ehip_step_append_attention(self.h, src_k.ptr, src_v.ptr, q.ptr, k_slab.ptr,

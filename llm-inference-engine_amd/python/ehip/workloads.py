@@ -35,7 +35,7 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-from . import KV_BF16, KV_F32, KV_INT8, lib
+from . import KV_BF16, KV_F32, KV_FP8, KV_INT8, lib
 
 POOL_SLACK = 1.25
 VALUE_Q, VALUE_K, VALUE_V, VALUE_NEW_K, VALUE_NEW_V = 4, 5, 6, 7, 8
@@ -156,7 +156,7 @@ class Workload:
 
     @property
     def kv_bytes(self) -> int:
-        return {KV_BF16: 2, KV_INT8: 1}.get(self.kv_dtype, 4)
+        return {KV_BF16: 2, KV_INT8: 1, KV_FP8: 1}.get(self.kv_dtype, 4)
 
     def decode_rows(self) -> np.ndarray:
         return np.flatnonzero(self.query_lens == 1)
@@ -176,7 +176,7 @@ class Workload:
         q_o = 4 * R * H * d * 2
         bt = 4 * int(np.sum((L + bs - 1) // bs)) + 4 * (B + 1) + 4 * B
         append = R * self.kv_heads * d * 2 * (4 + s) if with_append else 0
-        if self.kv_dtype == KV_INT8:
+        if self.kv_dtype in (KV_INT8, KV_FP8):
             # the K and V scales of every unique (block, kv head) tile
             unique_kv += 8 * self.kv_heads * (int(np.sum((L + bs - 1) // bs)) - shared_extra)
         return {"unique_kv": unique_kv, "logical_kv": logical_kv, "q_o": q_o, "tables": bt,

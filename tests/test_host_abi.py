@@ -89,8 +89,8 @@ def test_plan_empty_step(ehip_mod):
 
 
 @pytest.mark.parametrize("kw", [dict(block_size=12), dict(block_size=128), dict(heads=30),
-                                dict(kv_dtype=3), dict(head_dim=0), dict(slab_blocks=0),
-                                dict(head_dim=512)])
+                                dict(kv_dtype=4), dict(kv_dtype=-1), dict(head_dim=0),
+                                dict(slab_blocks=0), dict(head_dim=512)])
 def test_plan_rejects_bad_geometry(ehip_mod, kw):
     rc = ehip_mod.plan_counts(geom(ehip_mod, **kw), simple_step(ehip_mod, [40]))[0]
     assert rc in (ehip_mod.INVALID_ARGUMENT, ehip_mod.UNIMPLEMENTED)
@@ -366,25 +366,27 @@ def test_plan_joint_group_member_rule(ehip_mod):
     assert rc == 0 and shared == 2 * 25 * 16
 
 
-def test_plan_int8_shapes_and_append_groups(ehip_mod):
-    """INT8 KV: shapes outside the kernels' coverage are Unimplemented (9);
-    rows landing in one block must take consecutive slots (2 otherwise);
-    rows sharing leading blocks get joint items, as for bf16."""
+@pytest.mark.parametrize("fmt", ["int8", "fp8"])
+def test_plan_int8_shapes_and_append_groups(ehip_mod, fmt):
+    """INT8 and FP8 KV: shapes outside the kernels' coverage are
+    Unimplemented (9); rows landing in one block must take consecutive slots
+    (2 otherwise); rows sharing leading blocks get joint items, as for bf16."""
     E = ehip_mod
+    kv = E.KV_FP8 if fmt == "fp8" else E.KV_INT8
     tabs = [np.arange(4, dtype=np.int32), np.arange(4, 8, dtype=np.int32)]
     st = E.StepArrays(np.array([3, 1], np.int32), np.array([40, 20], np.int64), tabs,
                       np.array([37, 38, 39, 4 * 16 + 19], np.int64))
-    ok = E.geometry(32, 8, 128, 16, E.KV_INT8, 16, 0.088)
+    ok = E.geometry(32, 8, 128, 16, kv, 16, 0.088)
     assert E.plan_counts(ok, st, joint=True)[0] == 0
-    for bad in (E.geometry(14, 2, 64, 16, E.KV_INT8, 8, 0.125),   # g = 7
-                E.geometry(32, 8, 96, 16, E.KV_INT8, 8, 0.1),     # d = 96
-                E.geometry(32, 8, 128, 8, E.KV_INT8, 16, 0.088)):  # bs = 8
+    for bad in (E.geometry(14, 2, 64, 16, kv, 8, 0.125),   # g = 7
+                E.geometry(32, 8, 96, 16, kv, 8, 0.1),     # d = 96
+                E.geometry(32, 8, 128, 8, kv, 16, 0.088)):  # bs = 8
         assert E.plan_counts(bad, st)[0] == 9
     gap = E.StepArrays(np.array([3, 1], np.int32), np.array([40, 20], np.int64), tabs,
                        np.array([36, 38, 39, 4 * 16 + 19], np.int64))
     assert E.plan_counts(ok, gap)[0] == 2
     # two sequences forked from one prefix share 8 leading blocks (128 keys):
-    # one joint range per kv head, for INT8 as for bf16
+    # one joint range per kv head, for INT8/FP8 as for bf16
     shared = [np.arange(10, dtype=np.int32), np.array(list(range(8)) + [10, 11], np.int32)]
     st2 = E.StepArrays(np.array([1, 1], np.int32), np.array([150, 150], np.int64), shared,
                        np.array([9 * 16 + 5, 11 * 16 + 5], np.int64))
