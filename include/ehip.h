@@ -315,10 +315,11 @@ int ehip_step_attention_int8(ehip_ctx* ctx, const float* d_q, const void* d_k_sl
 /* FP8 KV (geometry kv_dtype EHIP_KV_FP8): the same per-(block, kv head)
  * scaled format and entry points as INT8, with E4M3 codes in place of int8:
  * scale = max|x| / 448 when a block's range grows, code = E4M3(x / scale) with
- * round to nearest even (NaN stays NaN, 0x7F). The reference reserves only
- * the INT8 element type in that seam (docs/design/paged-kv-cache.md:219-231);
- * FP8 is a second element type behind the same scale parameters. Covered
- * shapes as for INT8. */
+ * round to nearest even (NaN stays NaN, 0x7F). The reference reserves the
+ * element type for its FP8 KV cache (tensor::DataType::kFP8E4M3,
+ * src/tensor/dtype.h:39; docs/design/tensor.md:159) and the scaled-slab seam
+ * (docs/design/paged-kv-cache.md:219-231) without implementing either.
+ * Covered shapes as for INT8. */
 int ehip_step_kv_append_fp8(ehip_ctx* ctx, const float* d_src_k, const float* d_src_v,
                             void* d_k_slab, void* d_v_slab, float* d_k_scale, float* d_v_scale);
 int ehip_step_attention_fp8(ehip_ctx* ctx, const float* d_q, const void* d_k_slab,
