@@ -871,12 +871,12 @@ int ehip_step_append_attention(ehip_ctx* ctx, const float* d_src_k, const float*
   if (ehip::BlockStride(g) != int64_t{g.kv_heads} * g.block_size * g.head_dim)
     return SetError(ctx, EHIP_UNIMPLEMENTED, "append needs the dense Hkv*bs*d block stride");
   // One launch (plus the split merge) when every row is a decode row on the
-  // bf16 matrix-core kernel: the items ending at their rows' last keys append.
+  // matrix-core kernel: the items ending at their rows' last keys append.
   const char* env = std::getenv("EHIP_FUSED_APPEND");
   const bool allowed = !(env && env[0] == '0');
-  if (allowed && plan.all_decode && g.kv_dtype == EHIP_KV_BF16 && !plan.items.empty() &&
+  if (allowed && plan.all_decode && !plan.items.empty() &&
       reinterpret_cast<uintptr_t>(d_src_k) % 8 == 0 && reinterpret_cast<uintptr_t>(d_src_v) % 8 == 0 &&
-      ehip::DecodeMfmaCovers(StepDecodeParams(ctx, d_q, d_k_slab, d_v_slab, d_out)))
+      ehip::DecodeMfmaCovers(StepDecodeParams(ctx, d_q, d_k_slab, d_v_slab, d_out), g.kv_dtype))
     return LaunchAttention(ctx, d_q, d_k_slab, d_v_slab, d_out, nullptr, nullptr, d_src_k,
                            d_src_v);
   EHIP_HIP(ctx, ehip::LaunchKvScatter(d_src_k, d_src_v, ctx->d_slots,

@@ -116,14 +116,15 @@ int PrefillRowsPerItem(int kv_dtype, int d, int group, int bs, int64_t slab_byte
 // between the two publishes the partials: no device-wide fences or counters.
 hipError_t LaunchDecode(const DecodeParams& p, int kv_dtype, QueueState* queue, hipStream_t stream);
 
-// Whether the bf16 MFMA decode kernel covers p (d 64/128, g 1/2/4/8, bs >= 16,
-// 16-byte aligned operands, not forced to the VALU kernel by
-// EHIP_DECODE_KERNEL=valu). Only it performs the fused append.
-bool DecodeMfmaCovers(const DecodeParams& p);
-// bf16-KV decode with QK^T on MFMA; returns false (nothing launched) when the
-// shape is not covered (d not 64/128, g not 1/2/4/8, bs < 16, misaligned).
-bool LaunchDecodeMfma(const DecodeParams& p, QueueState* queue, hipStream_t stream,
-                      hipError_t* err);
+// Whether the matrix-core decode kernel covers p for this KV type (bf16: d
+// 64/128, g 1/2/4/8; fp32: d 64, g 1/2/4/7/8; bs >= 16, 16-byte aligned
+// operands, not forced to the VALU kernel by EHIP_DECODE_KERNEL=valu). Only
+// it performs the fused append.
+bool DecodeMfmaCovers(const DecodeParams& p, int kv_dtype);
+// bf16- or fp32-KV decode with QK^T on MFMA; returns false (nothing launched)
+// when DecodeMfmaCovers does not hold.
+bool LaunchDecodeMfma(const DecodeParams& p, int kv_dtype, QueueState* queue,
+                      hipStream_t stream, hipError_t* err);
 // INT8 or FP8 (E4M3) KV decode (paged_decode_q8.hip); false when the shape
 // is not covered.
 bool LaunchDecodeQ8(const DecodeParams& p, bool fp8, hipStream_t stream, hipError_t* err);

@@ -613,12 +613,13 @@ hipError_t LaunchSplits(const DecodeParams& p, int kv_dtype, QueueState* queue,
     if (LaunchDecodeQ8(p, kv_dtype == EHIP_KV_FP8, stream, &err)) return err;
     return hipErrorInvalidValue;
   }
-  if (kv_dtype != EHIP_KV_BF16) return LaunchTyped<float>(p, stream);
-  // EHIP_DECODE_KERNEL=valu selects the all-VALU kernel for bf16 as well.
+  // The matrix-core kernel where it covers the shape (EHIP_DECODE_KERNEL=valu
+  // selects the all-VALU kernels).
   hipError_t err = hipSuccess;
-  if (LaunchDecodeMfma(p, queue, stream, &err)) return err;
+  if (LaunchDecodeMfma(p, kv_dtype, queue, stream, &err)) return err;
   // Only the MFMA kernel performs a fused append; the caller checked coverage.
   if (p.new_k != nullptr) return hipErrorInvalidValue;
+  if (kv_dtype != EHIP_KV_BF16) return LaunchTyped<float>(p, stream);
   return LaunchTyped<uint16_t>(p, stream);
 }
 
@@ -627,8 +628,9 @@ hipError_t LaunchSplits(const DecodeParams& p, int kv_dtype, QueueState* queue,
 hipError_t LaunchDecode(const DecodeParams& p, int kv_dtype, QueueState* queue,
                         hipStream_t stream) {
   // Small fp32 steps without prefill chunks: one workgroup per (row, kv head),
-  // merged in LDS (the plan's split partials are not used).
-  if (kv_dtype == EHIP_KV_F32 && p.n_items > 0 && !p.has_prefill) {
+  // merged in LDS (the plan's split partials are not used). Not for a fused
+  // append, which only the matrix-core kernel performs.
+  if (kv_dtype == EHIP_KV_F32 && p.n_items > 0 && !p.has_prefill && p.new_k == nullptr) {
     hipError_t e = hipSuccess;
     if (LaunchSmallStep(p, stream, &e)) return e;
   }

@@ -32,6 +32,7 @@
 // while the current one is computed.
 #include <cstdlib>
 #include <cstring>
+#include <type_traits>
 
 #include "decode_common.h"
 #include "device_util.h"
@@ -59,27 +60,47 @@ __device__ __forceinline__ float Max16(float x) {
   return x;
 }
 
-// TH 16-token halves of K and V (one MFMA N-tile each) for one tile.
-template <int D, int TH>
+// TH 16-token halves of K and V (one MFMA N-tile each) for one tile. KV is
+// the slab element: uint16_t (bf16) or float. A lane's K operand of a chunk
+// is 8 elements (KW 16-byte vectors); its V pair is 4 or 8 bytes.
+template <class KV, int D, int TH>
 struct Tile {
   static constexpr int NC = D / 32;
+  static constexpr int KW = sizeof(KV) / 2;  // 16-byte K vectors per lane per chunk
   static constexpr int VLPT = D / 2;    // PV lanes per token row (2 elements each)
   static constexpr int VT = 64 / VLPT;  // token rows per V load instruction
   static constexpr int VJ = 16 / VT;    // V loads per 16-token half
-  uint4 k[TH][NC];
-  uint32_t v[TH][VJ];
+  using VW = std::conditional_t<sizeof(KV) == 4, uint2, uint32_t>;
+  uint4 k[TH][NC][KW];
+  VW v[TH][VJ];
   int phys[TH];
 };
 
+// Two V elements of a lane as floats.
+__device__ __forceinline__ void VPair(uint32_t r, float& v0, float& v1) {
+  v0 = Bf16Lo(r);
+  v1 = Bf16Hi(r);
+}
+__device__ __forceinline__ void VPair(uint2 r, float& v0, float& v1) {
+  v0 = __uint_as_float(r.x);
+  v1 = __uint_as_float(r.y);
+}
+
+// KV: uint16_t (bf16 slabs; K is the MFMA B operand as stored) or float (fp32
+// slabs, d = 64: Q and each K row are split into three bf16 parts and the six
+// leading products are accumulated, so the scores keep fp32 accuracy; V stays
+// fp32 on the VALU).
 // QL: keep the Q operands in LDS (read per MFMA) instead of 8·NC registers,
 // so the wide shapes fit two wavefronts per SIMD.
 // OCC: wavefronts per SIMD the register allocation must allow.
 // FUSE: the launch carries the step's new K/V rows (fused append); the
 // instance without it has no append code at all.
-template <int D, int G, int RMAX, int TH, int NBUF, bool QL, int OCC, bool FUSE>
+template <class KV, int D, int G, int RMAX, int TH, int NBUF, bool QL, int OCC, bool FUSE>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(OCC)))
-void DecodeMfmaBf16(DecodeParams p) {
-  using T = Tile<D, TH>;
+void DecodeMfma(DecodeParams p) {
+  using T = Tile<KV, D, TH>;
+  constexpr bool F32 = sizeof(KV) == 4;
+  constexpr int KW = T::KW;
   constexpr int TT = 16 * TH;        // tokens per tile
   constexpr int GV = G * RMAX;       // virtual heads (row-major over the item's rows)
   constexpr int NC = T::NC;          // MFMA k-chunks over head_dim
@@ -91,10 +112,12 @@ void DecodeMfmaBf16(DecodeParams p) {
   static_assert(GV >= 1 && GV <= 16 && (D == 64 || D == 128), "shape");
 
   __shared__ float p_lds[TT * HP];
-  __shared__ uint4 q_lds[QL ? 2 * NC * 64 : 1];
-  // Fused append: the row's new K and V as bf16 pairs (element 2i, 2i + 1).
-  __shared__ uint4 knew_lds[FUSE ? D / 8 : 1];
-  __shared__ uint32_t vnew_lds[FUSE ? D / 2 : 1];
+  constexpr int NQ = F32 ? 3 : 2;  // bf16 parts of Q
+  __shared__ uint4 q_lds[QL ? NQ * NC * 64 : 1];
+  // Fused append: the row's new K row as stored (bf16 or fp32) and its V
+  // pairs (element 2i, 2i + 1 per entry).
+  __shared__ uint4 knew_lds[FUSE ? D * static_cast<int>(sizeof(KV)) / 16 : 1];
+  __shared__ typename T::VW vnew_lds[FUSE ? D / 2 : 1];
 
   const int lane = threadIdx.x;
   // Persistent wavefronts: a workgroup's first item is its index; each later
@@ -158,12 +181,13 @@ void DecodeMfmaBf16(DecodeParams p) {
   }
   const int lb0 = tb / bs;
   const int tab = LoadRangeTable(p, it.table_off, tb, te, lane);
-  const uint16_t* kbase = static_cast<const uint16_t*>(p.k_slab) + int64_t{hk} * bs * D;
-  const uint16_t* vbase = static_cast<const uint16_t*>(p.v_slab) + int64_t{hk} * bs * D;
+  const KV* kbase = static_cast<const KV*>(p.k_slab) + int64_t{hk} * p.head_stride;
+  const KV* vbase = static_cast<const KV*>(p.v_slab) + int64_t{hk} * p.head_stride;
   const int bmask = bs - 1;
+  constexpr int ES = static_cast<int>(sizeof(KV));
   // Per-lane byte offsets inside a (block, head) tile: loop-invariant.
-  const int koff = (n * D + kq * 8) * 2;
-  const int voff = (tv * D + ev) * 2;
+  const int koff = (n * D + kq * 8) * ES;
+  const int voff = (tv * D + ev) * ES;
   // Fused append: the item ending at its row's last key (position te - 1)
   // streams keys [tb, te - 1) from the slab and takes the new key from the
   // step's new rows in one more step after the loop.
@@ -187,18 +211,26 @@ void DecodeMfmaBf16(DecodeParams p) {
       const bool ok = th < kend && phys >= 0;
       t.phys[h2] = ok ? phys : -1;
       const int64_t boff = int64_t{ok ? phys : 0} * p.block_stride + (th & bmask) * D;
-      const uint32_t range = ok ? static_cast<uint32_t>(min(16, kend - th) * D * 2) : 0u;
+      const uint32_t range = ok ? static_cast<uint32_t>(min(16, kend - th) * D * ES) : 0u;
       const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<uint16_t*>(kbase + boff), 0, range, 0x00020000);
+          const_cast<KV*>(kbase + boff), 0, range, 0x00020000);
       const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<uint16_t*>(vbase + boff), 0, range, 0x00020000);
+          const_cast<KV*>(vbase + boff), 0, range, 0x00020000);
 #pragma unroll
       for (int c = 0; c < NC; ++c)
-        t.k[h2][c] = __builtin_bit_cast(
-            uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, koff + c * 64, 0, kKvLoadAux));
 #pragma unroll
-      for (int j = 0; j < VJ; ++j)
-        t.v[h2][j] = __builtin_amdgcn_raw_buffer_load_b32(rv, voff + j * VT * D * 2, 0, kKvLoadAux);
+        for (int w = 0; w < KW; ++w)
+          t.k[h2][c][w] = __builtin_bit_cast(
+              uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, koff + c * 32 * ES + w * 16, 0,
+                                                           kKvLoadAux));
+#pragma unroll
+      for (int j = 0; j < VJ; ++j) {
+        if constexpr (F32)
+          t.v[h2][j] = __builtin_bit_cast(
+              uint2, __builtin_amdgcn_raw_buffer_load_b64(rv, voff + j * VT * D * ES, 0, kKvLoadAux));
+        else
+          t.v[h2][j] = __builtin_amdgcn_raw_buffer_load_b32(rv, voff + j * VT * D * ES, 0, kKvLoadAux);
+      }
     }
   };
 
@@ -211,30 +243,37 @@ void DecodeMfmaBf16(DecodeParams p) {
     load(bufA, tb, false);
   if constexpr (NBUF == 3) load(bufB, tb + TT, false);
 
-  // Fused append: the item ending at its row's last key narrows that key's
-  // new K/V rows (the reference's round-to-nearest-even), stores them at the
-  // row's slot for later steps, and keeps them in LDS for its last step (no
-  // other item reads that row, and this item never loads it from the slab).
+  // Fused append: the item ending at its row's last key stores that key's
+  // new K/V rows at the row's slot for later steps (bf16 slabs: narrowed with
+  // the reference's round-to-nearest-even; fp32: as given), and keeps them in
+  // LDS for its last step (no other item reads that row, and this item never
+  // loads it from the slab).
   if (fuse) {
     const int row = it.rows[0];
     const int pair = lane % (D / 2);
     const int64_t src = (int64_t{row} * p.kv_heads + hk) * D + 2 * pair;
     const float2 kx = *reinterpret_cast<const float2*>(p.new_k + src);
     const float2 vx = *reinterpret_cast<const float2*>(p.new_v + src);
-    const uint32_t kp = Fp32ToBf16Bits(kx.x) | (Fp32ToBf16Bits(kx.y) << 16);
-    const uint32_t vp = Fp32ToBf16Bits(vx.x) | (Fp32ToBf16Bits(vx.y) << 16);
-    reinterpret_cast<uint32_t*>(knew_lds)[pair] = kp;
+    typename T::VW kp, vp;
+    if constexpr (F32) {
+      kp = make_uint2(__float_as_uint(kx.x), __float_as_uint(kx.y));
+      vp = make_uint2(__float_as_uint(vx.x), __float_as_uint(vx.y));
+    } else {
+      kp = Fp32ToBf16Bits(kx.x) | (Fp32ToBf16Bits(kx.y) << 16);
+      vp = Fp32ToBf16Bits(vx.x) | (Fp32ToBf16Bits(vx.y) << 16);
+    }
+    reinterpret_cast<typename T::VW*>(knew_lds)[pair] = kp;
     vnew_lds[pair] = vp;
     const int64_t slot = p.slots[row];
     if (slot >= 0 && slot < p.slab_blocks * bs) {
       const int64_t blk = slot / bs;
-      const int64_t dst = blk * p.block_stride + int64_t{hk} * bs * D + (slot - blk * bs) * D +
-                          2 * pair;
+      const int64_t dst = blk * p.block_stride + int64_t{hk} * p.head_stride +
+                          (slot - blk * bs) * D + 2 * pair;
       if (lane < D / 2) {
-        uint16_t* kslab = static_cast<uint16_t*>(const_cast<void*>(p.k_slab));
-        uint16_t* vslab = static_cast<uint16_t*>(const_cast<void*>(p.v_slab));
-        *reinterpret_cast<uint32_t*>(kslab + dst) = kp;
-        *reinterpret_cast<uint32_t*>(vslab + dst) = vp;
+        KV* kslab = static_cast<KV*>(const_cast<void*>(p.k_slab));
+        KV* vslab = static_cast<KV*>(const_cast<void*>(p.v_slab));
+        *reinterpret_cast<typename T::VW*>(kslab + dst) = kp;
+        *reinterpret_cast<typename T::VW*>(vslab + dst) = vp;
       }
     } else if (lane == 0) {
       atomicOr(p.err, kErrSlotRange);
@@ -242,23 +281,27 @@ void DecodeMfmaBf16(DecodeParams p) {
     __syncthreads();  // the LDS rows are read by the tile patch below
   }
 
-  // Q as MFMA A operands: q = hi + lo, both bf16 (round-to-nearest-even
-  // narrowing, branch-free); padding virtual heads are zero.
-  bf16x8_t qa_hi[NC], qa_lo[NC];
+  // Q as MFMA A operands in NQ bf16 parts (round-to-nearest-even narrowing of
+  // the remainder, branch-free): q = q0 + q1 (bf16 K) or q0 + q1 + q2 (fp32
+  // K); padding virtual heads are zero.
+  bf16x8_t qa[NQ][NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     const float x[8] = {qraw[c][0].x, qraw[c][0].y, qraw[c][0].z, qraw[c][0].w,
                         qraw[c][1].x, qraw[c][1].y, qraw[c][1].z, qraw[c][1].w};
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const float xv = live ? x[i] : 0.f;
-      const __bf16 hb = static_cast<__bf16>(xv);
-      qa_hi[c][i] = hb;
-      qa_lo[c][i] = static_cast<__bf16>(xv - static_cast<float>(hb));
+      float r = live ? x[i] : 0.f;
+#pragma unroll
+      for (int k = 0; k < NQ; ++k) {
+        const __bf16 b = static_cast<__bf16>(r);
+        qa[k][c][i] = b;
+        r -= static_cast<float>(b);
+      }
     }
     if constexpr (QL) {
-      q_lds[(2 * c) * 64 + lane] = __builtin_bit_cast(uint4, qa_hi[c]);
-      q_lds[(2 * c + 1) * 64 + lane] = __builtin_bit_cast(uint4, qa_lo[c]);
+#pragma unroll
+      for (int k = 0; k < NQ; ++k) q_lds[(NQ * c + k) * 64 + lane] = __builtin_bit_cast(uint4, qa[k][c]);
     }
   }
 
@@ -282,11 +325,41 @@ void DecodeMfmaBf16(DecodeParams p) {
       acc[h2] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        const bf16x8_t kb = AsBf16x8(t.k[h2][c]);
-        const bf16x8_t qh = QL ? AsBf16x8(q_lds[(2 * c) * 64 + lane]) : qa_hi[c];
-        const bf16x8_t ql = QL ? AsBf16x8(q_lds[(2 * c + 1) * 64 + lane]) : qa_lo[c];
-        acc[h2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qh, kb, acc[h2], 0, 0, 0);
-        acc[h2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ql, kb, acc[h2], 0, 0, 0);
+        bf16x8_t qp[NQ];
+#pragma unroll
+        for (int k = 0; k < NQ; ++k) qp[k] = QL ? AsBf16x8(q_lds[(NQ * c + k) * 64 + lane]) : qa[k][c];
+        if constexpr (F32) {
+          // K = k0 + k1 + k2 (bf16 parts of the fp32 row): the six products
+          // of parts whose indices sum to at most 2, smallest first. What is
+          // left out is below 2^-24 of |q||k| per element (a 2 x 2 split
+          // leaves ~2^-17, too coarse for the fp32 reference's 1e-4 / 1e-5
+          // elementwise criterion at logit scales ~4).
+          const uint4 a = t.k[h2][c][0], b = t.k[h2][c][1];
+          const float x[8] = {__uint_as_float(a.x), __uint_as_float(a.y), __uint_as_float(a.z),
+                              __uint_as_float(a.w), __uint_as_float(b.x), __uint_as_float(b.y),
+                              __uint_as_float(b.z), __uint_as_float(b.w)};
+          bf16x8_t kp[3];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            float r = x[i];
+#pragma unroll
+            for (int k = 0; k < 3; ++k) {
+              const __bf16 bb = static_cast<__bf16>(r);
+              kp[k][i] = bb;
+              r -= static_cast<float>(bb);
+            }
+          }
+          acc[h2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qp[0], kp[2], acc[h2], 0, 0, 0);
+          acc[h2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qp[1], kp[1], acc[h2], 0, 0, 0);
+          acc[h2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qp[2], kp[0], acc[h2], 0, 0, 0);
+          acc[h2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qp[0], kp[1], acc[h2], 0, 0, 0);
+          acc[h2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qp[1], kp[0], acc[h2], 0, 0, 0);
+          acc[h2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qp[0], kp[0], acc[h2], 0, 0, 0);
+        } else {
+          const bf16x8_t kb = AsBf16x8(t.k[h2][c][0]);
+          acc[h2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qp[0], kb, acc[h2], 0, 0, 0);
+          acc[h2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qp[1], kb, acc[h2], 0, 0, 0);
+        }
       }
     }
     float s[TH][4];
@@ -335,8 +408,8 @@ void DecodeMfmaBf16(DecodeParams p) {
 #pragma unroll
       for (int j = 0; j < VJ; ++j) {
         const int tt = 16 * h2 + j * VT + tv;
-        const uint32_t r = t.v[h2][j];
-        const float v0 = Bf16Lo(r), v1 = Bf16Hi(r);
+        float v0, v1;
+        VPair(t.v[h2][j], v0, v1);
         float pv[HP];
 #pragma unroll
         for (int r4 = 0; r4 < HR; ++r4) {
@@ -398,10 +471,13 @@ void DecodeMfmaBf16(DecodeParams p) {
       tn.phys[h2] = h2 == 0 ? 0 : -1;
 #pragma unroll
       for (int c = 0; c < NC; ++c)
-        tn.k[h2][c] = (h2 == 0 && n == 0) ? knew_lds[c * 4 + kq] : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+        for (int w = 0; w < KW; ++w)
+          tn.k[h2][c][w] = (h2 == 0 && n == 0) ? knew_lds[(c * 32 + kq * 8) * ES / 16 + w]
+                                               : make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
       for (int j = 0; j < VJ; ++j)
-        tn.v[h2][j] = (h2 == 0 && j * VT + tv == 0) ? vnew_lds[lane % VLPT] : 0u;
+        tn.v[h2][j] = (h2 == 0 && j * VT + tv == 0) ? vnew_lds[lane % VLPT] : typename T::VW{};
     }
     process(tn, newpos, te);
   }
@@ -501,52 +577,85 @@ void LaunchPersistent(K kernel, const DecodeParams& p, hipStream_t stream, bool 
   hipLaunchKernelGGL(kernel, dim3(grid), dim3(64), 0, stream, p);
 }
 
-template <int D, int G, int RMAX, bool FUSE>
+template <class KV, int D, int G, int RMAX, bool FUSE>
 void LaunchShape(const DecodeParams& p, hipStream_t stream, bool wide, bool deep, bool persist) {
   // Two wavefronts per SIMD wherever the shape fits 256 registers without
   // spilling (the 16-virtual-head and triple-buffered 128-wide shapes do not).
   constexpr bool QL = D * G * RMAX >= 1024;
   constexpr int OCC = (D == 128 && G * RMAX >= 16) ? 1 : 2;
   constexpr int OCC3 = D == 128 ? 1 : 2;
-  if (wide && deep)
-    LaunchPersistent(DecodeMfmaBf16<D, G, RMAX, 2, 3, QL, OCC3, FUSE>, p, stream, persist);
-  else if (wide)
-    LaunchPersistent(DecodeMfmaBf16<D, G, RMAX, 2, 2, QL, OCC, FUSE>, p, stream, persist);
-  else if (deep)
-    LaunchPersistent(DecodeMfmaBf16<D, G, RMAX, 1, 3, QL, OCC3, FUSE>, p, stream, persist);
-  else
-    LaunchPersistent(DecodeMfmaBf16<D, G, RMAX, 1, 2, QL, OCC, FUSE>, p, stream, persist);
+  if constexpr (sizeof(KV) == 4) {
+    // fp32 slabs: the default shape only (32-key tiles, two buffers).
+    LaunchPersistent(DecodeMfma<KV, D, G, RMAX, 2, 2, QL, OCC, FUSE>, p, stream, persist);
+  } else {
+    if (wide && deep)
+      LaunchPersistent(DecodeMfma<KV, D, G, RMAX, 2, 3, QL, OCC3, FUSE>, p, stream, persist);
+    else if (wide)
+      LaunchPersistent(DecodeMfma<KV, D, G, RMAX, 2, 2, QL, OCC, FUSE>, p, stream, persist);
+    else if (deep)
+      LaunchPersistent(DecodeMfma<KV, D, G, RMAX, 1, 3, QL, OCC3, FUSE>, p, stream, persist);
+    else
+      LaunchPersistent(DecodeMfma<KV, D, G, RMAX, 1, 2, QL, OCC, FUSE>, p, stream, persist);
+  }
 }
 
-template <int D, int G, int RMAX>
+template <class KV, int D, int G, int RMAX>
 void LaunchShape(const DecodeParams& p, hipStream_t stream, bool wide, bool deep, bool persist) {
   if (p.new_k != nullptr)
-    LaunchShape<D, G, RMAX, true>(p, stream, wide, deep, persist);
+    LaunchShape<KV, D, G, RMAX, true>(p, stream, wide, deep, persist);
   else
-    LaunchShape<D, G, RMAX, false>(p, stream, wide, deep, persist);
+    LaunchShape<KV, D, G, RMAX, false>(p, stream, wide, deep, persist);
+}
+
+// Rows per item the kernel is instantiated for: 1, 2, or 4 for groups of three
+// or four sharers (the plan caps a group at 16 / g rows, so 4 only for g <= 4).
+template <class KV, int D, int G>
+bool LaunchRows(const DecodeParams& p, hipStream_t stream, bool wide, bool deep, bool persist) {
+  const int rows = p.n_joint > 0 ? p.joint_rows : 1;
+  if constexpr (G <= 4) {
+    if (rows > 2) {
+      LaunchShape<KV, D, G, 4>(p, stream, wide, deep, persist);
+      return true;
+    }
+  }
+  if (rows > 2) return false;
+  if (rows == 2)
+    LaunchShape<KV, D, G, 2>(p, stream, wide, deep, persist);
+  else
+    LaunchShape<KV, D, G, 1>(p, stream, wide, deep, persist);
+  return true;
 }
 
 }  // namespace
 
-bool DecodeMfmaCovers(const DecodeParams& p) {
+bool DecodeMfmaCovers(const DecodeParams& p, int kv_dtype) {
+  const bool f32 = kv_dtype == EHIP_KV_F32;
+  if (!f32 && kv_dtype != EHIP_KV_BF16) return false;
+  // 16-byte K/V vectors: bf16 rows start on 8-element, fp32 on 4-element
+  // multiples of the slab base.
+  const int64_t vec = f32 ? 4 : 8;
   const bool aligned = (reinterpret_cast<uintptr_t>(p.k_slab) % 16 == 0) &&
                        (reinterpret_cast<uintptr_t>(p.v_slab) % 16 == 0) &&
                        (reinterpret_cast<uintptr_t>(p.q) % 16 == 0) &&
                        (reinterpret_cast<uintptr_t>(p.out) % 16 == 0) &&
-                       (p.block_stride % 8 == 0);
-  const bool shape = (p.d == 64 || p.d == 128) &&
-                     (p.group == 1 || p.group == 2 || p.group == 4 || p.group == 8);
+                       (p.block_stride % vec == 0) && (p.head_stride % vec == 0);
+  // fp32: head_dim 64 (the 128-wide fp32 tiles would not fit two wavefronts
+  // per SIMD) and g in {1, 2, 4, 7, 8}; bf16: head_dim 64 or 128, g in {1, 2, 4, 8}.
+  const bool shape = f32 ? (p.d == 64 && (p.group == 1 || p.group == 2 || p.group == 4 ||
+                                          p.group == 7 || p.group == 8))
+                         : ((p.d == 64 || p.d == 128) &&
+                            (p.group == 1 || p.group == 2 || p.group == 4 || p.group == 8));
   const char* pick = std::getenv("EHIP_DECODE_KERNEL");
   const bool valu = pick && std::strcmp(pick, "valu") == 0;
   return aligned && shape && p.bs >= 16 && !valu;
 }
 
-bool LaunchDecodeMfma(const DecodeParams& params, QueueState* queue, hipStream_t stream,
-                      hipError_t* err) {
+bool LaunchDecodeMfma(const DecodeParams& params, int kv_dtype, QueueState* queue,
+                      hipStream_t stream, hipError_t* err) {
   DecodeParams p = params;
   p.queue = queue->d_counters;
   p.queue_done = queue->d_done;
-  if (!DecodeMfmaCovers(p)) return false;
+  if (!DecodeMfmaCovers(p, kv_dtype)) return false;
   // 32-token tiles (two MFMA halves per tile, double-buffered) measured best
   // on C4; EHIP_DECODE_TILE=16 selects one half per tile (fewer registers).
   const char* tile = std::getenv("EHIP_DECODE_TILE");
@@ -554,41 +663,36 @@ bool LaunchDecodeMfma(const DecodeParams& params, QueueState* queue, hipStream_t
   // EHIP_DECODE_BUFS=3: three tiles in registers (two in flight).
   const char* bufs = std::getenv("EHIP_DECODE_BUFS");
   const bool deep = bufs && std::strcmp(bufs, "3") == 0;
-  const bool joint = p.n_joint > 0;
   // EHIP_DECODE_PERSIST=0: one workgroup per item (the hardware dispatcher
   // hands out the items instead of the queue).
   const char* pers = std::getenv("EHIP_DECODE_PERSIST");
   const bool persist = !(pers && std::strcmp(pers, "0") == 0);
-  // Rows per item: 1, 2, or 4 for groups of three or four sharers (the plan
-  // caps a group at 16 / g rows, so 4 only for g <= 4).
-  const int rows = joint ? p.joint_rows : 1;
-#define EHIP_MFMA_CASE(DD, GG)                                   \
-  if (p.d == DD && p.group == GG) {                              \
-    if constexpr (GG <= 4) {                                     \
-      if (rows > 2) {                                            \
-        LaunchShape<DD, GG, 4>(p, stream, wide, deep, persist);  \
-        *err = hipGetLastError();                                \
-        return true;                                             \
-      }                                                          \
-    }                                                            \
-    if (rows > 2) return false;                                  \
-    if (rows == 2)                                               \
-      LaunchShape<DD, GG, 2>(p, stream, wide, deep, persist);    \
-    else                                                         \
-      LaunchShape<DD, GG, 1>(p, stream, wide, deep, persist);    \
-    *err = hipGetLastError();                                    \
-    return true;                                                 \
+  bool ok = false;
+#define EHIP_MFMA_CASE(KV, DD, GG) \
+  else if (p.d == DD && p.group == GG) ok = LaunchRows<KV, DD, GG>(p, stream, wide, deep, persist);
+  if (kv_dtype == EHIP_KV_F32) {
+    if (false) {
+    }
+    EHIP_MFMA_CASE(float, 64, 1)
+    EHIP_MFMA_CASE(float, 64, 2)
+    EHIP_MFMA_CASE(float, 64, 4)
+    EHIP_MFMA_CASE(float, 64, 7)
+    EHIP_MFMA_CASE(float, 64, 8)
+  } else {
+    if (false) {
+    }
+    EHIP_MFMA_CASE(uint16_t, 128, 1)
+    EHIP_MFMA_CASE(uint16_t, 128, 2)
+    EHIP_MFMA_CASE(uint16_t, 128, 4)
+    EHIP_MFMA_CASE(uint16_t, 128, 8)
+    EHIP_MFMA_CASE(uint16_t, 64, 1)
+    EHIP_MFMA_CASE(uint16_t, 64, 2)
+    EHIP_MFMA_CASE(uint16_t, 64, 4)
+    EHIP_MFMA_CASE(uint16_t, 64, 8)
   }
-  EHIP_MFMA_CASE(128, 1)
-  EHIP_MFMA_CASE(128, 2)
-  EHIP_MFMA_CASE(128, 4)
-  EHIP_MFMA_CASE(128, 8)
-  EHIP_MFMA_CASE(64, 1)
-  EHIP_MFMA_CASE(64, 2)
-  EHIP_MFMA_CASE(64, 4)
-  EHIP_MFMA_CASE(64, 8)
 #undef EHIP_MFMA_CASE
-  return false;
+  if (ok) *err = hipGetLastError();
+  return ok;
 }
 
 }  // namespace ehip

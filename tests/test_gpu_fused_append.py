@@ -1,10 +1,11 @@
 """ehip_step_append_attention: the step's KV append and attention in one
-launch for all-decode bf16 steps (the item that ends at a row's last key
-stores the row's new K/V and uses them directly), and the two-launch order
-for every other step. Either way the slabs must equal the oracle's append bit
-for bit and the outputs meet the decode bar against the reference on the same
-bf16-rounded cache (1e-4 relative per output vector, the reference allclose);
-fused and separate launches agree to within that bar."""
+launch for all-decode steps on the matrix-core decode kernel (bf16 slabs, and
+fp32 slabs with head_dim 64; the item that ends at a row's last key stores the
+row's new K/V and uses them directly), and the two-launch order for every
+other step. Either way the slabs must equal the oracle's append bit for bit
+and the outputs meet the decode bar against the reference on the same cache
+(bf16-rounded for bf16 slabs; 1e-4 relative per output vector, the reference
+allclose); fused and separate launches agree to within that bar."""
 import numpy as np
 import pytest
 
@@ -67,13 +68,17 @@ def _check(got, ref):
     assert allclose_ref(got, ref, 1e-4, 1e-5)
 
 
-@pytest.mark.parametrize("H,Hkv,d,bs", [(32, 8, 128, 16), (64, 8, 128, 16), (14, 2, 64, 16),
-                                        (8, 8, 128, 32), (16, 2, 64, 64), (8, 1, 128, 16)])
-def test_fused_append_decode_step(gctx, ehip_mod, orc, H, Hkv, d, bs):
+@pytest.mark.parametrize("H,Hkv,d,bs,kv", [(32, 8, 128, 16, "bf16"), (64, 8, 128, 16, "bf16"),
+                                           (14, 2, 64, 16, "bf16"), (8, 8, 128, 32, "bf16"),
+                                           (16, 2, 64, 64, "bf16"), (8, 1, 128, 16, "bf16"),
+                                           (14, 2, 64, 16, "f32"), (8, 2, 64, 32, "f32"),
+                                           (8, 8, 64, 16, "f32")])
+def test_fused_append_decode_step(gctx, ehip_mod, orc, H, Hkv, d, bs, kv):
     """Ragged decode rows, including rows of one key (only the new token),
     rows whose last key range holds just the new key, and long split rows."""
     lens = [1, 2, 17, 33, 129, 1025, 1026, 2049, 4000, 64, 65, 8193]
-    w = _workload(ehip_mod, H, Hkv, d, bs, lens, seed=H + d + bs)
+    dtype = ehip_mod.KV_F32 if kv == "f32" else ehip_mod.KV_BF16
+    w = _workload(ehip_mod, H, Hkv, d, bs, lens, seed=H + d + bs, dtype=dtype)
     fused, ref = _run(gctx, ehip_mod, orc, w, fused=True)
     _check(fused, ref)
     separate, _ = _run(gctx, ehip_mod, orc, w, fused=False)
@@ -96,10 +101,11 @@ def test_fused_append_with_joint_items(gctx, ehip_mod, orc):
 
 @pytest.mark.parametrize("case", ["fp32", "chunk", "valu"])
 def test_append_attention_falls_back_to_two_launches(gctx, ehip_mod, orc, case, monkeypatch):
-    """fp32 slabs, a step with a prefill chunk, and the VALU decode kernel take
-    the append launch then the attention launch, with the same results."""
+    """fp32 slabs of head_dim 128 (the fp32 matrix-core kernel covers 64), a
+    step with a prefill chunk, and the VALU decode kernel take the append
+    launch then the attention launch, with the same results."""
     if case == "fp32":
-        w = _workload(ehip_mod, 14, 2, 64, 16, [513, 17, 1], seed=5, dtype=ehip_mod.KV_F32)
+        w = _workload(ehip_mod, 16, 2, 128, 16, [513, 17, 1], seed=5, dtype=ehip_mod.KV_F32)
     elif case == "chunk":
         w = _workload(ehip_mod, 32, 8, 128, 16, [300, 40, 1000], seed=6, qlens=[1, 20, 1])
     else:

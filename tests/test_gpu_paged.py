@@ -650,19 +650,21 @@ FORK_GROUPS = [(20, [700, 530, 900, 400, 655]),  # five sharers of 320 keys
 @pytest.mark.parametrize("H,Hkv,d,kv", [(32, 8, 128, "mfma"), (16, 8, 64, "mfma"),
                                         (8, 8, 128, "mfma"), (64, 8, 128, "mfma"),
                                         (32, 8, 128, "valu"), (14, 2, 64, "f32"),
-                                        (8, 8, 64, "f32")])
+                                        (8, 8, 64, "f32"), (14, 2, 64, "f32valu"),
+                                        (16, 2, 128, "f32")])
 def test_decode_fork_groups_beyond_pairs(gctx, ehip_mod, orc, H, Hkv, d, kv, monkeypatch):
     """Joint work items of up to min(4, 16 / g) rows over fork groups' shared
     prefixes (groups of five and three sharers, a pair, unshared rows),
-    through the bf16 MFMA kernel (its virtual heads: g per row, up to 16),
-    the bf16 VALU kernel and the fp32 VALU kernel (rows one after the other):
-    against the oracle, and against the plain per-row partition."""
-    monkeypatch.setenv("EHIP_DECODE_KERNEL", "valu" if kv == "valu" else "mfma")
+    through the MFMA kernel (its virtual heads: g per row, up to 16; bf16, and
+    fp32 at head_dim 64), the bf16 and fp32 VALU kernels (rows one after the
+    other; fp32 head_dim 128 always): against the oracle, and against the
+    plain per-row partition."""
+    monkeypatch.setenv("EHIP_DECODE_KERNEL", "valu" if kv.endswith("valu") else "mfma")
     monkeypatch.setenv("EHIP_DECODE_WG", "0")  # joint items live in the split-KV path
     rng = np.random.default_rng(H + 3 * d)
     bs = 16
     q, ks, vs, tables, lengths = fork_group_case(rng, FORK_GROUPS, Hkv, d, bs, H)
-    bf16 = kv != "f32"
+    bf16 = not kv.startswith("f32")
     if bf16:
         ks_b, vs_b = orc.to_bf16_bits(ks), orc.to_bf16_bits(vs)
         kd, vd = gctx.to_device(ks_b), gctx.to_device(vs_b)
@@ -718,3 +720,35 @@ def test_small_step_workgroup_per_row(gctx, orc, H, Hkv, d, lens, monkeypatch):
         outs.append(out.download(np.float32, q.shape))
         check_fp32(outs[-1], ref)
     assert rel_norm(outs[0], outs[1]) <= FP32_REL
+
+
+@pytest.mark.parametrize("kernel", ["mfma", "valu"])
+def test_c2_layer_fp32_kernels(gctx, ehip_mod, orc, kernel, monkeypatch):
+    """One layer of the C2 step as drawn (32 rows, 14q/2kv, d = 64, fp32 slabs,
+    split-KV) on the fp32 matrix-core kernel (Q and K in three bf16 parts,
+    six products per chunk) and on the all-VALU kernel: both meet the fp32
+    bar (1e-4 relative per output vector, the reference allclose) against the
+    oracle on the same post-append cache."""
+    from ehip import workloads
+    monkeypatch.setenv("EHIP_DECODE_KERNEL", kernel)
+    w = workloads.c2()
+    H, Hkv, d, bs = w.heads, w.kv_heads, w.head_dim, w.block_size
+    kpool, vpool = seeded_pool(orc, w, 301)
+    kn, vn, q = new_rows(orc, w, 401)
+    g = ehip_mod.geometry(H, Hkv, d, bs, w.kv_dtype, w.pool_blocks, w.scale)
+    st = ehip_mod.StepArrays(w.query_lens, w.context_lens, w.tables, w.slot_mapping)
+    assert gctx.step_upload(g, st) == 0, gctx.last_error()
+    dk, dv, dq = gctx.to_device(kpool), gctx.to_device(vpool), gctx.to_device(q)
+    dkn, dvn = gctx.to_device(kn), gctx.to_device(vn)
+    out = gctx.alloc(q.nbytes)
+    assert gctx.step_append_attention(dkn, dvn, dq, dk, dv, out) == 0, gctx.last_error()
+    gctx.sync()
+    got = out.download(np.float32, q.shape)
+    orc.kv_scatter(kn, vn, w.slot_mapping, Hkv, d, bs, kpool, vpool)
+    assert np.array_equal(dk.download(np.float32, kpool.shape).view(np.uint32),
+                          kpool.view(np.uint32))
+    ref = orc.paged_decode_batched(q, kpool, vpool, w.tables, w.context_lens, H, Hkv, d, bs,
+                                   w.scale)
+    check_fp32(got, ref)
+    for b in (dk, dv, dq, dkn, dvn, out):
+        b.free()
