@@ -639,7 +639,7 @@ def main():
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
             "kernel": "the layer's append + paged decode attention call (decode kernel with "
-                      "the append fused for all-decode bf16 steps, + split merge)",
+                      "the append fused for all-decode steps on the matrix-core kernel, + split merge)",
             "algorithmic_bytes_per_launch": attn_bytes,
             "avg_launch_us": round(attn_avg * 1e6, 3),
             "launches_timed": int(attn.size),

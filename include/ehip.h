@@ -28,16 +28,19 @@
  *     KV element type is fp32 or bf16 (bf16 = the reference's
  *     Fp32ToBf16Bits round-to-nearest-even, src/tensor/half.h:112-124).
  *   - Queries and outputs are fp32, [rows, H, d] contiguous. Softmax,
- *     running sums and accumulation are fp32 everywhere. The products differ
- *     by kernel: fp32 KV is all-fp32 on the vector ALUs; bf16-KV decode
- *     multiplies bf16 K by q split into bf16 hi + lo parts (q = hi + lo to
- *     about 2^-17 relative) on the matrix cores, and P.V in fp32; the causal
- *     prefill-chunk kernel rounds q and the probabilities P to bf16 for its
- *     matrix-core products (fp32 accumulate); INT8 KV forms exact integer
- *     q.k products of a three-digit int8 split of q; FP8 KV multiplies the
- *     E4M3 keys by a four-digit E4M3 split of q (about 2^-16 relative) on the
- *     fp8 matrix cores. The parity bars these give are stated beside each
- *     test.
+ *     running sums and accumulation are fp32 everywhere, and P.V is fp32 on
+ *     the vector ALUs in every decode kernel. The q.k products differ by
+ *     kernel: bf16-KV decode multiplies bf16 K by q split into bf16 hi + lo
+ *     parts (q = hi + lo to about 2^-17 relative) on the matrix cores;
+ *     fp32-KV decode at head_dim 64 splits q and K into three bf16 parts each
+ *     and accumulates the six leading products on the matrix cores (what is
+ *     left out is below 2^-24 of |q||k| per element), and is all-fp32 on the
+ *     vector ALUs at other head sizes; INT8 KV forms exact integer q.k
+ *     products of a three-digit int8 split of q; FP8 KV widens the E4M3 keys
+ *     to bf16 (exact) and multiplies them by q in bf16 hi + lo parts. The
+ *     causal prefill-chunk kernel rounds q and the probabilities P to bf16
+ *     for its matrix-core products (fp32 accumulate). The parity bars these
+ *     give are stated beside each test.
  *   - A context is used from one host thread at a time (the reference's
  *     single engine thread, src/runtime/engine.h:27-33).
  */
