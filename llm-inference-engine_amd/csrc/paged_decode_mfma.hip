@@ -128,7 +128,9 @@ void DecodeMfma(DecodeParams p) {
   // wavefronts finish together), early enough to hide the atomic's latency.
   // On its way out each wavefront counts itself in; the last one (which then
   // knows every ticket has been drawn) clears every counter for the next
-  // launch, so a launch leaves them as it found them: zero.
+  // launch, so a launch leaves them as it found them: zero. A launch whose
+  // grid covers every item (each wavefront's first item is its only one)
+  // touches no counter at all: no tickets, no count on the way out.
   // Descriptors come through the scalar unit: the rows' split slots and the
   // next item are requested together before the item's results are stored,
   // so neither waits behind outstanding vector memory operations (vmcnt
@@ -138,6 +140,7 @@ void DecodeMfma(DecodeParams p) {
   // below gridDim.x are first items (workgroup i starts with item i), the
   // rest go out by ticket, from the first such index at or above gridDim.x.
   const int nq = min(kItemQueues, static_cast<int>(gridDim.x));
+  const bool queued = static_cast<int>(gridDim.x) < p.n_items;
   const int q = static_cast<int>(blockIdx.x) % nq;
   const int first_queued = q + nq * ((static_cast<int>(gridDim.x) - q + nq - 1) / nq);
   uint32_t* const my_queue = p.queue + q * kQueueStride;
@@ -315,7 +318,7 @@ void DecodeMfma(DecodeParams p) {
   for (int h = 0; h < GV; ++h) o[h][0] = o[h][1] = 0.f;
 
   auto process = [&](const T& t, int t0, int tend) {
-    if (!drawn && t0 + kDrawAhead >= tend) {  // wavefront-uniform
+    if (queued && !drawn && t0 + kDrawAhead >= tend) {  // wavefront-uniform
       drawn = true;
       if (lane == 0) ticket = atomicAdd(my_queue, 1u);
     }
@@ -538,7 +541,7 @@ void DecodeMfma(DecodeParams p) {
     }
   }
   }
-  if (lane == 0 && atomicAdd(p.queue_done, 1u) == gridDim.x - 1) {
+  if (queued && lane == 0 && atomicAdd(p.queue_done, 1u) == gridDim.x - 1) {
     for (int k = 0; k < nq; ++k) atomicExch(p.queue + k * kQueueStride, 0u);
     atomicExch(p.queue_done, 0u);
   }

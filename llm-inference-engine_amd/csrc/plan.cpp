@@ -18,6 +18,11 @@ constexpr int32_t kTile = 64;             // split lengths are whole 64-key unit
 // 150 -> 141 us, and C5, 268 -> 262 us; C4's items are all at the cap).
 constexpr int64_t kTargetItems = 2048;
 constexpr int32_t kMinSplit = 128;
+// Steps this small (fewer than 128 items of kMinSplit keys) are latency-bound:
+// each wavefront's walk over its range sets the time, so they split into
+// single 64-key units (C1, 513 keys x 2 kv heads: 14 us against 17.5 us per
+// attention call; C2, 500 items of 128 keys, is faster as it is).
+constexpr int64_t kSmallStepUnits = int64_t{128} * kMinSplit;
 constexpr int32_t kMaxSplitsPerRow = 64;  // bounds the merge a single wave performs
 
 int Fail(std::string* err, int code, const char* fmt, long long a = 0, long long b = 0,
@@ -99,7 +104,7 @@ int32_t ChooseSplitTokens(const ehip_geometry& g, int64_t unit_tokens) {
     if (v > 0) target = v;
   }
   int64_t s = (unit_tokens + target - 1) / target;
-  s = RoundUp(std::max<int64_t>(s, kMinSplit), kTile);
+  s = RoundUp(std::max<int64_t>(s, unit_tokens < kSmallStepUnits ? kTile : kMinSplit), kTile);
   return static_cast<int32_t>(std::min<int64_t>(s, max_split));
 }
 

@@ -140,7 +140,7 @@ def test_int8_steps_bit_exact_append_and_attention(gctx, ehip_mod, orc, H, Hkv, 
 
 
 @pytest.mark.parametrize("fmt", FORMATS)
-@pytest.mark.parametrize("split", ["128", "2048"])
+@pytest.mark.parametrize("split", ["64", "128", "2048"])
 def test_int8_long_rows_split_and_merged(gctx, ehip_mod, orc, monkeypatch, split, fmt):
     """Decode rows long enough to be split into several key ranges (the split
     partials go through the shared merge); 2048-key ranges span 128 blocks, the

@@ -73,6 +73,24 @@ def test_plan_split_override_and_long_rows(ehip_mod, monkeypatch):
     assert items == 8 * (64 + 1 + 1 + 2)
 
 
+def test_plan_small_steps_split_into_64_key_units(ehip_mod):
+    """A step with fewer than 128 items of 128 keys (128 * 128 kv-head-keys)
+    is split into 64-key ranges; C2 and larger keep at least 128 keys."""
+    from ehip import workloads
+    for w, want in ((workloads.c1(), 64), (workloads.c2(), 128)):
+        g = ehip_mod.geometry(w.heads, w.kv_heads, w.head_dim, w.block_size, w.kv_dtype,
+                              w.pool_blocks, w.scale)
+        st = ehip_mod.StepArrays(w.query_lens, w.context_lens, w.tables, w.slot_mapping)
+        rc, rows, items, partials, split = ehip_mod.plan_counts(g, st)
+        assert rc == 0 and split == want
+        assert items == expected_items(w.context_lens, w.kv_heads, split)
+    # the boundary: 8 kv heads x 2047 keys is below 16384 units, 8 x 2048 is not
+    for L, want in ((2047, 64), (2048, 128)):
+        rc, rows, items, partials, split = ehip_mod.plan_counts(
+            geom(ehip_mod, slab_blocks=200), simple_step(ehip_mod, [L]))
+        assert rc == 0 and split == want
+
+
 def test_plan_prefill_rows_are_causal(ehip_mod, monkeypatch):
     monkeypatch.setenv("EHIP_SPLIT_TOKENS", "128")
     monkeypatch.setenv("EHIP_NO_JOINT", "1")
@@ -367,7 +385,7 @@ def test_plan_joint_group_member_rule(ehip_mod):
 
 
 @pytest.mark.parametrize("fmt", ["int8", "fp8"])
-def test_plan_int8_shapes_and_append_groups(ehip_mod, fmt):
+def test_plan_int8_shapes_and_append_groups(ehip_mod, fmt, monkeypatch):
     """INT8 and FP8 KV: shapes outside the kernels' coverage are
     Unimplemented (9); rows landing in one block must take consecutive slots
     (2 otherwise); rows sharing leading blocks get joint items, as for bf16."""
@@ -386,7 +404,8 @@ def test_plan_int8_shapes_and_append_groups(ehip_mod, fmt):
                        np.array([36, 38, 39, 4 * 16 + 19], np.int64))
     assert E.plan_counts(ok, gap)[0] == 2
     # two sequences forked from one prefix share 8 leading blocks (128 keys):
-    # one joint range per kv head, for INT8/FP8 as for bf16
+    # one joint range per kv head at 128-key splits, for INT8/FP8 as for bf16
+    monkeypatch.setenv("EHIP_SPLIT_TOKENS", "128")
     shared = [np.arange(10, dtype=np.int32), np.array(list(range(8)) + [10, 11], np.int32)]
     st2 = E.StepArrays(np.array([1, 1], np.int32), np.array([150, 150], np.int64), shared,
                        np.array([9 * 16 + 5, 11 * 16 + 5], np.int64))
