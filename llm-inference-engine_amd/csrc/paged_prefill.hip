@@ -10,21 +10,19 @@
 // here K/V are read through the block table directly.
 //
 // Work: one workgroup of 4 wavefronts per (sequence, kv head, M query rows);
-// wavefront w owns 16 of those rows for 4 of the kv head's g query heads
-// (g = 4: M = 64, the wavefronts take rows 16w..; g = 8: M = 32, two row
-// groups x two head groups). Each wavefront keeps 4 (row block, head)
-// accumulator blocks, so every K and V operand read from LDS feeds four
-// MFMAs and every 16 KiB K/V tile staged in LDS serves 4M (row, head) pairs.
-// Keys stream in 32-token tiles staged in LDS (double-buffered, loaded two
-// tiles ahead into registers). K and V tiles are both row-major
-// [token][d] with rows padded to 288 bytes (256 + 32), written with 16-byte
-// stores. The gfx950 LDS has 64 banks for reads and serves a 16-byte read in
-// passes of 16 lanes: with a row stride of 72 dwords (8 mod 64) the MFMA A
-// operand of K (16 tokens x 8 elements per lane, one 16-byte read) and the
-// PV B operand of V read with ds_read_b64_tr_b16 (two transposed 8-byte reads
-// per lane: 4 tokens x 16 columns of 4 rows per 16-lane group) are both free
-// of bank conflicts, and the 16-byte stores (8 lanes per pass on 32 banks)
-// write 128 contiguous bytes per pass.
+// wavefront w owns 16 of those rows for 2 of the kv head's g query heads
+// (g = 4: M = 32, two row groups x two head groups; g = 8: M = 16, four head
+// groups). Each wavefront keeps 2 (row block, head) accumulator blocks, so
+// every K and V operand read from LDS feeds two MFMAs.
+// Keys stream in 32-token tiles that go from the slab straight into LDS
+// (buffer_load ... lds, no staging registers) into three buffers, two tiles
+// ahead of compute. K and V tiles are both row-major [token][d], 256-byte
+// rows with their 16-byte chunks XOR-swizzled by 2 (row mod 8) (a load
+// instruction writes 1 KiB of consecutive LDS, so rows cannot be padded).
+// The MFMA A operand of K (16 tokens x 8 elements per lane, one 16-byte read)
+// and the PV operand of V read with ds_read_b64_tr_b16 (two transposed 8-byte
+// reads per lane: 4 tokens x 16 columns of 4 rows per 16-lane group) read the
+// swizzled chunks.
 // S^T = K Q^T (v_mfma_f32_16x16x32_bf16, A = K, B = Q^T): lane l holds
 // scores of tokens 4*(l/16) + i of each 16-token half for query row l % 16,
 // which is exactly the A-operand layout P needs for O = P V once the two
@@ -32,7 +30,6 @@
 // (max/sum per row) runs in fp32 across the 4 lanes that share a row; the
 // output rescale is skipped for a tile in which no row's running max moved.
 #include <climits>
-#include <cstdlib>
 
 #include "decode_common.h"
 #include "device_util.h"
@@ -53,14 +50,9 @@ constexpr int kWaves = 4;
 // (head) accumulator blocks of 16 rows: 4 wavefronts over g / hb head groups.
 constexpr int PrefillRows(int g, int hb) { return 16 * (kWaves / (g / hb)); }
 
-// Accumulator blocks per wavefront (EHIP_PREFILL_HB=2|4 selects; 2 default).
-int PrefillHeadsPerWave() {
-  static const int hb = [] {
-    const char* e = std::getenv("EHIP_PREFILL_HB");
-    return e && e[0] == '4' ? 4 : 2;
-  }();
-  return hb;
-}
+// Accumulator blocks (heads) per wavefront: each K and V operand read from
+// LDS feeds two MFMAs.
+constexpr int kHeadsPerWave = 2;
 
 // ds_read_b64_tr_b16: lane i of each 16-lane group receives element i % 4 of
 // the 8 bytes addressed by lanes 4j + i / 4 of the group, for j = 0..3.
@@ -94,21 +86,25 @@ __device__ __forceinline__ float RowSum(float x) {
 
 template <int D>
 struct PrefillSmem {
-  static constexpr int ROW = D * 2 + 32;  // bytes per K or V row (padded)
+  static constexpr int ROW = D * 2;  // bytes per K or V row (16-byte chunks XOR-swizzled)
   static constexpr int TILE = kTile * ROW;
-  static constexpr int BYTES = 2 * 2 * TILE;  // K and V, double-buffered
-  // Q^T operands of every wavefront (when kept in LDS):
-  // [wave][head][chunk][lane] x 16 bytes.
-  static constexpr int QBYTES = kWaves * 4 * (D / 32) * 64 * 16;
-  static constexpr int SMALL = BYTES;           // Q^T in registers
-  static constexpr int TOTAL = BYTES + QBYTES;  // Q^T in LDS
 };
 
-template <int D, int G, int HB>
-__global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) {
-  // HB: heads (accumulator blocks) per wavefront. Q operands stay in
-  // registers for HB = 2 and move to LDS for HB = 4 (register pressure).
-  constexpr bool QL = HB > 2;
+// LDS byte offset of 16-byte chunk c of K/V row r inside a tile. The chunks of
+// a row are XOR-swizzled by 2 (r mod 8): rows are 256 bytes apart (the tile
+// loads write whole 1 KiB runs of LDS, so rows cannot be padded), and the
+// swizzle spreads both MFMA operand reads (a 16-byte K read of 16 rows at
+// one chunk; a transposed V read of 4 rows at two chunks) over the banks.
+__device__ __forceinline__ int SwzOff(int r, int c) { return r * 256 + ((c ^ (2 * (r & 7))) << 4); }
+
+// OCC: wavefronts per SIMD. 3 makes the register allocation fit 168 (a few
+// values spilled outside the tile loop; the three 48 KiB tile buffers of
+// three workgroups fit a CU's LDS). 2 leaves it unconstrained: it lands at
+// 180-186 registers, and a target of 2 (182/178) measured 4% slower on C3.
+template <int D, int G, int OCC>
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(OCC == 3 ? 3 : 1)))
+void PrefillMfmaBf16(PrefillParams p) {
+  constexpr int HB = kHeadsPerWave;   // heads (accumulator blocks) per wavefront
   constexpr int NHG = G / HB;         // head groups
   constexpr int RG = kWaves / NHG;    // 16-row groups per workgroup
   constexpr int M = 16 * RG;          // query rows per workgroup
@@ -121,7 +117,6 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
   constexpr int KV_VECS = kTile * D / 8;  // 16-byte vectors per tile (K or V)
   static_assert(KV_VECS == 2 * kWaves * 64, "tile / block shape");
 
-  extern __shared__ __align__(16) unsigned char smem[];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -146,11 +141,9 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
   const int qnw = min(16, max(0, T - r0));   // its live rows (0: nothing to compute)
   const int wend = min(P + r0 + qnw, key1);  // keys this wavefront's rows attend here
 
-  // Q^T as MFMA B operands (bf16, round-to-nearest-even): lane l holds
-  // Q[row r0 + l%16][c*32 + 8*kq .. +8] for each of its heads. They are kept
-  // in LDS (each is read once per tile) rather than in 64 registers.
-  uint4* qlds = reinterpret_cast<uint4*>(smem + SM::BYTES) + wave * HB * NC * 64;
-  bf16x8_t qreg[QL ? 1 : HB][NC];
+  // Q^T as MFMA B operands (bf16, round-to-nearest-even), in registers:
+  // lane l holds Q[row r0 + l%16][c*32 + 8*kq .. +8] for each of its heads.
+  bf16x8_t qreg[HB][NC];
   {
     const int qr = r0 + min(n, max(qnw, 1) - 1);
 #pragma unroll
@@ -165,10 +158,7 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
         bf16x8_t qv;
 #pragma unroll
         for (int i = 0; i < 8; ++i) qv[i] = static_cast<__bf16>(x[i]);
-        if constexpr (QL)
-          qlds[(hh * NC + c) * 64 + lane] = __builtin_bit_cast(uint4, qv);
-        else
-          qreg[QL ? 0 : hh][c] = qv;
+        qreg[hh][c] = qv;
       }
     }
   }
@@ -178,12 +168,18 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
   const uint16_t* kslab = static_cast<const uint16_t*>(p.k_slab) + int64_t{hk} * bs * D;
   const uint16_t* vslab = static_cast<const uint16_t*>(p.v_slab) + int64_t{hk} * bs * D;
   constexpr int EG = D / 8;  // 8-element groups per row
-  // Two staging slots: each holds a later tile's two 16-byte vectors of K and
-  // of V (K0, K1, V0, V1), so global loads run two tiles ahead of compute.
-  uint4 stA0, stA1, stA2, stA3, stB0, stB1, stB2, stB3;
+  // K/V tiles go from the slab straight into LDS (buffer_load ... lds: no
+  // staging registers), into three buffers, two tiles ahead of compute.
+  static_assert(D == 128, "tile loads write 4 rows of 256 bytes per instruction");
+  __shared__ __align__(16) unsigned char lt0[2 * SM::TILE];
+  __shared__ __align__(16) unsigned char lt1[2 * SM::TILE];
+  __shared__ __align__(16) unsigned char lt2[2 * SM::TILE];
   bool bad = false;
-  // Thread -> K and V vectors u = tid and tid + 256 (token u / EG, group u % EG).
-  const int tk0 = tid / EG, tk1 = (tid + kWaves * 64) / EG, ek = tid % EG;
+  // Thread -> K and V rows tk0 = tid / 16 and tk1 = tk0 + 16: one load
+  // instruction of a wavefront writes the 1 KiB of rows 4w..4w+3 (then
+  // 16+4w..), lane l the 16 bytes at 16 l, which hold chunk (l % 16) ^ 2 (row
+  // mod 8) of its row: the lane reads that chunk from the slab.
+  const int tk0 = tid / EG, tk1 = tk0 + kTile / 2, ek = tid % EG;
   // bs is a power of two: block index and slot by shift and mask. A 32-key
   // tile spans at most two blocks (bs >= 16, tiles start at multiples of
   // 32): their two ids are read once per wavefront and selected per thread,
@@ -203,7 +199,7 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kslab), 0, 0xFFFFFFFFu, 0x00020000);
   const __amdgpu_buffer_rsrc_t rv =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vslab), 0, 0xFFFFFFFFu, 0x00020000);
-  const uint32_t ko = static_cast<uint32_t>(ek * 16);
+  const uint32_t ko = static_cast<uint32_t>((ek ^ (2 * (tk0 & 7))) * 16);
 #define EHIP_PF_IDLOAD(ID, K0)                                                               \
   do {                                                                                      \
     const int kb0 = min((K0) >> bsh, last_blk);                                             \
@@ -211,7 +207,8 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
     ID##1 = __builtin_amdgcn_raw_buffer_load_b32(                                            \
         rt, static_cast<uint32_t>(min(kb0 + 1, last_blk)) * 4u, 0, 0);                      \
   } while (0)
-#define EHIP_PF_GLOAD(ST, K0, ID)                                                              \
+#define EHIP_PF_LDSP(x) ((__attribute__((address_space(3))) void*)(x))
+#define EHIP_PF_GLOAD(BUF, K0, ID)                                                             \
   do {                                                                                      \
     const int kb0 = min((K0) >> bsh, last_blk);                                             \
     int id0 = __builtin_amdgcn_readfirstlane(ID##0);                                         \
@@ -225,10 +222,14 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
                         static_cast<uint32_t>((pk0 & bmask) * D * 2) + ko;                   \
     const uint32_t a1 = static_cast<uint32_t>((pk1 >> bsh) != kb0 ? id1 : id0) * stride_b +  \
                         static_cast<uint32_t>((pk1 & bmask) * D * 2) + ko;                   \
-    ST##0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, a0, 0, 0)); \
-    ST##1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, a1, 0, 0)); \
-    ST##2 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, a0, 0, 0)); \
-    ST##3 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, a1, 0, 0)); \
+    unsigned char* const lk = (BUF) + wave * 1024;                                           \
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, EHIP_PF_LDSP(lk), 16, a0, 0, 0, 0);        \
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, EHIP_PF_LDSP(lk + SM::TILE / 2), 16, a1, 0, \
+                                             0, 0);                                         \
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, EHIP_PF_LDSP(lk + SM::TILE), 16, a0, 0, 0,  \
+                                             0);                                            \
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(                                                \
+        rv, EHIP_PF_LDSP(lk + SM::TILE + SM::TILE / 2), 16, a1, 0, 0, 0);                   \
   } while (0)
 
   // Per head state. Scores/probabilities live in the S^T layout (row n =
@@ -246,23 +247,13 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
   const float sl2 = p.scale_log2;          // scores -> log2 domain
 
   const int ntiles = (key1 - key0 + kTile - 1) / kTile;
-  // Writes a staged tile into LDS buffer BUF (K then V, both row-major).
-#define EHIP_PF_STORE(ST, BUF)                                            \
-  do {                                                                  \
-    unsigned char* kw = smem + (BUF) * (2 * SM::TILE);                   \
-    unsigned char* vw = kw + SM::TILE;                                   \
-    *reinterpret_cast<uint4*>(kw + tk0 * SM::ROW + ek * 16) = ST##0;     \
-    *reinterpret_cast<uint4*>(kw + tk1 * SM::ROW + ek * 16) = ST##1;     \
-    *reinterpret_cast<uint4*>(vw + tk0 * SM::ROW + ek * 16) = ST##2;     \
-    *reinterpret_cast<uint4*>(vw + tk1 * SM::ROW + ek * 16) = ST##3;     \
-  } while (0)
-  auto compute_tile = [&](int tile, int buf) __attribute__((always_inline)) {
+  auto compute_tile = [&](int tile, const unsigned char* buf) __attribute__((always_inline)) {
     const int k0 = key0 + tile * kTile;
     // Wavefront-uniform: a tile wholly past this wavefront's last row (the
     // other row groups' diagonal) is skipped.
     if (k0 < wend) {
-      const unsigned char* kb = smem + buf * (2 * SM::TILE);
-      const unsigned char* vb = kb + SM::TILE;
+      const unsigned char* kb = buf;
+      const unsigned char* vb = buf + SM::TILE;
       // Keys past this lane's query position (or past the workgroup's last
       // key) are masked.
       const bool diag = k0 + kTile > P + r0 || k0 + kTile > key1;
@@ -279,12 +270,10 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
 #pragma unroll
         for (int h2 = 0; h2 < 2; ++h2)
           ka[h2] = __builtin_bit_cast(
-              bf16x8_t, *reinterpret_cast<const uint4*>(kb + (16 * h2 + n) * SM::ROW +
-                                                        (c * 32 + kq * 8) * 2));
+              bf16x8_t, *reinterpret_cast<const uint4*>(kb + SwzOff(16 * h2 + n, 4 * c + kq)));
 #pragma unroll
         for (int hh = 0; hh < HB; ++hh) {
-          const bf16x8_t qv = QL ? __builtin_bit_cast(bf16x8_t, qlds[(hh * NC + c) * 64 + lane])
-                                 : qreg[QL ? 0 : hh][c];
+          const bf16x8_t qv = qreg[hh][c];
 #pragma unroll
           for (int h2 = 0; h2 < 2; ++h2)
             s[hh][h2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[h2], qv, s[hh][h2], 0, 0, 0);
@@ -368,11 +357,13 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
       // 4kq + s/4 (+16), columns 16nb + 4(s%4) .. +3, and lane n receives
       // column 16nb + n of the group's 4 rows. The B operand is P^T, which is
       // this lane's P values as they are (row n, the same 8 tokens).
-      const unsigned char* vl = vb + (4 * kq + (n >> 2)) * SM::ROW + (n & 3) * 8;
+      const int vr = 4 * kq + (n >> 2);
+      const unsigned char* vl = vb + (n & 1) * 8;
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
-        const bf16x4_t v0 = TransposedRead(vl + nb * 32);
-        const bf16x4_t v1 = TransposedRead(vl + 16 * SM::ROW + nb * 32);
+        const int vo = SwzOff(vr, 2 * nb + ((n & 3) >> 1));
+        const bf16x4_t v0 = TransposedRead(vl + vo);
+        const bf16x4_t v1 = TransposedRead(vl + 16 * SM::ROW + vo);
         const bf16x8_t vbv = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
         for (int hh = 0; hh < HB; ++hh)
@@ -380,35 +371,50 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
       }
     }
   };
-  // Tile t is staged in slot t % 2 and LDS buffer t % 2; its slot is
-  // refilled with tile t + 2 right after it is written to LDS.
-  // The loop waits for one slot's loads while the other slot's are still in
-  // flight (vmcnt counts loads in issue order). That holds only if every path
-  // into the loop head has issued slot A's loads before slot B's: so the
-  // loads run unconditionally (tiles past the item's end re-read its last
-  // rows, clamped, and an odd last tile's partner is computed as an empty
-  // tile), and the prologue's two loads are kept in order (the scheduler
-  // may otherwise issue B's first, and every wait becomes a wait for all).
-  uint32_t idA0, idA1, idB0, idB1;  // block ids of each slot's next tile
+  // Tile t goes to LDS buffer t % 3 (ids slot t % 3). Step t: wait until
+  // this wavefront's loads of tile t have landed, barrier (every
+  // wavefront's part of tile t is in LDS, and every wavefront is done
+  // reading tile t - 1, whose buffer takes tile t + 2), issue tile t + 2's
+  // loads and the block ids of tile t + 5, compute tile t. The loads run
+  // unconditionally (tiles past the item's end re-read its last rows,
+  // clamped; such steps compute nothing), so at every wait the same vector
+  // memory operations follow tile t's loads in issue order: the ids of
+  // tile t + 3, tile t + 1's four loads and the ids of tile t + 4 (vmcnt
+  // retires them in order; the compiler barriers keep that order).
+  uint32_t idA0, idA1, idB0, idB1, idC0, idC1;  // block ids of each buffer's next tile
+#define EHIP_PF_FENCE() asm volatile("" ::: "memory")
   EHIP_PF_IDLOAD(idA, key0);
   EHIP_PF_IDLOAD(idB, key0 + kTile);
-  EHIP_PF_GLOAD(stA, key0, idA);
-  EHIP_PF_IDLOAD(idA, key0 + 2 * kTile);
-  __builtin_amdgcn_sched_barrier(0);
-  EHIP_PF_GLOAD(stB, key0 + kTile, idB);
-  EHIP_PF_IDLOAD(idB, key0 + 3 * kTile);
-  for (int tile = 0; tile < ntiles; tile += 2) {
-    EHIP_PF_STORE(stA, 0);
-    __syncthreads();
-    EHIP_PF_GLOAD(stA, key0 + (tile + 2) * kTile, idA);
-    EHIP_PF_IDLOAD(idA, key0 + (tile + 4) * kTile);
-    compute_tile(tile, 0);
-    EHIP_PF_STORE(stB, 1);
-    __syncthreads();
-    EHIP_PF_GLOAD(stB, key0 + (tile + 3) * kTile, idB);
-    EHIP_PF_IDLOAD(idB, key0 + (tile + 5) * kTile);
-    compute_tile(tile + 1, 1);  // no work when tile + 1 == ntiles
+  EHIP_PF_IDLOAD(idC, key0 + 2 * kTile);
+  EHIP_PF_FENCE();
+  EHIP_PF_GLOAD(lt0, key0, idA);
+  EHIP_PF_FENCE();
+  EHIP_PF_IDLOAD(idA, key0 + 3 * kTile);
+  EHIP_PF_FENCE();
+  EHIP_PF_GLOAD(lt1, key0 + kTile, idB);
+  EHIP_PF_FENCE();
+  EHIP_PF_IDLOAD(idB, key0 + 4 * kTile);
+  EHIP_PF_FENCE();
+#define EHIP_PF_STEP(T, X, Y, IDY)                                      \
+  do {                                                                  \
+    asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");       \
+    EHIP_PF_GLOAD(Y, key0 + ((T) + 2) * kTile, IDY);                     \
+    EHIP_PF_FENCE();                                                    \
+    EHIP_PF_IDLOAD(IDY, key0 + ((T) + 5) * kTile);                       \
+    EHIP_PF_FENCE();                                                    \
+    compute_tile((T), (X));                                             \
+  } while (0)
+  for (int tile = 0; tile < ntiles; tile += 3) {
+    EHIP_PF_STEP(tile, lt0, lt2, idC);
+    EHIP_PF_STEP(tile + 1, lt1, lt0, idA);
+    EHIP_PF_STEP(tile + 2, lt2, lt1, idB);
   }
+  // Loads past the item's end may still be in flight: they write this
+  // workgroup's LDS, so they land before the workgroup ends.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#undef EHIP_PF_STEP
+#undef EHIP_PF_FENCE
+#undef EHIP_PF_LDSP
 
   // Row sums: each lane holds a partial over its tokens; the 4 lanes of a
   // row (l % 16 equal) together hold the row total. O^T puts output row n,
@@ -446,7 +452,6 @@ __global__ __launch_bounds__(kWaves * 64) void PrefillMfmaBf16(PrefillParams p) 
   if (__any(bad) && lane == 0) atomicOr(p.err, kErrBlockRange);
 #undef EHIP_PF_GLOAD
 #undef EHIP_PF_IDLOAD
-#undef EHIP_PF_STORE
 }
 
 }  // namespace
@@ -457,17 +462,27 @@ bool LaunchPrefillMfma(const PrefillParams& p, hipStream_t stream, hipError_t* e
     return true;
   }
   const dim3 grid(p.n_items), block(kWaves * 64);
-  const int hb = PrefillHeadsPerWave();
-#define EHIP_PREFILL_CASE(DD, GG)                                                         \
-  if (p.d == DD && p.group == GG) {                                                       \
-    if (hb == 4)                                                                          \
-      hipLaunchKernelGGL((PrefillMfmaBf16<DD, GG, 4>), grid, block,                       \
-                         PrefillSmem<DD>::TOTAL, stream, p);                              \
-    else                                                                                  \
-      hipLaunchKernelGGL((PrefillMfmaBf16<DD, GG, 2>), grid, block, PrefillSmem<DD>::SMALL, \
-                         stream, p);                                                      \
-    *err = hipGetLastError();                                                             \
-    return true;                                                                          \
+  // Three workgroups per CU where the launch has work for several rounds of
+  // them (the C5 re-prefill, 2048 workgroups: 277-278 us against 285 us at
+  // two); two where it is bound by its longest blocks' walk (C3's 600
+  // workgroups: 36.8 us at two against 38.6-39.6 us at three, the critical
+  // blocks sharing their CU with more neighbours).
+  static const int cus = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      return 256;
+    return n > 0 ? n : 256;
+  }();
+  const bool occ3 = p.n_items >= 4 * cus;
+#define EHIP_PREFILL_CASE(DD, GG)                                                  \
+  if (p.d == DD && p.group == GG) {                                                \
+    if (occ3)                                                                      \
+      hipLaunchKernelGGL((PrefillMfmaBf16<DD, GG, 3>), grid, block, 0, stream, p); \
+    else                                                                           \
+      hipLaunchKernelGGL((PrefillMfmaBf16<DD, GG, 2>), grid, block, 0, stream, p); \
+    *err = hipGetLastError();                                                      \
+    return true;                                                                   \
   }
   EHIP_PREFILL_CASE(128, 4)
   EHIP_PREFILL_CASE(128, 8)
@@ -478,7 +493,7 @@ bool LaunchPrefillMfma(const PrefillParams& p, hipStream_t stream, hipError_t* e
 int PrefillRowsPerItem(int kv_dtype, int d, int group, int bs, int64_t slab_bytes) {
   if (kv_dtype != EHIP_KV_BF16 || d != 128 || (group != 4 && group != 8) || bs < 16) return 0;
   if (slab_bytes > int64_t{0xFFFFFFFF}) return 0;  // 32-bit K/V byte offsets
-  return PrefillRows(group, PrefillHeadsPerWave());
+  return PrefillRows(group, kHeadsPerWave);
 }
 
 }  // namespace ehip
