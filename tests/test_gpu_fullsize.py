@@ -114,16 +114,20 @@ def test_benched_layer_at_full_size(gctx, ehip_mod, orc, config):
     check(w, got, ref_r, ref32)
 
 
-def test_c5_reprefill_chunk_sampled_rows(gctx, ehip_mod, orc):
+@pytest.mark.parametrize("heads", [64, 32])
+def test_c5_reprefill_chunk_sampled_rows(gctx, ehip_mod, orc, heads):
     """C5's preempt-and-recompute event: an evicted sequence re-prefilled as
     one 4096-row causal chunk (P = 0) with its K/V appended in the same step.
     Row t of the chunk equals a single-row decode over keys [0, t] of the
-    post-append cache: checked on the first and last rows and every 64th."""
+    post-append cache: checked on the first and last rows and every 64th.
+    Both launches have at least 4 prefill workgroups per CU (2048 for g = 8,
+    1024 for g = 4 on 256 CUs), so they run the three-workgroups-per-CU
+    instances of the prefill kernel."""
     from ehip import workloads
     c5 = workloads.c5()
     T, bs = 4096, c5.block_size
     table = np.asarray(c5.tables[0][:T // bs], np.int32)
-    w = workloads._finish("C5-reprefill", c5.heads, c5.kv_heads, c5.head_dim, bs, c5.kv_dtype,
+    w = workloads._finish("C5-reprefill", heads, c5.kv_heads, c5.head_dim, bs, c5.kv_dtype,
                           1, [T], [T], [table], c5.pool_blocks, c5.qkv_std, seed=c5.seed)
     H, Hkv, d = w.heads, w.kv_heads, w.head_dim
     k32, v32 = c5.pool(0)
