@@ -358,6 +358,27 @@ def test_split_count_independence(gctx, orc, split, monkeypatch):
     check_fp32(got, ref)
 
 
+@pytest.mark.parametrize("H", [32, 64])
+def test_merge_of_wide_groups(gctx, orc, H, monkeypatch):
+    # One kv head for all H query heads, and a row cut into the most splits a
+    # row may have (64): 64 * 32 = 2048 (max, sum) pairs still fit the merge
+    # workgroup's LDS; 64 * 64 = 4096 take the one-wavefront sequential merge.
+    monkeypatch.setenv("EHIP_SPLIT_TOKENS", "128")
+    monkeypatch.setenv("EHIP_DECODE_WG", "0")
+    rng = np.random.default_rng(H)
+    lengths = [8192, 300, 1, 2500]
+    Hkv, d, bs = 1, 64, 16
+    q, ks, vs, tables = batched_case(orc, rng, lengths, H, Hkv, d, bs)
+    out = gctx.alloc(q.nbytes)
+    assert gctx.paged_decode_batched(gctx.to_device(q), gctx.to_device(ks), gctx.to_device(vs),
+                                     tables, lengths, H, Hkv, d, bs, 0, ks.shape[0],
+                                     scale_for(d), out) == 0
+    gctx.sync()
+    got = out.download(np.float32, q.shape)
+    ref = orc.paged_decode_batched(q, ks, vs, tables, lengths, H, Hkv, d, bs, scale_for(d))
+    check_fp32(got, ref)
+
+
 # ------------------------------------------------------------------ step path
 def run_step(gctx, ehip_mod, orc, w, seed, layers=1):
     """Upload one step, then per layer append + attend on the GPU; the oracle
