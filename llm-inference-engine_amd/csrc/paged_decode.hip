@@ -471,15 +471,34 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void DecodeGeneric(DecodeParam
 
 // ----------------------------------------------------------------------------
 // Split merge. A (row, kv head) group with more than one split is merged by
-// ceil(g*d / 256) workgroups of 256 threads, one output element per thread:
-// the group's (max, sum) pairs are read into LDS in one parallel sweep, the g
-// per-head weights 2^(m_s - M) / L are formed there, and each thread then sums
-// its element's split partials with independent loads, so a group costs a few
-// memory round trips whatever its split count.
+// ceil(g*d / (256*EPT)) workgroups of 256 threads, EPT consecutive output
+// elements of one head per thread (EPT = 4, 16-byte loads and stores, when d
+// and the output allow it): the group's (max, sum) pairs are read into LDS in
+// one parallel sweep, the g per-head weights 2^(m_s - M) / L are formed there,
+// and each thread then sums its elements' split partials with independent
+// loads, so a group costs a few memory round trips whatever its split count.
 constexpr int kMergeThreads = 256;
 constexpr int kMergeMaxPairs = 2048;  // nsplit * g held in LDS (16 KiB)
 
+template <int EPT>
+struct MergeVec;
+template <>
+struct MergeVec<1> {
+  using T = float;
+  __device__ static float Fma(float w, float x, float acc) { return fmaf(w, x, acc); }
+};
+template <>
+struct MergeVec<4> {
+  using T = float4;
+  __device__ static float4 Fma(float w, float4 x, float4 acc) {
+    return make_float4(fmaf(w, x.x, acc.x), fmaf(w, x.y, acc.y), fmaf(w, x.z, acc.z),
+                       fmaf(w, x.w, acc.w));
+  }
+};
+
+template <int EPT>
 __global__ __launch_bounds__(kMergeThreads) void MergeSplitsKernel(DecodeParams p, int chunks) {
+  using V = typename MergeVec<EPT>::T;
   __shared__ float2 ml[kMergeMaxPairs];
   const int64_t grp = blockIdx.x / chunks;
   const int chunk = static_cast<int>(blockIdx.x - grp * chunks);
@@ -498,16 +517,18 @@ __global__ __launch_bounds__(kMergeThreads) void MergeSplitsKernel(DecodeParams 
     return;
   }
   const int gd = g * d;
-  const int j = chunk * kMergeThreads + tid;
+  const int j = (chunk * kMergeThreads + tid) * EPT;  // first element; d % EPT == 0
   const bool has = j < gd;
   const int h = has ? j / d : 0;
-  const float* po = p.part_o + pbase * gd + (has ? j : 0);
+  const int gdv = gd / EPT;
+  const V* po = reinterpret_cast<const V*>(p.part_o + pbase * gd + (has ? j : 0));
   // The partial outputs do not depend on the weights: the first kMergeBatch
   // of them are loaded together with the (max, sum) pairs.
   constexpr int kMergeBatch = 16;
-  float ov[kMergeBatch];
+  V ov[kMergeBatch];
 #pragma unroll
-  for (int s = 0; s < kMergeBatch; ++s) ov[s] = s < nsplit ? po[int64_t{s} * gd] : 0.f;
+  for (int s = 0; s < kMergeBatch; ++s)
+    if (s < nsplit) ov[s] = po[int64_t{s} * gdv];
   const float2* src = reinterpret_cast<const float2*>(p.part_ml) + pbase * g;
   for (int i = tid; i < npairs; i += kMergeThreads) ml[i] = src[i];
   __syncthreads();
@@ -521,14 +542,14 @@ __global__ __launch_bounds__(kMergeThreads) void MergeSplitsKernel(DecodeParams 
   }
   __syncthreads();
   if (!has) return;
-  float acc = 0.f;
+  V acc{};
 #pragma unroll
   for (int s = 0; s < kMergeBatch; ++s)
-    if (s < nsplit) acc = fmaf(ml[s * g + h].x, ov[s], acc);
+    if (s < nsplit) acc = MergeVec<EPT>::Fma(ml[s * g + h].x, ov[s], acc);
 #pragma unroll 8
   for (int s = kMergeBatch; s < nsplit; ++s)
-    acc = fmaf(ml[s * g + h].x, po[int64_t{s} * gd], acc);
-  p.out[(int64_t{row} * p.heads + int64_t{hk} * g) * d + j] = acc;
+    acc = MergeVec<EPT>::Fma(ml[s * g + h].x, po[int64_t{s} * gdv], acc);
+  *reinterpret_cast<V*>(p.out + (int64_t{row} * p.heads + int64_t{hk} * g) * d + j) = acc;
 }
 
 template <class KV>
@@ -640,9 +661,24 @@ hipError_t LaunchDecode(const DecodeParams& p, int kv_dtype, QueueState* queue,
   // Only the rows that were split: a step dominated by prefill-chunk rows
   // (which need no merge) launches no idle merge blocks.
   const int64_t groups = int64_t{p.n_merge} * p.kv_heads;
-  const int chunks = (p.group * p.d + kMergeThreads - 1) / kMergeThreads;
-  hipLaunchKernelGGL(MergeSplitsKernel, dim3(groups * chunks), dim3(kMergeThreads), 0, stream, p,
-                     chunks);
+  const int gd = p.group * p.d;
+  // Four elements per thread for merges of 2^18 output elements or more,
+  // where fewer instructions per element pay (merge kernel, rocprofv3: C4's
+  // 2048 groups of 512 elements 7.8 -> 6.7 us, C5's 256 groups of 1024
+  // 8.8 -> 8.5 us). Small merges keep one element per thread, whose extra
+  // threads put more loads in flight at once (C2's 64 groups of 448: 4.7
+  // against 5.0 us with four). The partial workspace is 256-byte aligned; the
+  // output row offset is a multiple of d floats.
+  const bool wide = groups * gd >= (int64_t{1} << 18);
+  if (wide && p.d % 4 == 0 && reinterpret_cast<uintptr_t>(p.out) % 16 == 0) {
+    const int chunks = (gd + 4 * kMergeThreads - 1) / (4 * kMergeThreads);
+    hipLaunchKernelGGL(MergeSplitsKernel<4>, dim3(groups * chunks), dim3(kMergeThreads), 0,
+                       stream, p, chunks);
+  } else {
+    const int chunks = (gd + kMergeThreads - 1) / kMergeThreads;
+    hipLaunchKernelGGL(MergeSplitsKernel<1>, dim3(groups * chunks), dim3(kMergeThreads), 0,
+                       stream, p, chunks);
+  }
   return hipGetLastError();
 }
 

@@ -379,6 +379,28 @@ def test_merge_of_wide_groups(gctx, orc, H, monkeypatch):
     check_fp32(got, ref)
 
 
+@pytest.mark.parametrize("split", ["128", "256"])
+def test_large_merge_four_elements_per_thread(gctx, orc, split, monkeypatch):
+    # At least 32 split rows x 8 kv heads x 1024 elements = 2^18: the merge
+    # takes four elements per thread; the 2049- and 4000-key rows have more
+    # than the 16 splits whose partials are loaded before the weights are
+    # formed.
+    monkeypatch.setenv("EHIP_SPLIT_TOKENS", split)
+    monkeypatch.setenv("EHIP_DECODE_WG", "0")
+    rng = np.random.default_rng(int(split))
+    lengths = [int(x) for x in rng.integers(300, 900, size=40)] + [1, 2049, 4000]
+    H, Hkv, d, bs = 64, 8, 128, 16
+    q, ks, vs, tables = batched_case(orc, rng, lengths, H, Hkv, d, bs)
+    out = gctx.alloc(q.nbytes)
+    assert gctx.paged_decode_batched(gctx.to_device(q), gctx.to_device(ks), gctx.to_device(vs),
+                                     tables, lengths, H, Hkv, d, bs, 0, ks.shape[0],
+                                     scale_for(d), out) == 0
+    gctx.sync()
+    got = out.download(np.float32, q.shape)
+    ref = orc.paged_decode_batched(q, ks, vs, tables, lengths, H, Hkv, d, bs, scale_for(d))
+    check_fp32(got, ref)
+
+
 # ------------------------------------------------------------------ step path
 def run_step(gctx, ehip_mod, orc, w, seed, layers=1):
     """Upload one step, then per layer append + attend on the GPU; the oracle
