@@ -27,8 +27,11 @@ Prints ONE JSON line (metric/value/unit as BASELINE.json names them):
                  0 (fp32 K/V); its outputs are also the parity checker;
   parity       = the benched step's layer 0 against that oracle: the append
                  (bit-exact slabs), the outputs against the reference run on
-                 the bf16-rounded K/V (max_rel, allclose) and on the original
-                 fp32 K/V (max_abs).
+                 the bf16-rounded K/V (per-vector max_rel, allclose) and on
+                 the original fp32 K/V (max_abs); "pass" is those bars. The
+                 elementwise max_rel <= 1e-4 gate is reported beside them
+                 ("elementwise_max_rel_gate", with whether the reference's own
+                 scalar and AVX2 backends meet it against each other).
 """
 from __future__ import annotations
 
@@ -212,6 +215,17 @@ def cpu_baseline_and_parity(w, layer0, seconds: float):
         par["bars"]["vs_reference_on_fp32_kv"] = "max_abs <= 2e-2"
         ok = ok and par["vs_reference_on_fp32_kv"]["max_abs"] <= 2e-2
     par["pass"] = bool(ok)
+    # The north star's literal fp32 gate is the elementwise max_rel <= 1e-4.
+    # It is reported as its own gate, not folded into "pass": the reference's
+    # own scalar and AVX2 backends miss it against each other on this cache
+    # (near-zero outputs of cancelling sums keep only rounding noise), which
+    # is why the bar above is per output vector plus the reference allclose.
+    elem = par[gate]["max_rel"]
+    ref_elem = par["reference_scalar_vs_avx2"]["max_rel"]
+    par["elementwise_max_rel_gate"] = {
+        "bar": "max_rel <= 1e-4 (elementwise)", "value": elem, "met": bool(elem <= 1e-4),
+        "reference_scalar_vs_avx2": ref_elem,
+        "reference_meets_it": bool(ref_elem <= 1e-4)}
     return base, par
 
 

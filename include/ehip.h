@@ -222,6 +222,24 @@ int ehip_decode_attention_f32(ehip_ctx* ctx, const float* d_q, const float* d_k,
                               float* d_out, int64_t heads, int64_t kv_heads, int64_t d,
                               int64_t l_dim, float scale);
 
+/* kernels::PrefillAttentionVarlenF32 (src/kernels/attention.h:221-227), in the
+ * reference's argument order: sequence b's query rows are [cu_seqlens[b],
+ * cu_seqlens[b+1]) of d_q/d_out [sum T, H, d], attending causally over its
+ * own contiguous head-major cache d_k_seqs[b] / d_v_seqs[b] ([Hkv, L_b, d],
+ * L_b = h_l_dims[b] >= T_b: P_b = L_b - T_b cached keys, then the chunk's).
+ * cu_seqlens, the pointer arrays and l_dims are host arrays (the K/V they
+ * point at are device memory). Every sequence is validated before anything is
+ * launched; then each runs through the paged kernels over an identity table,
+ * as ehip_prefill_attention_f32 (one plan and launch per sequence: the step
+ * path, ehip_step_upload + ehip_step_attention, is the one-launch route over
+ * paged slabs). num_seqs == 0 is a no-op. fp32. */
+int ehip_prefill_attention_varlen_f32(ehip_ctx* ctx, const float* d_q,
+                                      const int32_t* h_cu_seqlens, int64_t num_seqs,
+                                      const float* const* h_k_seqs,
+                                      const float* const* h_v_seqs, const int64_t* h_l_dims,
+                                      float* d_out, int64_t heads, int64_t kv_heads, int64_t d,
+                                      float scale);
+
 /* No counterpart in the reference: the allocation-free variant of
  * ehip_paged_decode_attention_f32 (same arguments and results), for callers
  * that cannot allocate device memory — code under HIP graph capture, tight
@@ -229,9 +247,11 @@ int ehip_decode_attention_f32(ehip_ctx* ctx, const float* d_q, const float* d_k,
  * partials live in a static per-device scratch array of 4 MiB, written by a
  * kernel (no allocation, copy or host staging per call); rows that would need
  * more (key splits x H x (d + 2) x 4 bytes of partials, plus the plan) get
- * ResourceExhausted. Every call on a device shares that device's array:
- * calls that overlap on one device (two streams, two contexts) race and must
- * be ordered by the caller. */
+ * ResourceExhausted. Every call on a device shares that device's array, and
+ * eager calls run in call order whichever context or stream makes them (each
+ * waits for the previous call's end through a per-device event). A call made
+ * on a stream under graph capture is ordered only by its graph: replays of
+ * it must not overlap eager calls on the same device. */
 int ehip_paged_decode_attention_f32_noalloc(ehip_ctx* ctx, const float* d_q,
                                             const float* d_k_slab, const float* d_v_slab,
                                             const int32_t* d_block_table, int64_t num_blocks,

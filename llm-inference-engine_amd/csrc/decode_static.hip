@@ -12,6 +12,14 @@
 // never uses the array's name as a device address: the address is fetched
 // once per device with hipGetSymbolAddress (InitStaticScratch, called from
 // context creation with that device current) and kept per device.
+//
+// Calls on one device share its array, whichever context or stream makes
+// them, so eager calls are ordered through a per-device event: each call's
+// stream waits for the event (the previous call's end), launches, and records
+// the event again, all under one lock. A call on a stream that is being
+// captured into a graph skips the event (a capture may not wait on work
+// recorded outside it): replays of such a graph are ordered by the stream
+// they are launched on, and must not overlap eager calls on the device.
 #include <hip/hip_runtime.h>
 
 #include <mutex>
@@ -27,6 +35,7 @@ static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
 
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
+hipEvent_t g_scratch_done[kMaxDevices] = {};  // end of the device's last eager call
 
 __global__ __launch_bounds__(64) void WriteRowPlan(RowDesc* rows, WorkItem* items,
                                                   int32_t* merge_rows, int32_t length,
@@ -57,8 +66,12 @@ hipError_t InitStaticScratch(int device) {
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (g_scratch_ptr[device]) return hipSuccess;
   void* ptr = nullptr;
-  const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
   if (e != hipSuccess) return e;
+  hipEvent_t done = nullptr;
+  e = hipEventCreateWithFlags(&done, hipEventDisableTiming);
+  if (e != hipSuccess) return e;
+  g_scratch_done[device] = done;
   g_scratch_ptr[device] = ptr;
   return hipSuccess;
 }
@@ -70,18 +83,24 @@ size_t StaticScratchNeed(int64_t nsplit, int kv_heads, int group, int d) {
 }
 
 hipError_t LaunchSingleRowStatic(const DecodeParams& base, int device, int32_t length,
-                                 int32_t split_len, int32_t nsplit, QueueState* queue,
-                                 hipStream_t stream) {
+                                 int32_t split_len, int32_t nsplit, const Tuning& tune,
+                                 QueueState* queue, hipStream_t stream) {
   if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
-  unsigned char* s = nullptr;
-  {
-    std::lock_guard<std::mutex> lock(g_scratch_mu);
-    s = static_cast<unsigned char*>(g_scratch_ptr[device]);
-  }
-  if (!s) return hipErrorNotInitialized;
   const int n_items = nsplit * base.kv_heads;
   if (StaticScratchNeed(nsplit, base.kv_heads, base.group, base.d) > kStaticScratchBytes)
     return hipErrorInvalidValue;
+  // Held until the call's kernels are enqueued and the device event records
+  // their end: calls from other threads and contexts queue behind it.
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  unsigned char* s = static_cast<unsigned char*>(g_scratch_ptr[device]);
+  hipEvent_t done = g_scratch_done[device];
+  if (!s || !done) return hipErrorNotInitialized;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipError_t e = hipStreamIsCapturing(stream, &cap); e != hipSuccess) return e;
+  const bool ordered = cap == hipStreamCaptureStatusNone;
+  if (ordered) {
+    if (hipError_t e = hipStreamWaitEvent(stream, done, 0); e != hipSuccess) return e;
+  }
   auto* rows = reinterpret_cast<RowDesc*>(s);
   auto* items = reinterpret_cast<WorkItem*>(s + 256);
   auto* merge = reinterpret_cast<int32_t*>(s + 256 + Align256(n_items * sizeof(WorkItem)));
@@ -102,7 +121,9 @@ hipError_t LaunchSingleRowStatic(const DecodeParams& base, int device, int32_t l
   p.max_length = length;
   p.has_prefill = 0;
   p.head_stride = int64_t{base.bs} * base.d;
-  return LaunchDecode(p, EHIP_KV_F32, queue, stream);
+  if (hipError_t e = LaunchDecode(p, EHIP_KV_F32, tune, queue, stream); e != hipSuccess) return e;
+  if (ordered) return hipEventRecord(done, stream);
+  return hipSuccess;
 }
 
 }  // namespace ehip

@@ -20,6 +20,7 @@ struct ehip_ctx {
   hipStream_t stream = nullptr;      // the stream every call enqueues on
   hipStream_t own_stream = nullptr;  // the context's own (created at init)
   char last_error[512] = {};  // fixed storage: reporting an error allocates nothing
+  ehip::Tuning tune;          // EHIP_* switches, read once at creation
 
   // Step descriptor: host staging (pinned, double-buffered so building step
   // n+1 never overwrites a buffer whose copy is still queued) and its device
@@ -240,7 +241,7 @@ int LaunchAttention(ehip_ctx* ctx, const float* q, const void* k_slab, const voi
   p.v_scale = v_scale;
   p.new_k = new_k;
   p.new_v = new_v;
-  EHIP_HIP(ctx, ehip::LaunchDecode(p, g.kv_dtype, &ctx->queue, ctx->stream));
+  EHIP_HIP(ctx, ehip::LaunchDecode(p, g.kv_dtype, ctx->tune, &ctx->queue, ctx->stream));
   return EHIP_OK;
 }
 
@@ -305,6 +306,7 @@ int ehip_init(int device, ehip_ctx** out) {
   ehip_ctx* ctx = new (std::nothrow) ehip_ctx;
   if (!ctx) return EHIP_OUT_OF_MEMORY;
   ctx->device = device;
+  ctx->tune = ehip::ReadTuning();
   int rc = EHIP_OK;
   do {
     hipError_t e = hipSetDevice(device);
@@ -579,7 +581,7 @@ int ehip_paged_decode_attention_f32(ehip_ctx* ctx, const float* d_q, const float
     return SetError(ctx, EHIP_INVALID_ARGUMENT, "null decode operand");
   Plan plan;
   std::string err;
-  if (int rc = ehip::BuildSingleRowPlan(g, length, num_blocks, &plan, &err))
+  if (int rc = ehip::BuildSingleRowPlan(g, length, num_blocks, ctx->tune, &plan, &err))
     return SetError(ctx, rc, "%s", err.c_str());
   if (int rc = UploadPlan(ctx, g, std::move(plan), d_block_table)) return rc;
   return LaunchAttention(ctx, d_q, d_k_slab, d_v_slab, d_out);
@@ -613,7 +615,7 @@ int ehip_paged_decode_attention_f32_noalloc(ehip_ctx* ctx, const float* d_q,
   if ((length + block_size - 1) / block_size > num_blocks)
     return SetError(ctx, EHIP_INVALID_ARGUMENT, "ceil(length/bs) exceeds num_blocks=%lld",
                     static_cast<long long>(num_blocks));
-  const int32_t split_len = ehip::SingleRowSplitTokens(g, length);
+  const int32_t split_len = ehip::SingleRowSplitTokens(g, length, ctx->tune);
   const int64_t nsplit = (length + split_len - 1) / split_len;
   const int group = g.heads / g.kv_heads;
   const size_t need = ehip::StaticScratchNeed(nsplit, g.kv_heads, group, g.head_dim);
@@ -639,8 +641,8 @@ int ehip_paged_decode_attention_f32_noalloc(ehip_ctx* ctx, const float* d_q,
   p.bs = g.block_size;
   p.scale_log2 = g.scale * 1.4426950408889634f;
   EHIP_HIP(ctx, ehip::LaunchSingleRowStatic(p, ctx->device, static_cast<int32_t>(length),
-                                            split_len, static_cast<int32_t>(nsplit), &ctx->queue,
-                                            ctx->stream));
+                                            split_len, static_cast<int32_t>(nsplit), ctx->tune,
+                                            &ctx->queue, ctx->stream));
   return EHIP_OK;
 }
 
@@ -674,7 +676,7 @@ int ContiguousAttention(ehip_ctx* ctx, const float* d_q, const float* d_k, const
   const ehip_step_desc s{1, 0, &qlen, &l_dim, offsets, ids.data(), nullptr};
   Plan plan;
   std::string err;
-  if (int rc = ehip::BuildPlan(g, s, &plan, &err, 0, /*head_major=*/true))
+  if (int rc = ehip::BuildPlan(g, s, ctx->tune, &plan, &err, 0, /*head_major=*/true))
     return SetError(ctx, rc, "%s", err.c_str());
   if (int rc = UploadPlan(ctx, g, std::move(plan), nullptr, l_dim * d)) return rc;
   return LaunchAttention(ctx, d_q, d_k, d_v, d_out);
@@ -691,6 +693,50 @@ int ehip_decode_attention_f32(ehip_ctx* ctx, const float* d_q, const float* d_k,
                               float* d_out, int64_t heads, int64_t kv_heads, int64_t d,
                               int64_t l_dim, float scale) {
   return ContiguousAttention(ctx, d_q, d_k, d_v, d_out, 1, heads, kv_heads, d, l_dim, scale);
+}
+
+int ehip_prefill_attention_varlen_f32(ehip_ctx* ctx, const float* d_q,
+                                      const int32_t* h_cu_seqlens, int64_t num_seqs,
+                                      const float* const* h_k_seqs,
+                                      const float* const* h_v_seqs, const int64_t* h_l_dims,
+                                      float* d_out, int64_t heads, int64_t kv_heads, int64_t d,
+                                      float scale) {
+  if (int rc = CheckCtx(ctx)) return rc;
+  if (num_seqs < 0 || num_seqs > INT32_MAX)
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "num_seqs=%lld out of range",
+                    static_cast<long long>(num_seqs));
+  if (num_seqs == 0) return EHIP_OK;  // the reference's B == 0 no-op
+  if (!h_cu_seqlens || !h_k_seqs || !h_v_seqs || !h_l_dims || !d_q || !d_out)
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "null varlen operand");
+  if (heads < 1 || kv_heads < 1 || d < 1 || heads > INT32_MAX || kv_heads > INT32_MAX ||
+      d > INT32_MAX || heads % kv_heads != 0)
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "heads=%lld kv_heads=%lld d=%lld invalid",
+                    static_cast<long long>(heads), static_cast<long long>(kv_heads),
+                    static_cast<long long>(d));
+  if (h_cu_seqlens[0] != 0)
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "cu_seqlens[0]=%d must be 0", h_cu_seqlens[0]);
+  // All-or-nothing: every sequence is checked before the first launch.
+  for (int64_t b = 0; b < num_seqs; ++b) {
+    const int64_t T = int64_t{h_cu_seqlens[b + 1]} - h_cu_seqlens[b];
+    const int64_t L = h_l_dims[b];
+    if (T < 1 || L < T || L > (int64_t{1} << 30))
+      return SetError(ctx, EHIP_INVALID_ARGUMENT,
+                      "sequence %lld: need 1 <= T (%lld) <= L (%lld) <= 2^30",
+                      static_cast<long long>(b), static_cast<long long>(T),
+                      static_cast<long long>(L));
+    if (!h_k_seqs[b] || !h_v_seqs[b])
+      return SetError(ctx, EHIP_INVALID_ARGUMENT, "sequence %lld: null K/V",
+                      static_cast<long long>(b));
+  }
+  const int64_t row = heads * d;
+  for (int64_t b = 0; b < num_seqs; ++b) {
+    const int64_t r0 = h_cu_seqlens[b];
+    const int64_t T = int64_t{h_cu_seqlens[b + 1]} - r0;
+    if (int rc = ContiguousAttention(ctx, d_q + r0 * row, h_k_seqs[b], h_v_seqs[b],
+                                     d_out + r0 * row, T, heads, kv_heads, d, h_l_dims[b], scale))
+      return rc;
+  }
+  return EHIP_OK;
 }
 
 namespace {
@@ -733,7 +779,8 @@ int BatchedDecode(ehip_ctx* ctx, int kv_dtype, const float* d_q, const void* d_k
   ehip_step_desc s{static_cast<int32_t>(num_seqs), 0, qlens.data(), h_lengths, offsets.data(),
                    ids.data(), nullptr};
   Plan plan;
-  if (int rc = ehip::BuildPlan(g, s, &plan, &err)) return SetError(ctx, rc, "%s", err.c_str());
+  if (int rc = ehip::BuildPlan(g, s, ctx->tune, &plan, &err))
+    return SetError(ctx, rc, "%s", err.c_str());
   if (int rc = UploadPlan(ctx, g, std::move(plan), nullptr)) return rc;
   return LaunchAttention(ctx, d_q, d_k_slab, d_v_slab, d_out);
 }
@@ -781,7 +828,7 @@ int ehip_step_upload(ehip_ctx* ctx, const ehip_geometry* geom, const ehip_step_d
   if (!geom || !step) return SetError(ctx, EHIP_INVALID_ARGUMENT, "null geometry or step");
   Plan plan;
   std::string err;
-  if (int rc = ehip::BuildPlan(*geom, *step, &plan, &err, StepPrefillRows(*geom)))
+  if (int rc = ehip::BuildPlan(*geom, *step, ctx->tune, &plan, &err, StepPrefillRows(*geom)))
     return SetError(ctx, rc, "%s", err.c_str());
   return UploadPlan(ctx, *geom, std::move(plan), nullptr);
 }
@@ -872,11 +919,10 @@ int ehip_step_append_attention(ehip_ctx* ctx, const float* d_src_k, const float*
     return SetError(ctx, EHIP_UNIMPLEMENTED, "append needs the dense Hkv*bs*d block stride");
   // One launch (plus the split merge) when every row is a decode row on the
   // matrix-core kernel: the items ending at their rows' last keys append.
-  const char* env = std::getenv("EHIP_FUSED_APPEND");
-  const bool allowed = !(env && env[0] == '0');
-  if (allowed && plan.all_decode && !plan.items.empty() &&
+  if (ctx->tune.fused_append && plan.all_decode && !plan.items.empty() &&
       reinterpret_cast<uintptr_t>(d_src_k) % 8 == 0 && reinterpret_cast<uintptr_t>(d_src_v) % 8 == 0 &&
-      ehip::DecodeMfmaCovers(StepDecodeParams(ctx, d_q, d_k_slab, d_v_slab, d_out), g.kv_dtype))
+      ehip::DecodeMfmaCovers(StepDecodeParams(ctx, d_q, d_k_slab, d_v_slab, d_out), g.kv_dtype,
+                             ctx->tune))
     return LaunchAttention(ctx, d_q, d_k_slab, d_v_slab, d_out, nullptr, nullptr, d_src_k,
                            d_src_v);
   EHIP_HIP(ctx, ehip::LaunchKvScatter(d_src_k, d_src_v, ctx->d_slots,
@@ -970,7 +1016,7 @@ int ehip_plan_counts(const ehip_geometry* geom, const ehip_step_desc* step, int6
   if (!geom || !step) return EHIP_INVALID_ARGUMENT;
   Plan plan;
   std::string err;
-  if (int rc = ehip::BuildPlan(*geom, *step, &plan, &err)) return rc;
+  if (int rc = ehip::BuildPlan(*geom, *step, ehip::ReadTuning(), &plan, &err)) return rc;
   if (rows) *rows = static_cast<int64_t>(plan.rows.size());
   if (items) *items = static_cast<int64_t>(plan.items.size());
   if (partials) *partials = plan.partials;
@@ -985,7 +1031,7 @@ int ehip_plan_items(const ehip_geometry* geom, const ehip_step_desc* step, int32
   if (!geom || !step || !n || cap < 0 || (cap > 0 && !out)) return EHIP_INVALID_ARGUMENT;
   Plan plan;
   std::string err;
-  if (int rc = ehip::BuildPlan(*geom, *step, &plan, &err)) return rc;
+  if (int rc = ehip::BuildPlan(*geom, *step, ehip::ReadTuning(), &plan, &err)) return rc;
   *n = static_cast<int64_t>(plan.items.size());
   const int64_t m = std::min<int64_t>(cap, *n);
   for (int64_t i = 0; i < m; ++i) {
@@ -1009,7 +1055,9 @@ int ehip_plan_prefill_items(const ehip_geometry* geom, const ehip_step_desc* ste
   if (!geom || !step || !n || cap < 0 || (cap > 0 && !out)) return EHIP_INVALID_ARGUMENT;
   Plan plan;
   std::string err;
-  if (int rc = ehip::BuildPlan(*geom, *step, &plan, &err, StepPrefillRows(*geom))) return rc;
+  if (int rc = ehip::BuildPlan(*geom, *step, ehip::ReadTuning(), &plan, &err,
+                               StepPrefillRows(*geom)))
+    return rc;
   *n = static_cast<int64_t>(plan.prefill.size());
   const int64_t m = std::min<int64_t>(cap, *n);
   for (int64_t i = 0; i < m; ++i) {

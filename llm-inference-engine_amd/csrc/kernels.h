@@ -114,16 +114,17 @@ int PrefillRowsPerItem(int kv_dtype, int d, int group, int bs, int64_t slab_byte
 // item; picks the specialised (dtype, d, g) kernel or the generic one), then,
 // if any row was split, the merge of the split partials. The kernel boundary
 // between the two publishes the partials: no device-wide fences or counters.
-hipError_t LaunchDecode(const DecodeParams& p, int kv_dtype, QueueState* queue, hipStream_t stream);
+hipError_t LaunchDecode(const DecodeParams& p, int kv_dtype, const Tuning& tune, QueueState* queue,
+                        hipStream_t stream);
 
 // Whether the matrix-core decode kernel covers p for this KV type (bf16: d
 // 64/128, g 1/2/4/8; fp32: d 64, g 1/2/4/7/8; bs >= 16, 16-byte aligned
-// operands, not forced to the VALU kernel by EHIP_DECODE_KERNEL=valu). Only
-// it performs the fused append.
-bool DecodeMfmaCovers(const DecodeParams& p, int kv_dtype);
+// operands, not forced to the VALU kernel by Tuning::decode_valu). Only it
+// performs the fused append.
+bool DecodeMfmaCovers(const DecodeParams& p, int kv_dtype, const Tuning& tune);
 // bf16- or fp32-KV decode with QK^T on MFMA; returns false (nothing launched)
 // when DecodeMfmaCovers does not hold.
-bool LaunchDecodeMfma(const DecodeParams& p, int kv_dtype, QueueState* queue,
+bool LaunchDecodeMfma(const DecodeParams& p, int kv_dtype, const Tuning& tune, QueueState* queue,
                       hipStream_t stream, hipError_t* err);
 // INT8 or FP8 (E4M3) KV decode (paged_decode_q8.hip); false when the shape
 // is not covered.
@@ -158,7 +159,8 @@ hipError_t LaunchRopeKvAppend(float* q, const float* src_k, const float* src_v,
 // Allocation-free single-sequence decode (decode_static.hip): the one-row
 // plan and its split partials live in a per-device static scratch array of
 // kStaticScratchBytes. InitStaticScratch fetches the array's address on the
-// current device (once per device; called at context creation).
+// current device and creates the device's ordering event (once per device;
+// called at context creation).
 constexpr size_t kStaticScratchBytes = size_t{4} << 20;
 hipError_t InitStaticScratch(int device);
 // Scratch bytes a row cut into nsplit key splits needs (plan + partials).
@@ -166,11 +168,14 @@ size_t StaticScratchNeed(int64_t nsplit, int kv_heads, int group, int d);
 // Writes the plan of one row of `length` keys, cut into nsplit splits of
 // split_len keys, into the device's scratch and runs the fp32 decode (and the
 // split merge) on it; base carries everything else (q, slabs, table, out,
-// geometry). hipErrorNotInitialized if the device's address was not fetched,
-// hipErrorInvalidValue if the plan does not fit.
+// geometry). Eager calls on one device run in call order, whichever context
+// or stream makes them (each waits for the previous call's end). A call on a
+// capturing stream is not ordered that way. hipErrorNotInitialized if the
+// device's address was not fetched, hipErrorInvalidValue if the plan does not
+// fit.
 hipError_t LaunchSingleRowStatic(const DecodeParams& base, int device, int32_t length,
-                                 int32_t split_len, int32_t nsplit, QueueState* queue,
-                                 hipStream_t stream);
+                                 int32_t split_len, int32_t nsplit, const Tuning& tune,
+                                 QueueState* queue, hipStream_t stream);
 
 hipError_t LaunchFillNormal(void* dst, int64_t n, int dtype, float mean, float stddev,
                             uint64_t seed, hipStream_t stream);

@@ -586,10 +586,10 @@ hipError_t LaunchTyped(const DecodeParams& p, hipStream_t stream) {
 
 // Workgroup-per-unit decode for small fp32 steps; false when it does not
 // apply (too many units, a row longer than NW wavefronts' table slices, or a
-// shape without a specialised kernel). EHIP_DECODE_WG=0 turns it off.
-bool LaunchSmallStep(const DecodeParams& p, hipStream_t stream, hipError_t* err) {
-  const char* env = std::getenv("EHIP_DECODE_WG");
-  if (env && env[0] == '0') return false;
+// shape without a specialised kernel). Tuning::decode_wg = false turns it off.
+bool LaunchSmallStep(const DecodeParams& p, const Tuning& tune, hipStream_t stream,
+                     hipError_t* err) {
+  if (!tune.decode_wg) return false;
   const int64_t units = int64_t{p.n_rows} * p.kv_heads;
   if (units < 1 || units > kWgMaxUnits) return false;
   const bool aligned = (reinterpret_cast<uintptr_t>(p.k_slab) % 16 == 0) &&
@@ -625,8 +625,8 @@ bool LaunchSmallStep(const DecodeParams& p, hipStream_t stream, hipError_t* err)
   return false;
 }
 
-hipError_t LaunchSplits(const DecodeParams& p, int kv_dtype, QueueState* queue,
-                        hipStream_t stream) {
+hipError_t LaunchSplits(const DecodeParams& p, int kv_dtype, const Tuning& tune,
+                        QueueState* queue, hipStream_t stream) {
   if (ScaledKv(kv_dtype)) {
     // No VALU fallback for INT8/FP8: the plan validation admits only the
     // shapes the MFMA kernel covers.
@@ -634,10 +634,10 @@ hipError_t LaunchSplits(const DecodeParams& p, int kv_dtype, QueueState* queue,
     if (LaunchDecodeQ8(p, kv_dtype == EHIP_KV_FP8, stream, &err)) return err;
     return hipErrorInvalidValue;
   }
-  // The matrix-core kernel where it covers the shape (EHIP_DECODE_KERNEL=valu
+  // The matrix-core kernel where it covers the shape (Tuning::decode_valu
   // selects the all-VALU kernels).
   hipError_t err = hipSuccess;
-  if (LaunchDecodeMfma(p, kv_dtype, queue, stream, &err)) return err;
+  if (LaunchDecodeMfma(p, kv_dtype, tune, queue, stream, &err)) return err;
   // Only the MFMA kernel performs a fused append; the caller checked coverage.
   if (p.new_k != nullptr) return hipErrorInvalidValue;
   if (kv_dtype != EHIP_KV_BF16) return LaunchTyped<float>(p, stream);
@@ -646,17 +646,17 @@ hipError_t LaunchSplits(const DecodeParams& p, int kv_dtype, QueueState* queue,
 
 }  // namespace
 
-hipError_t LaunchDecode(const DecodeParams& p, int kv_dtype, QueueState* queue,
-                        hipStream_t stream) {
+hipError_t LaunchDecode(const DecodeParams& p, int kv_dtype, const Tuning& tune,
+                        QueueState* queue, hipStream_t stream) {
   // Small fp32 steps without prefill chunks: one workgroup per (row, kv head),
   // merged in LDS (the plan's split partials are not used). Not for a fused
   // append, which only the matrix-core kernel performs.
   if (kv_dtype == EHIP_KV_F32 && p.n_items > 0 && !p.has_prefill && p.new_k == nullptr) {
     hipError_t e = hipSuccess;
-    if (LaunchSmallStep(p, stream, &e)) return e;
+    if (LaunchSmallStep(p, tune, stream, &e)) return e;
   }
   // Split rows may come from prefill key splits alone (no decode items).
-  hipError_t e = p.n_items > 0 ? LaunchSplits(p, kv_dtype, queue, stream) : hipSuccess;
+  hipError_t e = p.n_items > 0 ? LaunchSplits(p, kv_dtype, tune, queue, stream) : hipSuccess;
   if (e != hipSuccess || p.n_merge == 0) return e;
   // Only the rows that were split: a step dominated by prefill-chunk rows
   // (which need no merge) launches no idle merge blocks.

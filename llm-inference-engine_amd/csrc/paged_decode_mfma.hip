@@ -564,24 +564,29 @@ int ResidentWaves() {
   return cus * per_cu;
 }
 
+// Launch knobs resolved from the context's tuning switches.
+struct Knobs {
+  bool wide;       // 32-key tiles (two MFMA halves)
+  bool deep;       // three tiles in registers
+  bool persist;    // persistent wavefronts drawing items from the queue
+  int32_t slots;   // cap on persistent wavefronts (0: the resident count)
+};
+
 template <auto K>
-void LaunchPersistent(const DecodeParams& p, hipStream_t stream, bool persist) {
+void LaunchPersistent(const DecodeParams& p, hipStream_t stream, const Knobs& kn) {
   int grid = p.n_items;
-  if (persist) {
-    // EHIP_DECODE_SLOTS caps the grid below the resident count (tests use it
-    // to make every wavefront take many items from the queue).
+  if (kn.persist) {
+    // Tuning::decode_slots caps the grid below the resident count (tests use
+    // it to make every wavefront take many items from the queue).
     int slots = ResidentWaves<K>();
-    if (const char* cap = std::getenv("EHIP_DECODE_SLOTS")) {
-      const long c = std::strtol(cap, nullptr, 10);
-      if (c > 0 && (slots <= 0 || c < slots)) slots = static_cast<int>(c);
-    }
+    if (kn.slots > 0 && (slots <= 0 || kn.slots < slots)) slots = kn.slots;
     if (slots > 0 && slots < grid) grid = slots;
   }
   hipLaunchKernelGGL(K, dim3(grid), dim3(64), 0, stream, p);
 }
 
 template <class KV, int D, int G, int RMAX, bool FUSE>
-void LaunchShape(const DecodeParams& p, hipStream_t stream, bool wide, bool deep, bool persist) {
+void LaunchShape(const DecodeParams& p, hipStream_t stream, const Knobs& kn) {
   // Two wavefronts per SIMD wherever the shape fits 256 registers without
   // spilling (the 16-virtual-head and triple-buffered 128-wide shapes do not).
   constexpr bool QL = D * G * RMAX >= 1024;
@@ -591,49 +596,49 @@ void LaunchShape(const DecodeParams& p, hipStream_t stream, bool wide, bool deep
     // fp32 slabs: the default shape only (32-key tiles, two buffers). Three
     // buffers for small steps (all items in one round of resident wavefronts,
     // one per SIMD) measured the same on C2: 23.5 against 23.6 us per layer.
-    LaunchPersistent<DecodeMfma<KV, D, G, RMAX, 2, 2, QL, OCC, FUSE>>(p, stream, persist);
+    LaunchPersistent<DecodeMfma<KV, D, G, RMAX, 2, 2, QL, OCC, FUSE>>(p, stream, kn);
   } else {
-    if (wide && deep)
-      LaunchPersistent<DecodeMfma<KV, D, G, RMAX, 2, 3, QL, OCC3, FUSE>>(p, stream, persist);
-    else if (wide)
-      LaunchPersistent<DecodeMfma<KV, D, G, RMAX, 2, 2, QL, OCC, FUSE>>(p, stream, persist);
-    else if (deep)
-      LaunchPersistent<DecodeMfma<KV, D, G, RMAX, 1, 3, QL, OCC3, FUSE>>(p, stream, persist);
+    if (kn.wide && kn.deep)
+      LaunchPersistent<DecodeMfma<KV, D, G, RMAX, 2, 3, QL, OCC3, FUSE>>(p, stream, kn);
+    else if (kn.wide)
+      LaunchPersistent<DecodeMfma<KV, D, G, RMAX, 2, 2, QL, OCC, FUSE>>(p, stream, kn);
+    else if (kn.deep)
+      LaunchPersistent<DecodeMfma<KV, D, G, RMAX, 1, 3, QL, OCC3, FUSE>>(p, stream, kn);
     else
-      LaunchPersistent<DecodeMfma<KV, D, G, RMAX, 1, 2, QL, OCC, FUSE>>(p, stream, persist);
+      LaunchPersistent<DecodeMfma<KV, D, G, RMAX, 1, 2, QL, OCC, FUSE>>(p, stream, kn);
   }
 }
 
 template <class KV, int D, int G, int RMAX>
-void LaunchShape(const DecodeParams& p, hipStream_t stream, bool wide, bool deep, bool persist) {
+void LaunchShape(const DecodeParams& p, hipStream_t stream, const Knobs& kn) {
   if (p.new_k != nullptr)
-    LaunchShape<KV, D, G, RMAX, true>(p, stream, wide, deep, persist);
+    LaunchShape<KV, D, G, RMAX, true>(p, stream, kn);
   else
-    LaunchShape<KV, D, G, RMAX, false>(p, stream, wide, deep, persist);
+    LaunchShape<KV, D, G, RMAX, false>(p, stream, kn);
 }
 
 // Rows per item the kernel is instantiated for: 1, 2, or 4 for groups of three
 // or four sharers (the plan caps a group at 16 / g rows, so 4 only for g <= 4).
 template <class KV, int D, int G>
-bool LaunchRows(const DecodeParams& p, hipStream_t stream, bool wide, bool deep, bool persist) {
+bool LaunchRows(const DecodeParams& p, hipStream_t stream, const Knobs& kn) {
   const int rows = p.n_joint > 0 ? p.joint_rows : 1;
   if constexpr (G <= 4) {
     if (rows > 2) {
-      LaunchShape<KV, D, G, 4>(p, stream, wide, deep, persist);
+      LaunchShape<KV, D, G, 4>(p, stream, kn);
       return true;
     }
   }
   if (rows > 2) return false;
   if (rows == 2)
-    LaunchShape<KV, D, G, 2>(p, stream, wide, deep, persist);
+    LaunchShape<KV, D, G, 2>(p, stream, kn);
   else
-    LaunchShape<KV, D, G, 1>(p, stream, wide, deep, persist);
+    LaunchShape<KV, D, G, 1>(p, stream, kn);
   return true;
 }
 
 }  // namespace
 
-bool DecodeMfmaCovers(const DecodeParams& p, int kv_dtype) {
+bool DecodeMfmaCovers(const DecodeParams& p, int kv_dtype, const Tuning& tune) {
   const bool f32 = kv_dtype == EHIP_KV_F32;
   if (!f32 && kv_dtype != EHIP_KV_BF16) return false;
   // 16-byte K/V vectors: bf16 rows start on 8-element, fp32 on 4-element
@@ -650,31 +655,24 @@ bool DecodeMfmaCovers(const DecodeParams& p, int kv_dtype) {
                                           p.group == 7 || p.group == 8))
                          : ((p.d == 64 || p.d == 128) &&
                             (p.group == 1 || p.group == 2 || p.group == 4 || p.group == 8));
-  const char* pick = std::getenv("EHIP_DECODE_KERNEL");
-  const bool valu = pick && std::strcmp(pick, "valu") == 0;
-  return aligned && shape && p.bs >= 16 && !valu;
+  return aligned && shape && p.bs >= 16 && !tune.decode_valu;
 }
 
-bool LaunchDecodeMfma(const DecodeParams& params, int kv_dtype, QueueState* queue,
-                      hipStream_t stream, hipError_t* err) {
+bool LaunchDecodeMfma(const DecodeParams& params, int kv_dtype, const Tuning& tune,
+                      QueueState* queue, hipStream_t stream, hipError_t* err) {
   DecodeParams p = params;
   p.queue = queue->d_counters;
   p.queue_done = queue->d_done;
-  if (!DecodeMfmaCovers(p, kv_dtype)) return false;
+  if (!DecodeMfmaCovers(p, kv_dtype, tune)) return false;
   // 32-token tiles (two MFMA halves per tile, double-buffered) measured best
-  // on C4; EHIP_DECODE_TILE=16 selects one half per tile (fewer registers).
-  const char* tile = std::getenv("EHIP_DECODE_TILE");
-  const bool wide = !(tile && std::strcmp(tile, "16") == 0);
-  // EHIP_DECODE_BUFS=3: three tiles in registers (two in flight).
-  const char* bufs = std::getenv("EHIP_DECODE_BUFS");
-  const bool deep = bufs && std::strcmp(bufs, "3") == 0;
-  // EHIP_DECODE_PERSIST=0: one workgroup per item (the hardware dispatcher
+  // on C4; decode_tile16 selects one half per tile (fewer registers),
+  // decode_bufs3 three tiles in registers (two in flight), and
+  // decode_persist = false one workgroup per item (the hardware dispatcher
   // hands out the items instead of the queue).
-  const char* pers = std::getenv("EHIP_DECODE_PERSIST");
-  const bool persist = !(pers && std::strcmp(pers, "0") == 0);
+  const Knobs kn{!tune.decode_tile16, tune.decode_bufs3, tune.decode_persist, tune.decode_slots};
   bool ok = false;
 #define EHIP_MFMA_CASE(KV, DD, GG) \
-  else if (p.d == DD && p.group == GG) ok = LaunchRows<KV, DD, GG>(p, stream, wide, deep, persist);
+  else if (p.d == DD && p.group == GG) ok = LaunchRows<KV, DD, GG>(p, stream, kn);
   if (kv_dtype == EHIP_KV_F32) {
     if (false) {
     }

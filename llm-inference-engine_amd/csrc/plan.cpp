@@ -5,6 +5,7 @@
 #include <cstdio>
 #include <climits>
 #include <cstdlib>
+#include <cstring>
 #include <utility>
 
 namespace ehip {
@@ -36,6 +37,36 @@ int Fail(std::string* err, int code, const char* fmt, long long a = 0, long long
 int64_t RoundUp(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
 }  // namespace
+
+Tuning ReadTuning() {
+  Tuning t;
+  auto flag = [](const char* name, char off) {
+    const char* v = std::getenv(name);
+    return !(v && v[0] == off);
+  };
+  if (const char* v = std::getenv("EHIP_SPLIT_TOKENS")) {
+    const long x = std::strtol(v, nullptr, 10);
+    if (x > 0) t.split_tokens = static_cast<int32_t>(std::min<long>(x, INT32_MAX / 2));
+  }
+  if (const char* v = std::getenv("EHIP_TARGET_ITEMS")) {
+    const long x = std::strtol(v, nullptr, 10);
+    if (x > 0) t.target_items = x;
+  }
+  t.joint = flag("EHIP_NO_JOINT", '1');
+  t.prefill = flag("EHIP_PREFILL", '0');
+  if (const char* v = std::getenv("EHIP_PREFILL_SPLIT")) t.prefill_split = std::strtod(v, nullptr);
+  if (const char* v = std::getenv("EHIP_DECODE_KERNEL")) t.decode_valu = std::strcmp(v, "valu") == 0;
+  if (const char* v = std::getenv("EHIP_DECODE_TILE")) t.decode_tile16 = std::strcmp(v, "16") == 0;
+  if (const char* v = std::getenv("EHIP_DECODE_BUFS")) t.decode_bufs3 = std::strcmp(v, "3") == 0;
+  t.decode_persist = flag("EHIP_DECODE_PERSIST", '0');
+  if (const char* v = std::getenv("EHIP_DECODE_SLOTS")) {
+    const long x = std::strtol(v, nullptr, 10);
+    if (x > 0) t.decode_slots = static_cast<int32_t>(std::min<long>(x, INT32_MAX));
+  }
+  t.decode_wg = flag("EHIP_DECODE_WG", '0');
+  t.fused_append = flag("EHIP_FUSED_APPEND", '0');
+  return t;
+}
 
 int64_t BlockStride(const ehip_geometry& g) {
   return g.block_stride != 0 ? g.block_stride
@@ -92,17 +123,12 @@ int32_t MaxSplitTokens(const ehip_geometry& g) {
   return (ScaledKv(g.kv_dtype) ? 128 : 64) * g.block_size;
 }
 
-int32_t ChooseSplitTokens(const ehip_geometry& g, int64_t unit_tokens) {
+int32_t ChooseSplitTokens(const ehip_geometry& g, int64_t unit_tokens, const Tuning& tune) {
   const int32_t max_split = MaxSplitTokens(g);
-  if (const char* env = std::getenv("EHIP_SPLIT_TOKENS")) {
-    const long v = std::strtol(env, nullptr, 10);
-    if (v > 0) return static_cast<int32_t>(std::min<int64_t>(RoundUp(v, kTile), max_split));
-  }
+  if (tune.split_tokens > 0)
+    return static_cast<int32_t>(std::min<int64_t>(RoundUp(tune.split_tokens, kTile), max_split));
   int64_t target = ScaledKv(g.kv_dtype) ? kTargetItems / 2 : kTargetItems;
-  if (const char* env = std::getenv("EHIP_TARGET_ITEMS")) {
-    const long v = std::strtol(env, nullptr, 10);
-    if (v > 0) target = v;
-  }
+  if (tune.target_items > 0) target = tune.target_items;
   int64_t s = (unit_tokens + target - 1) / target;
   s = RoundUp(std::max<int64_t>(s, unit_tokens < kSmallStepUnits ? kTile : kMinSplit), kTile);
   return static_cast<int32_t>(std::min<int64_t>(s, max_split));
@@ -117,8 +143,8 @@ int32_t RowSplitTokens(const ehip_geometry& g, int32_t base, int32_t len) {
   return sl;
 }
 
-int32_t SingleRowSplitTokens(const ehip_geometry& g, int64_t length) {
-  const int32_t base = ChooseSplitTokens(g, length * g.kv_heads);
+int32_t SingleRowSplitTokens(const ehip_geometry& g, int64_t length, const Tuning& tune) {
+  const int32_t base = ChooseSplitTokens(g, length * g.kv_heads, tune);
   return RowSplitTokens(g, base, static_cast<int32_t>(length));
 }
 
@@ -126,9 +152,13 @@ namespace {
 
 constexpr int32_t kMinJointTokens = 128;  // shorter shared runs are not worth a joint pass
 
-// Full leading blocks two rows read from the same physical block ids.
+// Full leading blocks two rows read from the same physical block ids, short
+// of each row's last key: a row whose length is a multiple of bs keeps its
+// last block for a range of its own, so every row has a non-joint range
+// ending at its last key (the item that appends the row's new token in the
+// fused append + attention launch).
 int32_t SharedFullBlocks(const Plan& plan, const RowDesc& a, const RowDesc& b, int32_t bs) {
-  const int32_t limit = std::min(a.length, b.length) / bs;
+  const int32_t limit = (std::min(a.length, b.length) - 1) / bs;
   if (a.table_off == b.table_off) return limit;  // rows of one sequence
   const int32_t* ta = plan.table_ids.data() + a.table_off;
   const int32_t* tb = plan.table_ids.data() + b.table_off;
@@ -150,7 +180,7 @@ struct KeyRange {
 // (joint ranges first), assigns partial slots and orders the work longest
 // first.
 // skip[r] > 0: row r is served by the prefill kernel in skip[r] key splits.
-void FinishPlan(const ehip_geometry& g, Plan* plan, bool allow_joint,
+void FinishPlan(const ehip_geometry& g, const Tuning& tune, Plan* plan, bool allow_joint,
                 const std::vector<int32_t>* skip = nullptr) {
   const int32_t bs = g.block_size;
   const size_t n = plan->rows.size();
@@ -158,7 +188,7 @@ void FinishPlan(const ehip_geometry& g, Plan* plan, bool allow_joint,
   int64_t units = 0;
   for (size_t r = 0; r < n; ++r)
     if (!skipped(r)) units += int64_t{plan->rows[r].length} * g.kv_heads;
-  const int32_t base = ChooseSplitTokens(g, units);
+  const int32_t base = ChooseSplitTokens(g, units, tune);
   plan->split_tokens = base;
   plan->groups.clear();
   plan->group_start.assign(1, 0);
@@ -167,9 +197,8 @@ void FinishPlan(const ehip_geometry& g, Plan* plan, bool allow_joint,
   plan->shared_tokens = 0;
 
   std::vector<int32_t> joint_len(n, 0);
-  const char* no_joint = std::getenv("EHIP_NO_JOINT");
   const int cap = JointRowsCap(g.heads / g.kv_heads);
-  if (allow_joint && cap >= 2 && n >= 2 && !(no_joint && no_joint[0] == '1')) {
+  if (allow_joint && tune.joint && cap >= 2 && n >= 2) {
     std::vector<int32_t> order;
     order.reserve(n);
     for (size_t i = 0; i < n; ++i)
@@ -366,8 +395,8 @@ int BuildQ8Groups(const ehip_geometry& g, Plan* plan, std::string* err) {
 
 }  // namespace
 
-int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::string* err,
-              int prefill_rows, bool head_major) {
+int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, const Tuning& tune, Plan* plan,
+              std::string* err, int prefill_rows, bool head_major) {
   ehip_geometry checked = g;
   if (head_major) {
     if (g.block_stride != int64_t{g.block_size} * g.head_dim)
@@ -388,7 +417,7 @@ int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::
   plan->max_length = 0;
   const int32_t B = s.num_seqs;
   if (B == 0) {
-    FinishPlan(g, plan, false);
+    FinishPlan(g, tune, plan, false);
     return EHIP_OK;
   }
   if (!s.h_query_lens || !s.h_context_lens || !s.h_table_offsets || !s.h_table_ids)
@@ -449,8 +478,7 @@ int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::
 
   // Chunks big enough for the MFMA prefill kernel leave the decode partition.
   std::vector<int32_t> skip(plan->rows.size(), 0);
-  const char* pf = std::getenv("EHIP_PREFILL");
-  if (prefill_rows > 0 && !(pf && pf[0] == '0')) {
+  if (prefill_rows > 0 && tune.prefill) {
     struct Block { int32_t b, q0, keys; };
     std::vector<Block> blocks;
     std::vector<int32_t> row_base(B + 1, 0);
@@ -469,14 +497,12 @@ int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::
     // Key splits: a block with more than twice the per-workgroup share of
     // the step's tiles is cut into splits of about that share, so the last
     // query blocks of a long chunk do not walk all their keys alone
-    // (EHIP_PREFILL_SPLIT=0 keeps every block whole).
-    // EHIP_PREFILL_SPLIT: 0 keeps every block whole; a number x > 0 splits
-    // blocks longer than x shares (default 2: on C3, x = 1 measured 58.9 us
-    // per layer against 45.7 us, as the extra partials and merge cost more
-    // than the shorter critical path saves; the C5 re-prefill is the same
-    // either way).
-    const char* ps = std::getenv("EHIP_PREFILL_SPLIT");
-    const double split_mult = ps ? std::strtod(ps, nullptr) : 2.0;
+    // Tuning::prefill_split: 0 keeps every block whole; a number x > 0
+    // splits blocks longer than x shares (default 2: on C3, x = 1 measured
+    // 58.9 us per layer against 45.7 us, as the extra partials and merge cost
+    // more than the shorter critical path saves; the C5 re-prefill is the
+    // same either way).
+    const double split_mult = tune.prefill_split;
     const bool split_ok = split_mult > 0.0;
     const int64_t share = std::max<int64_t>(
         kMinPrefillSplitTiles,
@@ -525,7 +551,7 @@ int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::
                                             s.h_table_offsets[bl.b], pc.kb, pc.ke});
     }
   }
-  FinishPlan(g, plan, true, &skip);
+  FinishPlan(g, tune, plan, true, &skip);
   if (plan->partials < 0)
     return Fail(err, EHIP_UNIMPLEMENTED, "a row needs %lld or more key splits",
                 int64_t{1} << kSplitBits);
@@ -533,8 +559,8 @@ int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::
   return EHIP_OK;
 }
 
-int BuildSingleRowPlan(const ehip_geometry& g, int64_t length, int64_t num_blocks, Plan* plan,
-                       std::string* err) {
+int BuildSingleRowPlan(const ehip_geometry& g, int64_t length, int64_t num_blocks,
+                       const Tuning& tune, Plan* plan, std::string* err) {
   if (int rc = ValidateGeometry(g, err)) return rc;
   if (length < 1 || length > (int64_t{1} << 30))
     return Fail(err, EHIP_INVALID_ARGUMENT, "length=%lld out of range", length);
@@ -545,7 +571,7 @@ int BuildSingleRowPlan(const ehip_geometry& g, int64_t length, int64_t num_block
   plan->max_length = length;
   plan->table_ids.clear();
   plan->slots.clear();
-  FinishPlan(g, plan, false);
+  FinishPlan(g, tune, plan, false);
   return EHIP_OK;
 }
 

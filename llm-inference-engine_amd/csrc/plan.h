@@ -28,6 +28,30 @@
 
 namespace ehip {
 
+// Tuning switches (EHIP_* environment variables), read once when a context is
+// created and carried by it, as the reference memoizes its dispatch choice in
+// a function-local static (src/kernels/paged_attention.cpp:93, :125): the
+// planner and the launch paths never read the environment. The context-free
+// planning entry points (ehip_plan_counts / _items / _prefill_items) read it
+// per call.
+struct Tuning {
+  int32_t split_tokens = 0;    // EHIP_SPLIT_TOKENS: fixed base split length (0: per step)
+  int64_t target_items = 0;    // EHIP_TARGET_ITEMS: decode work-item target (0: default)
+  bool joint = true;           // EHIP_NO_JOINT=1: no joint items over shared prefixes
+  bool prefill = true;         // EHIP_PREFILL=0: chunk rows stay on the decode kernels
+  double prefill_split = 2.0;  // EHIP_PREFILL_SPLIT: key-split threshold in shares (0: none)
+  bool decode_valu = false;    // EHIP_DECODE_KERNEL=valu: all-VALU decode kernels
+  bool decode_tile16 = false;  // EHIP_DECODE_TILE=16: one 16-key MFMA half per tile
+  bool decode_bufs3 = false;   // EHIP_DECODE_BUFS=3: three tiles in registers
+  bool decode_persist = true;  // EHIP_DECODE_PERSIST=0: one workgroup per work item
+  int32_t decode_slots = 0;    // EHIP_DECODE_SLOTS: cap on persistent wavefronts (0: none)
+  bool decode_wg = true;       // EHIP_DECODE_WG=0: no workgroup-per-row small fp32 steps
+  bool fused_append = true;    // EHIP_FUSED_APPEND=0: append and attention in two launches
+};
+
+// The switches as the environment sets them now.
+Tuning ReadTuning();
+
 // One query row: its sequence's table slice and the keys it attends (a decode
 // row attends the whole post-append context; row t of a prefill chunk
 // attends P + t + 1 keys). Its splits own partial slots
@@ -150,8 +174,8 @@ inline bool ScaledKv(int kv_dtype) { return kv_dtype == EHIP_KV_INT8 || kv_dtype
 
 // Base split length: sized so that the step yields enough work items to fill
 // the chip (a few per SIMD) without drowning in partial-merge traffic.
-// EHIP_SPLIT_TOKENS overrides it (rounded to a multiple of 64).
-int32_t ChooseSplitTokens(const ehip_geometry& g, int64_t unit_tokens);
+// Tuning::split_tokens overrides it (rounded to a multiple of 64).
+int32_t ChooseSplitTokens(const ehip_geometry& g, int64_t unit_tokens, const Tuning& tune);
 // Longest key range of one decode work item.
 int32_t MaxSplitTokens(const ehip_geometry& g);
 // Split length of one row of `len` keys given the step's base length: the
@@ -160,13 +184,13 @@ int32_t MaxSplitTokens(const ehip_geometry& g);
 int32_t RowSplitTokens(const ehip_geometry& g, int32_t base, int32_t len);
 // The split length BuildSingleRowPlan gives a row of `length` keys (the
 // single-sequence decode's partition), without building the plan.
-int32_t SingleRowSplitTokens(const ehip_geometry& g, int64_t length);
+int32_t SingleRowSplitTokens(const ehip_geometry& g, int64_t length, const Tuning& tune);
 
 // Validates the step (lengths, CSR offsets, every table id and slot in range)
 // and builds the plan. Chunks of at least kMinPrefillRows rows go to the MFMA
 // prefill kernel when it covers the geometry (prefill_rows > 0: query rows
-// per prefill work item; EHIP_PREFILL=0
-// keeps every row on the decode kernels); their rows get nsplit = 0.
+// per prefill work item; Tuning::prefill = false keeps every row on the
+// decode kernels); their rows get nsplit = 0.
 constexpr int32_t kMinPrefillRows = 16;
 constexpr int32_t kPrefillTile = 32;       // keys per prefill tile
 constexpr int32_t kPrefillSlots = 512;     // workgroups resident at once (2 per CU)
@@ -174,12 +198,12 @@ constexpr int32_t kMinPrefillSplitTiles = 8;
 // head_major: K/V are one contiguous [Hkv, L, d] cache read through an
 // identity table (block_stride = bs * d, kv heads L * d apart), so the slab
 // rule block_stride >= Hkv * bs * d does not apply.
-int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, Plan* plan, std::string* err,
-              int prefill_rows = 0, bool head_major = false);
+int BuildPlan(const ehip_geometry& g, const ehip_step_desc& s, const Tuning& tune, Plan* plan,
+              std::string* err, int prefill_rows = 0, bool head_major = false);
 
 // Plan for one row reading a device-resident table (single-sequence paged
 // decode): one row of `length` keys, table offset 0.
-int BuildSingleRowPlan(const ehip_geometry& g, int64_t length, int64_t num_blocks, Plan* plan,
-                       std::string* err);
+int BuildSingleRowPlan(const ehip_geometry& g, int64_t length, int64_t num_blocks,
+                       const Tuning& tune, Plan* plan, std::string* err);
 
 }  // namespace ehip

@@ -91,6 +91,8 @@ def lib():
                                            _i64, C.c_float],
             "ehip_decode_attention_f32": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
                                           C.c_float],
+            "ehip_prefill_attention_varlen_f32": [_vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp,
+                                                  _i64, _i64, _i64, C.c_float],
             "ehip_paged_decode_attention_f32_noalloc": [_vp, _vp, _vp, _vp, _vp, _i64, _i64,
                                                         _i64, _i64, _i64, _i64, _i64, _i64,
                                                         C.c_float, _vp],
@@ -300,6 +302,19 @@ class Context:
         return lib().ehip_paged_decode_attention_f32(
             self.h, q.ptr, k_slab.ptr, v_slab.ptr, table.ptr, num_blocks, length, heads,
             kv_heads, d, bs, block_stride, slab_blocks, scale, out.ptr)
+
+    def prefill_attention_varlen(self, q, cu_seqlens, k_seqs, v_seqs, l_dims, out, heads,
+                                 kv_heads, d, scale) -> int:
+        """q/out device buffers [sum T, H, d]; cu_seqlens, l_dims host arrays;
+        k_seqs / v_seqs lists of device buffers ([Hkv, L_b, d] each)."""
+        cu = np.ascontiguousarray(cu_seqlens, np.int32)
+        ls = np.ascontiguousarray(l_dims, np.int64)
+        ks = (_vp * max(1, len(k_seqs)))(*[k.ptr for k in k_seqs])
+        vs = (_vp * max(1, len(v_seqs)))(*[v.ptr for v in v_seqs])
+        return lib().ehip_prefill_attention_varlen_f32(
+            self.h, q.ptr if q else None, cu.ctypes.data, len(k_seqs), C.cast(ks, _vp),
+            C.cast(vs, _vp), ls.ctypes.data, out.ptr if out else None, heads, kv_heads, d,
+            scale)
 
     def paged_decode_batched(self, q, k_slab, v_slab, tables, lengths, heads, kv_heads, d, bs,
                              block_stride, slab_blocks, scale, out, bf16=False) -> int:

@@ -42,3 +42,22 @@ def gctx(ehip_mod):
     ctx = ehip_mod.Context(0)
     yield ctx
     ctx.close()
+
+
+@pytest.fixture
+def tctx(ehip_mod, monkeypatch):
+    """A context reads the EHIP_* tuning switches once, when it is created.
+    tctx(NAME=value, ...) sets switches (undone after the test) and returns a
+    new context that carries them; every context made is closed at teardown."""
+    made = []
+
+    def make(**env):
+        for k, v in env.items():
+            monkeypatch.setenv(k, str(v))
+        ctx = ehip_mod.Context(0)
+        made.append(ctx)
+        return ctx
+
+    yield make
+    for ctx in made:
+        ctx.close()

@@ -27,20 +27,30 @@ def log(msg):
     print(f"[fullsize] {msg}", flush=True)
 
 
-def run_layer(gctx, ehip_mod, w, q, k32, v32, kn, vn):
+def run_layer(gctx, ehip_mod, w, q, k32, v32, kn, vn, fused=False):
     """Upload the bf16 slabs and the step's rows, append + attend one layer on
-    the GPU; return the output and the post-append slabs."""
+    the GPU; return the output and the post-append slabs. fused: through
+    ehip_step_append_attention (the benched call: for an all-decode step one
+    launch of the persistent decode kernel with the append folded in, its
+    wavefronts taking items by ticket once the plan has more items than
+    resident wavefronts), else the append launch, then the attention call."""
     from ehip import workloads
     g = ehip_mod.geometry(w.heads, w.kv_heads, w.head_dim, w.block_size, w.kv_dtype,
                           w.pool_blocks, w.scale)
     st = ehip_mod.StepArrays(w.query_lens, w.context_lens, w.tables, w.slot_mapping)
     assert gctx.step_upload(g, st) == 0, gctx.last_error()
+    rows, items, partials = gctx.step_info()
+    log(f"{'fused' if fused else 'two launches'}: rows={rows} work items={items} "
+        f"partials={partials}")
     dk = gctx.to_device(workloads.to_bf16_bits(k32))
     dv = gctx.to_device(workloads.to_bf16_bits(v32))
     dq, dkn, dvn = gctx.to_device(q), gctx.to_device(kn), gctx.to_device(vn)
     out = gctx.alloc(q.nbytes)
-    assert gctx.step_kv_append(dkn, dvn, dk, dv) == 0, gctx.last_error()
-    assert gctx.step_attention(dq, dk, dv, out) == 0, gctx.last_error()
+    if fused:
+        assert gctx.step_append_attention(dkn, dvn, dq, dk, dv, out) == 0, gctx.last_error()
+    else:
+        assert gctx.step_kv_append(dkn, dvn, dk, dv) == 0, gctx.last_error()
+        assert gctx.step_attention(dq, dk, dv, out) == 0, gctx.last_error()
     gctx.sync()
     got = out.download(np.float32, q.shape)
     shape = k32.shape
@@ -101,7 +111,12 @@ def check(w, got, ref_r, ref32):
 def test_benched_layer_at_full_size(gctx, ehip_mod, orc, config):
     """Layer 0 of the config's benched step as drawn: C4 (256 sequences,
     sum L ~ 609k, pair-shared prefixes), C5 (8 x 32769 + 24 rows, 64q/8kv),
-    C3 (4 causal chunks + 60 decodes)."""
+    C3 (4 causal chunks + 60 decodes), each through the two-launch path and
+    through the fused call the bench times. C4 (5,640 work items) and C5
+    (2,960) have more items than the 2,048 resident decode wavefronts, so the
+    fused kernel runs with its item queue active; C3's mixed step takes the
+    two launches either way. Both runs leave the same slabs (the oracle's
+    append, bit for bit); each run's outputs meet the bars."""
     from ehip import workloads
     w = workloads.CONFIGS[config]()
     log(f"{config}: B={w.num_seqs} rows={w.rows} sumL={int(w.context_lens.sum())} "
@@ -110,8 +125,15 @@ def test_benched_layer_at_full_size(gctx, ehip_mod, orc, config):
     q = w.q(0)
     kn, vn = w.new_kv(0)
     got, kd, vd = run_layer(gctx, ehip_mod, w, q, k32, v32, kn, vn)
+    got_f, kd_f, vd_f = run_layer(gctx, ehip_mod, w, q, k32, v32, kn, vn, fused=True)
+    assert np.array_equal(kd_f, kd) and np.array_equal(vd_f, vd), \
+        "the fused append left different slabs"
+    del kd_f, vd_f
     ref_r, ref32 = references(orc, w, q, k32, v32, kn, vn, kd, vd)
+    log("two launches:")
     check(w, got, ref_r, ref32)
+    log("fused:")
+    check(w, got_f, ref_r, ref32)
 
 
 @pytest.mark.parametrize("heads", [64, 32])

@@ -85,9 +85,12 @@ def test_fused_append_decode_step(gctx, ehip_mod, orc, H, Hkv, d, bs, kv):
     assert rel_norm(fused, separate) <= 1e-5
 
 
-def test_fused_append_with_joint_items(gctx, ehip_mod, orc):
+@pytest.mark.parametrize("slots", [None, "5", "64"])
+def test_fused_append_with_joint_items(gctx, ehip_mod, orc, tctx, slots):
     """The C4 shape with pair-shared prefixes (joint items never cover a row's
-    last key: only the rows' own items append)."""
+    last key: only the rows' own items append), on a grid covering every item
+    and on 5 or 64 persistent wavefronts that take the items, joint and
+    appending ones alike, by ticket: bit-identical to the full grid."""
     from ehip import workloads
     w = workloads.c4(num_seqs=24, share_frac=0.3)
     rc, rows, items, partials, split, joint, shared = ehip_mod.plan_counts(
@@ -97,10 +100,37 @@ def test_fused_append_with_joint_items(gctx, ehip_mod, orc):
     assert rc == 0 and joint > 0
     fused, ref = _run(gctx, ehip_mod, orc, w, fused=True, seed=41)
     _check(fused, ref)
+    if slots is not None:
+        assert int(slots) < items
+        queued, _ = _run(tctx(EHIP_DECODE_SLOTS=slots), ehip_mod, orc, w, fused=True, seed=41)
+        assert np.array_equal(queued.view(np.uint32), fused.view(np.uint32))
+
+
+@pytest.mark.parametrize("slots", ["7", "64"])
+@pytest.mark.parametrize("H,Hkv,d,bs,kv", [(32, 8, 128, 16, "bf16"), (64, 8, 128, 16, "bf16"),
+                                           (16, 2, 64, 64, "bf16"), (14, 2, 64, 16, "f32")])
+def test_fused_append_items_taken_by_ticket(gctx, ehip_mod, orc, tctx, H, Hkv, d, bs, kv, slots):
+    """The fused launch with the decode grid capped below the plan's items, so
+    its persistent wavefronts take items (the appending ones among them) from
+    their sub-queues by ticket, as at the benched sizes (C4: 5,640 items, C5:
+    2,960, on 2,048 resident wavefronts). Slabs bit-exact against the oracle's
+    append, outputs to the decode bar, and bit-identical to the launch whose
+    grid covers every item (an item computes the same sums whichever
+    wavefront takes it)."""
+    lens = [1, 2, 17, 33, 129, 1025, 1026, 2049, 4000, 64, 65, 8193]
+    dtype = ehip_mod.KV_F32 if kv == "f32" else ehip_mod.KV_BF16
+    w = _workload(ehip_mod, H, Hkv, d, bs, lens, seed=H + d + bs + 1, dtype=dtype)
+    full, ref = _run(gctx, ehip_mod, orc, w, fused=True)
+    ctx = tctx(EHIP_DECODE_SLOTS=slots)
+    queued, ref_q = _run(ctx, ehip_mod, orc, w, fused=True)
+    _, items, _ = ctx.step_info()
+    assert int(slots) < items, items
+    _check(queued, ref_q)
+    assert np.array_equal(queued.view(np.uint32), full.view(np.uint32))
 
 
 @pytest.mark.parametrize("case", ["fp32", "chunk", "valu"])
-def test_append_attention_falls_back_to_two_launches(gctx, ehip_mod, orc, case, monkeypatch):
+def test_append_attention_falls_back_to_two_launches(gctx, ehip_mod, orc, case, tctx):
     """fp32 slabs of head_dim 128 (the fp32 matrix-core kernel covers 64), a
     step with a prefill chunk, and the VALU decode kernel take the append
     launch then the attention launch, with the same results."""
@@ -109,7 +139,7 @@ def test_append_attention_falls_back_to_two_launches(gctx, ehip_mod, orc, case, 
     elif case == "chunk":
         w = _workload(ehip_mod, 32, 8, 128, 16, [300, 40, 1000], seed=6, qlens=[1, 20, 1])
     else:
-        monkeypatch.setenv("EHIP_DECODE_KERNEL", "valu")
+        gctx = tctx(EHIP_DECODE_KERNEL="valu")
         w = _workload(ehip_mod, 32, 8, 128, 16, [300, 40, 1000], seed=7)
     got, ref = _run(gctx, ehip_mod, orc, w, fused=True)
     rows = np.repeat(w.query_lens, w.query_lens) == 1

@@ -95,10 +95,10 @@ def run_case(gctx, ehip_mod, orc, w, layers, int8=False):
                 x.free()
 
 
-def test_graph_replay_bf16_persistent_decode(gctx, ehip_mod, orc, monkeypatch):
+def test_graph_replay_bf16_persistent_decode(ehip_mod, orc, tctx):
     """bf16 C4 shape at 24 sequences (joint items), the persistent decode
     kernel on 5 wavefronts so each drains the queue, three layers."""
-    monkeypatch.setenv("EHIP_DECODE_SLOTS", "5")
+    gctx = tctx(EHIP_DECODE_SLOTS="5")
     from ehip import workloads
     run_case(gctx, ehip_mod, orc, workloads.c4(num_seqs=24, share_frac=0.3), layers=3)
 

@@ -141,11 +141,11 @@ def test_int8_steps_bit_exact_append_and_attention(gctx, ehip_mod, orc, H, Hkv, 
 
 @pytest.mark.parametrize("fmt", FORMATS)
 @pytest.mark.parametrize("split", ["64", "128", "2048"])
-def test_int8_long_rows_split_and_merged(gctx, ehip_mod, orc, monkeypatch, split, fmt):
+def test_int8_long_rows_split_and_merged(ehip_mod, orc, tctx, split, fmt):
     """Decode rows long enough to be split into several key ranges (the split
     partials go through the shared merge); 2048-key ranges span 128 blocks, the
     longest an INT8 work item takes."""
-    monkeypatch.setenv("EHIP_SPLIT_TOKENS", split)
+    gctx = tctx(EHIP_SPLIT_TOKENS=split)
     rng = np.random.default_rng(7)
     H, Hkv, d, bs = 32, 8, 128, 16
     lens = [1500, 2049, 17, 640, 4100]
@@ -185,7 +185,7 @@ def shared_pair_tables(rng, pairs, bs, extra=7, groups=()):
 
 @pytest.mark.parametrize("fmt", FORMATS)
 @pytest.mark.parametrize("H,Hkv,d", [(32, 8, 128), (64, 8, 128), (8, 2, 64), (8, 8, 128)])
-def test_int8_shared_prefix_joint_items(gctx, ehip_mod, orc, monkeypatch, H, Hkv, d, fmt):
+def test_int8_shared_prefix_joint_items(ehip_mod, orc, tctx, H, Hkv, d, fmt):
     """Pair-shared prefix blocks (the C4 construction's sharing) and, for
     g <= 4, a fork of four rows through the INT8 kernel: with joint work items
     (one pass over the shared blocks, row r's g heads in MFMA rows
@@ -198,7 +198,7 @@ def test_int8_shared_prefix_joint_items(gctx, ehip_mod, orc, monkeypatch, H, Hkv
     quads = [(20, [500, 700, 330, 900])] if H // Hkv <= 4 else []
     outs = []
     for flag in ("0", "1"):
-        monkeypatch.setenv("EHIP_NO_JOINT", flag)
+        gctx = tctx(EHIP_NO_JOINT=flag)
         rng = np.random.default_rng(H + d)
         tabs, pool = shared_pair_tables(rng, pairs, bs, groups=quads)
         lens = [L for la, lb, _ in pairs for L in (la, lb)] + [L for _, ls in quads for L in ls]

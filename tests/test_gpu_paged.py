@@ -297,10 +297,10 @@ def test_batched_decode_heterogeneous_lengths(gctx, orc, bs):
 
 @pytest.mark.parametrize("kernel", ["mfma", "valu"])
 @pytest.mark.parametrize("bs", [16, 64, 8])
-def test_batched_decode_bf16_kv(gctx, orc, kernel, bs, monkeypatch):
+def test_batched_decode_bf16_kv(orc, kernel, bs, tctx):
     # Both bf16 kernels (QK^T on MFMA, or all-VALU); bs = 8 always takes the
     # VALU kernel.
-    monkeypatch.setenv("EHIP_DECODE_KERNEL", kernel)
+    gctx = tctx(EHIP_DECODE_KERNEL=kernel)
     rng = np.random.default_rng(77 + bs)
     lengths = list(rng.integers(1, 3000, 24))
     H, Hkv, d = 32, 8, 128
@@ -339,11 +339,10 @@ def test_bf16_decode_gqa_sweep(gctx, orc, H, Hkv, d):
 
 
 @pytest.mark.parametrize("split", ["64", "128", "512", "1024"])
-def test_split_count_independence(gctx, orc, split, monkeypatch):
+def test_split_count_independence(orc, split, tctx):
     # The merged result must not depend on how the keys were split (the
     # split-KV path: the workgroup-per-row kernel for small steps is off).
-    monkeypatch.setenv("EHIP_SPLIT_TOKENS", split)
-    monkeypatch.setenv("EHIP_DECODE_WG", "0")
+    gctx = tctx(EHIP_SPLIT_TOKENS=split, EHIP_DECODE_WG="0")
     rng = np.random.default_rng(3)
     lengths = [4000, 17, 1025, 2048, 64]
     H, Hkv, d, bs = 32, 8, 128, 16
@@ -359,12 +358,11 @@ def test_split_count_independence(gctx, orc, split, monkeypatch):
 
 
 @pytest.mark.parametrize("H", [32, 64])
-def test_merge_of_wide_groups(gctx, orc, H, monkeypatch):
+def test_merge_of_wide_groups(orc, H, tctx):
     # One kv head for all H query heads, and a row cut into the most splits a
     # row may have (64): 64 * 32 = 2048 (max, sum) pairs still fit the merge
     # workgroup's LDS; 64 * 64 = 4096 take the one-wavefront sequential merge.
-    monkeypatch.setenv("EHIP_SPLIT_TOKENS", "128")
-    monkeypatch.setenv("EHIP_DECODE_WG", "0")
+    gctx = tctx(EHIP_SPLIT_TOKENS="128", EHIP_DECODE_WG="0")
     rng = np.random.default_rng(H)
     lengths = [8192, 300, 1, 2500]
     Hkv, d, bs = 1, 64, 16
@@ -380,13 +378,12 @@ def test_merge_of_wide_groups(gctx, orc, H, monkeypatch):
 
 
 @pytest.mark.parametrize("split", ["128", "256"])
-def test_large_merge_four_elements_per_thread(gctx, orc, split, monkeypatch):
+def test_large_merge_four_elements_per_thread(orc, split, tctx):
     # At least 32 split rows x 8 kv heads x 1024 elements = 2^18: the merge
     # takes four elements per thread; the 2049- and 4000-key rows have more
     # than the 16 splits whose partials are loaded before the weights are
     # formed.
-    monkeypatch.setenv("EHIP_SPLIT_TOKENS", split)
-    monkeypatch.setenv("EHIP_DECODE_WG", "0")
+    gctx = tctx(EHIP_SPLIT_TOKENS=split, EHIP_DECODE_WG="0")
     rng = np.random.default_rng(int(split))
     lengths = [int(x) for x in rng.integers(300, 900, size=40)] + [1, 2049, 4000]
     H, Hkv, d, bs = 64, 8, 128, 16
@@ -452,10 +449,10 @@ def run_step(gctx, ehip_mod, orc, w, seed, layers=1):
 
 
 @pytest.mark.parametrize("wg", ["1", "0"])
-def test_step_c2_ragged_decode(gctx, ehip_mod, orc, wg, monkeypatch):
+def test_step_c2_ragged_decode(ehip_mod, orc, wg, tctx):
     """C2 shape (B=32, L~U[64,2048]+1, fp32 pool 1.25x need): two layers of
     append + attention through the per-step descriptor."""
-    monkeypatch.setenv("EHIP_DECODE_WG", wg)  # workgroup per (row, kv head), or split-KV
+    gctx = tctx(EHIP_DECODE_WG=wg)  # workgroup per (row, kv head), or split-KV
     from ehip import workloads
     w = workloads.c2()
     for got, ref, *_ in run_step(gctx, ehip_mod, orc, w, 7, layers=2):
@@ -489,11 +486,11 @@ def fp32_reference(orc, w, kpool, vpool, q, cu):
 
 
 @pytest.mark.parametrize("prefill", ["1", "0"])
-def test_step_c3_mixed_prefill_and_decode(gctx, ehip_mod, orc, prefill, monkeypatch):
+def test_step_c3_mixed_prefill_and_decode(ehip_mod, orc, prefill, tctx):
     """C3 composition scaled down (2 causal chunks + 12 decodes, bf16 KV): the
     chunks run on the MFMA prefill kernel (or, with EHIP_PREFILL=0, on the
     decode kernels), the decodes on the decode kernel."""
-    monkeypatch.setenv("EHIP_PREFILL", prefill)
+    gctx = tctx(EHIP_PREFILL=prefill)
     from ehip import workloads
     w = workloads.c3()
     keep = [0, 1] + list(range(4, 16))
@@ -543,14 +540,14 @@ def test_prefill_chunk_shapes(gctx, ehip_mod, orc, H, Hkv, T, P):
 
 @pytest.mark.parametrize("H,Hkv", [(32, 8), (64, 8)])
 @pytest.mark.parametrize("T,P", [(512, 1024), (700, 0), (96, 4000)])
-def test_prefill_key_splits(gctx, ehip_mod, orc, H, Hkv, T, P, monkeypatch):
+def test_prefill_key_splits(ehip_mod, orc, H, Hkv, T, P, tctx):
     """Prefill blocks cut into key splits (the long ones relative to the
     step's prefill work) and merged by the split merge: against the
     references, and against the same step with every block whole."""
     w = chunk_workload(H, Hkv, T, P, extra_decodes=3, seed=T + P + H + 7)
     outs, partials = [], []
     for flag in ("1", "0"):
-        monkeypatch.setenv("EHIP_PREFILL_SPLIT", flag)
+        gctx = tctx(EHIP_PREFILL_SPLIT=flag)
         (got, ref, kpool, vpool, q, cu), = run_step(gctx, ehip_mod, orc, w, 41)
         partials.append(gctx.step_info()[2])
         if flag == "1":
@@ -565,7 +562,7 @@ def test_prefill_key_splits(gctx, ehip_mod, orc, H, Hkv, T, P, monkeypatch):
 
 
 @pytest.mark.parametrize("slots", ["1", "7", "40", "64", "300"])
-def test_persistent_decode_queue(gctx, ehip_mod, orc, slots, monkeypatch):
+def test_persistent_decode_queue(ehip_mod, orc, slots, tctx):
     """The MFMA decode kernel's wavefronts take their later items from the
     launch's sub-queue counters (up to 32, one per wavefront index modulo
     their count). With the grid capped to a few wavefronts every one of them
@@ -575,10 +572,9 @@ def test_persistent_decode_queue(gctx, ehip_mod, orc, slots, monkeypatch):
     and within the bars of the oracle."""
     from ehip import workloads
     w = workloads.c4(num_seqs=24, share_frac=0.3)
-    monkeypatch.setenv("EHIP_DECODE_PERSIST", "0")
+    gctx = tctx(EHIP_DECODE_PERSIST="0")
     base = run_step(gctx, ehip_mod, orc, w, 17, layers=3)
-    monkeypatch.setenv("EHIP_DECODE_PERSIST", "1")
-    monkeypatch.setenv("EHIP_DECODE_SLOTS", slots)
+    gctx = tctx(EHIP_DECODE_PERSIST="1", EHIP_DECODE_SLOTS=slots)
     got = run_step(gctx, ehip_mod, orc, w, 17, layers=3)
     for (g, ref, *_), (b, *_) in zip(got, base):
         assert np.array_equal(g.view(np.uint32), b.view(np.uint32))
@@ -586,10 +582,10 @@ def test_persistent_decode_queue(gctx, ehip_mod, orc, slots, monkeypatch):
 
 
 @pytest.mark.parametrize("kernel", ["mfma", "valu"])
-def test_step_c4_shape_with_shared_prefix_blocks(gctx, ehip_mod, orc, kernel, monkeypatch):
+def test_step_c4_shape_with_shared_prefix_blocks(ehip_mod, orc, kernel, tctx):
     """C4 construction (log-uniform lengths, pair-shared prefix blocks, bf16)
     at 24 sequences."""
-    monkeypatch.setenv("EHIP_DECODE_KERNEL", kernel)
+    gctx = tctx(EHIP_DECODE_KERNEL=kernel)
     from ehip import workloads
     w = workloads.c4(num_seqs=24, share_frac=0.3)
     assert (w.refcount == 2).any()
@@ -598,11 +594,11 @@ def test_step_c4_shape_with_shared_prefix_blocks(gctx, ehip_mod, orc, kernel, mo
 
 
 @pytest.mark.parametrize("joint", ["1", "0"])
-def test_step_shared_prefix_fp32_valu(gctx, ehip_mod, orc, joint, monkeypatch):
-    monkeypatch.setenv("EHIP_DECODE_WG", "0")  # joint items live in the split-KV path
+def test_step_shared_prefix_fp32_valu(ehip_mod, orc, joint, tctx):
     """Pair-shared prefix blocks through the fp32 VALU kernel, with and without
     joint work items (joint items are processed row by row there)."""
-    monkeypatch.setenv("EHIP_NO_JOINT", "0" if joint == "1" else "1")
+    # Joint items live in the split-KV path (no workgroup-per-row kernel).
+    gctx = tctx(EHIP_DECODE_WG="0", EHIP_NO_JOINT="0" if joint == "1" else "1")
     from ehip import workloads
     w = workloads.c4(num_seqs=12, share_frac=0.4)
     w.kv_dtype = ehip_mod.KV_F32
@@ -610,14 +606,14 @@ def test_step_shared_prefix_fp32_valu(gctx, ehip_mod, orc, joint, monkeypatch):
     check_fp32(got, ref)
 
 
-def test_step_joint_items_match_plain_partition(gctx, ehip_mod, orc, monkeypatch):
+def test_step_joint_items_match_plain_partition(ehip_mod, orc, tctx):
     """Joint items (one pass over shared blocks for two rows) against the plain
     per-row partition on the same bf16 step."""
     from ehip import workloads
     w = workloads.c4(num_seqs=16, share_frac=0.4)
     outs = []
     for flag in ("0", "1"):
-        monkeypatch.setenv("EHIP_NO_JOINT", flag)
+        gctx = tctx(EHIP_NO_JOINT=flag)
         (got, ref, *_), = run_step(gctx, ehip_mod, orc, w, 21)
         check_fp32(got, ref)
         outs.append(got)
@@ -695,15 +691,16 @@ FORK_GROUPS = [(20, [700, 530, 900, 400, 655]),  # five sharers of 320 keys
                                         (32, 8, 128, "valu"), (14, 2, 64, "f32"),
                                         (8, 8, 64, "f32"), (14, 2, 64, "f32valu"),
                                         (16, 2, 128, "f32")])
-def test_decode_fork_groups_beyond_pairs(gctx, ehip_mod, orc, H, Hkv, d, kv, monkeypatch):
+def test_decode_fork_groups_beyond_pairs(ehip_mod, orc, H, Hkv, d, kv, tctx):
     """Joint work items of up to min(4, 16 / g) rows over fork groups' shared
     prefixes (groups of five and three sharers, a pair, unshared rows),
     through the MFMA kernel (its virtual heads: g per row, up to 16; bf16, and
     fp32 at head_dim 64), the bf16 and fp32 VALU kernels (rows one after the
     other; fp32 head_dim 128 always): against the oracle, and against the
     plain per-row partition."""
-    monkeypatch.setenv("EHIP_DECODE_KERNEL", "valu" if kv.endswith("valu") else "mfma")
-    monkeypatch.setenv("EHIP_DECODE_WG", "0")  # joint items live in the split-KV path
+    kernel = "valu" if kv.endswith("valu") else "mfma"
+    # Joint items live in the split-KV path (no workgroup-per-row kernel).
+    gctx = tctx(EHIP_DECODE_KERNEL=kernel, EHIP_DECODE_WG="0")
     rng = np.random.default_rng(H + 3 * d)
     bs = 16
     q, ks, vs, tables, lengths = fork_group_case(rng, FORK_GROUPS, Hkv, d, bs, H)
@@ -725,7 +722,7 @@ def test_decode_fork_groups_beyond_pairs(gctx, ehip_mod, orc, H, Hkv, d, kv, mon
     qd = gctx.to_device(q)
     outs = []
     for flag in ("0", "1"):
-        monkeypatch.setenv("EHIP_NO_JOINT", flag)
+        gctx = tctx(EHIP_NO_JOINT=flag)
         out = gctx.alloc(q.nbytes)
         assert gctx.paged_decode_batched(qd, kd, vd, tables, lengths, H, Hkv, d, bs, 0,
                                          ks.shape[0], scale_for(d), out, bf16=bf16) == 0, \
@@ -743,7 +740,7 @@ def test_decode_fork_groups_beyond_pairs(gctx, ehip_mod, orc, H, Hkv, d, kv, mon
                                      (8, 1, 128), (24, 3, 64)])
 @pytest.mark.parametrize("lens", [[1, 17, 33, 1500, 513], [1024, 1536, 1], [32, 64, 96],
                                   [4000, 17]])
-def test_small_step_workgroup_per_row(gctx, orc, H, Hkv, d, lens, monkeypatch):
+def test_small_step_workgroup_per_row(orc, H, Hkv, d, lens, tctx):
     """Small fp32 steps with short rows take one workgroup per (row, kv head),
     its wavefronts splitting the row's tiles and merging in LDS (a 4000-key
     row goes to the split-KV path instead): against the oracle, and against
@@ -754,7 +751,7 @@ def test_small_step_workgroup_per_row(gctx, orc, H, Hkv, d, lens, monkeypatch):
     ref = orc.paged_decode_batched(q, ks, vs, tables, lens, H, Hkv, d, bs, scale_for(d))
     outs = []
     for wg in ("1", "0"):
-        monkeypatch.setenv("EHIP_DECODE_WG", wg)
+        gctx = tctx(EHIP_DECODE_WG=wg)
         out = gctx.alloc(q.nbytes)
         assert gctx.paged_decode_batched(gctx.to_device(q), gctx.to_device(ks),
                                          gctx.to_device(vs), tables, lens, H, Hkv, d, bs, 0,
@@ -766,14 +763,14 @@ def test_small_step_workgroup_per_row(gctx, orc, H, Hkv, d, lens, monkeypatch):
 
 
 @pytest.mark.parametrize("kernel", ["mfma", "valu"])
-def test_c2_layer_fp32_kernels(gctx, ehip_mod, orc, kernel, monkeypatch):
+def test_c2_layer_fp32_kernels(ehip_mod, orc, kernel, tctx):
     """One layer of the C2 step as drawn (32 rows, 14q/2kv, d = 64, fp32 slabs,
     split-KV) on the fp32 matrix-core kernel (Q and K in three bf16 parts,
     six products per chunk) and on the all-VALU kernel: both meet the fp32
     bar (1e-4 relative per output vector, the reference allclose) against the
     oracle on the same post-append cache."""
     from ehip import workloads
-    monkeypatch.setenv("EHIP_DECODE_KERNEL", kernel)
+    gctx = tctx(EHIP_DECODE_KERNEL=kernel)
     w = workloads.c2()
     H, Hkv, d, bs = w.heads, w.kv_heads, w.head_dim, w.block_size
     kpool, vpool = seeded_pool(orc, w, 301)

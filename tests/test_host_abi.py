@@ -173,7 +173,8 @@ def test_c4_sharing_and_byte_accounting():
 def joint_expectation(w, split, bs=16, min_joint=128):
     """Mirror of the planner's pairing for tables that share only as forked
     prefixes: rows ordered by (first block id, table, index), adjacent rows
-    sharing >= min_joint keys of full leading blocks are paired."""
+    sharing >= min_joint keys of full leading blocks, short of either row's
+    last key, are paired."""
     n = len(w.context_lens)
     first = [int(t[0]) for t in w.tables]
     order = sorted(range(n), key=lambda r: (first[r], r))
@@ -182,7 +183,7 @@ def joint_expectation(w, split, bs=16, min_joint=128):
     i = 0
     while i + 1 < n:
         a, b = order[i], order[i + 1]
-        L = min(int(w.context_lens[a]), int(w.context_lens[b])) // bs
+        L = (min(int(w.context_lens[a]), int(w.context_lens[b])) - 1) // bs
         c = 0
         while c < L and w.tables[a][c] == w.tables[b][c]:
             c += 1
@@ -244,13 +245,15 @@ def test_plan_chunk_rows_group_up(ehip_mod, monkeypatch):
     monkeypatch.setenv("EHIP_SPLIT_TOKENS", "128")
     # A chunk of 300 rows over 100 cached keys: row t attends 101 + t keys;
     # consecutive rows of one sequence read the same table, so they form
-    # joint groups of four (g = 4: 16 / 4 virtual-head rows).
+    # joint groups of four (g = 4: 16 / 4 virtual-head rows). A joint prefix
+    # is whole blocks short of every member's last key.
     st = simple_step(ehip_mod, [400], qlens=np.array([300], np.int32))
     rc, rows, items, partials, split, joint, shared = ehip_mod.plan_counts(geom(ehip_mod), st,
                                                                            joint=True)
     assert rc == 0 and rows == 300
     lens = [101 + t for t in range(300)]
-    groups = greedy_groups(list(range(300)), lambda a, b: min(lens[a], lens[b]) // 16, cap=4)
+    groups = greedy_groups(list(range(300)), lambda a, b: (min(lens[a], lens[b]) - 1) // 16,
+                           cap=4)
     assert max(len(m) for m, _ in groups) == 4
     joint_len = [0] * 300
     exp_joint = exp_shared = 0
@@ -461,3 +464,29 @@ def test_plan_prefill_split_ids_cover_recorded_splits(ehip_mod, H, Hkv, T, P):
     # requested pieces of 10 tiles make 63 pieces.
     if (H, Hkv, T, P) == (8, 2, 16, 20000):
         assert {p[3] for v in blocks.values() for p in v} == {63}
+
+
+@pytest.mark.parametrize("L", [256, 257, 512])
+def test_plan_every_row_keeps_a_range_ending_at_its_last_key(ehip_mod, L):
+    """Rows whose tables agree on every block (a length that is a multiple of
+    the block size included) still get a range of their own that ends at
+    their last key: the item that appends the row's new token in the fused
+    append + attention launch. The joint prefix stops a block short of it."""
+    bs = 16
+    n = (L + bs - 1) // bs
+    shared = np.arange(n, dtype=np.int32)
+    # Two decode rows over one table (as a fork that has not diverged yet),
+    # and an unrelated third row.
+    other = np.arange(n, 2 * n, dtype=np.int32)
+    st = ehip_mod.StepArrays(np.ones(3, np.int32), np.array([L, L, L], np.int64),
+                             [shared, shared, other], np.arange(3, dtype=np.int64))
+    g = geom(ehip_mod, slab_blocks=2 * n + 4)
+    rc, items = ehip_mod.plan_items(g, st)
+    assert rc == 0
+    assert (items[:, 1] >= 0).any(), "the shared prefix should make joint items"
+    check_partition(items, [L, L, L], 8)
+    for r in range(3):
+        own = items[(items[:, 0] == r) & (items[:, 1] < 0)]
+        assert (own[:, 5] == L).sum() == 8, f"row {r}: no range of its own ending at {L}"
+    joint = items[items[:, 1] >= 0]
+    assert joint[:, 5].max() <= (L - 1) // bs * bs

@@ -75,3 +75,43 @@ def test_noalloc_decode_rejects_rows_beyond_its_scratch(gctx, ehip_mod):
     assert "scratch" in gctx.last_error()
     for b in (dq, dk, dv, out, dt):
         b.free()
+
+
+def test_noalloc_two_contexts_share_the_scratch_in_call_order(gctx, ehip_mod, orc):
+    """Two contexts on one device (two streams) issue _noalloc calls of
+    different lengths in turn, with no synchronisation between the calls: the
+    device's one scratch array serves them all, and each call waits for the
+    previous call's end whichever context made it. Every output equals the
+    allocating entry point's on the same inputs. Every table holds valid ids
+    for the longest row, so each call reads in bounds whatever its plan."""
+    L_ = ehip_mod.lib()
+    H, Hkv, d, bs = 32, 8, 128, 16
+    lengths = [20000, 3000, 20000, 700]
+    nblk = (max(lengths) + bs - 1) // bs
+    other = ehip_mod.Context(0)
+    try:
+        cases, want = [], []
+        for i, L in enumerate(lengths):
+            q, ks, vs, table = _case(orc, 900 + 10 * i, L, H, Hkv, d, bs)
+            table = np.concatenate([table, np.zeros(nblk - len(table), np.int32)])
+            want.append(_call(gctx, ehip_mod, L_.ehip_paged_decode_attention_f32, q, ks, vs,
+                              table, L, H, Hkv, d, bs))
+            bufs = [gctx.to_device(x) for x in (q, ks, vs, table)]
+            cases.append((L, ks.shape[0], bufs, gctx.alloc(q.nbytes), q.shape))
+        for i, (L, slab_blocks, (dq, dk, dv, dt), out, _) in enumerate(cases):
+            ctx = gctx if i % 2 == 0 else other
+            print(f"[noalloc] context {i % 2}: L={L}", flush=True)
+            rc = L_.ehip_paged_decode_attention_f32_noalloc(
+                ctx.h, dq.ptr, dk.ptr, dv.ptr, dt.ptr, nblk, L, H, Hkv, d, bs, Hkv * bs * d,
+                slab_blocks, C.c_float(scale_for(d)), out.ptr)
+            assert rc == 0, ctx.last_error()
+        gctx.sync()
+        other.sync()
+        for (L, _, bufs, out, shape), ref in zip(cases, want):
+            got = out.download(np.float32, shape)
+            assert rel_norm(got, ref) <= FP32_REL, L
+            assert allclose_ref(got, ref, 1e-4, 1e-5)
+            for b in bufs + [out]:
+                b.free()
+    finally:
+        other.close()
