@@ -84,6 +84,11 @@ __device__ __forceinline__ float RowSum(float x) {
   return RowReduce(x, [](float a, float b) { return a + b; });
 }
 
+__device__ __forceinline__ float Max4(float a, float b, float c, float d) {
+  return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b),
+                                       __builtin_elementwise_maximum(c, d));
+}
+
 template <int D>
 struct PrefillSmem {
   static constexpr int ROW = D * 2;  // bytes per K or V row (16-byte chunks XOR-swizzled)
@@ -105,6 +110,12 @@ template <int D, int G, int OCC>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(OCC == 3 ? 3 : 1)))
 void PrefillMfmaBf16(PrefillParams p) {
   constexpr int HB = kHeadsPerWave;   // heads (accumulator blocks) per wavefront
+  // Fold the softmax's scale and reference into the QK^T MFMA (one FMA less
+  // per score), with IEEE maxima and pairwise row sums. Measured on MI355X:
+  // at three workgroups per CU (issue-bound, the C5 re-prefill) 330 -> 323 us
+  // per layer; at two (bound by the longest blocks' tile latency, C3's
+  // chunks) 37.0 -> 39.0 us, so only there.
+  constexpr bool kFold = OCC == 3;
   constexpr int NHG = G / HB;         // head groups
   constexpr int RG = kWaves / NHG;    // 16-row groups per workgroup
   constexpr int M = 16 * RG;          // query rows per workgroup
@@ -142,7 +153,9 @@ void PrefillMfmaBf16(PrefillParams p) {
   const int wend = min(P + r0 + qnw, key1);  // keys this wavefront's rows attend here
 
   // Q^T as MFMA B operands (bf16, round-to-nearest-even), in registers:
-  // lane l holds Q[row r0 + l%16][c*32 + 8*kq .. +8] for each of its heads.
+  // lane l holds Q[row r0 + l%16][c*32 + 8*kq .. +8] for each of its heads
+  // (with kFold scaled by scale * log2(e) before the rounding, so the MFMA
+  // leaves scores in the log2 units of the softmax).
   bf16x8_t qreg[HB][NC];
   {
     const int qr = r0 + min(n, max(qnw, 1) - 1);
@@ -157,7 +170,7 @@ void PrefillMfmaBf16(PrefillParams p) {
         const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
         bf16x8_t qv;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) qv[i] = static_cast<__bf16>(x[i]);
+        for (int i = 0; i < 8; ++i) qv[i] = static_cast<__bf16>(kFold ? x[i] * p.scale_log2 : x[i]);
         qreg[hh][c] = qv;
       }
     }
@@ -244,7 +257,6 @@ void PrefillMfmaBf16(PrefillParams p) {
     for (int nb = 0; nb < NB; ++nb) o[hh][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
   const int qpos = P + r0 + n;  // this lane's query position (S^T layout)
-  const float sl2 = p.scale_log2;          // scores -> log2 domain
 
   const int ntiles = (key1 - key0 + kTile - 1) / kTile;
   auto compute_tile = [&](int tile, const unsigned char* buf) __attribute__((always_inline)) {
@@ -260,10 +272,16 @@ void PrefillMfmaBf16(PrefillParams p) {
       const int lim = min(qpos, key1 - 1);
 
       // S^T for all heads: each K operand feeds HB MFMAs, each Q operand two
-      // (the tile's halves).
+      // (the tile's halves). With kFold the accumulators start at -ref and Q
+      // carries scale * log2(e), so they finish as the exponents of the
+      // probabilities (score * scale * log2(e) - ref); otherwise one FMA per
+      // score forms them.
       f32x4_t s[HB][2];
 #pragma unroll
-      for (int hh = 0; hh < HB; ++hh) s[hh][0] = s[hh][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      for (int hh = 0; hh < HB; ++hh) {
+        const float nr = !kFold || ref[hh] == -INFINITY ? 0.f : -ref[hh];
+        s[hh][0] = s[hh][1] = f32x4_t{nr, nr, nr, nr};
+      }
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         bf16x8_t ka[2];
@@ -279,8 +297,8 @@ void PrefillMfmaBf16(PrefillParams p) {
             s[hh][h2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[h2], qv, s[hh][h2], 0, 0, 0);
         }
       }
-      // s[hh][h2][i] = score(token k0 + 16*h2 + 4*kq + i, query row n), raw
-      // q.k. Only tiles reaching the diagonal mask anything.
+      // s[hh][h2][i] = exponent of token k0 + 16*h2 + 4*kq + i for query row
+      // n. Only tiles reaching the diagonal mask anything.
       if (diag) {
 #pragma unroll
         for (int hh = 0; hh < HB; ++hh)
@@ -302,14 +320,42 @@ void PrefillMfmaBf16(PrefillParams p) {
 #pragma unroll
       for (int hh = 0; hh < HB; ++hh) {
         const float r = ref[hh] == -INFINITY ? 0.f : ref[hh];
-        float tm = -INFINITY;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          t[hh][j] = fmaf(s[hh][j >> 2][j & 3], sl2, -r);  // masked scores stay -inf
-          tm = fmaxf(tm, t[hh][j]);
+        for (int j = 0; j < 8; ++j)  // masked scores stay -inf
+          t[hh][j] = kFold ? s[hh][j >> 2][j & 3] : fmaf(s[hh][j >> 2][j & 3], p.scale_log2, -r);
+        if constexpr (kFold) {
+          // The MFMA results are not known to be canonical, so the IEEE
+          // maximum (NaN-propagating: v_maximum3_f32 on gfx950) replaces
+          // fmaxf, which would canonicalise each one first.
+          const float m0 = Max4(t[hh][0], t[hh][1], t[hh][2], t[hh][3]);
+          const float m1 = Max4(t[hh][4], t[hh][5], t[hh][6], t[hh][7]);
+          tmax[hh] = __builtin_elementwise_maximum(m0, m1);
+        } else {
+          float tm = -INFINITY;  // FMA results: fmaxf chains become v_max3_f32
+#pragma unroll
+          for (int j = 0; j < 8; ++j) tm = fmaxf(tm, t[hh][j]);
+          tmax[hh] = tm;
         }
-        tmax[hh] = tm;
-        need = need || ref[hh] == -INFINITY || tm > kRefSlack;
+        need = need || ref[hh] == -INFINITY || tmax[hh] > kRefSlack;
+      }
+      // The tile's V operands (two transposed reads per 16-column block) of
+      // the first two blocks are requested ahead of the PV MFMAs, and each
+      // PV step requests the block two ahead. With kFold the first two go
+      // out here, before the softmax; on the two-per-CU instance issuing
+      // them before the rescale branch measured slower (C3 37.0 -> 39.1 us),
+      // so there they go out after it.
+      const int vr = 4 * kq + (n >> 2);
+      const unsigned char* vl = vb + (n & 1) * 8;
+      auto vread = [&](int nb) __attribute__((always_inline)) {
+        const int vo = SwzOff(vr, 2 * nb + ((n & 3) >> 1));
+        const bf16x4_t v0 = TransposedRead(vl + vo);
+        const bf16x4_t v1 = TransposedRead(vl + 16 * SM::ROW + vo);
+        return __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+      };
+      bf16x8_t vop[NB];
+      if constexpr (kFold) {
+        vop[0] = vread(0);
+        vop[1] = vread(1);
       }
       if (__any(need)) {
         bool moved = false;
@@ -341,14 +387,23 @@ void PrefillMfmaBf16(PrefillParams p) {
       bf16x8_t pa[HB];
 #pragma unroll
       for (int hh = 0; hh < HB; ++hh) {
-        float ps = 0.f;
+        float pv[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const float pv = Exp2(t[hh][j]);
-          ps += pv;
-          pa[hh][j] = static_cast<__bf16>(pv);
+          pv[j] = Exp2(t[hh][j]);
+          pa[hh][j] = static_cast<__bf16>(pv[j]);
         }
-        l[hh] += ps;  // lane-partial over this lane's tokens
+        // Lane-partial row sum over this lane's tokens: pairwise with kFold
+        // (three dependent adds deep), in token order otherwise (measured
+        // faster on the latency-bound two-per-CU instance).
+        float ps = 0.f;
+        if constexpr (kFold) {
+          ps = ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) ps += pv[j];
+        }
+        l[hh] += ps;
       }
       // O^T += V^T P^T: each V operand read once, HB MFMAs. The A operand of
       // lane (n, kq) is V[token][16nb + n] over tokens 4kq..4kq+3 and
@@ -357,17 +412,16 @@ void PrefillMfmaBf16(PrefillParams p) {
       // 4kq + s/4 (+16), columns 16nb + 4(s%4) .. +3, and lane n receives
       // column 16nb + n of the group's 4 rows. The B operand is P^T, which is
       // this lane's P values as they are (row n, the same 8 tokens).
-      const int vr = 4 * kq + (n >> 2);
-      const unsigned char* vl = vb + (n & 1) * 8;
+      if constexpr (!kFold) {
+        vop[0] = vread(0);
+        vop[1] = vread(1);
+      }
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
-        const int vo = SwzOff(vr, 2 * nb + ((n & 3) >> 1));
-        const bf16x4_t v0 = TransposedRead(vl + vo);
-        const bf16x4_t v1 = TransposedRead(vl + 16 * SM::ROW + vo);
-        const bf16x8_t vbv = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+        if (nb + 2 < NB) vop[nb + 2] = vread(nb + 2);
 #pragma unroll
         for (int hh = 0; hh < HB; ++hh)
-          o[hh][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vbv, pa[hh], o[hh][nb], 0, 0, 0);
+          o[hh][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop[nb], pa[hh], o[hh][nb], 0, 0, 0);
       }
     }
   };
