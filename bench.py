@@ -75,7 +75,7 @@ def parse():
     ap.add_argument("--no-ceiling-probe", action="store_true",
                     help="skip the read-bandwidth probes that price the practical ceiling")
     ap.add_argument("--no-extras", action="store_true",
-                    help="skip the prefill, fused RoPE and re-prefill side measurements")
+                    help="skip the prefill, fused RoPE, o_proj and re-prefill side measurements")
     ap.add_argument("--kv", default="auto", choices=["auto", "int8", "fp8"],
                     help="KV element type: the config's own (auto), or INT8 or FP8 (E4M3) "
                          "with per-(block, kv head) scales")
@@ -320,6 +320,38 @@ def time_rope_append(ctx, ehip, w, slabs, qs, kns, vns, layers, reps=5):
     return {"rows": R, "bytes_per_launch": nbytes, "us_per_launch": round(t_rope * 1e6, 2),
             "gbps": round(nbytes / t_rope / 1e9, 1),
             "plain_append_us_per_launch": round(t_plain * 1e6, 2)}
+
+
+def time_o_proj(ctx, ehip, w, outs, layers, reps=5):
+    """The attention output's consumer, o_proj (ehip_packed_gemm): per layer
+    y [rows, hidden] = ctx [rows, H*d] W^T with a bf16 checkpoint weight per
+    layer (hidden = H*d for the configs' models), packed once into the
+    reference's panel layout. Algorithmic flops 2*rows*H*d*hidden; weight
+    bytes hidden*H*d*2 per launch."""
+    m, k = w.rows, w.heads * w.head_dim
+    n = k
+    wts = []
+    for layer in range(layers):
+        raw = ctx.alloc(n * k * 2)
+        ctx.fill_normal(raw, n * k, ehip.KV_BF16, 0.0, float(1.0 / np.sqrt(k)), 7000 + layer)
+        wp = ctx.alloc(((n + 15) // 16) * k * 16 * 2)
+        ctx._check(ctx.pack_weight_panels(raw, ehip.WEIGHT_BF16, n, k, wp))
+        raw.free()
+        wts.append(wp)
+    y = ctx.alloc(m * n * 4)
+    t = time_calls(ctx, layers, reps, lambda layer: ctx._check(
+        ctx.packed_gemm(outs[layer], m, k, wts[layer], ehip.WEIGHT_BF16, n, None, y)))
+    for b in wts + [y]:
+        b.free()
+    flops = 2 * m * k * n
+    tf = flops / t / 1e12
+    return {"m": m, "k": k, "n": n, "weight_dtype": "bf16", "us_per_launch": round(t * 1e6, 2),
+            "tflops": round(tf, 2), "weight_gbps": round(n * k * 2 / t / 1e9, 1),
+            "roofline": {"bound": "mfma", "achieved": round(tf, 2),
+                         "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                         "kernel": "o_proj packed GEMM (x in three bf16 planes: 3x the "
+                                   "algorithmic flops issued)"}}
 
 
 def c5_reprefill(ctx, ehip, w, slabs, layers, reps=3):
@@ -580,6 +612,10 @@ def main():
         ra = time_rope_append(ctx, ehip, w, bench.slabs, bench.qs, bench.kns, bench.vns, layers)
         result_extra["rope_append"] = ra
         log(f"[bench] fused RoPE + append: {ra}")
+        op = time_o_proj(ctx, ehip, w, bench.outs, layers)
+        result_extra["o_proj"] = op
+        log(f"[bench] o_proj: {op['us_per_launch']} us/launch, {op['tflops']} TFLOP/s, "
+            f"weights {op['weight_gbps']} GB/s")
         if w.name == "C5":
             ev = c5_reprefill(ctx, ehip, w, bench.slabs, layers)
             result_extra["reprefill_event"] = ev

@@ -70,6 +70,9 @@ enum {
  * OCP E4M3 format (4 exponent bits with bias 7, 3 mantissa bits, largest
  * finite value 448, codes 0x7F / 0xFF NaN). */
 enum { EHIP_KV_F32 = 0, EHIP_KV_BF16 = 1, EHIP_KV_INT8 = 2, EHIP_KV_FP8 = 3 };
+/* Weight storage of the packed linear layer (the reference's PackedLinear
+ * weight dtypes kFloat32 / kBFloat16 / kFloat16, src/model/packed_linear.h:31-36). */
+enum { EHIP_WEIGHT_F32 = 0, EHIP_WEIGHT_BF16 = 1, EHIP_WEIGHT_F16 = 2 };
 
 typedef struct ehip_ctx ehip_ctx;
 
@@ -221,6 +224,29 @@ int ehip_prefill_attention_f32(ehip_ctx* ctx, const float* d_q, const float* d_k
 int ehip_decode_attention_f32(ehip_ctx* ctx, const float* d_q, const float* d_k, const float* d_v,
                               float* d_out, int64_t heads, int64_t kv_heads, int64_t d,
                               int64_t l_dim, float scale);
+
+/* The attention output's consumer, o_proj (src/model/optimized_model.cpp:346:
+ * layer.o_proj->forward(ctx, tmp), a PackedLinear).
+ *
+ * kernels::PackWeightPanels (src/kernels/gemm.h:61-64): d_w [n, k] row-major
+ * (weight_dtype EHIP_WEIGHT_F32 = fp32, _BF16 / _F16 = 16-bit bit patterns)
+ * repacked into the reference's panel layout d_wp [ceil(n/16), k, 16]:
+ * Wp[p, kk, r] = W[p*16 + r, kk], 0 past n (a pure permute, same dtype).
+ * d_wp holds ceil(n/16)*k*16 elements (kernels::PackedWeightElements). */
+int ehip_pack_weight_panels(ehip_ctx* ctx, const void* d_w, int32_t weight_dtype, int64_t n,
+                            int64_t k, void* d_wp);
+/* kernels::PackedGemm (src/kernels/gemm.h:76-78): y[m, n] = x[m, k] W^T
+ * (+ bias[n], added after the k sum) over the packed weight. x, bias, y fp32;
+ * y fully overwritten. On the matrix cores x is cut into three bf16 planes
+ * and the weight into the planes its type needs to be exact (1 bf16, 2 fp16,
+ * 3 fp32); the products of planes whose indices sum to at most 2 are summed
+ * in fp32 (what is left out is below 2^-24 of |x||w| per term). Within the
+ * reference's GEMM tolerance (allclose rtol 1e-4, atol 1e-5 sqrt(k)) of its
+ * scalar result; deterministic. Calls with few row tiles split k over
+ * workgroups and add the partials in split order (a workspace the context
+ * owns). d_bias may be null. */
+int ehip_packed_gemm(ehip_ctx* ctx, const float* d_x, int64_t m, int64_t k, const void* d_wp,
+                     int32_t weight_dtype, int64_t n, const float* d_bias, float* d_y);
 
 /* kernels::PrefillAttentionVarlenF32 (src/kernels/attention.h:221-227), in the
  * reference's argument order: sequence b's query rows are [cu_seqlens[b],

@@ -35,6 +35,10 @@ struct ehip_ctx {
   // Split-KV partials (max, sum, unnormalised output per split).
   float* d_part = nullptr;
   size_t d_part_bytes = 0;
+  // Split-k partial sums of the packed linear layer.
+  float* d_gemm = nullptr;
+  size_t d_gemm_bytes = 0;
+  int cus = 256;  // compute units of the device
   int32_t* d_err = nullptr;
   // Item-queue counters of the persistent decode kernel, in the error page
   // (zeroed at creation; every launch leaves them zero).
@@ -321,6 +325,10 @@ int ehip_init(int device, ehip_ctx** out) {
     constexpr size_t kQueueWord = 1024;
     constexpr size_t kPageBytes =
         4 * (kQueueWord + (ehip::kItemQueues + 1) * size_t{ehip::kQueueStride});
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess &&
+        cus > 0)
+      ctx->cus = cus;
     e = hipMalloc(&ctx->d_err, kPageBytes);
     if (e != hipSuccess) { rc = HipFail(ctx, e, "hipMalloc(err)"); break; }
     e = hipMemset(ctx->d_err, 0, kPageBytes);
@@ -351,6 +359,7 @@ int ehip_destroy(ehip_ctx* ctx) {
   }
   if (ctx->d_desc) (void)hipFree(ctx->d_desc);
   if (ctx->d_part) (void)hipFree(ctx->d_part);
+  if (ctx->d_gemm) (void)hipFree(ctx->d_gemm);
   if (ctx->d_err) (void)hipFree(ctx->d_err);
   if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
   delete ctx;
@@ -693,6 +702,68 @@ int ehip_decode_attention_f32(ehip_ctx* ctx, const float* d_q, const float* d_k,
                               float* d_out, int64_t heads, int64_t kv_heads, int64_t d,
                               int64_t l_dim, float scale) {
   return ContiguousAttention(ctx, d_q, d_k, d_v, d_out, 1, heads, kv_heads, d, l_dim, scale);
+}
+
+namespace {
+bool WeightDtypeOk(int32_t t) {
+  return t == EHIP_WEIGHT_F32 || t == EHIP_WEIGHT_BF16 || t == EHIP_WEIGHT_F16;
+}
+}  // namespace
+
+int ehip_pack_weight_panels(ehip_ctx* ctx, const void* d_w, int32_t weight_dtype, int64_t n,
+                            int64_t k, void* d_wp) {
+  if (int rc = CheckCtx(ctx)) return rc;
+  // The reference CHECKs n, k >= 1 and non-null operands (src/kernels/gemm.cpp:123-125).
+  if (n < 1 || k < 1 || n > (int64_t{1} << 31) || k > (int64_t{1} << 31))
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "pack: n=%lld k=%lld must be in [1, 2^31]",
+                    static_cast<long long>(n), static_cast<long long>(k));
+  if (!WeightDtypeOk(weight_dtype))
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "pack: weight_dtype=%d is not F32/BF16/F16",
+                    weight_dtype);
+  if (!d_w || !d_wp) return SetError(ctx, EHIP_INVALID_ARGUMENT, "pack: null operand");
+  EHIP_HIP(ctx, ehip::LaunchPackWeightPanels(d_w, weight_dtype, n, k, d_wp, ctx->stream));
+  return EHIP_OK;
+}
+
+int ehip_packed_gemm(ehip_ctx* ctx, const float* d_x, int64_t m, int64_t k, const void* d_wp,
+                     int32_t weight_dtype, int64_t n, const float* d_bias, float* d_y) {
+  if (int rc = CheckCtx(ctx)) return rc;
+  // The reference CHECKs m, k, n >= 1 and a supported dtype (src/kernels/gemm.h:76-78).
+  if (m < 1 || k < 1 || n < 1 || m > (int64_t{1} << 31) || k > (int64_t{1} << 31) ||
+      n > (int64_t{1} << 31))
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "gemm: m=%lld k=%lld n=%lld must be in [1, 2^31]",
+                    static_cast<long long>(m), static_cast<long long>(k),
+                    static_cast<long long>(n));
+  if (!WeightDtypeOk(weight_dtype))
+    return SetError(ctx, EHIP_INVALID_ARGUMENT, "gemm: weight_dtype=%d is not F32/BF16/F16",
+                    weight_dtype);
+  if (!d_x || !d_wp || !d_y) return SetError(ctx, EHIP_INVALID_ARGUMENT, "gemm: null operand");
+  if (reinterpret_cast<uintptr_t>(d_wp) % 16 != 0)
+    return SetError(ctx, EHIP_INVALID_ARGUMENT,
+                    "gemm: the packed weight must be 16-byte aligned (ehip_malloc gives 256)");
+  ehip::GemmParams p{};
+  ehip::PlanPackedGemm(m, k, n, ctx->cus, &p);
+  p.x = d_x;
+  p.wp = d_wp;
+  p.bias = d_bias;
+  p.y = d_y;
+  p.x_vec = (k % 4 == 0 && reinterpret_cast<uintptr_t>(d_x) % 16 == 0) ? 1 : 0;
+  if (p.splits > 1) {
+    const size_t need = static_cast<size_t>(p.splits) * static_cast<size_t>(m) *
+                        static_cast<size_t>(n) * sizeof(float);
+    if (need > ctx->d_gemm_bytes) {
+      const size_t bytes = std::max(need, ctx->d_gemm_bytes * 3 / 2);
+      EHIP_HIP(ctx, hipStreamSynchronize(ctx->stream));  // queued calls may use it
+      if (ctx->d_gemm) EHIP_HIP(ctx, hipFree(ctx->d_gemm));
+      ctx->d_gemm = nullptr;
+      ctx->d_gemm_bytes = 0;
+      EHIP_HIP(ctx, hipMalloc(&ctx->d_gemm, bytes));
+      ctx->d_gemm_bytes = bytes;
+    }
+    p.part = ctx->d_gemm;
+  }
+  EHIP_HIP(ctx, ehip::LaunchPackedGemm(p, weight_dtype, ctx->stream));
+  return EHIP_OK;
 }
 
 int ehip_prefill_attention_varlen_f32(ehip_ctx* ctx, const float* d_q,

@@ -177,6 +177,26 @@ hipError_t LaunchSingleRowStatic(const DecodeParams& base, int device, int32_t l
                                  int32_t split_len, int32_t nsplit, const Tuning& tune,
                                  QueueState* queue, hipStream_t stream);
 
+// Packed linear layer (packed_gemm.hip): y[m, n] = x[m, k] W^T (+ bias) over
+// the reference's panel layout [ceil(n/16), k, 16].
+struct GemmParams {
+  const float* x;       // [m, k]
+  const void* wp;       // packed weight
+  const float* bias;    // [n] or null
+  float* y;             // [m, n]
+  float* part;          // [splits, m, n] partial sums (splits > 1)
+  int64_t m, k, n;
+  int64_t panels;       // ceil(n / 16)
+  int64_t k_split;      // k per split (a multiple of 32)
+  int32_t splits;
+  int32_t x_vec;        // x rows are 16-byte aligned (k % 4 == 0, aligned base)
+};
+// Tiles and k splits for a call (cus: the device's CU count).
+void PlanPackedGemm(int64_t m, int64_t k, int64_t n, int cus, GemmParams* p);
+hipError_t LaunchPackedGemm(const GemmParams& p, int weight_dtype, hipStream_t stream);
+hipError_t LaunchPackWeightPanels(const void* w, int weight_dtype, int64_t n, int64_t k, void* wp,
+                                  hipStream_t stream);
+
 hipError_t LaunchFillNormal(void* dst, int64_t n, int dtype, float mean, float stddev,
                             uint64_t seed, hipStream_t stream);
 

@@ -31,6 +31,10 @@ KV_BF16 = 1
 KV_INT8 = 2
 KV_FP8 = 3
 
+WEIGHT_F32 = 0
+WEIGHT_BF16 = 1
+WEIGHT_F16 = 2
+
 _i32 = C.c_int32
 _i64 = C.c_int64
 _vp = C.c_void_p
@@ -93,6 +97,8 @@ def lib():
                                           C.c_float],
             "ehip_prefill_attention_varlen_f32": [_vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp,
                                                   _i64, _i64, _i64, C.c_float],
+            "ehip_pack_weight_panels": [_vp, _vp, _i32, _i64, _i64, _vp],
+            "ehip_packed_gemm": [_vp, _vp, _i64, _i64, _vp, _i32, _i64, _vp, _vp],
             "ehip_paged_decode_attention_f32_noalloc": [_vp, _vp, _vp, _vp, _vp, _i64, _i64,
                                                         _i64, _i64, _i64, _i64, _i64, _i64,
                                                         C.c_float, _vp],
@@ -315,6 +321,15 @@ class Context:
             self.h, q.ptr if q else None, cu.ctypes.data, len(k_seqs), C.cast(ks, _vp),
             C.cast(vs, _vp), ls.ctypes.data, out.ptr if out else None, heads, kv_heads, d,
             scale)
+
+    def pack_weight_panels(self, w, weight_dtype, n, k, wp) -> int:
+        """Device buffers: w [n, k] -> wp [ceil(n/16), k, 16] (same dtype)."""
+        return lib().ehip_pack_weight_panels(self.h, w.ptr, weight_dtype, n, k, wp.ptr)
+
+    def packed_gemm(self, x, m, k, wp, weight_dtype, n, bias, y) -> int:
+        """Device buffers: y [m, n] = x [m, k] W^T (+ bias) over the packed wp."""
+        return lib().ehip_packed_gemm(self.h, x.ptr, m, k, wp.ptr, weight_dtype, n,
+                                      bias.ptr if bias is not None else None, y.ptr)
 
     def paged_decode_batched(self, q, k_slab, v_slab, tables, lengths, heads, kv_heads, d, bs,
                              block_stride, slab_blocks, scale, out, bf16=False) -> int:

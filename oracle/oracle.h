@@ -24,6 +24,10 @@
  *                                    force; causal-mask and GQA closed forms.
  *   - orc_kv_scatter/gather        : independent slot closed form + round trip,
  *                                    bit-exact vs oracle/_ref.
+ *   - orc_pack_weight_panels_* /    : bit-exact vs oracle/_ref (the reference's
+ *     orc_packed_gemm                scalar GemmTile and PackWeightPanels);
+ *                                    fp64 brute force on small shapes; fp16
+ *                                    widening exhaustive vs numpy float16.
  *
  * Error convention: functions return 0 on success and a core::StatusCode value
  * (2 = InvalidArgument) where the reference CHECK-aborts on a programmer error
@@ -168,6 +172,20 @@ void orc_kv_gather_f32(const float* k_slab, const float* v_slab,
 int orc_cpu_attention(const float* q, const float* k, const float* v,
                       int64_t t_dim, int64_t heads, int64_t kv_heads, int64_t d,
                       int64_t l_dim, float scale, float* out);
+
+/* ---- packed linear layer (the attention output's consumer, o_proj) ----
+ * Weight dtype codes: 0 fp32, 1 bf16 bits, 2 fp16 bits.
+ * kernels::PackWeightPanels (src/kernels/gemm.cpp:119-151): w [n, k] ->
+ * wp [ceil(n/16), k, 16], wp[p, kk, r] = w[p*16 + r, kk], 0 past n. */
+void orc_pack_weight_panels_u16(const uint16_t* w, int64_t n, int64_t k, uint16_t* wp);
+void orc_pack_weight_panels_f32(const float* w, int64_t n, int64_t k, float* wp);
+/* IEEE binary16 bits -> fp32 (src/tensor/half.h:84-109). */
+float orc_fp16_bits_to_fp32(uint16_t h);
+/* kernels::PackedGemm's scalar tile (src/kernels/scalar/gemm.cpp:21-41) and
+ * store (src/kernels/internal/gemm_common.h:22-41): per output row and panel
+ * a 16-wide fp32 accumulator summed in ascending k, bias added after. */
+int orc_packed_gemm(const float* x, int64_t m, int64_t k, const void* wp, int dtype, int64_t n,
+                    const float* bias, float* y);
 
 #ifdef __cplusplus
 }

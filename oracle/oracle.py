@@ -92,6 +92,15 @@ def lib():
         L.orc_cpu_attention.argtypes = [_f32p, _f32p, _f32p, _i64, _i64, _i64, _i64, _i64,
                                         C.c_float, _f32p]
         L.orc_cpu_attention.restype = C.c_int
+        L.orc_pack_weight_panels_u16.argtypes = [_u16p, _i64, _i64, _u16p]
+        L.orc_pack_weight_panels_u16.restype = None
+        L.orc_pack_weight_panels_f32.argtypes = [_f32p, _i64, _i64, _f32p]
+        L.orc_pack_weight_panels_f32.restype = None
+        L.orc_fp16_bits_to_fp32.argtypes = [C.c_uint16]
+        L.orc_fp16_bits_to_fp32.restype = C.c_float
+        L.orc_packed_gemm.argtypes = [_f32p, _i64, _i64, C.c_void_p, C.c_int, _i64, C.c_void_p,
+                                      _f32p]
+        L.orc_packed_gemm.restype = C.c_int
         _lib = L
     return _lib
 
@@ -123,6 +132,13 @@ def ref():
         R.ref_rope_apply_f32.restype = None
         R.ref_kv_gather_f32.argtypes = [_f32p, _f32p, _i32p, _i64, _i64, _i64, _i64,
                                         _f32p, _f32p]
+        R.ref_pack_weight_panels_u16.argtypes = [_u16p, _i64, _i64, _u16p]
+        R.ref_pack_weight_panels_u16.restype = None
+        R.ref_pack_weight_panels_f32.argtypes = [_f32p, _i64, _i64, _f32p]
+        R.ref_pack_weight_panels_f32.restype = None
+        R.ref_packed_gemm.argtypes = [C.c_int, C.c_int, _f32p, _i64, _i64, C.c_void_p, _i64,
+                                      C.c_void_p, _f32p]
+        R.ref_packed_gemm.restype = None
         _ref = R
     return _ref
 
@@ -395,3 +411,49 @@ def paged_to_contig(slab, table, length, kv_heads, d, bs):
     blocks = slab[np.asarray(table[:nb], np.int64)]          # [nb, Hkv, bs, d]
     full = blocks.transpose(1, 0, 2, 3).reshape(kv_heads, nb * bs, d)
     return np.ascontiguousarray(full[:, :length])
+
+
+# ---- packed linear layer (o_proj) -------------------------------------------
+WEIGHT_F32, WEIGHT_BF16, WEIGHT_F16 = 0, 1, 2
+
+
+def pack_weight_panels(w: np.ndarray, use_ref: bool = False) -> np.ndarray:
+    """kernels::PackWeightPanels: w [n, k] (float32, or uint16 bit patterns of
+    bf16 / fp16) -> [ceil(n/16), k, 16] of the same dtype, 0 past n."""
+    n, k = w.shape
+    panels = (n + 15) // 16
+    if w.dtype == np.float32:
+        out = np.empty((panels, k, 16), np.float32)
+        fn = (ref().ref_pack_weight_panels_f32 if use_ref else lib().orc_pack_weight_panels_f32)
+    else:
+        w = w.astype(np.uint16, copy=False)
+        out = np.empty((panels, k, 16), np.uint16)
+        fn = (ref().ref_pack_weight_panels_u16 if use_ref else lib().orc_pack_weight_panels_u16)
+    fn(np.ascontiguousarray(w).reshape(-1), n, k, out.reshape(-1))
+    return out
+
+
+def fp16_bits_to_f32(b: int) -> float:
+    return float(lib().orc_fp16_bits_to_fp32(int(b)))
+
+
+def packed_gemm(x: np.ndarray, wp: np.ndarray, dtype: int, n: int, bias=None, isa: int = 0,
+                use_ref: bool = False) -> np.ndarray:
+    """kernels::PackedGemm: y [m, n] = x [m, k] W^T (+ bias) over the packed
+    weight; the restatement of the scalar tile, or (use_ref) the reference's
+    own tile of `isa` (0 scalar, 1 AVX2, -1 the public threaded entry)."""
+    x = np.ascontiguousarray(x, np.float32)
+    m, k = x.shape
+    y = np.empty((m, n), np.float32)
+    wpc = np.ascontiguousarray(wp)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    bp = None if b is None else b.ctypes.data
+    if use_ref:
+        ref().ref_packed_gemm(isa, dtype, x.reshape(-1), m, k, wpc.ctypes.data, n, bp,
+                              y.reshape(-1))
+    else:
+        rc = lib().orc_packed_gemm(x.reshape(-1), m, k, wpc.ctypes.data, dtype, n, bp,
+                                   y.reshape(-1))
+        if rc != 0:
+            raise ValueError(f"orc_packed_gemm rejected the call ({rc})")
+    return y

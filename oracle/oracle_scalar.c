@@ -812,3 +812,78 @@ void orc_rope_apply_f32(int isa, float* x, int64_t t, int64_t hx, int64_t d,
     }
   }
 }
+
+/* ------------------------------------------------------------------------ */
+/* Packed linear layer (kernels::PackWeightPanels / PackedGemm).            */
+/* ------------------------------------------------------------------------ */
+enum { ORC_NR = 16 }; /* kernels::kNr (src/kernels/gemm.h:39) */
+
+void orc_pack_weight_panels_u16(const uint16_t* w, int64_t n, int64_t k, uint16_t* wp) {
+  const int64_t panels = (n + ORC_NR - 1) / ORC_NR;
+  for (int64_t p = 0; p < panels; ++p)
+    for (int64_t kk = 0; kk < k; ++kk)
+      for (int64_t r = 0; r < ORC_NR; ++r) {
+        const int64_t row = p * ORC_NR + r;
+        wp[(p * k + kk) * ORC_NR + r] = row < n ? w[row * k + kk] : 0;
+      }
+}
+
+void orc_pack_weight_panels_f32(const float* w, int64_t n, int64_t k, float* wp) {
+  const int64_t panels = (n + ORC_NR - 1) / ORC_NR;
+  for (int64_t p = 0; p < panels; ++p)
+    for (int64_t kk = 0; kk < k; ++kk)
+      for (int64_t r = 0; r < ORC_NR; ++r) {
+        const int64_t row = p * ORC_NR + r;
+        wp[(p * k + kk) * ORC_NR + r] = row < n ? w[row * k + kk] : 0.0f;
+      }
+}
+
+static float orc_bits_f32(uint32_t b) {
+  float f;
+  memcpy(&f, &b, sizeof(f));
+  return f;
+}
+
+float orc_fp16_bits_to_fp32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t exponent = (h >> 10) & 0x1Fu;
+  const uint32_t mantissa = h & 0x03FFu;
+  if (exponent == 0x1Fu) return orc_bits_f32(sign | 0x7F800000u | (mantissa << 13));
+  if (exponent == 0u) {
+    if (mantissa == 0u) return orc_bits_f32(sign);
+    /* Subnormal: normalise on the leading set bit n (0..9): 1.xxx * 2^(n-24). */
+    int nb = 31 - __builtin_clz(mantissa);
+    const uint32_t exp32 = 103u + (uint32_t)nb;
+    const uint32_t man32 = (mantissa << (23u - (uint32_t)nb)) & 0x007FFFFFu;
+    return orc_bits_f32(sign | (exp32 << 23) | man32);
+  }
+  return orc_bits_f32(sign | ((exponent + 112u) << 23) | (mantissa << 13));
+}
+
+static float orc_widen(const void* wp, int dtype, int64_t i) {
+  if (dtype == 0) return ((const float*)wp)[i];
+  const uint16_t b = ((const uint16_t*)wp)[i];
+  return dtype == 1 ? orc_bits_f32((uint32_t)b << 16) : orc_fp16_bits_to_fp32(b);
+}
+
+int orc_packed_gemm(const float* x, int64_t m, int64_t k, const void* wp, int dtype, int64_t n,
+                    const float* bias, float* y) {
+  if (m < 1 || k < 1 || n < 1 || dtype < 0 || dtype > 2) return 2;
+  const int64_t panels = (n + ORC_NR - 1) / ORC_NR;
+  for (int64_t mm = 0; mm < m; ++mm) {
+    const float* x_row = x + mm * k;
+    for (int64_t p = 0; p < panels; ++p) {
+      float acc[ORC_NR] = {0};
+      for (int64_t kk = 0; kk < k; ++kk) {
+        const float a = x_row[kk];
+        const int64_t base = (p * k + kk) * ORC_NR;
+        for (int64_t r = 0; r < ORC_NR; ++r) acc[r] += a * orc_widen(wp, dtype, base + r);
+      }
+      const int64_t col0 = p * ORC_NR;
+      const int64_t ncols = ORC_MIN(ORC_NR, n - col0);
+      float* y_row = y + mm * n + col0;
+      for (int64_t r = 0; r < ncols; ++r) y_row[r] = bias ? acc[r] + bias[col0 + r] : acc[r];
+    }
+  }
+  return 0;
+}

@@ -19,6 +19,9 @@
 #include "kernels/kv_scatter.h"
 #include "kernels/paged_attention.h"
 #include "kernels/internal/rope_impl.h"
+#include "kernels/gemm.h"
+#include "kernels/internal/gemm_impl.h"
+#include "tensor/dtype.h"
 #include "kernels/rope.h"
 
 namespace k = engine::kernels;
@@ -165,6 +168,40 @@ void ref_kv_gather_f32(const float* k_slab, const float* v_slab,
                        std::int64_t d, float* out_k, float* out_v) {
   k::KvGatherF32(k_slab, v_slab, block_table, block_size, length, kv_heads, d,
                  out_k, out_v);
+}
+
+// Packed linear layer (src/kernels/gemm.h): the panel pack, and the GEMM with
+// isa 0 = the scalar tile over every row and panel (bit-identical to a naive
+// ascending-k loop), 1 = the AVX2 tile, -1 = the public threaded PackedGemm.
+// dtype: 0 fp32, 1 bf16, 2 fp16.
+void ref_pack_weight_panels_u16(const std::uint16_t* w, std::int64_t n, std::int64_t k,
+                                std::uint16_t* wp) {
+  k::PackWeightPanels(w, n, k, wp);
+}
+void ref_pack_weight_panels_f32(const float* w, std::int64_t n, std::int64_t k, float* wp) {
+  k::PackWeightPanels(w, n, k, wp);
+}
+void ref_packed_gemm(int isa, int dtype, const float* x, std::int64_t m, std::int64_t kk,
+                     const void* wp, std::int64_t n, const float* bias, float* y) {
+  namespace t = engine::tensor;
+  const t::DataType dt = dtype == 0 ? t::DataType::kFloat32
+                         : dtype == 1 ? t::DataType::kBFloat16 : t::DataType::kFloat16;
+  if (isa < 0) {
+    k::PackedGemm(x, m, kk, wp, dt, n, bias, y);
+    return;
+  }
+  const std::int64_t panels = k::PackedPanels(n);
+  const auto* w16 = static_cast<const std::uint16_t*>(wp);
+  const auto* w32 = static_cast<const float*>(wp);
+  if (isa == 0) {
+    if (dtype == 0) k::scalar::GemmTileF32(x, kk, n, w32, bias, y, 0, m, 0, panels);
+    else if (dtype == 1) k::scalar::GemmTileBf16(x, kk, n, w16, bias, y, 0, m, 0, panels);
+    else k::scalar::GemmTileF16(x, kk, n, w16, bias, y, 0, m, 0, panels);
+  } else {
+    if (dtype == 0) k::avx2::GemmTileF32(x, kk, n, w32, bias, y, 0, m, 0, panels);
+    else if (dtype == 1) k::avx2::GemmTileBf16(x, kk, n, w16, bias, y, 0, m, 0, panels);
+    else k::avx2::GemmTileF16(x, kk, n, w16, bias, y, 0, m, 0, panels);
+  }
 }
 
 }  // extern "C"

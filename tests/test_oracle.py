@@ -580,3 +580,73 @@ def test_fp8_dequant_matches_closed_form(orc):
     s = rng.uniform(0.01, 1, (3, 2)).astype(np.float32)
     x = orc.fp8_dequant(q, s)
     assert np.array_equal(x, orc.e4m3_to_f32(q) * s[:, :, None, None])
+
+
+# ---- packed linear layer (o_proj): kernels::PackWeightPanels / PackedGemm ----
+GEMM_SHAPES = [(16, 64, 64), (16, 64, 96), (16, 176, 64), (8, 64, 512), (1, 64, 64),
+               (1, 2048, 512), (130, 300, 70), (7, 1, 33), (65, 129, 1000), (5, 40, 17)]
+
+
+def _gemm_weights(orc, n, k, dtype, seed):
+    wf = orc.fill_normal(n * k, 0.0, 1.0, seed).reshape(n, k)
+    if dtype == 0:
+        return wf
+    if dtype == 1:
+        return orc.to_bf16_bits(wf)
+    return wf.astype(np.float16).view(np.uint16)
+
+
+def test_pack_weight_panels_closed_form(orc):
+    """Wp[p, k, r] = W[p*16 + r, k], zero past n (packed_gemm_test.cpp:96-121)."""
+    rng = np.random.default_rng(3)
+    for n, k in [(17, 5), (16, 3), (40, 9), (1, 1)]:
+        w = rng.standard_normal((n, k)).astype(np.float32)
+        wp = orc.pack_weight_panels(w)
+        want = np.zeros(((n + 15) // 16 * 16, k), np.float32)
+        want[:n] = w
+        want = want.reshape(-1, 16, k).transpose(0, 2, 1)
+        assert np.array_equal(wp, want)
+
+
+def test_fp16_widening_exhaustive(orc):
+    """Every binary16 pattern (normals, subnormals, +-0, inf, NaN payloads)
+    against numpy's float16 -> float32 (src/tensor/half.h:84-109)."""
+    bits = np.arange(65536, dtype=np.uint16)
+    want = bits.view(np.float16).astype(np.float32)
+    got = np.array([orc.fp16_bits_to_f32(int(b)) for b in bits], np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype", [0, 1, 2])
+def test_packed_gemm_fp64_brute_force(orc, dtype):
+    """Independent of the restatement's loop: the fp64 product of the widened
+    weights, within fp32 accumulation rounding (k * 2^-23 of sum |x w|)."""
+    rng = np.random.default_rng(10 + dtype)
+    for m, k, n in [(3, 50, 20), (1, 7, 33), (9, 129, 16)]:
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        w = _gemm_weights(orc, n, k, dtype, 20 + m)
+        wf = (w if dtype == 0 else orc.bf16_bits_to_f32(w) if dtype == 1
+              else w.view(np.float16).astype(np.float32)).astype(np.float64)
+        bias = rng.standard_normal(n).astype(np.float32)
+        y = orc.packed_gemm(x, orc.pack_weight_panels(w), dtype, n, bias)
+        exact = x.astype(np.float64) @ wf.T + bias
+        bound = k * 2.0 ** -23 * (np.abs(x).astype(np.float64) @ np.abs(wf).T + np.abs(bias))
+        assert (np.abs(y - exact) <= bound + 1e-30).all()
+
+
+@needs_ref
+@pytest.mark.parametrize("dtype", [0, 1, 2])
+def test_packed_gemm_bit_exact_vs_reference_scalar(orc, dtype):
+    """The restatement against the reference's own scalar GemmTile and
+    PackWeightPanels, compiled from its sources: same bits."""
+    for i, (m, k, n) in enumerate(GEMM_SHAPES):
+        x = orc.fill_normal(m * k, 0.0, 1.0, 300 + i).reshape(m, k)
+        w = _gemm_weights(orc, n, k, dtype, 400 + i)
+        wp = orc.pack_weight_panels(w)
+        assert np.array_equal(wp.view(np.uint8), orc.pack_weight_panels(w, use_ref=True).view(np.uint8))
+        bias = orc.fill_normal(n, 0.0, 1.0, 500 + i) if i % 2 else None
+        y = orc.packed_gemm(x, wp, dtype, n, bias)
+        r = orc.packed_gemm(x, wp, dtype, n, bias, isa=0, use_ref=True)
+        assert np.array_equal(y.view(np.uint32), r.view(np.uint32)), (m, k, n)
