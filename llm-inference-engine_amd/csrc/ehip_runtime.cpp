@@ -748,9 +748,13 @@ int ehip_packed_gemm(ehip_ctx* ctx, const float* d_x, int64_t m, int64_t k, cons
   p.bias = d_bias;
   p.y = d_y;
   p.x_vec = (k % 4 == 0 && reinterpret_cast<uintptr_t>(d_x) % 16 == 0) ? 1 : 0;
-  if (p.splits > 1) {
-    const size_t need = static_cast<size_t>(p.splits) * static_cast<size_t>(m) *
-                        static_cast<size_t>(n) * sizeof(float);
+  {
+    // x's bf16 planes, then (split k) the partial sums, 256 bytes apart.
+    const size_t planes = (ehip::PackedGemmPlaneBytes(p) + 255) & ~size_t{255};
+    const size_t partial = p.splits > 1 ? static_cast<size_t>(p.splits) * static_cast<size_t>(m) *
+                                              static_cast<size_t>(n) * sizeof(float)
+                                        : 0;
+    const size_t need = planes + partial;
     if (need > ctx->d_gemm_bytes) {
       const size_t bytes = std::max(need, ctx->d_gemm_bytes * 3 / 2);
       EHIP_HIP(ctx, hipStreamSynchronize(ctx->stream));  // queued calls may use it
@@ -760,7 +764,9 @@ int ehip_packed_gemm(ehip_ctx* ctx, const float* d_x, int64_t m, int64_t k, cons
       EHIP_HIP(ctx, hipMalloc(&ctx->d_gemm, bytes));
       ctx->d_gemm_bytes = bytes;
     }
-    p.part = ctx->d_gemm;
+    p.xp = reinterpret_cast<uint16_t*>(ctx->d_gemm);
+    p.part = p.splits > 1 ? reinterpret_cast<float*>(reinterpret_cast<char*>(ctx->d_gemm) + planes)
+                          : nullptr;
   }
   EHIP_HIP(ctx, ehip::LaunchPackedGemm(p, weight_dtype, ctx->stream));
   return EHIP_OK;

@@ -181,11 +181,13 @@ hipError_t LaunchSingleRowStatic(const DecodeParams& base, int device, int32_t l
 // the reference's panel layout [ceil(n/16), k, 16].
 struct GemmParams {
   const float* x;       // [m, k]
+  uint16_t* xp;         // x's three bf16 planes [3][m_pad][k_pad] (workspace)
   const void* wp;       // packed weight
   const float* bias;    // [n] or null
   float* y;             // [m, n]
   float* part;          // [splits, m, n] partial sums (splits > 1)
   int64_t m, k, n;
+  int64_t m_pad, k_pad;  // m, k rounded up to whole 64 x 64 tiles
   int64_t panels;       // ceil(n / 16)
   int64_t k_split;      // k per split (a multiple of 32)
   int32_t splits;
@@ -193,6 +195,8 @@ struct GemmParams {
 };
 // Tiles and k splits for a call (cus: the device's CU count).
 void PlanPackedGemm(int64_t m, int64_t k, int64_t n, int cus, GemmParams* p);
+// Workspace bytes of x's planes for the planned call.
+size_t PackedGemmPlaneBytes(const GemmParams& p);
 hipError_t LaunchPackedGemm(const GemmParams& p, int weight_dtype, hipStream_t stream);
 hipError_t LaunchPackWeightPanels(const void* w, int weight_dtype, int64_t n, int64_t k, void* wp,
                                   hipStream_t stream);

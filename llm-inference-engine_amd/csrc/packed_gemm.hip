@@ -16,9 +16,13 @@
 // out are below 2^-24 of |x||w| per term. A bf16 weight therefore costs three
 // MFMAs per 32-k chunk and block, fp16 five, fp32 six.
 //
+// x is cut into its planes once per call by a pre-pass (SplitRows) that
+// writes them zero-padded to whole 64 x 64 tiles, so every column tile reads
+// ready operands instead of re-cutting x.
+//
 // Work: one workgroup of 4 wavefronts per (64 rows, 8 panels = 128 columns,
-// k range). Each k step of 64 stages x (as its three planes, rows padded to
-// 72 elements so the 16 lanes of an A-operand read hit distinct banks) and
+// k range). Each k step of 64 stages x's three planes (rows padded to 72
+// elements so the 16 lanes of an A-operand read hit distinct banks) and
 // the 8 panels' 64 rows (as the weight's planes, the panel layout as stored)
 // in LDS; the next step's global loads are in flight meanwhile. A wavefront
 // owns 32 rows x 64 columns: 2 x 4 blocks of 16 x 16. The A operand of
@@ -126,29 +130,24 @@ __global__ __launch_bounds__(kThreads) void PackedGemmMfma(GemmParams p) {
   const int64_t kb = int64_t{split} * p.k_split;
   const int64_t ke = kb + p.k_split < p.k ? kb + p.k_split : p.k;
 
-  // Global loads: x row xr, 16 consecutive k from xk; panel rows wk and
+  // Global loads: 16 consecutive k from xk of x row xr in each plane (the
+  // planes are zero-padded to whole tiles: no masks); panel rows wk and
   // wk + 32 (16 weights each) of panel wpp.
   const int xr = tid >> 2, xk = (tid & 3) * 16;
-  const bool x_ok = m0 + xr < p.m;
-  const float* xrow = p.x + (x_ok ? (m0 + xr) * p.k : 0);
+  const int64_t plane = p.m_pad * p.k_pad;
+  const __bf16* xrow = reinterpret_cast<const __bf16*>(p.xp) + (m0 + xr) * p.k_pad;
   const int wpp = tid >> 5, wk = tid & 31;  // panel wpp, k rows wk and wk + 32
   const bool w_ok = pb + wpp < p.panels;
   const T* wpanel = static_cast<const T*>(p.wp) + (w_ok ? int64_t{pb + wpp} * p.k * kNr : 0);
 
-  float xv[16];
+  bf16x8_t xv[kXP][2];
   uint4 wv[2][WE];
   auto gload = [&](int64_t k0) {
-    const int64_t kx = k0 + xk;
-    if (p.x_vec && x_ok && kx + 16 <= ke) {
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const float4 a = *reinterpret_cast<const float4*>(xrow + kx + 4 * v);
-        xv[4 * v] = a.x; xv[4 * v + 1] = a.y; xv[4 * v + 2] = a.z; xv[4 * v + 3] = a.w;
-      }
-    } else {
+    for (int pl = 0; pl < kXP; ++pl)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) xv[i] = (x_ok && kx + i < ke) ? xrow[kx + i] : 0.f;
-    }
+      for (int h = 0; h < 2; ++h)
+        xv[pl][h] = *reinterpret_cast<const bf16x8_t*>(xrow + pl * plane + k0 + xk + 8 * h);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int64_t kw = k0 + wk + 32 * h;
@@ -160,19 +159,10 @@ __global__ __launch_bounds__(kThreads) void PackedGemmMfma(GemmParams p) {
   };
   auto lstore = [&]() {
 #pragma unroll
-    for (int g8 = 0; g8 < 2; ++g8) {
-      bf16x8_t xp[kXP];
+    for (int pl = 0; pl < kXP; ++pl)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        __bf16 parts[kXP];
-        Planes<kXP>(xv[8 * g8 + i], parts);
-#pragma unroll
-        for (int pl = 0; pl < kXP; ++pl) xp[pl][i] = parts[pl];
-      }
-#pragma unroll
-      for (int pl = 0; pl < kXP; ++pl)
-        *reinterpret_cast<bf16x8_t*>(&xs[pl][xr * kXRow + xk + 8 * g8]) = xp[pl];
-    }
+      for (int h = 0; h < 2; ++h)
+        *reinterpret_cast<bf16x8_t*>(&xs[pl][xr * kXRow + xk + 8 * h]) = xv[pl][h];
     // Each panel row as WP planes: 16 weights, two 16-byte stores per plane.
 #pragma unroll
     for (int hr = 0; hr < 2; ++hr) {
@@ -278,6 +268,38 @@ __global__ __launch_bounds__(kThreads) void PackedGemmMfma(GemmParams p) {
   }
 }
 
+// x [m, k] fp32 -> its three bf16 planes [3][m_pad][k_pad], zero past m and
+// k; one thread per 8 consecutive elements of a padded row.
+__global__ __launch_bounds__(256) void SplitRows(GemmParams p, __bf16* xp) {
+  const int64_t groups = p.m_pad * (p.k_pad / 8);
+  const int64_t g = int64_t{blockIdx.x} * 256 + threadIdx.x;
+  if (g >= groups) return;
+  const int64_t row = g / (p.k_pad / 8);
+  const int64_t k0 = (g - row * (p.k_pad / 8)) * 8;
+  float v[8];
+  if (p.x_vec && row < p.m && k0 + 8 <= p.k) {
+    const float4 a = *reinterpret_cast<const float4*>(p.x + row * p.k + k0);
+    const float4 b = *reinterpret_cast<const float4*>(p.x + row * p.k + k0 + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = (row < p.m && k0 + i < p.k) ? p.x[row * p.k + k0 + i] : 0.f;
+  }
+  bf16x8_t out[kXP];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    __bf16 parts[kXP];
+    Planes<kXP>(v[i], parts);
+#pragma unroll
+    for (int pl = 0; pl < kXP; ++pl) out[pl][i] = parts[pl];
+  }
+  const int64_t plane = p.m_pad * p.k_pad;
+#pragma unroll
+  for (int pl = 0; pl < kXP; ++pl)
+    *reinterpret_cast<bf16x8_t*>(xp + pl * plane + row * p.k_pad + k0) = out[pl];
+}
+
 // y = (partial 0 + partial 1 + ...) in split order, then + bias.
 __global__ __launch_bounds__(256) void GemmSplitReduce(GemmParams p) {
   const int64_t total = p.m * p.n;
@@ -311,6 +333,8 @@ void PlanPackedGemm(int64_t m, int64_t k, int64_t n, int cus, GemmParams* p) {
   p->m = m;
   p->k = k;
   p->n = n;
+  p->m_pad = (m + kBM - 1) / kBM * kBM;
+  p->k_pad = (k + kBK - 1) / kBK * kBK;
   p->panels = (n + kNr - 1) / kNr;
   const int64_t tiles = ((m + kBM - 1) / kBM) * ((p->panels + kBP - 1) / kBP);
   const int64_t steps = (k + kBK - 1) / kBK;
@@ -327,7 +351,18 @@ void PlanPackedGemm(int64_t m, int64_t k, int64_t n, int cus, GemmParams* p) {
   p->splits = static_cast<int32_t>((steps + per - 1) / per);
 }
 
+size_t PackedGemmPlaneBytes(const GemmParams& p) {
+  return static_cast<size_t>(kXP) * static_cast<size_t>(p.m_pad) * static_cast<size_t>(p.k_pad) *
+         sizeof(uint16_t);
+}
+
 hipError_t LaunchPackedGemm(const GemmParams& p, int weight_dtype, hipStream_t stream) {
+  {
+    const int64_t groups = p.m_pad * (p.k_pad / 8);
+    hipLaunchKernelGGL(SplitRows, dim3(static_cast<uint32_t>((groups + 255) / 256)), dim3(256), 0,
+                       stream, p, reinterpret_cast<__bf16*>(p.xp));
+    if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+  }
   const dim3 grid(static_cast<uint32_t>((p.panels + kBP - 1) / kBP),
                   static_cast<uint32_t>((p.m + kBM - 1) / kBM), static_cast<uint32_t>(p.splits));
   switch (weight_dtype) {
