@@ -59,6 +59,8 @@ struct DecodeParams {
   uint32_t* queue;          // kItemQueues ticket counters, kQueueStride words apart
                             // (zero at launch; MFMA kernel only)
   uint32_t* queue_done;     // wavefronts finished (zero at launch)
+  int32_t queue_spread;     // sub-queue of workgroup b: (b / 8) mod count (else b mod count)
+  int32_t queues;           // sub-queues used, 1..kItemQueues
 };
 
 // The persistent decode kernel's item queue is split into kItemQueues

@@ -139,9 +139,14 @@ void DecodeMfma(DecodeParams p) {
   // Sub-queue q of nq serves items q, q + nq, ... in list order: the ones
   // below gridDim.x are first items (workgroup i starts with item i), the
   // rest go out by ticket, from the first such index at or above gridDim.x.
-  const int nq = min(kItemQueues, static_cast<int>(gridDim.x));
+  const int nq = min(p.queues, static_cast<int>(gridDim.x));
   const bool queued = static_cast<int>(gridDim.x) < p.n_items;
-  const int q = static_cast<int>(blockIdx.x) % nq;
+  // Workgroup b runs on XCD b mod 8. Spread: sub-queue (b / 8) mod nq, served
+  // by workgroups of every XCD (a grid of at least 8 nq workgroups gives
+  // every sub-queue some); else b mod nq, one XCD's workgroups per sub-queue.
+  const int q = (p.queue_spread && static_cast<int>(gridDim.x) >= 8 * nq)
+                    ? (static_cast<int>(blockIdx.x) >> 3) % nq
+                    : static_cast<int>(blockIdx.x) % nq;
   const int first_queued = q + nq * ((static_cast<int>(gridDim.x) - q + nq - 1) / nq);
   uint32_t* const my_queue = p.queue + q * kQueueStride;
   int item_idx = blockIdx.x;
@@ -663,6 +668,8 @@ bool LaunchDecodeMfma(const DecodeParams& params, int kv_dtype, const Tuning& tu
   DecodeParams p = params;
   p.queue = queue->d_counters;
   p.queue_done = queue->d_done;
+  p.queue_spread = tune.decode_qspread ? 1 : 0;
+  p.queues = tune.decode_queues > 0 ? std::min(tune.decode_queues, kItemQueues) : kItemQueues;
   if (!DecodeMfmaCovers(p, kv_dtype, tune)) return false;
   // 32-token tiles (two MFMA halves per tile, double-buffered) measured best
   // on C4; decode_tile16 selects one half per tile (fewer registers),

@@ -52,6 +52,10 @@ Tuning ReadTuning() {
     const long x = std::strtol(v, nullptr, 10);
     if (x > 0) t.target_items = x;
   }
+  if (const char* v = std::getenv("EHIP_TAIL_SPLIT")) {
+    const long x = std::strtol(v, nullptr, 10);
+    if (x >= 0) t.tail_split = static_cast<int32_t>(std::min<long>(x, INT32_MAX / 2));
+  }
   t.joint = flag("EHIP_NO_JOINT", '1');
   t.prefill = flag("EHIP_PREFILL", '0');
   if (const char* v = std::getenv("EHIP_PREFILL_SPLIT")) t.prefill_split = std::strtod(v, nullptr);
@@ -64,6 +68,11 @@ Tuning ReadTuning() {
     if (x > 0) t.decode_slots = static_cast<int32_t>(std::min<long>(x, INT32_MAX));
   }
   t.decode_wg = flag("EHIP_DECODE_WG", '0');
+  t.decode_qspread = flag("EHIP_DECODE_QSPREAD", '0');
+  if (const char* v = std::getenv("EHIP_DECODE_QUEUES")) {
+    const long x = std::strtol(v, nullptr, 10);
+    if (x > 0) t.decode_queues = static_cast<int32_t>(std::min<long>(x, 1 << 20));
+  }
   t.fused_append = flag("EHIP_FUSED_APPEND", '0');
   return t;
 }
@@ -271,12 +280,38 @@ void FinishPlan(const ehip_geometry& g, const Tuning& tune, Plan* plan, bool all
       ranges.push_back(kr);
     }
   }
+  // Tail pieces (Tuning::tail_split > 0): when a step has more items than
+  // the queue hands out first, the keys of each row past its last whole
+  // range go out in pieces of that length. Ordered costliest first, they are
+  // the queue's last items, so the wavefronts that free up first share the
+  // end of the launch in small steps instead of the last whole ranges (one
+  // wavefront streams ~3 GB/s: a 1024-key bf16 range of d = 128 takes
+  // ~170 us). Off by default: on C4, 256-key pieces measured no faster and
+  // their extra partials cost the merge 1.5 us.
+  int32_t ts = static_cast<int32_t>(RoundUp(tune.tail_split, kTile));
+  if (ts > 0) {
+    // Items at whole ranges: the queue is active only past the target.
+    int64_t est = static_cast<int64_t>(ranges.size());
+    for (size_t r = 0; r < n; ++r)
+      if (!skipped(r))
+        est += (plan->rows[r].length - joint_len[r] + split_len[r] - 1) / split_len[r];
+    const int64_t target = tune.target_items > 0 ? tune.target_items : kTargetItems;
+    if (est * g.kv_heads <= target) ts = 0;
+  }
   for (size_t r = 0; r < n; ++r) {
     if (skipped(r)) continue;
-    const int32_t sl = split_len[r];
-    for (int32_t t = joint_len[r]; t < plan->rows[r].length; t += sl)
-      ranges.push_back(KeyRange{{static_cast<int32_t>(r), -1, -1, -1}, t,
-                                std::min(plan->rows[r].length, t + sl)});
+    const int32_t sl = split_len[r], L = plan->rows[r].length, P = joint_len[r];
+    int32_t head_end = L;  // [P, head_end) in ranges of sl, [head_end, L) in tail pieces
+    if (ts > 0 && ts < sl) {
+      const int32_t whole = (L - P) / sl;
+      const int32_t e = P + whole * sl;
+      const int32_t joint_splits = (P + sl - 1) / sl;
+      if (joint_splits + whole + (L - e + ts - 1) / ts <= kMaxSplitsPerRow) head_end = e;
+    }
+    for (int32_t t = P; t < head_end; t += sl)
+      ranges.push_back(KeyRange{{static_cast<int32_t>(r), -1, -1, -1}, t, std::min(head_end, t + sl)});
+    for (int32_t t = head_end; t < L; t += ts)
+      ranges.push_back(KeyRange{{static_cast<int32_t>(r), -1, -1, -1}, t, std::min(L, t + ts)});
   }
 
   // Split indices follow key order within a row. Joint ranges cover the

@@ -37,6 +37,7 @@ namespace ehip {
 struct Tuning {
   int32_t split_tokens = 0;    // EHIP_SPLIT_TOKENS: fixed base split length (0: per step)
   int64_t target_items = 0;    // EHIP_TARGET_ITEMS: decode work-item target (0: default)
+  int32_t tail_split = 0;      // EHIP_TAIL_SPLIT: tail piece length (0: none)
   bool joint = true;           // EHIP_NO_JOINT=1: no joint items over shared prefixes
   bool prefill = true;         // EHIP_PREFILL=0: chunk rows stay on the decode kernels
   double prefill_split = 2.0;  // EHIP_PREFILL_SPLIT: key-split threshold in shares (0: none)
@@ -45,6 +46,8 @@ struct Tuning {
   bool decode_bufs3 = false;   // EHIP_DECODE_BUFS=3: three tiles in registers
   bool decode_persist = true;  // EHIP_DECODE_PERSIST=0: one workgroup per work item
   int32_t decode_slots = 0;    // EHIP_DECODE_SLOTS: cap on persistent wavefronts (0: none)
+  bool decode_qspread = true;  // EHIP_DECODE_QSPREAD=0: each sub-queue served by one XCD
+  int32_t decode_queues = 0;   // EHIP_DECODE_QUEUES: item sub-queues (0: default)
   bool decode_wg = true;       // EHIP_DECODE_WG=0: no workgroup-per-row small fp32 steps
   bool fused_append = true;    // EHIP_FUSED_APPEND=0: append and attention in two launches
 };

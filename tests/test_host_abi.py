@@ -37,18 +37,34 @@ def simple_step(ehip_mod, lens, qlens=None, bs=16, slots=None, start=0):
     return ehip_mod.StepArrays(q, lens, tabs, slots)
 
 
-def expected_items(lens, hkv, split, bs=16):
-    items = 0
+def expected_items(lens, hkv, split, bs=16, tail=256, target=2048):
+    """Items of a plan without joint groups: each row in ranges of its split
+    length; when the ranges exceed the target item count, the keys past a
+    row's last whole range go in tail pieces (unless that would take the row
+    past 64 splits)."""
+    rows = []
     for L in lens:
         s = split
         if math.ceil(L / s) > 64:
             s = min(64 * bs, math.ceil(math.ceil(L / 64) / 64) * 64)
-        items += math.ceil(L / s) * hkv
+        rows.append((int(L), s))
+    est = sum(math.ceil(L / s) for L, s in rows) * hkv
+    items = 0
+    for L, s in rows:
+        n = math.ceil(L / s)
+        if tail and tail < s and est > target:
+            pieces = L // s + math.ceil((L - (L // s) * s) / tail)
+            if pieces <= 64:
+                n = pieces
+        items += n * hkv
     return items
 
 
-def test_plan_partitions_c4_shape(ehip_mod, monkeypatch):
+@pytest.mark.parametrize("tail", [None, 0, 128, 512])
+def test_plan_partitions_c4_shape(ehip_mod, monkeypatch, tail):
     monkeypatch.setenv("EHIP_NO_JOINT", "1")  # plain per-row partition
+    if tail is not None:
+        monkeypatch.setenv("EHIP_TAIL_SPLIT", str(tail))
     from ehip import workloads
     w = workloads.c4()
     g = ehip_mod.geometry(w.heads, w.kv_heads, w.head_dim, w.block_size, w.kv_dtype,
@@ -58,8 +74,11 @@ def test_plan_partitions_c4_shape(ehip_mod, monkeypatch):
     assert rc == 0
     assert rows == 256
     assert split % 64 == 0 and 128 <= split <= 64 * w.block_size
-    assert items == expected_items(w.context_lens, w.kv_heads, split)
+    assert items == expected_items(w.context_lens, w.kv_heads, split, tail=tail or 0)
     assert partials == items  # one partial slot per (row, kv head, split)
+    if tail:
+        # C4 is past the item target: the tail pieces add items.
+        assert items > expected_items(w.context_lens, w.kv_heads, split, tail=0)
 
 
 def test_plan_split_override_and_long_rows(ehip_mod, monkeypatch):
@@ -196,7 +215,22 @@ def joint_expectation(w, split, bs=16, min_joint=128):
     return joint_len, pairs
 
 
-def test_plan_joint_items_for_shared_prefixes(ehip_mod):
+def own_ranges(L, P, split, tail):
+    """A row's ranges past its joint prefix P: whole ranges of split keys,
+    then the rest in tail pieces (if the row stays within 64 splits)."""
+    if tail and tail < split:
+        whole = (L - P) // split
+        pieces = whole + math.ceil((L - P - whole * split) / tail)
+        if math.ceil(P / split) + pieces <= 64:
+            return pieces
+    return math.ceil((L - P) / split)
+
+
+@pytest.mark.parametrize("tail", [None, 256])
+def test_plan_joint_items_for_shared_prefixes(ehip_mod, monkeypatch, tail):
+    if tail is not None:
+        monkeypatch.setenv("EHIP_TAIL_SPLIT", str(tail))
+    tail = tail or 0  # off by default; C4 is past the item target, so 256 applies
     from ehip import workloads
     w = workloads.c4()
     g = ehip_mod.geometry(w.heads, w.kv_heads, w.head_dim, w.block_size, w.kv_dtype,
@@ -210,10 +244,10 @@ def test_plan_joint_items_for_shared_prefixes(ehip_mod):
     # every pair shares exactly the blocks the workload forked (>= 8 blocks)
     assert shared <= 16 * w.notes["shared_blocks"]
     exp_joint = sum(math.ceil(joint_len[a] / split) for a, _ in pairs) * w.kv_heads
-    exp_private = sum(math.ceil((int(L) - P) / split) for L, P in zip(w.context_lens, joint_len))
+    exp_private = sum(own_ranges(int(L), P, split, tail) for L, P in zip(w.context_lens, joint_len))
     assert joint == exp_joint
     assert items == exp_joint + exp_private * w.kv_heads
-    nsplit = [math.ceil(P / split) + math.ceil((int(L) - P) / split)
+    nsplit = [math.ceil(P / split) + own_ranges(int(L), P, split, tail)
               for L, P in zip(w.context_lens, joint_len)]
     assert partials == sum(nsplit) * w.kv_heads
 
