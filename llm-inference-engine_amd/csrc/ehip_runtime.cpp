@@ -742,7 +742,7 @@ int ehip_packed_gemm(ehip_ctx* ctx, const float* d_x, int64_t m, int64_t k, cons
     return SetError(ctx, EHIP_INVALID_ARGUMENT,
                     "gemm: the packed weight must be 16-byte aligned (ehip_malloc gives 256)");
   ehip::GemmParams p{};
-  ehip::PlanPackedGemm(m, k, n, ctx->cus, &p);
+  ehip::PlanPackedGemm(m, k, n, weight_dtype, ctx->cus, &p);
   p.x = d_x;
   p.wp = d_wp;
   p.bias = d_bias;

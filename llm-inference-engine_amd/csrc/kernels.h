@@ -191,12 +191,13 @@ struct GemmParams {
   int64_t m, k, n;
   int64_t m_pad, k_pad;  // m, k rounded up to whole 64 x 64 tiles
   int64_t panels;       // ceil(n / 16)
+  int32_t group_panels;  // panels per workgroup (the weight type's tile width)
   int64_t k_split;      // k per split (a multiple of 32)
   int32_t splits;
   int32_t x_vec;        // x rows are 16-byte aligned (k % 4 == 0, aligned base)
 };
 // Tiles and k splits for a call (cus: the device's CU count).
-void PlanPackedGemm(int64_t m, int64_t k, int64_t n, int cus, GemmParams* p);
+void PlanPackedGemm(int64_t m, int64_t k, int64_t n, int weight_dtype, int cus, GemmParams* p);
 // Workspace bytes of x's planes for the planned call.
 size_t PackedGemmPlaneBytes(const GemmParams& p);
 hipError_t LaunchPackedGemm(const GemmParams& p, int weight_dtype, hipStream_t stream);

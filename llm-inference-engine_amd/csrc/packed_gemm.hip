@@ -20,12 +20,13 @@
 // writes them zero-padded to whole 64 x 64 tiles, so every column tile reads
 // ready operands instead of re-cutting x.
 //
-// Work: one workgroup of 4 wavefronts per (64 rows, 8 panels = 128 columns,
-// k range). Each k step of 64 stages x's three planes (rows padded to 72
-// elements so the 16 lanes of an A-operand read hit distinct banks) and
-// the 8 panels' 64 rows (as the weight's planes, the panel layout as stored)
-// in LDS; the next step's global loads are in flight meanwhile. A wavefront
-// owns 32 rows x 64 columns: 2 x 4 blocks of 16 x 16. The A operand of
+// Work: one workgroup of 4 wavefronts per (64 rows, BP panels, k range):
+// BP = 16 (256 columns) for bf16 weights, 8 (128) for fp16 and fp32. Each k
+// step of 64 stages x's three planes (rows padded to 72 elements so the 16
+// lanes of an A-operand read hit distinct banks) and the panels' 64 rows (as
+// the weight's planes, the panel layout as stored) in LDS; the next step's
+// global loads are in flight meanwhile. A wavefront owns 32 rows x BP/2
+// panels: 2 x BP/2 blocks of 16 x 16. The A operand of
 // lane (n, q) is row n at k = 4q..4q+3 and 16+4q..16+4q+3 (two 8-byte reads);
 // the B operand is the same k set of panel column n, read with
 // ds_read_b64_tr_b16 from the [k][16] panel rows.
@@ -49,7 +50,6 @@ typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 
 constexpr int kNr = 16;     // the reference's panel width (kernels::kNr)
 constexpr int kBM = 64;     // rows per workgroup
-constexpr int kBP = 8;      // panels per workgroup (128 columns)
 constexpr int kBK = 64;     // k per step (two 32-k MFMA chunks)
 constexpr int kXP = 3;      // bf16 planes of x
 constexpr int kXRow = 72;   // bf16 elements per LDS row of an x plane (64 + 8)
@@ -107,12 +107,16 @@ __device__ __forceinline__ bf16x4_t TransposedRead(const __bf16* p) {
   return __builtin_bit_cast(bf16x4_t, r);
 }
 
-template <int WT>
+template <int WT, int BP>
 __global__ __launch_bounds__(kThreads) void PackedGemmMfma(GemmParams p) {
   using W = WeightType<WT>;
   using T = typename W::T;
   constexpr int WP = W::WP;
   constexpr int WE = 16 * static_cast<int>(sizeof(T)) / 16;  // 16-byte loads per panel row
+  constexpr int kBP = BP;
+  constexpr int NW = kBP / 2;          // panels per wavefront
+  constexpr int KS = kThreads / kBP;   // threads per panel in the loads (k-row stride)
+  constexpr int RPT = kBK / KS;        // panel rows a thread loads per step
 
   __shared__ __align__(16) __bf16 xs[kXP][kBM * kXRow];
   __shared__ __align__(16) __bf16 ws[WP][kBP * kBK * kNr];
@@ -123,7 +127,7 @@ __global__ __launch_bounds__(kThreads) void PackedGemmMfma(GemmParams p) {
   const int n16 = lane & 15;
   const int q = lane >> 4;
   const int wr = wave >> 1;  // rows 32*wr .. +32 of the tile
-  const int wc = wave & 1;   // panels 4*wc .. +4 of the tile
+  const int wc = wave & 1;   // panels NW*wc .. +NW of the tile
   const int64_t m0 = int64_t{blockIdx.y} * kBM;
   const int pb = static_cast<int>(blockIdx.x) * kBP;
   const int split = blockIdx.z;
@@ -132,16 +136,16 @@ __global__ __launch_bounds__(kThreads) void PackedGemmMfma(GemmParams p) {
 
   // Global loads: 16 consecutive k from xk of x row xr in each plane (the
   // planes are zero-padded to whole tiles: no masks); panel rows wk and
-  // wk + 32 (16 weights each) of panel wpp.
+  // wk + KS, ... (16 weights each) of panel wpp.
   const int xr = tid >> 2, xk = (tid & 3) * 16;
   const int64_t plane = p.m_pad * p.k_pad;
   const __bf16* xrow = reinterpret_cast<const __bf16*>(p.xp) + (m0 + xr) * p.k_pad;
-  const int wpp = tid >> 5, wk = tid & 31;  // panel wpp, k rows wk and wk + 32
+  const int wpp = tid / KS, wk = tid % KS;  // panel wpp, k rows wk + KS * h
   const bool w_ok = pb + wpp < p.panels;
   const T* wpanel = static_cast<const T*>(p.wp) + (w_ok ? int64_t{pb + wpp} * p.k * kNr : 0);
 
   bf16x8_t xv[kXP][2];
-  uint4 wv[2][WE];
+  uint4 wv[RPT][WE];
   auto gload = [&](int64_t k0) {
 #pragma unroll
     for (int pl = 0; pl < kXP; ++pl)
@@ -149,8 +153,8 @@ __global__ __launch_bounds__(kThreads) void PackedGemmMfma(GemmParams p) {
       for (int h = 0; h < 2; ++h)
         xv[pl][h] = *reinterpret_cast<const bf16x8_t*>(xrow + pl * plane + k0 + xk + 8 * h);
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int64_t kw = k0 + wk + 32 * h;
+    for (int h = 0; h < RPT; ++h) {
+      const int64_t kw = k0 + wk + KS * h;
       const bool ok = w_ok && kw < ke;
       const uint4* src = reinterpret_cast<const uint4*>(wpanel + (ok ? kw : 0) * kNr);
 #pragma unroll
@@ -165,7 +169,7 @@ __global__ __launch_bounds__(kThreads) void PackedGemmMfma(GemmParams p) {
         *reinterpret_cast<bf16x8_t*>(&xs[pl][xr * kXRow + xk + 8 * h]) = xv[pl][h];
     // Each panel row as WP planes: 16 weights, two 16-byte stores per plane.
 #pragma unroll
-    for (int hr = 0; hr < 2; ++hr) {
+    for (int hr = 0; hr < RPT; ++hr) {
       const T* w = reinterpret_cast<const T*>(wv[hr]);
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
@@ -183,17 +187,17 @@ __global__ __launch_bounds__(kThreads) void PackedGemmMfma(GemmParams p) {
         }
 #pragma unroll
         for (int pl = 0; pl < WP; ++pl)
-          *reinterpret_cast<bf16x8_t*>(&ws[pl][(wpp * kBK + wk + 32 * hr) * kNr + 8 * h]) =
+          *reinterpret_cast<bf16x8_t*>(&ws[pl][(wpp * kBK + wk + KS * hr) * kNr + 8 * h]) =
               wpl[pl];
       }
     }
   };
 
-  f32x4_t acc[2][4];
+  f32x4_t acc[2][NW];
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb) acc[rb][cb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int cb = 0; cb < NW; ++cb) acc[rb][cb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   auto compute = [&]() {
 #pragma unroll
@@ -211,8 +215,8 @@ __global__ __launch_bounds__(kThreads) void PackedGemmMfma(GemmParams p) {
       }
     }
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb) {
-      const int panel = 4 * wc + cb;
+    for (int cb = 0; cb < NW; ++cb) {
+      const int panel = NW * wc + cb;
       bf16x8_t b[WP];
 #pragma unroll
       for (int pl = 0; pl < WP; ++pl) {
@@ -248,10 +252,10 @@ __global__ __launch_bounds__(kThreads) void PackedGemmMfma(GemmParams p) {
     compute();
   }
 
-  // acc[rb][cb][i] = y[row 32wr + 16rb + 4q + i][column of panel 4wc + cb, n16].
+  // acc[rb][cb][i] = y[row 32wr + 16rb + 4q + i][column of panel NW wc + cb, n16].
 #pragma unroll
-  for (int cb = 0; cb < 4; ++cb) {
-    const int64_t col = int64_t{pb + 4 * wc + cb} * kNr + n16;
+  for (int cb = 0; cb < NW; ++cb) {
+    const int64_t col = int64_t{pb + NW * wc + cb} * kNr + n16;
     if (col >= p.n) continue;
     const float bias = (p.splits == 1 && p.bias) ? p.bias[col] : 0.f;
 #pragma unroll
@@ -329,7 +333,14 @@ __global__ __launch_bounds__(256) void PackPanels(const T* w, int64_t n, int64_t
 
 }  // namespace
 
-void PlanPackedGemm(int64_t m, int64_t k, int64_t n, int cus, GemmParams* p) {
+void PlanPackedGemm(int64_t m, int64_t k, int64_t n, int weight_dtype, int cus, GemmParams* p) {
+  // 16 panels (256 columns) per workgroup for bf16 weights and up to 256
+  // rows: each x row is then staged for twice the columns (C4 o_proj 58.5 ->
+  // 56 us, C5 63 -> 60 us). Taller calls keep 8 (C3's 2382 rows: 350 against
+  // 365 us at 16), as do fp16 and fp32 weights, whose two or three weight
+  // planes would not fit LDS at 16.
+  const int kBP = (weight_dtype == EHIP_WEIGHT_BF16 && m <= 256) ? 16 : 8;
+  p->group_panels = kBP;
   p->m = m;
   p->k = k;
   p->n = n;
@@ -338,10 +349,12 @@ void PlanPackedGemm(int64_t m, int64_t k, int64_t n, int cus, GemmParams* p) {
   p->panels = (n + kNr - 1) / kNr;
   const int64_t tiles = ((m + kBM - 1) / kBM) * ((p->panels + kBP - 1) / kBP);
   const int64_t steps = (k + kBK - 1) / kBK;
-  // Enough workgroups for four per CU (a workgroup keeps one step of loads
-  // in flight, so the chip's share of them sets the bandwidth); each split
-  // keeps at least 2 steps.
-  int64_t splits = (4 * int64_t{cus} + tiles - 1) / tiles;
+  // Enough workgroups for one round at the tile's occupancy (two per CU for
+  // the 256-column tile, about four otherwise: a workgroup keeps one step of
+  // loads in flight, so the chip's share of them sets the bandwidth); each
+  // split keeps at least 2 steps.
+  const int64_t per_cu = kBP == 16 ? 2 : 4;
+  int64_t splits = (per_cu * int64_t{cus} + tiles - 1) / tiles;
   splits = splits < 1 ? 1 : splits;
   const int64_t max_splits = steps / 2 > 1 ? steps / 2 : 1;
   splits = splits > max_splits ? max_splits : splits;
@@ -363,17 +376,22 @@ hipError_t LaunchPackedGemm(const GemmParams& p, int weight_dtype, hipStream_t s
                        stream, p, reinterpret_cast<__bf16*>(p.xp));
     if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
   }
-  const dim3 grid(static_cast<uint32_t>((p.panels + kBP - 1) / kBP),
+  const dim3 grid(static_cast<uint32_t>((p.panels + p.group_panels - 1) / p.group_panels),
                   static_cast<uint32_t>((p.m + kBM - 1) / kBM), static_cast<uint32_t>(p.splits));
   switch (weight_dtype) {
     case EHIP_WEIGHT_F32:
-      hipLaunchKernelGGL(PackedGemmMfma<EHIP_WEIGHT_F32>, grid, dim3(kThreads), 0, stream, p);
+      hipLaunchKernelGGL((PackedGemmMfma<EHIP_WEIGHT_F32, 8>), grid, dim3(kThreads), 0, stream, p);
       break;
     case EHIP_WEIGHT_BF16:
-      hipLaunchKernelGGL(PackedGemmMfma<EHIP_WEIGHT_BF16>, grid, dim3(kThreads), 0, stream, p);
+      if (p.group_panels == 16)
+        hipLaunchKernelGGL((PackedGemmMfma<EHIP_WEIGHT_BF16, 16>), grid, dim3(kThreads), 0, stream,
+                           p);
+      else
+        hipLaunchKernelGGL((PackedGemmMfma<EHIP_WEIGHT_BF16, 8>), grid, dim3(kThreads), 0, stream,
+                           p);
       break;
     case EHIP_WEIGHT_F16:
-      hipLaunchKernelGGL(PackedGemmMfma<EHIP_WEIGHT_F16>, grid, dim3(kThreads), 0, stream, p);
+      hipLaunchKernelGGL((PackedGemmMfma<EHIP_WEIGHT_F16, 8>), grid, dim3(kThreads), 0, stream, p);
       break;
     default:
       return hipErrorInvalidValue;
