@@ -17,7 +17,11 @@ pytestmark = pytest.mark.gpu
 # (32 rows, 896 -> 896), a C3-sized chunk slice (600 rows).
 SHAPES = [(16, 64, 64), (16, 64, 96), (16, 176, 64), (8, 64, 512), (1, 64, 64),
           (1, 2048, 512), (4, 2048, 8192), (33, 8192, 256), (130, 300, 70), (7, 1, 33),
-          (65, 129, 1000), (5, 40, 17), (256, 4096, 4096), (32, 896, 896), (600, 4096, 1024)]
+          (65, 129, 1000), (5, 40, 17), (32, 896, 896)]
+# The largest shapes run for the bf16 checkpoints the configs use (the CPU
+# oracle's fp32 and fp16 passes at these sizes would dominate the suite).
+CASES = ([(s, d) for s in SHAPES for d in ("bf16", "f16", "f32")] +
+         [((256, 4096, 4096), "bf16"), ((600, 4096, 1024), "bf16")])
 
 
 def _weights(orc, ehip_mod, n, k, dtype, seed):
@@ -48,12 +52,10 @@ def _run(gctx, ehip_mod, x, w, dtype, bias):
     return y, wp, dwp
 
 
-@pytest.mark.parametrize("m,k,n", SHAPES)
-@pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
-def test_packed_gemm_matches_reference_tile(gctx, ehip_mod, orc, m, k, n, dtype):
+@pytest.mark.parametrize("shape,dtype", CASES, ids=lambda v: "x".join(map(str, v)) if isinstance(v, tuple) else v)
+def test_packed_gemm_matches_reference_tile(gctx, ehip_mod, orc, shape, dtype):
+    m, k, n = shape
     dt = {"bf16": ehip_mod.WEIGHT_BF16, "f16": ehip_mod.WEIGHT_F16, "f32": ehip_mod.WEIGHT_F32}[dtype]
-    if m * k * n > 1e9 and dtype != "bf16":
-        pytest.skip("largest shapes run for the bf16 checkpoints the configs use")
     seed = 100 + m + k + n
     x = orc.fill_normal(m * k, 0.0, 1.0, seed).reshape(m, k)
     w = _weights(orc, ehip_mod, n, k, dt, seed + 1)
