@@ -60,7 +60,7 @@ struct ItemRef {
   int tb;
   int te;
   int table_off;
-  int first[2];  // block ids of the first two 16-token halves, or -1
+  int first[4];  // block ids of the first four 16-token halves, or -1
   bool last;     // the range ends at its row's last key
 };
 
@@ -78,6 +78,8 @@ __device__ __forceinline__ ItemRef DecodeItem(const WorkItem& it) {
   r.table_off = it.table_off;
   r.first[0] = it.first_block0;
   r.first[1] = it.first_block1;
+  r.first[2] = it.first_block2;
+  r.first[3] = it.first_block3;
   return r;
 }
 

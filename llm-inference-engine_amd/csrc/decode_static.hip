@@ -54,7 +54,7 @@ __global__ __launch_bounds__(64) void WriteRowPlan(RowDesc* rows, WorkItem* item
   const int hk = i - s * kv_heads;
   const int tb = s * split_len;
   const int te = min(length, tb + split_len);
-  items[i] = WorkItem{0, -1, tb, te, hk | (s << kHkBits), 0, -1, -1};
+  items[i] = WorkItem{0, -1, tb, te, hk | (s << kHkBits), 0, -1, -1, -1, -1};
 }
 
 size_t Align256(size_t x) { return (x + 255) & ~size_t{255}; }

@@ -208,14 +208,16 @@ void DecodeMfma(DecodeParams p) {
   // slab rows never reach the PV sums, whatever they hold), and a half beyond
   // the range, or on a rejected block id, gets an empty descriptor whose loads
   // return zeros without touching memory. Scores of such rows are masked.
-  // given: the halves' block ids come from the work item (first tile only).
-  auto load = [&](T& t, int t0, bool given) {
+  // gh >= 0: the halves' block ids come from the work item, which carries
+  // the item's first four halves (gh: the tile's first half); gh < 0: from
+  // the table slice.
+  auto load = [&](T& t, int t0, int gh) {
 #pragma unroll
     for (int h2 = 0; h2 < TH; ++h2) {
       const int th = t0 + 16 * h2;  // wavefront-uniform; a half lies in one block (bs >= 16)
       const int phys =
-          given ? it.first[h2 > 0 ? 1 : 0]
-                : __builtin_amdgcn_readlane(tab, max(0, min(th, kend - 1) / bs - lb0));
+          gh >= 0 ? it.first[min(gh + h2, 3)]
+                  : __builtin_amdgcn_readlane(tab, max(0, min(th, kend - 1) / bs - lb0));
       const bool ok = th < kend && phys >= 0;
       t.phys[h2] = ok ? phys : -1;
       const int64_t boff = int64_t{ok ? phys : 0} * p.block_stride + (th & bmask) * D;
@@ -243,13 +245,18 @@ void DecodeMfma(DecodeParams p) {
   };
 
   T bufA, bufB, bufC;
-  // First tiles in flight while Q is split; the first one does not wait for
-  // the table when the item carries its block ids.
-  if (it.first[0] >= 0)
-    load(bufA, tb, true);
-  else
-    load(bufA, tb, false);
-  if constexpr (NBUF == 3) load(bufB, tb + TT, false);
+  // The first two tiles go in flight at once, while Q is split; when the
+  // item carries their block ids neither waits for the table slice.
+  if (it.first[0] >= 0) {
+    load(bufA, tb, 0);
+    if (it.first[TT / 16] >= 0)
+      load(bufB, tb + TT, TT / 16);
+    else
+      load(bufB, tb + TT, -1);
+  } else {
+    load(bufA, tb, -1);
+    load(bufB, tb + TT, -1);
+  }
 
   // Fused append: the item ending at its row's last key stores that key's
   // new K/V rows at the row's slot for later steps (bf16 slabs: narrowed with
@@ -451,22 +458,22 @@ void DecodeMfma(DecodeParams p) {
   // is empty: every score masked, the state unchanged.)
   if constexpr (NBUF == 2) {
     for (int t0 = tb;; t0 += 2 * TT) {
-      load(bufB, t0 + TT, false);
       process(bufA, t0, kend);
       if (t0 + TT >= kend) break;
-      load(bufA, t0 + 2 * TT, false);
+      load(bufA, t0 + 2 * TT, -1);
       process(bufB, t0 + TT, kend);
       if (t0 + 2 * TT >= kend) break;
+      load(bufB, t0 + 3 * TT, -1);
     }
   } else {
     for (int t0 = tb;; t0 += 3 * TT) {
-      load(bufC, t0 + 2 * TT, false);
+      load(bufC, t0 + 2 * TT, -1);
       process(bufA, t0, kend);
       if (t0 + TT >= kend) break;
-      load(bufA, t0 + 3 * TT, false);
+      load(bufA, t0 + 3 * TT, -1);
       process(bufB, t0 + TT, kend);
       if (t0 + 2 * TT >= kend) break;
-      load(bufB, t0 + 4 * TT, false);
+      load(bufB, t0 + 4 * TT, -1);
       process(bufC, t0 + 2 * TT, kend);
       if (t0 + 3 * TT >= kend) break;
     }

@@ -177,13 +177,15 @@ void DecodeMfmaQ8(DecodeParams p) {
   const __amdgpu_buffer_rsrc_t rvs = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<float*>(p.v_scale), 0, scale_range, 0x00020000);
 
-  auto load = [&](T& t, int t0, bool given) {
+  // gh >= 0: the halves' block ids come from the work item (its first four
+  // halves; gh: the tile's first half); gh < 0: from the table slice.
+  auto load = [&](T& t, int t0, int gh) {
 #pragma unroll
     for (int h2 = 0; h2 < TH; ++h2) {
       const int th = t0 + 16 * h2;  // wavefront-uniform; a half lies in one block (bs >= 16)
       const int bi = min(th, te - 1) / bs - lb0;  // wavefront-uniform, < 128
-      const int phys = given ? it.first[h2 > 0 ? 1 : 0]
-                             : __builtin_amdgcn_readlane(bi < 64 ? tab : tab2, bi & 63);
+      const int phys = gh >= 0 ? it.first[min(gh + h2, 3)]
+                               : __builtin_amdgcn_readlane(bi < 64 ? tab : tab2, bi & 63);
       const bool ok = th < te && phys >= 0;
       t.phys[h2] = ok ? phys : -1;
       const int64_t boff = int64_t{ok ? phys : 0} * p.block_stride + (th & bmask) * D;
@@ -207,10 +209,18 @@ void DecodeMfmaQ8(DecodeParams p) {
   };
 
   T bufA, bufB;
-  if (it.first[0] >= 0)
-    load(bufA, tb, true);
-  else
-    load(bufA, tb, false);
+  // The first two tiles go in flight at once; when the item carries their
+  // block ids neither waits for the table slice.
+  if (it.first[0] >= 0) {
+    load(bufA, tb, 0);
+    if (it.first[TT / 16] >= 0)
+      load(bufB, tb + TT, TT / 16);
+    else
+      load(bufB, tb + TT, -1);
+  } else {
+    load(bufA, tb, -1);
+    load(bufB, tb + TT, -1);
+  }
 
   // Query operands: int8, three digits per 16-element chunk (KL chunks);
   // FP8 keys, bf16 hi + lo per 8-element chunk (KB / 8 chunks).
@@ -398,12 +408,12 @@ void DecodeMfmaQ8(DecodeParams p) {
   };
 
   for (int t0 = tb;; t0 += 2 * TT) {
-    load(bufB, t0 + TT, false);
     process(bufA, t0);
     if (t0 + TT >= te) break;
-    load(bufA, t0 + 2 * TT, false);
+    load(bufA, t0 + 2 * TT, -1);
     process(bufB, t0 + TT);
     if (t0 + 2 * TT >= te) break;
+    load(bufB, t0 + 3 * TT, -1);
   }
 
   ReportRejectedBlocks(p, tab);

@@ -56,6 +56,10 @@ Tuning ReadTuning() {
     const long x = std::strtol(v, nullptr, 10);
     if (x >= 0) t.tail_split = static_cast<int32_t>(std::min<long>(x, INT32_MAX / 2));
   }
+  if (const char* v = std::getenv("EHIP_TAIL_FRAC")) {
+    const double x = std::strtod(v, nullptr);
+    if (x >= 0 && x <= 1) t.tail_frac = x;
+  }
   t.joint = flag("EHIP_NO_JOINT", '1');
   t.prefill = flag("EHIP_PREFILL", '0');
   if (const char* v = std::getenv("EHIP_PREFILL_SPLIT")) t.prefill_split = std::strtod(v, nullptr);
@@ -184,6 +188,71 @@ struct KeyRange {
   bool joint() const { return rows[1] >= 0; }
 };
 
+// Tail pieces. When a step has more items than the queue hands out first,
+// the queue's last items set the launch's end: a wavefront streams ~3 GB/s
+// (a 1024-key bf16 range of d = 128 takes ~170 us), and on C4 the items that
+// started in the last 120 us were up to 648 keys long, ~8% of the step's
+// keys. The smallest single-row ranges, up to Tuning::tail_frac of the
+// step's keys (times rows), are cut into pieces of Tuning::tail_split keys;
+// ordered costliest first, the pieces are the queue's last items. A row keeps
+// at most kMaxSplitsPerRow ranges. Off by default: every extra item costs its
+// wavefront ~8 us of startup, more than the shorter tail saves (C4 attention
+// call, 100 interleaved calls each: 398.8 us without pieces, 404.9 / 407.9 /
+// 413.8 us with 128-key pieces over 5 / 8 / 12% of the keys).
+void CutTail(const ehip_geometry& g, const Tuning& tune, const std::vector<RowDesc>& rows,
+             std::vector<KeyRange>* ranges) {
+  const int32_t ts = static_cast<int32_t>(RoundUp(tune.tail_split, kTile));
+  const int64_t target = tune.target_items > 0 ? tune.target_items : kTargetItems;
+  if (ts <= 0 || tune.tail_frac <= 0 ||
+      static_cast<int64_t>(ranges->size()) * g.kv_heads <= target)
+    return;
+  std::vector<KeyRange>& rg = *ranges;
+  int64_t total = 0;
+  std::vector<int32_t> count(rows.size(), 0);
+  std::vector<size_t> cand;
+  for (size_t i = 0; i < rg.size(); ++i) {
+    int rws = 0;
+    for (int32_t r : rg[i].rows)
+      if (r >= 0) {
+        ++rws;
+        ++count[r];
+      }
+    total += int64_t{rg[i].te - rg[i].tb} * rws;
+    if (!rg[i].joint() && rg[i].te - rg[i].tb > ts) cand.push_back(i);
+  }
+  std::stable_sort(cand.begin(), cand.end(), [&](size_t a, size_t b) {
+    return rg[a].te - rg[a].tb < rg[b].te - rg[b].tb;
+  });
+  const double budget = tune.tail_frac * static_cast<double>(total);
+  int64_t acc = 0;
+  std::vector<char> cut(rg.size(), 0);
+  for (size_t i : cand) {
+    const int32_t len = rg[i].te - rg[i].tb;
+    if (static_cast<double>(acc + len) > budget) break;
+    const int32_t r = rg[i].rows[0];
+    const int32_t extra = (len + ts - 1) / ts - 1;
+    if (count[r] + extra > kMaxSplitsPerRow) continue;
+    count[r] += extra;
+    acc += len;
+    cut[i] = 1;
+  }
+  std::vector<KeyRange> out;
+  out.reserve(rg.size() + static_cast<size_t>(acc / ts) + 1);
+  for (size_t i = 0; i < rg.size(); ++i) {
+    if (!cut[i]) {
+      out.push_back(rg[i]);
+      continue;
+    }
+    for (int32_t t = rg[i].tb; t < rg[i].te; t += ts) {
+      KeyRange kr = rg[i];
+      kr.tb = t;
+      kr.te = std::min(rg[i].te, t + ts);
+      out.push_back(kr);
+    }
+  }
+  rg.swap(out);
+}
+
 // Groups rows that share leading blocks (greedy over rows ordered by their
 // first block id and table), splits every row into whole-tile key ranges
 // (joint ranges first), assigns partial slots and orders the work longest
@@ -280,39 +349,13 @@ void FinishPlan(const ehip_geometry& g, const Tuning& tune, Plan* plan, bool all
       ranges.push_back(kr);
     }
   }
-  // Tail pieces (Tuning::tail_split > 0): when a step has more items than
-  // the queue hands out first, the keys of each row past its last whole
-  // range go out in pieces of that length. Ordered costliest first, they are
-  // the queue's last items, so the wavefronts that free up first share the
-  // end of the launch in small steps instead of the last whole ranges (one
-  // wavefront streams ~3 GB/s: a 1024-key bf16 range of d = 128 takes
-  // ~170 us). Off by default: on C4, 256-key pieces measured no faster and
-  // their extra partials cost the merge 1.5 us.
-  int32_t ts = static_cast<int32_t>(RoundUp(tune.tail_split, kTile));
-  if (ts > 0) {
-    // Items at whole ranges: the queue is active only past the target.
-    int64_t est = static_cast<int64_t>(ranges.size());
-    for (size_t r = 0; r < n; ++r)
-      if (!skipped(r))
-        est += (plan->rows[r].length - joint_len[r] + split_len[r] - 1) / split_len[r];
-    const int64_t target = tune.target_items > 0 ? tune.target_items : kTargetItems;
-    if (est * g.kv_heads <= target) ts = 0;
-  }
   for (size_t r = 0; r < n; ++r) {
     if (skipped(r)) continue;
-    const int32_t sl = split_len[r], L = plan->rows[r].length, P = joint_len[r];
-    int32_t head_end = L;  // [P, head_end) in ranges of sl, [head_end, L) in tail pieces
-    if (ts > 0 && ts < sl) {
-      const int32_t whole = (L - P) / sl;
-      const int32_t e = P + whole * sl;
-      const int32_t joint_splits = (P + sl - 1) / sl;
-      if (joint_splits + whole + (L - e + ts - 1) / ts <= kMaxSplitsPerRow) head_end = e;
-    }
-    for (int32_t t = P; t < head_end; t += sl)
-      ranges.push_back(KeyRange{{static_cast<int32_t>(r), -1, -1, -1}, t, std::min(head_end, t + sl)});
-    for (int32_t t = head_end; t < L; t += ts)
-      ranges.push_back(KeyRange{{static_cast<int32_t>(r), -1, -1, -1}, t, std::min(L, t + ts)});
+    const int32_t sl = split_len[r], L = plan->rows[r].length;
+    for (int32_t t = joint_len[r]; t < L; t += sl)
+      ranges.push_back(KeyRange{{static_cast<int32_t>(r), -1, -1, -1}, t, std::min(L, t + sl)});
   }
+  CutTail(g, tune, plan->rows, &ranges);
 
   // Split indices follow key order within a row. Joint ranges cover the
   // leading keys of every member, so numbering them first (in key order)
@@ -358,7 +401,7 @@ void FinishPlan(const ehip_geometry& g, const Tuning& tune, Plan* plan, bool all
     for (int32_t hk = 0; hk < g.kv_heads; ++hk)
       entries.push_back(Entry{WorkItem{kr.rows[0], kr.rows[1], kr.tb, kr.te,
                                        PackHkSplit(hk, split_of[i]) | (last ? kLastRangeFlag : 0),
-                                       plan->rows[kr.rows[0]].table_off, 0, 0},
+                                       plan->rows[kr.rows[0]].table_off, 0, 0, 0, 0},
                               ItemRowsX{kr.rows[2], kr.rows[3]}});
   }
   plan->joint_items = static_cast<int64_t>(n_joint_ranges) * g.kv_heads;
@@ -380,17 +423,21 @@ void FinishPlan(const ehip_geometry& g, const Tuning& tune, Plan* plan, bool all
     plan->items_x.reserve(entries.size());
     for (const Entry& e : entries) plan->items_x.push_back(e.x);
   }
-  // The block ids of each item's first two 16-token halves ride in the item,
-  // so a wavefront can issue its first K/V loads without waiting for its
-  // table slice (-1 when the table is device-resident and unknown here).
+  // The block ids of each item's first four 16-token halves ride in the
+  // item, so a wavefront issues its first two tiles' K/V loads at once
+  // without waiting for its table slice (-1 when the table is
+  // device-resident and unknown here).
   for (WorkItem& w : plan->items) {
     if (plan->table_ids.empty()) {
-      w.first_block0 = w.first_block1 = -1;
+      w.first_block0 = w.first_block1 = w.first_block2 = w.first_block3 = -1;
       continue;
     }
     const int32_t* t = plan->table_ids.data() + w.table_off;
-    w.first_block0 = t[w.tok_begin / g.block_size];
-    w.first_block1 = t[std::min(w.tok_begin + 16, w.tok_end - 1) / g.block_size];
+    auto at = [&](int32_t off) { return t[std::min(w.tok_begin + off, w.tok_end - 1) / g.block_size]; };
+    w.first_block0 = at(0);
+    w.first_block1 = at(16);
+    w.first_block2 = at(32);
+    w.first_block3 = at(48);
   }
 }
 

@@ -37,7 +37,8 @@ namespace ehip {
 struct Tuning {
   int32_t split_tokens = 0;    // EHIP_SPLIT_TOKENS: fixed base split length (0: per step)
   int64_t target_items = 0;    // EHIP_TARGET_ITEMS: decode work-item target (0: default)
-  int32_t tail_split = 0;      // EHIP_TAIL_SPLIT: tail piece length (0: none)
+  int32_t tail_split = 0;      // EHIP_TAIL_SPLIT: tail piece length in keys (0: no tail pieces)
+  double tail_frac = 0.08;     // EHIP_TAIL_FRAC: share of the step's keys cut into tail pieces
   bool joint = true;           // EHIP_NO_JOINT=1: no joint items over shared prefixes
   bool prefill = true;         // EHIP_PREFILL=0: chunk rows stay on the decode kernels
   double prefill_split = 2.0;  // EHIP_PREFILL_SPLIT: key-split threshold in shares (0: none)
@@ -83,6 +84,8 @@ struct WorkItem {
   int32_t table_off;
   int32_t first_block0;  // block id of token tok_begin (-1: read the table)
   int32_t first_block1;  // block id of token min(tok_begin + 16, tok_end - 1)
+  int32_t first_block2;  // block id of token min(tok_begin + 32, tok_end - 1)
+  int32_t first_block3;  // block id of token min(tok_begin + 48, tok_end - 1)
 };
 
 // Rows 3 and 4 of a joint item (-1 where absent), parallel to the work list

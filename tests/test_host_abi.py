@@ -37,27 +37,45 @@ def simple_step(ehip_mod, lens, qlens=None, bs=16, slots=None, start=0):
     return ehip_mod.StepArrays(q, lens, tabs, slots)
 
 
-def expected_items(lens, hkv, split, bs=16, tail=256, target=2048):
+def cut_tail(ranges, hkv, tail, frac=0.08, target=2048):
+    """Range count per row after the planner's tail pieces. ranges: list of
+    (rows, length) in the planner's order (joint ranges first, then rows in
+    order, each in key order). When the ranges exceed the target item count,
+    the smallest single-row ranges longer than the piece length, up to frac of
+    the keys (times rows), are cut into pieces (a row keeps <= 64 ranges)."""
+    count = {}
+    for rows, _ in ranges:
+        for r in rows:
+            count[r] = count.get(r, 0) + 1
+    tail = -(-tail // 64) * 64 if tail else 0
+    if not tail or frac <= 0 or len(ranges) * hkv <= target:
+        return count
+    total = sum(n * len(rows) for rows, n in ranges)
+    cand = sorted((i for i, (rows, n) in enumerate(ranges) if len(rows) == 1 and n > tail),
+                  key=lambda i: ranges[i][1])
+    acc = 0
+    for i in cand:
+        rows, n = ranges[i]
+        if acc + n > frac * total:
+            break
+        extra = -(-n // tail) - 1
+        if count[rows[0]] + extra > 64:
+            continue
+        count[rows[0]] += extra
+        acc += n
+    return count
+
+
+def expected_items(lens, hkv, split, bs=16, tail=0):
     """Items of a plan without joint groups: each row in ranges of its split
-    length; when the ranges exceed the target item count, the keys past a
-    row's last whole range go in tail pieces (unless that would take the row
-    past 64 splits)."""
-    rows = []
-    for L in lens:
+    length (grown to keep at most 64 per row), then the tail pieces."""
+    ranges = []
+    for r, L in enumerate(lens):
         s = split
         if math.ceil(L / s) > 64:
             s = min(64 * bs, math.ceil(math.ceil(L / 64) / 64) * 64)
-        rows.append((int(L), s))
-    est = sum(math.ceil(L / s) for L, s in rows) * hkv
-    items = 0
-    for L, s in rows:
-        n = math.ceil(L / s)
-        if tail and tail < s and est > target:
-            pieces = L // s + math.ceil((L - (L // s) * s) / tail)
-            if pieces <= 64:
-                n = pieces
-        items += n * hkv
-    return items
+        ranges += [((r,), min(s, int(L) - t)) for t in range(0, int(L), s)]
+    return sum(cut_tail(ranges, hkv, tail).values()) * hkv
 
 
 @pytest.mark.parametrize("tail", [None, 0, 128, 512])
@@ -76,7 +94,7 @@ def test_plan_partitions_c4_shape(ehip_mod, monkeypatch, tail):
     assert split % 64 == 0 and 128 <= split <= 64 * w.block_size
     assert items == expected_items(w.context_lens, w.kv_heads, split, tail=tail or 0)
     assert partials == items  # one partial slot per (row, kv head, split)
-    if tail:
+    if tail and tail < split:
         # C4 is past the item target: the tail pieces add items.
         assert items > expected_items(w.context_lens, w.kv_heads, split, tail=0)
 
@@ -215,17 +233,6 @@ def joint_expectation(w, split, bs=16, min_joint=128):
     return joint_len, pairs
 
 
-def own_ranges(L, P, split, tail):
-    """A row's ranges past its joint prefix P: whole ranges of split keys,
-    then the rest in tail pieces (if the row stays within 64 splits)."""
-    if tail and tail < split:
-        whole = (L - P) // split
-        pieces = whole + math.ceil((L - P - whole * split) / tail)
-        if math.ceil(P / split) + pieces <= 64:
-            return pieces
-    return math.ceil((L - P) / split)
-
-
 @pytest.mark.parametrize("tail", [None, 256])
 def test_plan_joint_items_for_shared_prefixes(ehip_mod, monkeypatch, tail):
     if tail is not None:
@@ -244,12 +251,18 @@ def test_plan_joint_items_for_shared_prefixes(ehip_mod, monkeypatch, tail):
     # every pair shares exactly the blocks the workload forked (>= 8 blocks)
     assert shared <= 16 * w.notes["shared_blocks"]
     exp_joint = sum(math.ceil(joint_len[a] / split) for a, _ in pairs) * w.kv_heads
-    exp_private = sum(own_ranges(int(L), P, split, tail) for L, P in zip(w.context_lens, joint_len))
+    ranges = []
+    for a, b in pairs:
+        P = joint_len[a]
+        ranges += [((a, b), min(split, P - t)) for t in range(0, P, split)]
+    for r, L in enumerate(w.context_lens):
+        P = joint_len[r]
+        ranges += [((r,), min(split, int(L) - t)) for t in range(P, int(L), split)]
+    nsplit = cut_tail(ranges, w.kv_heads, tail)
+    n_ranges = len(ranges) + sum(nsplit.values()) - sum(len(rw) for rw, _ in ranges)
     assert joint == exp_joint
-    assert items == exp_joint + exp_private * w.kv_heads
-    nsplit = [math.ceil(P / split) + own_ranges(int(L), P, split, tail)
-              for L, P in zip(w.context_lens, joint_len)]
-    assert partials == sum(nsplit) * w.kv_heads
+    assert items == n_ranges * w.kv_heads
+    assert partials == sum(nsplit.values()) * w.kv_heads
 
 
 def greedy_groups(order, shared_blocks, cap, bs=16, min_joint=128):
