@@ -86,6 +86,22 @@ __device__ __forceinline__ void VPair(uint2 r, float& v0, float& v1) {
   v1 = __uint_as_float(r.y);
 }
 
+// Orders a wavefront's own LDS stores before its later reads (and the reads
+// before later stores) within an item. A one-wavefront workgroup uses the
+// workgroup barrier; with several wavefronts per item each wavefront walks
+// its own tiles, so the order is kept at wavefront scope (LDS operations of
+// one wavefront execute in issue order).
+template <int WPI>
+__device__ __forceinline__ void ItemSync() {
+  if constexpr (WPI == 1) {
+    __syncthreads();
+  } else {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+}
+
 // KV: uint16_t (bf16 slabs; K is the MFMA B operand as stored) or float (fp32
 // slabs, d = 64: Q and each K row are split into three bf16 parts and the six
 // leading products are accumulated, so the scores keep fp32 accuracy; V stays
@@ -95,8 +111,16 @@ __device__ __forceinline__ void VPair(uint2 r, float& v0, float& v1) {
 // OCC: wavefronts per SIMD the register allocation must allow.
 // FUSE: the launch carries the step's new K/V rows (fused append); the
 // instance without it has no append code at all.
-template <class KV, int D, int G, int RMAX, int TH, int NBUF, bool QL, int OCC, bool FUSE>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(OCC)))
+// WPI: wavefronts per work item. With WPI > 1 (launches whose grid covers
+// every item, no queue) the item's whole tiles are cut into WPI contiguous
+// runs, one per wavefront of the workgroup; each wavefront keeps its own
+// softmax state and the workgroup combines the WPI states in LDS
+// (log-sum-exp, as the split merge does) before wavefront 0 stores the item's
+// result: an item's latency is then its wavefronts' shorter walks, with no
+// more split partials for the merge launch to read.
+template <class KV, int D, int G, int RMAX, int TH, int NBUF, bool QL, int OCC, bool FUSE,
+          int WPI = 1>
+__global__ __launch_bounds__(64 * WPI) __attribute__((amdgpu_waves_per_eu(OCC)))
 void DecodeMfma(DecodeParams p) {
   using T = Tile<KV, D, TH>;
   constexpr bool F32 = sizeof(KV) == 4;
@@ -110,8 +134,9 @@ void DecodeMfma(DecodeParams p) {
   constexpr int VT = T::VT;
   constexpr int VJ = T::VJ;
   static_assert(GV >= 1 && GV <= 16 && (D == 64 || D == 128), "shape");
+  static_assert(WPI == 1 || (!QL && NBUF == 2), "items over several wavefronts: Q in registers");
 
-  __shared__ float p_lds[TT * HP];
+  __shared__ float p_lds_all[WPI][TT * HP];
   constexpr int NQ = F32 ? 3 : 2;  // bf16 parts of Q
   __shared__ uint4 q_lds[QL ? NQ * NC * 64 : 1];
   // Fused append: the row's new K row as stored (bf16 or fp32) and its V
@@ -119,7 +144,9 @@ void DecodeMfma(DecodeParams p) {
   __shared__ uint4 knew_lds[FUSE ? D * static_cast<int>(sizeof(KV)) / 16 : 1];
   __shared__ typename T::VW vnew_lds[FUSE ? D / 2 : 1];
 
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wv = WPI > 1 ? static_cast<int>(threadIdx.x >> 6) : 0;  // wavefront of the item
+  float* const p_lds = p_lds_all[wv];
   // Persistent wavefronts: a workgroup's first item is its index; each later
   // one comes by ticket from the workgroup's sub-queue. The ticket
   // is drawn when at most kDrawAhead keys of the current item remain: late
@@ -140,7 +167,7 @@ void DecodeMfma(DecodeParams p) {
   // below gridDim.x are first items (workgroup i starts with item i), the
   // rest go out by ticket, from the first such index at or above gridDim.x.
   const int nq = min(p.queues, static_cast<int>(gridDim.x));
-  const bool queued = static_cast<int>(gridDim.x) < p.n_items;
+  const bool queued = WPI == 1 && static_cast<int>(gridDim.x) < p.n_items;
   // Workgroup b runs on XCD b mod 8. Spread: sub-queue (b / 8) mod nq, served
   // by workgroups of every XCD (a grid of at least 8 nq workgroups gives
   // every sub-queue some); else b mod nq, one XCD's workgroups per sub-queue.
@@ -199,9 +226,17 @@ void DecodeMfma(DecodeParams p) {
   // Fused append: the item ending at its row's last key (position te - 1)
   // streams keys [tb, te - 1) from the slab and takes the new key from the
   // step's new rows in one more step after the loop.
-  const bool fuse = FUSE && it.last;  // wavefront-uniform
+  const bool fuse_item = FUSE && it.last;        // workgroup-uniform
+  const bool fuse = fuse_item && wv == WPI - 1;  // the wavefront that appends
   const int newpos = te - 1;
-  const int kend = fuse ? newpos : te;  // keys the tile loop reads from the slab
+  const int kend = fuse_item ? newpos : te;  // keys the tile loops read from the slab
+  // This wavefront's slab keys [wtb, wte): the item's whole tiles in WPI runs.
+  int wtb = tb, wte = kend;
+  if constexpr (WPI > 1) {
+    const int per = ((kend - tb + TT - 1) / TT + WPI - 1) / WPI;
+    wtb = min(kend, tb + wv * per * TT);
+    wte = min(kend, tb + (wv + 1) * per * TT);
+  }
 
   // Each half's descriptor starts at its first token row and covers only the
   // rows inside the range: rows past the range end read as zeros (so stale
@@ -247,15 +282,15 @@ void DecodeMfma(DecodeParams p) {
   T bufA, bufB, bufC;
   // The first two tiles go in flight at once, while Q is split; when the
   // item carries their block ids neither waits for the table slice.
-  if (it.first[0] >= 0) {
+  if (wv == 0 && it.first[0] >= 0) {
     load(bufA, tb, 0);
     if (it.first[TT / 16] >= 0)
       load(bufB, tb + TT, TT / 16);
     else
       load(bufB, tb + TT, -1);
   } else {
-    load(bufA, tb, -1);
-    load(bufB, tb + TT, -1);
+    load(bufA, wtb, -1);
+    load(bufB, wtb + TT, -1);
   }
 
   // Fused append: the item ending at its row's last key stores that key's
@@ -293,7 +328,7 @@ void DecodeMfma(DecodeParams p) {
     } else if (lane == 0) {
       atomicOr(p.err, kErrSlotRange);
     }
-    __syncthreads();  // the LDS rows are read by the tile patch below
+    ItemSync<WPI>();  // the LDS rows are read by the tile patch below
   }
 
   // Q as MFMA A operands in NQ bf16 parts (round-to-nearest-even narrowing of
@@ -409,7 +444,7 @@ void DecodeMfma(DecodeParams p) {
         *reinterpret_cast<float4*>(&p_lds[(16 * h2 + n) * HP + 4 * kq]) =
             make_float4(s[h2][0], s[h2][1], s[h2][2], s[h2][3]);
     }
-    __syncthreads();
+    ItemSync<WPI>();
 #pragma unroll
     for (int h = 0; h < GV; ++h) {
       if (h / G >= nrows) break;
@@ -448,7 +483,7 @@ void DecodeMfma(DecodeParams p) {
         if ((j & 3) == 3) __builtin_amdgcn_sched_barrier(0);
       }
     }
-    __syncthreads();  // p_lds is rewritten by the next tile
+    ItemSync<WPI>();  // p_lds is rewritten by the next tile
   };
 
   // A work item's range is never empty (tb < te), so the loop has no entry
@@ -457,12 +492,14 @@ void DecodeMfma(DecodeParams p) {
   // (For a fused item whose range is the new key alone the loop's one tile
   // is empty: every score masked, the state unchanged.)
   if constexpr (NBUF == 2) {
-    for (int t0 = tb;; t0 += 2 * TT) {
+    // (A wavefront's run is empty only when the item has fewer tiles than
+    // WPI.)
+    for (int t0 = wtb; WPI == 1 || wtb < wte; t0 += 2 * TT) {
       process(bufA, t0, kend);
-      if (t0 + TT >= kend) break;
+      if (t0 + TT >= wte) break;
       load(bufA, t0 + 2 * TT, -1);
       process(bufB, t0 + TT, kend);
-      if (t0 + 2 * TT >= kend) break;
+      if (t0 + 2 * TT >= wte) break;
       load(bufB, t0 + 3 * TT, -1);
     }
   } else {
@@ -509,6 +546,50 @@ void DecodeMfma(DecodeParams p) {
   float lrow[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) lrow[i] = SumGroup16(lsum[i]);
+  if constexpr (WPI > 1) {
+    // Combine the wavefronts' states: M = max_w m_w, L = sum_w l_w 2^(m_w - M),
+    // O = sum_w o_w 2^(m_w - M) per virtual head. Every wavefront reaches
+    // this barrier once (one item per workgroup); wavefront 0 goes on.
+    __shared__ float ml_lds[WPI][GV][2];
+    __shared__ float o_lds[WPI][GV][D];
+#pragma unroll
+    for (int h = 0; h < GV; ++h) {
+      const float mh = ReadLane(m[h & 3], 16 * (h >> 2));
+      const float lh = ReadLane(lrow[h & 3], 16 * (h >> 2));
+      if (lane == 0) {
+        ml_lds[wv][h][0] = mh;
+        ml_lds[wv][h][1] = lh;
+      }
+      if (lane < VLPT) *reinterpret_cast<float2*>(&o_lds[wv][h][ev]) = make_float2(o[h][0], o[h][1]);
+    }
+    __syncthreads();
+    if (wv != 0) return;
+#pragma unroll
+    for (int h = 0; h < GV; ++h) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < WPI; ++w) mx = fmaxf(mx, ml_lds[w][h][0]);
+      float L = 0.f, o0 = 0.f, o1 = 0.f;
+#pragma unroll
+      for (int w = 0; w < WPI; ++w) {
+        const float sc = mx == -INFINITY ? 0.f : Exp2(ml_lds[w][h][0] - mx);
+        L += ml_lds[w][h][1] * sc;
+        const float2 ow = *reinterpret_cast<const float2*>(&o_lds[w][h][ev]);
+        o0 += ow.x * sc;
+        o1 += ow.y * sc;
+      }
+      o[h][0] = o0;
+      o[h][1] = o1;
+      // Back into the per-row layout the stores read: lane 16 j, slot i holds
+      // virtual head 4 j + i.
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if ((h & 3) == i && (h >> 2) == kq) {
+          m[i] = mx;
+          lrow[i] = L;
+        }
+    }
+  }
 
   RowDesc rds[RMAX];
 #pragma unroll
@@ -559,9 +640,9 @@ void DecodeMfma(DecodeParams p) {
   }
 }
 
-// Workgroups (one wavefront each) a launch of kernel K keeps resident: its
+// Workgroups of THREADS threads a launch of kernel K keeps resident: its
 // occupancy per CU times the CU count, queried once per (kernel, device).
-template <auto K>
+template <auto K, int THREADS = 64>
 int ResidentWaves() {
   constexpr int kDevices = 64;
   static int cached[kDevices] = {};
@@ -570,7 +651,7 @@ int ResidentWaves() {
   if (dev >= 0 && dev < kDevices && cached[dev] > 0) return cached[dev];
   int cus = 0, per_cu = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, K, 64, 0) != hipSuccess)
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, K, THREADS, 0) != hipSuccess)
     return 0;
   if (dev >= 0 && dev < kDevices) cached[dev] = cus * per_cu;
   return cus * per_cu;
@@ -582,6 +663,7 @@ struct Knobs {
   bool deep;       // three tiles in registers
   bool persist;    // persistent wavefronts drawing items from the queue
   int32_t slots;   // cap on persistent wavefronts (0: the resident count)
+  bool split4;     // fp32 steps whose items fit one round: 4 wavefronts per item
 };
 
 template <auto K>
@@ -608,6 +690,20 @@ void LaunchShape(const DecodeParams& p, hipStream_t stream, const Knobs& kn) {
     // fp32 slabs: the default shape only (32-key tiles, two buffers). Three
     // buffers for small steps (all items in one round of resident wavefronts,
     // one per SIMD) measured the same on C2: 23.5 against 23.6 us per layer.
+    // Steps of at least 256 items that all fit one round of 4-wavefront
+    // workgroups (C2's 500) spread each item over 4 wavefronts: 22.4 against
+    // 22.9 us per C2 layer (interleaved calls). C2's time is the memory
+    // system serving one ~35 MB burst (~3.6 TB/s: 500 wavefronts see their
+    // first tile 5.4 us into the launch, 2000 see it at 10.5 us), so the
+    // shorter walks gain little; C1's 16 items lost 0.7 us and keep one
+    // wavefront per item.
+    if constexpr (!QL) {
+      constexpr auto K4 = DecodeMfma<KV, D, G, RMAX, 2, 2, QL, OCC, FUSE, 4>;
+      if (kn.split4 && p.n_items >= 256 && p.n_items <= ResidentWaves<K4, 256>()) {
+        hipLaunchKernelGGL(K4, dim3(p.n_items), dim3(256), 0, stream, p);
+        return;
+      }
+    }
     LaunchPersistent<DecodeMfma<KV, D, G, RMAX, 2, 2, QL, OCC, FUSE>>(p, stream, kn);
   } else {
     if (kn.wide && kn.deep)
@@ -683,7 +779,8 @@ bool LaunchDecodeMfma(const DecodeParams& params, int kv_dtype, const Tuning& tu
   // decode_bufs3 three tiles in registers (two in flight), and
   // decode_persist = false one workgroup per item (the hardware dispatcher
   // hands out the items instead of the queue).
-  const Knobs kn{!tune.decode_tile16, tune.decode_bufs3, tune.decode_persist, tune.decode_slots};
+  const Knobs kn{!tune.decode_tile16, tune.decode_bufs3, tune.decode_persist, tune.decode_slots,
+                 tune.decode_split4};
   bool ok = false;
 #define EHIP_MFMA_CASE(KV, DD, GG) \
   else if (p.d == DD && p.group == GG) ok = LaunchRows<KV, DD, GG>(p, stream, kn);

@@ -72,6 +72,7 @@ Tuning ReadTuning() {
     if (x > 0) t.decode_slots = static_cast<int32_t>(std::min<long>(x, INT32_MAX));
   }
   t.decode_wg = flag("EHIP_DECODE_WG", '0');
+  t.decode_split4 = flag("EHIP_DECODE_SPLIT4", '0');
   t.decode_qspread = flag("EHIP_DECODE_QSPREAD", '0');
   if (const char* v = std::getenv("EHIP_DECODE_QUEUES")) {
     const long x = std::strtol(v, nullptr, 10);

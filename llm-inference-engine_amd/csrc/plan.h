@@ -50,6 +50,7 @@ struct Tuning {
   bool decode_qspread = true;  // EHIP_DECODE_QSPREAD=0: each sub-queue served by one XCD
   int32_t decode_queues = 0;   // EHIP_DECODE_QUEUES: item sub-queues (0: default)
   bool decode_wg = true;       // EHIP_DECODE_WG=0: no workgroup-per-row small fp32 steps
+  bool decode_split4 = true;   // EHIP_DECODE_SPLIT4=0: one wavefront per item in small fp32 steps
   bool fused_append = true;    // EHIP_FUSED_APPEND=0: append and attention in two launches
 };
 

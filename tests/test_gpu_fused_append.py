@@ -85,6 +85,37 @@ def test_fused_append_decode_step(gctx, ehip_mod, orc, H, Hkv, d, bs, kv):
     assert rel_norm(fused, separate) <= 1e-5
 
 
+@pytest.mark.parametrize("fused", [True, False])
+@pytest.mark.parametrize("H,Hkv,d,bs", [(14, 2, 64, 16), (8, 8, 64, 16), (8, 2, 64, 32),
+                                        (16, 2, 64, 64), (8, 1, 64, 16)])
+def test_fp32_items_over_four_wavefronts(gctx, ehip_mod, orc, tctx, H, Hkv, d, bs, fused):
+    """Small fp32 steps (256 or more items, every one in one round of
+    4-wavefront workgroups) spread each item's tiles over the workgroup's four
+    wavefronts, which combine their softmax states in LDS. Rows of one key,
+    items shorter than four tiles (wavefronts with no tiles), a last range
+    holding only the new key, long split rows; fused append and two launches:
+    slabs bit-exact and outputs to the decode bar against the oracle, and
+    within the fp32 bar of one wavefront per item (EHIP_DECODE_SPLIT4=0)."""
+    base = [1, 2, 17, 33, 63, 64, 65, 97, 129, 300, 1025, 2049]
+    # Rows repeated until the plan has 256..480 items: the 4-wavefront
+    # launch takes steps of at least 256 items that fit one round (2 such
+    # workgroups per CU).
+    for reps in range(1, 16):
+        w = _workload(ehip_mod, H, Hkv, d, bs, base * reps, seed=H + d + bs + 7,
+                      dtype=ehip_mod.KV_F32)
+        items = ehip_mod.plan_counts(
+            ehip_mod.geometry(H, Hkv, d, bs, w.kv_dtype, w.pool_blocks, w.scale),
+            ehip_mod.StepArrays(w.query_lens, w.context_lens, w.tables, w.slot_mapping))[2]
+        if items >= 256:
+            break
+    assert 256 <= items <= 480, items
+    got, ref = _run(gctx, ehip_mod, orc, w, fused=fused)
+    _check(got, ref)
+    one, _ = _run(tctx(EHIP_DECODE_SPLIT4="0"), ehip_mod, orc, w, fused=fused)
+    _check(one, ref)
+    assert rel_norm(got, one) <= 1e-5
+
+
 @pytest.mark.parametrize("slots", [None, "5", "64"])
 def test_fused_append_with_joint_items(gctx, ehip_mod, orc, tctx, slots):
     """The C4 shape with pair-shared prefixes (joint items never cover a row's

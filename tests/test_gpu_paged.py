@@ -736,6 +736,36 @@ def test_decode_fork_groups_beyond_pairs(ehip_mod, orc, H, Hkv, d, kv, tctx):
         b.free()
 
 
+@pytest.mark.parametrize("H,Hkv,reps", [(14, 2, 3), (8, 8, 1), (16, 4, 2)])
+def test_fp32_joint_items_over_four_wavefronts(ehip_mod, orc, H, Hkv, reps, tctx):
+    """fp32 fork groups (head_dim 64) in a step of 256..480 items: joint items
+    of 2 (g = 7) and 4 (g = 1) rows over four wavefronts per item, and g = 4,
+    whose 16 virtual heads keep Q in LDS and so stay one wavefront per item:
+    against the oracle, and against one wavefront per item."""
+    rng = np.random.default_rng(H + Hkv)
+    bs, d = 16, 64
+    q, ks, vs, tables, lengths = fork_group_case(rng, FORK_GROUPS * reps, Hkv, d, bs, H)
+    geo = ehip_mod.geometry(H, Hkv, d, bs, ehip_mod.KV_F32, ks.shape[0], scale_for(d))
+    st = ehip_mod.StepArrays(np.ones(len(lengths), np.int32), np.asarray(lengths, np.int64),
+                             tables)
+    rc, _, items, _, _, joint, _ = ehip_mod.plan_counts(geo, st, joint=True)
+    assert rc == 0 and joint > 0 and 256 <= items <= 480, items
+    ref = orc.paged_decode_batched(q, ks, vs, tables, lengths, H, Hkv, d, bs, scale_for(d))
+    outs = []
+    for split4 in ("1", "0"):
+        gctx = tctx(EHIP_DECODE_SPLIT4=split4, EHIP_DECODE_WG="0")
+        qd, kd, vd = gctx.to_device(q), gctx.to_device(ks), gctx.to_device(vs)
+        out = gctx.alloc(q.nbytes)
+        assert gctx.paged_decode_batched(qd, kd, vd, tables, lengths, H, Hkv, d, bs, 0,
+                                         ks.shape[0], scale_for(d), out) == 0, gctx.last_error()
+        gctx.sync()
+        outs.append(out.download(np.float32, q.shape))
+        check_fp32(outs[-1], ref)
+        for b in (qd, kd, vd, out):
+            b.free()
+    assert rel_norm(outs[0], outs[1]) <= FP32_REL
+
+
 @pytest.mark.parametrize("H,Hkv,d", [(14, 2, 64), (32, 8, 128), (8, 8, 128), (28, 4, 64),
                                      (8, 1, 128), (24, 3, 64)])
 @pytest.mark.parametrize("lens", [[1, 17, 33, 1500, 513], [1024, 1536, 1], [32, 64, 96],
