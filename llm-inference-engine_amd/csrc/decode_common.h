@@ -18,18 +18,25 @@ __device__ __forceinline__ int64_t PartialIndex(const RowDesc& rd, int kv_heads,
   return int64_t{rd.split_base} * kv_heads + int64_t{hk} * rd.nsplit + split;
 }
 
-// Table entries of logical blocks lb0 .. lb0+63 of a key range (lb0 =
-// tb / bs), one per lane: -1 past the range, -2 for an id outside the slab
-// (ReportRejectedBlocks flags those at the end of the item). The load is
-// unconditional and branch-free (lanes past the range re-read its last
-// entry) so it issues together with the item's other loads.
+// Table entry j of a key range's logical blocks lb0, lb0 + 1, ... (lb0 =
+// tb / bs), called with j = lane and j = 64 + lane for the range's two
+// 64-block halves (ranges are at most 128 blocks): -1 past the range, -2 for
+// an id outside the slab (ReportRejectedBlocks flags those at the end of the
+// item). The load is unconditional and branch-free (lanes past the range
+// re-read its last entry) so it issues together with the item's other loads.
 __device__ __forceinline__ int LoadRangeTable(const DecodeParams& p, int table_off, int tb,
-                                              int te, int lane) {
+                                              int te, int j) {
   const int lb0 = tb / p.bs;
-  const int nblk = (te - 1) / p.bs - lb0 + 1;  // <= 64: ranges are <= 64 * bs keys
-  const int raw = p.table[table_off + lb0 + min(lane, nblk - 1)];
+  const int nblk = (te - 1) / p.bs - lb0 + 1;  // <= 128
+  const int raw = p.table[table_off + lb0 + min(j, nblk - 1)];
   const bool bad = raw < 0 || raw >= p.slab_blocks;
-  return lane < nblk ? (bad ? -2 : raw) : -1;
+  return j < nblk ? (bad ? -2 : raw) : -1;
+}
+
+// Block id bi (< 128, wavefront-uniform) of a range's slice held as two
+// per-lane halves.
+__device__ __forceinline__ int RangeTableId(int tab, int tab2, int bi) {
+  return __builtin_amdgcn_readlane(bi < 64 ? tab : tab2, bi & 63);
 }
 
 // Work-item and row descriptors are read-only for a launch. Read through the

@@ -117,6 +117,7 @@ __device__ __forceinline__ void DecodeValuRow(const DecodeParams& p, int row, in
 
   const int lb0 = tb / bs;
   const int tab = LoadRangeTable(p, table_off, tb, te, lane);
+  const int tab2 = LoadRangeTable(p, table_off, tb, te, 64 + lane);
   const KV* kbase = static_cast<const KV*>(p.k_slab) + int64_t{hk} * p.head_stride;
   const KV* vbase = static_cast<const KV*>(p.v_slab) + int64_t{hk} * p.head_stride;
   const int lane_off = (tl * D + sub * EPV) * static_cast<int>(sizeof(KV));
@@ -145,7 +146,7 @@ __device__ __forceinline__ void DecodeValuRow(const DecodeParams& p, int row, in
       // zeros and a row group past the end (or on a rejected block id) reads
       // nothing at all. Loads are non-temporal: every tile streams once.
       const int j0 = t0 + r * TPR;  // wavefront-uniform
-      const int ph = __builtin_amdgcn_readlane(tab, min(j0, te - 1) / bs - lb0);
+      const int ph = RangeTableId(tab, tab2, min(j0, te - 1) / bs - lb0);
       const bool ok = j0 < te && ph >= 0;
       t.phys[r] = ok ? ph : -1;
       const int64_t off = int64_t{ok ? ph : 0} * p.block_stride + int64_t{j0 & (bs - 1)} * D;
@@ -240,6 +241,7 @@ __device__ __forceinline__ void DecodeValuRow(const DecodeParams& p, int row, in
   }
 
   ReportRejectedBlocks(p, tab);
+  ReportRejectedBlocks(p, tab2);
 #pragma unroll
   for (int h = 0; h < G; ++h) {
     l[h] = SumAcross<LPT>(l[h]);

@@ -143,6 +143,10 @@ void DecodeMfma(DecodeParams p) {
   // pairs (element 2i, 2i + 1 per entry).
   __shared__ uint4 knew_lds[FUSE ? D * static_cast<int>(sizeof(KV)) / 16 : 1];
   __shared__ typename T::VW vnew_lds[FUSE ? D / 2 : 1];
+  // The item's table slice (up to 128 block ids), per wavefront: read by
+  // broadcast LDS loads when a tile's loads are issued, so no register holds
+  // it through the item.
+  __shared__ int tab_lds[WPI][128];
 
   const int lane = threadIdx.x & 63;
   const int wv = WPI > 1 ? static_cast<int>(threadIdx.x >> 6) : 0;  // wavefront of the item
@@ -216,6 +220,7 @@ void DecodeMfma(DecodeParams p) {
   }
   const int lb0 = tb / bs;
   const int tab = LoadRangeTable(p, it.table_off, tb, te, lane);
+  const int tab2 = LoadRangeTable(p, it.table_off, tb, te, 64 + lane);
   const KV* kbase = static_cast<const KV*>(p.k_slab) + int64_t{hk} * p.head_stride;
   const KV* vbase = static_cast<const KV*>(p.v_slab) + int64_t{hk} * p.head_stride;
   const int bmask = bs - 1;
@@ -252,7 +257,8 @@ void DecodeMfma(DecodeParams p) {
       const int th = t0 + 16 * h2;  // wavefront-uniform; a half lies in one block (bs >= 16)
       const int phys =
           gh >= 0 ? it.first[min(gh + h2, 3)]
-                  : __builtin_amdgcn_readlane(tab, max(0, min(th, kend - 1) / bs - lb0));
+                  : __builtin_amdgcn_readfirstlane(
+                        tab_lds[wv][max(0, min(th, kend - 1) / bs - lb0)]);
       const bool ok = th < kend && phys >= 0;
       t.phys[h2] = ok ? phys : -1;
       const int64_t boff = int64_t{ok ? phys : 0} * p.block_stride + (th & bmask) * D;
@@ -279,16 +285,29 @@ void DecodeMfma(DecodeParams p) {
     }
   };
 
+  // The table slice into LDS (waiting for its two loads), rejected ids
+  // flagged; no register keeps it afterwards.
+  auto stash = [&]() {
+    tab_lds[wv][lane] = tab;
+    tab_lds[wv][64 + lane] = tab2;
+    ReportRejectedBlocks(p, tab);
+    ReportRejectedBlocks(p, tab2);
+  };
+
   T bufA, bufB, bufC;
   // The first two tiles go in flight at once, while Q is split; when the
   // item carries their block ids neither waits for the table slice.
   if (wv == 0 && it.first[0] >= 0) {
     load(bufA, tb, 0);
-    if (it.first[TT / 16] >= 0)
+    if (it.first[TT / 16] >= 0) {
       load(bufB, tb + TT, TT / 16);
-    else
+      stash();
+    } else {
+      stash();
       load(bufB, tb + TT, -1);
+    }
   } else {
+    stash();
     load(bufA, wtb, -1);
     load(bufB, wtb + TT, -1);
   }
@@ -534,7 +553,6 @@ void DecodeMfma(DecodeParams p) {
     process(tn, newpos, te);
   }
 
-  ReportRejectedBlocks(p, tab);
   // Token-parallel partial sums (d = 64) -> per (virtual head, element) totals.
   if constexpr (VT > 1) {
 #pragma unroll

@@ -25,6 +25,18 @@ constexpr int32_t kMinSplit = 128;
 // attention call; C2, 500 items of 128 keys, is faster as it is).
 constexpr int64_t kSmallStepUnits = int64_t{128} * kMinSplit;
 constexpr int32_t kMaxSplitsPerRow = 64;  // bounds the merge a single wave performs
+// Large steps (one item per resident wavefront would already mean ranges of
+// at least kLargeStep keys) take ranges of kLargeMin..kLargeMax keys. Measured
+// on MI355X (attention call per layer, one process, interleaved calls):
+//   C4 (4.9M kv-head-keys):  1024: 397.0  1280: 393.7  1536: 389.0  2048: 408.8 us
+//   C5 (2.9M):               1024: 279.5  1408: 262.3  1792: 275.5  2048: 274.8 us
+//   C3 (1.1M decode, + the prefill chunks): 576: 151.6  768: 148.4  1024: 143.4
+//                            1536: 156.7  2048: 184.7 us
+// Fewer, longer items carry fewer startups and partials; past ~1536 keys the
+// last items' walks set the tail.
+constexpr int64_t kLargeStep = 512;
+constexpr int64_t kLargeMin = 1024;
+constexpr int64_t kLargeMax = 1536;
 
 int Fail(std::string* err, int code, const char* fmt, long long a = 0, long long b = 0,
          long long c = 0) {
@@ -131,10 +143,9 @@ int ValidateGeometry(const ehip_geometry& g, std::string* err) {
 }
 
 int32_t MaxSplitTokens(const ehip_geometry& g) {
-  // A work item's table slice sits in the wavefront's lanes: one block id per
-  // lane (64 blocks), two per lane for the INT8/FP8 kernel (128 blocks), whose
-  // items carry half the bytes per key and so want longer ranges.
-  return (ScaledKv(g.kv_dtype) ? 128 : 64) * g.block_size;
+  // A work item's table slice sits in the wavefront's lanes, two block ids
+  // per lane: 128 blocks.
+  return 128 * g.block_size;
 }
 
 int32_t ChooseSplitTokens(const ehip_geometry& g, int64_t unit_tokens, const Tuning& tune) {
@@ -144,6 +155,7 @@ int32_t ChooseSplitTokens(const ehip_geometry& g, int64_t unit_tokens, const Tun
   int64_t target = ScaledKv(g.kv_dtype) ? kTargetItems / 2 : kTargetItems;
   if (tune.target_items > 0) target = tune.target_items;
   int64_t s = (unit_tokens + target - 1) / target;
+  if (!ScaledKv(g.kv_dtype) && s >= kLargeStep) s = std::clamp(s, kLargeMin, kLargeMax);
   s = RoundUp(std::max<int64_t>(s, unit_tokens < kSmallStepUnits ? kTile : kMinSplit), kTile);
   return static_cast<int32_t>(std::min<int64_t>(s, max_split));
 }

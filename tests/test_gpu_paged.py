@@ -338,7 +338,7 @@ def test_bf16_decode_gqa_sweep(gctx, orc, H, Hkv, d):
     check_fp32(got, ref)
 
 
-@pytest.mark.parametrize("split", ["64", "128", "512", "1024"])
+@pytest.mark.parametrize("split", ["64", "128", "512", "1024", "2048"])
 def test_split_count_independence(orc, split, tctx):
     # The merged result must not depend on how the keys were split (the
     # split-KV path: the workgroup-per-row kernel for small steps is off).

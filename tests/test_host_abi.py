@@ -73,7 +73,7 @@ def expected_items(lens, hkv, split, bs=16, tail=0):
     for r, L in enumerate(lens):
         s = split
         if math.ceil(L / s) > 64:
-            s = min(64 * bs, math.ceil(math.ceil(L / 64) / 64) * 64)
+            s = min(128 * bs, math.ceil(math.ceil(L / 64) / 64) * 64)
         ranges += [((r,), min(s, int(L) - t)) for t in range(0, int(L), s)]
     return sum(cut_tail(ranges, hkv, tail).values()) * hkv
 
@@ -91,7 +91,7 @@ def test_plan_partitions_c4_shape(ehip_mod, monkeypatch, tail):
     rc, rows, items, partials, split = ehip_mod.plan_counts(g, st)
     assert rc == 0
     assert rows == 256
-    assert split % 64 == 0 and 128 <= split <= 64 * w.block_size
+    assert split % 64 == 0 and 128 <= split <= 128 * w.block_size
     assert items == expected_items(w.context_lens, w.kv_heads, split, tail=tail or 0)
     assert partials == items  # one partial slot per (row, kv head, split)
     if tail and tail < split:
