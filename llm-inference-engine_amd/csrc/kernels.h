@@ -67,9 +67,14 @@ struct DecodeParams {
 // sub-queues: sub-queue q serves the items whose index is q modulo the
 // sub-queue count, to the wavefronts whose index is q modulo it. One counter
 // takes every ticket of a launch through one memory channel's atomic unit,
-// which serialises them (about 12 ns apiece on MI355X); 32 counters in
-// separate 256-byte lines draw in parallel.
+// which serialises them (about 12 ns apiece on MI355X); counters in separate
+// 256-byte lines draw in parallel. Up to kItemQueues of them; kDefaultQueues
+// by default. Fewer sub-queues balance the end of a launch better (each is
+// drawn by more wavefronts): C4 with 1536-key items, one process, interleaved
+// calls: 388.5 us at 32, 386.7 at 16, 384.2 at 8, 384.4 at 4, 383.3 at 1.
+// Eight keeps most of that and 8x one counter's ticket rate.
 constexpr int kItemQueues = 32;
+constexpr int kDefaultQueues = 8;
 constexpr int kQueueStride = 64;  // words between counters
 
 // The item-queue counters of a context (kItemQueues ticket counters and the

@@ -790,7 +790,7 @@ bool LaunchDecodeMfma(const DecodeParams& params, int kv_dtype, const Tuning& tu
   p.queue = queue->d_counters;
   p.queue_done = queue->d_done;
   p.queue_spread = tune.decode_qspread ? 1 : 0;
-  p.queues = tune.decode_queues > 0 ? std::min(tune.decode_queues, kItemQueues) : kItemQueues;
+  p.queues = tune.decode_queues > 0 ? std::min(tune.decode_queues, kItemQueues) : kDefaultQueues;
   if (!DecodeMfmaCovers(p, kv_dtype, tune)) return false;
   // 32-token tiles (two MFMA halves per tile, double-buffered) measured best
   // on C4; decode_tile16 selects one half per tile (fewer registers),

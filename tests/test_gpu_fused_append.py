@@ -160,18 +160,21 @@ def test_fused_append_items_taken_by_ticket(gctx, ehip_mod, orc, tctx, H, Hkv, d
     assert np.array_equal(queued.view(np.uint32), full.view(np.uint32))
 
 
+@pytest.mark.parametrize("queues", ["8", "32"])
 @pytest.mark.parametrize("spread", ["1", "0"])
 @pytest.mark.parametrize("H,Hkv,d,bs", [(32, 8, 128, 16), (64, 8, 128, 16)])
-def test_fused_append_sub_queues_across_xcds(gctx, ehip_mod, orc, tctx, H, Hkv, d, bs, spread):
-    """A capped grid of 300 wavefronts (at least 8 per sub-queue): with the
-    spread mapping each sub-queue is drawn by wavefronts b with b / 8 = q
-    (mod 32), one from every XCD, instead of b = q (mod 32). Every item is
-    still served exactly once: the same slabs and bit-identical outputs to the
-    launch whose grid covers every item."""
+def test_fused_append_sub_queues_across_xcds(gctx, ehip_mod, orc, tctx, H, Hkv, d, bs, spread,
+                                             queues):
+    """A capped grid of 300 wavefronts (at least 8 per sub-queue) over 8 (the
+    default) or 32 sub-queues: with the spread mapping each sub-queue is drawn
+    by wavefronts b with b / 8 = q (mod the count), one from every XCD, instead
+    of b = q (mod the count). Every item is still served exactly once: the
+    same slabs and bit-identical outputs to the launch whose grid covers every
+    item."""
     lens = [1, 2, 17, 33, 129, 1025, 1026, 2049, 4000, 64, 65, 8193]
     w = _workload(ehip_mod, H, Hkv, d, bs, lens, seed=H + d + bs + 2)
     full, ref = _run(gctx, ehip_mod, orc, w, fused=True)
-    ctx = tctx(EHIP_DECODE_SLOTS="300", EHIP_DECODE_QSPREAD=spread)
+    ctx = tctx(EHIP_DECODE_SLOTS="300", EHIP_DECODE_QSPREAD=spread, EHIP_DECODE_QUEUES=queues)
     queued, ref_q = _run(ctx, ehip_mod, orc, w, fused=True)
     _, items, _ = ctx.step_info()
     assert 300 < items, items
