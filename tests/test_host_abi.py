@@ -110,6 +110,44 @@ def test_plan_split_override_and_long_rows(ehip_mod, monkeypatch):
     assert items == 8 * (64 + 1 + 1 + 2)
 
 
+def test_plan_large_steps_take_1024_to_1536_key_ranges(ehip_mod):
+    """Steps whose one-item-per-wavefront length (kv-head-keys / 2048) is 512
+    keys or more take ranges clamped to [1024, 1536] keys (the measured best
+    of C3's decode rows, C4 and C5); smaller steps keep the target length, and
+    INT8 plans their own rule."""
+    from ehip import workloads
+    for name, want in (("c4", 1536), ("c5", 1408), ("c2", 128)):
+        w = getattr(workloads, name)()
+        g = ehip_mod.geometry(w.heads, w.kv_heads, w.head_dim, w.block_size, w.kv_dtype,
+                              w.pool_blocks, w.scale)
+        st = ehip_mod.StepArrays(w.query_lens, w.context_lens, w.tables, w.slot_mapping)
+        rc, rows, items, partials, split = ehip_mod.plan_counts(g, st)
+        assert rc == 0 and split == want, (name, split)
+    # C3's decode rows alone (what its mixed step leaves to the decode kernel):
+    # 1.06M kv-head-keys give a 515-key target, raised to 1024.
+    w = workloads.c3()
+    idx = [i for i, t in enumerate(w.query_lens) if t == 1]
+    st = ehip_mod.StepArrays([1] * len(idx), [w.context_lens[i] for i in idx],
+                             [w.tables[i] for i in idx])
+    g = ehip_mod.geometry(w.heads, w.kv_heads, w.head_dim, w.block_size, w.kv_dtype,
+                          w.pool_blocks, w.scale)
+    assert ehip_mod.plan_counts(g, st)[4] == 1024
+    # The boundary (256 rows x 8 kv heads = 2048 units): rows of 511 keys give
+    # a 511-key target (rounded to 512-key ranges), rows of 512 keys reach the
+    # large-step clamp and take 1024.
+    for L, want in ((511, 512), (512, 1024)):
+        lens = [L] * 256
+        rc, rows, items, partials, split = ehip_mod.plan_counts(
+            geom(ehip_mod, slab_blocks=256 * ((L + 15) // 16)), simple_step(ehip_mod, lens))
+        assert rc == 0 and split == want, (L, split)
+    # INT8 keeps its own rule (half the item target, 128-block ranges).
+    w = workloads.c4()
+    g = ehip_mod.geometry(w.heads, w.kv_heads, w.head_dim, w.block_size, ehip_mod.KV_INT8,
+                          w.pool_blocks, w.scale)
+    st = ehip_mod.StepArrays(w.query_lens, w.context_lens, w.tables, w.slot_mapping)
+    assert ehip_mod.plan_counts(g, st)[4] == 128 * w.block_size
+
+
 def test_plan_small_steps_split_into_64_key_units(ehip_mod):
     """A step with fewer than 128 items of 128 keys (128 * 128 kv-head-keys)
     is split into 64-key ranges; C2 and larger keep at least 128 keys."""
