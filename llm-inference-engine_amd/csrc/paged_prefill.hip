@@ -155,9 +155,12 @@ void PrefillMfmaBf16(PrefillParams p) {
   // Q^T as MFMA B operands (bf16, round-to-nearest-even), in registers:
   // lane l holds Q[row r0 + l%16][c*32 + 8*kq .. +8] for each of its heads
   // (with kFold scaled by scale * log2(e) before the rounding, so the MFMA
-  // leaves scores in the log2 units of the softmax).
+  // leaves scores in the log2 units of the softmax). The fp32 rows are
+  // loaded after the first tiles' block ids and converted after the first
+  // tiles' K/V loads are issued (below).
   bf16x8_t qreg[HB][NC];
-  {
+  float4 qraw[HB][NC][2];
+  auto load_q = [&]() __attribute__((always_inline)) {
     const int qr = r0 + min(n, max(qnw, 1) - 1);
 #pragma unroll
     for (int hh = 0; hh < HB; ++hh) {
@@ -165,16 +168,24 @@ void PrefillMfmaBf16(PrefillParams p) {
       const float* qp = p.q + (int64_t{it.row_base + min(qr, T - 1)} * p.heads + head) * D + kq * 8;
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        const float4 a = *reinterpret_cast<const float4*>(qp + c * 32);
-        const float4 b = *reinterpret_cast<const float4*>(qp + c * 32 + 4);
+        qraw[hh][c][0] = *reinterpret_cast<const float4*>(qp + c * 32);
+        qraw[hh][c][1] = *reinterpret_cast<const float4*>(qp + c * 32 + 4);
+      }
+    }
+  };
+  auto convert_q = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int hh = 0; hh < HB; ++hh)
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const float4 a = qraw[hh][c][0], b = qraw[hh][c][1];
         const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
         bf16x8_t qv;
 #pragma unroll
         for (int i = 0; i < 8; ++i) qv[i] = static_cast<__bf16>(kFold ? x[i] * p.scale_log2 : x[i]);
         qreg[hh][c] = qv;
       }
-    }
-  }
+  };
 
   // Tile loads: thread -> (token, 8-element group), two K and two V vectors
   // per tile, at the same slab offsets.
@@ -428,18 +439,24 @@ void PrefillMfmaBf16(PrefillParams p) {
   // Tile t goes to LDS buffer t % 3 (ids slot t % 3). Step t: wait until
   // this wavefront's loads of tile t have landed, barrier (every
   // wavefront's part of tile t is in LDS, and every wavefront is done
-  // reading tile t - 1, whose buffer takes tile t + 2), issue tile t + 2's
-  // loads and the block ids of tile t + 5, compute tile t. The loads run
-  // unconditionally (tiles past the item's end re-read its last rows,
-  // clamped; such steps compute nothing), so at every wait the same vector
-  // memory operations follow tile t's loads in issue order: the ids of
-  // tile t + 3, tile t + 1's four loads and the ids of tile t + 4 (vmcnt
-  // retires them in order; the compiler barriers keep that order).
+  // reading tile t - 1, whose buffer takes tile t + 2), compute tile t and
+  // issue tile t + 2's loads and the block ids of tile t + 5 (in the order
+  // below). At every wait the same vector memory operations follow tile t's
+  // loads in issue order: the ids of tile t + 3, tile t + 1's four loads and
+  // the ids of tile t + 4 (vmcnt retires them in order; the compiler
+  // barriers keep that order).
+  // Start: the first three tiles' block ids, then the query rows (neither
+  // waits for the other), then tile 0's and tile 1's K/V once their ids are
+  // in, then the queries' conversion. A C3 timeline of the start (entry to
+  // the first tile in LDS, ~4.8 us at a launch's start) measured the same
+  // with the rows loaded first: the first ids alone take 3.5-4 us to land.
   uint32_t idA0, idA1, idB0, idB1, idC0, idC1;  // block ids of each buffer's next tile
 #define EHIP_PF_FENCE() asm volatile("" ::: "memory")
   EHIP_PF_IDLOAD(idA, key0);
   EHIP_PF_IDLOAD(idB, key0 + kTile);
   EHIP_PF_IDLOAD(idC, key0 + 2 * kTile);
+  EHIP_PF_FENCE();
+  load_q();
   EHIP_PF_FENCE();
   EHIP_PF_GLOAD(lt0, key0, idA);
   EHIP_PF_FENCE();
@@ -449,24 +466,52 @@ void PrefillMfmaBf16(PrefillParams p) {
   EHIP_PF_FENCE();
   EHIP_PF_IDLOAD(idB, key0 + 4 * kTile);
   EHIP_PF_FENCE();
-#define EHIP_PF_STEP(T, X, Y, IDY)                                      \
+  __builtin_amdgcn_sched_barrier(0);
+  convert_q();
+  // Where a step issues tile t + 2's loads. On the two-per-CU instance
+  // (bound by its longest blocks' walk) after computing tile t: right after
+  // each barrier every wavefront of the workgroup would issue its loads at
+  // once, and the later ones wait for the earlier ones to be accepted (a
+  // per-tile C3 timeline put that at 0.28 of a 1.08 us step; C3 chunks
+  // 35.3 -> 33.7 us). On the three-per-CU instance (issue-bound, three
+  // workgroups' loads interleave anyway) before it, which keeps them two
+  // tiles ahead (C5 re-prefill 314 against 316 us after).
+  constexpr bool kLoadsAfter = OCC == 2;
+#define EHIP_PF_LOADS(T, Y, IDY)                                        \
   do {                                                                  \
-    asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");       \
+    EHIP_PF_FENCE();                                                    \
     EHIP_PF_GLOAD(Y, key0 + ((T) + 2) * kTile, IDY);                     \
     EHIP_PF_FENCE();                                                    \
     EHIP_PF_IDLOAD(IDY, key0 + ((T) + 5) * kTile);                       \
     EHIP_PF_FENCE();                                                    \
+  } while (0)
+#define EHIP_PF_STEP(T, X, Y, IDY)                                      \
+  do {                                                                  \
+    asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");       \
+    if constexpr (!kLoadsAfter) EHIP_PF_LOADS(T, Y, IDY);               \
     compute_tile((T), (X));                                             \
   } while (0)
-  for (int tile = 0; tile < ntiles; tile += 3) {
+  // The walk ends with the item's last tile (before that step's loads when
+  // they come after the tile). The loads stay unconditional otherwise, so the
+  // count above holds at every step and the compiler's own waits stay exact
+  // (the last steps load tiles past the item's end: its last rows again,
+  // clamped).
+  for (int tile = 0;; tile += 3) {
     EHIP_PF_STEP(tile, lt0, lt2, idC);
+    if (tile + 1 >= ntiles) break;
+    if constexpr (kLoadsAfter) EHIP_PF_LOADS(tile, lt2, idC);
     EHIP_PF_STEP(tile + 1, lt1, lt0, idA);
+    if (tile + 2 >= ntiles) break;
+    if constexpr (kLoadsAfter) EHIP_PF_LOADS(tile + 1, lt0, idA);
     EHIP_PF_STEP(tile + 2, lt2, lt1, idB);
+    if (tile + 3 >= ntiles) break;
+    if constexpr (kLoadsAfter) EHIP_PF_LOADS(tile + 2, lt1, idB);
   }
   // Loads past the item's end may still be in flight: they write this
   // workgroup's LDS, so they land before the workgroup ends.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #undef EHIP_PF_STEP
+#undef EHIP_PF_LOADS
 #undef EHIP_PF_FENCE
 #undef EHIP_PF_LDSP
 
