@@ -224,6 +224,16 @@ void PrefillMfmaBf16(PrefillParams p) {
   const __amdgpu_buffer_rsrc_t rv =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vslab), 0, 0xFFFFFFFFu, 0x00020000);
   const uint32_t ko = static_cast<uint32_t>((ek ^ (2 * (tk0 & 7))) * 16);
+  // A whole tile (tiles start at multiples of 32 keys): row tk0 sits in its
+  // first block, at slot (k0 mod bs) + tk0; row tk1 in its second block at
+  // slot tk0 when bs = 16, else in the first at slot (k0 mod bs) + tk1. So
+  // each load offset is a wavefront-uniform part (block id x stride, plus
+  // the tile's slot offset) and these per-thread parts: 2 VALU instructions
+  // per tile instead of ~20. Measured on the three-per-CU instance (VALU
+  // issue-bound): C5 re-prefill 316 -> 310 us; on the two-per-CU one
+  // (latency-bound) C3 chunks 31.5 -> 31.9 us, so only there.
+  const uint32_t c0 = static_cast<uint32_t>(tk0 * D * 2) + ko;
+  const uint32_t c1 = static_cast<uint32_t>((bs == 16 ? tk0 : tk1) * D * 2) + ko;
 #define EHIP_PF_IDLOAD(ID, K0)                                                               \
   do {                                                                                      \
     const int kb0 = min((K0) >> bsh, last_blk);                                             \
@@ -241,11 +251,19 @@ void PrefillMfmaBf16(PrefillParams p) {
     bad = bad | !okb;                                                                        \
     id0 = okb ? id0 : 0;                                                                     \
     id1 = okb ? id1 : 0;                                                                     \
-    const int pk0 = min((K0) + tk0, key1 - 1), pk1 = min((K0) + tk1, key1 - 1);             \
-    const uint32_t a0 = static_cast<uint32_t>((pk0 >> bsh) != kb0 ? id1 : id0) * stride_b +  \
-                        static_cast<uint32_t>((pk0 & bmask) * D * 2) + ko;                   \
-    const uint32_t a1 = static_cast<uint32_t>((pk1 >> bsh) != kb0 ? id1 : id0) * stride_b +  \
-                        static_cast<uint32_t>((pk1 & bmask) * D * 2) + ko;                   \
+    uint32_t a0, a1;                                                                         \
+    if (OCC == 3 && (K0) + kTile <= key1) {                                                  \
+      const uint32_t so = static_cast<uint32_t>(((K0) & bmask) * D * 2);                     \
+      a0 = static_cast<uint32_t>(id0) * stride_b + so + c0;                                  \
+      a1 = static_cast<uint32_t>(bs == 16 ? id1 : id0) * stride_b + so + c1;                 \
+    } else {                                                                                 \
+      /* The item's last tile: rows past its end read its last row. */                       \
+      const int pk0 = min((K0) + tk0, key1 - 1), pk1 = min((K0) + tk1, key1 - 1);            \
+      a0 = static_cast<uint32_t>((pk0 >> bsh) != kb0 ? id1 : id0) * stride_b +               \
+           static_cast<uint32_t>((pk0 & bmask) * D * 2) + ko;                                \
+      a1 = static_cast<uint32_t>((pk1 >> bsh) != kb0 ? id1 : id0) * stride_b +               \
+           static_cast<uint32_t>((pk1 & bmask) * D * 2) + ko;                                \
+    }                                                                                        \
     unsigned char* const lk = (BUF) + wave * 1024;                                           \
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, EHIP_PF_LDSP(lk), 16, a0, 0, 0, 0);        \
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, EHIP_PF_LDSP(lk + SM::TILE / 2), 16, a1, 0, \
