@@ -138,6 +138,14 @@ __global__ __launch_bounds__(kThreads) void PackedGemmMfma(GemmParams p) {
   // planes are zero-padded to whole tiles: no masks); panel rows wk and
   // wk + KS, ... (16 weights each) of panel wpp.
   const int xr = tid >> 2, xk = (tid & 3) * 16;
+  // A tile's rows past m are never stored, and each output row depends on its
+  // own x row only, so the x rows of wholly dead 32-row halves (a decode
+  // call's m <= 32 in a 64-row tile) are neither loaded nor computed: x's
+  // L2 -> CU traffic and the MFMA work halve there. Whether a thread's row
+  // (and a wavefront's half) is live is uniform per wavefront.
+  const int rows_live = static_cast<int>(p.m - m0 < kBM ? p.m - m0 : kBM);
+  const bool x_live = (xr & ~31) < rows_live;
+  const bool wave_live = 32 * wr < rows_live;
   const int64_t plane = p.m_pad * p.k_pad;
   const __bf16* xrow = reinterpret_cast<const __bf16*>(p.xp) + (m0 + xr) * p.k_pad;
   const int wpp = tid / KS, wk = tid % KS;  // panel wpp, k rows wk + KS * h
@@ -147,11 +155,13 @@ __global__ __launch_bounds__(kThreads) void PackedGemmMfma(GemmParams p) {
   bf16x8_t xv[kXP][2];
   uint4 wv[RPT][WE];
   auto gload = [&](int64_t k0) {
+    if (x_live) {
 #pragma unroll
-    for (int pl = 0; pl < kXP; ++pl)
+      for (int pl = 0; pl < kXP; ++pl)
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
-        xv[pl][h] = *reinterpret_cast<const bf16x8_t*>(xrow + pl * plane + k0 + xk + 8 * h);
+        for (int h = 0; h < 2; ++h)
+          xv[pl][h] = *reinterpret_cast<const bf16x8_t*>(xrow + pl * plane + k0 + xk + 8 * h);
+    }
 #pragma unroll
     for (int h = 0; h < RPT; ++h) {
       const int64_t kw = k0 + wk + KS * h;
@@ -162,11 +172,13 @@ __global__ __launch_bounds__(kThreads) void PackedGemmMfma(GemmParams p) {
     }
   };
   auto lstore = [&]() {
+    if (x_live) {
 #pragma unroll
-    for (int pl = 0; pl < kXP; ++pl)
+      for (int pl = 0; pl < kXP; ++pl)
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
-        *reinterpret_cast<bf16x8_t*>(&xs[pl][xr * kXRow + xk + 8 * h]) = xv[pl][h];
+        for (int h = 0; h < 2; ++h)
+          *reinterpret_cast<bf16x8_t*>(&xs[pl][xr * kXRow + xk + 8 * h]) = xv[pl][h];
+    }
     // Each panel row as WP planes: 16 weights, two 16-byte stores per plane.
 #pragma unroll
     for (int hr = 0; hr < RPT; ++hr) {
@@ -200,6 +212,7 @@ __global__ __launch_bounds__(kThreads) void PackedGemmMfma(GemmParams p) {
     for (int cb = 0; cb < NW; ++cb) acc[rb][cb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   auto compute = [&]() {
+    if (!wave_live) return;
 #pragma unroll
     for (int kc = 0; kc < kBK / 32; ++kc) {
     bf16x8_t a[2][kXP];
