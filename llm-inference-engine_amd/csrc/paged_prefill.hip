@@ -224,7 +224,8 @@ void PrefillMfmaBf16(PrefillParams p) {
   const __amdgpu_buffer_rsrc_t rv =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vslab), 0, 0xFFFFFFFFu, 0x00020000);
   const uint32_t ko = static_cast<uint32_t>((ek ^ (2 * (tk0 & 7))) * 16);
-  // A whole tile (tiles start at multiples of 32 keys): row tk0 sits in its
+  // A whole tile starting at a multiple of 32 keys (the planner cuts key
+  // ranges at multiples of 32; the load checks it): row tk0 sits in its
   // first block, at slot (k0 mod bs) + tk0; row tk1 in its second block at
   // slot tk0 when bs = 16, else in the first at slot (k0 mod bs) + tk1. So
   // each load offset is a wavefront-uniform part (block id x stride, plus
@@ -252,7 +253,7 @@ void PrefillMfmaBf16(PrefillParams p) {
     id0 = okb ? id0 : 0;                                                                     \
     id1 = okb ? id1 : 0;                                                                     \
     uint32_t a0, a1;                                                                         \
-    if (OCC == 3 && (K0) + kTile <= key1) {                                                  \
+    if (OCC == 3 && (K0) + kTile <= key1 && ((K0) & (kTile - 1)) == 0) {                    \
       const uint32_t so = static_cast<uint32_t>(((K0) & bmask) * D * 2);                     \
       a0 = static_cast<uint32_t>(id0) * stride_b + so + c0;                                  \
       a1 = static_cast<uint32_t>(bs == 16 ? id1 : id0) * stride_b + so + c1;                 \
