@@ -66,6 +66,9 @@ __device__ __forceinline__ float Max16F(float x) {
 
 typedef __attribute__((ext_vector_type(4))) int i32x4_t;
 
+// Lazy rescaling slack (log2 units): probabilities stay below 2^8.
+constexpr float kRefSlack = 8.f;
+
 // Byte k of w as an unsigned integer in float (v_cvt_f32_ubyte).
 __device__ __forceinline__ float UByteF(uint32_t w, int k) {
   return static_cast<float>((w >> (8 * k)) & 0xFFu);
@@ -325,28 +328,47 @@ void DecodeMfmaQ8(DecodeParams p) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) s[h2][i] = valid ? dot[i] * (sq4[i] * sc) : -INFINITY;
     }
-    float alpha[4];
+    // Lazy rescaling (FlashAttention-3, Shah et al. 2024): each head row
+    // keeps a reference m (log2 units; -inf until the row meets a key) that
+    // moves only when a tile's row max exceeds it by more than kRefSlack, so
+    // probabilities stay below 2^kRefSlack and most tiles need neither the
+    // row reduction nor the output rescale: each lane checks its own scores
+    // and the wavefront takes the slow path when any lane must.
+    bool need = false;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int h2 = 0; h2 < TH; ++h2) need = need || s[h2][i] > m[i] + kRefSlack;
+    const bool rescale = __any(need);
+    float alpha[4] = {1.f, 1.f, 1.f, 1.f};
+    if (rescale) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float mx = s[0][i];
+#pragma unroll
+        for (int h2 = 1; h2 < TH; ++h2) mx = fmaxf(mx, s[h2][i]);
+        mx = Max16F(mx);
+        const bool mv = mx > m[i] + kRefSlack;  // the same in the row's 16 lanes
+        alpha[i] = mv && m[i] != -INFINITY ? Exp2(m[i] - mx) : 1.f;
+        m[i] = mv ? mx : m[i];
+        lsum[i] *= alpha[i];
+        if constexpr (!F8) cofs[i] *= alpha[i];
+      }
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float mx = s[0][i];
-#pragma unroll
-      for (int h2 = 1; h2 < TH; ++h2) mx = fmaxf(mx, s[h2][i]);
-      mx = Max16F(mx);
-      const float mn = fmaxf(m[i], mx);
-      alpha[i] = mn == -INFINITY ? 1.f : Exp2(m[i] - mn);
-      m[i] = mn;
       float ps = 0.f, pc = 0.f;
 #pragma unroll
       for (int h2 = 0; h2 < TH; ++h2) {
-        const float pr = mn == -INFINITY ? 0.f : Exp2(s[h2][i] - mn);
+        const float pr = m[i] == -INFINITY ? 0.f : Exp2(s[h2][i] - m[i]);
         ps += pr;
         // The half's V scale rides on the probability (one multiply per
         // score here instead of one per V element in the PV loop).
         s[h2][i] = pr * t.vs[h2];
         if constexpr (!F8) pc += s[h2][i];
       }
-      lsum[i] = lsum[i] * alpha[i] + ps;
-      if constexpr (!F8) cofs[i] = cofs[i] * alpha[i] + pc;
+      lsum[i] += ps;
+      if constexpr (!F8) cofs[i] += pc;
     }
     if (kq < HR) {
 #pragma unroll
@@ -355,14 +377,16 @@ void DecodeMfmaQ8(DecodeParams p) {
             make_float4(s[h2][0], s[h2][1], s[h2][2], s[h2][3]);
     }
     __syncthreads();
+    if (rescale) {
 #pragma unroll
-    for (int h = 0; h < GV; ++h) {
-      if (h / G >= nrows) break;
-      const float a = ReadLaneF(alpha[h & 3], 16 * (h >> 2));
-      o[h][0] *= a;
-      o[h][1] *= a;
-      o[h][2] *= a;
-      o[h][3] *= a;
+      for (int h = 0; h < GV; ++h) {
+        if (h / G >= nrows) break;
+        const float a = ReadLaneF(alpha[h & 3], 16 * (h >> 2));
+        o[h][0] *= a;
+        o[h][1] *= a;
+        o[h][2] *= a;
+        o[h][3] *= a;
+      }
     }
 #pragma unroll
     for (int h2 = 0; h2 < TH; ++h2) {
