@@ -52,6 +52,9 @@ __device__ __forceinline__ float ReadLane(float x, int lane) {
 }
 
 // Max over each 16-lane row.
+// Lazy rescaling slack (log2 units): probabilities stay below 2^8.
+constexpr float kRefSlack = 8.f;
+
 __device__ __forceinline__ float Max16(float x) {
   x = fmaxf(x, Dpp<0xB1>(x));
   x = fmaxf(x, Dpp<0x4E>(x));
@@ -438,24 +441,42 @@ void DecodeMfma(DecodeParams p) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) s[h2][i] = valid ? acc[h2][i] * p.scale_log2 : -INFINITY;
     }
-    float alpha[4];
+    // Lazy rescaling (FlashAttention-3, Shah et al. 2024): each head row
+    // keeps a reference m (log2 units; -inf until the row meets a key) that
+    // moves only when a tile's row max exceeds it by more than kRefSlack, so
+    // probabilities stay below 2^kRefSlack and most tiles need neither the
+    // row reduction nor the output rescale: each lane checks its own scores
+    // and the wavefront takes the slow path when any lane must. (An
+    // all-masked tile moves nothing.)
+    bool need = false;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int h2 = 0; h2 < TH; ++h2) need = need || s[h2][i] > m[i] + kRefSlack;
+    const bool rescale = __any(need);
+    float alpha[4] = {1.f, 1.f, 1.f, 1.f};
+    if (rescale) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float mx = s[0][i];
+#pragma unroll
+        for (int h2 = 1; h2 < TH; ++h2) mx = fmaxf(mx, s[h2][i]);
+        mx = Max16(mx);
+        const bool mv = mx > m[i] + kRefSlack;  // the same in the row's 16 lanes
+        alpha[i] = mv && m[i] != -INFINITY ? Exp2(m[i] - mx) : 1.f;
+        m[i] = mv ? mx : m[i];
+        lsum[i] *= alpha[i];
+      }
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float mx = s[0][i];
-#pragma unroll
-      for (int h2 = 1; h2 < TH; ++h2) mx = fmaxf(mx, s[h2][i]);
-      mx = Max16(mx);
-      const float mn = fmaxf(m[i], mx);
-      // An all-masked tile leaves mn at -inf: keep the state unchanged.
-      alpha[i] = mn == -INFINITY ? 1.f : Exp2(m[i] - mn);
-      m[i] = mn;
       float ps = 0.f;
 #pragma unroll
       for (int h2 = 0; h2 < TH; ++h2) {
-        s[h2][i] = mn == -INFINITY ? 0.f : Exp2(s[h2][i] - mn);
+        s[h2][i] = m[i] == -INFINITY ? 0.f : Exp2(s[h2][i] - m[i]);
         ps += s[h2][i];
       }
-      lsum[i] = lsum[i] * alpha[i] + ps;
+      lsum[i] += ps;
     }
     if (kq < HR) {
 #pragma unroll
@@ -464,12 +485,14 @@ void DecodeMfma(DecodeParams p) {
             make_float4(s[h2][0], s[h2][1], s[h2][2], s[h2][3]);
     }
     ItemSync<WPI>();
+    if (rescale) {
 #pragma unroll
-    for (int h = 0; h < GV; ++h) {
-      if (h / G >= nrows) break;
-      const float a = ReadLane(alpha[h & 3], 16 * (h >> 2));
-      o[h][0] *= a;
-      o[h][1] *= a;
+      for (int h = 0; h < GV; ++h) {
+        if (h / G >= nrows) break;
+        const float a = ReadLane(alpha[h & 3], 16 * (h >> 2));
+        o[h][0] *= a;
+        o[h][1] *= a;
+      }
     }
 #pragma unroll
     for (int h2 = 0; h2 < TH; ++h2) {
