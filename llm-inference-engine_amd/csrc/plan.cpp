@@ -72,6 +72,7 @@ Tuning ReadTuning() {
     const double x = std::strtod(v, nullptr);
     if (x >= 0 && x <= 1) t.tail_frac = x;
   }
+  if (const char* v = std::getenv("EHIP_SPLIT_EVEN")) t.split_even = v[0] == '1' ? 1 : v[0] == '0' ? 0 : -1;
   t.joint = flag("EHIP_NO_JOINT", '1');
   t.prefill = flag("EHIP_PREFILL", '0');
   if (const char* v = std::getenv("EHIP_PREFILL_SPLIT")) t.prefill_split = std::strtod(v, nullptr);
@@ -148,12 +149,16 @@ int32_t MaxSplitTokens(const ehip_geometry& g) {
   return 128 * g.block_size;
 }
 
+static int64_t DecodeItemTarget(const ehip_geometry& g, const Tuning& tune) {
+  if (tune.target_items > 0) return tune.target_items;
+  return ScaledKv(g.kv_dtype) ? kTargetItems / 2 : kTargetItems;
+}
+
 int32_t ChooseSplitTokens(const ehip_geometry& g, int64_t unit_tokens, const Tuning& tune) {
   const int32_t max_split = MaxSplitTokens(g);
   if (tune.split_tokens > 0)
     return static_cast<int32_t>(std::min<int64_t>(RoundUp(tune.split_tokens, kTile), max_split));
-  int64_t target = ScaledKv(g.kv_dtype) ? kTargetItems / 2 : kTargetItems;
-  if (tune.target_items > 0) target = tune.target_items;
+  const int64_t target = DecodeItemTarget(g, tune);
   int64_t s = (unit_tokens + target - 1) / target;
   if (!ScaledKv(g.kv_dtype) && s >= kLargeStep) s = std::clamp(s, kLargeMin, kLargeMax);
   s = RoundUp(std::max<int64_t>(s, unit_tokens < kSmallStepUnits ? kTile : kMinSplit), kTile);
@@ -200,6 +205,17 @@ struct KeyRange {
   int32_t tb, te;
   bool joint() const { return rows[1] >= 0; }
 };
+
+// Piece length for cutting `keys` keys into ranges of at most sl keys, evened
+// out: the same number of pieces, of whole kTile units, the last one the
+// shortest (a run of 1.1 sl keys makes two pieces of ~0.55 sl instead of
+// sl + 0.1 sl).
+int32_t EvenStep(int32_t sl, int32_t keys) {
+  if (keys <= sl) return sl;
+  const int32_t pieces = (keys + sl - 1) / sl;
+  return static_cast<int32_t>(
+      std::min<int64_t>(sl, RoundUp((keys + pieces - 1) / pieces, kTile)));
+}
 
 // Tail pieces. When a step has more items than the queue hands out first,
 // the queue's last items set the launch's end: a wavefront streams ~3 GB/s
@@ -351,23 +367,38 @@ void FinishPlan(const ehip_geometry& g, const Tuning& tune, Plan* plan, bool all
 
   // Key ranges: a group's shared prefix [0, P) in joint ranges, then each
   // row's own keys [P, L), in pieces of the row's split length. Every range
-  // becomes one work item per kv head.
+  // becomes one work item per kv head. When every item gets a wavefront of
+  // its own (no more items than the decode target), the pieces of each run
+  // are evened out (same count): C3's 1256 decode items, attention call
+  // 135.2 against 138.0 us (three interleaved pairs of contexts). With more
+  // items than that the queue hands out the short last pieces of fixed-length
+  // cuts last, which balances better: even cuts took C4 from 385.4 to 398.9 us
+  // and C5 from 262.3 to 295.8 us.
   std::vector<KeyRange> ranges;
-  for (size_t k = 0; k < n_groups; ++k) {
-    const auto [b, e] = members(k);
-    const int32_t sl = split_len[*b], P = joint_len[*b];
-    for (int32_t t = 0; t < P; t += sl) {
-      KeyRange kr{{-1, -1, -1, -1}, t, std::min(P, t + sl)};
-      std::copy(b, e, kr.rows);
-      ranges.push_back(kr);
+  auto cut_ranges = [&](bool even) {
+    ranges.clear();
+    for (size_t k = 0; k < n_groups; ++k) {
+      const auto [b, e] = members(k);
+      const int32_t P = joint_len[*b];
+      const int32_t sl = even ? EvenStep(split_len[*b], P) : split_len[*b];
+      for (int32_t t = 0; t < P; t += sl) {
+        KeyRange kr{{-1, -1, -1, -1}, t, std::min(P, t + sl)};
+        std::copy(b, e, kr.rows);
+        ranges.push_back(kr);
+      }
     }
-  }
-  for (size_t r = 0; r < n; ++r) {
-    if (skipped(r)) continue;
-    const int32_t sl = split_len[r], L = plan->rows[r].length;
-    for (int32_t t = joint_len[r]; t < L; t += sl)
-      ranges.push_back(KeyRange{{static_cast<int32_t>(r), -1, -1, -1}, t, std::min(L, t + sl)});
-  }
+    for (size_t r = 0; r < n; ++r) {
+      if (skipped(r)) continue;
+      const int32_t L = plan->rows[r].length;
+      const int32_t sl = even ? EvenStep(split_len[r], L - joint_len[r]) : split_len[r];
+      for (int32_t t = joint_len[r]; t < L; t += sl)
+        ranges.push_back(KeyRange{{static_cast<int32_t>(r), -1, -1, -1}, t, std::min(L, t + sl)});
+    }
+  };
+  cut_ranges(tune.split_even > 0);
+  if (tune.split_even < 0 &&
+      static_cast<int64_t>(ranges.size()) * g.kv_heads <= DecodeItemTarget(g, tune))
+    cut_ranges(true);
   CutTail(g, tune, plan->rows, &ranges);
 
   // Split indices follow key order within a row. Joint ranges cover the

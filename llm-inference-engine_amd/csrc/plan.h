@@ -39,6 +39,8 @@ struct Tuning {
   int64_t target_items = 0;    // EHIP_TARGET_ITEMS: decode work-item target (0: default)
   int32_t tail_split = 0;      // EHIP_TAIL_SPLIT: tail piece length in keys (0: no tail pieces)
   double tail_frac = 0.08;     // EHIP_TAIL_FRAC: share of the step's keys cut into tail pieces
+  int8_t split_even = -1;      // EHIP_SPLIT_EVEN=1/0: a row's ranges of near-equal length
+                               // always / never (default: when items <= the item target)
   bool joint = true;           // EHIP_NO_JOINT=1: no joint items over shared prefixes
   bool prefill = true;         // EHIP_PREFILL=0: chunk rows stay on the decode kernels
   double prefill_split = 2.0;  // EHIP_PREFILL_SPLIT: key-split threshold in shares (0: none)

@@ -110,6 +110,37 @@ def test_plan_split_override_and_long_rows(ehip_mod, monkeypatch):
     assert items == 8 * (64 + 1 + 1 + 2)
 
 
+@pytest.mark.parametrize("even", [None, "0", "1"])
+def test_plan_even_ranges_when_every_item_has_a_wavefront(ehip_mod, monkeypatch, even):
+    """A step with no more items than the decode target (2048) cuts each row
+    into the same number of ranges as fixed-length cuts, but of near-equal
+    length: every range but the last has RoundUp(ceil(L / n), 64) keys and the
+    last is no longer. EHIP_SPLIT_EVEN=0 keeps fixed cuts (sl, sl, ..., rest);
+    =1 forces even cuts."""
+    monkeypatch.setenv("EHIP_SPLIT_TOKENS", "1024")
+    monkeypatch.setenv("EHIP_NO_JOINT", "1")
+    if even is not None:
+        monkeypatch.setenv("EHIP_SPLIT_EVEN", even)
+    lens = [1100, 3000, 1024, 4097, 300, 2049]
+    rc, items = ehip_mod.plan_items(geom(ehip_mod, slab_blocks=1000), simple_step(ehip_mod, lens))
+    assert rc == 0
+    sl = 1024
+    for r, L in enumerate(lens):
+        mine = items[(items[:, 0] == r) & (items[:, 6] == 0)]
+        spans = sorted((int(kb), int(ke)) for kb, ke in mine[:, 4:6])
+        n = -(-L // sl)
+        assert len(spans) == n, (L, spans)  # the same count either way
+        assert spans[0][0] == 0 and spans[-1][1] == L
+        assert all(a[1] == b[0] for a, b in zip(spans, spans[1:]))
+        step = sl if even == "0" else min(sl, -(-(-(-L // n)) // 64) * 64)
+        assert all(ke - kb == step for kb, ke in spans[:-1]), (L, spans)
+        assert spans[-1][1] - spans[-1][0] <= step
+    if even != "0":
+        # 1100 keys: two ranges of 576 and 524 instead of 1024 and 76.
+        mine = items[(items[:, 0] == 0) & (items[:, 6] == 0)]
+        assert sorted(int(ke - kb) for kb, ke in mine[:, 4:6]) == [524, 576]
+
+
 def test_plan_large_steps_take_1024_to_1536_key_ranges(ehip_mod):
     """Steps whose one-item-per-wavefront length (kv-head-keys / 2048) is 512
     keys or more take ranges clamped to [1024, 1536] keys (the measured best
